@@ -1,0 +1,409 @@
+"""Benchmark of the MI355X packed-trit GEMV fabric (one GPU).
+
+Default workload ("C2"): the Llama-3.2-1B projection
+sweep at M = 1 -- 16 layers x {Wq 2048->2048, Wk/Wv 2048->512, Wo 2048->2048,
+Wgate/Wup 2048->8192, Wdown 8192->2048}, every layer with its own seeded
+ternary weights (P(-1)=P(0)=P(+1)=1/3, 2-bit packed), int8 activations
+U[-127,127].  One step = one pass of the hot path over the whole sweep: the
+112 GEMVs as ONE work-list launch.  Weights are rotated over `--copies`
+independently seeded copies of the sweep (4 x 243 MB > the 256 MB Infinity
+Cache), so every step streams its weights from HBM.
+
+Also reported (not `value`): the same sweep as one launch per GEMV (112
+launches) and as 4 launches per layer grouped like a decode step
+({q,k,v}, {o}, {gate,up}, {down}); the C3 BitNet-2B sweep (fp32 activations
+quantized in the kernel prologue) with --config bitnet; the C4 batched GEMM
+with --config batched --m M.
+
+value = MACs of the sweep / (time per step); roofline.achieved = algorithmic
+bytes per launch (packed W K*N/4 + X + Y 4N, summed over the sweep) / mean
+launch duration from HIP events on the launch stream.
+cpu_baseline = the reference's own mm_row (oracle/_ref, single thread,
+compiled from the reference sources with its flags) on one layer of the same
+weights, or the C restatement when the reference build is absent.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "M=1 packed-trit GEMV GMAC/s + achieved HBM GB/s (% of 8 TB/s), layer sweep"
+HBM_PEAK_GBS = 8000.0
+MFMA_I8_PEAK_TOPS = 5000.0
+
+LLAMA = dict(name="llama-3.2-1b", layers=16, p_zero=1.0 / 3.0,
+             shapes=[("Wq", 2048, 2048), ("Wk", 2048, 512), ("Wv", 2048, 512), ("Wo", 2048, 2048),
+                     ("Wgate", 2048, 8192), ("Wup", 2048, 8192), ("Wdown", 8192, 2048)],
+             groups=[["Wq", "Wk", "Wv"], ["Wo"], ["Wgate", "Wup"], ["Wdown"]])
+BITNET = dict(name="bitnet-b1.58-2b-4t", layers=30, p_zero=0.4,
+              shapes=[("Wq", 2560, 2560), ("Wk", 2560, 640), ("Wv", 2560, 640), ("Wo", 2560, 2560),
+                      ("Wgate", 2560, 6912), ("Wup", 2560, 6912), ("Wdown", 6912, 2560)],
+              groups=[["Wq", "Wk", "Wv"], ["Wo"], ["Wgate", "Wup"], ["Wdown"]])
+# activation vector shared by each group (a decode step quantizes once per group)
+X_OF = {"Wq": "attn", "Wk": "attn", "Wv": "attn", "Wo": "o", "Wgate": "ffn", "Wup": "ffn", "Wdown": "down"}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def scale_of(seed: int) -> float:
+    # per-tensor fp32 weight scale in U[0.01, 0.1] from the seed
+    return 0.01 + 0.09 * (((seed * 2654435761) & 0xFFFFFFFF) / 2 ** 32)
+
+
+class Sweep:
+    """All weights / activations / outputs of one sweep copy set."""
+
+    def __init__(self, cfg, copies: int, fp32_x: bool, base_seed: int = 1):
+        import torch
+        import ter_amd as T
+        self.cfg = cfg
+        self.copies = []
+        for c in range(copies):
+            layers = []
+            for l in range(cfg["layers"]):
+                lw = {}
+                for i, (nm, K, N) in enumerate(cfg["shapes"]):
+                    seed = base_seed * 1_000_003 + c * 10_007 + l * 101 + i
+                    v11 = T.synth_v11(K, N, seed=seed, p_zero=cfg["p_zero"])
+                    W = T.PackedTrits.from_v11(v11, K, N, scale_of(seed))
+                    lw[nm] = (W, v11 if c == 0 and l == 0 else None, seed)
+                    del v11
+                layers.append(lw)
+            self.copies.append(layers)
+        torch.cuda.synchronize()
+        # activations: one vector per group and layer (shared by all copies)
+        self.x = []
+        for l in range(cfg["layers"]):
+            xd = {}
+            for nm, K, N in cfg["shapes"]:
+                key = X_OF[nm]
+                if key in xd:
+                    continue
+                seed = 777_777 + l * 13 + len(xd)
+                if fp32_x:
+                    g = torch.Generator(device="cuda")
+                    g.manual_seed(seed)
+                    xd[key] = torch.randn(K, dtype=torch.float32, device="cuda", generator=g)
+                else:
+                    xd[key] = T.synth_i8(K, seed=seed, lo=-127, hi=127)
+            self.x.append(xd)
+        self.y = [{nm: torch.empty(N, dtype=torch.float32, device="cuda") for nm, K, N in cfg["shapes"]}
+                  for _ in range(cfg["layers"])]
+        self.fp32_x = fp32_x
+
+    def items(self, c, names=None, layers=None):
+        out = []
+        for l in (range(self.cfg["layers"]) if layers is None else layers):
+            for nm, K, N in self.cfg["shapes"]:
+                if names is not None and nm not in names:
+                    continue
+                W = self.copies[c][l][nm][0]
+                out.append(dict(w=W, x=self.x[l][X_OF[nm]], x_scale=0.0312, y=self.y[l][nm]))
+        return out
+
+
+def alg_bytes(cfg, fp32_x: bool, m: int = 1) -> int:
+    b = 0
+    for nm, K, N in cfg["shapes"]:
+        b += K * N // 4 + m * K * (4 if fp32_x else 1) + m * N * 4
+    return b * cfg["layers"]
+
+
+def macs(cfg, m: int = 1) -> int:
+    return sum(K * N for _, K, N in cfg["shapes"]) * cfg["layers"] * m
+
+
+def lane_macs(cfg) -> int:
+    # reference lane-MAC convention ceil(K/27)*27*N (cuda/ter_cuda_packed.cu:254)
+    return sum(((K + 26) // 27) * 27 * N for _, K, N in cfg["shapes"]) * cfg["layers"]
+
+
+def time_launches(launch_fns, steps: int, warmup: int):
+    """Run launch_fns[i % len] for warmup + steps; returns (wall ms per step,
+    mean HIP-event ms per step).  Each step is bracketed by events on the
+    launch stream (torch's current stream)."""
+    import torch
+    n = len(launch_fns)
+    for i in range(warmup):
+        launch_fns[i % n]()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        launch_fns[(warmup + i) % n]()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    evm = sorted(a.elapsed_time(b) for a, b in ev)
+    return wall, sum(evm) / len(evm), evm[len(evm) // 2]
+
+
+def graph_of(fn):
+    """Capture fn's launches (on torch's current stream) into a HIP graph."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def cpu_baseline(sw: Sweep, budget_s: float):
+    """Reference mm_row (oracle/_ref) on layer 0 of copy 0, 1 thread."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    use_ref = O.ref_available()
+    cfg = sw.cfg
+    total_macs, total_t, reps, checked = 0, 0.0, 0, True
+    ctxs = []
+    for nm, K, N in cfg["shapes"]:
+        W, v11, seed = sw.copies[0][0][nm]
+        Wi = O.v11_unpack(v11.cpu().numpy(), K, N)
+        x = sw.x[0][X_OF[nm]]
+        if sw.fp32_x:
+            q, xs = O.quant_int8(x.cpu().numpy())   # quantizer timed separately (not included)
+        else:
+            q, xs = x.cpu().numpy(), np.float32(0.0312)
+        X = q.astype(np.int32)[None, :]
+        ctxs.append((nm, K, N, X, float(xs), Wi, W.scale))
+    runners = []
+    for nm, K, N, X, xs, Wi, ws in ctxs:
+        if use_ref:
+            r = O.RefMmRow(X, xs, Wi, ws)
+            runners.append((nm, K, N, (lambda r=r: r.run(0))))
+        else:
+            runners.append((nm, K, N, (lambda X=X, xs=xs, Wi=Wi, ws=ws: O.mm_row(X, 0, xs, Wi, ws)[1])))
+    del ctxs
+    t_start = time.perf_counter()
+    while True:
+        for nm, K, N, run in runners:
+            t0 = time.perf_counter()
+            out = run()
+            total_t += time.perf_counter() - t0
+            total_macs += K * N
+            if reps == 0:  # the sample is checked against the GPU outputs of the same weights
+                gpu = sw.y[0][nm].cpu().numpy()
+                checked = checked and bool((gpu.view(np.int32) == out.view(np.int32)).all())
+        reps += 1
+        if time.perf_counter() - t_start > budget_s:
+            break
+    return dict(value=round(total_macs / total_t / 1e9, 4), unit="GMAC/s", cores=1,
+                kind="reference" if use_ref else "port",
+                sample=f"layer 0 of the {cfg['name']} sweep (7 GEMVs, {reps} passes, "
+                       f"{total_t:.1f} s of mm_row time), int32 payload 4 B/trit, 1 thread",
+                matches_gpu_bitexact=checked)
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch from profiles/<name>_pmc.txt (written from two
+    rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, scaled by the copy-kernel
+    calibration): a line 'traffic_bytes_per_launch: <int>'."""
+    p = os.path.join(ROOT, "profiles", f"{name}_pmc.txt")
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def run_m1(args, cfg, fp32_x: bool):
+    import torch
+    import ter_amd as T
+    t0 = time.perf_counter()
+    sw = Sweep(cfg, args.copies, fp32_x)
+    log(f"[bench] built {args.copies} copies of the {cfg['name']} sweep in {time.perf_counter() - t0:.1f} s")
+    plans = [T.Plan(sw.items(c)) for c in range(args.copies)]
+    bytes_alg = alg_bytes(cfg, fp32_x)
+    assert plans[0].bytes == bytes_alg, (plans[0].bytes, bytes_alg)
+    mac = macs(cfg)
+
+    # timed region (the contract's K steps, bracketed by synchronize)
+    fns = [p.launch for p in plans]
+    for i in range(args.warmup):
+        fns[i % len(fns)]()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for i in range(args.steps):
+        fns[(args.warmup + i) % len(fns)]()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t_start) * 1e3 / args.steps
+    log(f"[bench] work-list sweep: {ms_step * 1e3:.2f} us/step (wall)")
+
+    # per-launch kernel time from HIP events on the launch stream
+    _, ev_mean, ev_med = time_launches(fns, args.steps, 2)
+    achieved_gbs = bytes_alg / (ev_mean * 1e-3) / 1e9
+    log(f"[bench] work-list sweep: {ev_mean * 1e3:.2f} us/launch (events), {achieved_gbs:.0f} GB/s")
+
+    modes = {"worklist_1_launch": dict(us=round(ev_mean * 1e3, 2), us_median=round(ev_med * 1e3, 2),
+                                       gbs=round(achieved_gbs, 1))}
+    if not args.quick:
+        # The same sweep as (a) one launch per GEMV and (b) 4 launches per
+        # layer grouped like a decode step; both captured in HIP graphs so the
+        # Python launch cost is not what is measured.
+        def per_gemv(c):
+            def f():
+                for it in sw.items(c):
+                    T.gemv(it["w"], it["x"], y=it["y"], x_scale=it["x_scale"])
+            return f
+        grp_plans = [[T.Plan(sw.items(c, names=g, layers=[l])) for l in range(cfg["layers"]) for g in cfg["groups"]]
+                     for c in range(args.copies)]
+
+        def grouped(c):
+            def f():
+                for p in grp_plans[c]:
+                    p.launch()
+            return f
+        for mode, mk, nl in (("per_gemv_launch", per_gemv, len(sw.items(0))),
+                             ("layer_grouped_4_per_layer", grouped, len(grp_plans[0]))):
+            graphs = [graph_of(mk(c)) for c in range(args.copies)]
+            _, evm, _ = time_launches([g.replay for g in graphs], max(20, args.steps // 4), 4)
+            modes[mode] = dict(launches=nl, us=round(evm * 1e3, 2), gbs=round(bytes_alg / (evm * 1e-3) / 1e9, 1),
+                               hip_graph=True)
+        log(f"[bench] modes: {modes}")
+
+    cpu = None
+    if not args.no_cpu:
+        plans[0].launch()
+        torch.cuda.synchronize()
+        cpu = cpu_baseline(sw, args.cpu_seconds)
+        log(f"[bench] cpu baseline: {cpu}")
+
+    value = mac / (ms_step * 1e-3) / 1e9
+    name = "sweep_" + cfg["name"].split("-")[0]
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GMAC/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"C{2 if cfg is LLAMA else 3}: {cfg['name']} projection sweep at M=1, "
+                         f"{cfg['layers']} layers x 7 GEMVs in one work-list launch, "
+                         f"{'fp32 X absmax-quantized in the kernel prologue' if fp32_x else 'int8 X'}, "
+                         f"weights rotated over {args.copies} seeded copies"),
+            "layers": cfg["layers"],
+            "shapes": [[nm, K, N] for nm, K, N in cfg["shapes"]],
+            "packed_weight_bytes": sum(K * N // 4 for _, K, N in cfg["shapes"]) * cfg["layers"],
+            "rotation_footprint_bytes": sum(K * N // 4 for _, K, N in cfg["shapes"]) * cfg["layers"] * args.copies,
+        },
+        "hbm_gbs": round(achieved_gbs, 1),
+        "hbm_frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+        "lane_gmacs": round(lane_macs(cfg) / (ms_step * 1e-3) / 1e9, 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+            "traffic": read_traffic(name),
+            "kernel": "gemv_t16_kernel",
+            "bytes_per_launch": bytes_alg,
+            "mean_launch_us": round(ev_mean * 1e3, 3),
+        },
+        "cpu_baseline": cpu,
+        "modes": modes,
+    }
+    return out
+
+
+def run_batched(args):
+    import torch
+    import ter_amd as T
+    cfg = BITNET
+    M = args.m
+    layers = []
+    for l in range(cfg["layers"]):
+        lw = {}
+        for i, (nm, K, N) in enumerate(cfg["shapes"]):
+            seed = 5_000_000 + l * 101 + i
+            lw[nm] = T.PackedTrits.from_v11(T.synth_v11(K, N, seed=seed, p_zero=cfg["p_zero"]), K, N, scale_of(seed))
+        layers.append(lw)
+    X = {}
+    g = torch.Generator(device="cuda")
+    g.manual_seed(11)
+    for nm, K, N in cfg["shapes"]:
+        X[X_OF[nm]] = torch.randn((M, K), dtype=torch.float32, device="cuda", generator=g)
+    q = {k: torch.empty(v.shape, dtype=torch.int8, device="cuda") for k, v in X.items()}
+    s = {k: torch.empty(M, dtype=torch.float32, device="cuda") for k in X}
+    Y = {nm: torch.empty((M, N), dtype=torch.float32, device="cuda") for nm, K, N in cfg["shapes"]}
+
+    def step():
+        for k in X:
+            T.quant_int8(X[k], q[k], s[k])
+        for l in range(cfg["layers"]):
+            for nm, K, N in cfg["shapes"]:
+                T.mm_batched(layers[l][nm], q[X_OF[nm]], y=Y[nm], x_scale_dev=s[X_OF[nm]])
+    wall, evm, _ = time_launches([step], args.steps, args.warmup)
+    mac = macs(cfg, M)
+    b = alg_bytes(cfg, True, M)
+    gbs = b / (evm * 1e-3) / 1e9
+    tops = 2 * mac / (evm * 1e-3) / 1e12
+    return {
+        "metric": f"batched packed-trit GEMM, M={M}, BitNet-2B sweep",
+        "value": round(mac / (evm * 1e-3) / 1e9, 1), "unit": "GMAC/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(evm, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": f"C4: {cfg['name']} 30 layers x 7 GEMMs at M={M}, fp32 X per-row absmax int8"},
+        "hbm_gbs": round(gbs, 1), "mfma_tops": round(tops, 2), "mfma_frac": round(tops / MFMA_I8_PEAK_TOPS, 4),
+        "roofline": {"bound": "hbm" if M <= 64 else "mfma",
+                     "achieved": round(gbs if M <= 64 else tops * 1000, 1),
+                     "peak": HBM_PEAK_GBS if M <= 64 else MFMA_I8_PEAK_TOPS * 1000,
+                     "unit": "GB/s" if M <= 64 else "GOP/s", "frac": round(gbs / HBM_PEAK_GBS if M <= 64 else tops / MFMA_I8_PEAK_TOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": None,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--config", choices=["llama", "bitnet", "batched"], default="llama")
+    ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
+    ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--quick", action="store_true", help="skip the per-GEMV / grouped launch modes")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures ONE GPU; --gpus {args.gpus} (WORLD_SIZE={world}) is not "
+              "supported (the GEMV shards by output columns across GPUs; see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.config == "batched":
+        out = run_batched(args)
+    else:
+        cfg = LLAMA if args.config == "llama" else BITNET
+        out = run_m1(args, cfg, fp32_x=(args.config == "bitnet"))
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

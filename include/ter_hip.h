@@ -1,0 +1,249 @@
+/*
+ * ter_hip.h -- C-ABI of the MI355X (gfx950) packed-trit matmul fabric.
+ *
+ * Drop-in boundary for ter's packed-trit GEMV/GEMM.  Plain C types only:
+ * device pointers are `void*`/typed pointers, a HIP stream is passed as
+ * `void*` (a hipStream_t; NULL = the null stream).  Every entry point returns
+ * an int status in the ter_k4 style (0 = ok, negative = error) and never
+ * aborts the process.
+ *
+ * Reference interfaces this header replaces (paths in the xaskasdf/ter tree):
+ *   - the packed weight handle  WPK{uint8_t* data; float scale; size_t bytes}
+ *       cuda/ter_cuda_forward_packed.cu:400
+ *   - the GPU GEMV launcher     mm_packed_dispatch(X, scale_x_dev, W, out, K, N, stream)
+ *       cuda/ter_cuda_forward_packed.cu:493-500
+ *   - the CPU GEMV contract     mm_row(sim, kt, id, Xt, row, Wt, K, N, out)
+ *       src/tx/forward.cpp:299-352 (internal linkage)
+ *   - the batched launchers     mm_bitnet_addonly_batched_k<M>(X, X_scale, W_col, K, N, w_scale, out)
+ *       cuda/ter_cuda_addonly_batched.cu:31-38
+ *   - the activation quantizer  quant_int8_k(x, y, scale_out, N)
+ *       cuda/ter_cuda_forward_packed.cu:40-62
+ *   - the K4 C-ABI              ter_k4_create/destroy/install_kernel/call/op_counts/reset_counters
+ *       include/ter_k4/ter_k4.h:29-55, src/k4/ter_k4.cpp:14-73
+ *   - the KernelTable slot      KernelTable::install/find, 32 slots, names < 32 chars
+ *       include/ter/kernels.hpp:21-38, src/sim/call_kernel.cpp:24-61
+ */
+#ifndef TER_HIP_H
+#define TER_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (ter_k4 values kept: src/k4/ter_k4.cpp:38,52-55) ---- */
+#define TER_HIP_OK             0
+#define TER_HIP_ERR_NULL      -1  /* null handle / pointer argument            */
+#define TER_HIP_ERR_NOTFOUND  -2  /* unknown kernel name                       */
+#define TER_HIP_ERR_ALLOC     -3  /* allocation failure                        */
+#define TER_HIP_ERR_NARGS     -4  /* more than 7 kernel-call arguments         */
+#define TER_HIP_ERR_SHAPE     -5  /* K/N/M out of range or buffer too small    */
+#define TER_HIP_ERR_PAYLOAD   -6  /* payload not ternary / X not int8 / blocked scales */
+#define TER_HIP_ERR_HIP       -7  /* HIP runtime error (launch, copy, device)  */
+#define TER_HIP_ERR_ALIGN     -8  /* device pointer misaligned                  */
+#define TER_HIP_ERR_FULL      -9  /* kernel table has no free slot             */
+#define TER_HIP_ERR_CONFLICT -10  /* a plan names one weight twice (shared fix-up slots) */
+
+/* ---- limits ---- */
+#define TER_HIP_K_MAX      32768  /* activation vector staged in LDS (int8)    */
+#define TER_HIP_N_MAX  (1 << 24)
+#define TER_HIP_M_MAX        256  /* batched rows per call                      */
+
+/* ---- activation kinds ---- */
+#define TER_HIP_X_I8   0  /* int8 X[K] with a host or device activation scale       */
+#define TER_HIP_X_F32  1  /* fp32 X[K]: absmax -> int8 inside the kernel prologue    */
+
+/*
+ * Packed ternary weight (replaces WPK, cuda/ter_cuda_forward_packed.cu:400).
+ *
+ * `data` holds the "T16" tile stream the kernels read: 1 KiB tiles of
+ * 16 output columns x 256 input rows, 2 bits per trit, stored as u = w + 1
+ * (see DESIGN.md for the bit layout), followed by `N` 64-bit fix-up slots
+ * (`fix`, zero at rest) used to combine split column strips.  The whole
+ * buffer is `ter_hip_wpk_bytes(K, N)` bytes of device memory owned by the
+ * caller.  `scale` is the per-tensor weight scale (Wt.scale; a ternary
+ * payload {-m,0,+m} is stored as {-1,0,+1} with m folded into `scale`).
+ */
+typedef struct ter_hip_wpk {
+    uint8_t*  data;    /* device: tile stream, then fix-up slots            */
+    size_t    bytes;   /* total device bytes (== ter_hip_wpk_bytes(K, N))    */
+    uint64_t* fix;     /* device: N fix-up slots inside `data`               */
+    int32_t   K, N;
+    float     scale;
+    int32_t   layout;  /* TER_HIP_LAYOUT_T16                                */
+} ter_hip_wpk_t;
+
+#define TER_HIP_LAYOUT_T16 16
+
+/* Activation operand of one GEMV / GEMM. */
+typedef struct ter_hip_act {
+    const void*  data;       /* device: int8 [M][K] (X_I8) or fp32 [M][K] (X_F32)      */
+    int32_t      kind;       /* TER_HIP_X_I8 or TER_HIP_X_F32                          */
+    float        scale;      /* X_I8: host activation scale, used when scale_dev NULL  */
+    const float* scale_dev;  /* X_I8: device activation scale(s) ([M]), or NULL       */
+    int8_t*      q_out;      /* X_F32: optional device copy of the quantized X [M][K]  */
+    float*       scale_out;  /* X_F32: optional device act scale(s) 1/scale ([M])     */
+} ter_hip_act_t;
+
+/* ---------------------------------------------------------------------- */
+/* Packed payload (TritTensor -> device tile stream)                       */
+/* ---------------------------------------------------------------------- */
+
+/* Device bytes needed for a K x N packed weight (tile stream + fix-up slots). */
+size_t ter_hip_wpk_bytes(int32_t K, int32_t N);
+
+/* Fill `w` for a caller-owned device buffer `dev_buf` of `buf_bytes` bytes
+ * (256-byte aligned).  Does not touch the device. */
+int ter_hip_wpk_init(ter_hip_wpk_t* w, void* dev_buf, size_t buf_bytes,
+                     int32_t K, int32_t N, float scale);
+
+/* Device repack of reference v11 bytes (W_col[j_byte*K + k], 4 columns per
+ * byte, code map 00=0 01=+1 10=-1 11=0; tools/convert_llama_to_packed.py:128-140)
+ * into `w`, and zero of its fix-up slots.  v11_dev: (N/4)*K device bytes;
+ * N must be a multiple of 4 (the v11 format's own requirement). */
+int ter_hip_pack_v11(ter_hip_wpk_t* w, const uint8_t* v11_dev, void* stream);
+
+/* Inverse of ter_hip_pack_v11 (device): write v11 bytes of `w` to v11_dev. */
+int ter_hip_unpack_v11(const ter_hip_wpk_t* w, uint8_t* v11_dev, void* stream);
+
+/* Host pack of a TritTensor payload (int32 [K][N] row-major, the orientation
+ * mm_row reads, src/tx/forward.cpp:337) into `w` (synchronous upload).  The
+ * payload must be ternary {-m, 0, +m} for one m > 0 (or all zero);
+ * `w->scale` becomes scale * m.  Returns TER_HIP_ERR_PAYLOAD otherwise.
+ * `magnitude_out` (optional) receives m. */
+int ter_hip_pack_payload(ter_hip_wpk_t* w, const int32_t* payload_host, float scale,
+                         int32_t* magnitude_out, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* M = 1 decode GEMV                                                       */
+/* ---------------------------------------------------------------------- */
+
+/* y[j] = float(acc[j]) * (x_scale * w->scale), acc[j] = sum_k x[k] * w[k][j].
+ * y (fp32 [N]) and acc (int32 [N]) are optional device outputs (at least one). */
+int ter_hip_gemv(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int32_t* acc,
+                 void* stream);
+
+/* Drop-in for mm_packed_dispatch (cuda/ter_cuda_forward_packed.cu:493-500):
+ * int8 X, device activation scale, fp32 out[N].  K, N must match W. */
+int ter_hip_mm_packed_dispatch(const int8_t* X, const float* scale_x_dev,
+                               const ter_hip_wpk_t* W, float* out, int32_t K, int32_t N,
+                               void* stream);
+
+/* Host-side mm_row contract (src/tx/forward.cpp:299-352): X is the host
+ * TritTensor payload (int32 [rows][K]), `row` selects the row; out (host
+ * fp32 [N]) = float(acc) * (x_scale * W.scale).  Every X value must fit int8
+ * (TER_HIP_ERR_PAYLOAD otherwise -- no CPU fallback).  Synchronous.
+ * `x_stage_dev` (K int8) and `y_stage_dev` (N fp32) are caller device
+ * buffers used for the transfer. */
+int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale,
+                   const ter_hip_wpk_t* W, int32_t N, float* out,
+                   int8_t* x_stage_dev, float* y_stage_dev, void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* Work lists: many independent GEMVs in ONE launch (layer sweeps)          */
+/* ---------------------------------------------------------------------- */
+typedef struct ter_hip_gemv_item {
+    const ter_hip_wpk_t* w;
+    ter_hip_act_t        x;
+    float*               y;    /* fp32 [N] or NULL */
+    int32_t*             acc;  /* int32 [N] or NULL */
+} ter_hip_gemv_item_t;
+
+typedef struct ter_hip_plan ter_hip_plan_t;
+
+/* Build a launch plan for `n` GEMVs (descriptor table copied to the device).
+ * wg_per_cu <= 0 picks the default occupancy.  Items sharing a weight must not
+ * appear twice in one plan. */
+int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items, int32_t n,
+                        int32_t wg_per_cu);
+int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream);
+/* Algorithmic bytes (packed W + X + Y) and MACs of one launch of the plan. */
+int ter_hip_plan_stats(const ter_hip_plan_t* plan, uint64_t* bytes, uint64_t* macs,
+                       int32_t* n_wg);
+void ter_hip_plan_destroy(ter_hip_plan_t* plan);
+
+/* ---------------------------------------------------------------------- */
+/* M > 1 batched GEMM (replaces mm_bitnet_addonly_batched_k /              */
+/* mm_packed_batched, cuda/ter_cuda_addonly_batched.cu:31-124)              */
+/* ---------------------------------------------------------------------- */
+
+/* Y[m][j] = float(acc[m][j]) * (x_scale[m] * w->scale).  x->data is [M][K];
+ * for X_F32 each row is quantized by absmax (quant_int8_k steps) into
+ * `x->q_out` / `x->scale_out` (both REQUIRED for X_F32, [M][K] / [M]).  For
+ * X_I8, x->scale_dev ([M]) is required. */
+int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, float* y,
+                 int32_t* acc, void* stream);
+
+/* Per-row absmax int8 quantizer (quant_int8_k, cuda/ter_cuda_forward_packed.cu:40-62):
+ * q[m][k] = rn(x[m][k] * 127/(max_k|x[m][k]| + 1e-9)), scale_out[m] = 1/that. */
+int ter_hip_quant_int8(const float* x, int32_t M, int32_t K, int8_t* q, float* scale_out,
+                       void* stream);
+
+/* ---------------------------------------------------------------------- */
+/* K4-style handle + KernelTable native slot                               */
+/* (include/ter_k4/ter_k4.h:29-55; include/ter/kernels.hpp:21-38)           */
+/* ---------------------------------------------------------------------- */
+typedef struct ter_hip_handle ter_hip_handle_t;
+
+/* A native kernel: receives the handle and up to 7 int64 register args
+ * (the R1..R7 convention of Sim::call_kernel, src/sim/call_kernel.cpp:64-78). */
+typedef int (*ter_hip_native_fn)(ter_hip_handle_t* h, const int64_t* args, size_t n_args);
+
+typedef struct {
+    uint64_t total_ops;
+    uint64_t tvmac;
+    uint64_t tvadd;
+    uint64_t tvsub;
+    uint64_t tvmul;
+} ter_hip_op_counts_t;  /* same fields as ter_k4_op_counts_t */
+
+/* Creates a handle bound to HIP device `device` with the default slot
+ * "tk_matmul_b_9t" (src/kernels/registry.cpp:18-20) installed as the native
+ * packed GEMV.  Returns NULL on failure. */
+ter_hip_handle_t* ter_hip_create(int32_t device);
+void ter_hip_destroy(ter_hip_handle_t* h);
+/* Install (or replace) a named native slot.  Names longer than 31 chars are
+ * truncated (KernelTable::kNameMax = 32).  TER_HIP_ERR_FULL after 32 slots. */
+int ter_hip_install_native(ter_hip_handle_t* h, const char* name, ter_hip_native_fn fn);
+/* Call a slot by name: -1 null, -2 unknown name, -4 n_args > 7
+ * (src/k4/ter_k4.cpp:52-55); otherwise the slot's return value. */
+int ter_hip_call(ter_hip_handle_t* h, const char* name, const int64_t* args, size_t n_args);
+void ter_hip_op_counts(const ter_hip_handle_t* h, ter_hip_op_counts_t* out);
+void ter_hip_reset_counters(ter_hip_handle_t* h);
+
+/* Argument convention of the default "tk_matmul_b_9t" native slot:
+ *   args[0] = (const ter_hip_wpk_t*) W
+ *   args[1] = (const ter_hip_act_t*) X
+ *   args[2] = (float*)   y   (device, may be 0)
+ *   args[3] = (int32_t*) acc (device, may be 0)
+ *   args[4] = (hipStream_t) stream
+ *   args[5] = M (rows; 1 = GEMV)
+ * It bumps tvmac by ceil(K/27) * N * M, the analytic count mm_row reports
+ * (src/tx/forward.cpp:349-350). */
+
+/* ---------------------------------------------------------------------- */
+/* Utilities                                                                */
+/* ---------------------------------------------------------------------- */
+
+/* Library version string. */
+const char* ter_hip_version(void);
+/* Text of the last error recorded by this thread (never NULL). */
+const char* ter_hip_last_error(void);
+
+/* Synthetic benchmark data, generated on the device from a counter-based
+ * splitmix64 stream (element i = k*N + n of the [K][N] trit matrix draws
+ * state seed + (i+1) * 0x9E3779B97F4A7C15).  u = top 32 bits; trit = 0 if
+ * u < t0, +1 if u < t1, else -1.  Writes reference v11 bytes. */
+int ter_hip_synth_v11(uint8_t* v11_dev, int32_t K, int32_t N, uint64_t seed,
+                      uint32_t t0, uint32_t t1, void* stream);
+/* int8 draws: x[i] = lo + ((u * (hi - lo + 1)) >> 32) with u as above. */
+int ter_hip_synth_i8(int8_t* x_dev, int64_t n, uint64_t seed, int32_t lo, int32_t hi,
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TER_HIP_H */

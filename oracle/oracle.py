@@ -1,0 +1,335 @@
+"""NumPy/ctypes front-end of the CPU oracle (test infrastructure only).
+
+Only tests/, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module.  It loads ``oracle/liboracle.so`` (the C
+restatement in ``ter_oracle.c``) and, when built, ``oracle/_ref/libter_ref.so``
+(the reference's own ``mm_row`` and quantizers compiled from its sources).
+
+Each wrapper names the reference file:line the underlying C function follows;
+the C file's header lists which test pins which function.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Optional, Tuple
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = os.path.join(HERE, "liboracle.so")
+_REF = os.path.join(HERE, "_ref", "libter_ref.so")
+
+_P = C.c_void_p
+_lib = None
+_ref = None
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def lib():
+    """The C oracle; raises if oracle/liboracle.so has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB):
+            raise RuntimeError(f"oracle not built: {_LIB} (run make -C oracle)")
+        L = C.CDLL(_LIB)
+        L.orc_code_to_trit.argtypes = [C.c_uint]
+        L.orc_code_to_trit.restype = C.c_int
+        L.orc_trit_to_code.argtypes = [C.c_int]
+        L.orc_trit_to_code.restype = C.c_uint
+        L.orc_v11_pack.argtypes = [_P, C.c_int, C.c_int, _P]
+        L.orc_v11_pack.restype = C.c_int
+        L.orc_v11_unpack.argtypes = [_P, C.c_int, C.c_int, _P]
+        L.orc_v11_unpack.restype = C.c_int
+        L.orc_mm_row.argtypes = [_P, C.c_int, C.c_float, _P, C.c_float, C.c_int, C.c_int, _P, _P]
+        L.orc_mm_row.restype = None
+        L.orc_mm_row_blocked.argtypes = [_P, C.c_int, C.c_float, _P, _P, C.c_int, C.c_int, C.c_int, _P]
+        L.orc_mm_row_blocked.restype = None
+        L.orc_gemv_v11.argtypes = [_P, C.c_float, _P, C.c_float, C.c_int, C.c_int, _P, _P]
+        L.orc_gemv_v11.restype = None
+        L.orc_gemm_v11.argtypes = [_P, _P, C.c_int, _P, C.c_float, C.c_int, C.c_int, _P, _P]
+        L.orc_gemm_v11.restype = None
+        L.orc_quant_int8.argtypes = [_P, C.c_int, _P, _P]
+        L.orc_quant_int8.restype = None
+        L.orc_quant_int8_rows.argtypes = [_P, C.c_int, C.c_int, _P, _P]
+        L.orc_quant_int8_rows.restype = None
+        L.orc_quantize_bitnet.argtypes = [_P, C.c_size_t, _P]
+        L.orc_quantize_bitnet.restype = C.c_float
+        L.orc_quantize_nt.argtypes = [_P, C.c_size_t, C.c_int, _P]
+        L.orc_quantize_nt.restype = C.c_float
+        L.orc_dequant_i2s.argtypes = [_P, C.c_size_t, _P]
+        L.orc_dequant_i2s.restype = None
+        L.orc_i2s_to_v11.argtypes = [_P, C.c_int, C.c_int, _P]
+        L.orc_i2s_to_v11.restype = C.c_int
+        L.orc_mm_row_tvmac.argtypes = [C.c_int, C.c_int]
+        L.orc_mm_row_tvmac.restype = C.c_uint64
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(_REF)
+
+
+def ref():
+    """The reference's own code (oracle/_ref); raises if it was not built."""
+    global _ref
+    if _ref is None:
+        if not ref_available():
+            raise RuntimeError(f"reference build absent: {_REF}")
+        R = C.CDLL(_REF)
+        R.ter_ref_ctx_new.argtypes = [_P, C.c_int, C.c_int, C.c_float, _P, C.c_int, C.c_float, _P, C.c_int]
+        R.ter_ref_ctx_new.restype = _P
+        R.ter_ref_ctx_run.argtypes = [_P, C.c_int, _P]
+        R.ter_ref_ctx_run.restype = C.c_int
+        R.ter_ref_ctx_tvmac.argtypes = [_P]
+        R.ter_ref_ctx_tvmac.restype = C.c_uint64
+        R.ter_ref_ctx_free.argtypes = [_P]
+        R.ter_ref_ctx_free.restype = None
+        R.ter_ref_quantize.argtypes = [_P, C.c_int, C.c_int, _P]
+        R.ter_ref_quantize.restype = C.c_float
+        R.ter_ref_quantize_bitnet.argtypes = [_P, C.c_int, _P]
+        R.ter_ref_quantize_bitnet.restype = C.c_float
+        _ref = R
+    return _ref
+
+
+# --------------------------------------------------------------------------
+# Layout helpers (include/ter/pack.hpp:8-21; tools/convert_llama_to_packed.py:128-140)
+# --------------------------------------------------------------------------
+def v11_pack(w_kn: np.ndarray) -> np.ndarray:
+    """Trits [K][N] (int8 in {-1,0,1}) -> v11 bytes [(N/4)*K]."""
+    w = np.ascontiguousarray(w_kn, dtype=np.int8)
+    K, N = w.shape
+    out = np.zeros((N // 4) * K, dtype=np.uint8)
+    rc = lib().orc_v11_pack(_ptr(w), K, N, _ptr(out))
+    if rc != 0:
+        raise ValueError(f"orc_v11_pack rc={rc}")
+    return out
+
+
+def v11_unpack(v11: np.ndarray, K: int, N: int) -> np.ndarray:
+    """v11 bytes -> int32 trits [K][N] (the TritTensor payload orientation)."""
+    b = np.ascontiguousarray(v11, dtype=np.uint8)
+    out = np.empty((K, N), dtype=np.int32)
+    rc = lib().orc_v11_unpack(_ptr(b), K, N, _ptr(out))
+    if rc != 0:
+        raise ValueError(f"orc_v11_unpack rc={rc}")
+    return out
+
+
+# --------------------------------------------------------------------------
+# mm_row and packed GEMV (src/tx/forward.cpp:331-346; cuda/ter_cuda_forward_packed.cu:346-397)
+# --------------------------------------------------------------------------
+def mm_row(X: np.ndarray, row: int, xs: float, W: np.ndarray, ws: float) -> Tuple[np.ndarray, np.ndarray]:
+    """Restated mm_row int path.  X int32 [rows][K], W int32 [K][N].
+    Returns (int64 acc[N], fp32 out[N])."""
+    X = np.ascontiguousarray(X, dtype=np.int32)
+    W = np.ascontiguousarray(W, dtype=np.int32)
+    K, N = W.shape
+    acc = np.empty(N, dtype=np.int64)
+    out = np.empty(N, dtype=np.float32)
+    lib().orc_mm_row(_ptr(X), int(row), float(xs), _ptr(W), float(ws), K, N, _ptr(acc), _ptr(out))
+    return acc, out
+
+
+def mm_row_blocked(X, row, xs, W, block_scales, block_size):
+    X = np.ascontiguousarray(X, dtype=np.int32)
+    W = np.ascontiguousarray(W, dtype=np.int32)
+    bsc = np.ascontiguousarray(block_scales, dtype=np.float32)
+    K, N = W.shape
+    out = np.empty(N, dtype=np.float32)
+    lib().orc_mm_row_blocked(_ptr(X), int(row), float(xs), _ptr(W), _ptr(bsc), int(block_size), K, N, _ptr(out))
+    return out
+
+
+def gemv_v11(x: np.ndarray, xs: float, v11: np.ndarray, ws: float, K: int, N: int):
+    """int8 x[K] times v11-packed W -> (int32 acc[N], fp32 out[N])."""
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    b = np.ascontiguousarray(v11, dtype=np.uint8)
+    acc = np.empty(N, dtype=np.int32)
+    out = np.empty(N, dtype=np.float32)
+    lib().orc_gemv_v11(_ptr(x), float(xs), _ptr(b), float(ws), K, N, _ptr(acc), _ptr(out))
+    return acc, out
+
+
+def gemm_v11(X: np.ndarray, xs: np.ndarray, v11: np.ndarray, ws: float, K: int, N: int):
+    """int8 X[M][K] (per-row scales xs[M]) times v11 W -> (int32 acc[M][N], fp32 out[M][N])."""
+    X = np.ascontiguousarray(X, dtype=np.int8)
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    b = np.ascontiguousarray(v11, dtype=np.uint8)
+    M = X.shape[0]
+    acc = np.empty((M, N), dtype=np.int32)
+    out = np.empty((M, N), dtype=np.float32)
+    lib().orc_gemm_v11(_ptr(X), _ptr(xs), M, _ptr(b), float(ws), K, N, _ptr(acc), _ptr(out))
+    return acc, out
+
+
+# --------------------------------------------------------------------------
+# Quantizers
+# --------------------------------------------------------------------------
+def quant_int8(x: np.ndarray) -> Tuple[np.ndarray, np.float32]:
+    """quant_int8_k (cuda/ter_cuda_forward_packed.cu:40-62): fp32 -> (int8, act_scale)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty(x.shape, dtype=np.int8)
+    s = np.zeros(1, dtype=np.float32)
+    lib().orc_quant_int8(_ptr(x), x.size, _ptr(q), _ptr(s))
+    return q, s[0]
+
+
+def quant_int8_rows(x: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    q = np.empty((M, K), dtype=np.int8)
+    s = np.empty(M, dtype=np.float32)
+    lib().orc_quant_int8_rows(_ptr(x), M, K, _ptr(q), _ptr(s))
+    return q, s
+
+
+def quantize_bitnet(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.size, dtype=np.int8)
+    s = lib().orc_quantize_bitnet(_ptr(x), x.size, _ptr(out))
+    return out, np.float32(s)
+
+
+def quantize_nt(x: np.ndarray, n_trits: int = 9):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.size, dtype=np.int32)
+    s = lib().orc_quantize_nt(_ptr(x), x.size, int(n_trits), _ptr(out))
+    return out, np.float32(s)
+
+
+def dequant_i2s(buf: np.ndarray, n: int) -> np.ndarray:
+    b = np.ascontiguousarray(buf, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    lib().orc_dequant_i2s(_ptr(b), n, _ptr(out))
+    return out
+
+
+def i2s_to_v11(raw: np.ndarray, K: int, N: int) -> np.ndarray:
+    b = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty((N // 4) * K, dtype=np.uint8)
+    rc = lib().orc_i2s_to_v11(_ptr(b), K, N, _ptr(out))
+    if rc != 0:
+        raise ValueError(f"orc_i2s_to_v11 rc={rc}")
+    return out
+
+
+def mm_row_tvmac(K: int, N: int) -> int:
+    return int(lib().orc_mm_row_tvmac(K, N))
+
+
+# --------------------------------------------------------------------------
+# The reference itself (oracle/_ref), for pinning the restatement and as the
+# CPU baseline.
+# --------------------------------------------------------------------------
+class RefMmRow:
+    """Holds reference TritTensors for X [rows][K] and W [K][N]; run() calls
+    the reference mm_row (src/tx/forward.cpp:299-352) only."""
+
+    def __init__(self, X: np.ndarray, xs: float, W: np.ndarray, ws: float,
+                 block_scales: Optional[np.ndarray] = None, block_size: int = 0):
+        X = np.ascontiguousarray(X, dtype=np.int32)
+        W = np.ascontiguousarray(W, dtype=np.int32)
+        if X.ndim == 1:
+            X = X.reshape(1, -1)
+        self.rows, self.K = X.shape
+        K2, self.N = W.shape
+        assert K2 == self.K
+        bs = None
+        if block_size > 0:
+            bs = np.ascontiguousarray(block_scales, dtype=np.float32)
+        self._h = ref().ter_ref_ctx_new(_ptr(X), self.rows, self.K, float(xs), _ptr(W), self.N,
+                                        float(ws), _ptr(bs) if bs is not None else None, int(block_size))
+        if not self._h:
+            raise MemoryError("ter_ref_ctx_new failed")
+        self.out = np.empty(self.N, dtype=np.float32)
+
+    def run(self, row: int = 0) -> np.ndarray:
+        rc = ref().ter_ref_ctx_run(self._h, int(row), _ptr(self.out))
+        if rc != 0:
+            raise RuntimeError(f"ter_ref_ctx_run rc={rc}")
+        return self.out
+
+    def tvmac(self) -> int:
+        return int(ref().ter_ref_ctx_tvmac(self._h))
+
+    def close(self):
+        if self._h:
+            ref().ter_ref_ctx_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def ref_quantize(x: np.ndarray, n_trits: int = 9):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.size, dtype=np.int32)
+    s = ref().ter_ref_quantize(_ptr(x), x.size, int(n_trits), _ptr(out))
+    return out, np.float32(s)
+
+
+def ref_quantize_bitnet(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.size, dtype=np.int8)
+    s = ref().ter_ref_quantize_bitnet(_ptr(x), x.size, _ptr(out))
+    return out, np.float32(s)
+
+
+# --------------------------------------------------------------------------
+# Portable seeded generators for test inputs (splitmix64; explicit integer ->
+# range mappings, so fixtures never depend on a C++ standard library's
+# distribution implementation).
+# --------------------------------------------------------------------------
+_M64 = (1 << 64) - 1
+
+
+def splitmix64(seed: int, n: int) -> np.ndarray:
+    """n outputs of splitmix64 starting from state `seed` (vectorised)."""
+    idx = np.arange(1, n + 1, dtype=np.uint64)
+    with np.errstate(over="ignore"):
+        z = np.uint64(seed & _M64) + idx * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    return z
+
+
+def rand_trits(seed: int, K: int, N: int, p_zero: float = 1.0 / 3.0) -> np.ndarray:
+    """Trits [K][N] in {-1,0,1}: P(0)=p_zero, P(+1)=P(-1)=(1-p_zero)/2."""
+    u = (splitmix64(seed, K * N) >> np.uint64(32)).astype(np.uint64)  # 32-bit uniform
+    t0 = np.uint64(int(round(p_zero * 2 ** 32)))
+    t1 = t0 + np.uint64(int(round((1.0 - p_zero) / 2.0 * 2 ** 32)))
+    w = np.where(u < t0, 0, np.where(u < t1, 1, -1)).astype(np.int8)
+    return w.reshape(K, N)
+
+
+def rand_int8(seed: int, n: int, lo: int = -127, hi: int = 127) -> np.ndarray:
+    u = (splitmix64(seed, n) >> np.uint64(32)).astype(np.uint64)
+    span = np.uint64(hi - lo + 1)
+    return ((u * span) >> np.uint64(32)).astype(np.int64).__add__(lo).astype(np.int8)
+
+
+def rand_normal_f32(seed: int, n: int) -> np.ndarray:
+    rng = np.random.Generator(np.random.PCG64(seed))
+    return rng.standard_normal(n, dtype=np.float32)
+
+
+def gemv_v11_cols(x: np.ndarray, xs: float, v11: np.ndarray, ws: float, K: int, N: int,
+                  byte_cols: np.ndarray):
+    """orc_gemv_v11 restricted to the v11 byte-columns `byte_cols` (each covers
+    output columns 4*jb .. 4*jb+3).  Returns (cols, acc, out) for those columns;
+    used to check full-size GEMVs on a sample of columns."""
+    jbs = np.asarray(sorted(set(int(j) for j in byte_cols)), dtype=np.int64)
+    v = np.ascontiguousarray(v11, dtype=np.uint8).reshape(N // 4, K)[jbs].reshape(-1)
+    acc, out = gemv_v11(x, xs, v, ws, K, 4 * len(jbs))
+    cols = (4 * jbs[:, None] + np.arange(4)[None, :]).reshape(-1)
+    return cols, acc, out

@@ -1,0 +1,316 @@
+/*
+ * ter_oracle.c -- CPU restatement of the reference ter hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP fabric in
+ * ter_amd/ is compared against.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it.  The product never links it and
+ * never falls back to it.
+ *
+ * Every function names the reference file:line it restates (paths relative
+ * to the xaskasdf/ter source tree).  The arithmetic follows the reference
+ * exactly: integer accumulation order does not matter (integer addition is
+ * associative), but every floating-point step is kept in the same order and
+ * precision as the reference so that fp32 outputs are bit-identical.
+ *
+ * Build: oracle/Makefile (gcc -O3 -mavx2 -mfma, the reference's own flags,
+ * CMakeLists.txt:28-30).  No -ffast-math and no FMA contraction.
+ *
+ * Parity pins (what checks each function; all in tests/):
+ *   orc_code_to_trit / orc_trit_to_code  -- tests/test_pack.cpp:8-15 and :29-33
+ *                                           restated as known answers.
+ *   orc_v11_pack / orc_v11_unpack        -- hand-derived byte known-answer tests,
+ *                                           the int4tc fixture of
+ *                                           cuda/ter_cuda_forward_packed_v13_int4tc.cu:512-547.
+ *   orc_mm_row                           -- oracle/_ref (the reference mm_row itself)
+ *                                           and the closed-form fixtures of
+ *                                           tests/test_kernel_matmul_b_small.cpp.
+ *   orc_mm_row_blocked                   -- oracle/_ref.
+ *   orc_gemv_v11                         -- equality with orc_mm_row on unpacked W.
+ *   orc_quant_int8                       -- closed-form tie / zero / amax cases.
+ *   orc_quantize_bitnet, orc_quantize_nt -- oracle/_ref.
+ *   orc_dequant_i2s                      -- tests/test_nt_dequant.cpp:37-61 block.
+ *   orc_i2s_to_v11                       -- decode equality with orc_dequant_i2s.
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#pragma STDC FP_CONTRACT OFF
+
+/* ------------------------------------------------------------------------ */
+/* 2-bit trit code map: include/ter/pack.hpp:8-21.                          */
+/* 00 = 0, 01 = +1, 10 = -1, 11 = 0 (reserved, decodes as zero).            */
+/* ------------------------------------------------------------------------ */
+int orc_code_to_trit(unsigned c) {
+    switch (c & 3u) {
+        case 1u: return +1;
+        case 2u: return -1;
+        default: return 0;
+    }
+}
+
+unsigned orc_trit_to_code(int t) { return t == 0 ? 0u : (t > 0 ? 1u : 2u); }
+
+/* ------------------------------------------------------------------------ */
+/* v11 column-major packed layout.                                          */
+/*   W_col[j_byte*K + k] holds output columns 4*j_byte .. 4*j_byte+3 at      */
+/*   input row k, column 4*j_byte+s at bits 2s..2s+1 (low bits = first col). */
+/* Packer: tools/convert_llama_to_packed.py:128-140.                         */
+/* Decoder: cuda/ter_cuda_forward_packed.cu:355-374 (byte at Wc = W_col +    */
+/* j_byte*K, code (b >> 2*sub) & 3 for column j_base+sub).                   */
+/* w_kn is the TritTensor payload orientation [K][N] row-major               */
+/* (src/host/load_gguf.cpp transpose_2d, src/tx/forward.cpp:337).            */
+/* ------------------------------------------------------------------------ */
+int orc_v11_pack(const int8_t* w_kn, int K, int N, uint8_t* out) {
+    if (K <= 0 || N <= 0 || (N % 4) != 0) return -5;
+    const int NB = N / 4;
+    for (int jb = 0; jb < NB; ++jb) {
+        for (int k = 0; k < K; ++k) {
+            unsigned b = 0;
+            for (int s = 0; s < 4; ++s)
+                b |= orc_trit_to_code(w_kn[(size_t)k * N + (size_t)(4 * jb + s)]) << (2 * s);
+            out[(size_t)jb * K + k] = (uint8_t)b;
+        }
+    }
+    return 0;
+}
+
+int orc_v11_unpack(const uint8_t* v11, int K, int N, int32_t* w_kn) {
+    if (K <= 0 || N <= 0 || (N % 4) != 0) return -5;
+    const int NB = N / 4;
+    for (int jb = 0; jb < NB; ++jb) {
+        const uint8_t* wc = v11 + (size_t)jb * K;
+        for (int k = 0; k < K; ++k) {
+            const unsigned b = wc[k];
+            for (int s = 0; s < 4; ++s)
+                w_kn[(size_t)k * N + (size_t)(4 * jb + s)] = orc_code_to_trit(b >> (2 * s));
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* mm_row, integer path: src/tx/forward.cpp:331-346.                         */
+/*   acc[j] = sum_k int64(X[row*K+k]) * int64(W[k*N+j]), k-outer / j-inner,  */
+/*   rows with X == 0 skipped (:334); s = Xt.scale * Wt.scale in fp32        */
+/*   (:342); out[j] = float(acc[j]) * s (:344).                              */
+/* acc_out (optional) receives the int64 accumulators.                      */
+/* ------------------------------------------------------------------------ */
+void orc_mm_row(const int32_t* X, int row, float xs, const int32_t* W, float ws,
+                int K, int N, int64_t* acc_out, float* out) {
+    int64_t* acc = acc_out ? acc_out : (int64_t*)malloc(sizeof(int64_t) * (size_t)N);
+    memset(acc, 0, sizeof(int64_t) * (size_t)N);
+    const int32_t* xp = X + (size_t)row * (size_t)K;
+    for (int k = 0; k < K; ++k) {
+        const int32_t xv = xp[k];
+        if (xv == 0) continue;
+        const int64_t xv64 = (int64_t)xv;
+        const int32_t* w_row = W + (size_t)k * (size_t)N;
+        for (int j = 0; j < N; ++j) acc[j] += xv64 * (int64_t)w_row[j];
+    }
+    const float s = xs * ws;
+    for (int j = 0; j < N; ++j) out[j] = (float)acc[j] * s;
+    if (!acc_out) free(acc);
+}
+
+/* ------------------------------------------------------------------------ */
+/* mm_row, per-block branch: src/tx/forward.cpp:308-330.                     */
+/* Double accumulation of xv * w * block_scales[(k*N+j)/bs]; out =           */
+/* float(facc * double(Xt.scale)).  The HIP boundary rejects per-block       */
+/* weights; this exists so the tests can state what is rejected.            */
+/* ------------------------------------------------------------------------ */
+void orc_mm_row_blocked(const int32_t* X, int row, float xs, const int32_t* W,
+                        const float* block_scales, int block_size, int K, int N,
+                        float* out) {
+    double* facc = (double*)calloc((size_t)N, sizeof(double));
+    const int32_t* xp = X + (size_t)row * (size_t)K;
+    for (int k = 0; k < K; ++k) {
+        const int32_t xv = xp[k];
+        if (xv == 0) continue;
+        const double xvd = (double)xv;
+        const size_t base = (size_t)k * (size_t)N;
+        const int32_t* w_row = W + base;
+        for (int j = 0; j < N; ++j) {
+            const size_t blk = (base + (size_t)j) / (size_t)block_size;
+            facc[j] += xvd * (double)w_row[j] * (double)block_scales[blk];
+        }
+    }
+    for (int j = 0; j < N; ++j) out[j] = (float)(facc[j] * (double)xs);
+    free(facc);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Packed GEMV semantics of mm_packed_v4 (v11 production kernel):            */
+/* cuda/ter_cuda_forward_packed.cu:346-397.  int8 X times v11-packed trits,  */
+/* int32 accumulation; out = float(acc) * (x_scale * w_scale) (:353,:393).   */
+/* The reference writes fp16; this fabric (and the oracle) keep fp32, which  */
+/* is the mm_row output type (src/tx/forward.cpp:344).                       */
+/* ------------------------------------------------------------------------ */
+void orc_gemv_v11(const int8_t* x, float xs, const uint8_t* v11, float ws, int K, int N,
+                  int32_t* acc_out, float* out) {
+    const int NB = N / 4;
+    const float s = xs * ws;
+    for (int jb = 0; jb < NB; ++jb) {
+        const uint8_t* wc = v11 + (size_t)jb * K;
+        int32_t acc[4] = {0, 0, 0, 0};
+        for (int k = 0; k < K; ++k) {
+            const int xv = x[k];
+            if (xv == 0) continue;
+            const unsigned b = wc[k];
+            for (int s2 = 0; s2 < 4; ++s2) acc[s2] += xv * orc_code_to_trit(b >> (2 * s2));
+        }
+        for (int s2 = 0; s2 < 4; ++s2) {
+            if (acc_out) acc_out[4 * jb + s2] = acc[s2];
+            if (out) out[4 * jb + s2] = (float)acc[s2] * s;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Batched semantics (M > 1): cuda/ter_cuda_addonly_batched.cu:31-124.        */
+/* X[M][K] int8 row-major, per-row activation scale X_scale[m];              */
+/* out[m*N+j] = float(acc[m][j]) * (X_scale[m] * w_scale) (:117-123).        */
+/* ------------------------------------------------------------------------ */
+void orc_gemm_v11(const int8_t* X, const float* xs, int M, const uint8_t* v11, float ws,
+                  int K, int N, int32_t* acc_out, float* out) {
+    for (int m = 0; m < M; ++m)
+        orc_gemv_v11(X + (size_t)m * K, xs[m], v11, ws, K, N,
+                     acc_out ? acc_out + (size_t)m * N : NULL,
+                     out ? out + (size_t)m * N : NULL);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Activation absmax -> int8 quantizer: quant_int8_k,                        */
+/* cuda/ter_cuda_forward_packed.cu:40-62 (same steps in the fused            */
+/* rmsnorm_quant_* prologues, cuda/ter_cuda_forward_bitnet.cu:94-103).       */
+/*   amax = max|x| + 1e-9f; scale = 127.f / amax;                            */
+/*   q = __float2int_rn(x * scale) (round half to even), clamped [-128,127]; */
+/*   act_scale = 1.f / scale.                                                */
+/* ------------------------------------------------------------------------ */
+void orc_quant_int8(const float* x, int n, int8_t* q, float* act_scale) {
+    float local = 0.f;
+    for (int i = 0; i < n; ++i) {
+        const float v = fabsf(x[i]);
+        if (v > local) local = v;
+    }
+    const float amax = local + 1e-9f;
+    const float scale = 127.0f / amax;
+    *act_scale = 1.0f / scale;
+    for (int i = 0; i < n; ++i) {
+        const float v = x[i] * scale;
+        int qi = (int)nearbyintf(v); /* default rounding mode: nearest-even */
+        if (qi > 127) qi = 127;
+        if (qi < -128) qi = -128;
+        q[i] = (int8_t)qi;
+    }
+}
+
+/* Per-row (per-token) variant used by the batched path: each row of X[M][K]
+ * is quantized independently with the quant_int8_k steps above
+ * (per-row X_scale of cuda/ter_cuda_addonly_batched.cu:33-38). */
+void orc_quant_int8_rows(const float* x, int M, int K, int8_t* q, float* act_scale) {
+    for (int m = 0; m < M; ++m)
+        orc_quant_int8(x + (size_t)m * K, K, q + (size_t)m * K, act_scale + m);
+}
+
+/* ------------------------------------------------------------------------ */
+/* BitNet absmean ternary quantizer: include/ter/bitnet.hpp:11-28.           */
+/* ------------------------------------------------------------------------ */
+float orc_quantize_bitnet(const float* in, size_t n, int8_t* out) {
+    if (n == 0) return 0.0f;
+    double sum_abs = 0.0;
+    for (size_t i = 0; i < n; ++i) sum_abs += fabs((double)in[i]);
+    const double scale = sum_abs / (double)n;
+    if (scale == 0.0) {
+        for (size_t i = 0; i < n; ++i) out[i] = 0;
+        return 0.0f;
+    }
+    for (size_t i = 0; i < n; ++i) {
+        const double q = (double)in[i] / scale;
+        long r = lround(q);
+        if (r > 1) r = 1;
+        if (r < -1) r = -1;
+        out[i] = (int8_t)r;
+    }
+    return (float)scale;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Format-B n-trit quantizer (TritTensor payload): src/numfmt/quantize.cpp:7-41 */
+/* scale = max|x| / ((3^n - 1)/2); payload = clamp(lround(x / scale)).       */
+/* Returns the scale (0 for an all-zero tensor; payload then all zero).      */
+/* ------------------------------------------------------------------------ */
+float orc_quantize_nt(const float* data, size_t n, int n_trits, int32_t* payload) {
+    int64_t mti = 1;
+    for (int i = 0; i < n_trits; ++i) mti *= 3;
+    mti = (mti - 1) / 2;
+    float max_abs = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        const float a = fabsf(data[i]);
+        if (a > max_abs) max_abs = a;
+    }
+    if (max_abs == 0.0f) {
+        memset(payload, 0, n * sizeof(int32_t));
+        return 0.0f;
+    }
+    const float scale = max_abs / (float)mti;
+    for (size_t i = 0; i < n; ++i) {
+        const float q = data[i] / scale;
+        int64_t r = (int64_t)lroundf(q);
+        if (r > mti) r = mti;
+        if (r < -mti) r = -mti;
+        payload[i] = (int32_t)r;
+    }
+    return scale;
+}
+
+/* ------------------------------------------------------------------------ */
+/* microsoft/BitNet i2_s decode: vendor/ntransformer/core/dequant.cpp:114-145 */
+/* 128-element blocks of 32 bytes; byte p holds positions p+32g at shift     */
+/* 6-2g; code map 0->-1, 1->0, 2->+1, 3->0; fp32 scale right after the codes. */
+/* ------------------------------------------------------------------------ */
+void orc_dequant_i2s(const uint8_t* src, size_t n_elems, float* out) {
+    static const float LUT[4] = {-1.0f, 0.0f, +1.0f, 0.0f};
+    float i2_scale = 1.0f;
+    memcpy(&i2_scale, src + n_elems / 4, sizeof(float));
+    const size_t n_blocks = n_elems / 128;
+    for (size_t blk = 0; blk < n_blocks; ++blk) {
+        const uint8_t* bb = src + blk * 32;
+        for (int p = 0; p < 32; ++p) {
+            const unsigned v = bb[p];
+            for (int g = 0; g < 4; ++g)
+                out[blk * 128 + (size_t)g * 32 + (size_t)p] = LUT[(v >> (6 - 2 * g)) & 3u] * i2_scale;
+        }
+    }
+    for (size_t i = n_blocks * 128; i < n_elems; ++i) out[i] = 0.0f;
+}
+
+/* ------------------------------------------------------------------------ */
+/* i2_s -> v11 repack: tools/convert_bitnet_to_packed.py:85-157.              */
+/* The GGUF tensor is (N, K) row-major (each row one output column's         */
+/* K-vector); microsoft codes are remapped with [2,0,1,0] to the ter code    */
+/* map, then packed to v11 (out[j_byte*K + k], low bits = first column).     */
+/* ------------------------------------------------------------------------ */
+int orc_i2s_to_v11(const uint8_t* raw, int K, int N, uint8_t* out) {
+    if (K <= 0 || N <= 0 || (K % 4) != 0 || (N % 4) != 0) return -5;
+    const size_t total = (size_t)N * (size_t)K;
+    if (total % 128 != 0) return -5;
+    static const uint8_t remap[4] = {2, 0, 1, 0};
+    memset(out, 0, total / 4);
+    for (size_t e = 0; e < total; ++e) {
+        const size_t blk = e / 128, pos = e % 128;
+        const size_t g = pos / 32, p = pos % 32;
+        const unsigned code = (raw[blk * 32 + p] >> (6 - 2 * g)) & 3u;
+        const unsigned ours = remap[code];
+        const size_t n = e / (size_t)K, k = e % (size_t)K;
+        out[(n / 4) * (size_t)K + k] |= (uint8_t)(ours << (2 * (n % 4)));
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Reference TVMAC accounting of mm_row: src/tx/forward.cpp:349-350.         */
+/* ------------------------------------------------------------------------ */
+uint64_t orc_mm_row_tvmac(int K, int N) { return (uint64_t)((K + 26) / 27) * (uint64_t)N; }

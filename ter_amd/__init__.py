@@ -1,0 +1,22 @@
+"""ter_amd -- MI355X (gfx950) packed-trit matmul fabric for ter.
+
+The hot path (packed-trit GEMV / batched GEMM) is hand-written HIP in
+ter_amd/csrc, exported through the C-ABI of include/ter_hip.h and bound here
+with ctypes.  See ter_amd.fabric for the host interface.
+"""
+from . import _lib  # noqa: F401
+from .fabric import (  # noqa: F401
+    Handle,
+    PackedTrits,
+    Plan,
+    gemv,
+    mm_batched,
+    mm_packed_dispatch,
+    mm_row,
+    quant_int8,
+    synth_i8,
+    synth_v11,
+)
+
+__all__ = ["Handle", "PackedTrits", "Plan", "gemv", "mm_batched", "mm_packed_dispatch", "mm_row",
+           "quant_int8", "synth_i8", "synth_v11"]

@@ -1,0 +1,142 @@
+"""ctypes bindings of libter_hip.so (the C-ABI declared in include/ter_hip.h).
+
+The library is loaded from the package directory only (it is built in-tree by
+ter_amd/build.py).  Loading fails loudly when it is missing: there is no
+Python or CPU fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libter_hip.so")
+
+# status codes (include/ter_hip.h)
+OK = 0
+ERR_NULL = -1
+ERR_NOTFOUND = -2
+ERR_ALLOC = -3
+ERR_NARGS = -4
+ERR_SHAPE = -5
+ERR_PAYLOAD = -6
+ERR_HIP = -7
+ERR_ALIGN = -8
+ERR_FULL = -9
+ERR_CONFLICT = -10
+
+K_MAX = 32768
+N_MAX = 1 << 24
+M_MAX = 256
+
+X_I8 = 0
+X_F32 = 1
+LAYOUT_T16 = 16
+
+
+class WPK(C.Structure):
+    """ter_hip_wpk_t -- the packed weight handle (replaces the reference's
+    WPK{data, scale, bytes}, cuda/ter_cuda_forward_packed.cu:400)."""
+    _fields_ = [
+        ("data", C.c_void_p),
+        ("bytes", C.c_size_t),
+        ("fix", C.c_void_p),
+        ("K", C.c_int32),
+        ("N", C.c_int32),
+        ("scale", C.c_float),
+        ("layout", C.c_int32),
+    ]
+
+
+class Act(C.Structure):
+    """ter_hip_act_t -- activation operand."""
+    _fields_ = [
+        ("data", C.c_void_p),
+        ("kind", C.c_int32),
+        ("scale", C.c_float),
+        ("scale_dev", C.c_void_p),
+        ("q_out", C.c_void_p),
+        ("scale_out", C.c_void_p),
+    ]
+
+
+class GemvItem(C.Structure):
+    _fields_ = [
+        ("w", C.POINTER(WPK)),
+        ("x", Act),
+        ("y", C.c_void_p),
+        ("acc", C.c_void_p),
+    ]
+
+
+class OpCounts(C.Structure):
+    _fields_ = [
+        ("total_ops", C.c_uint64),
+        ("tvmac", C.c_uint64),
+        ("tvadd", C.c_uint64),
+        ("tvsub", C.c_uint64),
+        ("tvmul", C.c_uint64),
+    ]
+
+
+NATIVE_FN = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(C.c_int64), C.c_size_t)
+
+# (name, restype, argtypes) for every exported symbol of include/ter_hip.h
+_P = C.c_void_p
+SIGNATURES = [
+    ("ter_hip_version", C.c_char_p, []),
+    ("ter_hip_last_error", C.c_char_p, []),
+    ("ter_hip_wpk_bytes", C.c_size_t, [C.c_int32, C.c_int32]),
+    ("ter_hip_wpk_init", C.c_int, [C.POINTER(WPK), _P, C.c_size_t, C.c_int32, C.c_int32, C.c_float]),
+    ("ter_hip_pack_v11", C.c_int, [C.POINTER(WPK), _P, _P]),
+    ("ter_hip_unpack_v11", C.c_int, [C.POINTER(WPK), _P, _P]),
+    ("ter_hip_pack_payload", C.c_int, [C.POINTER(WPK), _P, C.c_float, C.POINTER(C.c_int32), _P]),
+    ("ter_hip_gemv", C.c_int, [C.POINTER(WPK), C.POINTER(Act), _P, _P, _P]),
+    ("ter_hip_mm_packed_dispatch", C.c_int, [_P, _P, C.POINTER(WPK), _P, C.c_int32, C.c_int32, _P]),
+    ("ter_hip_mm_row", C.c_int, [_P, C.c_int32, C.c_int32, C.c_float, C.POINTER(WPK), C.c_int32, _P, _P, _P, _P]),
+    ("ter_hip_plan_create", C.c_int, [C.POINTER(C.c_void_p), C.POINTER(GemvItem), C.c_int32, C.c_int32]),
+    ("ter_hip_plan_launch", C.c_int, [_P, _P]),
+    ("ter_hip_plan_stats", C.c_int, [_P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_int32)]),
+    ("ter_hip_plan_destroy", None, [_P]),
+    ("ter_hip_gemm", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, _P, _P, _P]),
+    ("ter_hip_quant_int8", C.c_int, [_P, C.c_int32, C.c_int32, _P, _P, _P]),
+    ("ter_hip_create", _P, [C.c_int32]),
+    ("ter_hip_destroy", None, [_P]),
+    ("ter_hip_install_native", C.c_int, [_P, C.c_char_p, NATIVE_FN]),
+    ("ter_hip_call", C.c_int, [_P, C.c_char_p, C.POINTER(C.c_int64), C.c_size_t]),
+    ("ter_hip_op_counts", None, [_P, C.POINTER(OpCounts)]),
+    ("ter_hip_reset_counters", None, [_P]),
+    ("ter_hip_synth_v11", C.c_int, [_P, C.c_int32, C.c_int32, C.c_uint64, C.c_uint32, C.c_uint32, _P]),
+    ("ter_hip_synth_i8", C.c_int, [_P, C.c_int64, C.c_uint64, C.c_int32, C.c_int32, _P]),
+]
+
+_lib = None
+
+
+class TerHipError(RuntimeError):
+    def __init__(self, code: int, where: str):
+        msg = lib().ter_hip_last_error().decode(errors="replace")
+        super().__init__(f"{where} failed with status {code}: {msg}")
+        self.code = code
+
+
+def lib():
+    """Load libter_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m ter_amd.build` "
+                "(there is no fallback path)")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(code: int, where: str) -> None:
+    if code != OK:
+        raise TerHipError(code, where)

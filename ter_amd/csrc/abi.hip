@@ -1,0 +1,500 @@
+// abi.hip -- the extern "C" boundary (include/ter_hip.h).
+//
+// Validates every argument on the host before touching the device and
+// returns ter_k4-style status codes (src/k4/ter_k4.cpp:38,52-55); never
+// aborts.  There is no CPU compute path: a request the HIP kernels cannot
+// serve is an error.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace terhip {
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(TER_HIP_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_wpk(const ter_hip_wpk_t* w) {
+    if (!w || !w->data || !w->fix) return fail(TER_HIP_ERR_NULL, "null weight handle or buffer");
+    if (w->layout != TER_HIP_LAYOUT_T16) return fail(TER_HIP_ERR_PAYLOAD, "unknown weight layout %d", w->layout);
+    if (w->K < 1 || w->K > TER_HIP_K_MAX || w->N < 1 || w->N > TER_HIP_N_MAX)
+        return fail(TER_HIP_ERR_SHAPE, "weight shape K=%d N=%d out of range", w->K, w->N);
+    if (w->bytes < ter_hip_wpk_bytes(w->K, w->N)) return fail(TER_HIP_ERR_SHAPE, "weight buffer too small");
+    return TER_HIP_OK;
+}
+
+int check_act(const ter_hip_act_t* x, int M) {
+    if (!x || !x->data) return fail(TER_HIP_ERR_NULL, "null activation");
+    if (x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_F32)
+        return fail(TER_HIP_ERR_PAYLOAD, "unknown activation kind %d", x->kind);
+    if (x->kind == TER_HIP_X_F32 && !aligned(x->data, 4)) return fail(TER_HIP_ERR_ALIGN, "fp32 X misaligned");
+    if (M > 1 && x->kind == TER_HIP_X_I8 && !x->scale_dev)
+        return fail(TER_HIP_ERR_NULL, "batched int8 X needs per-row device scales");
+    return TER_HIP_OK;
+}
+
+std::mutex g_cu_mu;
+std::vector<int> g_cu;
+
+GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int32_t* acc, long long tile0) {
+    GemvDesc d{};
+    d.w = w->data;
+    d.x = x->data;
+    d.x_scale_dev = x->kind == TER_HIP_X_I8 ? x->scale_dev : nullptr;
+    d.y = y;
+    d.acc = acc;
+    d.xq_out = x->kind == TER_HIP_X_F32 ? x->q_out : nullptr;
+    d.xs_out = x->kind == TER_HIP_X_F32 ? x->scale_out : nullptr;
+    d.fix = reinterpret_cast<unsigned long long*>(w->fix);
+    d.tile0 = tile0;
+    d.K = w->K;
+    d.N = w->N;
+    d.Ku = units_of(w->K);
+    d.n_strips = strips_of(w->N);
+    d.w_scale = w->scale;
+    d.x_scale = x->scale;
+    d.x_kind = x->kind;
+    return d;
+}
+
+// Workgroups of one GEMV launch: every CU holds as many as fit at once
+// (occupancy query), so the static partition runs as a single wave of
+// resident workgroups.  wg_per_cu > 0 overrides (tuning).
+int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, int* n_wg) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const int cus = device_cu_count(dev);
+    if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
+    int per_cu = wg_per_cu;
+    if (per_cu <= 0) {
+        per_cu = gemv_max_wg_per_cu(lds_bytes);
+        if (per_cu <= 0) return fail(TER_HIP_ERR_HIP, "occupancy query failed");
+    }
+    long long g = (long long)cus * per_cu;
+    if (g > total_tiles) g = total_tiles;
+    if (g < 1) g = 1;
+    *n_wg = (int)g;
+    return TER_HIP_OK;
+}
+
+}  // namespace
+
+int device_cu_count(int device) {
+    std::lock_guard<std::mutex> lk(g_cu_mu);
+    if (device < 0) return -1;
+    if ((int)g_cu.size() <= device) g_cu.resize(device + 1, 0);
+    if (g_cu[device] == 0) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return -1;
+        g_cu[device] = v;
+    }
+    return g_cu[device];
+}
+
+}  // namespace terhip
+
+using namespace terhip;
+
+struct ter_hip_plan {
+    GemvDesc* descs_dev = nullptr;
+    int n = 0;
+    long long total_tiles = 0;
+    int n_wg = 0;
+    int lds_bytes = 0;
+    uint64_t bytes = 0, macs = 0;
+};
+
+struct ter_hip_handle {
+    int device = 0;
+    struct Slot {
+        char name[32];
+        ter_hip_native_fn fn;
+        bool used;
+    } slots[32];
+    ter_hip_op_counts_t counts;
+};
+
+extern "C" {
+
+const char* ter_hip_version(void) { return "ter_hip 0.1.0 (gfx950, T16 layout)"; }
+
+const char* ter_hip_last_error(void) { return g_last_error.c_str(); }
+
+size_t ter_hip_wpk_bytes(int32_t K, int32_t N) {
+    if (K < 1 || N < 1) return 0;
+    return tile_stream_bytes(K, N) + (size_t)N * sizeof(uint64_t);
+}
+
+int ter_hip_wpk_init(ter_hip_wpk_t* w, void* dev_buf, size_t buf_bytes, int32_t K, int32_t N, float scale) {
+    if (!w || !dev_buf) return fail(TER_HIP_ERR_NULL, "null weight handle or buffer");
+    if (K < 1 || K > TER_HIP_K_MAX || N < 1 || N > TER_HIP_N_MAX)
+        return fail(TER_HIP_ERR_SHAPE, "shape K=%d N=%d out of range (K<=%d)", K, N, TER_HIP_K_MAX);
+    if (!aligned(dev_buf, 256)) return fail(TER_HIP_ERR_ALIGN, "weight buffer must be 256-byte aligned");
+    const size_t need = ter_hip_wpk_bytes(K, N);
+    if (buf_bytes < need) return fail(TER_HIP_ERR_SHAPE, "weight buffer %zu < %zu bytes", buf_bytes, need);
+    w->data = static_cast<uint8_t*>(dev_buf);
+    w->bytes = need;
+    w->fix = reinterpret_cast<uint64_t*>(w->data + fix_offset(K, N));
+    w->K = K;
+    w->N = N;
+    w->scale = scale;
+    w->layout = TER_HIP_LAYOUT_T16;
+    return TER_HIP_OK;
+}
+
+int ter_hip_pack_v11(ter_hip_wpk_t* w, const uint8_t* v11_dev, void* stream) {
+    int rc = check_wpk(w);
+    if (rc) return rc;
+    if (!v11_dev) return fail(TER_HIP_ERR_NULL, "null v11 buffer");
+    if (w->N % 4) return fail(TER_HIP_ERR_SHAPE, "v11 needs N %% 4 == 0 (N=%d)", w->N);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = launch_pack_v11(v11_dev, w->data, w->K, w->N, st);
+    if (e != hipSuccess) return hip_fail(e, "pack_v11 launch");
+    e = hipMemsetAsync(w->fix, 0, (size_t)w->N * sizeof(uint64_t), st);
+    if (e != hipSuccess) return hip_fail(e, "fix-up slot clear");
+    return TER_HIP_OK;
+}
+
+int ter_hip_unpack_v11(const ter_hip_wpk_t* w, uint8_t* v11_dev, void* stream) {
+    int rc = check_wpk(w);
+    if (rc) return rc;
+    if (!v11_dev) return fail(TER_HIP_ERR_NULL, "null v11 buffer");
+    if (w->N % 4) return fail(TER_HIP_ERR_SHAPE, "v11 needs N %% 4 == 0 (N=%d)", w->N);
+    hipError_t e = launch_unpack_v11(w->data, v11_dev, w->K, w->N, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "unpack_v11 launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_pack_payload(ter_hip_wpk_t* w, const int32_t* payload, float scale, int32_t* magnitude_out,
+                         void* stream) {
+    int rc = check_wpk(w);
+    if (rc) return rc;
+    if (!payload) return fail(TER_HIP_ERR_NULL, "null payload");
+    const int K = w->K, N = w->N;
+    const size_t n = (size_t)K * (size_t)N;
+    int64_t m = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const int64_t a = payload[i] < 0 ? -(int64_t)payload[i] : (int64_t)payload[i];
+        if (a == 0) continue;
+        if (m == 0) m = a;
+        else if (a != m)
+            return fail(TER_HIP_ERR_PAYLOAD, "payload not ternary: |%lld| vs |%lld| at %zu", (long long)a,
+                        (long long)m, i);
+    }
+    const int Ku = units_of(K), ns = strips_of(N);
+    std::vector<uint32_t> host;
+    try {
+        host.assign(tile_stream_bytes(K, N) / 4, 0u);
+    } catch (...) {
+        return fail(TER_HIP_ERR_ALLOC, "host staging allocation");
+    }
+    for (int s = 0; s < ns; ++s)
+        for (int u = 0; u < Ku; ++u)
+            for (int lane = 0; lane < 64; ++lane)
+                for (int j = 0; j < 4; ++j) {
+                    const int r = lane >> 4, q = lane & 15;
+                    const int col = s * kStripCols + r * 4 + j;
+                    const int k0 = u * kUnitK + q * 16;
+                    uint32_t out = 0;
+                    for (int e = 0; e < 16; ++e) {
+                        const int k = k0 + e;
+                        uint32_t uv = 1u;
+                        if (col < N && k < K) {
+                            const int32_t p = payload[(size_t)k * N + col];
+                            uv = p > 0 ? 2u : (p < 0 ? 0u : 1u);
+                        }
+                        out |= uv << (8 * (e & 3) + 2 * (e >> 2));
+                    }
+                    host[(((size_t)s * Ku + u) * 64 + lane) * 4 + j] = out;
+                }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(w->data, host.data(), host.size() * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipMemsetAsync(w->fix, 0, (size_t)N * sizeof(uint64_t), st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "payload upload");
+    w->scale = scale * (float)(m == 0 ? 1 : m);
+    if (magnitude_out) *magnitude_out = (int32_t)(m == 0 ? 1 : m);
+    return TER_HIP_OK;
+}
+
+int ter_hip_gemv(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int32_t* acc, void* stream) {
+    int rc = check_wpk(w);
+    if (rc) return rc;
+    rc = check_act(x, 1);
+    if (rc) return rc;
+    if (!y && !acc) return fail(TER_HIP_ERR_NULL, "no output buffer");
+    const GemvDesc d = make_desc(w, x, y, acc, 0);
+    const long long total = (long long)d.n_strips * d.Ku;
+    int n_wg = 0;
+    const int lds = gemv_lds_bytes(w->K);
+    rc = pick_wg(total, 0, lds, &n_wg);
+    if (rc) return rc;
+    hipError_t e = launch_gemv(d, nullptr, 0, total, n_wg, lds, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "gemv launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_mm_packed_dispatch(const int8_t* X, const float* scale_x_dev, const ter_hip_wpk_t* W, float* out,
+                               int32_t K, int32_t N, void* stream) {
+    if (!X || !scale_x_dev || !W || !out) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (W->K != K || W->N != N) return fail(TER_HIP_ERR_SHAPE, "K/N (%d,%d) do not match W (%d,%d)", K, N, W->K, W->N);
+    ter_hip_act_t x{};
+    x.data = X;
+    x.kind = TER_HIP_X_I8;
+    x.scale_dev = scale_x_dev;
+    return ter_hip_gemv(W, &x, out, nullptr, stream);
+}
+
+int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale, const ter_hip_wpk_t* W, int32_t N,
+                   float* out, int8_t* x_stage_dev, float* y_stage_dev, void* stream) {
+    if (!X || !W || !out || !x_stage_dev || !y_stage_dev) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (row < 0) return fail(TER_HIP_ERR_SHAPE, "negative row");
+    if (W->K != K || W->N != N) return fail(TER_HIP_ERR_SHAPE, "K/N (%d,%d) do not match W (%d,%d)", K, N, W->K, W->N);
+    std::vector<int8_t> xb((size_t)K);
+    const int32_t* xr = X + (size_t)row * (size_t)K;
+    for (int k = 0; k < K; ++k) {
+        if (xr[k] < -128 || xr[k] > 127)
+            return fail(TER_HIP_ERR_PAYLOAD, "X[%d]=%d does not fit int8 (no CPU fallback)", k, xr[k]);
+        xb[(size_t)k] = (int8_t)xr[k];
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(x_stage_dev, xb.data(), (size_t)K, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return hip_fail(e, "X upload");
+    ter_hip_act_t x{};
+    x.data = x_stage_dev;
+    x.kind = TER_HIP_X_I8;
+    x.scale = x_scale;
+    int rc = ter_hip_gemv(W, &x, y_stage_dev, nullptr, stream);
+    if (rc) return rc;
+    e = hipMemcpyAsync(out, y_stage_dev, (size_t)N * sizeof(float), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "y download");
+    return TER_HIP_OK;
+}
+
+int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items, int32_t n, int32_t wg_per_cu) {
+    if (!plan || !items) return fail(TER_HIP_ERR_NULL, "null plan or items");
+    *plan = nullptr;
+    if (n < 1) return fail(TER_HIP_ERR_SHAPE, "empty work list");
+    std::vector<GemvDesc> ds((size_t)n);
+    long long tile = 0;
+    uint64_t bytes = 0, macs = 0;
+    int lds = 0;
+    for (int i = 0; i < n; ++i) {
+        const ter_hip_gemv_item_t& it = items[i];
+        int rc = check_wpk(it.w);
+        if (rc) return rc;
+        rc = check_act(&it.x, 1);
+        if (rc) return rc;
+        if (!it.y && !it.acc) return fail(TER_HIP_ERR_NULL, "item %d has no output", i);
+        for (int k = 0; k < i; ++k)
+            if (items[k].w->fix == it.w->fix)
+                return fail(TER_HIP_ERR_CONFLICT, "weight of item %d repeats item %d", i, k);
+        ds[(size_t)i] = make_desc(it.w, &it.x, it.y, it.acc, tile);
+        tile += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
+        const int lb = gemv_lds_bytes(it.w->K);
+        if (lb > lds) lds = lb;
+        bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 +
+                 (uint64_t)it.w->K * (it.x.kind == TER_HIP_X_F32 ? 4u : 1u) + (uint64_t)it.w->N * 4u;
+        macs += (uint64_t)it.w->K * (uint64_t)it.w->N;
+    }
+    int n_wg = 0;
+    int rc = pick_wg(tile, wg_per_cu, lds, &n_wg);
+    if (rc) return rc;
+    ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
+    if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
+    hipError_t e = hipMalloc(&p->descs_dev, sizeof(GemvDesc) * (size_t)n);
+    if (e != hipSuccess) {
+        delete p;
+        return hip_fail(e, "plan descriptor allocation");
+    }
+    e = hipMemcpy(p->descs_dev, ds.data(), sizeof(GemvDesc) * (size_t)n, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(p->descs_dev);
+        delete p;
+        return hip_fail(e, "plan descriptor upload");
+    }
+    p->n = n;
+    p->total_tiles = tile;
+    p->n_wg = n_wg;
+    p->lds_bytes = lds;
+    p->bytes = bytes;
+    p->macs = macs;
+    *plan = p;
+    return TER_HIP_OK;
+}
+
+int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
+    if (!plan) return fail(TER_HIP_ERR_NULL, "null plan");
+    GemvDesc none{};
+    hipError_t e = launch_gemv(none, plan->descs_dev, plan->n, plan->total_tiles, plan->n_wg, plan->lds_bytes,
+                               static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "plan launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_plan_stats(const ter_hip_plan_t* plan, uint64_t* bytes, uint64_t* macs, int32_t* n_wg) {
+    if (!plan) return fail(TER_HIP_ERR_NULL, "null plan");
+    if (bytes) *bytes = plan->bytes;
+    if (macs) *macs = plan->macs;
+    if (n_wg) *n_wg = plan->n_wg;
+    return TER_HIP_OK;
+}
+
+void ter_hip_plan_destroy(ter_hip_plan_t* plan) {
+    if (!plan) return;
+    (void)hipFree(plan->descs_dev);
+    delete plan;
+}
+
+int ter_hip_quant_int8(const float* x, int32_t M, int32_t K, int8_t* q, float* scale_out, void* stream) {
+    if (!x || !q || !scale_out) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (M < 1 || K < 1 || K > TER_HIP_K_MAX || M > 65535) return fail(TER_HIP_ERR_SHAPE, "M=%d K=%d out of range", M, K);
+    if (!aligned(x, 4)) return fail(TER_HIP_ERR_ALIGN, "fp32 X misaligned");
+    hipError_t e = launch_quant_rows(x, M, K, q, scale_out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "quant launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, float* y, int32_t* acc, void* stream) {
+    int rc = check_wpk(w);
+    if (rc) return rc;
+    if (M < 1 || M > TER_HIP_M_MAX) return fail(TER_HIP_ERR_SHAPE, "M=%d out of range [1,%d]", M, TER_HIP_M_MAX);
+    rc = check_act(x, M);
+    if (rc) return rc;
+    if (!y && !acc) return fail(TER_HIP_ERR_NULL, "no output buffer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int8_t* xq = static_cast<const int8_t*>(x->data);
+    const float* xs = x->scale_dev;
+    if (x->kind == TER_HIP_X_F32) {
+        if (!x->q_out || !x->scale_out)
+            return fail(TER_HIP_ERR_NULL, "fp32 batched X needs q_out and scale_out workspaces");
+        rc = ter_hip_quant_int8(static_cast<const float*>(x->data), M, w->K, x->q_out, x->scale_out, stream);
+        if (rc) return rc;
+        xq = x->q_out;
+        xs = x->scale_out;
+    }
+    hipError_t e = launch_gemm(w->data, w->K, w->N, xq, xs, M, w->scale, y, acc, st);
+    if (e != hipSuccess) return hip_fail(e, "gemm launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_synth_v11(uint8_t* v11_dev, int32_t K, int32_t N, uint64_t seed, uint32_t t0, uint32_t t1, void* stream) {
+    if (!v11_dev) return fail(TER_HIP_ERR_NULL, "null buffer");
+    if (K < 1 || N < 4 || N % 4) return fail(TER_HIP_ERR_SHAPE, "K=%d N=%d", K, N);
+    hipError_t e = launch_synth_v11(v11_dev, K, N, seed, t0, t1, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "synth launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_synth_i8(int8_t* x_dev, int64_t n, uint64_t seed, int32_t lo, int32_t hi, void* stream) {
+    if (!x_dev) return fail(TER_HIP_ERR_NULL, "null buffer");
+    if (n < 1 || lo > hi || lo < -128 || hi > 127) return fail(TER_HIP_ERR_SHAPE, "bad range");
+    hipError_t e = launch_synth_i8(x_dev, n, seed, lo, hi, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "synth launch");
+    return TER_HIP_OK;
+}
+
+// ---- K4-style handle + KernelTable native slot -------------------------
+
+static int native_matmul(ter_hip_handle_t* h, const int64_t* args, size_t n_args) {
+    if (n_args < 6) return fail(TER_HIP_ERR_NARGS, "tk_matmul_b_9t needs 6 args, got %zu", n_args);
+    const ter_hip_wpk_t* w = reinterpret_cast<const ter_hip_wpk_t*>(static_cast<intptr_t>(args[0]));
+    const ter_hip_act_t* x = reinterpret_cast<const ter_hip_act_t*>(static_cast<intptr_t>(args[1]));
+    float* y = reinterpret_cast<float*>(static_cast<intptr_t>(args[2]));
+    int32_t* acc = reinterpret_cast<int32_t*>(static_cast<intptr_t>(args[3]));
+    void* stream = reinterpret_cast<void*>(static_cast<intptr_t>(args[4]));
+    const int64_t M = args[5];
+    if (!w) return fail(TER_HIP_ERR_NULL, "null weight");
+    if (M < 1 || M > TER_HIP_M_MAX) return fail(TER_HIP_ERR_SHAPE, "M=%lld", (long long)M);
+    const int rc = M == 1 ? ter_hip_gemv(w, x, y, acc, stream) : ter_hip_gemm(w, x, (int32_t)M, y, acc, stream);
+    if (rc == TER_HIP_OK) {
+        const uint64_t n = (uint64_t)((w->K + 26) / 27) * (uint64_t)w->N * (uint64_t)M;
+        h->counts.tvmac += n;
+        h->counts.total_ops += n;
+    }
+    return rc;
+}
+
+ter_hip_handle_t* ter_hip_create(int32_t device) {
+    ter_hip_handle_t* h = new (std::nothrow) ter_hip_handle_t();
+    if (!h) return nullptr;
+    std::memset(h, 0, sizeof *h);
+    h->device = device;
+    if (ter_hip_install_native(h, "tk_matmul_b_9t", native_matmul) != TER_HIP_OK) {
+        delete h;
+        return nullptr;
+    }
+    return h;
+}
+
+void ter_hip_destroy(ter_hip_handle_t* h) { delete h; }
+
+int ter_hip_install_native(ter_hip_handle_t* h, const char* name, ter_hip_native_fn fn) {
+    if (!h || !name || !fn) return fail(TER_HIP_ERR_NULL, "null handle, name or function");
+    for (auto& s : h->slots)
+        if (s.used && std::strncmp(s.name, name, sizeof s.name - 1) == 0) {
+            s.fn = fn;
+            return TER_HIP_OK;
+        }
+    for (auto& s : h->slots) {
+        if (s.used) continue;
+        std::strncpy(s.name, name, sizeof s.name - 1);
+        s.name[sizeof s.name - 1] = '\0';
+        s.fn = fn;
+        s.used = true;
+        return TER_HIP_OK;
+    }
+    return fail(TER_HIP_ERR_FULL, "kernel table full (32 slots)");
+}
+
+int ter_hip_call(ter_hip_handle_t* h, const char* name, const int64_t* args, size_t n_args) {
+    if (!h || !name) return fail(TER_HIP_ERR_NULL, "null handle or name");
+    if (n_args > 7) return fail(TER_HIP_ERR_NARGS, "at most 7 args (R1..R7), got %zu", n_args);
+    if (n_args > 0 && !args) return fail(TER_HIP_ERR_NULL, "null args");
+    for (auto& s : h->slots)
+        if (s.used && std::strncmp(s.name, name, sizeof s.name) == 0) {
+            if (h->device >= 0) {
+                hipError_t e = hipSetDevice(h->device);
+                if (e != hipSuccess) return hip_fail(e, "hipSetDevice");
+            }
+            return s.fn(h, args, n_args);
+        }
+    return fail(TER_HIP_ERR_NOTFOUND, "no kernel named '%s'", name);
+}
+
+void ter_hip_op_counts(const ter_hip_handle_t* h, ter_hip_op_counts_t* out) {
+    if (!h || !out) return;
+    *out = h->counts;
+}
+
+void ter_hip_reset_counters(ter_hip_handle_t* h) {
+    if (h) std::memset(&h->counts, 0, sizeof h->counts);
+}
+
+}  // extern "C"

@@ -1,0 +1,76 @@
+// common.h -- shared definitions of the gfx950 packed-trit fabric.
+//
+// T16 tile layout (the HBM format every M=1 kernel streams):
+//   A K x N ternary matrix is cut into column strips of 16 output columns and
+//   units of 256 input rows.  Tile (strip s, unit u) is 1024 contiguous bytes
+//   at offset (s * Ku + u) * 1024, Ku = ceil(K / 256); strips are stored one
+//   after another, each strip's tiles in increasing u.
+//   Inside a tile, lane L = 0..63 of a wave64 owns bytes [16L, 16L + 16):
+//     row r = L / 16 -> output columns 16 s + 4 r + j   (j = 0..3, dword j)
+//     q     = L % 16 -> input rows    k0 = 256 u + 16 q .. k0 + 15
+//   Dword j holds 16 trits of column 16 s + 4 r + j: the trit of input row
+//   k0 + 4 f + b sits in byte b (0..3), bits 2f..2f+1 (f = 0..3), encoded as
+//   u = w + 1 in {0, 1, 2}.  Padding rows/columns hold u = 1 (w = 0).
+//   With that order, (dword >> 2f) & 0x03030303 is an int8x4 of u for the
+//   four consecutive rows k0 + 4f .. k0 + 4f + 3, which pair with the int8x4
+//   activation dword X[k0 + 4f .. k0 + 4f + 3] in one v_dot4.
+//   sum_k x_k w_kj = sum_k x_k u_kj - sum_k x_k, so the kernels subtract the
+//   activation sum of each 256-row unit once per column strip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ter_hip.h"
+
+namespace terhip {
+
+constexpr int kTileBytes = 1024;
+constexpr int kStripCols = 16;
+constexpr int kUnitK = 256;
+constexpr int kWaves = 4;                 // waves per workgroup of the GEMV kernel
+constexpr int kThreads = 64 * kWaves;
+
+inline int32_t units_of(int32_t K) { return (K + kUnitK - 1) / kUnitK; }
+inline int32_t strips_of(int32_t N) { return (N + kStripCols - 1) / kStripCols; }
+inline size_t tile_stream_bytes(int32_t K, int32_t N) {
+    return (size_t)strips_of(N) * (size_t)units_of(K) * kTileBytes;
+}
+inline size_t fix_offset(int32_t K, int32_t N) { return tile_stream_bytes(K, N); }
+
+// One GEMV of a work list, as the kernel reads it (device memory or kernarg).
+struct alignas(16) GemvDesc {
+    const uint8_t* w;            // T16 tile stream
+    const void* x;               // int8 [K] or fp32 [K]
+    const float* x_scale_dev;    // int8 input: device activation scale or null
+    float* y;                    // fp32 [N] or null
+    int32_t* acc;                // int32 [N] or null
+    int8_t* xq_out;              // fp32 input: quantized X copy or null
+    float* xs_out;               // fp32 input: activation scale copy or null
+    unsigned long long* fix;     // N fix-up slots, zero at rest
+    long long tile0;             // first tile of this GEMV in the launch's stream
+    int32_t K, N, Ku, n_strips;
+    float w_scale, x_scale;
+    int32_t x_kind, pad_;
+};
+
+// Host launchers (defined in the .hip files).
+hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, int n_list,
+                       long long total_tiles, int n_wg, int lds_bytes, hipStream_t st);
+hipError_t launch_pack_v11(const uint8_t* v11, uint8_t* t16, int K, int N, hipStream_t st);
+hipError_t launch_unpack_v11(const uint8_t* t16, uint8_t* v11, int K, int N, hipStream_t st);
+hipError_t launch_synth_v11(uint8_t* v11, int K, int N, uint64_t seed, uint32_t t0, uint32_t t1,
+                            hipStream_t st);
+hipError_t launch_synth_i8(int8_t* x, long long n, uint64_t seed, int lo, int hi, hipStream_t st);
+hipError_t launch_quant_rows(const float* x, int M, int K, int8_t* q, float* s, hipStream_t st);
+hipError_t launch_gemm(const uint8_t* w, int K, int N, const int8_t* xq, const float* xs, int M,
+                       float w_scale, float* y, int32_t* acc, hipStream_t st);
+
+// LDS bytes the GEMV kernel needs for a K: X (Ku*256 int8) + unit sums + scratch.
+inline int gemv_lds_bytes(int32_t K) { return units_of(K) * kUnitK + units_of(K) * 4 + 64; }
+
+int device_cu_count(int device);
+// Resident GEMV workgroups per CU at this LDS size (0 if the query fails).
+int gemv_max_wg_per_cu(int lds_bytes);
+
+}  // namespace terhip

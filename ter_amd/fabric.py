@@ -1,0 +1,305 @@
+"""Host-side interface of the gfx950 packed-trit fabric.
+
+Mirrors the reference's operator surface for this path, over the C-ABI of
+include/ter_hip.h (ctypes).  PyTorch is used only for device memory and
+streams.
+
+Reference names kept:
+  PackedTrits           <- WPK{data, scale, bytes}       cuda/ter_cuda_forward_packed.cu:400
+  mm_packed_dispatch    <- mm_packed_dispatch(...)       cuda/ter_cuda_forward_packed.cu:493-500
+  mm_row                <- mm_row(sim, kt, id, Xt, row, Wt, K, N, out)   src/tx/forward.cpp:299-352
+  mm_batched            <- mm_bitnet_addonly_batched_k<M>(...)          cuda/ter_cuda_addonly_batched.cu:31-124
+  quant_int8            <- quant_int8_k(x, y, scale_out, N)             cuda/ter_cuda_forward_packed.cu:40-62
+  Handle                <- ter_k4_create/call/op_counts/...             include/ter_k4/ter_k4.h:29-55
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+from . import _lib as L
+
+
+def _torch():
+    import torch  # imported lazily: the C-ABI checks below need no device
+    return torch
+
+
+def _ptr(t) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream=None) -> Optional[int]:
+    if stream is not None:
+        return stream
+    torch = _torch()
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _require_cuda(t, name: str, dtype=None, numel: Optional[int] = None):
+    torch = _torch()
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a CUDA (HIP) tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if numel is not None and t.numel() < numel:
+        raise ValueError(f"{name} holds {t.numel()} elements, needs {numel}")
+
+
+class PackedTrits:
+    """A K x N ternary weight resident on the device in the T16 tile layout.
+
+    Built from reference v11 bytes (the packed wire format of
+    tools/convert_llama_to_packed.py:128-140) or from a TritTensor payload
+    (int32 [K][N], include/ter/numfmt.hpp:17-36)."""
+
+    def __init__(self, K: int, N: int, scale: float, device=None):
+        torch = _torch()
+        self.K, self.N = int(K), int(N)
+        nbytes = L.lib().ter_hip_wpk_bytes(self.K, self.N)
+        if nbytes == 0:
+            raise ValueError(f"bad shape K={K} N={N}")
+        self.buf = torch.empty(nbytes, dtype=torch.uint8, device=device or "cuda")
+        self.wpk = L.WPK()
+        L.check(L.lib().ter_hip_wpk_init(C.byref(self.wpk), self.buf.data_ptr(), nbytes, self.K, self.N,
+                                         float(scale)), "ter_hip_wpk_init")
+        self.magnitude = 1
+
+    @property
+    def scale(self) -> float:
+        return self.wpk.scale
+
+    @property
+    def nbytes_packed(self) -> int:
+        """Algorithmic packed bytes K*N/4 (the reference GB/s convention)."""
+        return self.K * self.N // 4
+
+    @classmethod
+    def from_v11(cls, v11, K: int, N: int, scale: float, stream=None) -> "PackedTrits":
+        torch = _torch()
+        if isinstance(v11, np.ndarray):
+            v11 = torch.from_numpy(np.ascontiguousarray(v11, dtype=np.uint8)).cuda()
+        _require_cuda(v11, "v11", torch.uint8, (N // 4) * K)
+        w = cls(K, N, scale, device=v11.device)
+        L.check(L.lib().ter_hip_pack_v11(C.byref(w.wpk), v11.data_ptr(), _stream(stream)), "ter_hip_pack_v11")
+        return w
+
+    @classmethod
+    def from_payload(cls, payload: np.ndarray, scale: float, stream=None) -> "PackedTrits":
+        p = np.ascontiguousarray(payload, dtype=np.int32)
+        K, N = p.shape
+        w = cls(K, N, scale)
+        m = C.c_int32(0)
+        L.check(L.lib().ter_hip_pack_payload(C.byref(w.wpk), p.ctypes.data, float(scale), C.byref(m),
+                                             _stream(stream)), "ter_hip_pack_payload")
+        w.magnitude = m.value
+        return w
+
+    def to_v11(self, stream=None):
+        torch = _torch()
+        out = torch.empty((self.N // 4) * self.K, dtype=torch.uint8, device=self.buf.device)
+        L.check(L.lib().ter_hip_unpack_v11(C.byref(self.wpk), out.data_ptr(), _stream(stream)),
+                "ter_hip_unpack_v11")
+        return out
+
+
+def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None) -> L.Act:
+    torch = _torch()
+    a = L.Act()
+    a.data = x.data_ptr()
+    if x.dtype == torch.int8:
+        a.kind = L.X_I8
+        a.scale = float(x_scale) if x_scale is not None else 1.0
+        a.scale_dev = _ptr(x_scale_dev)
+    elif x.dtype == torch.float32:
+        a.kind = L.X_F32
+        a.q_out = _ptr(q_out)
+        a.scale_out = _ptr(scale_out)
+    else:
+        raise TypeError(f"activations must be int8 or float32, got {x.dtype}")
+    return a
+
+
+def gemv(W: PackedTrits, x, y=None, acc=None, x_scale: Optional[float] = None, x_scale_dev=None,
+         q_out=None, scale_out=None, stream=None):
+    """M = 1 GEMV.  x: int8 [K] (with x_scale or x_scale_dev) or fp32 [K]
+    (absmax-quantized in the kernel prologue).  Returns (y, acc)."""
+    torch = _torch()
+    _require_cuda(x, "x", None, W.K)
+    if y is None and acc is None:
+        y = torch.empty(W.N, dtype=torch.float32, device=x.device)
+    a = _act(x, x_scale, x_scale_dev, q_out, scale_out)
+    L.check(L.lib().ter_hip_gemv(C.byref(W.wpk), C.byref(a), _ptr(y), _ptr(acc), _stream(stream)),
+            "ter_hip_gemv")
+    return y, acc
+
+
+def mm_packed_dispatch(X, scale_x_dev, W: PackedTrits, out, K: int, N: int, stream=None):
+    """The reference launcher signature (cuda/ter_cuda_forward_packed.cu:493-500),
+    fp32 out instead of fp16."""
+    torch = _torch()
+    _require_cuda(X, "X", torch.int8, K)
+    _require_cuda(scale_x_dev, "scale_x_dev", torch.float32, 1)
+    _require_cuda(out, "out", torch.float32, N)
+    L.check(L.lib().ter_hip_mm_packed_dispatch(X.data_ptr(), scale_x_dev.data_ptr(), C.byref(W.wpk),
+                                               out.data_ptr(), int(K), int(N), _stream(stream)),
+            "ter_hip_mm_packed_dispatch")
+    return out
+
+
+def mm_row(Xt_payload: np.ndarray, row: int, x_scale: float, W: PackedTrits, K: int, N: int) -> np.ndarray:
+    """The mm_row contract (src/tx/forward.cpp:299-352): host TritTensor
+    payload X (int32 [rows][K]) -> host fp32 out[N].  X must fit int8."""
+    torch = _torch()
+    X = np.ascontiguousarray(Xt_payload, dtype=np.int32)
+    out = np.empty(N, dtype=np.float32)
+    xs = torch.empty(K, dtype=torch.int8, device=W.buf.device)
+    ys = torch.empty(N, dtype=torch.float32, device=W.buf.device)
+    L.check(L.lib().ter_hip_mm_row(X.ctypes.data, int(row), int(K), float(x_scale), C.byref(W.wpk), int(N),
+                                   out.ctypes.data, xs.data_ptr(), ys.data_ptr(), _stream(None)),
+            "ter_hip_mm_row")
+    return out
+
+
+def quant_int8(x, q=None, scale_out=None, stream=None):
+    """Per-row absmax int8 quantization of fp32 x [M][K] (quant_int8_k steps)."""
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    if q is None:
+        q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if scale_out is None:
+        scale_out = torch.empty(M, dtype=torch.float32, device=x.device)
+    L.check(L.lib().ter_hip_quant_int8(x2.data_ptr(), M, K, q.data_ptr(), scale_out.data_ptr(), _stream(stream)),
+            "ter_hip_quant_int8")
+    return q, scale_out
+
+
+def mm_batched(W: PackedTrits, X, y=None, acc=None, x_scale_dev=None, q_out=None, scale_out=None, stream=None):
+    """M > 1 GEMM on MFMA.  X: int8 [M][K] with per-row device scales
+    x_scale_dev [M], or fp32 [M][K] (rows quantized into q_out/scale_out,
+    allocated here when absent).  Returns (y [M][N], acc [M][N] or None)."""
+    torch = _torch()
+    _require_cuda(X, "X")
+    M = X.shape[0]
+    if y is None and acc is None:
+        y = torch.empty((M, W.N), dtype=torch.float32, device=X.device)
+    if X.dtype == torch.float32:
+        if q_out is None:
+            q_out = torch.empty((M, W.K), dtype=torch.int8, device=X.device)
+        if scale_out is None:
+            scale_out = torch.empty(M, dtype=torch.float32, device=X.device)
+    a = _act(X, None, x_scale_dev, q_out, scale_out)
+    L.check(L.lib().ter_hip_gemm(C.byref(W.wpk), C.byref(a), int(M), _ptr(y), _ptr(acc), _stream(stream)),
+            "ter_hip_gemm")
+    return y, acc
+
+
+class Plan:
+    """Many independent GEMVs in one launch (one work list).  `items` is a
+    sequence of dicts: {w: PackedTrits, x: tensor, y?, acc?, x_scale?,
+    x_scale_dev?, q_out?, scale_out?}."""
+
+    def __init__(self, items: Sequence[dict], wg_per_cu: int = 0):
+        n = len(items)
+        arr = (L.GemvItem * n)()
+        self._keep: List = []
+        for i, it in enumerate(items):
+            W = it["w"]
+            arr[i].w = C.pointer(W.wpk)
+            arr[i].x = _act(it["x"], it.get("x_scale"), it.get("x_scale_dev"), it.get("q_out"), it.get("scale_out"))
+            arr[i].y = _ptr(it.get("y"))
+            arr[i].acc = _ptr(it.get("acc"))
+            self._keep.append(W)
+        h = C.c_void_p()
+        L.check(L.lib().ter_hip_plan_create(C.byref(h), arr, n, int(wg_per_cu)), "ter_hip_plan_create")
+        self._h = h
+        b, m, g = C.c_uint64(), C.c_uint64(), C.c_int32()
+        L.check(L.lib().ter_hip_plan_stats(self._h, C.byref(b), C.byref(m), C.byref(g)), "ter_hip_plan_stats")
+        self.bytes, self.macs, self.n_wg = b.value, m.value, g.value
+
+    def launch(self, stream=None):
+        L.check(L.lib().ter_hip_plan_launch(self._h, _stream(stream)), "ter_hip_plan_launch")
+
+    def close(self):
+        if getattr(self, "_h", None):
+            L.lib().ter_hip_plan_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Handle:
+    """K4-style handle with the KernelTable native slot (ter_k4_create /
+    ter_k4_call / ter_k4_op_counts, include/ter_k4/ter_k4.h:29-55)."""
+
+    def __init__(self, device: int = 0):
+        self._h = L.lib().ter_hip_create(int(device))
+        if not self._h:
+            raise MemoryError("ter_hip_create failed")
+        self._fns = []
+
+    def install_native(self, name: str, fn) -> int:
+        cb = L.NATIVE_FN(fn)
+        self._fns.append(cb)
+        return L.lib().ter_hip_install_native(self._h, name.encode(), cb)
+
+    def call(self, name: str, args: Sequence[int]) -> int:
+        a = (C.c_int64 * max(1, len(args)))(*[int(v) for v in args])
+        return L.lib().ter_hip_call(self._h, name.encode() if name is not None else None, a, len(args))
+
+    def matmul(self, W: PackedTrits, x, y=None, acc=None, x_scale=None, x_scale_dev=None, M: int = 1,
+               q_out=None, scale_out=None, stream=None) -> int:
+        """Call the default "tk_matmul_b_9t" native slot."""
+        a = _act(x, x_scale, x_scale_dev, q_out, scale_out)
+        self._last_act = a
+        args = [C.addressof(W.wpk), C.addressof(a), _ptr(y) or 0, _ptr(acc) or 0, _stream(stream) or 0, int(M)]
+        return self.call("tk_matmul_b_9t", args)
+
+    def op_counts(self) -> dict:
+        c = L.OpCounts()
+        L.lib().ter_hip_op_counts(self._h, C.byref(c))
+        return {f: getattr(c, f) for f, _ in L.OpCounts._fields_}
+
+    def reset_counters(self):
+        L.lib().ter_hip_reset_counters(self._h)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            L.lib().ter_hip_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def synth_v11(K: int, N: int, seed: int, p_zero: float = 1.0 / 3.0, device="cuda", stream=None):
+    """Synthetic reference-v11 weight bytes generated on the device (counter-
+    based splitmix64; element k*N+n draws trit 0 with P=p_zero, else +1/-1
+    with equal probability)."""
+    torch = _torch()
+    t0 = int(round(p_zero * 2 ** 32))
+    t1 = t0 + int(round((1.0 - p_zero) / 2.0 * 2 ** 32))
+    out = torch.empty((N // 4) * K, dtype=torch.uint8, device=device)
+    L.check(L.lib().ter_hip_synth_v11(out.data_ptr(), int(K), int(N), int(seed) & (2 ** 64 - 1), t0,
+                                      min(t1, 2 ** 32 - 1), _stream(stream)), "ter_hip_synth_v11")
+    return out
+
+
+def synth_i8(n: int, seed: int, lo: int = -127, hi: int = 127, device="cuda", stream=None):
+    torch = _torch()
+    out = torch.empty(n, dtype=torch.int8, device=device)
+    L.check(L.lib().ter_hip_synth_i8(out.data_ptr(), int(n), int(seed) & (2 ** 64 - 1), int(lo), int(hi),
+                                     _stream(stream)), "ter_hip_synth_i8")
+    return out

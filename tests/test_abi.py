@@ -1,0 +1,196 @@
+"""CPU checks of the C-ABI boundary (no device needed).
+
+* libter_hip.so loads and exports every function include/ter_hip.h declares;
+* argument validation returns the ter_k4-style codes before any device work
+  (null -> -1, unknown kernel -> -2, > 7 args -> -4: src/k4/ter_k4.cpp:52-55);
+* the KernelTable native slot (install / find / call, 32 slots, names < 32
+  chars: include/ter/kernels.hpp:21-38) dispatches to an installed function.
+"""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from ter_amd import _lib as L
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ter_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w\s\*]*?\b(ter_hip_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if not n.endswith("_fn")))
+
+
+def test_library_exports_every_declared_symbol():
+    names = declared_functions()
+    assert len(names) == 24, names
+    lib = L.lib()
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    bound = {n for n, _, _ in L.SIGNATURES}
+    assert set(names) == bound, (set(names) ^ bound)
+
+
+def test_version_and_sizes():
+    lib = L.lib()
+    assert b"gfx950" in lib.ter_hip_version()
+    # T16: ceil(N/16) strips x ceil(K/256) tiles of 1 KiB + N 8-byte fix-up slots
+    assert lib.ter_hip_wpk_bytes(2048, 2048) == 128 * 8 * 1024 + 2048 * 8
+    assert lib.ter_hip_wpk_bytes(2560, 640) == 40 * 10 * 1024 + 640 * 8
+    assert lib.ter_hip_wpk_bytes(6912, 2560) == 160 * 27 * 1024 + 2560 * 8
+    assert lib.ter_hip_wpk_bytes(1, 1) == 1024 + 8
+    assert lib.ter_hip_wpk_bytes(0, 4) == 0
+
+
+def test_wpk_init_validation():
+    lib = L.lib()
+    w = L.WPK()
+    fake = 1 << 20  # never dereferenced: validation happens before device work
+    need = lib.ter_hip_wpk_bytes(64, 16)
+    assert lib.ter_hip_wpk_init(None, fake, need, 64, 16, 1.0) == L.ERR_NULL
+    assert lib.ter_hip_wpk_init(C.byref(w), None, need, 64, 16, 1.0) == L.ERR_NULL
+    assert lib.ter_hip_wpk_init(C.byref(w), fake + 4, need, 64, 16, 1.0) == L.ERR_ALIGN
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, need - 1, 64, 16, 1.0) == L.ERR_SHAPE
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, need, L.K_MAX + 1, 16, 1.0) == L.ERR_SHAPE
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, need, 64, 0, 1.0) == L.ERR_SHAPE
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, need, 64, 16, 0.5) == L.OK
+    assert w.K == 64 and w.N == 16 and w.layout == L.LAYOUT_T16 and w.scale == 0.5
+    assert w.fix == fake + 1024  # 1 strip x 1 unit tile, then the fix-up slots
+
+
+def test_gemv_validation_without_device():
+    lib = L.lib()
+    w = L.WPK()
+    fake = 1 << 20
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, lib.ter_hip_wpk_bytes(64, 16), 64, 16, 1.0) == L.OK
+    x = L.Act()
+    assert lib.ter_hip_gemv(C.byref(w), None, fake, None, None) == L.ERR_NULL
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_NULL  # x.data null
+    x.data = fake
+    x.kind = 7
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_PAYLOAD
+    x.kind = L.X_I8
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), None, None, None) == L.ERR_NULL  # no output
+    x.kind = L.X_F32
+    x.data = fake + 2
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_ALIGN
+    # mm_packed_dispatch shape mismatch
+    assert lib.ter_hip_mm_packed_dispatch(fake, fake, C.byref(w), fake, 64, 32, None) == L.ERR_SHAPE
+    # batched: M out of range, int8 X without per-row scales
+    x.data, x.kind = fake, L.X_I8
+    assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 0, fake, None, None) == L.ERR_SHAPE
+    assert lib.ter_hip_gemm(C.byref(w), C.byref(x), L.M_MAX + 1, fake, None, None) == L.ERR_SHAPE
+    assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 8, fake, None, None) == L.ERR_NULL
+    # unknown layout tag
+    w.layout = 3
+    x.scale_dev = fake
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_PAYLOAD
+
+
+def test_mm_row_rejects_non_int8_activations():
+    # The 9-trit host activations (+-9841, src/tx/forward.cpp:400) do not fit
+    # int8: the boundary refuses them instead of computing on the CPU.
+    import numpy as np
+    lib = L.lib()
+    w = L.WPK()
+    fake = 1 << 20
+    K, N = 64, 16
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, lib.ter_hip_wpk_bytes(K, N), K, N, 1.0) == L.OK
+    X = np.zeros((1, K), dtype=np.int32)
+    X[0, 5] = 9841
+    out = np.zeros(N, dtype=np.float32)
+    rc = lib.ter_hip_mm_row(X.ctypes.data, 0, K, 1.0, C.byref(w), N, out.ctypes.data, fake, fake, None)
+    assert rc == L.ERR_PAYLOAD
+    assert b"int8" in lib.ter_hip_last_error()
+    X[0, 5] = -129
+    rc = lib.ter_hip_mm_row(X.ctypes.data, 0, K, 1.0, C.byref(w), N, out.ctypes.data, fake, fake, None)
+    assert rc == L.ERR_PAYLOAD
+
+
+def test_pack_payload_rejects_non_ternary_and_blocked():
+    import numpy as np
+    lib = L.lib()
+    w = L.WPK()
+    fake = 1 << 20
+    K, N = 8, 4
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, lib.ter_hip_wpk_bytes(K, N), K, N, 1.0) == L.OK
+    p = np.zeros((K, N), dtype=np.int32)
+    p[0, 0], p[1, 1], p[2, 2] = 9841, -9841, 3  # two magnitudes -> not ternary
+    m = C.c_int32()
+    assert lib.ter_hip_pack_payload(C.byref(w), p.ctypes.data, 1.0, C.byref(m), None) == L.ERR_PAYLOAD
+
+
+def test_plan_validation():
+    lib = L.lib()
+    h = C.c_void_p()
+    items = (L.GemvItem * 1)()
+    assert lib.ter_hip_plan_create(None, items, 1, 0) == L.ERR_NULL
+    assert lib.ter_hip_plan_create(C.byref(h), items, 0, 0) == L.ERR_SHAPE
+    assert lib.ter_hip_plan_create(C.byref(h), items, 1, 0) == L.ERR_NULL  # null weight
+    w = L.WPK()
+    fake = 1 << 20
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, lib.ter_hip_wpk_bytes(64, 16), 64, 16, 1.0) == L.OK
+    items2 = (L.GemvItem * 2)()
+    for it in items2:
+        it.w = C.pointer(w)
+        it.x.data = fake
+        it.x.kind = L.X_I8
+        it.y = fake
+    assert lib.ter_hip_plan_create(C.byref(h), items2, 2, 0) == L.ERR_CONFLICT  # same weight twice
+
+
+def test_kernel_table_slots_and_codes():
+    lib = L.lib()
+    h = lib.ter_hip_create(-1)  # device -1: calls do not select a device (no GPU here)
+    assert h
+    try:
+        args = (C.c_int64 * 8)(*range(8))
+        assert lib.ter_hip_call(None, b"tk_matmul_b_9t", args, 1) == L.ERR_NULL
+        assert lib.ter_hip_call(h, None, args, 1) == L.ERR_NULL
+        assert lib.ter_hip_call(h, b"no_such_kernel", args, 1) == L.ERR_NOTFOUND
+        assert lib.ter_hip_call(h, b"tk_matmul_b_9t", args, 8) == L.ERR_NARGS
+        # the default matmul slot validates its own arguments
+        zero = (C.c_int64 * 6)(0, 0, 0, 0, 0, 1)
+        assert lib.ter_hip_call(h, b"tk_matmul_b_9t", zero, 6) == L.ERR_NULL   # null W
+        assert lib.ter_hip_call(h, b"tk_matmul_b_9t", zero, 5) == L.ERR_NARGS  # too few
+        seen = []
+
+        def native(hh, a, n):
+            seen.append([a[i] for i in range(n)])
+            return 42
+
+        cb = L.NATIVE_FN(native)
+        assert lib.ter_hip_install_native(h, b"tk_custom", cb) == L.OK
+        assert lib.ter_hip_call(h, b"tk_custom", args, 7) == 42
+        assert seen == [list(range(7))]
+        # 32 slots: 2 used (tk_matmul_b_9t, tk_custom) -> 30 more fit, then full
+        for i in range(30):
+            assert lib.ter_hip_install_native(h, b"slot%02d" % i, cb) == L.OK
+        assert lib.ter_hip_install_native(h, b"one_too_many", cb) == L.ERR_FULL
+        # re-installing an existing name replaces it (no new slot needed)
+        assert lib.ter_hip_install_native(h, b"slot00", cb) == L.OK
+        c = L.OpCounts()
+        lib.ter_hip_op_counts(h, C.byref(c))
+        assert c.tvmac == 0 and c.total_ops == 0  # failed calls count nothing
+        lib.ter_hip_reset_counters(h)
+    finally:
+        lib.ter_hip_destroy(h)
+
+
+def test_kernel_table_name_truncation():
+    # names keep at most 31 chars (KernelTable::kNameMax = 32, src/sim/call_kernel.cpp:41-42)
+    lib = L.lib()
+    h = lib.ter_hip_create(-1)
+    try:
+        cb = L.NATIVE_FN(lambda hh, a, n: 7)
+        long_name = b"k" * 40
+        assert lib.ter_hip_install_native(h, long_name, cb) == L.OK
+        args = (C.c_int64 * 1)(0)
+        assert lib.ter_hip_call(h, b"k" * 31, args, 0) == 7
+        assert lib.ter_hip_call(h, b"k" * 30, args, 0) == L.ERR_NOTFOUND
+    finally:
+        lib.ter_hip_destroy(h)

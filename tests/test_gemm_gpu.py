@@ -1,0 +1,104 @@
+"""GPU parity of the batched (M > 1) MFMA GEMM and the per-row quantizer.
+
+Bar as for the GEMV: int32 accumulators and int8 quantized activations
+bit-exact, fp32 outputs bit-exact (tolerance of the contract: 1e-5 relative).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+REL_TOL = 1e-5
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def assert_f32_equal(got, want):
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
+    assert rel.max(initial=0.0) <= REL_TOL
+    assert (got.view(np.int32) == want.view(np.int32)).all()
+
+
+CASES = [
+    (2, 300, 20), (8, 2560, 640), (16, 2048, 512), (17, 257, 36), (32, 2560, 640),
+    (64, 640, 128), (128, 2560, 640), (200, 512, 48), (256, 256, 16), (8, 6912, 256),
+]
+
+
+@pytest.mark.parametrize("M,K,N", CASES)
+def test_gemm_int8(cuda, M, K, N):
+    import torch
+    import ter_amd as T
+    w = O.rand_trits(M * 1000 + K, K, N, 0.4)
+    v11 = O.v11_pack(w)
+    X = O.rand_int8(M + K + N, M * K).reshape(M, K)
+    xs = (0.001 * (np.arange(M) + 1)).astype(np.float32)
+    W = T.PackedTrits.from_v11(v11, K, N, 0.043)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    T.mm_batched(W, dev(X), y=y, acc=acc, x_scale_dev=dev(xs))
+    ra, ry = O.gemm_v11(X, xs, v11, 0.043, K, N)
+    assert (host(acc) == ra).all()
+    assert_f32_equal(host(y), ry)
+
+
+@pytest.mark.parametrize("M,K,N", [(8, 2560, 640), (32, 6912, 64), (128, 2560, 128), (3, 100, 8)])
+def test_gemm_fp32_rows_quantized(cuda, M, K, N):
+    import torch
+    import ter_amd as T
+    w = O.rand_trits(K + N, K, N, 0.4)
+    v11 = O.v11_pack(w)
+    Xf = O.rand_normal_f32(M * 7 + 1, M * K).reshape(M, K)
+    Xf[0] *= 50.0  # rows with very different ranges quantize independently
+    W = T.PackedTrits.from_v11(v11, K, N, 0.021)
+    q = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    s = torch.empty(M, dtype=torch.float32, device="cuda")
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    T.mm_batched(W, dev(Xf), y=y, acc=acc, q_out=q, scale_out=s)
+    rq, rs = O.quant_int8_rows(Xf)
+    assert (host(q) == rq).all()
+    assert (host(s).view(np.int32) == rs.view(np.int32)).all()
+    ra, ry = O.gemm_v11(rq, rs, v11, 0.021, K, N)
+    assert (host(acc) == ra).all()
+    assert_f32_equal(host(y), ry)
+
+
+def test_gemm_m1_rows_match_gemv(cuda):
+    """Each row of the batched product equals the M = 1 GEMV of that row."""
+    import torch
+    import ter_amd as T
+    M, K, N = 8, 2048, 512
+    v11 = O.v11_pack(O.rand_trits(9, K, N))
+    X = O.rand_int8(10, M * K).reshape(M, K)
+    W = T.PackedTrits.from_v11(v11, K, N, 1.0)
+    acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+    T.mm_batched(W, dev(X), acc=acc, x_scale_dev=dev(np.ones(M, np.float32)))
+    A = host(acc)
+    for m in range(M):
+        a1 = torch.empty(N, dtype=torch.int32, device="cuda")
+        T.gemv(W, dev(X[m]), acc=a1, x_scale=1.0)
+        assert (host(a1) == A[m]).all()
+
+
+def test_quant_int8_kernel(cuda):
+    import ter_amd as T
+    x = O.rand_normal_f32(77, 5 * 6912).reshape(5, 6912)
+    x[2] = 0.0
+    x[3, 100] = 1e6
+    q, s = T.quant_int8(dev(x))
+    rq, rs = O.quant_int8_rows(x)
+    assert (host(q) == rq).all()
+    assert (host(s).view(np.int32) == rs.view(np.int32)).all()

@@ -1,0 +1,302 @@
+"""GPU parity of the M = 1 packed-trit GEMV against the CPU oracle.
+
+Bar: int32 accumulators bit-exact; fp32 outputs bit-exact (the kernel forms
+float(acc) * (x_scale * w_scale) in the reference's order; the stated
+tolerance of the contract is 1e-5 relative, REL_TOL below, and every fp32
+comparison here also asserts it).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+REL_TOL = 1e-5
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def assert_f32_equal(got, want):
+    got = np.asarray(got, np.float32)
+    want = np.asarray(want, np.float32)
+    rel = np.abs(got.astype(np.float64) - want) / np.maximum(np.abs(want.astype(np.float64)), 1e-30)
+    assert rel.max(initial=0.0) <= REL_TOL
+    assert (got.view(np.int32) == want.view(np.int32)).all(), "fp32 output not bit-identical"
+
+
+def gemv_case(K, N, seed, p0=1 / 3, xs=0.0312, ws=0.05):
+    import torch
+    import ter_amd as T
+    w = O.rand_trits(seed, K, N, p0)
+    v11 = O.v11_pack(w)
+    x = O.rand_int8(seed + 1, K)
+    W = T.PackedTrits.from_v11(v11, K, N, ws)
+    acc = torch.empty(N, dtype=torch.int32, device="cuda")
+    y = torch.empty(N, dtype=torch.float32, device="cuda")
+    T.gemv(W, dev(x), y=y, acc=acc, x_scale=xs)
+    ra, ry = O.gemv_v11(x, xs, v11, ws, K, N)
+    assert (host(acc) == ra).all(), f"int32 acc mismatch K={K} N={N}"
+    assert_f32_equal(host(y), ry)
+
+
+SHAPES = [
+    (2048, 2048),   # C1 (Llama Wq/Wo)
+    (2048, 512),    # Wk/Wv
+    (2048, 8192),   # Wgate/Wup
+    (8192, 2048),   # Wdown
+    (2560, 2560), (2560, 640), (2560, 6912), (6912, 2560),  # BitNet-2B
+    (128, 64),      # reference correctness-test shape
+    (64, 16), (1, 4), (300, 20), (257, 4), (4112, 100), (255, 1028),
+]
+
+
+@pytest.mark.parametrize("K,N", SHAPES)
+def test_gemv_shapes(cuda, K, N):
+    gemv_case(K, N, seed=K * 7 + N)
+
+
+def test_gemv_golden_reference_vectors(cuda, golden):
+    """Vectors written by the reference mm_row itself (tests/golden)."""
+    import torch
+    import ter_amd as T
+    g = golden("mm_row_random.npz")
+    for i in range(int(g["n_cases"])):
+        K, N = int(g[f"c{i}_K"]), int(g[f"c{i}_N"])
+        row = int(g[f"c{i}_row"])
+        x = g[f"c{i}_X"][row]
+        xs, ws = float(g[f"c{i}_xs"]), float(g[f"c{i}_ws"])
+        for W in (T.PackedTrits.from_v11(g[f"c{i}_v11"], K, N, ws),
+                  T.PackedTrits.from_payload(g[f"c{i}_W"].astype(np.int32), ws)):
+            acc = torch.empty(N, dtype=torch.int32, device="cuda")
+            y = torch.empty(N, dtype=torch.float32, device="cuda")
+            T.gemv(W, dev(x), y=y, acc=acc, x_scale=xs)
+            assert (host(acc).astype(np.int64) == g[f"c{i}_acc"]).all(), i
+            assert_f32_equal(host(y), g[f"c{i}_out"])
+
+
+def test_gemv_reference_fixtures(cuda, golden):
+    import torch
+    import ter_amd as T
+    f = golden("int4tc_fixture.npz")
+    K, N = int(f["K"]), int(f["N"])
+    W = T.PackedTrits.from_v11(f["v11"], K, N, 1.0)
+    acc = torch.empty(N, dtype=torch.int32, device="cuda")
+    T.gemv(W, dev(f["X"].astype(np.int8)), acc=acc, x_scale=1.0)
+    assert (host(acc).astype(np.int64) == f["acc"]).all()
+    m = golden("matmul_b_small.npz")
+    for xk, wk, ok in (("X1", "W1", "out1"), ("X2", "W2", "out2")):
+        # K = 27 / 54, N = 1 through the TritTensor-payload path
+        W = T.PackedTrits.from_payload(m[wk].astype(np.int32), 1.0)
+        acc = torch.empty(1, dtype=torch.int32, device="cuda")
+        T.gemv(W, dev(m[xk].astype(np.int8)), acc=acc, x_scale=1.0)
+        assert int(host(acc)[0]) == int(m[ok][0])
+
+
+def test_gemv_payload_magnitude_folded(cuda):
+    """A ternary payload {-m,0,+m} (e.g. 9-trit quantized BitNet weights,
+    src/host/load_gguf.cpp:111) is packed as {-1,0,+1} with m in the scale."""
+    import torch
+    import ter_amd as T
+    K, N = 100, 12
+    w = O.rand_trits(3, K, N).astype(np.int32) * 9841
+    x = O.rand_int8(4, K)
+    W = T.PackedTrits.from_payload(w, 0.001)
+    assert W.magnitude == 9841
+    acc = torch.empty(N, dtype=torch.int32, device="cuda")
+    T.gemv(W, dev(x), acc=acc, x_scale=1.0)
+    ref_acc, _ = O.mm_row(x.astype(np.int32)[None], 0, 1.0, w, 1.0)
+    assert (host(acc).astype(np.int64) * 9841 == ref_acc).all()
+
+
+def test_gemv_fp32_prologue(cuda):
+    """fp32 X quantized by absmax inside the kernel (quant_int8_k steps)."""
+    import torch
+    import ter_amd as T
+    for K, N, seed in ((2560, 2560, 1), (6912, 2560, 2), (300, 20, 3), (2560, 640, 4)):
+        w = O.rand_trits(seed, K, N, 0.4)
+        v11 = O.v11_pack(w)
+        xf = O.rand_normal_f32(seed + 50, K)
+        W = T.PackedTrits.from_v11(v11, K, N, 0.037)
+        q = torch.empty(K, dtype=torch.int8, device="cuda")
+        s = torch.empty(1, dtype=torch.float32, device="cuda")
+        acc = torch.empty(N, dtype=torch.int32, device="cuda")
+        y = torch.empty(N, dtype=torch.float32, device="cuda")
+        T.gemv(W, dev(xf), y=y, acc=acc, q_out=q, scale_out=s)
+        rq, rs = O.quant_int8(xf)
+        assert (host(q) == rq).all(), "in-kernel quantization differs"
+        assert host(s)[0].view(np.int32) == np.float32(rs).view(np.int32)
+        ra, ry = O.gemv_v11(rq, rs, v11, 0.037, K, N)
+        assert (host(acc) == ra).all()
+        assert_f32_equal(host(y), ry)
+
+
+def test_gemv_device_scale_and_dispatch(cuda):
+    import torch
+    import ter_amd as T
+    K, N = 2048, 512
+    w = O.rand_trits(21, K, N)
+    v11 = O.v11_pack(w)
+    x = O.rand_int8(22, K)
+    W = T.PackedTrits.from_v11(v11, K, N, 0.061)
+    sx = torch.tensor([0.0123], dtype=torch.float32, device="cuda")
+    out = torch.empty(N, dtype=torch.float32, device="cuda")
+    T.mm_packed_dispatch(dev(x), sx, W, out, K, N)
+    _, ry = O.gemv_v11(x, np.float32(0.0123), v11, 0.061, K, N)
+    assert_f32_equal(host(out), ry)
+
+
+def test_mm_row_host_contract(cuda):
+    import ter_amd as T
+    K, N = 300, 24
+    w = O.rand_trits(31, K, N).astype(np.int32)
+    X = O.rand_int8(32, 2 * K).astype(np.int32).reshape(2, K)
+    W = T.PackedTrits.from_payload(w, 0.02)
+    out = T.mm_row(X, 1, 0.5, W, K, N)
+    _, ref = O.mm_row(X, 1, 0.5, w, 0.02)
+    assert_f32_equal(out, ref)
+
+
+def test_gemv_edge_values(cuda):
+    import torch
+    import ter_amd as T
+    K, N = 1024, 64
+    w = O.rand_trits(41, K, N)
+    v11 = O.v11_pack(w)
+    W = T.PackedTrits.from_v11(v11, K, N, 1.0)
+    for x in (np.zeros(K, np.int8), np.full(K, -128, np.int8), np.full(K, 127, np.int8),
+              np.where(np.arange(K) % 2 == 0, -128, 127).astype(np.int8)):
+        acc = torch.empty(N, dtype=torch.int32, device="cuda")
+        T.gemv(W, dev(x), acc=acc, x_scale=1.0)
+        ra, _ = O.gemv_v11(x, 1.0, v11, 1.0, K, N)
+        assert (host(acc) == ra).all()
+    # all-zero and all-reserved (code 11) weights
+    for fill in (0x00, 0xFF):
+        Wz = T.PackedTrits.from_v11(np.full((N // 4) * K, fill, np.uint8), K, N, 1.0)
+        acc = torch.empty(N, dtype=torch.int32, device="cuda")
+        T.gemv(Wz, dev(O.rand_int8(5, K)), acc=acc, x_scale=1.0)
+        assert (host(acc) == 0).all()
+
+
+def test_v11_roundtrip_on_device(cuda):
+    import ter_amd as T
+    for K, N in ((300, 20), (2048, 512), (7, 4)):
+        v11 = O.v11_pack(O.rand_trits(K + N, K, N))
+        W = T.PackedTrits.from_v11(v11, K, N, 1.0)
+        assert (host(W.to_v11()) == v11).all()
+    # code 11 is normalised to 00 (both decode as 0, include/ter/pack.hpp:18-19)
+    W = T.PackedTrits.from_v11(np.full(8, 0xFF, np.uint8), 2, 16, 1.0)
+    assert (host(W.to_v11()) == 0).all()
+
+
+def test_synth_generator_matches_oracle(cuda):
+    import ter_amd as T
+    K, N = 96, 40
+    for p0 in (1 / 3, 0.4):
+        v = host(T.synth_v11(K, N, seed=1234, p_zero=p0))
+        assert (O.v11_unpack(v, K, N) == O.rand_trits(1234, K, N, p0)).all()
+    x = host(T.synth_i8(1000, seed=99))
+    assert (x == O.rand_int8(99, 1000)).all()
+
+
+@pytest.mark.parametrize("wg_per_cu", [1, 2, 3, 0])
+def test_plan_worklist_mixed(cuda, wg_per_cu):
+    """Many GEMVs in one launch: int8 and fp32 inputs, ragged shapes, strips
+    split across waves/workgroups (fix-up path); launched twice to check the
+    fix-up slots clean themselves."""
+    import torch
+    import ter_amd as T
+    specs = [(2048, 512, "i8"), (300, 20, "f32"), (2560, 640, "f32"), (8192, 2048, "i8"),
+             (64, 16, "i8"), (6912, 256, "f32"), (2048, 2048, "i8")]
+    items, refs = [], []
+    for i, (K, N, kind) in enumerate(specs):
+        v11 = O.v11_pack(O.rand_trits(500 + i, K, N))
+        W = T.PackedTrits.from_v11(v11, K, N, 0.01 * (i + 1))
+        y = torch.empty(N, dtype=torch.float32, device="cuda")
+        acc = torch.empty(N, dtype=torch.int32, device="cuda")
+        if kind == "i8":
+            x = O.rand_int8(600 + i, K)
+            items.append(dict(w=W, x=dev(x), x_scale=0.5, y=y, acc=acc))
+            ra, ry = O.gemv_v11(x, 0.5, v11, 0.01 * (i + 1), K, N)
+        else:
+            xf = O.rand_normal_f32(600 + i, K)
+            items.append(dict(w=W, x=dev(xf), y=y, acc=acc))
+            q, s = O.quant_int8(xf)
+            ra, ry = O.gemv_v11(q, s, v11, 0.01 * (i + 1), K, N)
+        refs.append((ra, ry))
+    plan = T.Plan(items, wg_per_cu=wg_per_cu)
+    for rep in range(2):
+        for it in items:
+            it["acc"].fill_(-7)
+            it["y"].fill_(-7)
+        plan.launch()
+        for it, (ra, ry) in zip(items, refs):
+            assert (host(it["acc"]) == ra).all(), (rep, it["w"].K, it["w"].N)
+            assert_f32_equal(host(it["y"]), ry)
+    for it in items:  # slots are zero at rest
+        K, N = it["w"].K, it["w"].N
+        fix = it["w"].buf[it["w"].buf.numel() - 8 * N:]
+        assert int(host(fix).astype(np.int64).sum()) == 0
+
+
+def test_handle_native_slot_counts(cuda):
+    import torch
+    import ter_amd as T
+    K, N = 2048, 512
+    v11 = O.v11_pack(O.rand_trits(71, K, N))
+    x = O.rand_int8(72, K)
+    W = T.PackedTrits.from_v11(v11, K, N, 0.5)
+    h = T.Handle(0)
+    acc = torch.empty(N, dtype=torch.int32, device="cuda")
+    assert h.matmul(W, dev(x), acc=acc, x_scale=1.0) == 0
+    ra, _ = O.gemv_v11(x, 1.0, v11, 0.5, K, N)
+    assert (host(acc) == ra).all()
+    assert h.op_counts()["tvmac"] == O.mm_row_tvmac(K, N)  # src/tx/forward.cpp:349-350
+    h.reset_counters()
+    assert h.op_counts()["tvmac"] == 0
+
+
+def test_llama_sweep_full_size_properties(cuda):
+    """C2 at full size (16 layers x 7 GEMVs, ~245 MB packed, one launch):
+    exact oracle check on sampled columns of every GEMV, plus linearity
+    acc(x1) + acc(x2) == acc(x1 + x2) and acc(-x) == -acc(x) on all columns."""
+    import torch
+    import ter_amd as T
+    shapes = [(2048, 2048), (2048, 512), (2048, 512), (2048, 2048), (2048, 8192), (2048, 8192), (8192, 2048)]
+    rng = np.random.default_rng(5)
+    Ws, v11s, xs = [], [], []
+    for layer in range(16):
+        for i, (K, N) in enumerate(shapes):
+            v = T.synth_v11(K, N, seed=10_000 + layer * 7 + i)
+            Ws.append(T.PackedTrits.from_v11(v, K, N, 0.05))
+            v11s.append(v)
+    xa = {K: O.rand_int8(K, K, -63, 63) for K in (2048, 8192)}
+    xb = {K: O.rand_int8(K + 1, K, -64, 64) for K in (2048, 8192)}
+
+    def run(xmap):
+        items, outs = [], []
+        for W in Ws:
+            acc = torch.empty(W.N, dtype=torch.int32, device="cuda")
+            items.append(dict(w=W, x=dev(xmap[W.K]), x_scale=1.0, acc=acc))
+            outs.append(acc)
+        T.Plan(items).launch()
+        torch.cuda.synchronize()
+        return [o.cpu().numpy() for o in outs]
+
+    a = run(xa)
+    b = run(xb)
+    s = run({K: (xa[K].astype(np.int16) + xb[K]).astype(np.int8) for K in xa})
+    n = run({K: (-xa[K].astype(np.int16)).astype(np.int8) for K in xa})
+    for i, W in enumerate(Ws):
+        assert (a[i] + b[i] == s[i]).all() and (n[i] == -a[i]).all(), i
+        jbs = rng.choice(W.N // 4, size=8, replace=False)
+        cols, ra, _ = O.gemv_v11_cols(xa[W.K], 1.0, host(v11s[i]), 1.0, W.K, W.N, jbs)
+        assert (a[i][cols] == ra).all(), i

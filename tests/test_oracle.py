@@ -1,0 +1,198 @@
+"""CPU checks that pin the oracle (oracle/ter_oracle.c) before it is trusted.
+
+Pins, per function:
+  * code map / v11 layout    -- hand-derived known-answer bytes (not the packer's
+                                own formula), code 11 -> 0 (tests/test_pack.cpp:29-33)
+  * mm_row, gemv_v11         -- golden vectors written by the reference mm_row itself
+                                (oracle/_ref, tests/golden/make_golden.py), the
+                                closed-form fixtures of tests/test_kernel_matmul_b_small.cpp
+                                and cuda/ter_cuda_forward_packed_v13_int4tc.cu:512-547,
+                                brute-force Python integers, and, where the reference
+                                tree is present, the reference build directly
+  * quant_int8               -- closed forms: exact half-way ties (round-half-even),
+                                all-zero input, the amax element -> +-127, act scale
+  * quantize_nt / bitnet     -- golden vectors from the reference quantizers
+  * dequant_i2s / i2s_to_v11 -- the i2_s block of tests/test_nt_dequant.cpp:37-61
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+
+# ---------------------------------------------------------------- code map
+def test_code_map_known_answers():
+    # include/ter/pack.hpp:8-21, tests/test_pack.cpp:8-15
+    assert [O.lib().orc_code_to_trit(c) for c in range(4)] == [0, 1, -1, 0]
+    assert [O.lib().orc_trit_to_code(t) for t in (0, 1, -1)] == [0, 1, 2]
+
+
+def test_v11_known_bytes():
+    # Derived by hand from tools/convert_llama_to_packed.py:128-140:
+    # byte (j_byte, k) at index j_byte*K + k, column 4*j_byte+s at bits 2s.
+    W = np.array([[+1, -1, 0, +1, 0, 0, -1, -1],
+                  [0, +1, +1, -1, -1, 0, 0, +1]], dtype=np.int8)  # [K=2][N=8]
+    got = O.v11_pack(W)
+    assert got.tolist() == [0x49, 0x94, 0xA0, 0x42]
+    assert (O.v11_unpack(got, 2, 8) == W).all()
+
+
+def test_v11_reserved_code_decodes_zero():
+    # tests/test_pack.cpp:29-33: 0b11 decodes as zero.
+    assert (O.v11_unpack(np.full(8, 0xFF, np.uint8), 2, 16) == 0).all()
+    # mixed: 0b11_01_10_11 -> [0, -1, +1, 0]
+    assert O.v11_unpack(np.array([0b11011011], np.uint8), 1, 4).tolist() == [[0, -1, 1, 0]]
+
+
+def test_v11_roundtrip_random():
+    w = O.rand_trits(5, 37, 24)
+    assert (O.v11_unpack(O.v11_pack(w), 37, 24) == w).all()
+
+
+# ---------------------------------------------------------------- mm_row
+def test_matmul_b_small_closed_form(golden):
+    g = golden("matmul_b_small.npz")
+    for xk, wk, ok in (("X1", "W1", "out1"), ("X2", "W2", "out2")):
+        X, W = g[xk], g[wk]
+        brute = sum(int(a) * int(b) for a, b in zip(X.tolist(), W[:, 0].tolist()))
+        acc, out = O.mm_row(X[None, :], 0, 1.0, W, 1.0)
+        assert int(acc[0]) == brute == int(g[ok][0])
+        assert out.view(np.int32)[0] == g[ok].view(np.int32)[0]
+    assert int(g["out1"][0]) == 13 and int(g["out2"][0]) == -70
+
+
+def test_int4tc_fixture(golden):
+    g = golden("int4tc_fixture.npz")
+    K, N = int(g["K"]), int(g["N"])
+    x = g["X"].astype(np.int8)
+    acc, out = O.gemv_v11(x, 1.0, g["v11"], 1.0, K, N)
+    assert (acc.astype(np.int64) == g["acc"]).all()
+    # brute force from the fixture's closed form t = (7k + 13n) % 3
+    for n in range(N):
+        s = 0
+        for k in range(K):
+            c = (k * 7 + n * 13) % 3
+            s += int(x[k]) * (1 if c == 1 else (-1 if c == 2 else 0))
+        assert s == int(acc[n])
+
+
+def test_mm_row_golden_random(golden):
+    g = golden("mm_row_random.npz")
+    for i in range(int(g["n_cases"])):
+        K, N = int(g[f"c{i}_K"]), int(g[f"c{i}_N"])
+        X = g[f"c{i}_X"].astype(np.int32)
+        W = g[f"c{i}_W"].astype(np.int32)
+        row = int(g[f"c{i}_row"])
+        xs, ws = float(g[f"c{i}_xs"]), float(g[f"c{i}_ws"])
+        acc, out = O.mm_row(X, row, xs, W, ws)
+        assert (acc == g[f"c{i}_acc"]).all(), i
+        assert (out.view(np.int32) == g[f"c{i}_out"].view(np.int32)).all(), i  # bit-exact fp32
+        assert (acc == (X[row].astype(np.int64) @ W.astype(np.int64))).all()
+        if N % 4 == 0:
+            acc2, out2 = O.gemv_v11(X[row].astype(np.int8), xs, g[f"c{i}_v11"], ws, K, N)
+            assert (acc2 == acc).all() and (out2.view(np.int32) == out.view(np.int32)).all()
+
+
+def test_mm_row_zero_skip_and_signs():
+    # X == 0 rows contribute nothing; negating X negates acc; W = 0 -> 0.
+    K, N = 64, 8
+    W = O.rand_trits(3, K, N).astype(np.int32)
+    X = O.rand_int8(4, K).astype(np.int32)
+    X[::3] = 0
+    a, _ = O.mm_row(X[None], 0, 1.0, W, 1.0)
+    b, _ = O.mm_row(-X[None], 0, 1.0, W, 1.0)
+    z, _ = O.mm_row(X[None], 0, 1.0, np.zeros_like(W), 1.0)
+    assert (a == -b).all() and (z == 0).all()
+
+
+def test_gemm_v11_matches_mm_row_per_row():
+    # Batched semantics: out[m] = float(acc[m]) * (xs[m] * ws)
+    # (cuda/ter_cuda_addonly_batched.cu:117-123) == mm_row on each row.
+    K, N, M = 96, 12, 5
+    W = O.rand_trits(8, K, N)
+    X = O.rand_int8(9, M * K).reshape(M, K)
+    xs = (np.arange(M, dtype=np.float32) + 1) * np.float32(0.013)
+    acc, out = O.gemm_v11(X, xs, O.v11_pack(W), 0.07, K, N)
+    for m in range(M):
+        a, o = O.mm_row(X.astype(np.int32), m, float(xs[m]), W.astype(np.int32), 0.07)
+        assert (acc[m] == a).all() and (out[m].view(np.int32) == o.view(np.int32)).all()
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference build oracle/_ref absent")
+def test_mm_row_vs_reference_build():
+    for seed, (K, N) in enumerate([(1, 1), (17, 5), (256, 16), (1000, 33)]):
+        W = O.rand_trits(100 + seed, K, N).astype(np.int32)
+        X = O.rand_int8(200 + seed, 2 * K).astype(np.int32).reshape(2, K)
+        r = O.RefMmRow(X, 0.5, W, 0.25)
+        ref = r.run(1).copy()
+        _, out = O.mm_row(X, 1, 0.5, W, 0.25)
+        assert (out.view(np.int32) == ref.view(np.int32)).all()
+        assert r.tvmac() == O.mm_row_tvmac(K, N)  # src/tx/forward.cpp:349-350
+
+
+@pytest.mark.skipif(not O.ref_available(), reason="reference build oracle/_ref absent")
+def test_mm_row_blocked_vs_reference_build():
+    K, N, bs = 40, 6, 32
+    W = O.rand_trits(31, K, N).astype(np.int32) * 7
+    X = O.rand_int8(32, K).astype(np.int32)
+    nb = (K * N + bs - 1) // bs
+    bsc = (np.arange(nb, dtype=np.float32) + 1) * np.float32(0.01)
+    r = O.RefMmRow(X, 0.3, W, 1.0, bsc, bs)
+    ref = r.run(0).copy()
+    out = O.mm_row_blocked(X[None], 0, 0.3, W, bsc, bs)
+    assert (out.view(np.int32) == ref.view(np.int32)).all()
+
+
+# ---------------------------------------------------------------- quantizers
+def test_quant_int8_half_way_ties():
+    # amax = 127/64 (exact in fp32); + 1e-9f is below half an ulp, so
+    # scale = 127 / amax = 64 exactly, and x = (2j+1)/128 lands on j + 0.5.
+    amax = np.float32(127.0 / 64.0)
+    x = np.array([amax, 1.5 / 64, 2.5 / 64, -0.5 / 64, -1.5 / 64, 3.5 / 64, 0.0], dtype=np.float32)
+    q, s = O.quant_int8(x)
+    assert q.tolist() == [127, 2, 2, 0, -2, 4, 0]   # round half to even (__float2int_rn)
+    assert s == np.float32(1.0 / 64.0)
+
+
+def test_quant_int8_zero_and_extremes():
+    q, s = O.quant_int8(np.zeros(10, np.float32))
+    assert (q == 0).all()
+    assert s == np.float32(1.0) / (np.float32(127.0) / np.float32(1e-9))
+    x = O.rand_normal_f32(5, 1000)
+    q, s = O.quant_int8(x)
+    i = int(np.argmax(np.abs(x)))
+    assert abs(int(q[i])) == 127 and np.sign(q[i]) == np.sign(x[i])
+    assert np.abs(q.astype(np.int32)).max() <= 127
+
+
+def test_quant_rows_independent():
+    x = O.rand_normal_f32(6, 3 * 50).reshape(3, 50)
+    x[1] *= 100
+    q, s = O.quant_int8_rows(x)
+    for m in range(3):
+        qm, sm = O.quant_int8(x[m])
+        assert (q[m] == qm).all() and s[m] == sm
+
+
+def test_quantizers_golden(golden):
+    g = golden("quantizers.npz")
+    q9, s9 = O.quantize_nt(g["x"], 9)
+    assert s9 == g["s9"] and (q9 == g["q9"]).all()
+    qb, sb = O.quantize_bitnet(g["x"])
+    assert sb == g["sb"] and (qb == g["qb"]).all()
+
+
+# ---------------------------------------------------------------- i2_s
+def test_i2s_block_golden(golden):
+    g = golden("i2s_block.npz")
+    out = O.dequant_i2s(g["buf"], int(g["n"]))
+    assert (out == g["expected"]).all()
+
+
+def test_i2s_to_v11_matches_dequant():
+    N, K = 8, 64  # N*K multiple of 128
+    raw = (O.splitmix64(77, N * K // 4) & np.uint64(0xFF)).astype(np.uint8)
+    buf = np.concatenate([raw, np.frombuffer(np.float32(1.0).tobytes(), np.uint8)])
+    dq = O.dequant_i2s(buf, N * K).reshape(N, K)   # (N, K) row-major, values -1/0/+1
+    W = O.v11_unpack(O.i2s_to_v11(raw, K, N), K, N)  # [K][N]
+    assert (W.T == dq.astype(np.int32)).all()
