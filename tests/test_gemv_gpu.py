@@ -92,13 +92,21 @@ def test_gemv_reference_fixtures(cuda, golden):
     acc = torch.empty(N, dtype=torch.int32, device="cuda")
     T.gemv(W, dev(f["X"].astype(np.int8)), acc=acc, x_scale=1.0)
     assert (host(acc).astype(np.int64) == f["acc"]).all()
+    # The closed-form fixtures of tests/test_kernel_matmul_b_small.cpp hold
+    # format-B weights in {-2..2} (i % 5 - 2): not ternary, so the boundary
+    # refuses them rather than computing them on the CPU.
     m = golden("matmul_b_small.npz")
-    for xk, wk, ok in (("X1", "W1", "out1"), ("X2", "W2", "out2")):
-        # K = 27 / 54, N = 1 through the TritTensor-payload path
-        W = T.PackedTrits.from_payload(m[wk].astype(np.int32), 1.0)
+    for wk in ("W1", "W2"):
+        with pytest.raises(T._lib.TerHipError) as e:
+            T.PackedTrits.from_payload(m[wk].astype(np.int32), 1.0)
+        assert e.value.code == T._lib.ERR_PAYLOAD
+    # Their ternary part (sign of W) goes through the payload path, K = 27 / 54, N = 1.
+    for xk, wk in (("X1", "W1"), ("X2", "W2")):
+        w = np.sign(m[wk]).astype(np.int32)
+        W = T.PackedTrits.from_payload(w, 1.0)
         acc = torch.empty(1, dtype=torch.int32, device="cuda")
         T.gemv(W, dev(m[xk].astype(np.int8)), acc=acc, x_scale=1.0)
-        assert int(host(acc)[0]) == int(m[ok][0])
+        assert int(host(acc)[0]) == int(m[xk].astype(np.int64) @ w[:, 0])
 
 
 def test_gemv_payload_magnitude_folded(cuda):
