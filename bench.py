@@ -210,11 +210,13 @@ def cpu_baseline(sw: Sweep, budget_s: float):
                 matches_gpu_bitexact=checked)
 
 
-def read_traffic(name: str):
-    """HBM bytes per launch from profiles/<name>_pmc.txt (written from two
-    rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, scaled by the copy-kernel
-    calibration): a line 'traffic_bytes_per_launch: <int>'."""
-    p = os.path.join(ROOT, "profiles", f"{name}_pmc.txt")
+def read_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` on `workload`, from the committed
+    rocprofv3 summary profiles/<kernel>-<workload>.md (two --pmc passes,
+    FETCH_SIZE then WRITE_SIZE, each scaled by what the same counter reads for
+    a copy kernel of known size): its line 'traffic_bytes_per_launch: <int>'.
+    None when no such summary exists."""
+    p = os.path.join(ROOT, "profiles", f"{kernel}-{workload}.md")
     if not os.path.exists(p):
         return None
     for line in open(p):
@@ -286,7 +288,7 @@ def run_m1(args, cfg, fp32_x: bool):
         log(f"[bench] cpu baseline: {cpu}")
 
     value = mac / (ms_step * 1e-3) / 1e9
-    name = "sweep_" + cfg["name"].split("-")[0]
+    workload = cfg["name"].split("-")[0] + "_sweep"
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -319,7 +321,7 @@ def run_m1(args, cfg, fp32_x: bool):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
-            "traffic": read_traffic(name),
+            "traffic": read_traffic("gemv_t16_kernel", workload),
             "kernel": "gemv_t16_kernel",
             "bytes_per_launch": bytes_alg,
             "mean_launch_us": round(ev_mean * 1e3, 3),
@@ -378,12 +380,30 @@ def run_batched(args):
     }
 
 
+def run_copy(args):
+    """A plain copy-shaped kernel of known size (torch.neg over 256 MiB of
+    fp32: 256 MiB read, 256 MiB written per launch).  Its rocprofv3
+    FETCH_SIZE / WRITE_SIZE readings calibrate the same counters taken on the
+    GEMV kernel."""
+    import torch
+    n = 64 << 20
+    a = torch.randn(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    wall, evm, _ = time_launches([lambda: torch.neg(a, out=b)], args.steps, args.warmup)
+    nbytes = 4 * n
+    return {"metric": "copy calibration (torch.neg fp32)", "value": round(2 * nbytes / (evm * 1e-3) / 1e9, 1),
+            "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(evm, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "f32", "data": "synthetic",
+            "config": {"workload": "copy", "read_bytes_per_launch": nbytes, "write_bytes_per_launch": nbytes}}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", choices=["llama", "bitnet", "batched"], default="llama")
+    ap.add_argument("--config", choices=["llama", "bitnet", "batched", "copy"], default="llama")
     ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
     ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -399,6 +419,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     if args.config == "batched":
         out = run_batched(args)
+    elif args.config == "copy":
+        out = run_copy(args)
     else:
         cfg = LLAMA if args.config == "llama" else BITNET
         out = run_m1(args, cfg, fp32_x=(args.config == "bitnet"))

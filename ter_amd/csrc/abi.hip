@@ -81,23 +81,29 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int
     return d;
 }
 
-// Workgroups of one GEMV launch: every CU holds as many as fit at once
-// (occupancy query), so the static partition runs as a single wave of
-// resident workgroups.  wg_per_cu > 0 overrides (tuning).
+// Workgroups of one GEMV launch: kGemvWgPerCu per CU (measured best for the
+// layer sweeps), capped by what fits at once (occupancy query) so the static
+// partition runs as a single wave of resident workgroups, and raised if a
+// wave's piece would exceed kMaxPieceTiles (its buffer resource spans at most
+// 2^31 bytes).  wg_per_cu > 0 overrides (tuning).
+constexpr int kGemvWgPerCu = 2;
+constexpr long long kMaxPieceTiles = 1 << 20;
+
 int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, int* n_wg) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     const int cus = device_cu_count(dev);
     if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
-    int per_cu = wg_per_cu;
-    if (per_cu <= 0) {
-        per_cu = gemv_max_wg_per_cu(lds_bytes);
-        if (per_cu <= 0) return fail(TER_HIP_ERR_HIP, "occupancy query failed");
-    }
+    const int fit = gemv_max_wg_per_cu(lds_bytes);
+    if (fit <= 0) return fail(TER_HIP_ERR_SHAPE, "GEMV workgroup does not fit a CU (LDS %d bytes)", lds_bytes);
+    int per_cu = wg_per_cu > 0 ? wg_per_cu : (kGemvWgPerCu < fit ? kGemvWgPerCu : fit);
     long long g = (long long)cus * per_cu;
+    const long long min_g = (total_tiles + kMaxPieceTiles * kWaves - 1) / (kMaxPieceTiles * kWaves);
+    if (g < min_g) g = min_g;
     if (g > total_tiles) g = total_tiles;
     if (g < 1) g = 1;
+    if (g > 0x7fffffffLL) return fail(TER_HIP_ERR_SHAPE, "work list too large");
     *n_wg = (int)g;
     return TER_HIP_OK;
 }

@@ -11,18 +11,25 @@
 // Work distribution.  All GEMVs of a launch form one stream of 1 KiB tiles.
 // The stream is cut into n_wg equal contiguous ranges, one per workgroup
 // (4 waves); consecutive ranges are kept on one XCD.  A workgroup walks its
-// range GEMV segment by GEMV segment: it stages that GEMV's int8 activation
-// vector in LDS (quantizing an fp32 vector by absmax in this prologue), then
-// its 4 waves split the segment's tiles into equal contiguous pieces.  A wave
-// accumulates a column strip over its tiles; when a piece covers a whole
-// strip the wave writes the outputs, otherwise it adds its partial sums into
-// the strip's 64-bit fix-up slots with one atomic per column (high bits count
-// the 256-row units seen, low 40 bits hold the signed partial sum); the wave
-// whose atomic completes the count writes the outputs and clears the slot.
-// Integer sums are order independent, so results are bit-exact whatever the
-// split.
+// range GEMV segment by GEMV segment: every wave first issues the loads of
+// its first batch of weight tiles, then the workgroup stages that GEMV's
+// int8 activation vector in LDS (quantizing an fp32 vector by absmax in this
+// prologue), then the 4 waves stream equal contiguous pieces of the segment.
 //
-// Inner loop per tile and lane: one global_load_dwordx4 of packed weights
+// A wave's piece is read through a buffer resource sized to the piece, with
+// two batches of tiles in registers: the loads of batch i + 1 are in flight
+// while batch i is reduced, and loads past the piece return zeros, so no
+// load is predicated.  All control flow is wave-uniform (scalar registers).
+// A wave accumulates a column strip over its tiles; a strip whose 256-row
+// units all lie in the piece is written directly.  The (at most two) strips
+// a piece shares with its neighbours are added, after the streaming loop,
+// into per-column 64-bit fix-up slots with one atomic per column (high bits
+// count the 256-row units seen, low 40 bits hold the signed partial sum);
+// the wave whose atomic completes the count writes the outputs and clears
+// the slot.  Integer sums are order independent, so results are bit-exact
+// whatever the split.
+//
+// Inner loop per tile and lane: one buffer_load_dwordx4 of packed weights
 // (64 trits: 4 columns x 16 rows), one ds_read_b128 of the matching 16 int8
 // activations, 5 bit operations + 4 v_dot4 per column dword.
 #include "common.h"
@@ -31,6 +38,17 @@ namespace terhip {
 namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+#define TER_GLOBAL __attribute__((address_space(1)))
+
+// Generic -> global address space, so accesses compile to global_* / buffer
+// instructions (flat ones also count against the LDS wait counter).
+template <typename T>
+__device__ __forceinline__ TER_GLOBAL T* gptr(T* p) {
+    return (TER_GLOBAL T*)p;
+}
+
+constexpr int kBatch = 4;  // tiles per batch; two batches per wave in flight
 
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
 __device__ __forceinline__ int row_sum16(int v) {
@@ -65,11 +83,57 @@ __device__ __forceinline__ int sum_bytes(const u32x4& v) {
     return s;
 }
 
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// quant_int8_k element step (cuda/ter_cuda_forward_packed.cu:55-58):
+// rint(x * scale) (round half to even), clamped to [-128, 127].
+__device__ __forceinline__ unsigned quant_byte(float x, float scale) {
+#pragma clang fp contract(off)
+    int q = (int)__builtin_rintf(x * scale);
+    q = q > 127 ? 127 : (q < -128 ? -128 : q);
+    return (unsigned)q & 0xFFu;
+}
+
+// Store one 16-byte activation chunk (k = 16 c) in LDS and its unit sum.
+__device__ __forceinline__ void put_chunk(int c, const u32x4& v, int8_t* lds_x, int* usum) {
+    *reinterpret_cast<u32x4*>(lds_x + c * 16) = v;
+    const int s = row_sum16(sum_bytes(v));
+    if ((threadIdx.x & 15) == 0) usum[c >> 4] = s;
+}
+
+// 16 fp32 activations x[k .. k+15] (zeros past K).
+__device__ __forceinline__ void load_f16(const float* xf, int k, int K, bool vec_ok, float (&v)[16]) {
+    if (vec_ok && k + 16 <= K) {
+        const TER_GLOBAL f32x4* p = gptr(reinterpret_cast<const f32x4*>(xf + k));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f32x4 f = p[i];
+            v[4 * i] = f.x;
+            v[4 * i + 1] = f.y;
+            v[4 * i + 2] = f.z;
+            v[4 * i + 3] = f.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = k + i < K ? gptr(xf)[k + i] : 0.f;
+    }
+}
+
+__device__ __forceinline__ u32x4 pack_q16(const float (&v)[16], float scale) {
+    unsigned wd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        wd[i] = quant_byte(v[4 * i], scale) | (quant_byte(v[4 * i + 1], scale) << 8) |
+                (quant_byte(v[4 * i + 2], scale) << 16) | (quant_byte(v[4 * i + 3], scale) << 24);
+    return u32x4{wd[0], wd[1], wd[2], wd[3]};
+}
+
 // Stage the activation vector of `d` into LDS as int8 [Ku*256] (zero padded)
 // plus per-unit sums usum[Ku].  Returns the activation scale.  For fp32 input
 // this is the absmax prologue of quant_int8_k (cuda/ter_cuda_forward_packed.cu:40-62):
 // amax = max|x| + 1e-9f, scale = 127.f / amax, q = rint(x * scale) clamped to
-// [-128, 127], act_scale = 1.f / scale.
+// [-128, 127], act_scale = 1.f / scale.  `owner` (the workgroup that starts
+// the GEMV) also writes the optional copies xq_out / xs_out.
 __device__ float stage_x(const GemvDesc& d, int8_t* lds_x, int* usum, float* red, bool owner) {
 #pragma clang fp contract(off)
     const int K = d.K;
@@ -82,7 +146,7 @@ __device__ float stage_x(const GemvDesc& d, int8_t* lds_x, int* usum, float* red
             const int k = c * 16;
             u32x4 v;
             if (vec_ok && k + 16 <= K) {
-                v = *reinterpret_cast<const u32x4*>(xp + k);
+                v = *gptr(reinterpret_cast<const u32x4*>(xp + k));
             } else {
                 unsigned wd[4];
 #pragma unroll
@@ -91,23 +155,38 @@ __device__ float stage_x(const GemvDesc& d, int8_t* lds_x, int* usum, float* red
 #pragma unroll
                     for (int b = 0; b < 4; ++b) {
                         const int kk = k + 4 * i + b;
-                        const unsigned by = kk < K ? (unsigned)(uint8_t)xp[kk] : 0u;
+                        const unsigned by = kk < K ? (unsigned)(uint8_t)gptr(xp)[kk] : 0u;
                         a |= by << (8 * b);
                     }
                     wd[i] = a;
                 }
                 v = u32x4{wd[0], wd[1], wd[2], wd[3]};
             }
-            *reinterpret_cast<u32x4*>(lds_x + k) = v;
-            const int s = row_sum16(sum_bytes(v));
-            if ((tid & 15) == 0) usum[c >> 4] = s;
+            put_chunk(c, v, lds_x, usum);
         }
-        return d.x_scale_dev ? *d.x_scale_dev : d.x_scale;
+        return d.x_scale_dev ? *gptr(d.x_scale_dev) : d.x_scale;
     }
-    // fp32 input: absmax, then quantize.
+    // fp32 input.  Up to 2 chunks (32 values) per thread are held in
+    // registers across the max reduction (K <= 8192 with 256 threads); longer
+    // vectors are read a second time for the quantization pass.
     const float* xf = static_cast<const float*>(d.x);
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(xf) & 15u) == 0);
+    const int c0 = tid, c1 = tid + kThreads;
+    float v0[16], v1[16];
     float m = 0.f;
-    for (int k = tid; k < K; k += kThreads) m = fmaxf(m, fabsf(xf[k]));
+    if (c0 < nchunks) load_f16(xf, c0 * 16, K, vec_ok, v0);
+    if (c1 < nchunks) load_f16(xf, c1 * 16, K, vec_ok, v1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        if (c0 < nchunks) m = fmaxf(m, fabsf(v0[i]));
+        if (c1 < nchunks) m = fmaxf(m, fabsf(v1[i]));
+    }
+    for (int c = tid + 2 * kThreads; c < nchunks; c += kThreads) {
+        float t[16];
+        load_f16(xf, c * 16, K, vec_ok, t);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(t[i]));
+    }
     m = wave_max(m);
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
@@ -116,119 +195,182 @@ __device__ float stage_x(const GemvDesc& d, int8_t* lds_x, int* usum, float* red
     const float scale = 127.0f / amax;
     const float act = 1.0f / scale;
     for (int c = tid; c < nchunks; c += kThreads) {
-        const int k = c * 16;
-        unsigned wd[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            unsigned a = 0;
-#pragma unroll
-            for (int b = 0; b < 4; ++b) {
-                const int kk = k + 4 * i + b;
-                int qv = 0;
-                if (kk < K) {
-                    const float v = xf[kk] * scale;
-                    qv = (int)__builtin_rintf(v);
-                    qv = qv > 127 ? 127 : (qv < -128 ? -128 : qv);
-                }
-                a |= ((unsigned)qv & 0xFFu) << (8 * b);
-            }
-            wd[i] = a;
+        u32x4 q;
+        if (c == c0) {
+            q = pack_q16(v0, scale);
+        } else if (c == c1) {
+            q = pack_q16(v1, scale);
+        } else {
+            float t[16];
+            load_f16(xf, c * 16, K, vec_ok, t);
+            q = pack_q16(t, scale);
         }
-        const u32x4 v = u32x4{wd[0], wd[1], wd[2], wd[3]};
-        *reinterpret_cast<u32x4*>(lds_x + k) = v;
-        const int s = row_sum16(sum_bytes(v));
-        if ((tid & 15) == 0) usum[c >> 4] = s;
+        put_chunk(c, q, lds_x, usum);
         if (owner && d.xq_out) {
-            for (int i = 0; i < 16 && k + i < K; ++i)
-                d.xq_out[k + i] = (int8_t)((wd[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+            const int k = c * 16;
+            const unsigned qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (k + i < K) gptr(d.xq_out)[k + i] = (int8_t)((qw[i >> 2] >> (8 * (i & 3))) & 0xFFu);
         }
     }
-    if (owner && tid == 0 && d.xs_out) *d.xs_out = act;
+    if (owner && tid == 0 && d.xs_out) *gptr(d.xs_out) = act;
     return act;
 }
 
 __device__ __forceinline__ void emit(const GemvDesc& d, int col, int val, float s) {
 #pragma clang fp contract(off)
-    if (d.acc) d.acc[col] = val;
-    if (d.y) d.y[col] = (float)val * s;
+    if (d.acc) gptr(d.acc)[col] = val;
+    if (d.y) gptr(d.y)[col] = (float)val * s;
 }
 
 // Accumulate 1 tile (16 bytes of this lane) into the 4 column accumulators.
 __device__ __forceinline__ void dot_tile(const u32x4& w, const u32x4& x, int (&a1)[4], int (&a4)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const unsigned d = w[j];
-        const unsigned d4 = d >> 4;
-        a1[j] = __builtin_amdgcn_sdot4((int)x.x, (int)(d & 0x03030303u), a1[j], false);
-        a4[j] = __builtin_amdgcn_sdot4((int)x.y, (int)(d & 0x0C0C0C0Cu), a4[j], false);
+        const unsigned dw = w[j];
+        const unsigned d4 = dw >> 4;
+        a1[j] = __builtin_amdgcn_sdot4((int)x.x, (int)(dw & 0x03030303u), a1[j], false);
+        a4[j] = __builtin_amdgcn_sdot4((int)x.y, (int)(dw & 0x0C0C0C0Cu), a4[j], false);
         a1[j] = __builtin_amdgcn_sdot4((int)x.z, (int)(d4 & 0x03030303u), a1[j], false);
         a4[j] = __builtin_amdgcn_sdot4((int)x.w, (int)(d4 & 0x0C0C0C0Cu), a4[j], false);
     }
 }
 
-constexpr int kBatch = 8;  // tiles in flight per wave
+// Column value of a strip (lanes with q < 4 own column 4 r + q); clears the
+// accumulators.  `corr` is the activation sum over the strip's units (the
+// u = w + 1 encoding adds it to every column).
+__device__ __forceinline__ int reduce_strip(int (&a1)[4], int (&a4)[4], int corr) {
+    const int q = threadIdx.x & 15;
+    int v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = row_sum16(a1[j] + (a4[j] >> 2));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) a1[j] = a4[j] = 0;
+    return (q == 0 ? v[0] : (q == 1 ? v[1] : (q == 2 ? v[2] : v[3]))) - corr;
+}
 
-// One wave processes local tiles [la, lb) of GEMV d.
-__device__ void run_wave(const GemvDesc& d, const int8_t* lds_x, const int* usum, float s,
-                         long long la, long long lb) {
+__device__ __forceinline__ int strip_col(int st) {
     const int lane = threadIdx.x & 63;
-    const int q = lane & 15;
-    const int r = lane >> 4;
-    const int Ku = d.Ku;
-    const uint8_t* wl = d.w + lane * 16;
-    long long lt = la;
-    while (lt < lb) {
-        const int st = (int)(lt / Ku);
-        const int u0 = (int)(lt - (long long)st * Ku);
-        const int n = (int)min((long long)(Ku - u0), lb - lt);
-        int a1[4] = {0, 0, 0, 0}, a4[4] = {0, 0, 0, 0};
-        int corr = 0;
-        const uint8_t* wt = wl + lt * kTileBytes;
-        for (int i0 = 0; i0 < n; i0 += kBatch) {
-            const int m = min(kBatch, n - i0);
-            u32x4 wv[kBatch];
-#pragma unroll
-            for (int i = 0; i < kBatch; ++i)
-                if (i < m)
-                    wv[i] = __builtin_nontemporal_load(
-                        reinterpret_cast<const u32x4*>(wt + (long long)(i0 + i) * kTileBytes));
-#pragma unroll
-            for (int i = 0; i < kBatch; ++i) {
-                if (i < m) {
-                    const int u = u0 + i0 + i;
-                    const u32x4 xv = *reinterpret_cast<const u32x4*>(lds_x + u * kUnitK + q * 16);
-                    corr += usum[u];
-                    dot_tile(wv[i], xv, a1, a4);
-                }
-            }
-        }
-        int v[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = row_sum16(a1[j] + (a4[j] >> 2));
-        int val = q == 0 ? v[0] : (q == 1 ? v[1] : (q == 2 ? v[2] : v[3]));
-        val -= corr;
-        const int col = st * kStripCols + r * 4 + q;
-        if (q < 4 && col < d.N) {
-            if (u0 == 0 && n == Ku) {
-                emit(d, col, val, s);
-            } else {
-                const unsigned long long add =
-                    ((unsigned long long)n << 40) + (unsigned long long)(long long)val;
-                const unsigned long long old = __hip_atomic_fetch_add(
-                    d.fix + col, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const long long tot = (long long)(old + add);
-                const long long units = (tot + (1LL << 39)) >> 40;
-                if (units == (long long)Ku) {
-                    const long long sum = tot - (units << 40);
-                    __hip_atomic_store(d.fix + col, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    emit(d, col, (int)sum, s);
-                }
-            }
-        }
-        lt += n;
+    return st * kStripCols + (lane >> 4) * 4 + (lane & 15);
+}
+
+__device__ __forceinline__ bool col_owner(const GemvDesc& d, int st) {
+    return (threadIdx.x & 15) < 4 && strip_col(st) < d.N;
+}
+
+// Fix-up slot word: units << 40 plus the signed partial sum.
+__device__ __forceinline__ unsigned long long part_word(int units, int val) {
+    return ((unsigned long long)units << 40) + (unsigned long long)(long long)val;
+}
+
+__device__ __forceinline__ unsigned long long part_add(const GemvDesc& d, int col, unsigned long long w) {
+    return __hip_atomic_fetch_add(gptr(d.fix) + col, w,
+                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// After this wave's add: if the slot now counts all Ku units, write the
+// column and clear the slot for the next launch.
+__device__ __forceinline__ void part_complete(const GemvDesc& d, int col, unsigned long long tot_u, float s) {
+    const long long tot = (long long)tot_u;
+    const long long units = (tot + (1LL << 39)) >> 40;
+    if (units == (long long)d.Ku) {
+        __hip_atomic_store(gptr(d.fix) + col, 0ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        emit(d, col, (int)(tot - (units << 40)), s);
     }
 }
 
+__device__ __forceinline__ u32x4 load_tile(__amdgpu_buffer_rsrc_t rs, int voff, int tile) {
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, voff, tile * kTileBytes, 2 /* nt */);
+}
+
+__device__ __forceinline__ void load_batch(u32x4 (&w)[kBatch], __amdgpu_buffer_rsrc_t rs, int voff, int i0) {
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) w[i] = load_tile(rs, voff, i0 + i);
+}
+
+struct Piece {
+    int st, u, u_start, corr;
+    int first_val, first_units, first_st;  // the leading partial strip, combined after the loop
+    bool has_first;
+    int a1[4], a4[4];
+};
+
+// Reduce tiles [i0, min(i0 + kBatch, n)) of the piece from registers `w`.
+__device__ __forceinline__ void compute_batch(const GemvDesc& d, const u32x4 (&w)[kBatch], int i0, int n,
+                                              const int8_t* lds_x, const int* usum, float s, Piece& p) {
+    const int q = threadIdx.x & 15;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+        if (i0 + i < n) {
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(lds_x + p.u * kUnitK + q * 16);
+            p.corr += usum[p.u];
+            dot_tile(w[i], xv, p.a1, p.a4);
+            ++p.u;
+            if (p.u == d.Ku) {
+                const int val = reduce_strip(p.a1, p.a4, p.corr);
+                if (p.u_start == 0) {
+                    if (col_owner(d, p.st)) emit(d, strip_col(p.st), val, s);
+                } else {
+                    p.first_val = val;
+                    p.first_units = p.u - p.u_start;
+                    p.first_st = p.st;
+                    p.has_first = true;
+                }
+                p.st += 1;
+                p.u = 0;
+                p.u_start = 0;
+                p.corr = 0;
+            }
+        }
+    }
+}
+
+// One wave streams local tiles [la, la + n) of GEMV d; `wa` holds the first
+// batch already.
+__device__ void run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usum, float s, int la, int n,
+                          __amdgpu_buffer_rsrc_t rs, int voff, u32x4 (&wa)[kBatch]) {
+    Piece p;
+    p.st = la / d.Ku;
+    p.u = la - p.st * d.Ku;
+    p.u_start = p.u;
+    p.corr = 0;
+    p.first_val = p.first_units = p.first_st = 0;
+    p.has_first = false;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) p.a1[j] = p.a4[j] = 0;
+    u32x4 wb[kBatch];
+    int i0 = 0;
+    while (true) {
+        load_batch(wb, rs, voff, i0 + kBatch);
+        compute_batch(d, wa, i0, n, lds_x, usum, s, p);
+        i0 += kBatch;
+        if (i0 >= n) break;
+        load_batch(wa, rs, voff, i0 + kBatch);
+        compute_batch(d, wb, i0, n, lds_x, usum, s, p);
+        i0 += kBatch;
+        if (i0 >= n) break;
+    }
+    // Strips shared with neighbouring pieces: add both partials, then check.
+    const bool has_last = p.u != p.u_start;
+    unsigned long long w_last = 0, o_last = 0, w_first = 0, o_first = 0;
+    if (has_last) {
+        w_last = part_word(p.u - p.u_start, reduce_strip(p.a1, p.a4, p.corr));
+        if (col_owner(d, p.st)) o_last = part_add(d, strip_col(p.st), w_last);
+    }
+    if (p.has_first) {
+        w_first = part_word(p.first_units, p.first_val);
+        if (col_owner(d, p.first_st)) o_first = part_add(d, strip_col(p.first_st), w_first);
+    }
+    if (has_last && col_owner(d, p.st)) part_complete(d, strip_col(p.st), o_last + w_last, s);
+    if (p.has_first && col_owner(d, p.first_st)) part_complete(d, strip_col(p.first_st), o_first + w_first, s);
+}
+
+// kList: GEMVs come from the device table `list` (plan launches); otherwise
+// the single descriptor is a kernel argument.  Two instantiations keep the
+// descriptor in scalar registers either way.
+template <bool kList>
 __global__ __launch_bounds__(kThreads) void gemv_t16_kernel(GemvDesc single,
                                                             const GemvDesc* __restrict__ list,
                                                             int n_list, long long total, int n_wg) {
@@ -240,7 +382,7 @@ __global__ __launch_bounds__(kThreads) void gemv_t16_kernel(GemvDesc single,
     if (t_begin >= t_end) return;
 
     int di = 0;
-    if (n_list > 0) {
+    if (kList) {
         int lo = 0, hi = n_list - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
@@ -248,22 +390,28 @@ __global__ __launch_bounds__(kThreads) void gemv_t16_kernel(GemvDesc single,
         }
         di = lo;
     }
+    const int wave = uniform(threadIdx.x >> 6);
+    const int voff = (threadIdx.x & 63) * 16;
     long long t = t_begin;
-    const int wave = threadIdx.x >> 6;
     while (t < t_end) {
-        const GemvDesc d = n_list > 0 ? list[di] : single;
+        const GemvDesc d = kList ? list[di] : single;
         const long long seg_end = min(t_end, d.tile0 + (long long)d.n_strips * d.Ku);
+        const long long nseg = seg_end - t;
+        const int la = (int)(t + nseg * wave / kWaves - d.tile0);
+        const int lb = (int)(t + nseg * (wave + 1) / kWaves - d.tile0);
+        const int n = lb - la;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(d.w + (long long)la * kTileBytes), 0, n * kTileBytes, 0x00020000);
+        u32x4 wa[kBatch];
+        load_batch(wa, rs, voff, 0);  // in flight while the activations are staged
         int8_t* lds_x = reinterpret_cast<int8_t*>(lds_raw);
         int* usum = reinterpret_cast<int*>(lds_raw + d.Ku * kUnitK);
         float* red = reinterpret_cast<float*>(lds_raw + d.Ku * kUnitK + d.Ku * 4);
         __syncthreads();  // the previous segment is done with LDS
         const float act = stage_x(d, lds_x, usum, red, t == d.tile0);
         __syncthreads();
-        const float s = act * d.w_scale;  // x_scale * w_scale, in this order (forward.cpp:342)
-        const long long n = seg_end - t;
-        const long long a = t + n * wave / kWaves;
-        const long long b = t + n * (wave + 1) / kWaves;
-        if (a < b) run_wave(d, lds_x, usum, s, a - d.tile0, b - d.tile0);
+        const float s = act * d.w_scale;  // x_scale * w_scale (forward.cpp:342)
+        if (n > 0) run_piece(d, lds_x, usum, s, la, n, rs, voff, wa);
         t = seg_end;
         ++di;
     }
@@ -273,15 +421,19 @@ __global__ __launch_bounds__(kThreads) void gemv_t16_kernel(GemvDesc single,
 
 int gemv_max_wg_per_cu(int lds_bytes) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel, kThreads, lds_bytes) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel<true>, kThreads, lds_bytes) != hipSuccess)
         return 0;
     return n;
 }
 
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, int n_list,
                        long long total_tiles, int n_wg, int lds_bytes, hipStream_t st) {
-    hipLaunchKernelGGL(gemv_t16_kernel, dim3(n_wg), dim3(kThreads), lds_bytes, st, single, list_dev,
-                       n_list, total_tiles, n_wg);
+    if (list_dev)
+        hipLaunchKernelGGL(gemv_t16_kernel<true>, dim3(n_wg), dim3(kThreads), lds_bytes, st, single, list_dev,
+                           n_list, total_tiles, n_wg);
+    else
+        hipLaunchKernelGGL(gemv_t16_kernel<false>, dim3(n_wg), dim3(kThreads), lds_bytes, st, single, list_dev,
+                           n_list, total_tiles, n_wg);
     return hipGetLastError();
 }
 
