@@ -128,8 +128,9 @@ def lane_macs(cfg) -> int:
 
 def time_launches(launch_fns, steps: int, warmup: int):
     """Run launch_fns[i % len] for warmup + steps; returns (wall ms per step,
-    mean HIP-event ms per step).  Each step is bracketed by events on the
-    launch stream (torch's current stream)."""
+    mean and median HIP-event ms per step).  The timed steps are bracketed by
+    synchronize; each step is bracketed by events on the launch stream
+    (torch's current stream)."""
     import torch
     n = len(launch_fns)
     for i in range(warmup):
@@ -236,25 +237,37 @@ def run_m1(args, cfg, fp32_x: bool):
     assert plans[0].bytes == bytes_alg, (plans[0].bytes, bytes_alg)
     mac = macs(cfg)
 
-    # timed region (the contract's K steps, bracketed by synchronize)
+    # Timed region: the contract's K steps, one work-list launch each, rotating
+    # over the weight copies, bracketed by synchronize.  HIP events on the
+    # launch stream bracket every launch (recorded without synchronizing), so
+    # the mean per-launch duration comes from the same region.  The launch is
+    # one ctypes call; the host stays ahead of the GPU (a launch takes far
+    # less host time than its kernel), so the wall time is the GPU's.
     fns = [p.launch for p in plans]
-    for i in range(args.warmup):
-        fns[i % len(fns)]()
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    for i in range(args.steps):
-        fns[(args.warmup + i) % len(fns)]()
-    torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t_start) * 1e3 / args.steps
-    log(f"[bench] work-list sweep: {ms_step * 1e3:.2f} us/step (wall)")
-
-    # per-launch kernel time from HIP events on the launch stream
-    _, ev_mean, ev_med = time_launches(fns, args.steps, 2)
+    ms_step, ev_mean, ev_med = time_launches(fns, args.steps, args.warmup)
     achieved_gbs = bytes_alg / (ev_mean * 1e-3) / 1e9
-    log(f"[bench] work-list sweep: {ev_mean * 1e3:.2f} us/launch (events), {achieved_gbs:.0f} GB/s")
+    log(f"[bench] work-list sweep: {ms_step * 1e3:.2f} us/step (wall), {ev_mean * 1e3:.2f} us/launch (events), "
+        f"{achieved_gbs:.0f} GB/s")
+
+    # The same launches replayed back to back from a HIP graph (one pass over
+    # all copies per replay), bracketed as a whole.
+    rot = graph_of(lambda: [p.launch() for p in plans])
+    n_rep = max(1, args.steps // len(plans))
+    for _ in range(2):
+        rot.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n_rep):
+        rot.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    g_mean = e0.elapsed_time(e1) / (n_rep * len(plans))
 
     modes = {"worklist_1_launch": dict(us=round(ev_mean * 1e3, 2), us_median=round(ev_med * 1e3, 2),
-                                       gbs=round(achieved_gbs, 1))}
+                                       gbs=round(achieved_gbs, 1)),
+             "worklist_graph_back_to_back": dict(us=round(g_mean * 1e3, 2),
+                                                 gbs=round(bytes_alg / (g_mean * 1e-3) / 1e9, 1))}
     if not args.quick:
         # The same sweep as (a) one launch per GEMV and (b) 4 launches per
         # layer grouped like a decode step; both captured in HIP graphs so the
@@ -359,7 +372,8 @@ def run_batched(args):
         for l in range(cfg["layers"]):
             for nm, K, N in cfg["shapes"]:
                 T.mm_batched(layers[l][nm], q[X_OF[nm]], y=Y[nm], x_scale_dev=s[X_OF[nm]])
-    wall, evm, _ = time_launches([step], args.steps, args.warmup)
+    g_step = graph_of(step)
+    wall, evm, _ = time_launches([g_step.replay], args.steps, args.warmup)
     mac = macs(cfg, M)
     b = alg_bytes(cfg, True, M)
     gbs = b / (evm * 1e-3) / 1e9
