@@ -176,6 +176,24 @@ void ter_hip_plan_destroy(ter_hip_plan_t* plan);
 int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, float* y,
                  int32_t* acc, void* stream);
 
+/* Many independent GEMMs in ONE launch (batched decode / prefill over a
+ * layer sweep; replaces one mm_bitnet_addonly_batched_k launch per
+ * projection).  X is int8 [M][K] (row stride K) with per-row device scales
+ * x_scale_dev[M] (quantize fp32 rows with ter_hip_quant_int8 first).  The
+ * plan is launched, queried and destroyed with ter_hip_plan_launch /
+ * ter_hip_plan_stats / ter_hip_plan_destroy. */
+typedef struct ter_hip_gemm_item {
+    const ter_hip_wpk_t* w;
+    const int8_t*        x;            /* device int8 [M][K]                 */
+    const float*         x_scale_dev;  /* device fp32 [M]                    */
+    int32_t              M;
+    float*               y;            /* fp32 [M][N] or NULL                */
+    int32_t*             acc;          /* int32 [M][N] or NULL               */
+} ter_hip_gemm_item_t;
+
+int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* items, int32_t n,
+                             int32_t wg_per_cu);
+
 /* Per-row absmax int8 quantizer (quant_int8_k, cuda/ter_cuda_forward_packed.cu:40-62):
  * q[m][k] = rn(x[m][k] * 127/(max_k|x[m][k]| + 1e-9)), scale_out[m] = 1/that. */
 int ter_hip_quant_int8(const float* x, int32_t M, int32_t K, int8_t* q, float* scale_out,

@@ -6,6 +6,7 @@ with ctypes.  See ter_amd.fabric for the host interface.
 """
 from . import _lib  # noqa: F401
 from .fabric import (  # noqa: F401
+    GemmPlan,
     Handle,
     PackedTrits,
     Plan,
@@ -18,5 +19,5 @@ from .fabric import (  # noqa: F401
     synth_v11,
 )
 
-__all__ = ["Handle", "PackedTrits", "Plan", "gemv", "mm_batched", "mm_packed_dispatch", "mm_row",
+__all__ = ["GemmPlan", "Handle", "PackedTrits", "Plan", "gemv", "mm_batched", "mm_packed_dispatch", "mm_row",
            "quant_int8", "synth_i8", "synth_v11"]

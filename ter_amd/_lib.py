@@ -69,6 +69,17 @@ class GemvItem(C.Structure):
     ]
 
 
+class GemmItem(C.Structure):
+    _fields_ = [
+        ("w", C.POINTER(WPK)),
+        ("x", C.c_void_p),
+        ("x_scale_dev", C.c_void_p),
+        ("M", C.c_int32),
+        ("y", C.c_void_p),
+        ("acc", C.c_void_p),
+    ]
+
+
 class OpCounts(C.Structure):
     _fields_ = [
         ("total_ops", C.c_uint64),
@@ -99,6 +110,7 @@ SIGNATURES = [
     ("ter_hip_plan_stats", C.c_int, [_P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_int32)]),
     ("ter_hip_plan_destroy", None, [_P]),
     ("ter_hip_gemm", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, _P, _P, _P]),
+    ("ter_hip_gemm_plan_create", C.c_int, [C.POINTER(C.c_void_p), C.POINTER(GemmItem), C.c_int32, C.c_int32]),
     ("ter_hip_quant_int8", C.c_int, [_P, C.c_int32, C.c_int32, _P, _P, _P]),
     ("ter_hip_create", _P, [C.c_int32]),
     ("ter_hip_destroy", None, [_P]),

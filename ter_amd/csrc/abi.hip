@@ -108,6 +108,49 @@ int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, int* n_wg) {
     return TER_HIP_OK;
 }
 
+// per_block: strips per block of the launch (kWaves * strips per wave for its row-block count).
+GemmDesc make_gemm_desc(const ter_hip_wpk_t* w, const int8_t* x, const float* xs, int M, float* y, int32_t* acc,
+                        long long block0, int per_block) {
+    GemmDesc d{};
+    d.w = w->data;
+    d.x = x;
+    d.xs = xs;
+    d.y = y;
+    d.acc = acc;
+    d.block0 = block0;
+    d.K = w->K;
+    d.N = w->N;
+    d.Ku = units_of(w->K);
+    d.n_strips = strips_of(w->N);
+    d.M = M;
+    d.ldx = w->K;
+    d.n_blocks = (d.n_strips + per_block - 1) / per_block;
+    d.w_scale = w->scale;
+    return d;
+}
+
+bool gemm_vec_ok(const GemmDesc& d) { return aligned(d.x, 16) && d.ldx % 16 == 0; }
+
+// GEMM workgroups: up to kGemmWgPerCu per CU (more weight bytes in flight
+// for the HBM-bound small-M blocks), capped by occupancy and by the block count.
+constexpr int kGemmWgPerCu = 8;
+
+int pick_gemm_wg(long long blocks, int mb, int wg_per_cu, int* n_wg) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const int cus = device_cu_count(dev);
+    if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
+    const int fit = gemm_max_wg_per_cu(mb);
+    if (fit <= 0) return fail(TER_HIP_ERR_HIP, "GEMM occupancy query failed");
+    const int per_cu = wg_per_cu > 0 ? wg_per_cu : (kGemmWgPerCu < fit ? kGemmWgPerCu : fit);
+    long long g = (long long)cus * per_cu;
+    if (g > blocks) g = blocks;
+    if (g < 1) g = 1;
+    *n_wg = (int)g;
+    return TER_HIP_OK;
+}
+
 }  // namespace
 
 int device_cu_count(int device) {
@@ -127,11 +170,14 @@ int device_cu_count(int device) {
 using namespace terhip;
 
 struct ter_hip_plan {
-    GemvDesc* descs_dev = nullptr;
+    void* descs_dev = nullptr;   // GemvDesc[n] (GEMV plan) or GemmDesc[n] (GEMM plan)
     int n = 0;
-    long long total_tiles = 0;
+    bool gemm = false;
+    long long total = 0;         // tiles (GEMV) or blocks (GEMM) of one launch
     int n_wg = 0;
-    int lds_bytes = 0;
+    int lds_bytes = 0;           // GEMV
+    int mb = 0;                  // GEMM row-block count
+    bool vec = false;            // GEMM: 16-byte X rows
     uint64_t bytes = 0, macs = 0;
 };
 
@@ -346,7 +392,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         return hip_fail(e, "plan descriptor upload");
     }
     p->n = n;
-    p->total_tiles = tile;
+    p->total = tile;
     p->n_wg = n_wg;
     p->lds_bytes = lds;
     p->bytes = bytes;
@@ -357,9 +403,16 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
 
 int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
     if (!plan) return fail(TER_HIP_ERR_NULL, "null plan");
-    GemvDesc none{};
-    hipError_t e = launch_gemv(none, plan->descs_dev, plan->n, plan->total_tiles, plan->n_wg, plan->lds_bytes,
-                               static_cast<hipStream_t>(stream));
+    hipError_t e;
+    if (plan->gemm) {
+        GemmDesc none{};
+        e = launch_gemm_list(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->n, plan->total, plan->n_wg,
+                             plan->mb, plan->vec, static_cast<hipStream_t>(stream));
+    } else {
+        GemvDesc none{};
+        e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->n, plan->total, plan->n_wg,
+                        plan->lds_bytes, static_cast<hipStream_t>(stream));
+    }
     if (e != hipSuccess) return hip_fail(e, "plan launch");
     return TER_HIP_OK;
 }
@@ -405,8 +458,71 @@ int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, floa
         xq = x->q_out;
         xs = x->scale_out;
     }
-    hipError_t e = launch_gemm(w->data, w->K, w->N, xq, xs, M, w->scale, y, acc, st);
+    const int mb = gemm_mb_of(M);
+    const GemmDesc d = make_gemm_desc(w, xq, xs, M, y, acc, 0, kWaves * gemm_strips_per_wave(mb));
+    int n_wg = 0;
+    rc = pick_gemm_wg(d.n_blocks, mb, 0, &n_wg);
+    if (rc) return rc;
+    hipError_t e = launch_gemm_list(d, nullptr, 0, d.n_blocks, n_wg, mb, gemm_vec_ok(d), st);
     if (e != hipSuccess) return hip_fail(e, "gemm launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* items, int32_t n,
+                             int32_t wg_per_cu) {
+    if (!plan || !items) return fail(TER_HIP_ERR_NULL, "null plan or items");
+    *plan = nullptr;
+    if (n < 1) return fail(TER_HIP_ERR_SHAPE, "empty work list");
+    std::vector<GemmDesc> ds((size_t)n);
+    long long blocks = 0;
+    uint64_t bytes = 0, macs = 0;
+    int max_m = 1;
+    bool vec = true;
+    for (int i = 0; i < n; ++i) {
+        const ter_hip_gemm_item_t& it = items[i];
+        int rc = check_wpk(it.w);
+        if (rc) return rc;
+        if (!it.x || !it.x_scale_dev) return fail(TER_HIP_ERR_NULL, "item %d: null X or X scales", i);
+        if (it.M < 1 || it.M > TER_HIP_M_MAX)
+            return fail(TER_HIP_ERR_SHAPE, "item %d: M=%d out of range [1,%d]", i, it.M, TER_HIP_M_MAX);
+        if (!it.y && !it.acc) return fail(TER_HIP_ERR_NULL, "item %d has no output", i);
+        if (it.M > max_m) max_m = it.M;
+    }
+    const int mb = gemm_mb_of(max_m);  // one row-block count (and block width) per launch
+    const int per_block = kWaves * gemm_strips_per_wave(mb);
+    for (int i = 0; i < n; ++i) {
+        const ter_hip_gemm_item_t& it = items[i];
+        ds[(size_t)i] = make_gemm_desc(it.w, it.x, it.x_scale_dev, it.M, it.y, it.acc, blocks, per_block);
+        blocks += ds[(size_t)i].n_blocks;
+        vec = vec && gemm_vec_ok(ds[(size_t)i]);
+        bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.M * it.w->K + (uint64_t)it.M * it.w->N * 4u;
+        macs += (uint64_t)it.M * (uint64_t)it.w->K * (uint64_t)it.w->N;
+    }
+    int n_wg = 0;
+    int rc = pick_gemm_wg(blocks, mb, wg_per_cu, &n_wg);
+    if (rc) return rc;
+    ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
+    if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
+    hipError_t e = hipMalloc(&p->descs_dev, sizeof(GemmDesc) * (size_t)n);
+    if (e != hipSuccess) {
+        delete p;
+        return hip_fail(e, "plan descriptor allocation");
+    }
+    e = hipMemcpy(p->descs_dev, ds.data(), sizeof(GemmDesc) * (size_t)n, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(p->descs_dev);
+        delete p;
+        return hip_fail(e, "plan descriptor upload");
+    }
+    p->n = n;
+    p->gemm = true;
+    p->total = blocks;
+    p->n_wg = n_wg;
+    p->mb = mb;
+    p->vec = vec;
+    p->bytes = bytes;
+    p->macs = macs;
+    *plan = p;
     return TER_HIP_OK;
 }
 

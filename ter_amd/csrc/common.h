@@ -54,6 +54,20 @@ struct alignas(16) GemvDesc {
     int32_t x_kind, pad_;
 };
 
+// One GEMM (M > 1) of a work list.  Its blocks (4 column strips x all K each)
+// are numbered block0 .. block0 + n_blocks - 1 in the launch's block stream.
+struct alignas(16) GemmDesc {
+    const uint8_t* w;            // T16 tile stream
+    const int8_t* x;             // int8 [M][ldx]
+    const float* xs;             // per-row activation scales [M] (device)
+    float* y;                    // fp32 [M][N] or null
+    int32_t* acc;                // int32 [M][N] or null
+    long long block0;
+    int32_t K, N, Ku, n_strips;
+    int32_t M, ldx, n_blocks;
+    float w_scale;
+};
+
 // Host launchers (defined in the .hip files).
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, int n_list,
                        long long total_tiles, int n_wg, int lds_bytes, hipStream_t st);
@@ -63,8 +77,16 @@ hipError_t launch_synth_v11(uint8_t* v11, int K, int N, uint64_t seed, uint32_t 
                             hipStream_t st);
 hipError_t launch_synth_i8(int8_t* x, long long n, uint64_t seed, int lo, int hi, hipStream_t st);
 hipError_t launch_quant_rows(const float* x, int M, int K, int8_t* q, float* s, hipStream_t st);
-hipError_t launch_gemm(const uint8_t* w, int K, int N, const int8_t* xq, const float* xs, int M,
-                       float w_scale, float* y, int32_t* acc, hipStream_t st);
+// Rows per MFMA row block group: MB = 1, 2, 4, 8, 16 for M up to 16, 32, 64, 128, 256.
+int gemm_mb_of(int M);
+// vec: every x pointer 16-byte aligned and every ldx a multiple of 16.
+hipError_t launch_gemm_list(const GemmDesc& single, const GemmDesc* list_dev, int n_list, long long total_blocks,
+                            int n_wg, int mb, bool vec, hipStream_t st);
+// Resident GEMM workgroups per CU for row-block count mb (0 if the query fails).
+int gemm_max_wg_per_cu(int mb);
+// Column strips per wave of the GEMM for row-block count mb (a block is
+// kWaves * that many strips).
+int gemm_strips_per_wave(int mb);
 
 // LDS bytes the GEMV kernel needs for a K: X (Ku*256 int8) + unit sums + scratch.
 inline int gemv_lds_bytes(int32_t K) { return units_of(K) * kUnitK + units_of(K) * 4 + 64; }

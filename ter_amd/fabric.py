@@ -237,6 +237,50 @@ class Plan:
             pass
 
 
+class GemmPlan:
+    """Many independent M > 1 GEMMs in one launch.  `items` is a sequence of
+    dicts {w: PackedTrits, x: int8 [M][K] tensor, x_scale_dev: fp32 [M]
+    tensor, y?: fp32 [M][N], acc?: int32 [M][N]}."""
+
+    def __init__(self, items: Sequence[dict], wg_per_cu: int = 0):
+        n = len(items)
+        arr = (L.GemmItem * n)()
+        self._keep: List = []
+        torch = _torch()
+        for i, it in enumerate(items):
+            W, x = it["w"], it["x"]
+            _require_cuda(x, "x", torch.int8)
+            if x.dim() != 2 or x.shape[1] != W.K:
+                raise ValueError(f"item {i}: x must be [M][{W.K}]")
+            arr[i].w = C.pointer(W.wpk)
+            arr[i].x = x.data_ptr()
+            arr[i].x_scale_dev = _ptr(it.get("x_scale_dev"))
+            arr[i].M = int(x.shape[0])
+            arr[i].y = _ptr(it.get("y"))
+            arr[i].acc = _ptr(it.get("acc"))
+            self._keep.append(W)
+        h = C.c_void_p()
+        L.check(L.lib().ter_hip_gemm_plan_create(C.byref(h), arr, n, int(wg_per_cu)), "ter_hip_gemm_plan_create")
+        self._h = h
+        b, m, g = C.c_uint64(), C.c_uint64(), C.c_int32()
+        L.check(L.lib().ter_hip_plan_stats(self._h, C.byref(b), C.byref(m), C.byref(g)), "ter_hip_plan_stats")
+        self.bytes, self.macs, self.n_wg = b.value, m.value, g.value
+
+    def launch(self, stream=None):
+        L.check(L.lib().ter_hip_plan_launch(self._h, _stream(stream)), "ter_hip_plan_launch")
+
+    def close(self):
+        if getattr(self, "_h", None):
+            L.lib().ter_hip_plan_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Handle:
     """K4-style handle with the KernelTable native slot (ter_k4_create /
     ter_k4_call / ter_k4_op_counts, include/ter_k4/ter_k4.h:29-55)."""

@@ -27,7 +27,7 @@ def declared_functions():
 
 def test_library_exports_every_declared_symbol():
     names = declared_functions()
-    assert len(names) == 24, names
+    assert len(names) == 25, names
     lib = L.lib()
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
@@ -141,6 +141,29 @@ def test_plan_validation():
         it.x.kind = L.X_I8
         it.y = fake
     assert lib.ter_hip_plan_create(C.byref(h), items2, 2, 0) == L.ERR_CONFLICT  # same weight twice
+
+
+def test_gemm_plan_validation():
+    lib = L.lib()
+    h = C.c_void_p()
+    items = (L.GemmItem * 1)()
+    assert lib.ter_hip_gemm_plan_create(None, items, 1, 0) == L.ERR_NULL
+    assert lib.ter_hip_gemm_plan_create(C.byref(h), items, 0, 0) == L.ERR_SHAPE
+    assert lib.ter_hip_gemm_plan_create(C.byref(h), items, 1, 0) == L.ERR_NULL  # null weight
+    w = L.WPK()
+    fake = 1 << 20
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, lib.ter_hip_wpk_bytes(64, 16), 64, 16, 1.0) == L.OK
+    items[0].w = C.pointer(w)
+    assert lib.ter_hip_gemm_plan_create(C.byref(h), items, 1, 0) == L.ERR_NULL  # null X
+    items[0].x = fake
+    items[0].x_scale_dev = fake
+    items[0].y = fake
+    for bad_m in (0, L.M_MAX + 1):
+        items[0].M = bad_m
+        assert lib.ter_hip_gemm_plan_create(C.byref(h), items, 1, 0) == L.ERR_SHAPE
+    items[0].M = 8
+    items[0].y = None
+    assert lib.ter_hip_gemm_plan_create(C.byref(h), items, 1, 0) == L.ERR_NULL  # no output
 
 
 def test_kernel_table_slots_and_codes():

@@ -102,3 +102,56 @@ def test_quant_int8_kernel(cuda):
     rq, rs = O.quant_int8_rows(x)
     assert (host(q) == rq).all()
     assert (host(s).view(np.int32) == rs.view(np.int32)).all()
+
+
+def test_gemm_plan_mixed(cuda):
+    """Many GEMMs in one launch (GemmPlan): ragged shapes, different M per
+    item, unaligned K (byte-wise X staging), launched twice."""
+    import torch
+    import ter_amd as T
+    specs = [(8, 2560, 640), (32, 2560, 2560), (3, 300, 20), (17, 6912, 256), (8, 2048, 512), (1, 64, 16)]
+    items, refs = [], []
+    for i, (M, K, N) in enumerate(specs):
+        v11 = O.v11_pack(O.rand_trits(900 + i, K, N, 0.4))
+        X = O.rand_int8(950 + i, M * K).reshape(M, K)
+        xs = (0.002 * (np.arange(M) + 1 + i)).astype(np.float32)
+        W = T.PackedTrits.from_v11(v11, K, N, 0.03 + 0.01 * i)
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+        items.append(dict(w=W, x=dev(X), x_scale_dev=dev(xs), y=y, acc=acc))
+        refs.append(O.gemm_v11(X, xs, v11, 0.03 + 0.01 * i, K, N))
+    for wg_per_cu in (0, 1):
+        plan = T.GemmPlan(items, wg_per_cu=wg_per_cu)
+        for rep in range(2):
+            for it in items:
+                it["acc"].fill_(-9)
+                it["y"].fill_(-9)
+            plan.launch()
+            for it, (ra, ry) in zip(items, refs):
+                assert (host(it["acc"]) == ra).all(), (wg_per_cu, rep, it["w"].K, it["w"].N)
+                assert_f32_equal(host(it["y"]), ry)
+        plan.close()
+
+
+@pytest.mark.parametrize("M", [8, 32, 128])
+def test_gemm_plan_bitnet_layer(cuda, M):
+    """One BitNet-2B layer (7 projections) at the C4 batch sizes in one launch."""
+    import torch
+    import ter_amd as T
+    shapes = [(2560, 2560), (2560, 640), (2560, 640), (2560, 2560), (2560, 6912), (2560, 6912), (6912, 2560)]
+    xs_of = {}
+    items, refs = [], []
+    for i, (K, N) in enumerate(shapes):
+        v11 = O.v11_pack(O.rand_trits(70 + i, K, N, 0.4))
+        if K not in xs_of:
+            Xf = O.rand_normal_f32(K + M, M * K).reshape(M, K)
+            q, s = O.quant_int8_rows(Xf)
+            xs_of[K] = (q, s, dev(q), dev(s))
+        q, s, qd, sd = xs_of[K]
+        W = T.PackedTrits.from_v11(v11, K, N, 0.05)
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        items.append(dict(w=W, x=qd, x_scale_dev=sd, y=y))
+        refs.append(O.gemm_v11(q, s, v11, 0.05, K, N)[1])
+    T.GemmPlan(items).launch()
+    for it, ry in zip(items, refs):
+        assert_f32_equal(host(it["y"]), ry)
