@@ -389,6 +389,9 @@ def run_batched(args):
     gbs = plan.bytes / (ev_plan * 1e-3) / 1e9
     tops = 2 * mac / (ev_plan * 1e-3) / 1e12
     hbm_bound = M <= 64
+    # the library streams M <= 16 when M rows of the widest X fit 64 KiB of LDS
+    ku = max(-(-K // 256) for _, K, _ in cfg["shapes"])
+    kernel = "gemm_stream_kernel" if M <= 16 and M * (ku * 256 + 16) + 64 <= 65536 else "gemm_t16_kernel"
     return {
         "metric": f"batched packed-trit GEMM, M={M}, BitNet-2B sweep",
         "value": round(mac / (wall * 1e-3) / 1e9, 1), "unit": "GMAC/s", "n_gpus": 1, "steps": args.steps,
@@ -403,7 +406,7 @@ def run_batched(args):
                      "peak": HBM_PEAK_GBS if hbm_bound else MFMA_I8_PEAK_TOPS,
                      "unit": "GB/s" if hbm_bound else "TOP/s",
                      "frac": round(gbs / HBM_PEAK_GBS if hbm_bound else tops / MFMA_I8_PEAK_TOPS, 4),
-                     "traffic": None, "kernel": "gemm_t16_kernel", "bytes_per_launch": plan.bytes,
+                     "traffic": None, "kernel": kernel, "bytes_per_launch": plan.bytes,
                      "mean_launch_us": round(ev_plan * 1e3, 3)},
         "cpu_baseline": None,
     }

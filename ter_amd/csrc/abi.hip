@@ -110,7 +110,7 @@ int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, int* n_wg) {
 
 // per_block: strips per block of the launch (kWaves * strips per wave for its row-block count).
 GemmDesc make_gemm_desc(const ter_hip_wpk_t* w, const int8_t* x, const float* xs, int M, float* y, int32_t* acc,
-                        long long block0, int per_block) {
+                        long long block0, int per_block, long long tile0) {
     GemmDesc d{};
     d.w = w->data;
     d.x = x;
@@ -118,6 +118,7 @@ GemmDesc make_gemm_desc(const ter_hip_wpk_t* w, const int8_t* x, const float* xs
     d.y = y;
     d.acc = acc;
     d.block0 = block0;
+    d.tile0 = tile0;
     d.K = w->K;
     d.N = w->N;
     d.Ku = units_of(w->K);
@@ -134,6 +135,26 @@ bool gemm_vec_ok(const GemmDesc& d) { return aligned(d.x, 16) && d.ldx % 16 == 0
 // GEMM workgroups: up to kGemmWgPerCu per CU (more weight bytes in flight
 // for the HBM-bound small-M blocks), capped by occupancy and by the block count.
 constexpr int kGemmWgPerCu = 8;
+
+// Streaming GEMM (M <= 16): kGemmWgPerCuStream workgroups per CU, capped by
+// occupancy at this LDS size.
+constexpr int kGemmWgPerCuStream = 2;
+
+int pick_stream_wg(long long tiles, int lds, int wg_per_cu, int* n_wg) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const int cus = device_cu_count(dev);
+    if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
+    const int fit = gemm_stream_max_wg_per_cu(lds);
+    if (fit <= 0) return fail(TER_HIP_ERR_HIP, "GEMM occupancy query failed");
+    const int per_cu = wg_per_cu > 0 ? wg_per_cu : (kGemmWgPerCuStream < fit ? kGemmWgPerCuStream : fit);
+    long long g = (long long)cus * per_cu;
+    if (g > tiles) g = tiles;
+    if (g < 1) g = 1;
+    *n_wg = (int)g;
+    return TER_HIP_OK;
+}
 
 int pick_gemm_wg(long long blocks, int mb, int wg_per_cu, int* n_wg) {
     int dev = 0;
@@ -178,6 +199,7 @@ struct ter_hip_plan {
     int lds_bytes = 0;           // GEMV
     int mb = 0;                  // GEMM row-block count
     bool vec = false;            // GEMM: 16-byte X rows
+    bool stream = false;         // GEMM: streaming kernel (M <= 16), total counts tiles
     uint64_t bytes = 0, macs = 0;
 };
 
@@ -404,7 +426,11 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
 int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
     if (!plan) return fail(TER_HIP_ERR_NULL, "null plan");
     hipError_t e;
-    if (plan->gemm) {
+    if (plan->gemm && plan->stream) {
+        GemmDesc none{};
+        e = launch_gemm_stream(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->n, plan->total,
+                               plan->n_wg, plan->lds_bytes, plan->vec, static_cast<hipStream_t>(stream));
+    } else if (plan->gemm) {
         GemmDesc none{};
         e = launch_gemm_list(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->n, plan->total, plan->n_wg,
                              plan->mb, plan->vec, static_cast<hipStream_t>(stream));
@@ -459,11 +485,20 @@ int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, floa
         xs = x->scale_out;
     }
     const int mb = gemm_mb_of(M);
-    const GemmDesc d = make_gemm_desc(w, xq, xs, M, y, acc, 0, kWaves * gemm_strips_per_wave(mb));
+    const GemmDesc d = make_gemm_desc(w, xq, xs, M, y, acc, 0, kWaves * gemm_strips_per_wave(mb), 0);
     int n_wg = 0;
-    rc = pick_gemm_wg(d.n_blocks, mb, 0, &n_wg);
-    if (rc) return rc;
-    hipError_t e = launch_gemm_list(d, nullptr, 0, d.n_blocks, n_wg, mb, gemm_vec_ok(d), st);
+    hipError_t e;
+    const int slds = gemm_stream_lds_bytes(M, w->K);
+    if (M <= 16 && slds <= kGemmStreamLdsMax) {
+        const long long tiles = (long long)d.n_strips * d.Ku;
+        rc = pick_stream_wg(tiles, slds, 0, &n_wg);
+        if (rc) return rc;
+        e = launch_gemm_stream(d, nullptr, 0, tiles, n_wg, slds, gemm_vec_ok(d), st);
+    } else {
+        rc = pick_gemm_wg(d.n_blocks, mb, 0, &n_wg);
+        if (rc) return rc;
+        e = launch_gemm_list(d, nullptr, 0, d.n_blocks, n_wg, mb, gemm_vec_ok(d), st);
+    }
     if (e != hipSuccess) return hip_fail(e, "gemm launch");
     return TER_HIP_OK;
 }
@@ -490,16 +525,22 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     }
     const int mb = gemm_mb_of(max_m);  // one row-block count (and block width) per launch
     const int per_block = kWaves * gemm_strips_per_wave(mb);
+    long long tiles = 0;
+    int max_k = 1;
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemm_item_t& it = items[i];
-        ds[(size_t)i] = make_gemm_desc(it.w, it.x, it.x_scale_dev, it.M, it.y, it.acc, blocks, per_block);
+        ds[(size_t)i] = make_gemm_desc(it.w, it.x, it.x_scale_dev, it.M, it.y, it.acc, blocks, per_block, tiles);
         blocks += ds[(size_t)i].n_blocks;
+        tiles += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
+        if (it.w->K > max_k) max_k = it.w->K;
         vec = vec && gemm_vec_ok(ds[(size_t)i]);
         bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.M * it.w->K + (uint64_t)it.M * it.w->N * 4u;
         macs += (uint64_t)it.M * (uint64_t)it.w->K * (uint64_t)it.w->N;
     }
     int n_wg = 0;
-    int rc = pick_gemm_wg(blocks, mb, wg_per_cu, &n_wg);
+    const int slds = gemm_stream_lds_bytes(max_m, max_k);
+    const bool stream = max_m <= 16 && slds <= kGemmStreamLdsMax;
+    int rc = stream ? pick_stream_wg(tiles, slds, wg_per_cu, &n_wg) : pick_gemm_wg(blocks, mb, wg_per_cu, &n_wg);
     if (rc) return rc;
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
@@ -516,7 +557,9 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     }
     p->n = n;
     p->gemm = true;
-    p->total = blocks;
+    p->stream = stream;
+    p->total = stream ? tiles : blocks;
+    p->lds_bytes = stream ? slds : 0;
     p->n_wg = n_wg;
     p->mb = mb;
     p->vec = vec;

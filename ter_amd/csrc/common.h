@@ -62,7 +62,8 @@ struct alignas(16) GemmDesc {
     const float* xs;             // per-row activation scales [M] (device)
     float* y;                    // fp32 [M][N] or null
     int32_t* acc;                // int32 [M][N] or null
-    long long block0;
+    long long block0;            // first block (unit-major kernel)
+    long long tile0;             // first tile in the launch's tile stream (streaming kernel)
     int32_t K, N, Ku, n_strips;
     int32_t M, ldx, n_blocks;
     float w_scale;
@@ -82,6 +83,14 @@ int gemm_mb_of(int M);
 // vec: every x pointer 16-byte aligned and every ldx a multiple of 16.
 hipError_t launch_gemm_list(const GemmDesc& single, const GemmDesc* list_dev, int n_list, long long total_blocks,
                             int n_wg, int mb, bool vec, hipStream_t st);
+// Streaming GEMM for M <= 16 (whole X of a GEMM staged in LDS, whole strips
+// per wave, no per-unit barrier).  lds_bytes = streaming_lds_bytes(max M, max K).
+inline int gemm_stream_lds_bytes(int M, int K) { return M * (units_of(K) * kUnitK + 16) + 16 * 4; }
+constexpr int kGemmStreamLdsMax = 64 * 1024;
+hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, int n_list, long long total_tiles,
+                              int n_wg, int lds_bytes, bool vec, hipStream_t st);
+int gemm_stream_max_wg_per_cu(int lds_bytes);
+
 // Resident GEMM workgroups per CU for row-block count mb (0 if the query fails).
 int gemm_max_wg_per_cu(int mb);
 // Column strips per wave of the GEMM for row-block count mb (a block is

@@ -99,10 +99,12 @@ __device__ __forceinline__ void load_unit(UnitRegs<MB, S>& r, const GemmDesc& d,
                                           __amdgpu_buffer_rsrc_t xr, int woff, int srow, int sch, int u) {
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-        const int soff = uniform((s * d.Ku + u) * kTileBytes);  // scalar offset: no waterfall loop
+        // tile offset in the range-checked vector offset (the scalar offset
+        // is not range-checked), so loads past the wave's strips read zeros
+        const int toff = woff + (s * d.Ku + u) * kTileBytes;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
-            r.w[s][ks] = __builtin_amdgcn_raw_buffer_load_b32(wr, woff + ks * 64, soff, 2 /* nt */);
+            r.w[s][ks] = __builtin_amdgcn_raw_buffer_load_b32(wr, toff + ks * 64, 0, 2 /* nt */);
     }
 #pragma unroll
     for (int i = 0; i < MB; ++i) r.x[i] = load_x16<kVec>(d, xr, srow + 16 * i, u * kUnitK + sch * 16);
@@ -253,6 +255,167 @@ __global__ __launch_bounds__(kThreads) void gemm_t16_kernel(GemmDesc single, con
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// Streaming variant for M <= 16 (one MFMA row block).  The work list is one
+// stream of tiles cut into equal contiguous ranges per workgroup, like the
+// M = 1 GEMV; a workgroup owns the strips whose first tile lies in its range.
+// Per GEMM segment it stages the whole X[0:M][0:Ku*256] in LDS once (plus
+// per-row sums), then each wave streams the tiles of a contiguous run of
+// whole strips with two batches of tiles in registers and no further
+// barrier.  A strip's 16 x 16 MFMA accumulator is written when its last
+// unit is in.
+constexpr int kSBatch = 4;
+
+template <bool kVec>
+__device__ __forceinline__ void stage_rows(const GemmDesc& d, int8_t* lx, int ldl, int* rsum) {
+    const int per_row = d.Ku * (kUnitK / 16);  // 16-byte chunks per row
+    const int nch = d.M * per_row;
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)d.x, 0, d.M * d.ldx, 0x00020000);
+    if (threadIdx.x < 16) rsum[threadIdx.x] = 0;
+    __syncthreads();
+    for (int c = threadIdx.x; c < nch; c += kThreads) {
+        const int row = c / per_row, ch = c - row * per_row;
+        const u32x4 v = load_x16<kVec>(d, xr, row, ch * 16);
+        *reinterpret_cast<u32x4*>(lx + row * ldl + ch * 16) = v;
+        // per_row is a multiple of 16, so the 16 lanes of a DPP row share `row`
+        const int s = row_sum16(sum_bytes(v));
+        if ((threadIdx.x & 15) == 0) atomicAdd(rsum + row, s);
+    }
+}
+
+__device__ __forceinline__ void stream_load(unsigned (&w)[kSBatch][4], __amdgpu_buffer_rsrc_t rs, int woff, int i0) {
+#pragma unroll
+    for (int i = 0; i < kSBatch; ++i) {
+        const int toff = woff + (i0 + i) * kTileBytes;  // range-checked: zeros past the wave's tiles
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) w[i][ks] = __builtin_amdgcn_raw_buffer_load_b32(rs, toff + ks * 64, 0, 2);
+    }
+}
+
+struct StreamState {
+    int strip, u;
+    i32x4 C;
+};
+
+__device__ __forceinline__ void stream_compute(const GemmDesc& d, const unsigned (&w)[kSBatch][4], int i0, int n,
+                                               const int8_t* arow, bool arow_ok, int st_base, const int* rsum,
+                                               const float (&xsr)[4], StreamState& p) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+#pragma unroll
+    for (int i = 0; i < kSBatch; ++i) {
+        if (i0 + i < n) {
+            const int8_t* ab = arow + p.u * kUnitK + g * 16;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                i32x4 A = *reinterpret_cast<const i32x4*>(ab + ks * 64);
+                if (!arow_ok) A = i32x4{0, 0, 0, 0};
+                const unsigned dw = w[i][ks];
+                const i32x4 B = i32x4{(int)(dw & 0x03030303u), (int)((dw >> 2) & 0x03030303u),
+                                      (int)((dw >> 4) & 0x03030303u), (int)((dw >> 6) & 0x03030303u)};
+                p.C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, p.C, 0, 0, 0);
+            }
+            if (++p.u == d.Ku) {
+                const int col = (st_base + p.strip) * kStripCols + j;
+                if (col < d.N) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int row = g * 4 + e;
+                        if (row < d.M) {
+                            const int val = p.C[e] - rsum[row];
+                            const long long o = (long long)row * d.N + col;
+                            if (d.acc) gptr(d.acc)[o] = val;
+                            if (d.y) gptr(d.y)[o] = (float)val * xsr[e];
+                        }
+                    }
+                }
+                p.C = i32x4{0, 0, 0, 0};
+                p.u = 0;
+                ++p.strip;
+            }
+        }
+    }
+}
+
+template <bool kList, bool kVec>
+__global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GemmDesc single, const GemmDesc* __restrict__ list,
+                                                               int n_list, long long total, int n_wg) {
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    int gi = blockIdx.x;
+    if ((n_wg & 7) == 0) gi = (gi & 7) * (n_wg >> 3) + (gi >> 3);
+    const long long t_begin = total * gi / n_wg;
+    const long long t_end = total * (gi + 1) / n_wg;
+    if (t_begin >= t_end) return;
+    int di = 0;
+    if (kList) {
+        int lo = 0, hi = n_list - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (list[mid].tile0 <= t_begin) lo = mid; else hi = mid - 1;
+        }
+        di = lo;
+    }
+    const int lane = threadIdx.x & 63;
+    const int wave = uniform(threadIdx.x >> 6);
+    const int g = lane >> 4, j = lane & 15;
+    const int woff = (j >> 2) * 256 + g * 16 + (j & 3) * 4;
+    long long t = t_begin;
+    while (t < t_end) {
+        const GemmDesc d = kList ? list[di] : single;
+        const long long seg_end = min(t_end, d.tile0 + (long long)d.n_strips * d.Ku);
+        const int la = (int)(t - d.tile0), lb = (int)(seg_end - d.tile0);
+        // the strips whose first tile lies in [la, lb)
+        const int st_a = (la + d.Ku - 1) / d.Ku, st_b = (lb + d.Ku - 1) / d.Ku;
+        const int ns = st_b - st_a;
+        const int w_a = st_a + ns * wave / kWaves, w_b = st_a + ns * (wave + 1) / kWaves;
+        const int n = (w_b - w_a) * d.Ku;  // this wave's tiles
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(d.w + (long long)w_a * d.Ku * kTileBytes), 0, n * kTileBytes, 0x00020000);
+        unsigned wa[kSBatch][4], wb[kSBatch][4];
+        stream_load(wa, rs, woff, 0);  // in flight while X is staged
+        const int ldl = d.Ku * kUnitK + 16;
+        int8_t* lx = reinterpret_cast<int8_t*>(lds_raw);
+        int* rsum = reinterpret_cast<int*>(lds_raw + d.M * ldl);
+        float xsr[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int row = g * 4 + e;
+            xsr[e] = row < d.M ? gptr(d.xs)[row] * d.w_scale : 0.f;
+        }
+        __syncthreads();  // the previous segment is done with LDS
+        if (ns > 0) stage_rows<kVec>(d, lx, ldl, rsum);
+        __syncthreads();
+        if (n > 0) {
+            const bool arow_ok = j < d.M;
+            const int8_t* arow = lx + (arow_ok ? j : 0) * ldl;
+            StreamState p{0, 0, i32x4{0, 0, 0, 0}};
+            int i0 = 0;
+            while (true) {
+                stream_load(wb, rs, woff, i0 + kSBatch);
+                stream_compute(d, wa, i0, n, arow, arow_ok, w_a, rsum, xsr, p);
+                i0 += kSBatch;
+                if (i0 >= n) break;
+                stream_load(wa, rs, woff, i0 + kSBatch);
+                stream_compute(d, wb, i0, n, arow, arow_ok, w_a, rsum, xsr, p);
+                i0 += kSBatch;
+                if (i0 >= n) break;
+            }
+        }
+        t = seg_end;
+        ++di;
+    }
+}
+
+template <bool kList, bool kVec>
+hipError_t launch_stream_t(const GemmDesc& single, const GemmDesc* list, int n_list, long long total, int n_wg,
+                           int lds, hipStream_t st) {
+    hipLaunchKernelGGL((gemm_stream_kernel<kList, kVec>), dim3(n_wg), dim3(kThreads), lds, st, single, list, n_list,
+                       total, n_wg);
+    return hipGetLastError();
+}
+
 template <int MB, int S>
 hipError_t launch_mbs(const GemmDesc& single, const GemmDesc* list, int n_list, long long total_blocks, int n_wg,
                       bool vec, hipStream_t st) {
@@ -289,22 +452,34 @@ int occupancy_mbs() {
 // MFMAs; a block of 4 waves covers 64 S columns).  Measured on the BitNet-2B
 // sweep: S = 1 at M <= 16 (more workgroups in flight), S = 2 up to M = 64,
 // S = 4 at M = 128 (LDS-read bound below that), 1 above (registers).
-int gemm_strips_per_wave(int mb) { return mb <= 1 ? 1 : (mb <= 4 ? 2 : (mb <= 8 ? 4 : 1)); }
+constexpr int strips_for(int mb) { return mb <= 1 ? 1 : (mb <= 4 ? 2 : (mb <= 8 ? 4 : 1)); }
+int gemm_strips_per_wave(int mb) { return strips_for(mb); }
 
 int gemm_max_wg_per_cu(int mb) {
-    const int s = gemm_strips_per_wave(mb);
-#define TER_OCC(MBV)                                              \
-    case MBV:                                                     \
-        return s == 1 ? occupancy_mbs<MBV, 1>() : (s == 2 ? occupancy_mbs<MBV, 2>() : occupancy_mbs<MBV, 4>());
     switch (mb) {
-        TER_OCC(1)
-        TER_OCC(2)
-        TER_OCC(4)
-        TER_OCC(8)
-        default:
-            return s == 1 ? occupancy_mbs<16, 1>() : (s == 2 ? occupancy_mbs<16, 2>() : occupancy_mbs<16, 4>());
+        case 1: return occupancy_mbs<1, strips_for(1)>();
+        case 2: return occupancy_mbs<2, strips_for(2)>();
+        case 4: return occupancy_mbs<4, strips_for(4)>();
+        case 8: return occupancy_mbs<8, strips_for(8)>();
+        default: return occupancy_mbs<16, strips_for(16)>();
     }
-#undef TER_OCC
+}
+
+int gemm_stream_max_wg_per_cu(int lds_bytes) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_stream_kernel<true, true>, kThreads, lds_bytes) !=
+        hipSuccess)
+        return 0;
+    return n;
+}
+
+hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, int n_list, long long total_tiles,
+                              int n_wg, int lds_bytes, bool vec, hipStream_t st) {
+    if (list_dev)
+        return vec ? launch_stream_t<true, true>(single, list_dev, n_list, total_tiles, n_wg, lds_bytes, st)
+                   : launch_stream_t<true, false>(single, list_dev, n_list, total_tiles, n_wg, lds_bytes, st);
+    return vec ? launch_stream_t<false, true>(single, list_dev, n_list, total_tiles, n_wg, lds_bytes, st)
+               : launch_stream_t<false, false>(single, list_dev, n_list, total_tiles, n_wg, lds_bytes, st);
 }
 
 int gemm_mb_of(int M) {
@@ -317,23 +492,13 @@ int gemm_mb_of(int M) {
 
 hipError_t launch_gemm_list(const GemmDesc& single, const GemmDesc* list_dev, int n_list, long long total_blocks,
                             int n_wg, int mb, bool vec, hipStream_t st) {
-    const int s = gemm_strips_per_wave(mb);
-#define TER_LAUNCH(MBV)                                                                                         \
-    case MBV:                                                                                                   \
-        if (s == 1) return launch_mbs<MBV, 1>(single, list_dev, n_list, total_blocks, n_wg, vec, st);           \
-        if (s == 2) return launch_mbs<MBV, 2>(single, list_dev, n_list, total_blocks, n_wg, vec, st);           \
-        return launch_mbs<MBV, 4>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
     switch (mb) {
-        TER_LAUNCH(1)
-        TER_LAUNCH(2)
-        TER_LAUNCH(4)
-        TER_LAUNCH(8)
-        default:
-            if (s == 1) return launch_mbs<16, 1>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
-            if (s == 2) return launch_mbs<16, 2>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
-            return launch_mbs<16, 4>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
+        case 1: return launch_mbs<1, strips_for(1)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
+        case 2: return launch_mbs<2, strips_for(2)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
+        case 4: return launch_mbs<4, strips_for(4)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
+        case 8: return launch_mbs<8, strips_for(8)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
+        default: return launch_mbs<16, strips_for(16)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
     }
-#undef TER_LAUNCH
 }
 
 }  // namespace terhip

@@ -281,8 +281,11 @@ __device__ __forceinline__ void part_complete(const GemvDesc& d, int col, unsign
     }
 }
 
+// The tile offset goes into the vector offset: the buffer's range check
+// covers the vector and immediate offsets but not the scalar one, and loads
+// past the piece must read zeros rather than whatever memory follows it.
 __device__ __forceinline__ u32x4 load_tile(__amdgpu_buffer_rsrc_t rs, int voff, int tile) {
-    return __builtin_amdgcn_raw_buffer_load_b128(rs, voff, tile * kTileBytes, 2 /* nt */);
+    return __builtin_amdgcn_raw_buffer_load_b128(rs, voff + tile * kTileBytes, 0, 2 /* nt */);
 }
 
 __device__ __forceinline__ void load_batch(u32x4 (&w)[kBatch], __amdgpu_buffer_rsrc_t rs, int voff, int i0) {

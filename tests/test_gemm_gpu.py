@@ -34,6 +34,7 @@ def assert_f32_equal(got, want):
 CASES = [
     (2, 300, 20), (8, 2560, 640), (16, 2048, 512), (17, 257, 36), (32, 2560, 640),
     (64, 640, 128), (128, 2560, 640), (200, 512, 48), (256, 256, 16), (8, 6912, 256),
+    (1, 2560, 640), (16, 6912, 64),  # M <= 16: streamed; M = 16 at K = 6912 exceeds its LDS and takes the row-block kernel
 ]
 
 
@@ -104,23 +105,22 @@ def test_quant_int8_kernel(cuda):
     assert (host(s).view(np.int32) == rs.view(np.int32)).all()
 
 
-def test_gemm_plan_mixed(cuda):
-    """Many GEMMs in one launch (GemmPlan): ragged shapes, different M per
-    item, unaligned K (byte-wise X staging), launched twice."""
+def run_plan(specs, seed, wgs):
+    """Build a GemmPlan over `specs`, launch it twice per launch shape and
+    compare every item with the oracle (outputs poisoned between launches)."""
     import torch
     import ter_amd as T
-    specs = [(8, 2560, 640), (32, 2560, 2560), (3, 300, 20), (17, 6912, 256), (8, 2048, 512), (1, 64, 16)]
     items, refs = [], []
     for i, (M, K, N) in enumerate(specs):
-        v11 = O.v11_pack(O.rand_trits(900 + i, K, N, 0.4))
-        X = O.rand_int8(950 + i, M * K).reshape(M, K)
+        v11 = O.v11_pack(O.rand_trits(seed + i, K, N, 0.4))
+        X = O.rand_int8(seed + 50 + i, M * K).reshape(M, K)
         xs = (0.002 * (np.arange(M) + 1 + i)).astype(np.float32)
         W = T.PackedTrits.from_v11(v11, K, N, 0.03 + 0.01 * i)
         y = torch.empty((M, N), dtype=torch.float32, device="cuda")
         acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
         items.append(dict(w=W, x=dev(X), x_scale_dev=dev(xs), y=y, acc=acc))
         refs.append(O.gemm_v11(X, xs, v11, 0.03 + 0.01 * i, K, N))
-    for wg_per_cu in (0, 1):
+    for wg_per_cu in wgs:
         plan = T.GemmPlan(items, wg_per_cu=wg_per_cu)
         for rep in range(2):
             for it in items:
@@ -131,6 +131,23 @@ def test_gemm_plan_mixed(cuda):
                 assert (host(it["acc"]) == ra).all(), (wg_per_cu, rep, it["w"].K, it["w"].N)
                 assert_f32_equal(host(it["y"]), ry)
         plan.close()
+
+
+def test_gemm_plan_mixed(cuda):
+    """Many GEMMs in one launch (GemmPlan): ragged shapes, different M per
+    item, unaligned K (byte-wise X staging), launched twice."""
+    run_plan([(8, 2560, 640), (32, 2560, 2560), (3, 300, 20), (17, 6912, 256), (8, 2048, 512), (1, 64, 16)],
+             900, (0, 1))
+
+
+@pytest.mark.parametrize("specs", [
+    [(8, 2560, 640), (3, 300, 20), (16, 2048, 512), (1, 64, 16), (5, 6912, 256), (12, 1000, 100)],
+    [(8, 2560, 640), (8, 2560, 2560), (1, 256, 16), (16, 512, 4000), (4, 6912, 2560)],
+], ids=["bytewise_x", "vector_x"])
+def test_gemm_plan_small_m(cuda, specs):
+    """M <= 16 plans run the streamed kernel: a workgroup's tile range may
+    start or end inside a strip or a GEMM, at several launch shapes."""
+    run_plan(specs, 700, (0, 1, 2))
 
 
 @pytest.mark.parametrize("M", [8, 32, 128])
