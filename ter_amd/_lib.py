@@ -1,7 +1,7 @@
 """ctypes bindings of libter_hip.so (the C-ABI declared in include/ter_hip.h).
 
-The library is loaded from the package directory only (it is built in-tree by
-ter_amd/build.py).  Loading fails loudly when it is missing: there is no
+The library is loaded from the package directory (it is built in-tree by
+ter_amd/build.py) unless TER_HIP_LIB names another build of it.  Loading fails loudly when it is missing: there is no
 Python or CPU fallback for any entry point.
 """
 from __future__ import annotations
@@ -10,7 +10,9 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libter_hip.so")
+# TER_HIP_LIB may name another build of the same library (e.g. a tuning build);
+# by default the in-tree one is loaded.
+LIB_PATH = os.environ.get("TER_HIP_LIB") or os.path.join(HERE, "libter_hip.so")
 
 # status codes (include/ter_hip.h)
 OK = 0

@@ -99,7 +99,7 @@ int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, int* n_wg) {
     if (fit <= 0) return fail(TER_HIP_ERR_SHAPE, "GEMV workgroup does not fit a CU (LDS %d bytes)", lds_bytes);
     int per_cu = wg_per_cu > 0 ? wg_per_cu : (kGemvWgPerCu < fit ? kGemvWgPerCu : fit);
     long long g = (long long)cus * per_cu;
-    const long long min_g = (total_tiles + kMaxPieceTiles * kWaves - 1) / (kMaxPieceTiles * kWaves);
+    const long long min_g = (total_tiles + kMaxPieceTiles * kGemvWaves - 1) / (kMaxPieceTiles * kGemvWaves);
     if (g < min_g) g = min_g;
     if (g > total_tiles) g = total_tiles;
     if (g < 1) g = 1;

@@ -28,8 +28,10 @@ namespace terhip {
 constexpr int kTileBytes = 1024;
 constexpr int kStripCols = 16;
 constexpr int kUnitK = 256;
-constexpr int kWaves = 4;                 // waves per workgroup of the GEMV kernel
+constexpr int kWaves = 4;                 // waves per workgroup of the GEMM kernels
 constexpr int kThreads = 64 * kWaves;
+constexpr int kGemvWaves = 4;             // waves per workgroup of the GEMV kernel
+constexpr int kGemvThreads = 64 * kGemvWaves;
 
 inline int32_t units_of(int32_t K) { return (K + kUnitK - 1) / kUnitK; }
 inline int32_t strips_of(int32_t N) { return (N + kStripCols - 1) / kStripCols; }

@@ -48,7 +48,7 @@ __device__ __forceinline__ TER_GLOBAL T* gptr(T* p) {
     return (TER_GLOBAL T*)p;
 }
 
-constexpr int kBatch = 4;  // tiles per batch; two batches per wave in flight
+constexpr int kBatch = 6;  // tiles per batch; two batches per wave in flight
 
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
 __device__ __forceinline__ int row_sum16(int v) {
@@ -128,60 +128,82 @@ __device__ __forceinline__ u32x4 pack_q16(const float (&v)[16], float scale) {
     return u32x4{wd[0], wd[1], wd[2], wd[3]};
 }
 
+// int8 activations x[k .. k+15] (zeros past K).
+__device__ __forceinline__ u32x4 load_i16(const int8_t* xp, int k, int K, bool vec_ok) {
+    if (vec_ok && k + 16 <= K) return *gptr(reinterpret_cast<const u32x4*>(xp + k));
+    unsigned wd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        unsigned a = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int kk = k + 4 * i + b;
+            const unsigned by = kk < K ? (unsigned)(uint8_t)gptr(xp)[kk] : 0u;
+            a |= by << (8 * b);
+        }
+        wd[i] = a;
+    }
+    return u32x4{wd[0], wd[1], wd[2], wd[3]};
+}
+
+// This thread's first two 16-element chunks of the activation vector
+// (chunks tid and tid + kGemvThreads), loaded into registers before the
+// weight batch is issued: a wave's loads return in issue order, so the
+// activations (L2-resident, shared by many workgroups) then arrive without
+// waiting behind the weight tiles from HBM.  That covers K <= 8192 with 256
+// threads; chunks beyond are loaded during staging.
+struct XPre {
+    float v0[16], v1[16];  // fp32 input
+    u32x4 q0, q1;          // int8 input
+};
+
+__device__ __forceinline__ void x_prefetch(const GemvDesc& d, XPre& r) {
+    const int nchunks = d.Ku * (kUnitK / 16);
+    const int c0 = threadIdx.x, c1 = threadIdx.x + kGemvThreads;
+    if (d.x_kind == TER_HIP_X_I8) {
+        const int8_t* xp = static_cast<const int8_t*>(d.x);
+        const bool vec_ok = ((reinterpret_cast<uintptr_t>(xp) & 15u) == 0);
+        if (c0 < nchunks) r.q0 = load_i16(xp, c0 * 16, d.K, vec_ok);
+        if (c1 < nchunks) r.q1 = load_i16(xp, c1 * 16, d.K, vec_ok);
+    } else {
+        const float* xf = static_cast<const float*>(d.x);
+        const bool vec_ok = ((reinterpret_cast<uintptr_t>(xf) & 15u) == 0);
+        if (c0 < nchunks) load_f16(xf, c0 * 16, d.K, vec_ok, r.v0);
+        if (c1 < nchunks) load_f16(xf, c1 * 16, d.K, vec_ok, r.v1);
+    }
+}
+
 // Stage the activation vector of `d` into LDS as int8 [Ku*256] (zero padded)
-// plus per-unit sums usum[Ku].  Returns the activation scale.  For fp32 input
-// this is the absmax prologue of quant_int8_k (cuda/ter_cuda_forward_packed.cu:40-62):
-// amax = max|x| + 1e-9f, scale = 127.f / amax, q = rint(x * scale) clamped to
-// [-128, 127], act_scale = 1.f / scale.  `owner` (the workgroup that starts
-// the GEMV) also writes the optional copies xq_out / xs_out.
-__device__ float stage_x(const GemvDesc& d, int8_t* lds_x, int* usum, float* red, bool owner) {
+// plus per-unit sums usum[Ku], starting from the chunks prefetched in `r`.
+// Returns the activation scale.  For fp32 input this is the absmax prologue
+// of quant_int8_k (cuda/ter_cuda_forward_packed.cu:40-62): amax = max|x| +
+// 1e-9f, scale = 127.f / amax, q = rint(x * scale) clamped to [-128, 127],
+// act_scale = 1.f / scale.  `owner` (the workgroup that starts the GEMV)
+// also writes the optional copies xq_out / xs_out.
+__device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* usum, float* red, bool owner) {
 #pragma clang fp contract(off)
     const int K = d.K;
     const int nchunks = d.Ku * (kUnitK / 16);
     const int tid = threadIdx.x;
+    const int c0 = tid, c1 = tid + kGemvThreads;
     if (d.x_kind == TER_HIP_X_I8) {
         const int8_t* xp = static_cast<const int8_t*>(d.x);
         const bool vec_ok = ((reinterpret_cast<uintptr_t>(xp) & 15u) == 0);
-        for (int c = tid; c < nchunks; c += kThreads) {
-            const int k = c * 16;
-            u32x4 v;
-            if (vec_ok && k + 16 <= K) {
-                v = *gptr(reinterpret_cast<const u32x4*>(xp + k));
-            } else {
-                unsigned wd[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    unsigned a = 0;
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) {
-                        const int kk = k + 4 * i + b;
-                        const unsigned by = kk < K ? (unsigned)(uint8_t)gptr(xp)[kk] : 0u;
-                        a |= by << (8 * b);
-                    }
-                    wd[i] = a;
-                }
-                v = u32x4{wd[0], wd[1], wd[2], wd[3]};
-            }
-            put_chunk(c, v, lds_x, usum);
-        }
+        if (c0 < nchunks) put_chunk(c0, r.q0, lds_x, usum);
+        if (c1 < nchunks) put_chunk(c1, r.q1, lds_x, usum);
+        for (int c = tid + 2 * kGemvThreads; c < nchunks; c += kGemvThreads)
+            put_chunk(c, load_i16(xp, c * 16, K, vec_ok), lds_x, usum);
         return d.x_scale_dev ? *gptr(d.x_scale_dev) : d.x_scale;
     }
-    // fp32 input.  Up to 2 chunks (32 values) per thread are held in
-    // registers across the max reduction (K <= 8192 with 256 threads); longer
-    // vectors are read a second time for the quantization pass.
     const float* xf = static_cast<const float*>(d.x);
     const bool vec_ok = ((reinterpret_cast<uintptr_t>(xf) & 15u) == 0);
-    const int c0 = tid, c1 = tid + kThreads;
-    float v0[16], v1[16];
     float m = 0.f;
-    if (c0 < nchunks) load_f16(xf, c0 * 16, K, vec_ok, v0);
-    if (c1 < nchunks) load_f16(xf, c1 * 16, K, vec_ok, v1);
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        if (c0 < nchunks) m = fmaxf(m, fabsf(v0[i]));
-        if (c1 < nchunks) m = fmaxf(m, fabsf(v1[i]));
+        if (c0 < nchunks) m = fmaxf(m, fabsf(r.v0[i]));
+        if (c1 < nchunks) m = fmaxf(m, fabsf(r.v1[i]));
     }
-    for (int c = tid + 2 * kThreads; c < nchunks; c += kThreads) {
+    for (int c = tid + 2 * kGemvThreads; c < nchunks; c += kGemvThreads) {
         float t[16];
         load_f16(xf, c * 16, K, vec_ok, t);
 #pragma unroll
@@ -190,16 +212,18 @@ __device__ float stage_x(const GemvDesc& d, int8_t* lds_x, int* usum, float* red
     m = wave_max(m);
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    m = red[0];
+#pragma unroll
+    for (int i = 1; i < kGemvWaves; ++i) m = fmaxf(m, red[i]);
     const float amax = m + 1e-9f;
     const float scale = 127.0f / amax;
     const float act = 1.0f / scale;
-    for (int c = tid; c < nchunks; c += kThreads) {
+    for (int c = tid; c < nchunks; c += kGemvThreads) {
         u32x4 q;
         if (c == c0) {
-            q = pack_q16(v0, scale);
+            q = pack_q16(r.v0, scale);
         } else if (c == c1) {
-            q = pack_q16(v1, scale);
+            q = pack_q16(r.v1, scale);
         } else {
             float t[16];
             load_f16(xf, c * 16, K, vec_ok, t);
@@ -374,7 +398,7 @@ __device__ void run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usu
 // the single descriptor is a kernel argument.  Two instantiations keep the
 // descriptor in scalar registers either way.
 template <bool kList>
-__global__ __launch_bounds__(kThreads) void gemv_t16_kernel(GemvDesc single,
+__global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
                                                             const GemvDesc* __restrict__ list,
                                                             int n_list, long long total, int n_wg) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -400,18 +424,20 @@ __global__ __launch_bounds__(kThreads) void gemv_t16_kernel(GemvDesc single,
         const GemvDesc d = kList ? list[di] : single;
         const long long seg_end = min(t_end, d.tile0 + (long long)d.n_strips * d.Ku);
         const long long nseg = seg_end - t;
-        const int la = (int)(t + nseg * wave / kWaves - d.tile0);
-        const int lb = (int)(t + nseg * (wave + 1) / kWaves - d.tile0);
+        const int la = (int)(t + nseg * wave / kGemvWaves - d.tile0);
+        const int lb = (int)(t + nseg * (wave + 1) / kGemvWaves - d.tile0);
         const int n = lb - la;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(d.w + (long long)la * kTileBytes), 0, n * kTileBytes, 0x00020000);
+        XPre xpre;
+        x_prefetch(d, xpre);          // activations first (see XPre)
         u32x4 wa[kBatch];
         load_batch(wa, rs, voff, 0);  // in flight while the activations are staged
         int8_t* lds_x = reinterpret_cast<int8_t*>(lds_raw);
         int* usum = reinterpret_cast<int*>(lds_raw + d.Ku * kUnitK);
         float* red = reinterpret_cast<float*>(lds_raw + d.Ku * kUnitK + d.Ku * 4);
         __syncthreads();  // the previous segment is done with LDS
-        const float act = stage_x(d, lds_x, usum, red, t == d.tile0);
+        const float act = stage_x(d, xpre, lds_x, usum, red, t == d.tile0);
         __syncthreads();
         const float s = act * d.w_scale;  // x_scale * w_scale (forward.cpp:342)
         if (n > 0) run_piece(d, lds_x, usum, s, la, n, rs, voff, wa);
@@ -424,7 +450,7 @@ __global__ __launch_bounds__(kThreads) void gemv_t16_kernel(GemvDesc single,
 
 int gemv_max_wg_per_cu(int lds_bytes) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel<true>, kThreads, lds_bytes) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel<true>, kGemvThreads, lds_bytes) != hipSuccess)
         return 0;
     return n;
 }
@@ -432,10 +458,10 @@ int gemv_max_wg_per_cu(int lds_bytes) {
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, int n_list,
                        long long total_tiles, int n_wg, int lds_bytes, hipStream_t st) {
     if (list_dev)
-        hipLaunchKernelGGL(gemv_t16_kernel<true>, dim3(n_wg), dim3(kThreads), lds_bytes, st, single, list_dev,
+        hipLaunchKernelGGL(gemv_t16_kernel<true>, dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, single, list_dev,
                            n_list, total_tiles, n_wg);
     else
-        hipLaunchKernelGGL(gemv_t16_kernel<false>, dim3(n_wg), dim3(kThreads), lds_bytes, st, single, list_dev,
+        hipLaunchKernelGGL(gemv_t16_kernel<false>, dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, single, list_dev,
                            n_list, total_tiles, n_wg);
     return hipGetLastError();
 }
