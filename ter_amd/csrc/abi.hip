@@ -191,7 +191,8 @@ int device_cu_count(int device) {
 using namespace terhip;
 
 struct ter_hip_plan {
-    void* descs_dev = nullptr;   // GemvDesc[n] (GEMV plan) or GemmDesc[n] (GEMM plan)
+    void* descs_dev = nullptr;   // GemvDesc[n] (GEMV plan) or GemmDesc[n] (GEMM plan), then first_dev
+    const int32_t* first_dev = nullptr;  // [n_wg] first descriptor of each workgroup's range
     int n = 0;
     bool gemm = false;
     long long total = 0;         // tiles (GEMV) or blocks (GEMM) of one launch
@@ -212,6 +213,39 @@ struct ter_hip_handle {
     } slots[32];
     ter_hip_op_counts_t counts;
 };
+
+// Device copy of a plan: the descriptors, followed by the index of each
+// workgroup's first descriptor (the kernels cut `total` units into n_wg
+// ranges, range g starting at total * g / n_wg; starts[i] is descriptor i's
+// first unit, strictly increasing).
+template <typename Desc>
+int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<long long>& starts, long long total,
+                int n_wg) {
+    std::vector<int32_t> first((size_t)n_wg);
+    size_t di = 0;
+    for (int g = 0; g < n_wg; ++g) {
+        const long long t = total * g / n_wg;
+        while (di + 1 < starts.size() && starts[di + 1] <= t) ++di;
+        first[(size_t)g] = (int32_t)di;
+    }
+    const size_t db = sizeof(Desc) * ds.size();
+    hipError_t e = hipMalloc(&p->descs_dev, db + sizeof(int32_t) * (size_t)n_wg);
+    if (e != hipSuccess) {
+        p->descs_dev = nullptr;
+        return hip_fail(e, "plan descriptor allocation");
+    }
+    e = hipMemcpy(p->descs_dev, ds.data(), db, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(static_cast<char*>(p->descs_dev) + db, first.data(), sizeof(int32_t) * (size_t)n_wg,
+                      hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(p->descs_dev);
+        p->descs_dev = nullptr;
+        return hip_fail(e, "plan descriptor upload");
+    }
+    p->first_dev = reinterpret_cast<const int32_t*>(static_cast<const char*>(p->descs_dev) + db);
+    return TER_HIP_OK;
+}
 
 extern "C" {
 
@@ -328,7 +362,7 @@ int ter_hip_gemv(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int32
     const int lds = gemv_lds_bytes(w->K);
     rc = pick_wg(total, 0, lds, &n_wg);
     if (rc) return rc;
-    hipError_t e = launch_gemv(d, nullptr, 0, total, n_wg, lds, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_gemv(d, nullptr, nullptr, total, n_wg, lds, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return TER_HIP_OK;
 }
@@ -376,6 +410,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     *plan = nullptr;
     if (n < 1) return fail(TER_HIP_ERR_SHAPE, "empty work list");
     std::vector<GemvDesc> ds((size_t)n);
+    std::vector<long long> starts((size_t)n);
     long long tile = 0;
     uint64_t bytes = 0, macs = 0;
     int lds = 0;
@@ -390,6 +425,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
             if (items[k].w->fix == it.w->fix)
                 return fail(TER_HIP_ERR_CONFLICT, "weight of item %d repeats item %d", i, k);
         ds[(size_t)i] = make_desc(it.w, &it.x, it.y, it.acc, tile);
+        starts[(size_t)i] = tile;
         tile += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
         const int lb = gemv_lds_bytes(it.w->K);
         if (lb > lds) lds = lb;
@@ -402,16 +438,10 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     if (rc) return rc;
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
-    hipError_t e = hipMalloc(&p->descs_dev, sizeof(GemvDesc) * (size_t)n);
-    if (e != hipSuccess) {
+    rc = upload_plan(p, ds, starts, tile, n_wg);
+    if (rc) {
         delete p;
-        return hip_fail(e, "plan descriptor allocation");
-    }
-    e = hipMemcpy(p->descs_dev, ds.data(), sizeof(GemvDesc) * (size_t)n, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-        (void)hipFree(p->descs_dev);
-        delete p;
-        return hip_fail(e, "plan descriptor upload");
+        return rc;
     }
     p->n = n;
     p->total = tile;
@@ -428,16 +458,16 @@ int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
     hipError_t e;
     if (plan->gemm && plan->stream) {
         GemmDesc none{};
-        e = launch_gemm_stream(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->n, plan->total,
+        e = launch_gemm_stream(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->first_dev, plan->total,
                                plan->n_wg, plan->lds_bytes, plan->vec, static_cast<hipStream_t>(stream));
     } else if (plan->gemm) {
         GemmDesc none{};
-        e = launch_gemm_list(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->n, plan->total, plan->n_wg,
-                             plan->mb, plan->vec, static_cast<hipStream_t>(stream));
+        e = launch_gemm_list(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->first_dev, plan->total,
+                             plan->n_wg, plan->mb, plan->vec, static_cast<hipStream_t>(stream));
     } else {
         GemvDesc none{};
-        e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->n, plan->total, plan->n_wg,
-                        plan->lds_bytes, static_cast<hipStream_t>(stream));
+        e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev, plan->total,
+                        plan->n_wg, plan->lds_bytes, static_cast<hipStream_t>(stream));
     }
     if (e != hipSuccess) return hip_fail(e, "plan launch");
     return TER_HIP_OK;
@@ -493,11 +523,11 @@ int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, floa
         const long long tiles = (long long)d.n_strips * d.Ku;
         rc = pick_stream_wg(tiles, slds, 0, &n_wg);
         if (rc) return rc;
-        e = launch_gemm_stream(d, nullptr, 0, tiles, n_wg, slds, gemm_vec_ok(d), st);
+        e = launch_gemm_stream(d, nullptr, nullptr, tiles, n_wg, slds, gemm_vec_ok(d), st);
     } else {
         rc = pick_gemm_wg(d.n_blocks, mb, 0, &n_wg);
         if (rc) return rc;
-        e = launch_gemm_list(d, nullptr, 0, d.n_blocks, n_wg, mb, gemm_vec_ok(d), st);
+        e = launch_gemm_list(d, nullptr, nullptr, d.n_blocks, n_wg, mb, gemm_vec_ok(d), st);
     }
     if (e != hipSuccess) return hip_fail(e, "gemm launch");
     return TER_HIP_OK;
@@ -527,9 +557,12 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     const int per_block = kWaves * gemm_strips_per_wave(mb);
     long long tiles = 0;
     int max_k = 1;
+    std::vector<long long> block_starts((size_t)n), tile_starts((size_t)n);
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemm_item_t& it = items[i];
         ds[(size_t)i] = make_gemm_desc(it.w, it.x, it.x_scale_dev, it.M, it.y, it.acc, blocks, per_block, tiles);
+        block_starts[(size_t)i] = blocks;
+        tile_starts[(size_t)i] = tiles;
         blocks += ds[(size_t)i].n_blocks;
         tiles += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
         if (it.w->K > max_k) max_k = it.w->K;
@@ -544,16 +577,10 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     if (rc) return rc;
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
-    hipError_t e = hipMalloc(&p->descs_dev, sizeof(GemmDesc) * (size_t)n);
-    if (e != hipSuccess) {
+    rc = stream ? upload_plan(p, ds, tile_starts, tiles, n_wg) : upload_plan(p, ds, block_starts, blocks, n_wg);
+    if (rc) {
         delete p;
-        return hip_fail(e, "plan descriptor allocation");
-    }
-    e = hipMemcpy(p->descs_dev, ds.data(), sizeof(GemmDesc) * (size_t)n, hipMemcpyHostToDevice);
-    if (e != hipSuccess) {
-        (void)hipFree(p->descs_dev);
-        delete p;
-        return hip_fail(e, "plan descriptor upload");
+        return rc;
     }
     p->n = n;
     p->gemm = true;

@@ -71,8 +71,11 @@ struct alignas(16) GemmDesc {
     float w_scale;
 };
 
-// Host launchers (defined in the .hip files).
-hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, int n_list,
+// Host launchers (defined in the .hip files).  Work-list launches take the
+// device descriptor table `list_dev` and `first_dev`, the index of each
+// workgroup's first descriptor (range g starts at total * g / n_wg); single
+// launches pass nullptr for both.
+hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const int32_t* first_dev,
                        long long total_tiles, int n_wg, int lds_bytes, hipStream_t st);
 hipError_t launch_pack_v11(const uint8_t* v11, uint8_t* t16, int K, int N, hipStream_t st);
 hipError_t launch_unpack_v11(const uint8_t* t16, uint8_t* v11, int K, int N, hipStream_t st);
@@ -83,14 +86,14 @@ hipError_t launch_quant_rows(const float* x, int M, int K, int8_t* q, float* s, 
 // Rows per MFMA row block group: MB = 1, 2, 4, 8, 16 for M up to 16, 32, 64, 128, 256.
 int gemm_mb_of(int M);
 // vec: every x pointer 16-byte aligned and every ldx a multiple of 16.
-hipError_t launch_gemm_list(const GemmDesc& single, const GemmDesc* list_dev, int n_list, long long total_blocks,
-                            int n_wg, int mb, bool vec, hipStream_t st);
+hipError_t launch_gemm_list(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
+                            long long total_blocks, int n_wg, int mb, bool vec, hipStream_t st);
 // Streaming GEMM for M <= 16 (whole X of a GEMM staged in LDS, whole strips
 // per wave, no per-unit barrier).  lds_bytes = streaming_lds_bytes(max M, max K).
 inline int gemm_stream_lds_bytes(int M, int K) { return M * (units_of(K) * kUnitK + 16) + 16 * 4; }
 constexpr int kGemmStreamLdsMax = 64 * 1024;
-hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, int n_list, long long total_tiles,
-                              int n_wg, int lds_bytes, bool vec, hipStream_t st);
+hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
+                              long long total_tiles, int n_wg, int lds_bytes, bool vec, hipStream_t st);
 int gemm_stream_max_wg_per_cu(int lds_bytes);
 
 // Resident GEMM workgroups per CU for row-block count mb (0 if the query fails).

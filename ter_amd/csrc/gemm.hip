@@ -145,7 +145,8 @@ __device__ __forceinline__ void run_unit(const UnitRegs<MB, S>& r, int8_t (*xl)[
 
 template <int MB, int S, bool kList, bool kVec>
 __global__ __launch_bounds__(kThreads) void gemm_t16_kernel(GemmDesc single, const GemmDesc* __restrict__ list,
-                                                            int n_list, long long total_blocks, int n_wg) {
+                                                            const int32_t* __restrict__ first, long long total_blocks,
+                                                            int n_wg) {
 #pragma clang fp contract(off)
     constexpr int ROWS = MB * 16;
     __shared__ __align__(16) int8_t xl[2][ROWS * kLdRow];
@@ -155,15 +156,7 @@ __global__ __launch_bounds__(kThreads) void gemm_t16_kernel(GemmDesc single, con
     const long long b_begin = total_blocks * gi / n_wg;
     const long long b_end = total_blocks * (gi + 1) / n_wg;
     if (b_begin >= b_end) return;
-    int di = 0;
-    if (kList) {
-        int lo = 0, hi = n_list - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (list[mid].block0 <= b_begin) lo = mid; else hi = mid - 1;
-        }
-        di = lo;
-    }
+    int di = kList ? first[gi] : 0;  // the descriptor holding this range's start
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = uniform(tid >> 6);
@@ -341,22 +334,15 @@ __device__ __forceinline__ void stream_compute(const GemmDesc& d, const unsigned
 
 template <bool kList, bool kVec>
 __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GemmDesc single, const GemmDesc* __restrict__ list,
-                                                               int n_list, long long total, int n_wg) {
+                                                               const int32_t* __restrict__ first, long long total,
+                                                               int n_wg) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     int gi = blockIdx.x;
     if ((n_wg & 7) == 0) gi = (gi & 7) * (n_wg >> 3) + (gi >> 3);
     const long long t_begin = total * gi / n_wg;
     const long long t_end = total * (gi + 1) / n_wg;
     if (t_begin >= t_end) return;
-    int di = 0;
-    if (kList) {
-        int lo = 0, hi = n_list - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (list[mid].tile0 <= t_begin) lo = mid; else hi = mid - 1;
-        }
-        di = lo;
-    }
+    int di = kList ? first[gi] : 0;  // the descriptor holding this range's start
     const int lane = threadIdx.x & 63;
     const int wave = uniform(threadIdx.x >> 6);
     const int g = lane >> 4, j = lane & 15;
@@ -409,30 +395,30 @@ __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GemmDesc single, 
 }
 
 template <bool kList, bool kVec>
-hipError_t launch_stream_t(const GemmDesc& single, const GemmDesc* list, int n_list, long long total, int n_wg,
+hipError_t launch_stream_t(const GemmDesc& single, const GemmDesc* list, const int32_t* first, long long total, int n_wg,
                            int lds, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_stream_kernel<kList, kVec>), dim3(n_wg), dim3(kThreads), lds, st, single, list, n_list,
+    hipLaunchKernelGGL((gemm_stream_kernel<kList, kVec>), dim3(n_wg), dim3(kThreads), lds, st, single, list, first,
                        total, n_wg);
     return hipGetLastError();
 }
 
 template <int MB, int S>
-hipError_t launch_mbs(const GemmDesc& single, const GemmDesc* list, int n_list, long long total_blocks, int n_wg,
+hipError_t launch_mbs(const GemmDesc& single, const GemmDesc* list, const int32_t* first, long long total_blocks, int n_wg,
                       bool vec, hipStream_t st) {
     if (list) {
         if (vec)
             hipLaunchKernelGGL((gemm_t16_kernel<MB, S, true, true>), dim3(n_wg), dim3(kThreads), 0, st, single, list,
-                               n_list, total_blocks, n_wg);
+                               first, total_blocks, n_wg);
         else
             hipLaunchKernelGGL((gemm_t16_kernel<MB, S, true, false>), dim3(n_wg), dim3(kThreads), 0, st, single, list,
-                               n_list, total_blocks, n_wg);
+                               first, total_blocks, n_wg);
     } else {
         if (vec)
             hipLaunchKernelGGL((gemm_t16_kernel<MB, S, false, true>), dim3(n_wg), dim3(kThreads), 0, st, single,
-                               list, n_list, total_blocks, n_wg);
+                               list, first, total_blocks, n_wg);
         else
             hipLaunchKernelGGL((gemm_t16_kernel<MB, S, false, false>), dim3(n_wg), dim3(kThreads), 0, st, single,
-                               list, n_list, total_blocks, n_wg);
+                               list, first, total_blocks, n_wg);
     }
     return hipGetLastError();
 }
@@ -473,13 +459,13 @@ int gemm_stream_max_wg_per_cu(int lds_bytes) {
     return n;
 }
 
-hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, int n_list, long long total_tiles,
-                              int n_wg, int lds_bytes, bool vec, hipStream_t st) {
+hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
+                              long long total_tiles, int n_wg, int lds_bytes, bool vec, hipStream_t st) {
     if (list_dev)
-        return vec ? launch_stream_t<true, true>(single, list_dev, n_list, total_tiles, n_wg, lds_bytes, st)
-                   : launch_stream_t<true, false>(single, list_dev, n_list, total_tiles, n_wg, lds_bytes, st);
-    return vec ? launch_stream_t<false, true>(single, list_dev, n_list, total_tiles, n_wg, lds_bytes, st)
-               : launch_stream_t<false, false>(single, list_dev, n_list, total_tiles, n_wg, lds_bytes, st);
+        return vec ? launch_stream_t<true, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st)
+                   : launch_stream_t<true, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st);
+    return vec ? launch_stream_t<false, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st)
+               : launch_stream_t<false, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st);
 }
 
 int gemm_mb_of(int M) {
@@ -490,14 +476,14 @@ int gemm_mb_of(int M) {
     return 16;
 }
 
-hipError_t launch_gemm_list(const GemmDesc& single, const GemmDesc* list_dev, int n_list, long long total_blocks,
-                            int n_wg, int mb, bool vec, hipStream_t st) {
+hipError_t launch_gemm_list(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
+                            long long total_blocks, int n_wg, int mb, bool vec, hipStream_t st) {
     switch (mb) {
-        case 1: return launch_mbs<1, strips_for(1)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
-        case 2: return launch_mbs<2, strips_for(2)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
-        case 4: return launch_mbs<4, strips_for(4)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
-        case 8: return launch_mbs<8, strips_for(8)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
-        default: return launch_mbs<16, strips_for(16)>(single, list_dev, n_list, total_blocks, n_wg, vec, st);
+        case 1: return launch_mbs<1, strips_for(1)>(single, list_dev, first_dev, total_blocks, n_wg, vec, st);
+        case 2: return launch_mbs<2, strips_for(2)>(single, list_dev, first_dev, total_blocks, n_wg, vec, st);
+        case 4: return launch_mbs<4, strips_for(4)>(single, list_dev, first_dev, total_blocks, n_wg, vec, st);
+        case 8: return launch_mbs<8, strips_for(8)>(single, list_dev, first_dev, total_blocks, n_wg, vec, st);
+        default: return launch_mbs<16, strips_for(16)>(single, list_dev, first_dev, total_blocks, n_wg, vec, st);
     }
 }
 

@@ -354,10 +354,34 @@ __device__ __forceinline__ void compute_batch(const GemvDesc& d, const u32x4 (&w
     }
 }
 
+// The fix-up atomics of a piece's shared strips, issued but not yet checked:
+// whether an add completed its column is examined only after the wave's next
+// piece (or at its exit), so the atomics' round trip overlaps streaming.
+struct Fixups {
+    unsigned long long o_last, w_last, o_first, w_first;  // returned old values, added words
+    int col_last, col_first;                              // -1: no add by this lane
+    float s;
+    float* y;
+    int32_t* acc;
+    unsigned long long* fix;
+    int Ku;
+};
+
+__device__ __forceinline__ void finish_fixups(const Fixups& f) {
+#pragma clang fp contract(off)
+    GemvDesc d{};
+    d.y = f.y;
+    d.acc = f.acc;
+    d.fix = f.fix;
+    d.Ku = f.Ku;
+    if (f.col_last >= 0) part_complete(d, f.col_last, f.o_last + f.w_last, f.s);
+    if (f.col_first >= 0) part_complete(d, f.col_first, f.o_first + f.w_first, f.s);
+}
+
 // One wave streams local tiles [la, la + n) of GEMV d; `wa` holds the first
-// batch already.
-__device__ void run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usum, float s, int la, int n,
-                          __amdgpu_buffer_rsrc_t rs, int voff, u32x4 (&wa)[kBatch]) {
+// batch already.  Returns the piece's fix-up adds, to be finished later.
+__device__ Fixups run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usum, float s, int la, int n,
+                            __amdgpu_buffer_rsrc_t rs, int voff, u32x4 (&wa)[kBatch]) {
     Piece p;
     p.st = la / d.Ku;
     p.u = la - p.st * d.Ku;
@@ -379,19 +403,30 @@ __device__ void run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usu
         i0 += kBatch;
         if (i0 >= n) break;
     }
-    // Strips shared with neighbouring pieces: add both partials, then check.
-    const bool has_last = p.u != p.u_start;
-    unsigned long long w_last = 0, o_last = 0, w_first = 0, o_first = 0;
-    if (has_last) {
-        w_last = part_word(p.u - p.u_start, reduce_strip(p.a1, p.a4, p.corr));
-        if (col_owner(d, p.st)) o_last = part_add(d, strip_col(p.st), w_last);
+    // Strips shared with neighbouring pieces: add both partials.
+    Fixups f;
+    f.o_last = f.w_last = f.o_first = f.w_first = 0;
+    f.col_last = f.col_first = -1;
+    f.s = s;
+    f.y = d.y;
+    f.acc = d.acc;
+    f.fix = d.fix;
+    f.Ku = d.Ku;
+    if (p.u != p.u_start) {
+        f.w_last = part_word(p.u - p.u_start, reduce_strip(p.a1, p.a4, p.corr));
+        if (col_owner(d, p.st)) {
+            f.col_last = strip_col(p.st);
+            f.o_last = part_add(d, f.col_last, f.w_last);
+        }
     }
     if (p.has_first) {
-        w_first = part_word(p.first_units, p.first_val);
-        if (col_owner(d, p.first_st)) o_first = part_add(d, strip_col(p.first_st), w_first);
+        f.w_first = part_word(p.first_units, p.first_val);
+        if (col_owner(d, p.first_st)) {
+            f.col_first = strip_col(p.first_st);
+            f.o_first = part_add(d, f.col_first, f.w_first);
+        }
     }
-    if (has_last && col_owner(d, p.st)) part_complete(d, strip_col(p.st), o_last + w_last, s);
-    if (p.has_first && col_owner(d, p.first_st)) part_complete(d, strip_col(p.first_st), o_first + w_first, s);
+    return f;
 }
 
 // kList: GEMVs come from the device table `list` (plan launches); otherwise
@@ -400,7 +435,8 @@ __device__ void run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usu
 template <bool kList>
 __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
                                                             const GemvDesc* __restrict__ list,
-                                                            int n_list, long long total, int n_wg) {
+                                                            const int32_t* __restrict__ first,
+                                                            long long total, int n_wg) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     int g = blockIdx.x;
     if ((n_wg & 7) == 0) g = (g & 7) * (n_wg >> 3) + (g >> 3);  // keep neighbouring ranges on one XCD
@@ -408,18 +444,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
     const long long t_end = total * (g + 1) / n_wg;
     if (t_begin >= t_end) return;
 
-    int di = 0;
-    if (kList) {
-        int lo = 0, hi = n_list - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (list[mid].tile0 <= t_begin) lo = mid; else hi = mid - 1;
-        }
-        di = lo;
-    }
+    int di = kList ? first[g] : 0;  // the descriptor holding tile t_begin
     const int wave = uniform(threadIdx.x >> 6);
     const int voff = (threadIdx.x & 63) * 16;
     long long t = t_begin;
+    Fixups prev;
+    bool have_prev = false;
     while (t < t_end) {
         const GemvDesc d = kList ? list[di] : single;
         const long long seg_end = min(t_end, d.tile0 + (long long)d.n_strips * d.Ku);
@@ -440,10 +470,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
         const float act = stage_x(d, xpre, lds_x, usum, red, t == d.tile0);
         __syncthreads();
         const float s = act * d.w_scale;  // x_scale * w_scale (forward.cpp:342)
-        if (n > 0) run_piece(d, lds_x, usum, s, la, n, rs, voff, wa);
+        if (n > 0) {
+            const Fixups f = run_piece(d, lds_x, usum, s, la, n, rs, voff, wa);
+            if (have_prev) finish_fixups(prev);
+            prev = f;
+            have_prev = true;
+        }
         t = seg_end;
         ++di;
     }
+    if (have_prev) finish_fixups(prev);
 }
 
 }  // namespace
@@ -455,14 +491,14 @@ int gemv_max_wg_per_cu(int lds_bytes) {
     return n;
 }
 
-hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, int n_list,
+hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const int32_t* first_dev,
                        long long total_tiles, int n_wg, int lds_bytes, hipStream_t st) {
     if (list_dev)
         hipLaunchKernelGGL(gemv_t16_kernel<true>, dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, single, list_dev,
-                           n_list, total_tiles, n_wg);
+                           first_dev, total_tiles, n_wg);
     else
         hipLaunchKernelGGL(gemv_t16_kernel<false>, dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, single, list_dev,
-                           n_list, total_tiles, n_wg);
+                           first_dev, total_tiles, n_wg);
     return hipGetLastError();
 }
 
