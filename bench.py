@@ -148,6 +148,18 @@ def time_launches(launch_fns, steps: int, warmup: int):
     return wall, sum(evm) / len(evm), evm[len(evm) // 2]
 
 
+def settle(fn, seconds: float = 0.5):
+    """Untimed launches for `seconds` of wall time before a measurement, on
+    top of the warmup steps: the GPU's clocks take a few hundred ms of load to
+    settle, longer than a small warmup count lasts."""
+    import torch
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
 def graph_of(fn):
     """Capture fn's launches (on torch's current stream) into a HIP graph."""
     import torch
@@ -251,6 +263,7 @@ def run_m1(args, cfg, fp32_x: bool):
         for i in range(k % len(plans)):
             plans[i].launch()
 
+    settle(rot.replay)
     run_steps(args.warmup)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -382,6 +395,7 @@ def run_batched(args):
             T.quant_int8(X[k], q[k], s[k])
         plan.launch()
     g_step = graph_of(step)
+    settle(g_step.replay)
     wall, evm, _ = time_launches([g_step.replay], args.steps, args.warmup)
     mac = macs(cfg, M)
     # the dominant kernel alone: the GEMM work list (int8 X, fp32 Y)
@@ -406,7 +420,8 @@ def run_batched(args):
                      "peak": HBM_PEAK_GBS if hbm_bound else MFMA_I8_PEAK_TOPS,
                      "unit": "GB/s" if hbm_bound else "TOP/s",
                      "frac": round(gbs / HBM_PEAK_GBS if hbm_bound else tops / MFMA_I8_PEAK_TOPS, 4),
-                     "traffic": None, "kernel": kernel, "bytes_per_launch": plan.bytes,
+                     "traffic": read_traffic(kernel, f"bitnet_batched_m{M}"), "kernel": kernel,
+                     "bytes_per_launch": plan.bytes,
                      "mean_launch_us": round(ev_plan * 1e3, 3)},
         "cpu_baseline": None,
     }
@@ -433,8 +448,8 @@ def run_copy(args):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", choices=["llama", "bitnet", "batched", "copy"], default="llama")
     ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
     ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
