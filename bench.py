@@ -403,9 +403,15 @@ def run_batched(args):
     gbs = plan.bytes / (ev_plan * 1e-3) / 1e9
     tops = 2 * mac / (ev_plan * 1e-3) / 1e12
     hbm_bound = M <= 64
-    # the library streams M <= 16 when M rows of the widest X fit 64 KiB of LDS
+    # the kernel the library picks: M <= 16 streams when M rows of the widest X
+    # fit 64 KiB of LDS; 16 < M <= 128 takes the LDS-ring kernel
     ku = max(-(-K // 256) for _, K, _ in cfg["shapes"])
-    kernel = "gemm_stream_kernel" if M <= 16 and M * (ku * 256 + 16) + 64 <= 65536 else "gemm_t16_kernel"
+    if M <= 16 and M * (ku * 256 + 16) + 64 <= 65536:
+        kernel = "gemm_stream_kernel"
+    elif 16 < M <= 128:
+        kernel = "gemm_lds_kernel"  # 16-byte aligned X rows (K here is a multiple of 16)
+    else:
+        kernel = "gemm_t16_kernel"
     return {
         "metric": f"batched packed-trit GEMM, M={M}, BitNet-2B sweep",
         "value": round(mac / (wall * 1e-3) / 1e9, 1), "unit": "GMAC/s", "n_gpus": 1, "steps": args.steps,

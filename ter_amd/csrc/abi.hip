@@ -201,6 +201,10 @@ struct ter_hip_plan {
     int mb = 0;                  // GEMM row-block count
     bool vec = false;            // GEMM: 16-byte X rows
     bool stream = false;         // GEMM: streaming kernel (M <= 16), total counts tiles
+    bool lds = false;            // GEMM: LDS-ring kernel (16 < M <= 128)
+    const GemmBlock* blocks_dev = nullptr;  // LDS-ring: [n_blocks] blocks, then
+    const int32_t* ranges_dev = nullptr;    //   [n_wg + 1] block ranges per workgroup
+    int n_blocks = 0;
     uint64_t bytes = 0, macs = 0;
 };
 
@@ -244,6 +248,58 @@ int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<
         return hip_fail(e, "plan descriptor upload");
     }
     p->first_dev = reinterpret_cast<const int32_t*>(static_cast<const char*>(p->descs_dev) + db);
+    return TER_HIP_OK;
+}
+
+// LDS-ring GEMM (16 < M <= 128, 16-byte aligned X): resident workgroups per
+// CU times the CU count, capped by the block count.
+int pick_lds_wg(long long blocks, int mb, int* n_wg) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const int cus = device_cu_count(dev);
+    if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
+    const int fit = gemm_lds_max_wg_per_cu(mb);
+    if (fit <= 0) return fail(TER_HIP_ERR_HIP, "GEMM occupancy query failed");
+    long long g = (long long)cus * fit;
+    if (g > blocks) g = blocks;
+    if (g < 1) g = 1;
+    *n_wg = (int)g;
+    return TER_HIP_OK;
+}
+
+// Device copy of an LDS-ring GEMM plan: descriptors, the block list, and the
+// per-workgroup block ranges, balanced by 256-row units: range g holds the
+// blocks whose first unit lies in [total * g / n_wg, total * (g + 1) / n_wg).
+int upload_lds_plan(ter_hip_plan* p, const std::vector<GemmDesc>& ds, const std::vector<GemmBlock>& blocks,
+                    const std::vector<long long>& unit0, long long total_units, int n_wg) {
+    std::vector<int32_t> ranges((size_t)n_wg + 1);
+    size_t b = 0;
+    for (int g = 0; g <= n_wg; ++g) {
+        const long long t = total_units * g / n_wg;
+        while (b < blocks.size() && unit0[b] < t) ++b;
+        ranges[(size_t)g] = (int32_t)b;
+    }
+    ranges[(size_t)n_wg] = (int32_t)blocks.size();
+    const size_t db = sizeof(GemmDesc) * ds.size(), bb = sizeof(GemmBlock) * blocks.size();
+    hipError_t e = hipMalloc(&p->descs_dev, db + bb + sizeof(int32_t) * ranges.size());
+    if (e != hipSuccess) {
+        p->descs_dev = nullptr;
+        return hip_fail(e, "plan descriptor allocation");
+    }
+    char* base = static_cast<char*>(p->descs_dev);
+    e = hipMemcpy(base, ds.data(), db, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(base + db, blocks.data(), bb, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(base + db + bb, ranges.data(), sizeof(int32_t) * ranges.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(p->descs_dev);
+        p->descs_dev = nullptr;
+        return hip_fail(e, "plan descriptor upload");
+    }
+    p->blocks_dev = reinterpret_cast<const GemmBlock*>(base + db);
+    p->ranges_dev = reinterpret_cast<const int32_t*>(base + db + bb);
+    p->n_blocks = (int)blocks.size();
     return TER_HIP_OK;
 }
 
@@ -456,7 +512,11 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
 int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
     if (!plan) return fail(TER_HIP_ERR_NULL, "null plan");
     hipError_t e;
-    if (plan->gemm && plan->stream) {
+    if (plan->gemm && plan->lds) {
+        GemmDesc none{};
+        e = launch_gemm_lds(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->blocks_dev, plan->ranges_dev,
+                            plan->n_blocks, plan->n_wg, plan->mb, static_cast<hipStream_t>(stream));
+    } else if (plan->gemm && plan->stream) {
         GemmDesc none{};
         e = launch_gemm_stream(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->first_dev, plan->total,
                                plan->n_wg, plan->lds_bytes, plan->vec, static_cast<hipStream_t>(stream));
@@ -519,11 +579,17 @@ int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, floa
     int n_wg = 0;
     hipError_t e;
     const int slds = gemm_stream_lds_bytes(M, w->K);
+    const int lbs = M > 16 && gemm_vec_ok(d) ? gemm_lds_strips_per_block(mb) : 0;
     if (M <= 16 && slds <= kGemmStreamLdsMax) {
         const long long tiles = (long long)d.n_strips * d.Ku;
         rc = pick_stream_wg(tiles, slds, 0, &n_wg);
         if (rc) return rc;
         e = launch_gemm_stream(d, nullptr, nullptr, tiles, n_wg, slds, gemm_vec_ok(d), st);
+    } else if (lbs > 0) {
+        const int nb = (d.n_strips + lbs - 1) / lbs;
+        rc = pick_lds_wg(nb, mb, &n_wg);
+        if (rc) return rc;
+        e = launch_gemm_lds(d, nullptr, nullptr, nullptr, nb, n_wg, mb, st);
     } else {
         rc = pick_gemm_wg(d.n_blocks, mb, 0, &n_wg);
         if (rc) return rc;
@@ -573,15 +639,33 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     int n_wg = 0;
     const int slds = gemm_stream_lds_bytes(max_m, max_k);
     const bool stream = max_m <= 16 && slds <= kGemmStreamLdsMax;
-    int rc = stream ? pick_stream_wg(tiles, slds, wg_per_cu, &n_wg) : pick_gemm_wg(blocks, mb, wg_per_cu, &n_wg);
-    if (rc) return rc;
+    const int lbs = !stream && max_m > 16 && vec ? gemm_lds_strips_per_block(mb) : 0;
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
-    rc = stream ? upload_plan(p, ds, tile_starts, tiles, n_wg) : upload_plan(p, ds, block_starts, blocks, n_wg);
+    int rc;
+    if (lbs > 0) {
+        // LDS-ring kernel: blocks of lbs strips, balanced by units
+        std::vector<GemmBlock> bl;
+        std::vector<long long> unit0;
+        long long units = 0;
+        for (int i = 0; i < n; ++i) {
+            for (int st = 0; st < ds[(size_t)i].n_strips; st += lbs) {
+                bl.push_back(GemmBlock{i, st});
+                unit0.push_back(units);
+                units += ds[(size_t)i].Ku;
+            }
+        }
+        rc = pick_lds_wg((long long)bl.size(), mb, &n_wg);
+        if (!rc) rc = upload_lds_plan(p, ds, bl, unit0, units, n_wg);
+    } else {
+        rc = stream ? pick_stream_wg(tiles, slds, wg_per_cu, &n_wg) : pick_gemm_wg(blocks, mb, wg_per_cu, &n_wg);
+        if (!rc) rc = stream ? upload_plan(p, ds, tile_starts, tiles, n_wg) : upload_plan(p, ds, block_starts, blocks, n_wg);
+    }
     if (rc) {
         delete p;
         return rc;
     }
+    p->lds = lbs > 0;
     p->n = n;
     p->gemm = true;
     p->stream = stream;

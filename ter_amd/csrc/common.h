@@ -98,6 +98,20 @@ int gemm_stream_max_wg_per_cu(int lds_bytes);
 
 // Resident GEMM workgroups per CU for row-block count mb (0 if the query fails).
 int gemm_max_wg_per_cu(int mb);
+
+// LDS-ring GEMM for 16 < M <= 128 (mb = 2, 4, 8; gemm_lds.hip).  Work is a
+// list of blocks, each `gemm_lds_strips_per_block(mb)` strips of one GEMM;
+// workgroup g (after the XCD remap) owns blocks [ranges[g], ranges[g+1]).
+// Single launches pass null lists and split n_blocks of `single` evenly.
+// Needs vec (16-byte aligned X rows).
+struct GemmBlock {
+    int32_t desc;    // index into the descriptor list
+    int32_t strip0;  // first strip of the block
+};
+int gemm_lds_strips_per_block(int mb);  // 0: no LDS-ring configuration for mb
+int gemm_lds_max_wg_per_cu(int mb);
+hipError_t launch_gemm_lds(const GemmDesc& single, const GemmDesc* list_dev, const GemmBlock* blocks_dev,
+                           const int32_t* ranges_dev, int n_blocks, int n_wg, int mb, hipStream_t st);
 // Column strips per wave of the GEMM for row-block count mb (a block is
 // kWaves * that many strips).
 int gemm_strips_per_wave(int mb);

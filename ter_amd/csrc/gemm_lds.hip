@@ -1,0 +1,367 @@
+// gemm_lds.hip -- batched packed-trit GEMM for 16 < M <= 128 on gfx950 MFMA,
+// fed through an LDS ring by direct global->LDS loads.
+//
+// Same semantics as gemm.hip (cuda/ter_cuda_addonly_batched.cu:117-123):
+// acc[m][j] = sum_k X[m][k] w[k][j] in exact int32, y = float(acc) * (xs[m] * w_scale).
+//
+// Work.  A block is BS consecutive column strips of one GEMM (all M rows,
+// all K).  The blocks of a launch are split over the workgroups in contiguous
+// ranges balanced by 256-row units (a block costs Ku units), consecutive
+// ranges on one XCD.  A workgroup (8 waves) walks its blocks unit by unit:
+// for unit u of block b it needs X[0:M, u] (M x 256 int8) and the BS weight
+// tiles (strip, u) of the block, 1 KiB each.
+//
+// Pipeline.  NST stages of LDS, each holding one unit's X rows and weight
+// tiles, are filled by buffer_load_dwordx4 ... lds (64 lanes x 16 bytes = one
+// 1 KiB LDS run per instruction; no registers involved) NST - 1 units ahead
+// of the MFMAs.  Per unit: wait for this wave's loads of the unit (explicit
+// vmcnt), barrier (every wave's loads landed, and every wave is done reading
+// the stage about to be refilled), issue the loads of unit + NST - 1, then
+// the MFMAs.  A wave's loads complete in issue order, so waiting until no
+// more operations are outstanding than the younger stages' loads guarantees
+// the stage has landed.  That holds with the epilogue's stores in flight too
+// (stores may complete out of order with respect to loads, but a wait that
+// leaves only the younger loads outstanding waits for them as well), so a
+// block's epilogue needs no drain.
+//
+// Operands.  X rows sit in LDS as 256-byte rows whose 16-byte chunks are
+// XOR-swizzled by the row's low 4 bits (chunk c of row r at position
+// c ^ (r & 15)), so the 16 rows an MFMA A operand reads hit distinct banks.
+// The wave grid is RS row groups x (8 / RS) strip groups; a wave holds
+// MBW x S accumulators (MBW row blocks of 16 x S strips).  Per 64-row slab a
+// wave reads MBW A operands (ds_read_b128) and S weight dwords (ds_read_b32,
+// lane = column j + 16 * k-group g, one dword = 16 trits of column j), expands
+// each 2-bit code u = w + 1 straight to the signed int8 w with one v_perm_b32
+// per 4 trits (a byte table {-1, 0, +1, 0} indexed by u), and issues
+// v_mfma_i32_16x16x64_i8.  Signed weights need no activation-sum correction.
+#include "common.h"
+
+namespace terhip {
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+#define TER_GLOBAL __attribute__((address_space(1)))
+#define TER_LDS __attribute__((address_space(3)))
+
+template <typename T>
+__device__ __forceinline__ TER_GLOBAL T* gptr(T* p) {
+    return (TER_GLOBAL T*)p;
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+constexpr int kLWaves = 8;
+constexpr int kLThreads = 64 * kLWaves;
+
+template <int MBW_, int S_, int RS_, int NST_>
+struct LCfg {
+    static constexpr int MBW = MBW_, S = S_, RS = RS_, NST = NST_;
+    static constexpr int MB = RS * MBW;               // row blocks of 16
+    static constexpr int SG = kLWaves / RS;           // strip groups
+    static constexpr int BS = SG * S;                 // strips per block
+    static constexpr int XB = MB * 16 * kUnitK;       // X bytes per stage
+    static constexpr int STB = XB + BS * kTileBytes;  // bytes per stage
+    static constexpr int XSO = NST * STB;             // row-scale slots: NST x 1 KiB
+    static constexpr int LDS = XSO + NST * 1024;
+    static constexpr int XI = XB / 1024;              // 1 KiB load runs of X per stage
+    static constexpr int NIW = (XI + BS) / kLWaves;   // load instructions per wave per stage
+    static_assert((XI + BS) % kLWaves == 0, "load runs must split evenly over the waves");
+    static_assert(NST >= 2 && NST <= 4, "stage count");
+};
+
+// The configuration per row-block count (M <= 32, 64, 128), measured on the
+// BitNet-2B sweep: every wave covers all rows (RS = 1) and 4 strips, so a
+// block is 32 strips and X is staged once per 32 weight tiles; three stages
+// where the LDS allows two workgroups per CU (M <= 32), two above.
+using Cfg2 = LCfg<2, 4, 1, 3>;
+using Cfg4 = LCfg<4, 4, 1, 2>;
+using Cfg8 = LCfg<8, 4, 1, 2>;
+
+// s_waitcnt immediate (gfx9 family): vmcnt(n), expcnt and lgkmcnt not waited on.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Barrier that orders memory for the compiler but adds no wait of its own
+// (the waits are explicit above it).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Wait until this wave's loads of the unit `behind` stages older than the
+// newest issued one have landed: `behind` = stages issued after it (0..NST-2).
+template <class C>
+__device__ __forceinline__ void wait_stage(int behind) {
+    if (C::NST >= 4 && behind >= 2) {
+        wait_vm<(C::NST >= 4 ? 2 : 0) * C::NIW>();
+    } else if (C::NST >= 3 && behind >= 1) {
+        wait_vm<C::NIW>();
+    } else {
+        wait_vm<0>();
+    }
+}
+
+// Issue this wave's share of the loads of unit u of the block starting at
+// strip st0 into `stage`.  xr covers X (M * ldx bytes: rows >= M read zeros);
+// wr covers the block's strips (strips past the matrix read zeros).
+template <class C>
+__device__ __forceinline__ void issue_stage(int ldx, int Ku, int u, unsigned char* stage,
+                                            __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr, int wave,
+                                            int lane) {
+#pragma unroll
+    for (int r = 0; r < C::NIW; ++r) {
+        const int q = wave + kLWaves * r;  // wave-uniform
+        if (q < C::XI) {
+            // rows 4q .. 4q+3: lane -> row 4q + lane / 16, stored chunk lane % 16
+            const int row = 4 * q + (lane >> 4);
+            const int chunk = (lane & 15) ^ (row & 15);
+            // (resource, LDS run, bytes per lane, vector offset, scalar offset, immediate offset, cache policy)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (TER_LDS void*)(stage + q * 1024), 16,
+                                                     row * ldx + u * kUnitK + chunk * 16, 0, 0, 0);
+        } else {
+            const int t = q - C::XI;  // tile (strip t of the block, unit u)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (TER_LDS void*)(stage + C::XB + t * 1024), 16,
+                                                     (t * Ku + u) * kTileBytes + lane * 16, 0, 0, 2 /* nt */);
+        }
+    }
+}
+
+// Signed int8 weights of 16 trits (one T16 dword) in MFMA B operand order:
+// byte b of word f is the trit of row 4 f + b; u = w + 1 -> w by table lookup.
+__device__ __forceinline__ i32x4 unpack_signed(unsigned dw) {
+    const unsigned kM = 0x03030303u, kT = 0x000100FFu;  // bytes: u=0 -> -1, 1 -> 0, 2 -> +1, 3 -> 0
+    return i32x4{(int)__builtin_amdgcn_perm(0u, kT, dw & kM), (int)__builtin_amdgcn_perm(0u, kT, (dw >> 2) & kM),
+                 (int)__builtin_amdgcn_perm(0u, kT, (dw >> 4) & kM), (int)__builtin_amdgcn_perm(0u, kT, (dw >> 6) & kM)};
+}
+
+template <class C>
+__device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg, int sg, int lane,
+                                              i32x4 (&acc)[C::S][C::MBW]) {
+    const int j = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+        i32x4 A[C::MBW];
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) {
+            const int row = (rg * C::MBW + mb) * 16 + j;  // row % 16 == j
+            A[mb] = *reinterpret_cast<const i32x4*>(stage + row * kUnitK + (((ks * 4 + g) ^ j) * 16));
+        }
+#pragma unroll
+        for (int s = 0; s < C::S; ++s) {
+            const unsigned dw = *reinterpret_cast<const unsigned*>(
+                stage + C::XB + (sg * C::S + s) * kTileBytes + (j >> 2) * 256 + g * 16 + (j & 3) * 4 + ks * 64);
+            const i32x4 B = unpack_signed(dw);
+#pragma unroll
+            for (int mb = 0; mb < C::MBW; ++mb)
+                acc[s][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mb], B, acc[s][mb], 0, 0, 0);
+        }
+    }
+}
+
+struct BlockRef {
+    GemmDesc d;
+    int st0;
+};
+
+template <bool kList>
+__device__ __forceinline__ BlockRef block_at(const GemmDesc& single, const GemmDesc* list,
+                                             const GemmBlock* blocks, int b, int bs) {
+    BlockRef r;
+    if (kList) {
+        const GemmBlock gb = blocks[b];
+        r.d = list[gb.desc];
+        r.st0 = gb.strip0;
+    } else {
+        r.d = single;
+        r.st0 = b * bs;
+    }
+    return r;
+}
+
+template <class C, bool kList>
+__global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, const GemmDesc* __restrict__ list,
+                                                             const GemmBlock* __restrict__ blocks,
+                                                             const int32_t* __restrict__ ranges, int n_blocks,
+                                                             int n_wg) {
+#pragma clang fp contract(off)
+    extern __shared__ __align__(1024) unsigned char lds[];
+    int gi = blockIdx.x;
+    if ((n_wg & 7) == 0) gi = (gi & 7) * (n_wg >> 3) + (gi >> 3);  // neighbouring ranges on one XCD
+    int b_lo, b_hi;
+    if (kList) {
+        b_lo = ranges[gi];
+        b_hi = ranges[gi + 1];
+    } else {
+        b_lo = (int)((long long)n_blocks * gi / n_wg);
+        b_hi = (int)((long long)n_blocks * (gi + 1) / n_wg);
+    }
+    if (b_lo >= b_hi) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = uniform(threadIdx.x >> 6);
+    const int rg = wave / C::SG, sg = wave % C::SG;
+    const int j = lane & 15, g = lane >> 4;
+
+    // issue side: the next unit to load
+    int ib = b_lo, iu = 0, n_issued = 0, i_stage = 0;
+    BlockRef bi = block_at<kList>(single, list, blocks, ib, C::BS);
+    auto rsrc_x = [](const GemmDesc& d) {
+        return __builtin_amdgcn_make_buffer_rsrc((void*)d.x, 0, d.M * d.ldx, 0x00020000);
+    };
+    auto rsrc_w = [](const BlockRef& r) {
+        const int ns = min(C::BS, r.d.n_strips - r.st0);
+        return __builtin_amdgcn_make_buffer_rsrc((void*)(r.d.w + (long long)r.st0 * r.d.Ku * kTileBytes), 0,
+                                                 ns * r.d.Ku * kTileBytes, 0x00020000);
+    };
+    __amdgpu_buffer_rsrc_t xr = rsrc_x(bi.d), wr = rsrc_w(bi);
+    // Block ib's row scales go to LDS slot ib % NST with its first unit (wave 0,
+    // one extra load: an extra operation only makes the stage waits stricter).
+    // The issue side runs at most NST - 1 units ahead, so a slot is refilled
+    // only after the block that used it has finished.
+    auto issue_next = [&]() {
+        if (iu == 0 && wave == 0) {
+            const __amdgpu_buffer_rsrc_t sr =
+                __builtin_amdgcn_make_buffer_rsrc((void*)bi.d.xs, 0, bi.d.M * 4, 0x00020000);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (TER_LDS void*)(lds + C::XSO + (ib % C::NST) * 1024), 16,
+                                                     lane * 16, 0, 0, 0);
+        }
+        issue_stage<C>(bi.d.ldx, bi.d.Ku, iu, lds + i_stage * C::STB, xr, wr, wave, lane);
+        ++n_issued;
+        i_stage = i_stage + 1 == C::NST ? 0 : i_stage + 1;
+        if (++iu == bi.d.Ku) {
+            iu = 0;
+            if (++ib < b_hi) {
+                bi = block_at<kList>(single, list, blocks, ib, C::BS);
+                xr = rsrc_x(bi.d);
+                wr = rsrc_w(bi);
+            }
+        }
+    };
+#pragma unroll
+    for (int p = 0; p < C::NST - 1; ++p)
+        if (ib < b_hi) issue_next();
+
+    // compute side
+    int cb = b_lo, cu = 0, it = 0, c_stage = 0;
+    BlockRef bc = block_at<kList>(single, list, blocks, cb, C::BS);
+    i32x4 acc[C::S][C::MBW];
+#pragma unroll
+    for (int s = 0; s < C::S; ++s)
+#pragma unroll
+        for (int mb = 0; mb < C::MBW; ++mb) acc[s][mb] = i32x4{0, 0, 0, 0};
+    while (true) {
+        wait_stage<C>(n_issued - it - 1);
+        lds_barrier();
+        if (ib < b_hi) issue_next();
+        compute_stage<C>(lds + c_stage * C::STB, rg, sg, lane, acc);
+        ++it;
+        c_stage = c_stage + 1 == C::NST ? 0 : c_stage + 1;
+        if (++cu == bc.d.Ku) {
+            // epilogue of block cb
+            const GemmDesc& d = bc.d;
+            const float* xs_l = reinterpret_cast<const float*>(lds + C::XSO + (cb % C::NST) * 1024);
+#pragma unroll
+            for (int mb = 0; mb < C::MBW; ++mb) {
+                const f32x4 xq = *reinterpret_cast<const f32x4*>(xs_l + (rg * C::MBW + mb) * 16 + g * 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int row = (rg * C::MBW + mb) * 16 + g * 4 + e;
+                    if (row < d.M) {
+                        const float sc = xq[e] * d.w_scale;
+#pragma unroll
+                        for (int s = 0; s < C::S; ++s) {
+                            const int col = (bc.st0 + sg * C::S + s) * kStripCols + j;
+                            if (col < d.N) {
+                                const long long o = (long long)row * d.N + col;
+                                const int val = acc[s][mb][e];
+                                if (d.acc) gptr(d.acc)[o] = val;
+                                if (d.y) gptr(d.y)[o] = (float)val * sc;
+                            }
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int s = 0; s < C::S; ++s)
+#pragma unroll
+                for (int mb = 0; mb < C::MBW; ++mb) acc[s][mb] = i32x4{0, 0, 0, 0};
+            if (++cb >= b_hi) break;
+            bc = block_at<kList>(single, list, blocks, cb, C::BS);
+            cu = 0;
+        }
+    }
+}
+
+// Allow the configuration's dynamic LDS (above the 64 KiB default) for both
+// instantiations; once per process (repeating it is harmless).
+template <class C>
+hipError_t allow_lds() {
+    static hipError_t done = [] {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_lds_kernel<C, true>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_lds_kernel<C, false>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS);
+        return e;
+    }();
+    return done;
+}
+
+template <class C>
+hipError_t launch_cfg(const GemmDesc& single, const GemmDesc* list, const GemmBlock* blocks, const int32_t* ranges,
+                      int n_blocks, int n_wg, hipStream_t st) {
+    const hipError_t e = allow_lds<C>();
+    if (e != hipSuccess) return e;
+    if (list)
+        hipLaunchKernelGGL((gemm_lds_kernel<C, true>), dim3(n_wg), dim3(kLThreads), C::LDS, st, single, list, blocks,
+                           ranges, n_blocks, n_wg);
+    else
+        hipLaunchKernelGGL((gemm_lds_kernel<C, false>), dim3(n_wg), dim3(kLThreads), C::LDS, st, single, list,
+                           blocks, ranges, n_blocks, n_wg);
+    return hipGetLastError();
+}
+
+template <class C>
+int occupancy_cfg() {
+    if (allow_lds<C>() != hipSuccess) return 0;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_lds_kernel<C, true>, kLThreads, C::LDS) != hipSuccess)
+        return 0;
+    return n;
+}
+
+}  // namespace
+
+int gemm_lds_strips_per_block(int mb) {
+    switch (mb) {
+        case 2: return Cfg2::BS;
+        case 4: return Cfg4::BS;
+        case 8: return Cfg8::BS;
+        default: return 0;
+    }
+}
+
+int gemm_lds_max_wg_per_cu(int mb) {
+    switch (mb) {
+        case 2: return occupancy_cfg<Cfg2>();
+        case 4: return occupancy_cfg<Cfg4>();
+        case 8: return occupancy_cfg<Cfg8>();
+        default: return 0;
+    }
+}
+
+hipError_t launch_gemm_lds(const GemmDesc& single, const GemmDesc* list_dev, const GemmBlock* blocks_dev,
+                           const int32_t* ranges_dev, int n_blocks, int n_wg, int mb, hipStream_t st) {
+    switch (mb) {
+        case 2: return launch_cfg<Cfg2>(single, list_dev, blocks_dev, ranges_dev, n_blocks, n_wg, st);
+        case 4: return launch_cfg<Cfg4>(single, list_dev, blocks_dev, ranges_dev, n_blocks, n_wg, st);
+        case 8: return launch_cfg<Cfg8>(single, list_dev, blocks_dev, ranges_dev, n_blocks, n_wg, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace terhip
