@@ -201,7 +201,7 @@ struct ter_hip_plan {
     int mb = 0;                  // GEMM row-block count
     bool vec = false;            // GEMM: 16-byte X rows
     bool stream = false;         // GEMM: streaming kernel (M <= 16), total counts tiles
-    bool lds = false;            // GEMM: LDS-ring kernel (16 < M <= 128)
+    bool lds = false;            // GEMM: LDS-ring kernel (M <= 128 where streaming does not apply)
     const GemmBlock* blocks_dev = nullptr;  // LDS-ring: [n_blocks] blocks, then
     const int32_t* ranges_dev = nullptr;    //   [n_wg + 1] block ranges per workgroup
     int n_blocks = 0;
@@ -251,7 +251,7 @@ int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<
     return TER_HIP_OK;
 }
 
-// LDS-ring GEMM (16 < M <= 128, 16-byte aligned X): resident workgroups per
+// LDS-ring GEMM (M <= 128, 16-byte aligned X): resident workgroups per
 // CU times the CU count, capped by the block count.
 int pick_lds_wg(long long blocks, int mb, int* n_wg) {
     int dev = 0;
@@ -579,7 +579,7 @@ int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, floa
     int n_wg = 0;
     hipError_t e;
     const int slds = gemm_stream_lds_bytes(M, w->K);
-    const int lbs = M > 16 && gemm_vec_ok(d) ? gemm_lds_strips_per_block(mb) : 0;
+    const int lbs = gemm_vec_ok(d) ? gemm_lds_strips_per_block(mb) : 0;
     if (M <= 16 && slds <= kGemmStreamLdsMax) {
         const long long tiles = (long long)d.n_strips * d.Ku;
         rc = pick_stream_wg(tiles, slds, 0, &n_wg);
@@ -639,7 +639,7 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     int n_wg = 0;
     const int slds = gemm_stream_lds_bytes(max_m, max_k);
     const bool stream = max_m <= 16 && slds <= kGemmStreamLdsMax;
-    const int lbs = !stream && max_m > 16 && vec ? gemm_lds_strips_per_block(mb) : 0;
+    const int lbs = !stream && vec ? gemm_lds_strips_per_block(mb) : 0;
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
     int rc;

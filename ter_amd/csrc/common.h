@@ -99,7 +99,8 @@ int gemm_stream_max_wg_per_cu(int lds_bytes);
 // Resident GEMM workgroups per CU for row-block count mb (0 if the query fails).
 int gemm_max_wg_per_cu(int mb);
 
-// LDS-ring GEMM for 16 < M <= 128 (mb = 2, 4, 8; gemm_lds.hip).  Work is a
+// LDS-ring GEMM for M <= 128 (mb = 1, 2, 4, 8; gemm_lds.hip), used where the
+// streaming kernel does not apply (M > 16, or M rows of X beyond its LDS).  Work is a
 // list of blocks, each `gemm_lds_strips_per_block(mb)` strips of one GEMM;
 // workgroup g (after the XCD remap) owns blocks [ranges[g], ranges[g+1]).
 // Single launches pass null lists and split n_blocks of `single` evenly.

@@ -1,4 +1,4 @@
-// gemm_lds.hip -- batched packed-trit GEMM for 16 < M <= 128 on gfx950 MFMA,
+// gemm_lds.hip -- batched packed-trit GEMM for M <= 128 on gfx950 MFMA,
 // fed through an LDS ring by direct global->LDS loads.
 //
 // Same semantics as gemm.hip (cuda/ter_cuda_addonly_batched.cu:117-123):
@@ -65,15 +65,17 @@ struct LCfg {
     static constexpr int XSO = NST * STB;             // row-scale slots: NST x 1 KiB
     static constexpr int LDS = XSO + NST * 1024;
     static constexpr int XI = XB / 1024;              // 1 KiB load runs of X per stage
-    static constexpr int NIW = (XI + BS) / kLWaves;   // load instructions per wave per stage
-    static_assert((XI + BS) % kLWaves == 0, "load runs must split evenly over the waves");
+    static constexpr int NI = XI + BS;                // load runs per stage, run q issued by wave q % 8
+    static constexpr int NIW = NI / kLWaves;          // runs of waves >= NR ...
+    static constexpr int NR = NI % kLWaves;           // ... and waves < NR issue one more
     static_assert(NST >= 2 && NST <= 4, "stage count");
 };
 
-// The configuration per row-block count (M <= 32, 64, 128), measured on the
+// The configuration per row-block count (M <= 16, 32, 64, 128), measured on the
 // BitNet-2B sweep: every wave covers all rows (RS = 1) and 4 strips, so a
 // block is 32 strips and X is staged once per 32 weight tiles; three stages
 // where the LDS allows two workgroups per CU (M <= 32), two above.
+using Cfg1 = LCfg<1, 4, 1, 3>;
 using Cfg2 = LCfg<2, 4, 1, 3>;
 using Cfg4 = LCfg<4, 4, 1, 2>;
 using Cfg8 = LCfg<8, 4, 1, 2>;
@@ -94,16 +96,25 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Wait until this wave's loads of the unit `behind` stages older than the
-// newest issued one have landed: `behind` = stages issued after it (0..NST-2).
-template <class C>
-__device__ __forceinline__ void wait_stage(int behind) {
+// newest issued one have landed: `behind` = stages issued after it (0..NST-2),
+// each holding N of this wave's loads.
+template <class C, int N>
+__device__ __forceinline__ void wait_stage_n(int behind) {
     if (C::NST >= 4 && behind >= 2) {
-        wait_vm<(C::NST >= 4 ? 2 : 0) * C::NIW>();
+        wait_vm<(C::NST >= 4 ? 2 : 0) * N>();
     } else if (C::NST >= 3 && behind >= 1) {
-        wait_vm<C::NIW>();
+        wait_vm<N>();
     } else {
         wait_vm<0>();
     }
+}
+
+template <class C>
+__device__ __forceinline__ void wait_stage(int behind, int wave) {
+    if (C::NR != 0 && wave < C::NR)
+        wait_stage_n<C, C::NIW + 1>(behind);
+    else
+        wait_stage_n<C, C::NIW>(behind);
 }
 
 // Issue this wave's share of the loads of unit u of the block starting at
@@ -114,8 +125,9 @@ __device__ __forceinline__ void issue_stage(int ldx, int Ku, int u, unsigned cha
                                             __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr, int wave,
                                             int lane) {
 #pragma unroll
-    for (int r = 0; r < C::NIW; ++r) {
+    for (int r = 0; r < C::NIW + (C::NR != 0); ++r) {
         const int q = wave + kLWaves * r;  // wave-uniform
+        if (C::NR != 0 && q >= C::NI) break;
         if (q < C::XI) {
             // rows 4q .. 4q+3: lane -> row 4q + lane / 16, stored chunk lane % 16
             const int row = 4 * q + (lane >> 4);
@@ -254,7 +266,7 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
 #pragma unroll
         for (int mb = 0; mb < C::MBW; ++mb) acc[s][mb] = i32x4{0, 0, 0, 0};
     while (true) {
-        wait_stage<C>(n_issued - it - 1);
+        wait_stage<C>(n_issued - it - 1, wave);
         lds_barrier();
         if (ib < b_hi) issue_next();
         compute_stage<C>(lds + c_stage * C::STB, rg, sg, lane, acc);
@@ -338,6 +350,7 @@ int occupancy_cfg() {
 
 int gemm_lds_strips_per_block(int mb) {
     switch (mb) {
+        case 1: return Cfg1::BS;
         case 2: return Cfg2::BS;
         case 4: return Cfg4::BS;
         case 8: return Cfg8::BS;
@@ -347,6 +360,7 @@ int gemm_lds_strips_per_block(int mb) {
 
 int gemm_lds_max_wg_per_cu(int mb) {
     switch (mb) {
+        case 1: return occupancy_cfg<Cfg1>();
         case 2: return occupancy_cfg<Cfg2>();
         case 4: return occupancy_cfg<Cfg4>();
         case 8: return occupancy_cfg<Cfg8>();
@@ -357,6 +371,7 @@ int gemm_lds_max_wg_per_cu(int mb) {
 hipError_t launch_gemm_lds(const GemmDesc& single, const GemmDesc* list_dev, const GemmBlock* blocks_dev,
                            const int32_t* ranges_dev, int n_blocks, int n_wg, int mb, hipStream_t st) {
     switch (mb) {
+        case 1: return launch_cfg<Cfg1>(single, list_dev, blocks_dev, ranges_dev, n_blocks, n_wg, st);
         case 2: return launch_cfg<Cfg2>(single, list_dev, blocks_dev, ranges_dev, n_blocks, n_wg, st);
         case 4: return launch_cfg<Cfg4>(single, list_dev, blocks_dev, ranges_dev, n_blocks, n_wg, st);
         case 8: return launch_cfg<Cfg8>(single, list_dev, blocks_dev, ranges_dev, n_blocks, n_wg, st);
