@@ -54,6 +54,11 @@ extern "C" {
 /* ---- activation kinds ---- */
 #define TER_HIP_X_I8   0  /* int8 X[K] with a host or device activation scale       */
 #define TER_HIP_X_F32  1  /* fp32 X[K]: absmax -> int8 inside the kernel prologue    */
+/* RMSNorm (fp16 gamma, eps) then absmax -> int8 inside the kernel prologue:
+ * the fused rmsnorm_quant_f32_in_k / rmsnorm_quant_fp16_in_k steps
+ * (cuda/ter_cuda_forward_bitnet.cu:64-146), with fp32 or fp16 X[K]. */
+#define TER_HIP_X_F32_RMS 2
+#define TER_HIP_X_F16_RMS 3
 
 /*
  * Packed ternary weight (replaces WPK, cuda/ter_cuda_forward_packed.cu:400).
@@ -85,6 +90,8 @@ typedef struct ter_hip_act {
     const float* scale_dev;  /* X_I8: device activation scale(s) ([M]), or NULL       */
     int8_t*      q_out;      /* X_F32: optional device copy of the quantized X [M][K]  */
     float*       scale_out;  /* X_F32: optional device act scale(s) 1/scale ([M])     */
+    const uint16_t* gamma;   /* RMS kinds: device fp16 RMSNorm weights [K]             */
+    float        eps;        /* RMS kinds: RMSNorm epsilon                             */
 } ter_hip_act_t;
 
 /* ---------------------------------------------------------------------- */
@@ -198,6 +205,17 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
  * q[m][k] = rn(x[m][k] * 127/(max_k|x[m][k]| + 1e-9)), scale_out[m] = 1/that. */
 int ter_hip_quant_int8(const float* x, int32_t M, int32_t K, int8_t* q, float* scale_out,
                        void* stream);
+
+/* Per-row fused RMSNorm + int8 quantizer, the drop-in for
+ * rmsnorm_quant_f32_in_k / rmsnorm_quant_fp16_in_k
+ * (cuda/ter_cuda_forward_bitnet.cu:64-146, launched <<<1,256>>> per row):
+ * kind TER_HIP_X_F32_RMS (x fp32 [M][K]) or TER_HIP_X_F16_RMS (x fp16 bits [M][K]);
+ * gamma fp16 bits [K].  Sum of squares in the reference's order (256 strided
+ * partials with fused multiply-adds, then the halving tree);
+ * rms_inv = 1 / sqrt(ss / K + eps), correctly rounded (the reference's rsqrtf
+ * is an approximation); n = (x * rms_inv) * gamma; then the quant_int8_k steps. */
+int ter_hip_rmsnorm_quant(const void* x, int32_t kind, const uint16_t* gamma, float eps, int32_t M,
+                          int32_t K, int8_t* q, float* scale_out, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* K4-style handle + KernelTable native slot                               */

@@ -56,6 +56,10 @@ def lib():
         L.orc_quant_int8.restype = None
         L.orc_quant_int8_rows.argtypes = [_P, C.c_int, C.c_int, _P, _P]
         L.orc_quant_int8_rows.restype = None
+        L.orc_half_to_float.argtypes = [C.c_uint16]
+        L.orc_half_to_float.restype = C.c_float
+        L.orc_rmsnorm_quant.argtypes = [_P, _P, _P, C.c_int, C.c_float, _P, _P, _P]
+        L.orc_rmsnorm_quant.restype = None
         L.orc_quantize_bitnet.argtypes = [_P, C.c_size_t, _P]
         L.orc_quantize_bitnet.restype = C.c_float
         L.orc_quantize_nt.argtypes = [_P, C.c_size_t, C.c_int, _P]
@@ -187,6 +191,23 @@ def quant_int8_rows(x: np.ndarray) -> Tuple[np.ndarray, np.ndarray]:
     s = np.empty(M, dtype=np.float32)
     lib().orc_quant_int8_rows(_ptr(x), M, K, _ptr(q), _ptr(s))
     return q, s
+
+
+def rmsnorm_quant(x: np.ndarray, gamma: np.ndarray, eps: float = 1e-5):
+    """rmsnorm_quant_{f32,fp16}_in_k (cuda/ter_cuda_forward_bitnet.cu:64-146):
+    x fp32 or fp16 [H], gamma fp16 [H] -> (int8 [H], act_scale, rms_inv)."""
+    gamma = np.ascontiguousarray(gamma, dtype=np.float16)
+    if x.dtype == np.float16:
+        x16, x32 = np.ascontiguousarray(x), None
+    else:
+        x16, x32 = None, np.ascontiguousarray(x, dtype=np.float32)
+    H = (x16 if x16 is not None else x32).size
+    q = np.empty(H, dtype=np.int8)
+    s = np.zeros(1, dtype=np.float32)
+    r = np.zeros(1, dtype=np.float32)
+    lib().orc_rmsnorm_quant(_ptr(x32) if x32 is not None else None, _ptr(x16) if x16 is not None else None,
+                            _ptr(gamma), H, C.c_float(eps), _ptr(q), _ptr(s), _ptr(r))
+    return q, s[0], r[0]
 
 
 def quantize_bitnet(x: np.ndarray):

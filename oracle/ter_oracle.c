@@ -27,6 +27,11 @@
  *   orc_mm_row_blocked                   -- oracle/_ref.
  *   orc_gemv_v11                         -- equality with orc_mm_row on unpacked W.
  *   orc_quant_int8                       -- closed-form tie / zero / amax cases.
+ *   orc_rmsnorm_quant                    -- closed forms (constant input, single
+ *                                           spike), scale invariance, fp16
+ *                                           widening of exact halves, the
+ *                                           summation order against a
+ *                                           double-precision bound.
  *   orc_quantize_bitnet, orc_quantize_nt -- oracle/_ref.
  *   orc_dequant_i2s                      -- tests/test_nt_dequant.cpp:37-61 block.
  *   orc_i2s_to_v11                       -- decode equality with orc_dequant_i2s.
@@ -213,6 +218,74 @@ void orc_quant_int8(const float* x, int n, int8_t* q, float* act_scale) {
 void orc_quant_int8_rows(const float* x, int M, int K, int8_t* q, float* act_scale) {
     for (int m = 0; m < M; ++m)
         orc_quant_int8(x + (size_t)m * K, K, q + (size_t)m * K, act_scale + m);
+}
+
+/* ------------------------------------------------------------------------ */
+/* IEEE binary16 -> binary32 (exact), the __half2float of the reference.     */
+/* ------------------------------------------------------------------------ */
+float orc_half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu, bits;
+    if (exp == 0x1Fu) {
+        bits = sign | 0x7F800000u | (man << 13);           /* inf / nan */
+    } else if (exp != 0) {
+        bits = sign | ((exp + 112u) << 23) | (man << 13);  /* normal */
+    } else if (man == 0) {
+        bits = sign;                                       /* zero */
+    } else {                                               /* subnormal: renormalize */
+        exp = 113;
+        while ((man & 0x400u) == 0) {
+            man <<= 1;
+            --exp;
+        }
+        bits = sign | (exp << 23) | ((man & 0x3FFu) << 13);
+    }
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Fused RMSNorm + int8 quantizer: rmsnorm_quant_f32_in_k and                 */
+/* rmsnorm_quant_fp16_in_k, cuda/ter_cuda_forward_bitnet.cu:64-146, launched  */
+/* with one block of 256 threads (:859, :873).  x is fp32 (x16 == NULL) or    */
+/* fp16 (x32 == NULL); gamma is fp16.                                         */
+/*   partial[t] = sum over i = t, t+256, ... (increasing) of x_i * x_i, each  */
+/*                step one fused multiply-add (nvcc contracts                 */
+/*                `local_sum += v * v` by default, -fmad=true);               */
+/*   tree: for s = 128, 64, ..., 1: partial[t] += partial[t + s] (t < s);     */
+/*   rms_inv = 1 / sqrt(partial[0] / H + eps).  The reference calls rsqrtf,   */
+/*            an approximation; this restatement and the fabric both use the  */
+/*            correctly rounded division and square root, so CPU and GPU      */
+/*            agree bit for bit (a documented deviation of <= 2 ulp in        */
+/*            rms_inv from the reference GPU build);                          */
+/*   n_i = (x_i * rms_inv) * gamma_i;                                         */
+/*   then the quant_int8_k steps on n (orc_quant_int8).                       */
+/* ------------------------------------------------------------------------ */
+void orc_rmsnorm_quant(const float* x32, const uint16_t* x16, const uint16_t* gamma, int H, float eps,
+                       int8_t* q, float* act_scale, float* rms_inv_out) {
+    float part[256];
+    for (int t = 0; t < 256; ++t) {
+        float acc = 0.f;
+        for (int i = t; i < H; i += 256) {
+            const float v = x32 ? x32[i] : orc_half_to_float(x16[i]);
+            acc = fmaf(v, v, acc);
+        }
+        part[t] = acc;
+    }
+    for (int s = 128; s > 0; s >>= 1)
+        for (int t = 0; t < s; ++t) part[t] += part[t + s];
+    const float rms_inv = 1.0f / sqrtf(part[0] / (float)H + eps);
+    if (rms_inv_out) *rms_inv_out = rms_inv;
+    float* n = (float*)malloc(sizeof(float) * (size_t)(H > 0 ? H : 1));
+    if (!n) return;
+    for (int i = 0; i < H; ++i) {
+        const float v = x32 ? x32[i] : orc_half_to_float(x16[i]);
+        const float a = v * rms_inv;
+        n[i] = a * orc_half_to_float(gamma[i]);
+    }
+    orc_quant_int8(n, H, q, act_scale);
+    free(n);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -15,9 +15,10 @@ from .fabric import (  # noqa: F401
     mm_packed_dispatch,
     mm_row,
     quant_int8,
+    rmsnorm_quant,
     synth_i8,
     synth_v11,
 )
 
 __all__ = ["GemmPlan", "Handle", "PackedTrits", "Plan", "gemv", "mm_batched", "mm_packed_dispatch", "mm_row",
-           "quant_int8", "synth_i8", "synth_v11"]
+           "quant_int8", "rmsnorm_quant", "synth_i8", "synth_v11"]

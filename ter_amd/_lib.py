@@ -33,6 +33,8 @@ M_MAX = 256
 
 X_I8 = 0
 X_F32 = 1
+X_F32_RMS = 2
+X_F16_RMS = 3
 LAYOUT_T16 = 16
 
 
@@ -59,6 +61,8 @@ class Act(C.Structure):
         ("scale_dev", C.c_void_p),
         ("q_out", C.c_void_p),
         ("scale_out", C.c_void_p),
+        ("gamma", C.c_void_p),
+        ("eps", C.c_float),
     ]
 
 
@@ -114,6 +118,7 @@ SIGNATURES = [
     ("ter_hip_gemm", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, _P, _P, _P]),
     ("ter_hip_gemm_plan_create", C.c_int, [C.POINTER(C.c_void_p), C.POINTER(GemmItem), C.c_int32, C.c_int32]),
     ("ter_hip_quant_int8", C.c_int, [_P, C.c_int32, C.c_int32, _P, _P, _P]),
+    ("ter_hip_rmsnorm_quant", C.c_int, [_P, C.c_int32, _P, C.c_float, C.c_int32, C.c_int32, _P, _P, _P]),
     ("ter_hip_create", _P, [C.c_int32]),
     ("ter_hip_destroy", None, [_P]),
     ("ter_hip_install_native", C.c_int, [_P, C.c_char_p, NATIVE_FN]),

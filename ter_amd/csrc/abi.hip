@@ -47,11 +47,21 @@ int check_wpk(const ter_hip_wpk_t* w) {
     return TER_HIP_OK;
 }
 
+bool is_rms(int kind) { return kind == TER_HIP_X_F32_RMS || kind == TER_HIP_X_F16_RMS; }
+
 int check_act(const ter_hip_act_t* x, int M) {
     if (!x || !x->data) return fail(TER_HIP_ERR_NULL, "null activation");
-    if (x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_F32)
+    if (x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_F32 && x->kind != TER_HIP_X_F32_RMS &&
+        x->kind != TER_HIP_X_F16_RMS)
         return fail(TER_HIP_ERR_PAYLOAD, "unknown activation kind %d", x->kind);
-    if (x->kind == TER_HIP_X_F32 && !aligned(x->data, 4)) return fail(TER_HIP_ERR_ALIGN, "fp32 X misaligned");
+    if ((x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS) && !aligned(x->data, 4))
+        return fail(TER_HIP_ERR_ALIGN, "fp32 X misaligned");
+    if (x->kind == TER_HIP_X_F16_RMS && !aligned(x->data, 2)) return fail(TER_HIP_ERR_ALIGN, "fp16 X misaligned");
+    if (is_rms(x->kind)) {
+        if (!x->gamma) return fail(TER_HIP_ERR_NULL, "RMSNorm activation without gamma");
+        if (!aligned(x->gamma, 2)) return fail(TER_HIP_ERR_ALIGN, "gamma misaligned");
+        if (!(x->eps >= 0.f)) return fail(TER_HIP_ERR_SHAPE, "RMSNorm eps must be >= 0");
+    }
     if (M > 1 && x->kind == TER_HIP_X_I8 && !x->scale_dev)
         return fail(TER_HIP_ERR_NULL, "batched int8 X needs per-row device scales");
     return TER_HIP_OK;
@@ -67,8 +77,10 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int
     d.x_scale_dev = x->kind == TER_HIP_X_I8 ? x->scale_dev : nullptr;
     d.y = y;
     d.acc = acc;
-    d.xq_out = x->kind == TER_HIP_X_F32 ? x->q_out : nullptr;
-    d.xs_out = x->kind == TER_HIP_X_F32 ? x->scale_out : nullptr;
+    d.xq_out = x->kind != TER_HIP_X_I8 ? x->q_out : nullptr;
+    d.xs_out = x->kind != TER_HIP_X_I8 ? x->scale_out : nullptr;
+    d.gamma = is_rms(x->kind) ? x->gamma : nullptr;
+    d.eps = x->eps;
     d.fix = reinterpret_cast<unsigned long long*>(w->fix);
     d.tile0 = tile0;
     d.K = w->K;
@@ -547,6 +559,20 @@ void ter_hip_plan_destroy(ter_hip_plan_t* plan) {
     delete plan;
 }
 
+int ter_hip_rmsnorm_quant(const void* x, int32_t kind, const uint16_t* gamma, float eps, int32_t M, int32_t K,
+                          int8_t* q, float* scale_out, void* stream) {
+    if (!x || !gamma || !q || !scale_out) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (!is_rms(kind)) return fail(TER_HIP_ERR_PAYLOAD, "kind %d is not an RMSNorm kind", kind);
+    if (M < 1 || K < 1 || K > TER_HIP_K_MAX || M > 65535) return fail(TER_HIP_ERR_SHAPE, "M=%d K=%d out of range", M, K);
+    if (!aligned(x, kind == TER_HIP_X_F32_RMS ? 4 : 2) || !aligned(gamma, 2))
+        return fail(TER_HIP_ERR_ALIGN, "x or gamma misaligned");
+    if (!(eps >= 0.f)) return fail(TER_HIP_ERR_SHAPE, "RMSNorm eps must be >= 0");
+    hipError_t e = launch_rmsnorm_quant_rows(x, kind == TER_HIP_X_F16_RMS, gamma, eps, M, K, q, scale_out,
+                                             static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm quant launch");
+    return TER_HIP_OK;
+}
+
 int ter_hip_quant_int8(const float* x, int32_t M, int32_t K, int8_t* q, float* scale_out, void* stream) {
     if (!x || !q || !scale_out) return fail(TER_HIP_ERR_NULL, "null argument");
     if (M < 1 || K < 1 || K > TER_HIP_K_MAX || M > 65535) return fail(TER_HIP_ERR_SHAPE, "M=%d K=%d out of range", M, K);
@@ -566,10 +592,13 @@ int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, floa
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int8_t* xq = static_cast<const int8_t*>(x->data);
     const float* xs = x->scale_dev;
-    if (x->kind == TER_HIP_X_F32) {
+    if (x->kind != TER_HIP_X_I8) {
         if (!x->q_out || !x->scale_out)
-            return fail(TER_HIP_ERR_NULL, "fp32 batched X needs q_out and scale_out workspaces");
-        rc = ter_hip_quant_int8(static_cast<const float*>(x->data), M, w->K, x->q_out, x->scale_out, stream);
+            return fail(TER_HIP_ERR_NULL, "fp32/fp16 batched X needs q_out and scale_out workspaces");
+        rc = x->kind == TER_HIP_X_F32
+                 ? ter_hip_quant_int8(static_cast<const float*>(x->data), M, w->K, x->q_out, x->scale_out, stream)
+                 : ter_hip_rmsnorm_quant(x->data, x->kind, x->gamma, x->eps, M, w->K, x->q_out, x->scale_out,
+                                         stream);
         if (rc) return rc;
         xq = x->q_out;
         xs = x->scale_out;

@@ -43,17 +43,19 @@ inline size_t fix_offset(int32_t K, int32_t N) { return tile_stream_bytes(K, N);
 // One GEMV of a work list, as the kernel reads it (device memory or kernarg).
 struct alignas(16) GemvDesc {
     const uint8_t* w;            // T16 tile stream
-    const void* x;               // int8 [K] or fp32 [K]
+    const void* x;               // int8 [K], fp32 [K] or fp16 [K] (x_kind)
     const float* x_scale_dev;    // int8 input: device activation scale or null
     float* y;                    // fp32 [N] or null
     int32_t* acc;                // int32 [N] or null
-    int8_t* xq_out;              // fp32 input: quantized X copy or null
-    float* xs_out;               // fp32 input: activation scale copy or null
+    int8_t* xq_out;              // quantized input: int8 X copy or null
+    float* xs_out;               // quantized input: activation scale copy or null
+    const uint16_t* gamma;       // RMS kinds: fp16 RMSNorm weights [K]
     unsigned long long* fix;     // N fix-up slots, zero at rest
     long long tile0;             // first tile of this GEMV in the launch's stream
     int32_t K, N, Ku, n_strips;
     float w_scale, x_scale;
-    int32_t x_kind, pad_;
+    int32_t x_kind;
+    float eps;                   // RMS kinds
 };
 
 // One GEMM (M > 1) of a work list.  Its blocks (4 column strips x all K each)
@@ -83,6 +85,9 @@ hipError_t launch_synth_v11(uint8_t* v11, int K, int N, uint64_t seed, uint32_t 
                             hipStream_t st);
 hipError_t launch_synth_i8(int8_t* x, long long n, uint64_t seed, int lo, int hi, hipStream_t st);
 hipError_t launch_quant_rows(const float* x, int M, int K, int8_t* q, float* s, hipStream_t st);
+// One workgroup of 256 threads per row; f16 selects fp16 input.
+hipError_t launch_rmsnorm_quant_rows(const void* x, bool f16, const uint16_t* gamma, float eps, int M, int K,
+                                     int8_t* q, float* s, hipStream_t st);
 // Rows per MFMA row block group: MB = 1, 2, 4, 8, 16 for M up to 16, 32, 64, 128, 256.
 int gemm_mb_of(int M);
 // vec: every x pointer 16-byte aligned and every ldx a multiple of 16.
@@ -117,8 +122,39 @@ hipError_t launch_gemm_lds(const GemmDesc& single, const GemmDesc* list_dev, con
 // kWaves * that many strips).
 int gemm_strips_per_wave(int mb);
 
-// LDS bytes the GEMV kernel needs for a K: X (Ku*256 int8) + unit sums + scratch.
-inline int gemv_lds_bytes(int32_t K) { return units_of(K) * kUnitK + units_of(K) * 4 + 64; }
+#if defined(__HIPCC__)
+__device__ inline float half_bits_to_float(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);  // exact widening
+}
+
+// Sum of one value per thread of a 256-thread block, paired exactly as the
+// reference's shared-memory tree (for s = 128, 64, ..., 1: partial[t] +=
+// partial[t + s]): shared memory for the two cross-wave levels, lane shuffles
+// within wave 0 below.  fp32 addition is commutative, so each level adds the
+// same two operands and the result is bit-identical.  Every thread gets it.
+__device__ inline float tree_sum256(float v, float* red) {
+    const int t = threadIdx.x;
+    red[t] = v;
+    __syncthreads();
+    if (t < 128) red[t] = red[t] + red[t + 128];
+    __syncthreads();
+    if (t < 64) {
+        float a = red[t] + red[t + 64];
+#pragma unroll
+        for (int s = 32; s >= 1; s >>= 1) a = a + __shfl_down(a, s);
+        if (t == 0) red[0] = a;
+    }
+    __syncthreads();
+    const float r = red[0];
+    __syncthreads();  // red may be reused
+    return r;
+}
+
+#endif
+
+// LDS bytes the GEMV kernel needs for a K: X (Ku*256 int8) + unit sums +
+// reduction scratch (one float per thread).
+inline int gemv_lds_bytes(int32_t K) { return units_of(K) * kUnitK + units_of(K) * 4 + kGemvThreads * 4; }
 
 int device_cu_count(int device);
 // Resident GEMV workgroups per CU at this LDS size (0 if the query fails).

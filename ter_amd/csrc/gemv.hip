@@ -153,9 +153,53 @@ __device__ __forceinline__ u32x4 load_i16(const int8_t* xp, int k, int K, bool v
 // waiting behind the weight tiles from HBM.  That covers K <= 8192 with 256
 // threads; chunks beyond are loaded during staging.
 struct XPre {
-    float v0[16], v1[16];  // fp32 input
+    float v0[16], v1[16];  // fp32 / fp16 input (as fp32)
     u32x4 q0, q1;          // int8 input
 };
+
+// 16 fp16 activations x[k .. k+15] as fp32 (zeros past K).
+__device__ __forceinline__ void load_h16(const uint16_t* xh, int k, int K, float (&v)[16]) {
+    if (((reinterpret_cast<uintptr_t>(xh + k) & 15u) == 0) && k + 16 <= K) {
+        const TER_GLOBAL u32x4* p = gptr(reinterpret_cast<const u32x4*>(xh + k));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const u32x4 w = p[i];
+            const unsigned wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[8 * i + 2 * j] = half_bits_to_float((uint16_t)(wd[j] & 0xFFFFu));
+                v[8 * i + 2 * j + 1] = half_bits_to_float((uint16_t)(wd[j] >> 16));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = k + i < K ? half_bits_to_float(gptr(xh)[k + i]) : 0.f;
+    }
+}
+
+// 16 activations of an fp32-family input (fp32, or fp16 for X_F16_RMS) as fp32.
+__device__ __forceinline__ void load_x16f(const GemvDesc& d, int k, float (&v)[16]) {
+    if (d.x_kind == TER_HIP_X_F16_RMS) {
+        load_h16(static_cast<const uint16_t*>(d.x), k, d.K, v);
+    } else {
+        const float* xf = static_cast<const float*>(d.x);
+        load_f16(xf, k, d.K, (reinterpret_cast<uintptr_t>(xf) & 15u) == 0, v);
+    }
+}
+
+__device__ __forceinline__ float x_at(const GemvDesc& d, int i) {
+    return d.x_kind == TER_HIP_X_F16_RMS ? half_bits_to_float(gptr(static_cast<const uint16_t*>(d.x))[i])
+                                         : gptr(static_cast<const float*>(d.x))[i];
+}
+
+// RMSNorm of the RMS kinds: n = (x * rms_inv) * gamma on 16 values at k.
+__device__ __forceinline__ void rms_apply(const GemvDesc& d, int k, float rms_inv, float (&v)[16]) {
+#pragma clang fp contract(off)
+    float g[16];
+    load_h16(d.gamma, k, d.K, g);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (v[i] * rms_inv) * g[i];
+}
 
 __device__ __forceinline__ void x_prefetch(const GemvDesc& d, XPre& r) {
     const int nchunks = d.Ku * (kUnitK / 16);
@@ -166,10 +210,8 @@ __device__ __forceinline__ void x_prefetch(const GemvDesc& d, XPre& r) {
         if (c0 < nchunks) r.q0 = load_i16(xp, c0 * 16, d.K, vec_ok);
         if (c1 < nchunks) r.q1 = load_i16(xp, c1 * 16, d.K, vec_ok);
     } else {
-        const float* xf = static_cast<const float*>(d.x);
-        const bool vec_ok = ((reinterpret_cast<uintptr_t>(xf) & 15u) == 0);
-        if (c0 < nchunks) load_f16(xf, c0 * 16, d.K, vec_ok, r.v0);
-        if (c1 < nchunks) load_f16(xf, c1 * 16, d.K, vec_ok, r.v1);
+        if (c0 < nchunks) load_x16f(d, c0 * 16, r.v0);
+        if (c1 < nchunks) load_x16f(d, c1 * 16, r.v1);
     }
 }
 
@@ -178,7 +220,11 @@ __device__ __forceinline__ void x_prefetch(const GemvDesc& d, XPre& r) {
 // Returns the activation scale.  For fp32 input this is the absmax prologue
 // of quant_int8_k (cuda/ter_cuda_forward_packed.cu:40-62): amax = max|x| +
 // 1e-9f, scale = 127.f / amax, q = rint(x * scale) clamped to [-128, 127],
-// act_scale = 1.f / scale.  `owner` (the workgroup that starts the GEMV)
+// act_scale = 1.f / scale.  The RMS kinds first apply the fused RMSNorm of
+// rmsnorm_quant_{f32,fp16}_in_k (cuda/ter_cuda_forward_bitnet.cu:64-146):
+// strided per-thread sums of squares (fused multiply-adds) reduced in the
+// reference's tree order, rms_inv = 1 / sqrt(ss / K + eps) correctly rounded,
+// x <- (x * rms_inv) * gamma.  `owner` (the workgroup that starts the GEMV)
 // also writes the optional copies xq_out / xs_out.
 __device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* usum, float* red, bool owner) {
 #pragma clang fp contract(off)
@@ -195,17 +241,34 @@ __device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* u
             put_chunk(c, load_i16(xp, c * 16, K, vec_ok), lds_x, usum);
         return d.x_scale_dev ? *gptr(d.x_scale_dev) : d.x_scale;
     }
-    const float* xf = static_cast<const float*>(d.x);
-    const bool vec_ok = ((reinterpret_cast<uintptr_t>(xf) & 15u) == 0);
+    const bool rms = d.x_kind != TER_HIP_X_F32;
+    float rms_inv = 1.0f;
+    if (rms) {
+        float part = 0.f;
+        for (int i = tid; i < K; i += kGemvThreads) {
+            const float v = x_at(d, i);
+            part = __builtin_fmaf(v, v, part);
+        }
+        rms_inv = 1.0f / __builtin_sqrtf(tree_sum256(part, red) / (float)K + d.eps);
+    }
+    float v0[16], v1[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        v0[i] = r.v0[i];
+        v1[i] = r.v1[i];
+    }
+    if (rms && c0 < nchunks) rms_apply(d, c0 * 16, rms_inv, v0);
+    if (rms && c1 < nchunks) rms_apply(d, c1 * 16, rms_inv, v1);
     float m = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        if (c0 < nchunks) m = fmaxf(m, fabsf(r.v0[i]));
-        if (c1 < nchunks) m = fmaxf(m, fabsf(r.v1[i]));
+        if (c0 < nchunks) m = fmaxf(m, fabsf(v0[i]));
+        if (c1 < nchunks) m = fmaxf(m, fabsf(v1[i]));
     }
     for (int c = tid + 2 * kGemvThreads; c < nchunks; c += kGemvThreads) {
         float t[16];
-        load_f16(xf, c * 16, K, vec_ok, t);
+        load_x16f(d, c * 16, t);
+        if (rms) rms_apply(d, c * 16, rms_inv, t);
 #pragma unroll
         for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(t[i]));
     }
@@ -221,12 +284,13 @@ __device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* u
     for (int c = tid; c < nchunks; c += kGemvThreads) {
         u32x4 q;
         if (c == c0) {
-            q = pack_q16(r.v0, scale);
+            q = pack_q16(v0, scale);
         } else if (c == c1) {
-            q = pack_q16(r.v1, scale);
+            q = pack_q16(v1, scale);
         } else {
             float t[16];
-            load_f16(xf, c * 16, K, vec_ok, t);
+            load_x16f(d, c * 16, t);
+            if (rms) rms_apply(d, c * 16, rms_inv, t);
             q = pack_q16(t, scale);
         }
         put_chunk(c, q, lds_x, usum);

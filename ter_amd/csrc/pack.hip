@@ -137,6 +137,54 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float* __restrict
     }
 }
 
+// One workgroup (256 threads) per row: the fused RMSNorm + int8 quantizer
+// (rmsnorm_quant_f32_in_k / rmsnorm_quant_fp16_in_k,
+// cuda/ter_cuda_forward_bitnet.cu:64-146) on row m of x[M][K]:
+// per-thread strided partial sums of squares with fused multiply-adds (the
+// reference build contracts `local_sum += v * v`), the reference's reduction
+// tree, rms_inv = 1 / sqrt(ss / K + eps) correctly rounded (the reference's
+// rsqrtf is an approximation), n = (x * rms_inv) * gamma, then quant_int8_k.
+__global__ __launch_bounds__(256) void rmsnorm_quant_rows_kernel(const void* __restrict__ x, int f16,
+                                                                 const uint16_t* __restrict__ gamma, float eps,
+                                                                 int K, int8_t* __restrict__ q,
+                                                                 float* __restrict__ scale_out) {
+#pragma clang fp contract(off)
+    __shared__ float red[256];
+    const int m = blockIdx.x, t = threadIdx.x;
+    const long long row0 = (long long)m * K;
+    auto xv = [&](int k) -> float {
+        return f16 ? half_bits_to_float(static_cast<const uint16_t*>(x)[row0 + k])
+                   : static_cast<const float*>(x)[row0 + k];
+    };
+    float part = 0.f;
+    for (int k = t; k < K; k += 256) {
+        const float v = xv(k);
+        part = __builtin_fmaf(v, v, part);
+    }
+    const float ss = tree_sum256(part, red);
+    const float rms_inv = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
+    float mx = 0.f;
+    for (int k = t; k < K; k += 256) {
+        const float n = (xv(k) * rms_inv) * half_bits_to_float(gamma[k]);
+        mx = fmaxf(mx, fabsf(n));
+    }
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) mx = fmaxf(mx, __shfl_xor(mx, s));
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float amax = mx + 1e-9f;
+    const float scale = 127.0f / amax;
+    if (t == 0) scale_out[m] = 1.0f / scale;
+    int8_t* qr = q + row0;
+    for (int k = t; k < K; k += 256) {
+        const float n = (xv(k) * rms_inv) * half_bits_to_float(gamma[k]);
+        int qi = (int)__builtin_rintf(n * scale);
+        qi = qi > 127 ? 127 : (qi < -128 ? -128 : qi);
+        qr[k] = (int8_t)qi;
+    }
+}
+
 inline unsigned grid_of(long long n, int block) { return (unsigned)((n + block - 1) / block); }
 
 }  // namespace
@@ -166,6 +214,12 @@ hipError_t launch_synth_v11(uint8_t* v11, int K, int N, uint64_t seed, uint32_t 
 
 hipError_t launch_synth_i8(int8_t* x, long long n, uint64_t seed, int lo, int hi, hipStream_t st) {
     hipLaunchKernelGGL(synth_i8_kernel, dim3(grid_of(n, 256)), dim3(256), 0, st, x, n, seed, lo, hi);
+    return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_quant_rows(const void* x, bool f16, const uint16_t* gamma, float eps, int M, int K,
+                                     int8_t* q, float* s, hipStream_t st) {
+    hipLaunchKernelGGL(rmsnorm_quant_rows_kernel, dim3(M), dim3(256), 0, st, x, f16 ? 1 : 0, gamma, eps, K, q, s);
     return hipGetLastError();
 }
 

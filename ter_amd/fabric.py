@@ -107,11 +107,25 @@ class PackedTrits:
         return out
 
 
-def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None) -> L.Act:
+def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=None, eps=1e-5) -> L.Act:
     torch = _torch()
     a = L.Act()
     a.data = x.data_ptr()
-    if x.dtype == torch.int8:
+    if gamma is not None:
+        # fused RMSNorm (fp16 gamma) + absmax quantization in the prologue
+        if gamma.dtype != torch.float16 or not gamma.is_cuda:
+            raise TypeError("gamma must be a CUDA float16 tensor")
+        if x.dtype == torch.float32:
+            a.kind = L.X_F32_RMS
+        elif x.dtype == torch.float16:
+            a.kind = L.X_F16_RMS
+        else:
+            raise TypeError(f"RMSNorm activations must be float32 or float16, got {x.dtype}")
+        a.gamma = gamma.data_ptr()
+        a.eps = float(eps)
+        a.q_out = _ptr(q_out)
+        a.scale_out = _ptr(scale_out)
+    elif x.dtype == torch.int8:
         a.kind = L.X_I8
         a.scale = float(x_scale) if x_scale is not None else 1.0
         a.scale_dev = _ptr(x_scale_dev)
@@ -125,14 +139,15 @@ def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None) -> L.Act
 
 
 def gemv(W: PackedTrits, x, y=None, acc=None, x_scale: Optional[float] = None, x_scale_dev=None,
-         q_out=None, scale_out=None, stream=None):
+         q_out=None, scale_out=None, gamma=None, eps: float = 1e-5, stream=None):
     """M = 1 GEMV.  x: int8 [K] (with x_scale or x_scale_dev) or fp32 [K]
-    (absmax-quantized in the kernel prologue).  Returns (y, acc)."""
+    (absmax-quantized in the kernel prologue); with gamma (fp16 [K]), x fp32 or
+    fp16 is RMS-normalized first (rmsnorm_quant_*_in_k steps).  Returns (y, acc)."""
     torch = _torch()
     _require_cuda(x, "x", None, W.K)
     if y is None and acc is None:
         y = torch.empty(W.N, dtype=torch.float32, device=x.device)
-    a = _act(x, x_scale, x_scale_dev, q_out, scale_out)
+    a = _act(x, x_scale, x_scale_dev, q_out, scale_out, gamma, eps)
     L.check(L.lib().ter_hip_gemv(C.byref(W.wpk), C.byref(a), _ptr(y), _ptr(acc), _stream(stream)),
             "ter_hip_gemv")
     return y, acc
@@ -179,21 +194,44 @@ def quant_int8(x, q=None, scale_out=None, stream=None):
     return q, scale_out
 
 
-def mm_batched(W: PackedTrits, X, y=None, acc=None, x_scale_dev=None, q_out=None, scale_out=None, stream=None):
+def rmsnorm_quant(x, gamma, eps: float = 1e-5, q=None, scale_out=None, stream=None):
+    """Per-row fused RMSNorm + int8 quantization (rmsnorm_quant_{f32,fp16}_in_k,
+    cuda/ter_cuda_forward_bitnet.cu:64-146) of x fp32 or fp16 [M][K] with fp16
+    gamma [K].  Returns (q int8 [M][K], scale_out fp32 [M])."""
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    kind = {torch.float32: L.X_F32_RMS, torch.float16: L.X_F16_RMS}.get(x.dtype)
+    if kind is None:
+        raise TypeError(f"x must be float32 or float16, got {x.dtype}")
+    if gamma.dtype != torch.float16 or gamma.numel() != K:
+        raise TypeError("gamma must be float16 [K]")
+    if q is None:
+        q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    if scale_out is None:
+        scale_out = torch.empty(M, dtype=torch.float32, device=x.device)
+    L.check(L.lib().ter_hip_rmsnorm_quant(x2.data_ptr(), kind, gamma.data_ptr(), C.c_float(eps), M, K, q.data_ptr(),
+                                          scale_out.data_ptr(), _stream(stream)), "ter_hip_rmsnorm_quant")
+    return q, scale_out
+
+
+def mm_batched(W: PackedTrits, X, y=None, acc=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=None,
+               eps: float = 1e-5, stream=None):
     """M > 1 GEMM on MFMA.  X: int8 [M][K] with per-row device scales
     x_scale_dev [M], or fp32 [M][K] (rows quantized into q_out/scale_out,
-    allocated here when absent).  Returns (y [M][N], acc [M][N] or None)."""
+    allocated here when absent); with gamma (fp16 [K]) the fp32 or fp16 rows
+    are RMS-normalized first.  Returns (y [M][N], acc [M][N] or None)."""
     torch = _torch()
     _require_cuda(X, "X")
     M = X.shape[0]
     if y is None and acc is None:
         y = torch.empty((M, W.N), dtype=torch.float32, device=X.device)
-    if X.dtype == torch.float32:
+    if X.dtype in (torch.float32, torch.float16):
         if q_out is None:
             q_out = torch.empty((M, W.K), dtype=torch.int8, device=X.device)
         if scale_out is None:
             scale_out = torch.empty(M, dtype=torch.float32, device=X.device)
-    a = _act(X, None, x_scale_dev, q_out, scale_out)
+    a = _act(X, None, x_scale_dev, q_out, scale_out, gamma, eps)
     L.check(L.lib().ter_hip_gemm(C.byref(W.wpk), C.byref(a), int(M), _ptr(y), _ptr(acc), _stream(stream)),
             "ter_hip_gemm")
     return y, acc
@@ -211,7 +249,8 @@ class Plan:
         for i, it in enumerate(items):
             W = it["w"]
             arr[i].w = C.pointer(W.wpk)
-            arr[i].x = _act(it["x"], it.get("x_scale"), it.get("x_scale_dev"), it.get("q_out"), it.get("scale_out"))
+            arr[i].x = _act(it["x"], it.get("x_scale"), it.get("x_scale_dev"), it.get("q_out"), it.get("scale_out"),
+                            it.get("gamma"), it.get("eps", 1e-5))
             arr[i].y = _ptr(it.get("y"))
             arr[i].acc = _ptr(it.get("acc"))
             self._keep.append(W)

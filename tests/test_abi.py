@@ -27,7 +27,7 @@ def declared_functions():
 
 def test_library_exports_every_declared_symbol():
     names = declared_functions()
-    assert len(names) == 25, names
+    assert len(names) == 26, names
     lib = L.lib()
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
@@ -85,6 +85,21 @@ def test_gemv_validation_without_device():
     assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 0, fake, None, None) == L.ERR_SHAPE
     assert lib.ter_hip_gemm(C.byref(w), C.byref(x), L.M_MAX + 1, fake, None, None) == L.ERR_SHAPE
     assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 8, fake, None, None) == L.ERR_NULL
+    # RMSNorm kinds: gamma required and aligned, eps >= 0, fp16 X 2-byte aligned
+    x.kind, x.data, x.scale_dev = L.X_F32_RMS, fake, None
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_NULL
+    x.gamma = fake + 1
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_ALIGN
+    x.gamma, x.eps = fake, -1.0
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_SHAPE
+    x.kind, x.eps, x.data = L.X_F16_RMS, 1e-5, fake + 1
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_ALIGN
+    assert lib.ter_hip_rmsnorm_quant(fake, L.X_I8, fake, 1e-5, 1, 64, fake, fake, None) == L.ERR_PAYLOAD
+    assert lib.ter_hip_rmsnorm_quant(fake, L.X_F32_RMS, None, 1e-5, 1, 64, fake, fake, None) == L.ERR_NULL
+    assert lib.ter_hip_rmsnorm_quant(fake, L.X_F32_RMS, fake, 1e-5, 0, 64, fake, fake, None) == L.ERR_SHAPE
+    assert lib.ter_hip_rmsnorm_quant(fake, L.X_F32_RMS, fake, float("nan"), 1, 64, fake, fake, None) == L.ERR_SHAPE
+    x.gamma, x.data, x.kind = None, fake, L.X_I8
+    x.scale_dev = None
     # unknown layout tag
     w.layout = 3
     x.scale_dev = fake

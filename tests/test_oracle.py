@@ -196,3 +196,102 @@ def test_i2s_to_v11_matches_dequant():
     dq = O.dequant_i2s(buf, N * K).reshape(N, K)   # (N, K) row-major, values -1/0/+1
     W = O.v11_unpack(O.i2s_to_v11(raw, K, N), K, N)  # [K][N]
     assert (W.T == dq.astype(np.int32)).all()
+
+
+# ---------------------------------------------------------------------------
+# Fused RMSNorm + int8 quantizer (rmsnorm_quant_{f32,fp16}_in_k,
+# cuda/ter_cuda_forward_bitnet.cu:64-146)
+# ---------------------------------------------------------------------------
+
+def test_half_to_float_exhaustive():
+    """The fp16 widening matches IEEE binary16 -> binary32 on every pattern."""
+    L = O.lib()
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([L.orc_half_to_float(int(b)) for b in bits], dtype=np.float32)
+    nan = np.isnan(want)
+    assert (np.isnan(got) == nan).all()
+    assert (got[~nan].view(np.uint32) == want[~nan].view(np.uint32)).all()
+
+
+def test_rmsnorm_quant_constant_input():
+    """x = c everywhere, gamma = 1: the sum of squares is exactly H c^2, so
+    rms_inv = 1 / sqrt(c^2 + eps) and every q is 127."""
+    for c, H in ((3.0, 2560), (-0.5, 6912), (1.0, 256)):
+        x = np.full(H, c, np.float32)
+        q, s, r = O.rmsnorm_quant(x, np.ones(H, np.float16), 1e-5)
+        want_r = np.float32(1.0) / np.sqrt(np.float32(c * c) + np.float32(1e-5))
+        assert r == want_r
+        assert (q == (127 if c > 0 else -127)).all()
+
+
+def test_rmsnorm_quant_single_spike():
+    """One nonzero element A at position p: ss = A^2, q[p] = +-127, others 0."""
+    H, p, A = 2560, 777, np.float32(-6.0)
+    x = np.zeros(H, np.float32)
+    x[p] = A
+    g = np.ones(H, np.float16)
+    g[p] = np.float16(0.5)
+    q, s, r = O.rmsnorm_quant(x, g, 1e-5)
+    want_r = np.float32(1.0) / np.sqrt(np.float32(A * A) / np.float32(H) + np.float32(1e-5))
+    assert r == want_r
+    assert q[p] == -127 and np.count_nonzero(q) == 1
+    n = (A * want_r) * np.float32(0.5)
+    assert s == np.float32(1.0) / (np.float32(127.0) / (np.abs(n) + np.float32(1e-9)))
+
+
+def test_rmsnorm_quant_power_of_two_scale_invariance():
+    """With eps = 0, scaling x by 2^k scales the sum of squares by 4^k and
+    rms_inv by 2^-k exactly, so q and the activation scale are unchanged."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(6912).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, 6912).astype(np.float16)
+    q0, s0, r0 = O.rmsnorm_quant(x, g, 0.0)
+    for k in (-3, 2, 5):
+        q1, s1, r1 = O.rmsnorm_quant(x * np.float32(2.0 ** k), g, 0.0)
+        assert (q1 == q0).all() and s1 == s0 and r1 == r0 * np.float32(2.0 ** -k)
+
+
+def test_rmsnorm_quant_summation_order():
+    """Pins the reference order (256 strided partials, then the tree
+    s = 128..1): with x[0]^2 = 2^24 and 255 ones, the tree gives exactly
+    2^24 + 254 (each level adds an exact even number to partial 0), whereas a
+    sequential sum loses every +1 and gives 2^24."""
+    H = 256
+    x = np.ones(H, np.float32)
+    x[0] = 4096.0
+    q, s, r = O.rmsnorm_quant(x, np.ones(H, np.float16), 0.0)
+    ss_tree = np.float32(2.0 ** 24 + 254)
+    assert r == np.float32(1.0) / np.sqrt(ss_tree / np.float32(H))
+    assert r != np.float32(1.0) / np.sqrt(np.float32(2.0 ** 24) / np.float32(H))
+
+
+def test_rmsnorm_quant_partials_use_fused_multiply_add():
+    """Each partial accumulates with a single rounding per step (v * v + acc
+    fused, as the reference's default contraction does).  Thread 0 sums
+    x[0]^2 then x[256]^2: with these values the fused result (exact product +
+    sum rounded once, computed in float64 where it is exact) differs from
+    rounding the square first."""
+    a = np.float32(0.48121202)
+    b = np.float32(1.3623949)
+    acc0 = np.float32(a * a)
+    # b*b has 48 significant bits and acc0 24 bits, 3 binades lower: their
+    # float64 sum is exact, so one rounding to float32 is the fused result
+    fused = np.float32(np.float64(b) * np.float64(b) + np.float64(acc0))
+    unfused = np.float32(np.float32(b * b) + acc0)
+    assert fused != unfused  # the case distinguishes the two
+    H = 512
+    x = np.zeros(H, np.float32)
+    x[0], x[256] = a, b
+    q, s, r = O.rmsnorm_quant(x, np.ones(H, np.float16), 0.0)
+    assert r == np.float32(1.0) / np.sqrt(fused / np.float32(H))
+
+
+def test_rmsnorm_quant_fp16_input_widens_exactly():
+    """fp16 input equals fp32 input holding the same (exactly widened) values."""
+    rng = np.random.default_rng(9)
+    x16 = rng.standard_normal(2560).astype(np.float16)
+    g = rng.uniform(0.5, 1.5, 2560).astype(np.float16)
+    a = O.rmsnorm_quant(x16, g, 1e-5)
+    b = O.rmsnorm_quant(x16.astype(np.float32), g, 1e-5)
+    assert (a[0] == b[0]).all() and a[1] == b[1] and a[2] == b[2]
