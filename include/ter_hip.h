@@ -115,6 +115,15 @@ int ter_hip_pack_v11(ter_hip_wpk_t* w, const uint8_t* v11_dev, void* stream);
 /* Inverse of ter_hip_pack_v11 (device): write v11 bytes of `w` to v11_dev. */
 int ter_hip_unpack_v11(const ter_hip_wpk_t* w, uint8_t* v11_dev, void* stream);
 
+/* Device repack of a microsoft/BitNet GGUF i2_s tensor (the codes of the
+ * (N, K) tensor, N*K/4 device bytes; replaces the host converter
+ * i2s_to_col_packed, tools/convert_bitnet_to_packed.py:85-157) into `w`, and
+ * zero of its fix-up slots.  The per-tensor scale is the fp32 that follows
+ * the codes in the file (read_i2s_scale, ibid.:85-91): pass it to
+ * ter_hip_wpk_init.  K and N must be multiples of 4 and N*K a multiple of
+ * 128 (whole i2_s blocks), as the converter requires. */
+int ter_hip_pack_i2s(ter_hip_wpk_t* w, const uint8_t* i2s_dev, void* stream);
+
 /* Host pack of a TritTensor payload (int32 [K][N] row-major, the orientation
  * mm_row reads, src/tx/forward.cpp:337) into `w` (synchronous upload).  The
  * payload must be ternary {-m, 0, +m} for one m > 0 (or all zero);

@@ -118,6 +118,7 @@ SIGNATURES = [
     ("ter_hip_gemm", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, _P, _P, _P]),
     ("ter_hip_gemm_plan_create", C.c_int, [C.POINTER(C.c_void_p), C.POINTER(GemmItem), C.c_int32, C.c_int32]),
     ("ter_hip_quant_int8", C.c_int, [_P, C.c_int32, C.c_int32, _P, _P, _P]),
+    ("ter_hip_pack_i2s", C.c_int, [C.POINTER(WPK), _P, _P]),
     ("ter_hip_rmsnorm_quant", C.c_int, [_P, C.c_int32, _P, C.c_float, C.c_int32, C.c_int32, _P, _P, _P]),
     ("ter_hip_create", _P, [C.c_int32]),
     ("ter_hip_destroy", None, [_P]),

@@ -356,6 +356,21 @@ int ter_hip_pack_v11(ter_hip_wpk_t* w, const uint8_t* v11_dev, void* stream) {
     return TER_HIP_OK;
 }
 
+int ter_hip_pack_i2s(ter_hip_wpk_t* w, const uint8_t* i2s_dev, void* stream) {
+    int rc = check_wpk(w);
+    if (rc) return rc;
+    if (!i2s_dev) return fail(TER_HIP_ERR_NULL, "null i2_s buffer");
+    if (w->K % 4 || w->N % 4 || ((long long)w->K * w->N) % 128)
+        return fail(TER_HIP_ERR_SHAPE, "i2_s needs K, N multiples of 4 and N*K a multiple of 128 (K=%d N=%d)", w->K,
+                    w->N);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = launch_pack_i2s(i2s_dev, w->data, w->K, w->N, st);
+    if (e != hipSuccess) return hip_fail(e, "pack_i2s launch");
+    e = hipMemsetAsync(w->fix, 0, (size_t)w->N * sizeof(uint64_t), st);
+    if (e != hipSuccess) return hip_fail(e, "fix-up slot clear");
+    return TER_HIP_OK;
+}
+
 int ter_hip_unpack_v11(const ter_hip_wpk_t* w, uint8_t* v11_dev, void* stream) {
     int rc = check_wpk(w);
     if (rc) return rc;

@@ -81,6 +81,7 @@ hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const i
                        long long total_tiles, int n_wg, int lds_bytes, hipStream_t st);
 hipError_t launch_pack_v11(const uint8_t* v11, uint8_t* t16, int K, int N, hipStream_t st);
 hipError_t launch_unpack_v11(const uint8_t* t16, uint8_t* v11, int K, int N, hipStream_t st);
+hipError_t launch_pack_i2s(const uint8_t* raw, uint8_t* t16, int K, int N, hipStream_t st);
 hipError_t launch_synth_v11(uint8_t* v11, int K, int N, uint64_t seed, uint32_t t0, uint32_t t1,
                             hipStream_t st);
 hipError_t launch_synth_i8(int8_t* x, long long n, uint64_t seed, int lo, int hi, hipStream_t st);

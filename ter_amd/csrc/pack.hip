@@ -47,6 +47,42 @@ __global__ void pack_v11_kernel(const uint8_t* __restrict__ v11, uint32_t* __res
     t16[i] = out;
 }
 
+// One thread per T16 dword, from microsoft/BitNet i2_s bytes
+// (tools/convert_bitnet_to_packed.py:85-157, vendor/ntransformer/core/dequant.cpp:114-145):
+// the (N, K) tensor row-major (element e = n K + k) in blocks of 128 elements
+// per 32 bytes; byte p of a block holds positions p, p+32, p+64, p+96 at
+// shifts 6, 4, 2, 0; codes 0 -> -1, 1 -> 0, 2 -> +1, 3 -> 0, i.e. u = w + 1 =
+// {0, 1, 2, 1}.  Padding rows / columns hold u = 1.
+__global__ void pack_i2s_kernel(const uint8_t* __restrict__ raw, uint32_t* __restrict__ t16, int K, int N,
+                                int Ku, long long n_dwords) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n_dwords) return;
+    const int j = (int)(i & 3);
+    const int lane = (int)((i >> 2) & 63);
+    const long long tile = i >> 8;
+    const int s = (int)(tile / Ku);
+    const int u = (int)(tile - (long long)s * Ku);
+    const int r = lane >> 4, q = lane & 15;
+    const int n = s * kStripCols + r * 4 + j;
+    const int k0 = u * kUnitK + q * 16;
+    unsigned out = 0;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int k = k0 + e;
+        unsigned uval = 1u;
+        if (n < N && k < K) {
+            const long long el = (long long)n * K + k;
+            const long long blk = el >> 7;
+            const int pos = (int)(el & 127);
+            const unsigned code = (raw[blk * 32 + (pos & 31)] >> (6 - 2 * (pos >> 5))) & 3u;
+            uval = code == 3u ? 1u : code;  // w + 1 for w = {-1, 0, +1, 0}
+        }
+        const int f = e >> 2, b = e & 3;
+        out |= uval << (8 * b + 2 * f);
+    }
+    t16[i] = out;
+}
+
 // One thread per v11 byte.
 __global__ void unpack_v11_kernel(const uint32_t* __restrict__ t16, uint8_t* __restrict__ v11, int K,
                                   int N, int Ku) {
@@ -193,6 +229,14 @@ hipError_t launch_pack_v11(const uint8_t* v11, uint8_t* t16, int K, int N, hipSt
     const int Ku = units_of(K);
     const long long n_dwords = (long long)strips_of(N) * Ku * (kTileBytes / 4);
     hipLaunchKernelGGL(pack_v11_kernel, dim3(grid_of(n_dwords, 256)), dim3(256), 0, st, v11,
+                       reinterpret_cast<uint32_t*>(t16), K, N, Ku, n_dwords);
+    return hipGetLastError();
+}
+
+hipError_t launch_pack_i2s(const uint8_t* raw, uint8_t* t16, int K, int N, hipStream_t st) {
+    const int Ku = units_of(K);
+    const long long n_dwords = (long long)strips_of(N) * Ku * (kTileBytes / 4);
+    hipLaunchKernelGGL(pack_i2s_kernel, dim3(grid_of(n_dwords, 256)), dim3(256), 0, st, raw,
                        reinterpret_cast<uint32_t*>(t16), K, N, Ku, n_dwords);
     return hipGetLastError();
 }

@@ -89,6 +89,18 @@ class PackedTrits:
         return w
 
     @classmethod
+    def from_i2s(cls, i2s, K: int, N: int, scale: float, stream=None) -> "PackedTrits":
+        """Device repack of a GGUF i2_s tensor's codes (N*K/4 bytes; the
+        per-tensor fp32 scale that follows them in the file is `scale`)."""
+        torch = _torch()
+        if isinstance(i2s, np.ndarray):
+            i2s = torch.from_numpy(np.ascontiguousarray(i2s, dtype=np.uint8)).cuda()
+        _require_cuda(i2s, "i2s", torch.uint8, N * K // 4)
+        w = cls(K, N, scale, device=i2s.device)
+        L.check(L.lib().ter_hip_pack_i2s(C.byref(w.wpk), i2s.data_ptr(), _stream(stream)), "ter_hip_pack_i2s")
+        return w
+
+    @classmethod
     def from_payload(cls, payload: np.ndarray, scale: float, stream=None) -> "PackedTrits":
         p = np.ascontiguousarray(payload, dtype=np.int32)
         K, N = p.shape

@@ -27,7 +27,7 @@ def declared_functions():
 
 def test_library_exports_every_declared_symbol():
     names = declared_functions()
-    assert len(names) == 26, names
+    assert len(names) == 27, names
     lib = L.lib()
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
@@ -85,6 +85,13 @@ def test_gemv_validation_without_device():
     assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 0, fake, None, None) == L.ERR_SHAPE
     assert lib.ter_hip_gemm(C.byref(w), C.byref(x), L.M_MAX + 1, fake, None, None) == L.ERR_SHAPE
     assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 8, fake, None, None) == L.ERR_NULL
+    # i2_s repack: null codes, K or N not a multiple of 4, N*K not whole 128-blocks
+    assert lib.ter_hip_pack_i2s(C.byref(w), None, None) == L.ERR_NULL
+    w2 = L.WPK()
+    assert lib.ter_hip_wpk_init(C.byref(w2), fake, lib.ter_hip_wpk_bytes(36, 4), 36, 4, 1.0) == L.OK
+    assert lib.ter_hip_pack_i2s(C.byref(w2), fake, None) == L.ERR_SHAPE
+    assert lib.ter_hip_wpk_init(C.byref(w2), fake, lib.ter_hip_wpk_bytes(64, 6), 64, 6, 1.0) == L.OK
+    assert lib.ter_hip_pack_i2s(C.byref(w2), fake, None) == L.ERR_SHAPE
     # RMSNorm kinds: gamma required and aligned, eps >= 0, fp16 X 2-byte aligned
     x.kind, x.data, x.scale_dev = L.X_F32_RMS, fake, None
     assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_NULL

@@ -308,3 +308,23 @@ def test_llama_sweep_full_size_properties(cuda):
         jbs = rng.choice(W.N // 4, size=8, replace=False)
         cols, ra, _ = O.gemv_v11_cols(xa[W.K], 1.0, host(v11s[i]), 1.0, W.K, W.N, jbs)
         assert (a[i][cols] == ra).all(), i
+
+
+@pytest.mark.parametrize("K,N", [(2560, 640), (6912, 2560), (128, 4), (64, 8), (384, 20)])
+def test_pack_i2s_matches_oracle_repack(cuda, K, N):
+    """Device repack of GGUF i2_s codes (tools/convert_bitnet_to_packed.py:85-157):
+    its v11 bytes equal the oracle's i2s_to_v11 of the same codes, and a GEMV
+    on it equals the oracle GEMV (K=384: ragged unit, N=20: ragged strip)."""
+    import torch
+    import ter_amd as T
+    raw = (O.splitmix64(K * 7 + N, N * K // 4) & np.uint64(0xFF)).astype(np.uint8)
+    W = T.PackedTrits.from_i2s(raw, K, N, 0.0271)
+    want_v11 = O.i2s_to_v11(raw, K, N)
+    assert (host(W.to_v11()) == want_v11).all()
+    x = O.rand_int8(K + 1, K)
+    acc = torch.empty(N, dtype=torch.int32, device="cuda")
+    y = torch.empty(N, dtype=torch.float32, device="cuda")
+    T.gemv(W, dev(x), y=y, acc=acc, x_scale=0.013)
+    ra, ry = O.gemv_v11(x, np.float32(0.013), want_v11, 0.0271, K, N)
+    assert (host(acc) == ra).all()
+    assert_f32_equal(host(y), ry)
