@@ -466,7 +466,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures ONE GPU; --gpus {args.gpus} (WORLD_SIZE={world}) is not "
-              "supported (the GEMV shards by output columns across GPUs; see DESIGN.md)", file=sys.stderr)
+              "supported (the GEMV would shard by output columns across GPUs)", file=sys.stderr)
         sys.exit(2)
     import torch
     assert torch.cuda.is_available(), "bench.py needs a GPU"

@@ -13,7 +13,7 @@
  *   - the GPU GEMV launcher     mm_packed_dispatch(X, scale_x_dev, W, out, K, N, stream)
  *       cuda/ter_cuda_forward_packed.cu:493-500
  *   - the CPU GEMV contract     mm_row(sim, kt, id, Xt, row, Wt, K, N, out)
- *       src/tx/forward.cpp:299-352 (internal linkage)
+ *       src/tx/forward.cpp:299-352 (internal linkage: bound through the KernelTable slot below)
  *   - the batched launchers     mm_bitnet_addonly_batched_k<M>(X, X_scale, W_col, K, N, w_scale, out)
  *       cuda/ter_cuda_addonly_batched.cu:31-38
  *   - the activation quantizer  quant_int8_k(x, y, scale_out, N)
@@ -59,13 +59,19 @@ extern "C" {
  * (cuda/ter_cuda_forward_bitnet.cu:64-146), with fp32 or fp16 X[K]. */
 #define TER_HIP_X_F32_RMS 2
 #define TER_HIP_X_F16_RMS 3
+/* relu^2(gate) * up, RMSNorm (fp16 gamma, eps), then absmax -> int8: the
+ * fused relu2_mul_rmsnorm_quant_k step in front of the FFN down projection
+ * (cuda/ter_cuda_forward_bitnet.cu:258-309, launched <<<1,1024>>> at :884).
+ * `data` is the fp16 gate [K], `up` the fp16 up projection [K]. */
+#define TER_HIP_X_RELU2_RMS 4
 
 /*
  * Packed ternary weight (replaces WPK, cuda/ter_cuda_forward_packed.cu:400).
  *
  * `data` holds the "T16" tile stream the kernels read: 1 KiB tiles of
  * 16 output columns x 256 input rows, 2 bits per trit, stored as u = w + 1
- * (see DESIGN.md for the bit layout), followed by `N` 64-bit fix-up slots
+ * (dword 4L+j of a tile holds column 4(L/16)+j of the tile's strip over rows
+ * 16(L%16)+e, e = 4f+b at bits 8b+2f), followed by `N` 64-bit fix-up slots
  * (`fix`, zero at rest) used to combine split column strips.  The whole
  * buffer is `ter_hip_wpk_bytes(K, N)` bytes of device memory owned by the
  * caller.  `scale` is the per-tensor weight scale (Wt.scale; a ternary
@@ -84,15 +90,37 @@ typedef struct ter_hip_wpk {
 
 /* Activation operand of one GEMV / GEMM. */
 typedef struct ter_hip_act {
-    const void*  data;       /* device: int8 [M][K] (X_I8) or fp32 [M][K] (X_F32)      */
-    int32_t      kind;       /* TER_HIP_X_I8 or TER_HIP_X_F32                          */
+    const void*  data;       /* device: int8 (X_I8), fp32 (X_F32, X_F32_RMS) or fp16
+                                (X_F16_RMS; the gate for X_RELU2_RMS) [M][K]            */
+    int32_t      kind;       /* TER_HIP_X_*                                            */
     float        scale;      /* X_I8: host activation scale, used when scale_dev NULL  */
     const float* scale_dev;  /* X_I8: device activation scale(s) ([M]), or NULL       */
     int8_t*      q_out;      /* X_F32: optional device copy of the quantized X [M][K]  */
     float*       scale_out;  /* X_F32: optional device act scale(s) 1/scale ([M])     */
     const uint16_t* gamma;   /* RMS kinds: device fp16 RMSNorm weights [K]             */
     float        eps;        /* RMS kinds: RMSNorm epsilon                             */
+    const uint16_t* up;      /* X_RELU2_RMS: device fp16 up projection [M][K]         */
 } ter_hip_act_t;
+
+/* Outputs of one GEMV / GEMM; any subset, at least one non-NULL.  With
+ * y = float(acc) * (x_scale * w->scale):
+ *   y     fp32 [M][N]
+ *   acc   int32 [M][N]
+ *   y16   fp16 bits [M][N] = half(y), round to nearest even: the reference's
+ *         projection output out[j] = __float2half((float)acc * scale)
+ *         (cuda/ter_cuda_forward_packed.cu:393, ter_cuda_forward_bitnet.cu:557,
+ *         ter_cuda_addonly_batched.cu:120)
+ *   resid fp32 [M][N], updated in place: resid += float(half(y)), the
+ *         projection followed by add_k_f32 into the residual stream
+ *         (cuda/ter_cuda_forward_bitnet.cu:51-54, :876, :887).  A plain
+ *         read-modify-write: no other work of the same launch may target the
+ *         same elements. */
+typedef struct ter_hip_out {
+    float*    y;
+    int32_t*  acc;
+    uint16_t* y16;
+    float*    resid;
+} ter_hip_out_t;
 
 /* ---------------------------------------------------------------------- */
 /* Packed payload (TritTensor -> device tile stream)                       */
@@ -140,12 +168,21 @@ int ter_hip_pack_payload(ter_hip_wpk_t* w, const int32_t* payload_host, float sc
  * y (fp32 [N]) and acc (int32 [N]) are optional device outputs (at least one). */
 int ter_hip_gemv(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int32_t* acc,
                  void* stream);
+/* ter_hip_gemv with every output form (ter_hip_out_t). */
+int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip_out_t* out,
+                     void* stream);
 
 /* Drop-in for mm_packed_dispatch (cuda/ter_cuda_forward_packed.cu:493-500):
  * int8 X, device activation scale, fp32 out[N].  K, N must match W. */
 int ter_hip_mm_packed_dispatch(const int8_t* X, const float* scale_x_dev,
                                const ter_hip_wpk_t* W, float* out, int32_t K, int32_t N,
                                void* stream);
+/* mm_packed_dispatch with the reference's own output type: fp16 out[N] =
+ * __float2half((float)acc * scale) (cuda/ter_cuda_forward_packed.cu:493-500,
+ * ter_cuda_forward_bitnet.cu:837-845). */
+int ter_hip_mm_packed_dispatch_f16(const int8_t* X, const float* scale_x_dev,
+                                   const ter_hip_wpk_t* W, uint16_t* out, int32_t K, int32_t N,
+                                   void* stream);
 
 /* Host-side mm_row contract (src/tx/forward.cpp:299-352): X is the host
  * TritTensor payload (int32 [rows][K]), `row` selects the row; out (host
@@ -165,13 +202,16 @@ typedef struct ter_hip_gemv_item {
     ter_hip_act_t        x;
     float*               y;    /* fp32 [N] or NULL */
     int32_t*             acc;  /* int32 [N] or NULL */
+    uint16_t*            y16;  /* fp16 [N] or NULL (ter_hip_out_t)            */
+    float*               resid;/* fp32 [N] residual, += half(y), or NULL      */
 } ter_hip_gemv_item_t;
 
 typedef struct ter_hip_plan ter_hip_plan_t;
 
 /* Build a launch plan for `n` GEMVs (descriptor table copied to the device).
  * wg_per_cu <= 0 picks the default occupancy.  Items sharing a weight must not
- * appear twice in one plan. */
+ * appear twice in one plan, and no two items may write overlapping `resid`
+ * ranges (TER_HIP_ERR_CONFLICT). */
 int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items, int32_t n,
                         int32_t wg_per_cu);
 int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream);
@@ -191,6 +231,9 @@ void ter_hip_plan_destroy(ter_hip_plan_t* plan);
  * X_I8, x->scale_dev ([M]) is required. */
 int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, float* y,
                  int32_t* acc, void* stream);
+/* ter_hip_gemm with every output form (ter_hip_out_t, [M][N] each). */
+int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M,
+                     const ter_hip_out_t* out, void* stream);
 
 /* Many independent GEMMs in ONE launch (batched decode / prefill over a
  * layer sweep; replaces one mm_bitnet_addonly_batched_k launch per
@@ -205,6 +248,8 @@ typedef struct ter_hip_gemm_item {
     int32_t              M;
     float*               y;            /* fp32 [M][N] or NULL                */
     int32_t*             acc;          /* int32 [M][N] or NULL               */
+    uint16_t*            y16;          /* fp16 [M][N] or NULL                */
+    float*               resid;        /* fp32 [M][N] residual or NULL       */
 } ter_hip_gemm_item_t;
 
 int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* items, int32_t n,
@@ -225,6 +270,16 @@ int ter_hip_quant_int8(const float* x, int32_t M, int32_t K, int8_t* q, float* s
  * is an approximation); n = (x * rms_inv) * gamma; then the quant_int8_k steps. */
 int ter_hip_rmsnorm_quant(const void* x, int32_t kind, const uint16_t* gamma, float eps, int32_t M,
                           int32_t K, int8_t* q, float* scale_out, void* stream);
+/* Per-row fused relu^2(gate) * up + RMSNorm + int8 quantizer, the drop-in for
+ * relu2_mul_rmsnorm_quant_k (cuda/ter_cuda_forward_bitnet.cu:258-309,
+ * <<<1,1024>>> per row at :884): gate, up fp16 bits [M][F], gamma fp16 [F].
+ * v = (g > 0 ? g*g : 0) * u; sum of squares in the 1024-thread order (1024
+ * strided partials with fused multiply-adds, tree from s = 512);
+ * rms_inv = 1 / sqrt(ss / F + eps), correctly rounded; n = (v * rms_inv) *
+ * gamma; then the quant_int8_k steps. */
+int ter_hip_relu2_rmsnorm_quant(const uint16_t* gate, const uint16_t* up, const uint16_t* gamma,
+                                float eps, int32_t M, int32_t F, int8_t* q, float* scale_out,
+                                void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* K4-style handle + KernelTable native slot                               */

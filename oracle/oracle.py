@@ -60,6 +60,14 @@ def lib():
         L.orc_half_to_float.restype = C.c_float
         L.orc_rmsnorm_quant.argtypes = [_P, _P, _P, C.c_int, C.c_float, _P, _P, _P]
         L.orc_rmsnorm_quant.restype = None
+        L.orc_float_to_half.argtypes = [C.c_float]
+        L.orc_float_to_half.restype = C.c_uint16
+        L.orc_float_to_half_n.argtypes = [_P, _P, C.c_size_t]
+        L.orc_float_to_half_n.restype = None
+        L.orc_relu2_rmsnorm_quant.argtypes = [_P, _P, _P, C.c_int, C.c_float, _P, _P, _P]
+        L.orc_relu2_rmsnorm_quant.restype = None
+        L.orc_residual_add_f16.argtypes = [_P, _P, C.c_int]
+        L.orc_residual_add_f16.restype = None
         L.orc_quantize_bitnet.argtypes = [_P, C.c_size_t, _P]
         L.orc_quantize_bitnet.restype = C.c_float
         L.orc_quantize_nt.argtypes = [_P, C.c_size_t, C.c_int, _P]
@@ -208,6 +216,36 @@ def rmsnorm_quant(x: np.ndarray, gamma: np.ndarray, eps: float = 1e-5):
     lib().orc_rmsnorm_quant(_ptr(x32) if x32 is not None else None, _ptr(x16) if x16 is not None else None,
                             _ptr(gamma), H, C.c_float(eps), _ptr(q), _ptr(s), _ptr(r))
     return q, s[0], r[0]
+
+
+def float_to_half_bits(x: np.ndarray) -> np.ndarray:
+    """binary32 -> binary16 bit patterns, round to nearest even."""
+    f = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    h = np.empty(f.size, dtype=np.uint16)
+    lib().orc_float_to_half_n(_ptr(f), _ptr(h), f.size)
+    return h
+
+
+def relu2_rmsnorm_quant(gate: np.ndarray, up: np.ndarray, gamma: np.ndarray, eps: float = 1e-5):
+    """relu2_mul_rmsnorm_quant_k (cuda/ter_cuda_forward_bitnet.cu:258-309):
+    fp16 gate, up, gamma [F] -> (int8 [F], act_scale, rms_inv)."""
+    g = np.ascontiguousarray(gate, dtype=np.float16)
+    u = np.ascontiguousarray(up, dtype=np.float16)
+    gm = np.ascontiguousarray(gamma, dtype=np.float16)
+    F = g.size
+    q = np.empty(F, dtype=np.int8)
+    s = np.zeros(1, dtype=np.float32)
+    r = np.zeros(1, dtype=np.float32)
+    lib().orc_relu2_rmsnorm_quant(_ptr(g), _ptr(u), _ptr(gm), F, C.c_float(eps), _ptr(q), _ptr(s), _ptr(r))
+    return q, s[0], r[0]
+
+
+def residual_add_f16(hidden: np.ndarray, y: np.ndarray) -> np.ndarray:
+    """add_k_f32 after an fp16 GEMV output: hidden + float(half(y))."""
+    h = np.array(hidden, dtype=np.float32, copy=True)
+    yy = np.ascontiguousarray(y, dtype=np.float32)
+    lib().orc_residual_add_f16(_ptr(h), _ptr(yy), h.size)
+    return h
 
 
 def quantize_bitnet(x: np.ndarray):

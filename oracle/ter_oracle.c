@@ -27,6 +27,14 @@
  *   orc_mm_row_blocked                   -- oracle/_ref.
  *   orc_gemv_v11                         -- equality with orc_mm_row on unpacked W.
  *   orc_quant_int8                       -- closed-form tie / zero / amax cases.
+ *   orc_float_to_half                    -- numpy's IEEE binary16 rounding on
+ *                                           edge sets and random patterns.
+ *   orc_relu2_rmsnorm_quant              -- closed forms (constant gate/up,
+ *                                           negative gates), equality with
+ *                                           orc_rmsnorm_quant where the
+ *                                           1024-thread order reduces to it,
+ *                                           a summation-order case.
+ *   orc_residual_add_f16                 -- orc_float_to_half / orc_half_to_float.
  *   orc_rmsnorm_quant                    -- closed forms (constant input, single
  *                                           spike), scale invariance, fp16
  *                                           widening of exact halves, the
@@ -286,6 +294,83 @@ void orc_rmsnorm_quant(const float* x32, const uint16_t* x16, const uint16_t* ga
     }
     orc_quant_int8(n, H, q, act_scale);
     free(n);
+}
+
+/* ------------------------------------------------------------------------ */
+/* binary32 -> binary16, round to nearest even (the reference's             */
+/* __float2half of its fp16 outputs, cuda/ter_cuda_forward_packed.cu:393).  */
+/* ------------------------------------------------------------------------ */
+uint16_t orc_float_to_half(float f) {
+    uint32_t x;
+    memcpy(&x, &f, sizeof x);
+    const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    const uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) return sign | (ax > 0x7F800000u ? 0x7E00u : 0x7C00u); /* nan / inf */
+    if (ax >= 0x477FF000u) return sign | 0x7C00u;                               /* rounds past 65504 */
+    if (ax < 0x38800000u) {                                                     /* half subnormal or zero */
+        if (ax < 0x33000000u) return sign;                                       /* below half of 2^-24 */
+        const uint32_t man = (ax & 0x7FFFFFu) | 0x800000u;
+        const int shift = 126 - (int)(ax >> 23);                                 /* 14 .. 24 */
+        const uint32_t q = man >> shift, rem = man & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        return sign | (uint16_t)(q + (rem > half || (rem == half && (q & 1u))));
+    }
+    const uint32_t e = (ax >> 23) - 112u, man = ax & 0x7FFFFFu;                  /* normal */
+    const uint32_t q = (e << 10) | (man >> 13), rem = man & 0x1FFFu;
+    return sign | (uint16_t)(q + (rem > 0x1000u || (rem == 0x1000u && (q & 1u))));
+}
+
+void orc_float_to_half_n(const float* f, uint16_t* h, size_t n) {
+    for (size_t i = 0; i < n; ++i) h[i] = orc_float_to_half(f[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Fused relu^2(gate) * up + RMSNorm + int8 quantizer:                       */
+/* relu2_mul_rmsnorm_quant_k, cuda/ter_cuda_forward_bitnet.cu:258-309,       */
+/* launched with one block of 1024 threads (:884).  gate, up, gamma fp16.    */
+/*   v_i = (g_i > 0 ? g_i * g_i : 0) * u_i;                                 */
+/*   partial[t] (t < 1024) = sum over i = t, t+1024, ... of v_i * v_i, each  */
+/*   step a fused multiply-add; tree s = 512, ..., 1; rms_inv as in         */
+/*   orc_rmsnorm_quant (correctly rounded); n_i = (v_i * rms_inv) * gamma_i; */
+/*   then quant_int8_k.                                                      */
+/* ------------------------------------------------------------------------ */
+static float relu2_mul(uint16_t g16, uint16_t u16) {
+    const float g = orc_half_to_float(g16), u = orc_half_to_float(u16);
+    const float r = g > 0.f ? g * g : 0.f;
+    return r * u;
+}
+
+void orc_relu2_rmsnorm_quant(const uint16_t* gate, const uint16_t* up, const uint16_t* gamma, int F, float eps,
+                             int8_t* q, float* act_scale, float* rms_inv_out) {
+    float part[1024];
+    for (int t = 0; t < 1024; ++t) {
+        float acc = 0.f;
+        for (int i = t; i < F; i += 1024) {
+            const float v = relu2_mul(gate[i], up[i]);
+            acc = fmaf(v, v, acc);
+        }
+        part[t] = acc;
+    }
+    for (int s = 512; s > 0; s >>= 1)
+        for (int t = 0; t < s; ++t) part[t] += part[t + s];
+    const float rms_inv = 1.0f / sqrtf(part[0] / (float)F + eps);
+    if (rms_inv_out) *rms_inv_out = rms_inv;
+    float* n = (float*)malloc(sizeof(float) * (size_t)(F > 0 ? F : 1));
+    if (!n) return;
+    for (int i = 0; i < F; ++i) {
+        const float a = relu2_mul(gate[i], up[i]) * rms_inv;
+        n[i] = a * orc_half_to_float(gamma[i]);
+    }
+    orc_quant_int8(n, F, q, act_scale);
+    free(n);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Residual add of an fp16-rounded projection output: add_k_f32,             */
+/* cuda/ter_cuda_forward_bitnet.cu:51-54, after the GEMV wrote               */
+/* __float2half((float)acc * scale): hidden[i] += float(half(y[i])).         */
+/* ------------------------------------------------------------------------ */
+void orc_residual_add_f16(float* hidden, const float* y, int n) {
+    for (int i = 0; i < n; ++i) hidden[i] = hidden[i] + orc_half_to_float(orc_float_to_half(y[i]));
 }
 
 /* ------------------------------------------------------------------------ */

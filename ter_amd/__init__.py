@@ -13,12 +13,15 @@ from .fabric import (  # noqa: F401
     gemv,
     mm_batched,
     mm_packed_dispatch,
+    mm_packed_dispatch_f16,
     mm_row,
     quant_int8,
+    relu2_rmsnorm_quant,
     rmsnorm_quant,
     synth_i8,
     synth_v11,
 )
 
-__all__ = ["GemmPlan", "Handle", "PackedTrits", "Plan", "gemv", "mm_batched", "mm_packed_dispatch", "mm_row",
-           "quant_int8", "rmsnorm_quant", "synth_i8", "synth_v11"]
+__all__ = ["GemmPlan", "Handle", "PackedTrits", "Plan", "gemv", "mm_batched", "mm_packed_dispatch",
+           "mm_packed_dispatch_f16", "mm_row", "quant_int8", "relu2_rmsnorm_quant", "rmsnorm_quant", "synth_i8",
+           "synth_v11"]

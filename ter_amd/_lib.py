@@ -35,6 +35,7 @@ X_I8 = 0
 X_F32 = 1
 X_F32_RMS = 2
 X_F16_RMS = 3
+X_RELU2_RMS = 4
 LAYOUT_T16 = 16
 
 
@@ -63,6 +64,17 @@ class Act(C.Structure):
         ("scale_out", C.c_void_p),
         ("gamma", C.c_void_p),
         ("eps", C.c_float),
+        ("up", C.c_void_p),
+    ]
+
+
+class Out(C.Structure):
+    """ter_hip_out_t -- output forms of one GEMV / GEMM."""
+    _fields_ = [
+        ("y", C.c_void_p),
+        ("acc", C.c_void_p),
+        ("y16", C.c_void_p),
+        ("resid", C.c_void_p),
     ]
 
 
@@ -72,6 +84,8 @@ class GemvItem(C.Structure):
         ("x", Act),
         ("y", C.c_void_p),
         ("acc", C.c_void_p),
+        ("y16", C.c_void_p),
+        ("resid", C.c_void_p),
     ]
 
 
@@ -83,6 +97,8 @@ class GemmItem(C.Structure):
         ("M", C.c_int32),
         ("y", C.c_void_p),
         ("acc", C.c_void_p),
+        ("y16", C.c_void_p),
+        ("resid", C.c_void_p),
     ]
 
 
@@ -109,17 +125,21 @@ SIGNATURES = [
     ("ter_hip_unpack_v11", C.c_int, [C.POINTER(WPK), _P, _P]),
     ("ter_hip_pack_payload", C.c_int, [C.POINTER(WPK), _P, C.c_float, C.POINTER(C.c_int32), _P]),
     ("ter_hip_gemv", C.c_int, [C.POINTER(WPK), C.POINTER(Act), _P, _P, _P]),
+    ("ter_hip_gemv_out", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.POINTER(Out), _P]),
     ("ter_hip_mm_packed_dispatch", C.c_int, [_P, _P, C.POINTER(WPK), _P, C.c_int32, C.c_int32, _P]),
+    ("ter_hip_mm_packed_dispatch_f16", C.c_int, [_P, _P, C.POINTER(WPK), _P, C.c_int32, C.c_int32, _P]),
     ("ter_hip_mm_row", C.c_int, [_P, C.c_int32, C.c_int32, C.c_float, C.POINTER(WPK), C.c_int32, _P, _P, _P, _P]),
     ("ter_hip_plan_create", C.c_int, [C.POINTER(C.c_void_p), C.POINTER(GemvItem), C.c_int32, C.c_int32]),
     ("ter_hip_plan_launch", C.c_int, [_P, _P]),
     ("ter_hip_plan_stats", C.c_int, [_P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_int32)]),
     ("ter_hip_plan_destroy", None, [_P]),
     ("ter_hip_gemm", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, _P, _P, _P]),
+    ("ter_hip_gemm_out", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, C.POINTER(Out), _P]),
     ("ter_hip_gemm_plan_create", C.c_int, [C.POINTER(C.c_void_p), C.POINTER(GemmItem), C.c_int32, C.c_int32]),
     ("ter_hip_quant_int8", C.c_int, [_P, C.c_int32, C.c_int32, _P, _P, _P]),
     ("ter_hip_pack_i2s", C.c_int, [C.POINTER(WPK), _P, _P]),
     ("ter_hip_rmsnorm_quant", C.c_int, [_P, C.c_int32, _P, C.c_float, C.c_int32, C.c_int32, _P, _P, _P]),
+    ("ter_hip_relu2_rmsnorm_quant", C.c_int, [_P, _P, _P, C.c_float, C.c_int32, C.c_int32, _P, _P, _P]),
     ("ter_hip_create", _P, [C.c_int32]),
     ("ter_hip_destroy", None, [_P]),
     ("ter_hip_install_native", C.c_int, [_P, C.c_char_p, NATIVE_FN]),

@@ -47,16 +47,22 @@ int check_wpk(const ter_hip_wpk_t* w) {
     return TER_HIP_OK;
 }
 
-bool is_rms(int kind) { return kind == TER_HIP_X_F32_RMS || kind == TER_HIP_X_F16_RMS; }
+bool is_rms(int kind) {
+    return kind == TER_HIP_X_F32_RMS || kind == TER_HIP_X_F16_RMS || kind == TER_HIP_X_RELU2_RMS;
+}
 
 int check_act(const ter_hip_act_t* x, int M) {
     if (!x || !x->data) return fail(TER_HIP_ERR_NULL, "null activation");
-    if (x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_F32 && x->kind != TER_HIP_X_F32_RMS &&
-        x->kind != TER_HIP_X_F16_RMS)
+    if (x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_F32 && !is_rms(x->kind))
         return fail(TER_HIP_ERR_PAYLOAD, "unknown activation kind %d", x->kind);
     if ((x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS) && !aligned(x->data, 4))
         return fail(TER_HIP_ERR_ALIGN, "fp32 X misaligned");
-    if (x->kind == TER_HIP_X_F16_RMS && !aligned(x->data, 2)) return fail(TER_HIP_ERR_ALIGN, "fp16 X misaligned");
+    if ((x->kind == TER_HIP_X_F16_RMS || x->kind == TER_HIP_X_RELU2_RMS) && !aligned(x->data, 2))
+        return fail(TER_HIP_ERR_ALIGN, "fp16 X misaligned");
+    if (x->kind == TER_HIP_X_RELU2_RMS) {
+        if (!x->up) return fail(TER_HIP_ERR_NULL, "relu2 activation without up");
+        if (!aligned(x->up, 2)) return fail(TER_HIP_ERR_ALIGN, "fp16 up misaligned");
+    }
     if (is_rms(x->kind)) {
         if (!x->gamma) return fail(TER_HIP_ERR_NULL, "RMSNorm activation without gamma");
         if (!aligned(x->gamma, 2)) return fail(TER_HIP_ERR_ALIGN, "gamma misaligned");
@@ -67,19 +73,74 @@ int check_act(const ter_hip_act_t* x, int M) {
     return TER_HIP_OK;
 }
 
+int check_out(const ter_hip_out_t* o) {
+    if (!o || (!o->y && !o->acc && !o->y16 && !o->resid)) return fail(TER_HIP_ERR_NULL, "no output buffer");
+    if (!aligned(o->y, 4) || !aligned(o->acc, 4) || !aligned(o->y16, 2) || !aligned(o->resid, 4))
+        return fail(TER_HIP_ERR_ALIGN, "output buffer misaligned");
+    return TER_HIP_OK;
+}
+
+// Algorithmic bytes per activation element (inputs, gamma included) and per
+// output element (a residual is read and written).
+unsigned act_bytes(int kind) {
+    switch (kind) {
+        case TER_HIP_X_F32: return 4;
+        case TER_HIP_X_F32_RMS: return 6;
+        case TER_HIP_X_F16_RMS: return 4;
+        case TER_HIP_X_RELU2_RMS: return 6;
+        default: return 1;
+    }
+}
+unsigned out_bytes(const ter_hip_out_t& o) {
+    return (o.y ? 4u : 0u) + (o.acc ? 4u : 0u) + (o.y16 ? 2u : 0u) + (o.resid ? 8u : 0u);
+}
+
+typedef std::vector<std::pair<uintptr_t, uintptr_t>> Ranges;
+
+bool overlaps(const std::pair<uintptr_t, uintptr_t>& a, const std::pair<uintptr_t, uintptr_t>& b) {
+    return a.first < b.second && b.first < a.second;
+}
+
+// Device byte ranges an activation operand reads (M rows of K elements).
+void act_ranges(const ter_hip_act_t* x, int M, int K, Ranges* out) {
+    const size_t n = (size_t)M * (size_t)K;
+    const size_t el = x->kind == TER_HIP_X_I8 ? 1 : (x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS ? 4 : 2);
+    out->emplace_back((uintptr_t)x->data, (uintptr_t)x->data + n * el);
+    if (x->kind == TER_HIP_X_RELU2_RMS && x->up) out->emplace_back((uintptr_t)x->up, (uintptr_t)(x->up + n));
+}
+
+// Residual targets of one launch must not overlap one another or any input
+// the launch reads: each element is a plain read-modify-write by the one
+// thread that finishes its column, while other workgroups may still be
+// reading their activations.
+int check_resid_overlap(const Ranges& resid, const Ranges& inputs) {
+    for (size_t i = 0; i < resid.size(); ++i) {
+        for (size_t k = 0; k < i; ++k)
+            if (overlaps(resid[i], resid[k]))
+                return fail(TER_HIP_ERR_CONFLICT, "residual outputs %zu and %zu overlap", i, k);
+        for (const auto& in : inputs)
+            if (overlaps(resid[i], in))
+                return fail(TER_HIP_ERR_CONFLICT, "residual output %zu overlaps an activation input", i);
+    }
+    return TER_HIP_OK;
+}
+
 std::mutex g_cu_mu;
 std::vector<int> g_cu;
 
-GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int32_t* acc, long long tile0) {
+GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip_out_t& o, long long tile0) {
     GemvDesc d{};
     d.w = w->data;
     d.x = x->data;
     d.x_scale_dev = x->kind == TER_HIP_X_I8 ? x->scale_dev : nullptr;
-    d.y = y;
-    d.acc = acc;
+    d.y = o.y;
+    d.acc = o.acc;
+    d.y16 = o.y16;
+    d.resid = o.resid;
     d.xq_out = x->kind != TER_HIP_X_I8 ? x->q_out : nullptr;
     d.xs_out = x->kind != TER_HIP_X_I8 ? x->scale_out : nullptr;
     d.gamma = is_rms(x->kind) ? x->gamma : nullptr;
+    d.up = x->kind == TER_HIP_X_RELU2_RMS ? x->up : nullptr;
     d.eps = x->eps;
     d.fix = reinterpret_cast<unsigned long long*>(w->fix);
     d.tile0 = tile0;
@@ -121,14 +182,16 @@ int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, int* n_wg) {
 }
 
 // per_block: strips per block of the launch (kWaves * strips per wave for its row-block count).
-GemmDesc make_gemm_desc(const ter_hip_wpk_t* w, const int8_t* x, const float* xs, int M, float* y, int32_t* acc,
+GemmDesc make_gemm_desc(const ter_hip_wpk_t* w, const int8_t* x, const float* xs, int M, const ter_hip_out_t& o,
                         long long block0, int per_block, long long tile0) {
     GemmDesc d{};
     d.w = w->data;
     d.x = x;
     d.xs = xs;
-    d.y = y;
-    d.acc = acc;
+    d.y = o.y;
+    d.acc = o.acc;
+    d.y16 = o.y16;
+    d.resid = o.resid;
     d.block0 = block0;
     d.tile0 = tile0;
     d.K = w->K;
@@ -434,12 +497,24 @@ int ter_hip_pack_payload(ter_hip_wpk_t* w, const int32_t* payload, float scale, 
 }
 
 int ter_hip_gemv(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int32_t* acc, void* stream) {
+    const ter_hip_out_t o{y, acc, nullptr, nullptr};
+    return ter_hip_gemv_out(w, x, &o, stream);
+}
+
+int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip_out_t* out, void* stream) {
     int rc = check_wpk(w);
     if (rc) return rc;
     rc = check_act(x, 1);
     if (rc) return rc;
-    if (!y && !acc) return fail(TER_HIP_ERR_NULL, "no output buffer");
-    const GemvDesc d = make_desc(w, x, y, acc, 0);
+    rc = check_out(out);
+    if (rc) return rc;
+    if (out->resid) {
+        Ranges in;
+        act_ranges(x, 1, w->K, &in);
+        rc = check_resid_overlap({{(uintptr_t)out->resid, (uintptr_t)(out->resid + w->N)}}, in);
+        if (rc) return rc;
+    }
+    const GemvDesc d = make_desc(w, x, *out, 0);
     const long long total = (long long)d.n_strips * d.Ku;
     int n_wg = 0;
     const int lds = gemv_lds_bytes(w->K);
@@ -459,6 +534,18 @@ int ter_hip_mm_packed_dispatch(const int8_t* X, const float* scale_x_dev, const 
     x.kind = TER_HIP_X_I8;
     x.scale_dev = scale_x_dev;
     return ter_hip_gemv(W, &x, out, nullptr, stream);
+}
+
+int ter_hip_mm_packed_dispatch_f16(const int8_t* X, const float* scale_x_dev, const ter_hip_wpk_t* W, uint16_t* out,
+                                   int32_t K, int32_t N, void* stream) {
+    if (!X || !scale_x_dev || !W || !out) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (W->K != K || W->N != N) return fail(TER_HIP_ERR_SHAPE, "K/N (%d,%d) do not match W (%d,%d)", K, N, W->K, W->N);
+    ter_hip_act_t x{};
+    x.data = X;
+    x.kind = TER_HIP_X_I8;
+    x.scale_dev = scale_x_dev;
+    const ter_hip_out_t o{nullptr, nullptr, out, nullptr};
+    return ter_hip_gemv_out(W, &x, &o, stream);
 }
 
 int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale, const ter_hip_wpk_t* W, int32_t N,
@@ -497,27 +584,34 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     long long tile = 0;
     uint64_t bytes = 0, macs = 0;
     int lds = 0;
+    Ranges resid, inputs;
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemv_item_t& it = items[i];
         int rc = check_wpk(it.w);
         if (rc) return rc;
         rc = check_act(&it.x, 1);
         if (rc) return rc;
-        if (!it.y && !it.acc) return fail(TER_HIP_ERR_NULL, "item %d has no output", i);
+        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid};
+        rc = check_out(&o);
+        if (rc) return rc;
         for (int k = 0; k < i; ++k)
             if (items[k].w->fix == it.w->fix)
                 return fail(TER_HIP_ERR_CONFLICT, "weight of item %d repeats item %d", i, k);
-        ds[(size_t)i] = make_desc(it.w, &it.x, it.y, it.acc, tile);
+        if (it.resid) resid.emplace_back((uintptr_t)it.resid, (uintptr_t)(it.resid + it.w->N));
+        act_ranges(&it.x, 1, it.w->K, &inputs);
+        ds[(size_t)i] = make_desc(it.w, &it.x, o, tile);
         starts[(size_t)i] = tile;
         tile += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
         const int lb = gemv_lds_bytes(it.w->K);
         if (lb > lds) lds = lb;
-        bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 +
-                 (uint64_t)it.w->K * (it.x.kind == TER_HIP_X_F32 ? 4u : 1u) + (uint64_t)it.w->N * 4u;
+        bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.w->K * act_bytes(it.x.kind) +
+                 (uint64_t)it.w->N * out_bytes(o);
         macs += (uint64_t)it.w->K * (uint64_t)it.w->N;
     }
+    int rc = check_resid_overlap(resid, inputs);
+    if (rc) return rc;
     int n_wg = 0;
-    int rc = pick_wg(tile, wg_per_cu, lds, &n_wg);
+    rc = pick_wg(tile, wg_per_cu, lds, &n_wg);
     if (rc) return rc;
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
@@ -582,9 +676,23 @@ int ter_hip_rmsnorm_quant(const void* x, int32_t kind, const uint16_t* gamma, fl
     if (!aligned(x, kind == TER_HIP_X_F32_RMS ? 4 : 2) || !aligned(gamma, 2))
         return fail(TER_HIP_ERR_ALIGN, "x or gamma misaligned");
     if (!(eps >= 0.f)) return fail(TER_HIP_ERR_SHAPE, "RMSNorm eps must be >= 0");
-    hipError_t e = launch_rmsnorm_quant_rows(x, kind == TER_HIP_X_F16_RMS, gamma, eps, M, K, q, scale_out,
+    if (kind == TER_HIP_X_RELU2_RMS) return fail(TER_HIP_ERR_PAYLOAD, "relu2 rows: use ter_hip_relu2_rmsnorm_quant");
+    hipError_t e = launch_rmsnorm_quant_rows(x, nullptr, kind, gamma, eps, M, K, q, scale_out,
                                              static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "rmsnorm quant launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_relu2_rmsnorm_quant(const uint16_t* gate, const uint16_t* up, const uint16_t* gamma, float eps, int32_t M,
+                                int32_t F, int8_t* q, float* scale_out, void* stream) {
+    if (!gate || !up || !gamma || !q || !scale_out) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (M < 1 || F < 1 || F > TER_HIP_K_MAX || M > 65535) return fail(TER_HIP_ERR_SHAPE, "M=%d F=%d out of range", M, F);
+    if (!aligned(gate, 2) || !aligned(up, 2) || !aligned(gamma, 2))
+        return fail(TER_HIP_ERR_ALIGN, "gate, up or gamma misaligned");
+    if (!(eps >= 0.f)) return fail(TER_HIP_ERR_SHAPE, "RMSNorm eps must be >= 0");
+    hipError_t e = launch_rmsnorm_quant_rows(gate, up, TER_HIP_X_RELU2_RMS, gamma, eps, M, F, q, scale_out,
+                                             static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "relu2 rmsnorm quant launch");
     return TER_HIP_OK;
 }
 
@@ -598,28 +706,45 @@ int ter_hip_quant_int8(const float* x, int32_t M, int32_t K, int8_t* q, float* s
 }
 
 int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, float* y, int32_t* acc, void* stream) {
+    const ter_hip_out_t o{y, acc, nullptr, nullptr};
+    return ter_hip_gemm_out(w, x, M, &o, stream);
+}
+
+int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, const ter_hip_out_t* out,
+                     void* stream) {
     int rc = check_wpk(w);
     if (rc) return rc;
     if (M < 1 || M > TER_HIP_M_MAX) return fail(TER_HIP_ERR_SHAPE, "M=%d out of range [1,%d]", M, TER_HIP_M_MAX);
     rc = check_act(x, M);
     if (rc) return rc;
-    if (!y && !acc) return fail(TER_HIP_ERR_NULL, "no output buffer");
+    rc = check_out(out);
+    if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int8_t* xq = static_cast<const int8_t*>(x->data);
     const float* xs = x->scale_dev;
+    if (out->resid) {  // the GEMM reads int8 rows: X itself or the q_out workspace
+        const int8_t* xr = x->kind == TER_HIP_X_I8 ? xq : x->q_out;
+        const size_t mk = (size_t)M * (size_t)w->K;
+        rc = check_resid_overlap({{(uintptr_t)out->resid, (uintptr_t)(out->resid + (size_t)M * w->N)}},
+                                 {{(uintptr_t)xr, (uintptr_t)(xr + mk)}});
+        if (rc) return rc;
+    }
     if (x->kind != TER_HIP_X_I8) {
         if (!x->q_out || !x->scale_out)
             return fail(TER_HIP_ERR_NULL, "fp32/fp16 batched X needs q_out and scale_out workspaces");
-        rc = x->kind == TER_HIP_X_F32
-                 ? ter_hip_quant_int8(static_cast<const float*>(x->data), M, w->K, x->q_out, x->scale_out, stream)
-                 : ter_hip_rmsnorm_quant(x->data, x->kind, x->gamma, x->eps, M, w->K, x->q_out, x->scale_out,
-                                         stream);
+        if (x->kind == TER_HIP_X_F32)
+            rc = ter_hip_quant_int8(static_cast<const float*>(x->data), M, w->K, x->q_out, x->scale_out, stream);
+        else if (x->kind == TER_HIP_X_RELU2_RMS)
+            rc = ter_hip_relu2_rmsnorm_quant(static_cast<const uint16_t*>(x->data), x->up, x->gamma, x->eps, M, w->K,
+                                             x->q_out, x->scale_out, stream);
+        else
+            rc = ter_hip_rmsnorm_quant(x->data, x->kind, x->gamma, x->eps, M, w->K, x->q_out, x->scale_out, stream);
         if (rc) return rc;
         xq = x->q_out;
         xs = x->scale_out;
     }
     const int mb = gemm_mb_of(M);
-    const GemmDesc d = make_gemm_desc(w, xq, xs, M, y, acc, 0, kWaves * gemm_strips_per_wave(mb), 0);
+    const GemmDesc d = make_gemm_desc(w, xq, xs, M, *out, 0, kWaves * gemm_strips_per_wave(mb), 0);
     int n_wg = 0;
     hipError_t e;
     const int slds = gemm_stream_lds_bytes(M, w->K);
@@ -653,6 +778,7 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     uint64_t bytes = 0, macs = 0;
     int max_m = 1;
     bool vec = true;
+    Ranges resid, inputs;
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemm_item_t& it = items[i];
         int rc = check_wpk(it.w);
@@ -660,9 +786,14 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
         if (!it.x || !it.x_scale_dev) return fail(TER_HIP_ERR_NULL, "item %d: null X or X scales", i);
         if (it.M < 1 || it.M > TER_HIP_M_MAX)
             return fail(TER_HIP_ERR_SHAPE, "item %d: M=%d out of range [1,%d]", i, it.M, TER_HIP_M_MAX);
-        if (!it.y && !it.acc) return fail(TER_HIP_ERR_NULL, "item %d has no output", i);
+        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid};
+        rc = check_out(&o);
+        if (rc) return rc;
+        if (it.resid) resid.emplace_back((uintptr_t)it.resid, (uintptr_t)(it.resid + (size_t)it.M * it.w->N));
+        inputs.emplace_back((uintptr_t)it.x, (uintptr_t)(it.x + (size_t)it.M * it.w->K));
         if (it.M > max_m) max_m = it.M;
     }
+    if (int rc = check_resid_overlap(resid, inputs)) return rc;
     const int mb = gemm_mb_of(max_m);  // one row-block count (and block width) per launch
     const int per_block = kWaves * gemm_strips_per_wave(mb);
     long long tiles = 0;
@@ -670,14 +801,16 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     std::vector<long long> block_starts((size_t)n), tile_starts((size_t)n);
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemm_item_t& it = items[i];
-        ds[(size_t)i] = make_gemm_desc(it.w, it.x, it.x_scale_dev, it.M, it.y, it.acc, blocks, per_block, tiles);
+        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid};
+        ds[(size_t)i] = make_gemm_desc(it.w, it.x, it.x_scale_dev, it.M, o, blocks, per_block, tiles);
         block_starts[(size_t)i] = blocks;
         tile_starts[(size_t)i] = tiles;
         blocks += ds[(size_t)i].n_blocks;
         tiles += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
         if (it.w->K > max_k) max_k = it.w->K;
         vec = vec && gemm_vec_ok(ds[(size_t)i]);
-        bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.M * it.w->K + (uint64_t)it.M * it.w->N * 4u;
+        bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.M * it.w->K +
+                 (uint64_t)it.M * it.w->N * out_bytes(o);
         macs += (uint64_t)it.M * (uint64_t)it.w->K * (uint64_t)it.w->N;
     }
     int n_wg = 0;

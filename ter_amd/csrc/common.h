@@ -43,13 +43,16 @@ inline size_t fix_offset(int32_t K, int32_t N) { return tile_stream_bytes(K, N);
 // One GEMV of a work list, as the kernel reads it (device memory or kernarg).
 struct alignas(16) GemvDesc {
     const uint8_t* w;            // T16 tile stream
-    const void* x;               // int8 [K], fp32 [K] or fp16 [K] (x_kind)
+    const void* x;               // int8 [K], fp32 [K] or fp16 [K] (x_kind; the gate for X_RELU2_RMS)
     const float* x_scale_dev;    // int8 input: device activation scale or null
     float* y;                    // fp32 [N] or null
     int32_t* acc;                // int32 [N] or null
     int8_t* xq_out;              // quantized input: int8 X copy or null
     float* xs_out;               // quantized input: activation scale copy or null
     const uint16_t* gamma;       // RMS kinds: fp16 RMSNorm weights [K]
+    const uint16_t* up;          // X_RELU2_RMS: fp16 up projection [K]
+    uint16_t* y16;               // fp16 [N] = half(y) or null
+    float* resid;                // fp32 [N]: resid += float(half(y)), or null
     unsigned long long* fix;     // N fix-up slots, zero at rest
     long long tile0;             // first tile of this GEMV in the launch's stream
     int32_t K, N, Ku, n_strips;
@@ -66,6 +69,8 @@ struct alignas(16) GemmDesc {
     const float* xs;             // per-row activation scales [M] (device)
     float* y;                    // fp32 [M][N] or null
     int32_t* acc;                // int32 [M][N] or null
+    uint16_t* y16;               // fp16 [M][N] = half(y) or null
+    float* resid;                // fp32 [M][N]: resid += float(half(y)), or null
     long long block0;            // first block (unit-major kernel)
     long long tile0;             // first tile in the launch's tile stream (streaming kernel)
     int32_t K, N, Ku, n_strips;
@@ -86,9 +91,10 @@ hipError_t launch_synth_v11(uint8_t* v11, int K, int N, uint64_t seed, uint32_t 
                             hipStream_t st);
 hipError_t launch_synth_i8(int8_t* x, long long n, uint64_t seed, int lo, int hi, hipStream_t st);
 hipError_t launch_quant_rows(const float* x, int M, int K, int8_t* q, float* s, hipStream_t st);
-// One workgroup of 256 threads per row; f16 selects fp16 input.
-hipError_t launch_rmsnorm_quant_rows(const void* x, bool f16, const uint16_t* gamma, float eps, int M, int K,
-                                     int8_t* q, float* s, hipStream_t st);
+// One workgroup of 256 threads per row; kind is TER_HIP_X_F32_RMS,
+// TER_HIP_X_F16_RMS or TER_HIP_X_RELU2_RMS (x = gate, up [M][K]).
+hipError_t launch_rmsnorm_quant_rows(const void* x, const uint16_t* up, int kind, const uint16_t* gamma, float eps,
+                                     int M, int K, int8_t* q, float* s, hipStream_t st);
 // Rows per MFMA row block group: MB = 1, 2, 4, 8, 16 for M up to 16, 32, 64, 128, 256.
 int gemm_mb_of(int M);
 // vec: every x pointer 16-byte aligned and every ldx a multiple of 16.
@@ -124,8 +130,48 @@ hipError_t launch_gemm_lds(const GemmDesc& single, const GemmDesc* list_dev, con
 int gemm_strips_per_wave(int mb);
 
 #if defined(__HIPCC__)
+#define TER_GLOBAL __attribute__((address_space(1)))
+
+// Generic -> global address space, so accesses compile to global_* / buffer
+// instructions (flat ones also count against the LDS wait counter).
+template <typename T>
+__device__ __forceinline__ TER_GLOBAL T* gptr(T* p) {
+    return (TER_GLOBAL T*)p;
+}
+
 __device__ inline float half_bits_to_float(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);  // exact widening
+}
+
+// binary32 -> binary16 in the default round-to-nearest-even mode (the
+// reference's __float2half of its fp16 outputs); overflow gives inf.
+__device__ inline uint16_t float_to_half_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+// Output element o of a GEMV / GEMM (GemvDesc or GemmDesc): acc, y =
+// float(acc) * s, y16 = half(y) (the reference's __float2half projection
+// output), resid += float(half(y)) (its add_k_f32 residual step).
+template <class D>
+__device__ __forceinline__ void emit_out(const D& d, long long o, int val, float s) {
+#pragma clang fp contract(off)
+    if (d.acc) gptr(d.acc)[o] = val;
+    const float y = (float)val * s;
+    if (d.y) gptr(d.y)[o] = y;
+    if (d.y16 || d.resid) {
+        const uint16_t h = float_to_half_bits(y);
+        if (d.y16) gptr(d.y16)[o] = h;
+        if (d.resid) gptr(d.resid)[o] = gptr(d.resid)[o] + half_bits_to_float(h);
+    }
+}
+
+// relu^2(gate) * up of relu2_mul_rmsnorm_quant_k
+// (cuda/ter_cuda_forward_bitnet.cu:273-276): the square rounds first, then
+// the product.
+__device__ inline float relu2_mul(float g, float u) {
+#pragma clang fp contract(off)
+    const float r = g > 0.f ? g * g : 0.f;
+    return r * u;
 }
 
 // Sum of one value per thread of a 256-thread block, paired exactly as the
@@ -149,6 +195,36 @@ __device__ inline float tree_sum256(float v, float* red) {
     const float r = red[0];
     __syncthreads();  // red may be reused
     return r;
+}
+
+// Sum of squares of v = relu2_mul(gate, up) over K elements in the order of
+// a 1024-thread block (relu2_mul_rmsnorm_quant_k,
+// cuda/ter_cuda_forward_bitnet.cu:270-284), computed by 256 threads: thread t
+// keeps the strided partials of virtual threads t, t+256, t+512, t+768
+// (fused multiply-adds), performs the tree's levels 512 and 256 itself, then
+// tree_sum256 does 128 .. 1.
+__device__ inline float relu2_sum_sq_1024(const uint16_t* gate, const uint16_t* up, int K, float* red) {
+    const int t = threadIdx.x;
+    float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+    for (int i = t; i < K; i += 1024) {
+        float v = relu2_mul(half_bits_to_float(gptr(gate)[i]), half_bits_to_float(gptr(up)[i]));
+        p0 = __builtin_fmaf(v, v, p0);
+        if (i + 256 < K) {
+            v = relu2_mul(half_bits_to_float(gptr(gate)[i + 256]), half_bits_to_float(gptr(up)[i + 256]));
+            p1 = __builtin_fmaf(v, v, p1);
+        }
+        if (i + 512 < K) {
+            v = relu2_mul(half_bits_to_float(gptr(gate)[i + 512]), half_bits_to_float(gptr(up)[i + 512]));
+            p2 = __builtin_fmaf(v, v, p2);
+        }
+        if (i + 768 < K) {
+            v = relu2_mul(half_bits_to_float(gptr(gate)[i + 768]), half_bits_to_float(gptr(up)[i + 768]));
+            p3 = __builtin_fmaf(v, v, p3);
+        }
+    }
+    p0 = p0 + p2;
+    p1 = p1 + p3;
+    return tree_sum256(p0 + p1, red);
 }
 
 #endif

@@ -35,12 +35,6 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-#define TER_GLOBAL __attribute__((address_space(1)))
-
-template <typename T>
-__device__ __forceinline__ TER_GLOBAL T* gptr(T* p) {
-    return (TER_GLOBAL T*)p;
-}
 
 __device__ __forceinline__ int row_sum16(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
@@ -237,8 +231,7 @@ __global__ __launch_bounds__(kThreads) void gemm_t16_kernel(GemmDesc single, con
                         if (row < d.M) {
                             const int val = C[s][mb][e] - rsum[row];
                             const long long o = (long long)row * d.N + col;
-                            if (d.acc) gptr(d.acc)[o] = val;
-                            if (d.y) gptr(d.y)[o] = (float)val * (gptr(d.xs)[row] * d.w_scale);
+                            emit_out(d, o, val, gptr(d.xs)[row] * d.w_scale);
                         }
                     }
                 }
@@ -319,8 +312,7 @@ __device__ __forceinline__ void stream_compute(const GemmDesc& d, const unsigned
                         if (row < d.M) {
                             const int val = p.C[e] - rsum[row];
                             const long long o = (long long)row * d.N + col;
-                            if (d.acc) gptr(d.acc)[o] = val;
-                            if (d.y) gptr(d.y)[o] = (float)val * xsr[e];
+                            emit_out(d, o, val, xsr[e]);
                         }
                     }
                 }

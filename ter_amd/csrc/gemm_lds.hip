@@ -41,13 +41,7 @@ namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-#define TER_GLOBAL __attribute__((address_space(1)))
 #define TER_LDS __attribute__((address_space(3)))
-
-template <typename T>
-__device__ __forceinline__ TER_GLOBAL T* gptr(T* p) {
-    return (TER_GLOBAL T*)p;
-}
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -290,8 +284,7 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
                             if (col < d.N) {
                                 const long long o = (long long)row * d.N + col;
                                 const int val = acc[s][mb][e];
-                                if (d.acc) gptr(d.acc)[o] = val;
-                                if (d.y) gptr(d.y)[o] = (float)val * sc;
+                                emit_out(d, o, val, sc);
                             }
                         }
                     }

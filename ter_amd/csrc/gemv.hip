@@ -39,14 +39,6 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-#define TER_GLOBAL __attribute__((address_space(1)))
-
-// Generic -> global address space, so accesses compile to global_* / buffer
-// instructions (flat ones also count against the LDS wait counter).
-template <typename T>
-__device__ __forceinline__ TER_GLOBAL T* gptr(T* p) {
-    return (TER_GLOBAL T*)p;
-}
 
 constexpr int kBatch = 6;  // tiles per batch; two batches per wave in flight
 
@@ -177,10 +169,36 @@ __device__ __forceinline__ void load_h16(const uint16_t* xh, int k, int K, float
     }
 }
 
-// 16 activations of an fp32-family input (fp32, or fp16 for X_F16_RMS) as fp32.
+// relu^2(gate) * up on 16 elements at k (zeros past K).
+__device__ __forceinline__ void load_relu2_16(const uint16_t* g, const uint16_t* u, int k, int K, float (&v)[16]) {
+    if ((((reinterpret_cast<uintptr_t>(g + k) | reinterpret_cast<uintptr_t>(u + k)) & 15u) == 0) && k + 16 <= K) {
+        const TER_GLOBAL u32x4* pg = gptr(reinterpret_cast<const u32x4*>(g + k));
+        const TER_GLOBAL u32x4* pu = gptr(reinterpret_cast<const u32x4*>(u + k));
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const u32x4 gw = pg[i], uw = pu[i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                v[8 * i + 2 * j] = relu2_mul(half_bits_to_float((uint16_t)(gw[j] & 0xFFFFu)),
+                                             half_bits_to_float((uint16_t)(uw[j] & 0xFFFFu)));
+                v[8 * i + 2 * j + 1] = relu2_mul(half_bits_to_float((uint16_t)(gw[j] >> 16)),
+                                                 half_bits_to_float((uint16_t)(uw[j] >> 16)));
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            v[i] = k + i < K ? relu2_mul(half_bits_to_float(gptr(g)[k + i]), half_bits_to_float(gptr(u)[k + i])) : 0.f;
+    }
+}
+
+// 16 activations of an fp32-family input (fp32, fp16 for X_F16_RMS, or
+// relu^2(gate) * up for X_RELU2_RMS) as fp32.
 __device__ __forceinline__ void load_x16f(const GemvDesc& d, int k, float (&v)[16]) {
     if (d.x_kind == TER_HIP_X_F16_RMS) {
         load_h16(static_cast<const uint16_t*>(d.x), k, d.K, v);
+    } else if (d.x_kind == TER_HIP_X_RELU2_RMS) {
+        load_relu2_16(static_cast<const uint16_t*>(d.x), d.up, k, d.K, v);
     } else {
         const float* xf = static_cast<const float*>(d.x);
         load_f16(xf, k, d.K, (reinterpret_cast<uintptr_t>(xf) & 15u) == 0, v);
@@ -188,8 +206,9 @@ __device__ __forceinline__ void load_x16f(const GemvDesc& d, int k, float (&v)[1
 }
 
 __device__ __forceinline__ float x_at(const GemvDesc& d, int i) {
-    return d.x_kind == TER_HIP_X_F16_RMS ? half_bits_to_float(gptr(static_cast<const uint16_t*>(d.x))[i])
-                                         : gptr(static_cast<const float*>(d.x))[i];
+    if (d.x_kind == TER_HIP_X_F32_RMS) return gptr(static_cast<const float*>(d.x))[i];
+    const float h = half_bits_to_float(gptr(static_cast<const uint16_t*>(d.x))[i]);
+    return d.x_kind == TER_HIP_X_F16_RMS ? h : relu2_mul(h, half_bits_to_float(gptr(d.up)[i]));
 }
 
 // RMSNorm of the RMS kinds: n = (x * rms_inv) * gamma on 16 values at k.
@@ -224,7 +243,9 @@ __device__ __forceinline__ void x_prefetch(const GemvDesc& d, XPre& r) {
 // rmsnorm_quant_{f32,fp16}_in_k (cuda/ter_cuda_forward_bitnet.cu:64-146):
 // strided per-thread sums of squares (fused multiply-adds) reduced in the
 // reference's tree order, rms_inv = 1 / sqrt(ss / K + eps) correctly rounded,
-// x <- (x * rms_inv) * gamma.  `owner` (the workgroup that starts the GEMV)
+// x <- (x * rms_inv) * gamma.  X_RELU2_RMS is relu2_mul_rmsnorm_quant_k
+// (cuda/ter_cuda_forward_bitnet.cu:258-309): x = relu^2(gate) * up and the
+// sum of squares in its 1024-thread order.  `owner` (the workgroup that starts the GEMV)
 // also writes the optional copies xq_out / xs_out.
 __device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* usum, float* red, bool owner) {
 #pragma clang fp contract(off)
@@ -244,12 +265,18 @@ __device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* u
     const bool rms = d.x_kind != TER_HIP_X_F32;
     float rms_inv = 1.0f;
     if (rms) {
-        float part = 0.f;
-        for (int i = tid; i < K; i += kGemvThreads) {
-            const float v = x_at(d, i);
-            part = __builtin_fmaf(v, v, part);
+        float ss;
+        if (d.x_kind == TER_HIP_X_RELU2_RMS) {
+            ss = relu2_sum_sq_1024(static_cast<const uint16_t*>(d.x), d.up, K, red);
+        } else {
+            float part = 0.f;
+            for (int i = tid; i < K; i += kGemvThreads) {
+                const float v = x_at(d, i);
+                part = __builtin_fmaf(v, v, part);
+            }
+            ss = tree_sum256(part, red);
         }
-        rms_inv = 1.0f / __builtin_sqrtf(tree_sum256(part, red) / (float)K + d.eps);
+        rms_inv = 1.0f / __builtin_sqrtf(ss / (float)K + d.eps);
     }
     float v0[16], v1[16];
 #pragma unroll
@@ -306,11 +333,7 @@ __device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* u
     return act;
 }
 
-__device__ __forceinline__ void emit(const GemvDesc& d, int col, int val, float s) {
-#pragma clang fp contract(off)
-    if (d.acc) gptr(d.acc)[col] = val;
-    if (d.y) gptr(d.y)[col] = (float)val * s;
-}
+__device__ __forceinline__ void emit(const GemvDesc& d, int col, int val, float s) { emit_out(d, col, val, s); }
 
 // Accumulate 1 tile (16 bytes of this lane) into the 4 column accumulators.
 __device__ __forceinline__ void dot_tile(const u32x4& w, const u32x4& x, int (&a1)[4], int (&a4)[4]) {
@@ -427,6 +450,8 @@ struct Fixups {
     float s;
     float* y;
     int32_t* acc;
+    uint16_t* y16;
+    float* resid;
     unsigned long long* fix;
     int Ku;
 };
@@ -436,6 +461,8 @@ __device__ __forceinline__ void finish_fixups(const Fixups& f) {
     GemvDesc d{};
     d.y = f.y;
     d.acc = f.acc;
+    d.y16 = f.y16;
+    d.resid = f.resid;
     d.fix = f.fix;
     d.Ku = f.Ku;
     if (f.col_last >= 0) part_complete(d, f.col_last, f.o_last + f.w_last, f.s);
@@ -474,6 +501,8 @@ __device__ Fixups run_piece(const GemvDesc& d, const int8_t* lds_x, const int* u
     f.s = s;
     f.y = d.y;
     f.acc = d.acc;
+    f.y16 = d.y16;
+    f.resid = d.resid;
     f.fix = d.fix;
     f.Ku = d.Ku;
     if (p.u != p.u_start) {

@@ -180,7 +180,10 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const float* __restrict
 // reference build contracts `local_sum += v * v`), the reference's reduction
 // tree, rms_inv = 1 / sqrt(ss / K + eps) correctly rounded (the reference's
 // rsqrtf is an approximation), n = (x * rms_inv) * gamma, then quant_int8_k.
-__global__ __launch_bounds__(256) void rmsnorm_quant_rows_kernel(const void* __restrict__ x, int f16,
+// X_RELU2_RMS is relu2_mul_rmsnorm_quant_k (ibid.:258-309, one 1024-thread
+// block per row): x = relu^2(gate) * up and its 1024-strided sum order.
+__global__ __launch_bounds__(256) void rmsnorm_quant_rows_kernel(const void* __restrict__ x,
+                                                                 const uint16_t* __restrict__ up, int kind,
                                                                  const uint16_t* __restrict__ gamma, float eps,
                                                                  int K, int8_t* __restrict__ q,
                                                                  float* __restrict__ scale_out) {
@@ -189,15 +192,21 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_rows_kernel(const void* __r
     const int m = blockIdx.x, t = threadIdx.x;
     const long long row0 = (long long)m * K;
     auto xv = [&](int k) -> float {
-        return f16 ? half_bits_to_float(static_cast<const uint16_t*>(x)[row0 + k])
-                   : static_cast<const float*>(x)[row0 + k];
+        if (kind == TER_HIP_X_F32_RMS) return static_cast<const float*>(x)[row0 + k];
+        const float h = half_bits_to_float(static_cast<const uint16_t*>(x)[row0 + k]);
+        return kind == TER_HIP_X_F16_RMS ? h : relu2_mul(h, half_bits_to_float(up[row0 + k]));
     };
-    float part = 0.f;
-    for (int k = t; k < K; k += 256) {
-        const float v = xv(k);
-        part = __builtin_fmaf(v, v, part);
+    float ss;
+    if (kind == TER_HIP_X_RELU2_RMS) {
+        ss = relu2_sum_sq_1024(static_cast<const uint16_t*>(x) + row0, up + row0, K, red);
+    } else {
+        float part = 0.f;
+        for (int k = t; k < K; k += 256) {
+            const float v = xv(k);
+            part = __builtin_fmaf(v, v, part);
+        }
+        ss = tree_sum256(part, red);
     }
-    const float ss = tree_sum256(part, red);
     const float rms_inv = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
     float mx = 0.f;
     for (int k = t; k < K; k += 256) {
@@ -261,9 +270,10 @@ hipError_t launch_synth_i8(int8_t* x, long long n, uint64_t seed, int lo, int hi
     return hipGetLastError();
 }
 
-hipError_t launch_rmsnorm_quant_rows(const void* x, bool f16, const uint16_t* gamma, float eps, int M, int K,
+hipError_t launch_rmsnorm_quant_rows(const void* x, const uint16_t* up, int kind, const uint16_t* gamma, float eps,
+                                     int M, int K,
                                      int8_t* q, float* s, hipStream_t st) {
-    hipLaunchKernelGGL(rmsnorm_quant_rows_kernel, dim3(M), dim3(256), 0, st, x, f16 ? 1 : 0, gamma, eps, K, q, s);
+    hipLaunchKernelGGL(rmsnorm_quant_rows_kernel, dim3(M), dim3(256), 0, st, x, up, kind, gamma, eps, K, q, s);
     return hipGetLastError();
 }
 

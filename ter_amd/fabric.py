@@ -119,15 +119,22 @@ class PackedTrits:
         return out
 
 
-def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=None, eps=1e-5) -> L.Act:
+def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=None, eps=1e-5, up=None) -> L.Act:
     torch = _torch()
     a = L.Act()
     a.data = x.data_ptr()
+    if up is not None and gamma is None:
+        raise TypeError("up (relu^2(gate) * up activations) needs gamma")
     if gamma is not None:
         # fused RMSNorm (fp16 gamma) + absmax quantization in the prologue
         if gamma.dtype != torch.float16 or not gamma.is_cuda:
             raise TypeError("gamma must be a CUDA float16 tensor")
-        if x.dtype == torch.float32:
+        if up is not None:
+            if x.dtype != torch.float16 or up.dtype != torch.float16 or not up.is_cuda or up.shape != x.shape:
+                raise TypeError("relu^2 activations: gate and up must be CUDA float16 tensors of one shape")
+            a.kind = L.X_RELU2_RMS
+            a.up = up.data_ptr()
+        elif x.dtype == torch.float32:
             a.kind = L.X_F32_RMS
         elif x.dtype == torch.float16:
             a.kind = L.X_F16_RMS
@@ -150,18 +157,32 @@ def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=No
     return a
 
 
+def _out(y, acc, y16, resid) -> L.Out:
+    o = L.Out()
+    o.y, o.acc, o.y16, o.resid = _ptr(y), _ptr(acc), _ptr(y16), _ptr(resid)
+    return o
+
+
 def gemv(W: PackedTrits, x, y=None, acc=None, x_scale: Optional[float] = None, x_scale_dev=None,
-         q_out=None, scale_out=None, gamma=None, eps: float = 1e-5, stream=None):
+         q_out=None, scale_out=None, gamma=None, eps: float = 1e-5, up=None, y16=None, resid=None, stream=None):
     """M = 1 GEMV.  x: int8 [K] (with x_scale or x_scale_dev) or fp32 [K]
     (absmax-quantized in the kernel prologue); with gamma (fp16 [K]), x fp32 or
-    fp16 is RMS-normalized first (rmsnorm_quant_*_in_k steps).  Returns (y, acc)."""
+    fp16 is RMS-normalized first (rmsnorm_quant_*_in_k steps), and with up as
+    well, x is the fp16 gate and the prologue is relu2_mul_rmsnorm_quant_k.
+    Outputs: y fp32, acc int32, y16 fp16 = half(y), resid fp32 += half(y);
+    y is allocated when none is given.  Returns (y, acc)."""
     torch = _torch()
     _require_cuda(x, "x", None, W.K)
-    if y is None and acc is None:
+    if y is None and acc is None and y16 is None and resid is None:
         y = torch.empty(W.N, dtype=torch.float32, device=x.device)
-    a = _act(x, x_scale, x_scale_dev, q_out, scale_out, gamma, eps)
-    L.check(L.lib().ter_hip_gemv(C.byref(W.wpk), C.byref(a), _ptr(y), _ptr(acc), _stream(stream)),
-            "ter_hip_gemv")
+    a = _act(x, x_scale, x_scale_dev, q_out, scale_out, gamma, eps, up)
+    if y16 is None and resid is None:
+        L.check(L.lib().ter_hip_gemv(C.byref(W.wpk), C.byref(a), _ptr(y), _ptr(acc), _stream(stream)),
+                "ter_hip_gemv")
+    else:
+        o = _out(y, acc, y16, resid)
+        L.check(L.lib().ter_hip_gemv_out(C.byref(W.wpk), C.byref(a), C.byref(o), _stream(stream)),
+                "ter_hip_gemv_out")
     return y, acc
 
 
@@ -175,6 +196,19 @@ def mm_packed_dispatch(X, scale_x_dev, W: PackedTrits, out, K: int, N: int, stre
     L.check(L.lib().ter_hip_mm_packed_dispatch(X.data_ptr(), scale_x_dev.data_ptr(), C.byref(W.wpk),
                                                out.data_ptr(), int(K), int(N), _stream(stream)),
             "ter_hip_mm_packed_dispatch")
+    return out
+
+
+def mm_packed_dispatch_f16(X, scale_x_dev, W: PackedTrits, out, K: int, N: int, stream=None):
+    """The reference launcher with its own output type: fp16 out[N] =
+    __float2half((float)acc * scale) (cuda/ter_cuda_forward_packed.cu:493-500)."""
+    torch = _torch()
+    _require_cuda(X, "X", torch.int8, K)
+    _require_cuda(scale_x_dev, "scale_x_dev", torch.float32, 1)
+    _require_cuda(out, "out", torch.float16, N)
+    L.check(L.lib().ter_hip_mm_packed_dispatch_f16(X.data_ptr(), scale_x_dev.data_ptr(), C.byref(W.wpk),
+                                                   out.data_ptr(), int(K), int(N), _stream(stream)),
+            "ter_hip_mm_packed_dispatch_f16")
     return out
 
 
@@ -227,32 +261,59 @@ def rmsnorm_quant(x, gamma, eps: float = 1e-5, q=None, scale_out=None, stream=No
     return q, scale_out
 
 
+def relu2_rmsnorm_quant(gate, up, gamma, eps: float = 1e-5, q=None, scale_out=None, stream=None):
+    """Per-row fused relu^2(gate) * up + RMSNorm + int8 quantization
+    (relu2_mul_rmsnorm_quant_k, cuda/ter_cuda_forward_bitnet.cu:258-309) of fp16
+    gate, up [M][F] with fp16 gamma [F].  Returns (q int8 [M][F], scale_out fp32 [M])."""
+    torch = _torch()
+    g2, u2 = gate.reshape(-1, gate.shape[-1]), up.reshape(-1, up.shape[-1])
+    M, F = g2.shape
+    if gate.dtype != torch.float16 or up.dtype != torch.float16 or u2.shape != g2.shape:
+        raise TypeError("gate and up must be float16 tensors of one shape")
+    if gamma.dtype != torch.float16 or gamma.numel() != F:
+        raise TypeError("gamma must be float16 [F]")
+    if q is None:
+        q = torch.empty((M, F), dtype=torch.int8, device=gate.device)
+    if scale_out is None:
+        scale_out = torch.empty(M, dtype=torch.float32, device=gate.device)
+    L.check(L.lib().ter_hip_relu2_rmsnorm_quant(g2.data_ptr(), u2.data_ptr(), gamma.data_ptr(), C.c_float(eps), M, F,
+                                                q.data_ptr(), scale_out.data_ptr(), _stream(stream)),
+            "ter_hip_relu2_rmsnorm_quant")
+    return q, scale_out
+
+
 def mm_batched(W: PackedTrits, X, y=None, acc=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=None,
-               eps: float = 1e-5, stream=None):
+               eps: float = 1e-5, up=None, y16=None, resid=None, stream=None):
     """M > 1 GEMM on MFMA.  X: int8 [M][K] with per-row device scales
     x_scale_dev [M], or fp32 [M][K] (rows quantized into q_out/scale_out,
     allocated here when absent); with gamma (fp16 [K]) the fp32 or fp16 rows
-    are RMS-normalized first.  Returns (y [M][N], acc [M][N] or None)."""
+    are RMS-normalized first, with up as well X is the fp16 gate of the
+    relu^2 prologue.  Outputs as gemv, [M][N] each.  Returns (y, acc)."""
     torch = _torch()
     _require_cuda(X, "X")
     M = X.shape[0]
-    if y is None and acc is None:
+    if y is None and acc is None and y16 is None and resid is None:
         y = torch.empty((M, W.N), dtype=torch.float32, device=X.device)
     if X.dtype in (torch.float32, torch.float16):
         if q_out is None:
             q_out = torch.empty((M, W.K), dtype=torch.int8, device=X.device)
         if scale_out is None:
             scale_out = torch.empty(M, dtype=torch.float32, device=X.device)
-    a = _act(X, None, x_scale_dev, q_out, scale_out, gamma, eps)
-    L.check(L.lib().ter_hip_gemm(C.byref(W.wpk), C.byref(a), int(M), _ptr(y), _ptr(acc), _stream(stream)),
-            "ter_hip_gemm")
+    a = _act(X, None, x_scale_dev, q_out, scale_out, gamma, eps, up)
+    if y16 is None and resid is None:
+        L.check(L.lib().ter_hip_gemm(C.byref(W.wpk), C.byref(a), int(M), _ptr(y), _ptr(acc), _stream(stream)),
+                "ter_hip_gemm")
+    else:
+        o = _out(y, acc, y16, resid)
+        L.check(L.lib().ter_hip_gemm_out(C.byref(W.wpk), C.byref(a), int(M), C.byref(o), _stream(stream)),
+                "ter_hip_gemm_out")
     return y, acc
 
 
 class Plan:
     """Many independent GEMVs in one launch (one work list).  `items` is a
-    sequence of dicts: {w: PackedTrits, x: tensor, y?, acc?, x_scale?,
-    x_scale_dev?, q_out?, scale_out?}."""
+    sequence of dicts: {w: PackedTrits, x: tensor, y?, acc?, y16?, resid?,
+    x_scale?, x_scale_dev?, q_out?, scale_out?, gamma?, eps?, up?}."""
 
     def __init__(self, items: Sequence[dict], wg_per_cu: int = 0):
         n = len(items)
@@ -262,9 +323,11 @@ class Plan:
             W = it["w"]
             arr[i].w = C.pointer(W.wpk)
             arr[i].x = _act(it["x"], it.get("x_scale"), it.get("x_scale_dev"), it.get("q_out"), it.get("scale_out"),
-                            it.get("gamma"), it.get("eps", 1e-5))
+                            it.get("gamma"), it.get("eps", 1e-5), it.get("up"))
             arr[i].y = _ptr(it.get("y"))
             arr[i].acc = _ptr(it.get("acc"))
+            arr[i].y16 = _ptr(it.get("y16"))
+            arr[i].resid = _ptr(it.get("resid"))
             self._keep.append(W)
         h = C.c_void_p()
         L.check(L.lib().ter_hip_plan_create(C.byref(h), arr, n, int(wg_per_cu)), "ter_hip_plan_create")
@@ -291,7 +354,8 @@ class Plan:
 class GemmPlan:
     """Many independent M > 1 GEMMs in one launch.  `items` is a sequence of
     dicts {w: PackedTrits, x: int8 [M][K] tensor, x_scale_dev: fp32 [M]
-    tensor, y?: fp32 [M][N], acc?: int32 [M][N]}."""
+    tensor, y?: fp32 [M][N], acc?: int32 [M][N], y16?: fp16 [M][N],
+    resid?: fp32 [M][N]}."""
 
     def __init__(self, items: Sequence[dict], wg_per_cu: int = 0):
         n = len(items)
@@ -309,6 +373,8 @@ class GemmPlan:
             arr[i].M = int(x.shape[0])
             arr[i].y = _ptr(it.get("y"))
             arr[i].acc = _ptr(it.get("acc"))
+            arr[i].y16 = _ptr(it.get("y16"))
+            arr[i].resid = _ptr(it.get("resid"))
             self._keep.append(W)
         h = C.c_void_p()
         L.check(L.lib().ter_hip_gemm_plan_create(C.byref(h), arr, n, int(wg_per_cu)), "ter_hip_gemm_plan_create")

@@ -27,7 +27,7 @@ def declared_functions():
 
 def test_library_exports_every_declared_symbol():
     names = declared_functions()
-    assert len(names) == 27, names
+    assert len(names) == 31, names
     lib = L.lib()
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
@@ -105,6 +105,39 @@ def test_gemv_validation_without_device():
     assert lib.ter_hip_rmsnorm_quant(fake, L.X_F32_RMS, None, 1e-5, 1, 64, fake, fake, None) == L.ERR_NULL
     assert lib.ter_hip_rmsnorm_quant(fake, L.X_F32_RMS, fake, 1e-5, 0, 64, fake, fake, None) == L.ERR_SHAPE
     assert lib.ter_hip_rmsnorm_quant(fake, L.X_F32_RMS, fake, float("nan"), 1, 64, fake, fake, None) == L.ERR_SHAPE
+    # relu^2 kind: up required and 2-byte aligned, gate 2-byte aligned
+    x.kind, x.data, x.gamma, x.up = L.X_RELU2_RMS, fake, fake, None
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_NULL
+    x.up = fake + 1
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_ALIGN
+    x.up, x.data = fake, fake + 1
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_ALIGN
+    x.up, x.gamma = None, None
+    q = lib.ter_hip_relu2_rmsnorm_quant
+    assert q(None, fake, fake, 1e-5, 1, 64, fake, fake, None) == L.ERR_NULL
+    assert q(fake, fake, fake, 1e-5, 1, L.K_MAX + 1, fake, fake, None) == L.ERR_SHAPE
+    assert q(fake, fake + 1, fake, 1e-5, 1, 64, fake, fake, None) == L.ERR_ALIGN
+    assert q(fake, fake, fake, -1.0, 1, 64, fake, fake, None) == L.ERR_SHAPE
+    assert lib.ter_hip_rmsnorm_quant(fake, L.X_RELU2_RMS, fake, 1e-5, 1, 64, fake, fake, None) == L.ERR_PAYLOAD
+    # output forms: at least one, each aligned to its element
+    x.data, x.kind, x.scale_dev = fake, L.X_I8, fake
+    o = L.Out()
+    assert lib.ter_hip_gemv_out(C.byref(w), C.byref(x), C.byref(o), None) == L.ERR_NULL
+    assert lib.ter_hip_gemv_out(C.byref(w), C.byref(x), None, None) == L.ERR_NULL
+    o.y16 = fake + 1
+    assert lib.ter_hip_gemv_out(C.byref(w), C.byref(x), C.byref(o), None) == L.ERR_ALIGN
+    o.y16, o.resid = None, fake + 2
+    assert lib.ter_hip_gemv_out(C.byref(w), C.byref(x), C.byref(o), None) == L.ERR_ALIGN
+    # a residual output that overlaps the activation the launch reads
+    x.kind, x.data, x.gamma = L.X_F32_RMS, fake, fake << 2
+    o.resid = fake + 64
+    assert lib.ter_hip_gemv_out(C.byref(w), C.byref(x), C.byref(o), None) == L.ERR_CONFLICT
+    x.kind, x.gamma = L.X_I8, None
+    assert lib.ter_hip_gemm_out(C.byref(w), C.byref(x), 8, C.byref(o), None) == L.ERR_CONFLICT
+    o.resid = None
+    assert lib.ter_hip_gemm_out(C.byref(w), C.byref(x), 8, C.byref(L.Out()), None) == L.ERR_NULL
+    assert lib.ter_hip_mm_packed_dispatch_f16(fake, fake, C.byref(w), fake, 64, 32, None) == L.ERR_SHAPE
+    assert lib.ter_hip_mm_packed_dispatch_f16(fake, fake, C.byref(w), None, 64, 16, None) == L.ERR_NULL
     x.gamma, x.data, x.kind = None, fake, L.X_I8
     x.scale_dev = None
     # unknown layout tag
@@ -163,6 +196,15 @@ def test_plan_validation():
         it.x.kind = L.X_I8
         it.y = fake
     assert lib.ter_hip_plan_create(C.byref(h), items2, 2, 0) == L.ERR_CONFLICT  # same weight twice
+    # two weights whose residual outputs overlap (a plain read-modify-write each)
+    w2 = L.WPK()
+    assert lib.ter_hip_wpk_init(C.byref(w2), fake << 1, lib.ter_hip_wpk_bytes(64, 16), 64, 16, 1.0) == L.OK
+    items2[1].w = C.pointer(w2)
+    items2[0].y, items2[1].y = None, None
+    items2[0].resid, items2[1].resid = fake << 3, (fake << 3) + 4 * 15
+    assert lib.ter_hip_plan_create(C.byref(h), items2, 2, 0) == L.ERR_CONFLICT
+    items2[1].resid = fake + 8  # item 0 reads X at fake: item 1 must not add into it
+    assert lib.ter_hip_plan_create(C.byref(h), items2, 2, 0) == L.ERR_CONFLICT
 
 
 def test_gemm_plan_validation():
@@ -186,6 +228,8 @@ def test_gemm_plan_validation():
     items[0].M = 8
     items[0].y = None
     assert lib.ter_hip_gemm_plan_create(C.byref(h), items, 1, 0) == L.ERR_NULL  # no output
+    items[0].y16 = fake + 1
+    assert lib.ter_hip_gemm_plan_create(C.byref(h), items, 1, 0) == L.ERR_ALIGN
 
 
 def test_kernel_table_slots_and_codes():

@@ -295,3 +295,117 @@ def test_rmsnorm_quant_fp16_input_widens_exactly():
     a = O.rmsnorm_quant(x16, g, 1e-5)
     b = O.rmsnorm_quant(x16.astype(np.float32), g, 1e-5)
     assert (a[0] == b[0]).all() and a[1] == b[1] and a[2] == b[2]
+
+
+# ---------------------------------------------------------------------------
+# fp16 output rounding, fused relu^2 * up + RMSNorm + int8 quantizer
+# (relu2_mul_rmsnorm_quant_k, cuda/ter_cuda_forward_bitnet.cu:258-309) and the
+# residual add of fp16-rounded projections (add_k_f32, :51-54)
+# ---------------------------------------------------------------------------
+
+def test_float_to_half_matches_ieee_rounding():
+    """Every high half-word with low half-words that cover ties, just-below
+    and just-above ties for normals and subnormals, and random patterns."""
+    hi = np.arange(1 << 16, dtype=np.uint32) << 16
+    lows = np.array([0x0000, 0x0001, 0x0FFF, 0x1000, 0x1001, 0x1FFF, 0x2000, 0x3000,
+                     0x7FFF, 0x8000, 0x8001, 0xFFFF], dtype=np.uint32)
+    rng = np.random.default_rng(11)
+    lows = np.concatenate([lows, rng.integers(0, 1 << 16, 20, dtype=np.uint32)])
+    bits = (hi[:, None] | lows[None, :]).ravel()
+    f = bits.view(np.float32)
+    got = O.float_to_half_bits(f)
+    want = f.astype(np.float16).view(np.uint16)
+    nan = np.isnan(f)
+    assert (got[~nan] == want[~nan]).all()
+    assert ((got[nan] & 0x7C00) == 0x7C00).all() and ((got[nan] & 0x03FF) != 0).all()
+
+
+def test_relu2_rmsnorm_quant_constant_inputs():
+    """gate = 2, up = 0.75: v = 3 everywhere, the sum of squares is exactly
+    9 F, so rms_inv = 1 / sqrt(9 + eps) and q = 127 (or -127 for up < 0)."""
+    for F, u in ((6912, 0.75), (1024, -0.75), (300, 0.75)):
+        g = np.full(F, 2.0, np.float16)
+        up = np.full(F, u, np.float16)
+        q, s, r = O.relu2_rmsnorm_quant(g, up, np.ones(F, np.float16), 1e-5)
+        assert r == np.float32(1.0) / np.sqrt(np.float32(9.0) + np.float32(1e-5))
+        assert (q == (127 if u > 0 else -127)).all()
+
+
+def test_relu2_rmsnorm_quant_negative_gates_vanish():
+    """relu^2 keeps only positive gates: gate <= 0 (including -0) gives v = 0
+    whatever up holds, so those positions quantize to 0 and do not enter the
+    sum of squares."""
+    F = 2048
+    rng = np.random.default_rng(3)
+    g = rng.uniform(0.25, 2.0, F).astype(np.float16)
+    up = rng.standard_normal(F).astype(np.float16)
+    gm = rng.uniform(0.5, 1.5, F).astype(np.float16)
+    neg = rng.random(F) < 0.5
+    g2 = g.copy()
+    g2[neg] = -g2[neg]
+    g2[5] = np.float16(-0.0)
+    neg[5] = True
+    q, s, r = O.relu2_rmsnorm_quant(g2, up, gm, 1e-5)
+    assert (q[neg] == 0).all()
+    up2 = up.copy()
+    up2[neg] = 0
+    g3 = g.copy()
+    g3[5] = np.float16(1.0)
+    q3, s3, r3 = O.relu2_rmsnorm_quant(g3, up2, gm, 1e-5)
+    assert (q3 == q).all() and s3 == s and r3 == r
+
+
+def test_relu2_rmsnorm_quant_reduces_to_rmsnorm_for_small_rows():
+    """gate = 1, up = x (fp16): v = x exactly.  For F <= 256 the 1024-thread
+    tree only adds zeros above level 128, so the result equals the 256-thread
+    RMSNorm quantizer on the same row."""
+    rng = np.random.default_rng(4)
+    for F in (1, 37, 256):
+        x = rng.standard_normal(F).astype(np.float16)
+        gm = rng.uniform(0.5, 1.5, F).astype(np.float16)
+        a = O.relu2_rmsnorm_quant(np.ones(F, np.float16), x, gm, 1e-5)
+        b = O.rmsnorm_quant(x, gm, 1e-5)
+        assert (a[0] == b[0]).all() and a[1] == b[1] and a[2] == b[2]
+
+
+def test_relu2_rmsnorm_quant_summation_order():
+    """Pins the 1024 strided partials and the tree from s = 512: with
+    v[0]^2 = 2^24 (gate 64, up 1), v[256]^2 = v[768]^2 = 1 and zeros
+    elsewhere, the tree adds 1 + 1 before meeting 2^24 and gives 2^24 + 2,
+    whereas 256 strided partials lose each +1 to ties-to-even."""
+    F = 769
+    g = np.zeros(F, np.float16)
+    g[0], g[256], g[768] = 64.0, 1.0, 1.0
+    q, s, r = O.relu2_rmsnorm_quant(g, np.ones(F, np.float16), np.ones(F, np.float16), 0.0)
+    want = np.float32(1.0) / np.sqrt(np.float32(2.0 ** 24 + 2) / np.float32(F))
+    other = np.float32(1.0) / np.sqrt(np.float32(2.0 ** 24) / np.float32(F))
+    assert want != other  # the case distinguishes the two orders
+    assert r == want
+    assert q[0] == 127 and q[256] == q[768] == 0
+
+
+def test_relu2_rmsnorm_quant_power_of_two_invariance():
+    """eps = 0: gate * 2^k scales v by 4^k and the sum of squares by 16^k
+    exactly, so q and the activation scale are unchanged."""
+    rng = np.random.default_rng(6)
+    F = 6912
+    g = rng.uniform(-1.0, 2.0, F).astype(np.float16)
+    up = rng.standard_normal(F).astype(np.float16)
+    gm = rng.uniform(0.5, 1.5, F).astype(np.float16)
+    q0, s0, r0 = O.relu2_rmsnorm_quant(g, up, gm, 0.0)
+    for k in (-2, 1):
+        q1, s1, r1 = O.relu2_rmsnorm_quant((g.astype(np.float32) * 2.0 ** k).astype(np.float16), up, gm, 0.0)
+        assert (q1 == q0).all() and s1 == s0 and r1 == r0 * np.float32(4.0 ** -k)
+
+
+def test_residual_add_rounds_projection_to_half():
+    """hidden += float(half(y)), overflow to inf past 65520 included."""
+    rng = np.random.default_rng(8)
+    h = rng.standard_normal(4096).astype(np.float32)
+    y = (rng.standard_normal(4096) * 100).astype(np.float32)
+    y[:4] = [65519.0, 65520.0, -70000.0, 1e-8]
+    got = O.residual_add_f16(h, y)
+    with np.errstate(over="ignore"):
+        want = h + y.astype(np.float16).astype(np.float32)
+    assert (got.view(np.uint32) == want.view(np.uint32)).all()
+    assert got[1] == np.inf and got[2] == -np.inf
