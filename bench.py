@@ -433,6 +433,97 @@ def run_batched(args):
     }
 
 
+def run_lm_head(args):
+    """The decode step's tail on BitNet-2B's shapes (V = 128256, H = 2560,
+    fp16 tied token embedding, 656.7 MB per token): RMSNorm of the fp32
+    hidden state + fp16 lm_head GEMV + argmax as ONE launch
+    (ter_hip_lm_head_argmax), rotating over 2 embedding copies (1.3 GB, far
+    beyond the 256 MB Infinity Cache).  Also reported: the reference's
+    launch structure (norm, GEMV writing fp16 logits, argmax: 3 launches)."""
+    import numpy as np
+    import torch
+    import ter_amd as T
+    V, H = 128256, 2560
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2026)
+    E = [(torch.randn(V, H, generator=g, device="cuda") * 0.03).to(torch.float16) for _ in range(2)]
+    hidden = torch.randn(H, generator=g, device="cuda") * 4
+    gamma = (torch.rand(H, generator=g, device="cuda") + 0.5).to(torch.float16)
+    tok = torch.empty(1, dtype=torch.int32, device="cuda")
+    st = T.ArgmaxState()
+    fns = [lambda e=e: T.lm_head_argmax(hidden, gamma, e, 1e-5, token_out=tok, state=st) for e in E]
+    rot = graph_of(lambda: [f() for f in fns])
+    settle(rot.replay)
+    for _ in range(max(1, args.warmup // 2)):
+        rot.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_start = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps // 2):
+        rot.replay()
+    for i in range(args.steps % 2):
+        fns[i]()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t_start) * 1e3 / args.steps
+    ev_mean = e0.elapsed_time(e1) / args.steps
+    nbytes = V * H * 2 + H * 4 + H * 2 + 4
+    gbs = nbytes / (ev_mean * 1e-3) / 1e9
+    log(f"[bench] lm_head tail: {ev_mean * 1e3:.2f} us/launch (events), {gbs:.0f} GB/s")
+
+    # the reference's structure: rmsnorm_f32_in_k, mm_fp16_lm_head_k, argmax
+    xn = torch.empty(H, dtype=torch.float16, device="cuda")
+    lg = torch.empty(V, dtype=torch.float16, device="cuda")
+    st2 = T.ArgmaxState()
+
+    def three(e):
+        T.rmsnorm_f16(hidden, gamma, 1e-5, y=xn)
+        T.lm_head_f16(xn, e, logits=lg)
+        T.argmax_f16(lg, out_idx=tok, state=st2)
+    rot3 = graph_of(lambda: [three(e) for e in E])
+    _, ev3, _ = time_launches([rot3.replay], max(20, args.steps // 4), 4)
+    ev3 /= 2
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        xh = T.rmsnorm_f16(hidden, gamma, 1e-5).cpu().numpy().ravel()
+        rows = 2048
+        Eh = E[0][:rows].cpu().numpy()
+        want = T.lm_head_f16(torch.from_numpy(xh).cuda(), E[0][:rows]).cpu().numpy()
+        done, t_cpu = 0, 0.0
+        t_begin = time.perf_counter()
+        ok = True
+        while True:
+            t0 = time.perf_counter()
+            got, _ = O.lm_head_f16(xh, Eh)
+            t_cpu += time.perf_counter() - t0
+            done += rows
+            ok = ok and bool((got.view(np.uint16) == want.view(np.uint16)).all())
+            if time.perf_counter() - t_begin > args.cpu_seconds:
+                break
+        cpu = dict(value=round(done * H * 2 / t_cpu / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                   sample=f"oracle orc_lm_head_f16 (C restatement of mm_fp16_lm_head_k) on the first {rows} rows of "
+                          f"the table, {done // rows} passes, {t_cpu:.1f} s, 1 thread",
+                   matches_gpu_bitexact=ok)
+        log(f"[bench] cpu baseline: {cpu}")
+    return {
+        "metric": "decode tail: RMSNorm + fp16 lm_head GEMV + argmax, HBM GB/s",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "C5 tail: bitnet-b1.58-2b-4t lm_head tied to fp16 token_embd [128256][2560], "
+                               "one launch per token (norm + GEMV + argmax), 2 rotated table copies",
+                   "V": V, "H": H},
+        "three_launch_us": round(ev3 * 1e3, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic("lm_head_kernel", "bitnet_lm_head"),
+                     "kernel": "lm_head_kernel", "bytes_per_launch": nbytes, "mean_launch_us": round(ev_mean * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+
+
 def run_copy(args):
     """A plain copy-shaped kernel of known size (torch.neg over 256 MiB of
     fp32: 256 MiB read, 256 MiB written per launch).  Its rocprofv3
@@ -456,7 +547,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", choices=["llama", "bitnet", "batched", "copy"], default="llama")
+    ap.add_argument("--config", choices=["llama", "bitnet", "batched", "lm_head", "copy"], default="llama")
     ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
     ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -474,6 +565,8 @@ def main():
         out = run_batched(args)
     elif args.config == "copy":
         out = run_copy(args)
+    elif args.config == "lm_head":
+        out = run_lm_head(args)
     else:
         cfg = LLAMA if args.config == "llama" else BITNET
         out = run_m1(args, cfg, fp32_x=(args.config == "bitnet"))

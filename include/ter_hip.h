@@ -282,6 +282,42 @@ int ter_hip_relu2_rmsnorm_quant(const uint16_t* gate, const uint16_t* up, const 
                                 void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Decode-step tail: final RMSNorm, fp16 lm_head over the tied token       */
+/* embedding, argmax (cuda/ter_cuda_forward_bitnet.cu:890-911)             */
+/* ---------------------------------------------------------------------- */
+/* Per-row RMSNorm with fp16 output, the drop-in for rmsnorm_f32_in_k
+ * (cuda/ter_cuda_forward_bitnet.cu:37-47, <<<1,256>>> per row): x fp32 [M][H],
+ * gamma fp16 [H], y fp16 [M][H] = half((x * rms_inv) * gamma); the sum of
+ * squares and rms_inv as ter_hip_rmsnorm_quant. */
+int ter_hip_rmsnorm_f16(const float* x, const uint16_t* gamma, float eps, int32_t M, int32_t H,
+                        uint16_t* y, void* stream);
+/* fp16 lm_head GEMV, the drop-in for mm_fp16_lm_head_k
+ * (cuda/ter_cuda_forward_bitnet.cu:388-429): logits[v] = half(sum_k x[k] *
+ * token_embd[v][k]) in the reference's fp32 order (32 strided lane partials
+ * over fp16 pairs, then the xor butterfly).  token_embd fp16 [V][H] row-major;
+ * x, token_embd 4-byte aligned for even H. */
+int ter_hip_lm_head_f16(const uint16_t* x_norm, const uint16_t* token_embd, uint16_t* logits,
+                        int32_t H, int32_t V, void* stream);
+/* argmax of fp16 logits [N], the drop-in for argmax_local_k + argmax_final_k
+ * (cuda/ter_cuda_forward_bitnet.cu:454-495, 128 parts): the same index,
+ * ties included (among equal maxima the reference's two reduction trees
+ * decide: smallest bit-reversed part, then smallest bit-reversed thread,
+ * then the first element); NaN and -inf never win; -1 if nothing is
+ * eligible.  One launch.  `state`: 16 bytes of device memory, zero before
+ * the first call (hipMemset) and left zero by every call; calls that share a
+ * state must not overlap in time. */
+int ter_hip_argmax_f16(const uint16_t* logits, int32_t N, int32_t* out_idx, uint64_t* state,
+                       void* stream);
+/* The whole tail in ONE launch (rmsnorm_f32_in_k + mm_fp16_lm_head_k +
+ * argmax, :890-911): hidden fp32 [H] -> x_norm -> logits -> *token_out.
+ * x_norm_out (fp16 [H]) and logits_out (fp16 [V]) are optional copies;
+ * token_out and state (as ter_hip_argmax_f16) are required.  H even;
+ * hidden 8-byte and gamma 4-byte aligned. */
+int ter_hip_lm_head_argmax(const float* hidden, const uint16_t* gamma, float eps,
+                           const uint16_t* token_embd, int32_t H, int32_t V, uint16_t* x_norm_out,
+                           uint16_t* logits_out, int32_t* token_out, uint64_t* state, void* stream);
+
+/* ---------------------------------------------------------------------- */
 /* K4-style handle + KernelTable native slot                               */
 /* (include/ter_k4/ter_k4.h:29-55; include/ter/kernels.hpp:21-38)           */
 /* ---------------------------------------------------------------------- */

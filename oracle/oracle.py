@@ -68,6 +68,12 @@ def lib():
         L.orc_relu2_rmsnorm_quant.restype = None
         L.orc_residual_add_f16.argtypes = [_P, _P, C.c_int]
         L.orc_residual_add_f16.restype = None
+        L.orc_rmsnorm_f16.argtypes = [_P, _P, C.c_int, C.c_float, _P, _P]
+        L.orc_rmsnorm_f16.restype = None
+        L.orc_lm_head_f16.argtypes = [_P, _P, C.c_int, C.c_int, _P, _P]
+        L.orc_lm_head_f16.restype = None
+        L.orc_argmax_f16.argtypes = [_P, C.c_int]
+        L.orc_argmax_f16.restype = C.c_int
         L.orc_quantize_bitnet.argtypes = [_P, C.c_size_t, _P]
         L.orc_quantize_bitnet.restype = C.c_float
         L.orc_quantize_nt.argtypes = [_P, C.c_size_t, C.c_int, _P]
@@ -246,6 +252,35 @@ def residual_add_f16(hidden: np.ndarray, y: np.ndarray) -> np.ndarray:
     yy = np.ascontiguousarray(y, dtype=np.float32)
     lib().orc_residual_add_f16(_ptr(h), _ptr(yy), h.size)
     return h
+
+
+def rmsnorm_f16(x: np.ndarray, gamma: np.ndarray, eps: float = 1e-5):
+    """rmsnorm_f32_in_k (cuda/ter_cuda_forward_bitnet.cu:37-47): fp32 x [H],
+    fp16 gamma [H] -> (fp16 y [H], rms_inv)."""
+    xx = np.ascontiguousarray(x, dtype=np.float32)
+    gm = np.ascontiguousarray(gamma, dtype=np.float16)
+    y = np.empty(xx.size, dtype=np.uint16)
+    r = np.zeros(1, dtype=np.float32)
+    lib().orc_rmsnorm_f16(_ptr(xx), _ptr(gm), xx.size, C.c_float(eps), _ptr(y), _ptr(r))
+    return y.view(np.float16), r[0]
+
+
+def lm_head_f16(x: np.ndarray, emb: np.ndarray):
+    """mm_fp16_lm_head_k (cuda/ter_cuda_forward_bitnet.cu:388-429): fp16 x [H],
+    fp16 token_embd [V][H] -> (fp16 logits [V], fp32 pre-rounding values [V])."""
+    xx = np.ascontiguousarray(x, dtype=np.float16)
+    E = np.ascontiguousarray(emb, dtype=np.float16)
+    V, H = E.shape
+    lg = np.empty(V, dtype=np.uint16)
+    acc = np.empty(V, dtype=np.float32)
+    lib().orc_lm_head_f16(_ptr(xx), _ptr(E), H, V, _ptr(lg), _ptr(acc))
+    return lg.view(np.float16), acc
+
+
+def argmax_f16(logits: np.ndarray) -> int:
+    """argmax_local_k + argmax_final_k (cuda/ter_cuda_forward_bitnet.cu:454-495)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float16)
+    return int(lib().orc_argmax_f16(_ptr(lg), lg.size))
 
 
 def quantize_bitnet(x: np.ndarray):

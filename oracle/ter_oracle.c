@@ -35,6 +35,17 @@
  *                                           1024-thread order reduces to it,
  *                                           a summation-order case.
  *   orc_residual_add_f16                 -- orc_float_to_half / orc_half_to_float.
+ *   orc_rmsnorm_f16                      -- rms_inv equal to orc_rmsnorm_quant's (one
+ *                                           reference order), constant-input closed
+ *                                           form, fp16 rounding of the product.
+ *   orc_lm_head_f16                      -- exact integer dot products, a case
+ *                                           that separates the lane-strided order
+ *                                           and butterfly from a sequential sum,
+ *                                           odd H.
+ *   orc_argmax_f16                       -- numpy argmax on unique maxima; on
+ *                                           ties the closed-form rule of the
+ *                                           two reduction trees; NaN / -inf never
+ *                                           win; all ineligible gives -1.
  *   orc_rmsnorm_quant                    -- closed forms (constant input, single
  *                                           spike), scale invariance, fp16
  *                                           widening of exact halves, the
@@ -371,6 +382,127 @@ void orc_relu2_rmsnorm_quant(const uint16_t* gate, const uint16_t* up, const uin
 /* ------------------------------------------------------------------------ */
 void orc_residual_add_f16(float* hidden, const float* y, int n) {
     for (int i = 0; i < n; ++i) hidden[i] = hidden[i] + orc_half_to_float(orc_float_to_half(y[i]));
+}
+
+/* ------------------------------------------------------------------------ */
+/* RMSNorm with fp16 output: rmsnorm_f32_in_k, cuda/ter_cuda_forward_bitnet.cu */
+/* :37-47, launched <<<1,256>>> before the lm_head (:890).  The sum of        */
+/* squares is orc_rmsnorm_quant's (256 strided fused multiply-add partials,   */
+/* the halving tree, correctly rounded rms_inv); y_i = half((x_i * rms_inv) * */
+/* gamma_i).                                                                  */
+/* ------------------------------------------------------------------------ */
+void orc_rmsnorm_f16(const float* x, const uint16_t* gamma, int H, float eps, uint16_t* y, float* rms_inv_out) {
+    float part[256];
+    for (int t = 0; t < 256; ++t) {
+        float acc = 0.f;
+        for (int i = t; i < H; i += 256) acc = fmaf(x[i], x[i], acc);
+        part[t] = acc;
+    }
+    for (int s = 128; s > 0; s >>= 1)
+        for (int t = 0; t < s; ++t) part[t] += part[t + s];
+    const float rms_inv = 1.0f / sqrtf(part[0] / (float)H + eps);
+    if (rms_inv_out) *rms_inv_out = rms_inv;
+    for (int i = 0; i < H; ++i) {
+        const float a = x[i] * rms_inv;
+        y[i] = orc_float_to_half(a * orc_half_to_float(gamma[i]));
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* fp16 lm_head GEMV: mm_fp16_lm_head_k, cuda/ter_cuda_forward_bitnet.cu:     */
+/* 388-429.  One 32-lane warp per vocabulary row v of token_embd [V][H]:      */
+/*   H even: lane l sums pairs k = l, l+32, ... < H/2 in that order,          */
+/*           acc += x[2k]*e[2k] + x[2k+1]*e[2k+1] (products of fp16 values    */
+/*           are exact in fp32, so the one rounding per step is the sum's     */
+/*           and no contraction choice can change it);                        */
+/*   H odd:  lane l sums elements k = l, l+32, ... < H, acc += x[k]*e[k];     */
+/*   then the xor butterfly o = 16, 8, 4, 2, 1 (acc_l += acc_{l^o} on every   */
+/*   lane at once); lane 0's value, rounded to fp16, is logits[v].           */
+/* acc_out (optional) receives lane 0's fp32 value.                          */
+/* ------------------------------------------------------------------------ */
+void orc_lm_head_f16(const uint16_t* x, const uint16_t* e, int H, int V, uint16_t* logits, float* acc_out) {
+    for (int v = 0; v < V; ++v) {
+        const uint16_t* row = e + (size_t)v * (size_t)H;
+        float lane[32];
+        for (int l = 0; l < 32; ++l) {
+            float acc = 0.f;
+            if (H % 2 == 0) {
+                for (int k = l; k < H / 2; k += 32) {
+                    const float p0 = orc_half_to_float(x[2 * k]) * orc_half_to_float(row[2 * k]);
+                    const float p1 = orc_half_to_float(x[2 * k + 1]) * orc_half_to_float(row[2 * k + 1]);
+                    acc += p0 + p1;
+                }
+            } else {
+                for (int k = l; k < H; k += 32) acc += orc_half_to_float(x[k]) * orc_half_to_float(row[k]);
+            }
+            lane[l] = acc;
+        }
+        for (int o = 16; o > 0; o >>= 1) {
+            float next[32];
+            for (int l = 0; l < 32; ++l) next[l] = lane[l] + lane[l ^ o];
+            memcpy(lane, next, sizeof lane);
+        }
+        if (acc_out) acc_out[v] = lane[0];
+        if (logits) logits[v] = orc_float_to_half(lane[0]);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Two-pass argmax over fp16 logits: argmax_local_k / argmax_final_k,        */
+/* cuda/ter_cuda_forward_bitnet.cu:454-495, launched with 128 parts of 256   */
+/* threads and a 128-thread final block (:906-911).  Part b covers           */
+/* [b*chunk, min(N, (b+1)*chunk)), chunk = ceil(N/128); thread t of a part   */
+/* keeps its first strict maximum over i = start+t, +256, ...; each tree     */
+/* level keeps the lower slot unless the upper is strictly greater.  Values  */
+/* not above -1e30 (-inf) and NaN never win; with none eligible the result   */
+/* is -1.                                                                    */
+/* ------------------------------------------------------------------------ */
+static void orc_tree_max(float* best, int* idx, int n) {
+    for (int s = n / 2; s > 0; s >>= 1)
+        for (int t = 0; t < s; ++t)
+            if (best[t + s] > best[t]) {
+                best[t] = best[t + s];
+                idx[t] = idx[t + s];
+            }
+}
+
+int orc_argmax_f16(const uint16_t* logits, int N) {
+    enum { PARTS = 128, THREADS = 256 };
+    float pmax[PARTS];
+    int pidx[PARTS];
+    const int chunk = (N + PARTS - 1) / PARTS;
+    for (int b = 0; b < PARTS; ++b) {
+        const int start = b * chunk;
+        const int end = N < start + chunk ? N : start + chunk;
+        float best[THREADS];
+        int idx[THREADS];
+        for (int t = 0; t < THREADS; ++t) {
+            best[t] = -1e30f;
+            idx[t] = -1;
+            for (int i = start + t; i < end; i += THREADS) {
+                const float v = orc_half_to_float(logits[i]);
+                if (v > best[t]) {
+                    best[t] = v;
+                    idx[t] = i;
+                }
+            }
+        }
+        orc_tree_max(best, idx, THREADS);
+        pmax[b] = best[0];
+        pidx[b] = idx[0];
+    }
+    float best[PARTS];
+    int idx[PARTS];
+    for (int t = 0; t < PARTS; ++t) {
+        best[t] = -1e30f;
+        idx[t] = -1;
+        if (pmax[t] > best[t]) {
+            best[t] = pmax[t];
+            idx[t] = pidx[t];
+        }
+    }
+    orc_tree_max(best, idx, PARTS);
+    return idx[0];
 }
 
 /* ------------------------------------------------------------------------ */

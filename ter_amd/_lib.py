@@ -140,6 +140,10 @@ SIGNATURES = [
     ("ter_hip_pack_i2s", C.c_int, [C.POINTER(WPK), _P, _P]),
     ("ter_hip_rmsnorm_quant", C.c_int, [_P, C.c_int32, _P, C.c_float, C.c_int32, C.c_int32, _P, _P, _P]),
     ("ter_hip_relu2_rmsnorm_quant", C.c_int, [_P, _P, _P, C.c_float, C.c_int32, C.c_int32, _P, _P, _P]),
+    ("ter_hip_rmsnorm_f16", C.c_int, [_P, _P, C.c_float, C.c_int32, C.c_int32, _P, _P]),
+    ("ter_hip_lm_head_f16", C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
+    ("ter_hip_argmax_f16", C.c_int, [_P, C.c_int32, _P, _P, _P]),
+    ("ter_hip_lm_head_argmax", C.c_int, [_P, _P, C.c_float, _P, C.c_int32, C.c_int32, _P, _P, _P, _P, _P]),
     ("ter_hip_create", _P, [C.c_int32]),
     ("ter_hip_destroy", None, [_P]),
     ("ter_hip_install_native", C.c_int, [_P, C.c_char_p, NATIVE_FN]),

@@ -857,6 +857,104 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     return TER_HIP_OK;
 }
 
+int ter_hip_rmsnorm_f16(const float* x, const uint16_t* gamma, float eps, int32_t M, int32_t H, uint16_t* y,
+                        void* stream) {
+    if (!x || !gamma || !y) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (M < 1 || M > 65535 || H < 1 || H > TER_HIP_K_MAX) return fail(TER_HIP_ERR_SHAPE, "M=%d H=%d out of range", M, H);
+    if (!aligned(x, 4) || !aligned(gamma, 2) || !aligned(y, 2)) return fail(TER_HIP_ERR_ALIGN, "x, gamma or y misaligned");
+    if (!(eps >= 0.f)) return fail(TER_HIP_ERR_SHAPE, "RMSNorm eps must be >= 0");
+    hipError_t e = launch_rmsnorm_f16_rows(x, gamma, eps, M, H, y, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm f16 launch");
+    return TER_HIP_OK;
+}
+
+namespace {
+
+// Workgroups of an lm_head launch: resident workgroups per CU times the CU
+// count, raised so no wave's row range spans 2^31 bytes (its buffer
+// resource), capped by the row pairs.
+int pick_lm_head_wg(int H, int V, int* n_wg) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const int cus = device_cu_count(dev);
+    if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
+    const int fit = lm_head_max_wg_per_cu(H);
+    if (fit <= 0) return fail(TER_HIP_ERR_SHAPE, "lm_head workgroup does not fit a CU (H=%d)", H);
+    long long g = (long long)cus * fit;
+    const long long bytes = (long long)V * H * 2;
+    const long long min_g = bytes / ((1LL << 30) * 4) + 1;  // 4 waves per workgroup, < 1 GiB per wave
+    if (g < min_g) g = min_g;
+    const long long pairs = ((long long)V + 1) / 2;
+    if (g > pairs) g = pairs;
+    if (g < 1) g = 1;
+    *n_wg = (int)g;
+    return TER_HIP_OK;
+}
+
+int check_lm_head(const uint16_t* emb, int H, int V) {
+    if (!emb) return fail(TER_HIP_ERR_NULL, "null token_embd");
+    if (H < 1 || H > TER_HIP_K_MAX || V < 1 || V > TER_HIP_N_MAX)
+        return fail(TER_HIP_ERR_SHAPE, "H=%d V=%d out of range", H, V);
+    if (H % 2 == 0 && !aligned(emb, 4)) return fail(TER_HIP_ERR_ALIGN, "token_embd must be 4-byte aligned");
+    if (!aligned(emb, 2)) return fail(TER_HIP_ERR_ALIGN, "token_embd misaligned");
+    return TER_HIP_OK;
+}
+
+}  // namespace
+
+int ter_hip_lm_head_f16(const uint16_t* x_norm, const uint16_t* token_embd, uint16_t* logits, int32_t H, int32_t V,
+                        void* stream) {
+    if (!x_norm || !logits) return fail(TER_HIP_ERR_NULL, "null argument");
+    int rc = check_lm_head(token_embd, H, V);
+    if (rc) return rc;
+    if (!aligned(x_norm, H % 2 == 0 ? 4 : 2) || !aligned(logits, 2)) return fail(TER_HIP_ERR_ALIGN, "x_norm or logits misaligned");
+    int n_wg = 0;
+    rc = pick_lm_head_wg(H, V, &n_wg);
+    if (rc) return rc;
+    hipError_t e = launch_lm_head(nullptr, nullptr, 0.f, x_norm, token_embd, H, V, nullptr, logits, nullptr, nullptr,
+                                  n_wg, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "lm_head launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_argmax_f16(const uint16_t* logits, int32_t N, int32_t* out_idx, uint64_t* state, void* stream) {
+    if (!logits || !out_idx || !state) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (N < 1 || N > TER_HIP_N_MAX) return fail(TER_HIP_ERR_SHAPE, "N=%d out of range", N);
+    if (!aligned(logits, 2) || !aligned(out_idx, 4) || !aligned(state, 8)) return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const int cus = device_cu_count(dev);
+    if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
+    long long g = ((long long)N + 1023) / 1024;  // about 4 elements per thread
+    if (g > cus) g = cus;
+    e = launch_argmax_f16(logits, N, out_idx, reinterpret_cast<unsigned long long*>(state), (int)g,
+                          static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "argmax launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_lm_head_argmax(const float* hidden, const uint16_t* gamma, float eps, const uint16_t* token_embd, int32_t H,
+                           int32_t V, uint16_t* x_norm_out, uint16_t* logits_out, int32_t* token_out, uint64_t* state,
+                           void* stream) {
+    if (!hidden || !gamma || !token_out || !state) return fail(TER_HIP_ERR_NULL, "null argument");
+    int rc = check_lm_head(token_embd, H, V);
+    if (rc) return rc;
+    if (H % 2) return fail(TER_HIP_ERR_SHAPE, "the fused RMSNorm prologue needs an even H (H=%d)", H);
+    if (!aligned(hidden, 8) || !aligned(gamma, 4) || !aligned(x_norm_out, 4) || !aligned(logits_out, 2) ||
+        !aligned(token_out, 4) || !aligned(state, 8))
+        return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
+    if (!(eps >= 0.f)) return fail(TER_HIP_ERR_SHAPE, "RMSNorm eps must be >= 0");
+    int n_wg = 0;
+    rc = pick_lm_head_wg(H, V, &n_wg);
+    if (rc) return rc;
+    hipError_t e = launch_lm_head(hidden, gamma, eps, nullptr, token_embd, H, V, x_norm_out, logits_out, token_out,
+                                  reinterpret_cast<unsigned long long*>(state), n_wg, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "lm_head launch");
+    return TER_HIP_OK;
+}
+
 int ter_hip_synth_v11(uint8_t* v11_dev, int32_t K, int32_t N, uint64_t seed, uint32_t t0, uint32_t t1, void* stream) {
     if (!v11_dev) return fail(TER_HIP_ERR_NULL, "null buffer");
     if (K < 1 || N < 4 || N % 4) return fail(TER_HIP_ERR_SHAPE, "K=%d N=%d", K, N);

@@ -310,6 +310,82 @@ def mm_batched(W: PackedTrits, X, y=None, acc=None, x_scale_dev=None, q_out=None
     return y, acc
 
 
+def rmsnorm_f16(x, gamma, eps: float = 1e-5, y=None, stream=None):
+    """Per-row RMSNorm with fp16 output (rmsnorm_f32_in_k,
+    cuda/ter_cuda_forward_bitnet.cu:37-47): fp32 x [M][H], fp16 gamma [H]."""
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    M, H = x2.shape
+    if x.dtype != torch.float32 or gamma.dtype != torch.float16 or gamma.numel() != H:
+        raise TypeError("x must be float32 [M][H] and gamma float16 [H]")
+    if y is None:
+        y = torch.empty((M, H), dtype=torch.float16, device=x.device)
+    L.check(L.lib().ter_hip_rmsnorm_f16(x2.data_ptr(), gamma.data_ptr(), C.c_float(eps), M, H, y.data_ptr(),
+                                        _stream(stream)), "ter_hip_rmsnorm_f16")
+    return y
+
+
+def lm_head_f16(x_norm, token_embd, logits=None, stream=None):
+    """fp16 lm_head GEMV (mm_fp16_lm_head_k, cuda/ter_cuda_forward_bitnet.cu:388-429):
+    x_norm fp16 [H], token_embd fp16 [V][H] -> logits fp16 [V]."""
+    torch = _torch()
+    V, H = token_embd.shape
+    if x_norm.dtype != torch.float16 or token_embd.dtype != torch.float16 or x_norm.numel() != H:
+        raise TypeError("x_norm must be float16 [H] and token_embd float16 [V][H]")
+    if logits is None:
+        logits = torch.empty(V, dtype=torch.float16, device=x_norm.device)
+    L.check(L.lib().ter_hip_lm_head_f16(x_norm.data_ptr(), token_embd.data_ptr(), logits.data_ptr(), H, V,
+                                        _stream(stream)), "ter_hip_lm_head_f16")
+    return logits
+
+
+class ArgmaxState:
+    """The 16-byte device state of the one-launch argmax (zero at rest)."""
+
+    def __init__(self, device="cuda"):
+        torch = _torch()
+        self.t = torch.zeros(2, dtype=torch.int64, device=device)
+
+    def ptr(self) -> int:
+        return self.t.data_ptr()
+
+
+def argmax_f16(logits, out_idx=None, state: Optional[ArgmaxState] = None, stream=None):
+    """argmax of fp16 logits with the reference's index (ties included):
+    argmax_local_k + argmax_final_k (cuda/ter_cuda_forward_bitnet.cu:454-495)."""
+    torch = _torch()
+    if logits.dtype != torch.float16:
+        raise TypeError("logits must be float16")
+    if out_idx is None:
+        out_idx = torch.empty(1, dtype=torch.int32, device=logits.device)
+    if state is None:
+        state = ArgmaxState(logits.device)
+    L.check(L.lib().ter_hip_argmax_f16(logits.data_ptr(), logits.numel(), out_idx.data_ptr(), state.ptr(),
+                                       _stream(stream)), "ter_hip_argmax_f16")
+    return out_idx
+
+
+def lm_head_argmax(hidden, gamma, token_embd, eps: float = 1e-5, token_out=None, state: Optional[ArgmaxState] = None,
+                   x_norm_out=None, logits_out=None, stream=None):
+    """The decode step's tail in one launch (cuda/ter_cuda_forward_bitnet.cu:890-911):
+    RMSNorm of fp32 hidden [H] -> fp16 lm_head over token_embd [V][H] -> argmax.
+    Returns token_out (int32 [1])."""
+    torch = _torch()
+    V, H = token_embd.shape
+    if hidden.dtype != torch.float32 or hidden.numel() != H:
+        raise TypeError("hidden must be float32 [H]")
+    if gamma.dtype != torch.float16 or token_embd.dtype != torch.float16:
+        raise TypeError("gamma and token_embd must be float16")
+    if token_out is None:
+        token_out = torch.empty(1, dtype=torch.int32, device=hidden.device)
+    if state is None:
+        state = ArgmaxState(hidden.device)
+    L.check(L.lib().ter_hip_lm_head_argmax(hidden.data_ptr(), gamma.data_ptr(), C.c_float(eps), token_embd.data_ptr(),
+                                           H, V, _ptr(x_norm_out), _ptr(logits_out), token_out.data_ptr(),
+                                           state.ptr(), _stream(stream)), "ter_hip_lm_head_argmax")
+    return token_out
+
+
 class Plan:
     """Many independent GEMVs in one launch (one work list).  `items` is a
     sequence of dicts: {w: PackedTrits, x: tensor, y?, acc?, y16?, resid?,

@@ -27,7 +27,7 @@ def declared_functions():
 
 def test_library_exports_every_declared_symbol():
     names = declared_functions()
-    assert len(names) == 31, names
+    assert len(names) == 35, names
     lib = L.lib()
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
@@ -144,6 +144,36 @@ def test_gemv_validation_without_device():
     w.layout = 3
     x.scale_dev = fake
     assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_PAYLOAD
+
+
+def test_lm_head_validation_without_device():
+    lib = L.lib()
+    fake = 1 << 20
+    # standalone RMSNorm -> fp16
+    assert lib.ter_hip_rmsnorm_f16(None, fake, 1e-5, 1, 64, fake, None) == L.ERR_NULL
+    assert lib.ter_hip_rmsnorm_f16(fake, fake, 1e-5, 0, 64, fake, None) == L.ERR_SHAPE
+    assert lib.ter_hip_rmsnorm_f16(fake + 2, fake, 1e-5, 1, 64, fake, None) == L.ERR_ALIGN
+    assert lib.ter_hip_rmsnorm_f16(fake, fake, -1.0, 1, 64, fake, None) == L.ERR_SHAPE
+    # lm_head GEMV: shapes, 4-byte alignment for even H
+    assert lib.ter_hip_lm_head_f16(fake, None, fake, 64, 10, None) == L.ERR_NULL
+    assert lib.ter_hip_lm_head_f16(fake, fake, fake, 0, 10, None) == L.ERR_SHAPE
+    assert lib.ter_hip_lm_head_f16(fake, fake, fake, 64, L.N_MAX + 1, None) == L.ERR_SHAPE
+    assert lib.ter_hip_lm_head_f16(fake, fake + 2, fake, 64, 10, None) == L.ERR_ALIGN
+    assert lib.ter_hip_lm_head_f16(fake + 2, fake, fake, 64, 10, None) == L.ERR_ALIGN
+    # argmax: state and output required
+    assert lib.ter_hip_argmax_f16(fake, 10, fake, None, None) == L.ERR_NULL
+    assert lib.ter_hip_argmax_f16(fake, 0, fake, fake, None) == L.ERR_SHAPE
+    assert lib.ter_hip_argmax_f16(fake, 10, fake, fake + 4, None) == L.ERR_ALIGN
+    # fused tail: even H only, token_out and state required, alignment
+    args = [fake, fake, 1e-5, fake, 64, 10, None, None, fake, fake, None]
+    bad = list(args); bad[8] = None
+    assert lib.ter_hip_lm_head_argmax(*bad) == L.ERR_NULL
+    bad = list(args); bad[4] = 63
+    assert lib.ter_hip_lm_head_argmax(*bad) == L.ERR_SHAPE
+    bad = list(args); bad[0] = fake + 4
+    assert lib.ter_hip_lm_head_argmax(*bad) == L.ERR_ALIGN
+    bad = list(args); bad[2] = float("nan")
+    assert lib.ter_hip_lm_head_argmax(*bad) == L.ERR_SHAPE
 
 
 def test_mm_row_rejects_non_int8_activations():

@@ -409,3 +409,113 @@ def test_residual_add_rounds_projection_to_half():
         want = h + y.astype(np.float16).astype(np.float32)
     assert (got.view(np.uint32) == want.view(np.uint32)).all()
     assert got[1] == np.inf and got[2] == -np.inf
+
+
+# ---------------------------------------------------------------------------
+# lm_head tail of the decode step: rmsnorm_f32_in_k (:37-47), mm_fp16_lm_head_k
+# (:388-429), argmax_local_k / argmax_final_k (:454-495) of
+# cuda/ter_cuda_forward_bitnet.cu
+# ---------------------------------------------------------------------------
+
+def test_rmsnorm_f16_shares_the_reference_sum_order():
+    """rmsnorm_f32_in_k and rmsnorm_quant_f32_in_k run the same 256-thread
+    sum: rms_inv agrees; constant input has the closed form
+    y = half(c / sqrt(c^2 + eps))."""
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal(2560) * 3).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, 2560).astype(np.float16)
+    y, r = O.rmsnorm_f16(x, g, 1e-5)
+    assert r == O.rmsnorm_quant(x, g, 1e-5)[2]
+    for c in (3.0, -0.25, 1000.0):
+        y, r = O.rmsnorm_f16(np.full(2560, c, np.float32), np.ones(2560, np.float16), 1e-5)
+        want_r = np.float32(1.0) / np.sqrt(np.float32(c * c) + np.float32(1e-5))
+        assert r == want_r
+        assert (y == np.float16(np.float32(c) * want_r)).all()
+
+
+def test_lm_head_exact_integer_dot_products():
+    """Small integer x and token_embd: every partial sum is an exact fp32
+    integer, so the logits are the fp16 rounding of the exact dot product
+    (even and odd H)."""
+    rng = np.random.default_rng(22)
+    for H, V in ((2560, 40), (2561, 7), (64, 3)):
+        x = rng.integers(-2, 3, H).astype(np.float16)
+        E = rng.integers(-2, 3, (V, H)).astype(np.float16)
+        lg, acc = O.lm_head_f16(x, E)
+        exact = E.astype(np.int64) @ x.astype(np.int64)
+        assert (acc == exact.astype(np.float32)).all()
+        assert (lg.view(np.uint16) == exact.astype(np.float64).astype(np.float16).view(np.uint16)).all()
+
+
+def test_lm_head_lane_order_and_butterfly():
+    """H = 64: 32 pairs, one per lane.  Lane 0 holds 2048, lane 16 holds 0,
+    the other 30 lanes 2^-13 (half an ulp of 2048).  The butterfly pairs
+    lanes (l, l+16) first, so the small terms combine before meeting 2048 and
+    the sum is exactly 2048 + 15 * 2^-12; a sequential sum loses each term to
+    ties-to-even and stays at 2048."""
+    H = 64
+    x = np.zeros(H, np.float16)
+    x[0::2] = 1.0
+    e = np.zeros((2, H), np.float16)
+    e[0, 0::2] = np.float16(2.0 ** -13)
+    e[0, 0] = 2048.0
+    e[0, 32] = 0.0  # pair 16
+    e[1] = e[0][::-1].copy()  # a second, independent row
+    lg, acc = O.lm_head_f16(x, e)
+    want = np.float32(2048.0 + 15 * 2.0 ** -12)
+    assert acc[0] == want
+    seq = np.float32(0)
+    for k in range(32):
+        seq = np.float32(seq + np.float32(e[0, 2 * k]))
+    assert seq == np.float32(2048.0) and seq != want  # the case distinguishes the orders
+    assert acc[1] == 0.0  # row 1 has its weights on the odd elements, where x is 0
+
+
+def _argmax_rule_key(i, N):
+    """Reference tie rule: among equal maxima, the local tree keeps the
+    lower slot unless the upper is strictly greater, so two threads meet at
+    the level of their lowest differing bit and the one with a 0 there wins:
+    the smallest bit-reversed thread id (8 bits) wins, likewise the smallest
+    bit-reversed part (7 bits); within a thread, the first element."""
+    chunk = -(-N // 128)
+    b, o = divmod(i, chunk)
+    t, k = o % 256, o // 256
+    rev = lambda v, n: int(format(v, f"0{n}b")[::-1], 2)
+    return (rev(b, 7), rev(t, 8), k)
+
+
+def test_argmax_unique_maximum_is_numpy_argmax():
+    rng = np.random.default_rng(23)
+    for N in (128256, 1000, 300, 100, 1):
+        x = rng.standard_normal(N).astype(np.float32)
+        x[rng.integers(N)] = 20.0
+        lg = x.astype(np.float16)
+        assert O.argmax_f16(lg) == int(np.argmax(lg))
+
+
+def test_argmax_ties_follow_the_tree_rule():
+    rng = np.random.default_rng(24)
+    for N in (128256, 1000, 300, 3000):
+        for trial in range(20):
+            lg = rng.standard_normal(N).astype(np.float16)
+            cand = rng.choice(N, size=int(rng.integers(2, 6)), replace=False)
+            lg[cand] = np.float16(9.0)
+            if trial % 5 == 0:
+                lg[cand[0]] = np.float16(-0.0)  # -0 == +0 for the comparisons
+                lg[cand[1:]] = np.float16(0.0)
+                lg[lg > 0] = -1.0
+            got = O.argmax_f16(lg)
+            want = min(cand, key=lambda i: _argmax_rule_key(int(i), N))
+            assert got == want, (N, trial, sorted(cand), got, want)
+
+
+def test_argmax_nan_and_minus_inf_never_win():
+    N = 1000
+    lg = np.full(N, -np.inf, np.float16)
+    assert O.argmax_f16(lg) == -1
+    lg[777] = np.float16(-65504.0)
+    assert O.argmax_f16(lg) == 777
+    lg[5] = np.float16(np.nan)
+    assert O.argmax_f16(lg) == 777
+    lg[900] = np.float16(np.inf)
+    assert O.argmax_f16(lg) == 900
