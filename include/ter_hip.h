@@ -303,9 +303,10 @@ int ter_hip_lm_head_f16(const uint16_t* x_norm, const uint16_t* token_embd, uint
  * ties included (among equal maxima the reference's two reduction trees
  * decide: smallest bit-reversed part, then smallest bit-reversed thread,
  * then the first element); NaN and -inf never win; -1 if nothing is
- * eligible.  One launch.  `state`: 16 bytes of device memory, zero before
- * the first call (hipMemset) and left zero by every call; calls that share a
- * state must not overlap in time. */
+ * eligible.  One launch.  `state`: TER_HIP_ARGMAX_STATE_BYTES of device
+ * memory (8-byte aligned), zero before the first call (hipMemset) and left
+ * zero by every call; calls that share a state must not overlap in time. */
+#define TER_HIP_ARGMAX_STATE_BYTES 16512
 int ter_hip_argmax_f16(const uint16_t* logits, int32_t N, int32_t* out_idx, uint64_t* state,
                        void* stream);
 /* The whole tail in ONE launch (rmsnorm_f32_in_k + mm_fp16_lm_head_k +

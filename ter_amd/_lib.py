@@ -37,6 +37,7 @@ X_F32_RMS = 2
 X_F16_RMS = 3
 X_RELU2_RMS = 4
 LAYOUT_T16 = 16
+ARGMAX_STATE_BYTES = 16512
 
 
 class WPK(C.Structure):

@@ -95,12 +95,11 @@ hipError_t launch_quant_rows(const float* x, int M, int K, int8_t* q, float* s, 
 // TER_HIP_X_F16_RMS or TER_HIP_X_RELU2_RMS (x = gate, up [M][K]).
 hipError_t launch_rmsnorm_quant_rows(const void* x, const uint16_t* up, int kind, const uint16_t* gamma, float eps,
                                      int M, int K, int8_t* q, float* s, hipStream_t st);
-// lm_head tail (lm_head.hip).  Fast path: H even and H/2 <= 32 * 64 pairs
-// (lm_head_fast_nj(H) > 0); any other H runs the generic kernel.  With
+// lm_head tail (lm_head.hip).  Fast path: H a multiple of 8 and at most
+// 4096 (lm_head_fast_nb(H) > 0); any other H runs the generic kernel.  With
 // `hidden` the launch normalizes it first (H even only); `state` (2 words,
 // zero at rest) is needed when token_out is set.
-int lm_head_fast_nj(int H);
-int lm_head_lds_bytes(int H);
+int lm_head_fast_nb(int H);
 int lm_head_max_wg_per_cu(int H);
 hipError_t launch_lm_head(const float* hidden, const uint16_t* gamma, float eps, const uint16_t* x16,
                           const uint16_t* emb, int H, int V, uint16_t* x_out, uint16_t* logits, int32_t* token_out,

@@ -25,12 +25,15 @@
 // key with one 64-bit atomic max per workgroup, and the last workgroup to
 // arrive decodes the index, writes it and returns the two state words to
 // zero, so the next launch (or graph replay) starts clean.
+#include <type_traits>
+
 #include "common.h"
 
 namespace terhip {
 namespace {
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kLmWaves = 4;
 constexpr int kLmThreads = kLmWaves * 64;
@@ -44,7 +47,7 @@ struct LmArgs {
     uint16_t* x_out;            // fp16 [H] copy of the normalized input or null
     uint16_t* logits;           // fp16 [V] or null
     int32_t* token_out;         // argmax index or null
-    unsigned long long* state;  // [2] zero at rest (argmax)
+    unsigned long long* state;  // argmax state, zero at rest (kArgGroups + 1 pairs)
     float eps;
     int H, V;
 };
@@ -89,9 +92,41 @@ __device__ __forceinline__ unsigned long long wave_max64(unsigned long long k) {
     return k;
 }
 
-// Workgroup maximum of the per-lane keys, then one atomic max per
-// workgroup; the last workgroup to arrive writes the index and clears the
-// state.  Every thread of the workgroup must call it.
+// Argmax state: kArgGroups groups of (key, count) words, 128 bytes apart,
+// then the top (key, count); all zero at rest.
+constexpr int kArgGroups = 128;
+constexpr int kArgStride = 16;  // words (128 bytes) between groups
+static_assert((kArgGroups + 1) * kArgStride * 8 == TER_HIP_ARGMAX_STATE_BYTES, "argmax state size");
+
+__device__ __forceinline__ unsigned long long amax(unsigned long long* p, unsigned long long v) {
+    return __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long aadd(unsigned long long* p, unsigned long long v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Fold key m into the (key, count) pair at p; true for the arrival that
+// makes the count n, which also takes the pair's maximum into *best and
+// clears the pair.  The max is performed (its old value returned) before
+// the arrival is counted, so the arrival that counts last sees every max:
+// read-modify-write atomics on one address are performed at one point, in
+// order.  No fence: a device-scope fence writes back and invalidates the
+// XCD's L2, which costs more than the whole argmax when every workgroup
+// does it.
+__device__ __forceinline__ bool arrive(unsigned long long* p, unsigned long long m, unsigned long long n,
+                                       unsigned long long* best) {
+    const unsigned long long old = amax(p, m);
+    asm volatile("" ::"v"((unsigned)old) : "memory");
+    if (aadd(p + 1, 1ull) != n - 1) return false;
+    *best = __hip_atomic_exchange(p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(p + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return true;
+}
+
+// Workgroup maximum of the per-lane keys, then two levels of atomics (a
+// group of workgroups, then the groups) so that no address takes more than
+// about n_wg / kArgGroups arrivals; the last arrival writes the index.
+// Every thread of the workgroup must call it.
 __device__ void argmax_finish(unsigned long long key, unsigned long long* kred, unsigned long long* state,
                               int32_t* token_out, int chunk) {
     key = wave_max64(key);
@@ -101,15 +136,13 @@ __device__ void argmax_finish(unsigned long long key, unsigned long long* kred, 
         unsigned long long m = kred[0];
 #pragma unroll
         for (int w = 1; w < kLmWaves; ++w) m = umax64(m, kred[w]);
-        if (m) atomicMax(state, m);
-        __threadfence();
-        const unsigned long long arrived = atomicAdd(state + 1, 1ull);
-        if (arrived == (unsigned long long)gridDim.x - 1ull) {
-            __threadfence();
-            const unsigned long long best = atomicExch(state, 0ull);
-            atomicExch(state + 1, 0ull);
+        const unsigned n_wg = gridDim.x, g = blockIdx.x % kArgGroups;
+        const unsigned groups = n_wg < (unsigned)kArgGroups ? n_wg : (unsigned)kArgGroups;
+        const unsigned in_group = (n_wg - g + kArgGroups - 1) / kArgGroups;
+        unsigned long long bg, best;
+        if (arrive(state + kArgStride * g, m, in_group, &bg) &&
+            arrive(state + kArgStride * kArgGroups, bg, groups, &best))
             *gptr(token_out) = argmax_index(best, chunk);
-        }
     }
 }
 
@@ -147,95 +180,154 @@ __device__ void stage_x_pairs(const LmArgs& a, uint32_t* xs, int npad, float* re
     __syncthreads();
 }
 
-// Row pair p of this wave (lanes 0-31: row 2p, lanes 32-63: row 2p + 1,
-// relative to the wave's first row): one dword per group j.
-template <int NJ>
-__device__ __forceinline__ void load_pair(uint32_t (&w)[NJ], __amdgpu_buffer_rsrc_t rs, int p, int nrows, int rowb,
-                                          int v, int half, int n2) {
-    const int row = 2 * p + half;
-    const bool row_ok = row < nrows;
-    const unsigned base = (unsigned)(row * rowb + 4 * v);
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const unsigned off = (row_ok && v + 32 * j < n2) ? base + 128u * j : kOob;
-        w[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 2 /* nt */);
+// Fast path (H a multiple of 8, H/2 <= 32 * 8 * NB pairs).  A wave runs
+// 8 vocabulary rows at once ("octet"): lane 8s + q serves row s of the octet
+// and the reference's virtual lanes 4q .. 4q+3, whose pairs 4q+i + 32j are
+// the 16 contiguous bytes 128j + 16q of the row.  So every load is a 16-byte
+// buffer_load_dwordx4 covering, per instruction, 128 contiguous bytes of
+// each of 8 adjacent rows, and each of the lane's 4 accumulators runs the
+// reference's sequential chain over j.  The butterfly's steps o = 16, 8, 4
+// pair lanes q ^ 4, q ^ 2, q ^ 1; o = 2, 1 pair accumulators i ^ 2, i ^ 1.
+// Per fp16 pair: p1 = x_hi * e_hi (exact), t = x_lo * e_lo + p1 rounded
+// once (exact products, so t equals the reference's rounding of the pair
+// sum), acc += t.  Batches of 8 groups (8 loads of 16 bytes per lane) are
+// double-buffered across the wave's whole sequence of octets.
+constexpr int kGroupsPerBatch = 8;
+
+// f(integral_constant<int, 0>) .. f(integral_constant<int, N - 1>), unrolled.
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void unroll_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        unroll_for<N, I + 1>(f);
     }
 }
 
-template <int NJ>
-__device__ __forceinline__ float dot_pair(const uint32_t (&w)[NJ], const uint32_t (&xr)[NJ]) {
+// Batch jb (groups 8 jb .. 8 jb + 7) of octet `oct` of the wave's rows.
+// Rows past the wave's range fall outside the buffer resource (the hardware
+// range check returns zeros, and no memory is read); pairs past H/2 in a
+// partial last group get an out-of-range offset.  Every lane issues every
+// load and there is no branch, so the loads stay counted in order.
+template <int JB, bool FULL>
+__device__ __forceinline__ void load_batch16(u32x4 (&w)[kGroupsPerBatch], __amdgpu_buffer_rsrc_t rs, int oct, int rowb,
+                                             int slot, int q, int n2) {
+    const unsigned base = (unsigned)((8 * oct + slot) * rowb + 16 * q);
+    const int lim = n2 - 4 * q;  // pairs of this lane's column that exist
+#pragma unroll
+    for (int g = 0; g < kGroupsPerBatch; ++g) {
+        constexpr int j0 = JB * kGroupsPerBatch;
+        const unsigned pen = FULL || 32 * (j0 + g) < lim ? 0u : kOob;
+        w[g] = __builtin_amdgcn_raw_buffer_load_b128(rs, base + pen + 128u * (j0 + g), 0, 2 /* nt */);
+    }
+}
+
+__device__ __forceinline__ float pair_term(unsigned x, unsigned e) {
+    const float p1 = __builtin_fmaf((float)__builtin_bit_cast(_Float16, (uint16_t)(x >> 16)),
+                                    (float)__builtin_bit_cast(_Float16, (uint16_t)(e >> 16)), 0.0f);
+    return __builtin_fmaf((float)__builtin_bit_cast(_Float16, (uint16_t)(x & 0xFFFFu)),
+                          (float)__builtin_bit_cast(_Float16, (uint16_t)(e & 0xFFFFu)), p1);
+}
+
+// FULL: H/2 == 256 NB, every group of every row exists (no masking).
+template <int NB, bool FULL>
+__global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmArgs a, int stage_rows) {
 #pragma clang fp contract(off)
-    float acc = 0.f;
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const float p0 = half_bits_to_float((uint16_t)(xr[j] & 0xFFFFu)) * half_bits_to_float((uint16_t)(w[j] & 0xFFFFu));
-        const float p1 = half_bits_to_float((uint16_t)(xr[j] >> 16)) * half_bits_to_float((uint16_t)(w[j] >> 16));
-        acc = acc + (p0 + p1);
-    }
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o);
-    return acc;
-}
-
-// Fast path, H even and H/2 <= 32 NJ: see the file comment.  The workgroup's
-// 4 waves each own a contiguous range of row pairs (ranges of all waves of
-// the grid in blockIdx order).
-template <int NJ>
-__global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmArgs a) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
+    constexpr int NJ = NB * kGroupsPerBatch;
     uint32_t* xs = reinterpret_cast<uint32_t*>(lds_raw);
     float* red = reinterpret_cast<float*>(lds_raw + NJ * 32 * 4);
     unsigned long long* kred = reinterpret_cast<unsigned long long*>(red + kLmThreads);
+    uint16_t* lg_stage = reinterpret_cast<uint16_t*>(kred + kLmWaves);
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
-    const int v = lane & 31, half = lane >> 5;
+    // wave-uniform in an SGPR, so the buffer resource built from it is too
+    // (a resource in VGPRs turns every load into a readfirstlane loop)
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int slot = lane >> 3, q = lane & 7;
     const int n2 = a.H >> 1;
     const int rowb = a.H * 2;
-    const long long P = ((long long)a.V + 1) / 2;
+    const long long O = ((long long)a.V + 7) / 8;
     const long long W = (long long)gridDim.x * kLmWaves;
     const long long gw = (long long)blockIdx.x * kLmWaves + wave;
-    const long long p0 = P * gw / W, p1 = P * (gw + 1) / W;
-    const int np = (int)(p1 - p0);
-    const long long r0 = 2 * p0;
-    const long long r1 = 2 * p1 < (long long)a.V ? 2 * p1 : (long long)a.V;
+    const long long o0 = O * gw / W, o1 = O * (gw + 1) / W;
+    const int n_oct = (int)(o1 - o0);
+    const long long r0 = 8 * o0;
+    const long long r1 = 8 * o1 < (long long)a.V ? 8 * o1 : (long long)a.V;
     const int nrows = (int)(r1 - r0);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(a.emb + r0 * a.H), 0, nrows * rowb, 0x00020000);
+    // logits of this wave's rows are staged in LDS and written at the end
+    // (stores between the loads would make every wait drain the loads)
+    const bool staged = a.logits && stage_rows > 0;
+    uint16_t* my_stage = lg_stage + wave * stage_rows;
 
-    uint32_t wa[NJ], wb[NJ];
-    if (np > 0) load_pair<NJ>(wa, rs, 0, nrows, rowb, v, half, n2);  // in flight during staging
+    u32x4 wa[kGroupsPerBatch], wb[kGroupsPerBatch];
+    load_batch16<0, FULL>(wa, rs, 0, rowb, slot, q, n2);  // in flight during staging
     stage_x_pairs(a, xs, NJ * 32, red);
-    uint32_t xr[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) xr[j] = xs[v + 32 * j];
 
     const int chunk = argmax_chunk(a.V);
     unsigned long long best = 0ull;
-    uint16_t mine = 0;
-    auto emit = [&](int p, float acc) {
-        const uint16_t h = float_to_half_bits(acc);
-        const int row = 2 * p + half;
-        if (row < nrows) {
-            if (a.token_out) best = umax64(best, argmax_key(h, (int)(r0 + row), chunk));
-            if ((p & 31) == v) mine = h;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    // Groups of batch JB of octet `oct` (w holds them), then for the last
+    // batch the butterfly and the row's outputs.
+    auto compute = [&](const u32x4 (&w)[kGroupsPerBatch], int oct, auto jb_tag) {
+        constexpr int JB = decltype(jb_tag)::value;
+        if constexpr (JB == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = 0.f;
         }
-        // one store per 32 pairs: lane v holds the logit of pair (p & ~31) + v
-        if (a.logits && ((p & 31) == 31 || p == np - 1)) {
-            const int rl = 2 * ((p & ~31) + v) + half;
-            if (v <= (p & 31) && rl < nrows) gptr(a.logits)[r0 + rl] = mine;
+#pragma unroll
+        for (int g = 0; g < kGroupsPerBatch; ++g) {
+            const int j = JB * kGroupsPerBatch + g;
+            const u32x4 x = *reinterpret_cast<const u32x4*>(xs + 32 * j + 4 * q);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = acc[i] + pair_term(x[i], w[g][i]);
+        }
+        if constexpr (JB == NB - 1) {
+            float r[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[i] = acc[i];
+#pragma unroll
+            for (int m = 4; m >= 1; m >>= 1)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) r[i] = r[i] + __shfl_xor(r[i], m);
+            const float tot = (r[0] + r[2]) + (r[1] + r[3]);
+            const int row = 8 * oct + slot;
+            if (q == 0 && row < nrows) {
+                const uint16_t h = float_to_half_bits(tot);
+                if (a.token_out) best = umax64(best, argmax_key(h, (int)(r0 + row), chunk));
+                if (staged) my_stage[row] = h;
+                else if (a.logits) gptr(a.logits)[r0 + row] = h;
+            }
         }
     };
-    for (int p = 0; p < np; p += 2) {
-        if (p + 1 < np) load_pair<NJ>(wb, rs, p + 1, nrows, rowb, v, half, n2);
-        emit(p, dot_pair<NJ>(wa, xr));
-        if (p + 1 >= np) break;
-        if (p + 2 < np) load_pair<NJ>(wa, rs, p + 2, nrows, rowb, v, half, n2);
-        emit(p + 1, dot_pair<NJ>(wb, xr));
+    // Static two-buffer schedule over a block of OPS octets (OPS * NB batches,
+    // an even count): batch t computes from buffer t & 1 while batch t + 1
+    // (possibly the next block's first) loads into the other.  Loads past the
+    // wave's octets read nothing (out of range); their computes are skipped.
+    constexpr int OPS = NB % 2 ? 2 : 1;
+    for (int o = 0; o < n_oct; o += OPS) {
+        unroll_for<OPS * NB>([&](auto t_tag) {
+            constexpr int t = decltype(t_tag)::value;
+            constexpr int tn = t + 1;
+            const int on = o + tn / NB;
+            if constexpr (t % 2 == 0) {
+                load_batch16<tn % NB, FULL>(wb, rs, on, rowb, slot, q, n2);
+                if (o + t / NB < n_oct) compute(wa, o + t / NB, std::integral_constant<int, t % NB>{});
+            } else {
+                load_batch16<tn % NB, FULL>(wa, rs, on, rowb, slot, q, n2);
+                if (o + t / NB < n_oct) compute(wb, o + t / NB, std::integral_constant<int, t % NB>{});
+            }
+        });
+    }
+    if (staged) {
+        // LDS operations of one wave complete in order: the staged values are visible to its other lanes
+        asm volatile("" ::: "memory");
+        for (int i = lane; i < nrows; i += 64) gptr(a.logits)[r0 + i] = my_stage[i];
     }
     if (a.token_out) argmax_finish(best, kred, a.state, a.token_out, chunk);
 }
 
-// Any H (odd, or H/2 above the fast path's 32 * 64 pairs): the reference's
+// Any H off the fast path (not a multiple of 8, or above 4096): the reference's
 // lane order with one load per element pair (or element), no pipelining.
 __global__ __launch_bounds__(kLmThreads) void lm_head_generic_kernel(LmArgs a, int npad) {
 #pragma clang fp contract(off)
@@ -310,34 +402,61 @@ __global__ __launch_bounds__(256) void rmsnorm_f16_rows_kernel(const float* __re
 
 }  // namespace
 
-int lm_head_fast_nj(int H) {
-    if (H & 1) return 0;
-    const int nj = (H / 2 + 31) / 32;
-    const int r = (nj + 7) / 8 * 8;
-    return r <= 64 ? r : 0;
+int lm_head_fast_nb(int H) {
+    if (H % 8) return 0;
+    const int nb = (H / 2 + 32 * kGroupsPerBatch - 1) / (32 * kGroupsPerBatch);
+    return nb <= 8 ? nb : 0;
 }
 
-int lm_head_lds_bytes(int H) {
-    const int nj = lm_head_fast_nj(H);
-    const int npad = nj ? nj * 32 : (H + 1) / 2;
-    return npad * 4 + kLmThreads * 4 + kLmWaves * 8;
+int lm_head_stage_rows(int H, int V, int n_wg) {
+    if (!lm_head_fast_nb(H)) return 0;
+    const long long O = ((long long)V + 7) / 8, W = (long long)n_wg * kLmWaves;
+    const long long rows = 8 * ((O + W - 1) / W);
+    return rows <= 2048 ? (int)rows : 0;  // at most 16 KiB of LDS for the staged logits
 }
+
+int lm_head_lds_bytes(int H, int stage_rows) {
+    const int nb = lm_head_fast_nb(H);
+    const int npad = nb ? nb * kGroupsPerBatch * 32 : (H + 1) / 2;
+    return npad * 4 + kLmThreads * 4 + kLmWaves * 8 + kLmWaves * stage_rows * 2;
+}
+
+namespace {
+
+// The kernel for H: lm_head_kernel<NB, FULL> on the fast path, else the
+// generic one (nullptr).
+typedef void (*LmKernel)(LmArgs, int);
+
+template <int NB>
+LmKernel fast_kernel(bool full) {
+    return full ? lm_head_kernel<NB, true> : lm_head_kernel<NB, false>;
+}
+
+LmKernel lm_kernel_of(int H) {
+    const int nb = lm_head_fast_nb(H);
+    const bool full = H / 2 == 32 * kGroupsPerBatch * nb;
+    switch (nb) {
+        case 1: return fast_kernel<1>(full);
+        case 2: return fast_kernel<2>(full);
+        case 3: return fast_kernel<3>(full);
+        case 4: return fast_kernel<4>(full);
+        case 5: return fast_kernel<5>(full);
+        case 6: return fast_kernel<6>(full);
+        case 7: return fast_kernel<7>(full);
+        case 8: return fast_kernel<8>(full);
+        default: return nullptr;
+    }
+}
+
+}  // namespace
 
 int lm_head_max_wg_per_cu(int H) {
-    const int nj = lm_head_fast_nj(H), lds = lm_head_lds_bytes(H);
+    const int lds = lm_head_lds_bytes(H, 2048);
+    const LmKernel k = lm_kernel_of(H);
     int n = 0;
-    hipError_t e;
-    switch (nj) {
-        case 8: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_kernel<8>, kLmThreads, lds); break;
-        case 16: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_kernel<16>, kLmThreads, lds); break;
-        case 24: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_kernel<24>, kLmThreads, lds); break;
-        case 32: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_kernel<32>, kLmThreads, lds); break;
-        case 40: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_kernel<40>, kLmThreads, lds); break;
-        case 48: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_kernel<48>, kLmThreads, lds); break;
-        case 56: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_kernel<56>, kLmThreads, lds); break;
-        case 64: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_kernel<64>, kLmThreads, lds); break;
-        default: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_generic_kernel, kLmThreads, lds); break;
-    }
+    const hipError_t e =
+        k ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, kLmThreads, lds)
+          : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, lm_head_generic_kernel, kLmThreads, lds);
     return e == hipSuccess ? n : 0;
 }
 
@@ -356,19 +475,13 @@ hipError_t launch_lm_head(const float* hidden, const uint16_t* gamma, float eps,
     a.eps = eps;
     a.H = H;
     a.V = V;
-    const int nj = lm_head_fast_nj(H), lds = lm_head_lds_bytes(H);
-    const dim3 g(n_wg), b(kLmThreads);
-    switch (nj) {
-        case 8: hipLaunchKernelGGL(lm_head_kernel<8>, g, b, lds, st, a); break;
-        case 16: hipLaunchKernelGGL(lm_head_kernel<16>, g, b, lds, st, a); break;
-        case 24: hipLaunchKernelGGL(lm_head_kernel<24>, g, b, lds, st, a); break;
-        case 32: hipLaunchKernelGGL(lm_head_kernel<32>, g, b, lds, st, a); break;
-        case 40: hipLaunchKernelGGL(lm_head_kernel<40>, g, b, lds, st, a); break;
-        case 48: hipLaunchKernelGGL(lm_head_kernel<48>, g, b, lds, st, a); break;
-        case 56: hipLaunchKernelGGL(lm_head_kernel<56>, g, b, lds, st, a); break;
-        case 64: hipLaunchKernelGGL(lm_head_kernel<64>, g, b, lds, st, a); break;
-        default: hipLaunchKernelGGL(lm_head_generic_kernel, g, b, lds, st, a, (H + 1) / 2); break;
-    }
+    const int srows = logits ? lm_head_stage_rows(H, V, n_wg) : 0;
+    const int lds = lm_head_lds_bytes(H, srows);
+    const LmKernel k = lm_kernel_of(H);
+    if (k)
+        hipLaunchKernelGGL(k, dim3(n_wg), dim3(kLmThreads), lds, st, a, srows);
+    else
+        hipLaunchKernelGGL(lm_head_generic_kernel, dim3(n_wg), dim3(kLmThreads), lds, st, a, (H + 1) / 2);
     return hipGetLastError();
 }
 

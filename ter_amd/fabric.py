@@ -340,11 +340,12 @@ def lm_head_f16(x_norm, token_embd, logits=None, stream=None):
 
 
 class ArgmaxState:
-    """The 16-byte device state of the one-launch argmax (zero at rest)."""
+    """The device state of the one-launch argmax (TER_HIP_ARGMAX_STATE_BYTES,
+    zero at rest; every call leaves it zero)."""
 
     def __init__(self, device="cuda"):
         torch = _torch()
-        self.t = torch.zeros(2, dtype=torch.int64, device=device)
+        self.t = torch.zeros(L.ARGMAX_STATE_BYTES // 8, dtype=torch.int64, device=device)
 
     def ptr(self) -> int:
         return self.t.data_ptr()

@@ -50,10 +50,10 @@ def test_rmsnorm_f16_rows(cuda, H):
         assert (f16_bits(y[r]) == f16_bits(want)).all(), r
 
 
-@pytest.mark.parametrize("H,V", [(2560, 1000), (2560, 4097), (2048, 300), (64, 33), (100, 50), (2561, 77),
-                                 (8200, 50), (2, 5)],
-                         ids=["bitnet-h", "odd-v", "llama-h", "one-group", "partial-group", "odd-h-generic",
-                              "wide-h-generic", "tiny"])
+@pytest.mark.parametrize("H,V", [(2560, 1000), (2560, 4097), (2048, 300), (64, 33), (1000, 300), (2056, 129),
+                                 (100, 50), (2561, 77), (8200, 50), (2, 5)],
+                         ids=["bitnet-h", "odd-v", "llama-h", "one-group", "masked-groups", "partial-group",
+                              "h-not-8-generic", "odd-h-generic", "wide-h-generic", "tiny"])
 def test_lm_head_logits(cuda, H, V):
     import torch
     import ter_amd as T
