@@ -34,6 +34,8 @@
 // each 2-bit code u = w + 1 straight to the signed int8 w with one v_perm_b32
 // per 4 trits (a byte table {-1, 0, +1, 0} indexed by u), and issues
 // v_mfma_i32_16x16x64_i8.  Signed weights need no activation-sum correction.
+#include <type_traits>
+
 #include "common.h"
 
 namespace terhip {
@@ -270,21 +272,57 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
             // epilogue of block cb
             const GemmDesc& d = bc.d;
             const float* xs_l = reinterpret_cast<const float*>(lds + C::XSO + (cb % C::NST) * 1024);
+            // For the 8-row-block configuration (M > 64, occupancy already
+            // fixed by its accumulators) fp32 / int32 outputs get a loop of
+            // their own: the fp16 and residual checks per element cost ~3% at
+            // M = 128.  Smaller configurations keep one loop (a second copy
+            // costs them a wave of occupancy).
+            auto epilogue = [&](auto plain_tag) {
+                constexpr bool kPlain = decltype(plain_tag)::value;
 #pragma unroll
-            for (int mb = 0; mb < C::MBW; ++mb) {
-                const f32x4 xq = *reinterpret_cast<const f32x4*>(xs_l + (rg * C::MBW + mb) * 16 + g * 4);
+                for (int mb = 0; mb < C::MBW; ++mb) {
+                    const f32x4 xq = *reinterpret_cast<const f32x4*>(xs_l + (rg * C::MBW + mb) * 16 + g * 4);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int row = (rg * C::MBW + mb) * 16 + g * 4 + e;
-                    if (row < d.M) {
-                        const float sc = xq[e] * d.w_scale;
+                    for (int e = 0; e < 4; ++e) {
+                        const int row = (rg * C::MBW + mb) * 16 + g * 4 + e;
+                        if (row < d.M) {
+                            const float sc = xq[e] * d.w_scale;
 #pragma unroll
-                        for (int s = 0; s < C::S; ++s) {
-                            const int col = (bc.st0 + sg * C::S + s) * kStripCols + j;
-                            if (col < d.N) {
-                                const long long o = (long long)row * d.N + col;
-                                const int val = acc[s][mb][e];
-                                emit_out(d, o, val, sc);
+                            for (int s = 0; s < C::S; ++s) {
+                                const int col = (bc.st0 + sg * C::S + s) * kStripCols + j;
+                                if (col < d.N) {
+                                    const long long o = (long long)row * d.N + col;
+                                    const int val = acc[s][mb][e];
+                                    if constexpr (kPlain) {
+                                        if (d.acc) gptr(d.acc)[o] = val;
+                                        if (d.y) gptr(d.y)[o] = (float)val * sc;
+                                    } else {
+                                        emit_out(d, o, val, sc);
+                                    }
+                                }
+                            }
+                        }
+                    }
+                }
+            };
+            if constexpr (C::MBW >= 8) {
+                if (!d.y16 && !d.resid)
+                    epilogue(std::true_type{});
+                else
+                    epilogue(std::false_type{});
+            } else {
+#pragma unroll
+                for (int mb = 0; mb < C::MBW; ++mb) {
+                    const f32x4 xq = *reinterpret_cast<const f32x4*>(xs_l + (rg * C::MBW + mb) * 16 + g * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int row = (rg * C::MBW + mb) * 16 + g * 4 + e;
+                        if (row < d.M) {
+                            const float sc = xq[e] * d.w_scale;
+#pragma unroll
+                            for (int s = 0; s < C::S; ++s) {
+                                const int col = (bc.st0 + sg * C::S + s) * kStripCols + j;
+                                if (col < d.N) emit_out(d, (long long)row * d.N + col, acc[s][mb][e], sc);
                             }
                         }
                     }
