@@ -319,6 +319,42 @@ int ter_hip_lm_head_argmax(const float* hidden, const uint16_t* gamma, float eps
                            uint16_t* logits_out, int32_t* token_out, uint64_t* state, void* stream);
 
 /* ---------------------------------------------------------------------- */
+/* Decode attention: RoPE + KV-cache write + attention, one launch per      */
+/* layer (rope_k, kv_copy_k, attention_k: cuda/ter_cuda_forward_bitnet.cu   */
+/* :185-214, 336-374, launched at :864-871; cuda/ter_cuda_forward_packed.cu  */
+/* :64-157 for the Llama forward)                                           */
+/* ---------------------------------------------------------------------- */
+#define TER_HIP_ROPE_NORM 0  /* pairs (2k, 2k+1): the Llama forward's rope_k  */
+#define TER_HIP_ROPE_NEOX 1  /* pairs (k, k + hd/2): BitNet (LLAMA_ROPE_TYPE_NEOX) */
+typedef struct ter_hip_attn ter_hip_attn_t;
+/* A decode-attention context for one model shape: n_heads query heads,
+ * n_kv_heads KV heads (n_heads a multiple of it; query head h reads KV head
+ * h * n_kv_heads / n_heads), head_dim 64 or 128, caches of s_max <= 4096
+ * positions laid out [s_max][n_kv_heads][head_dim] fp16 per layer (the
+ * reference's K_cache / V_cache slice of one layer), RoPE base theta.
+ * Holds the RoPE table (fl(1/fl(theta^(2k/hd))), positions times that, cos
+ * and sin in double rounded once to binary32) and the chunk workspace.
+ * Contexts are not shared between streams: launches of one context must not
+ * overlap in time. */
+int ter_hip_attn_create(ter_hip_attn_t** a, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                        int32_t s_max, float theta, int32_t rope_type);
+/* One token of one layer: q fp16 [n_heads][hd], k, v fp16 [n_kv_heads][hd]
+ * (projection outputs, before RoPE), *pos_dev the token's position
+ * (device int32, < s_max; a position outside [0, s_max) makes the launch
+ * write nothing).  Applies RoPE to q and k, writes k and v at
+ * position pos of k_cache / v_cache, and writes out fp16 [n_heads][hd] =
+ * softmax(q K^T / sqrt(hd)) V over positions 0 .. pos.  Scores are the
+ * reference's bit for bit; the softmax runs over chunks of 64 positions
+ * combined in order (fp16 outputs within one ulp of the reference's
+ * sequential order).  Caches 16-byte aligned. */
+int ter_hip_attn_decode(const ter_hip_attn_t* a, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        uint16_t* k_cache, uint16_t* v_cache, const int32_t* pos_dev, uint16_t* out,
+                        void* stream);
+/* RoPE in place on fp16 head vectors x [n_heads][hd] at *pos_dev (rope_k). */
+int ter_hip_rope(const ter_hip_attn_t* a, uint16_t* x, int32_t n_heads, const int32_t* pos_dev, void* stream);
+void ter_hip_attn_destroy(ter_hip_attn_t* a);
+
+/* ---------------------------------------------------------------------- */
 /* K4-style handle + KernelTable native slot                               */
 /* (include/ter_k4/ter_k4.h:29-55; include/ter/kernels.hpp:21-38)           */
 /* ---------------------------------------------------------------------- */

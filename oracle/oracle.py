@@ -74,6 +74,17 @@ def lib():
         L.orc_lm_head_f16.restype = None
         L.orc_argmax_f16.argtypes = [_P, C.c_int]
         L.orc_argmax_f16.restype = C.c_int
+        L.orc_expf.argtypes = [C.c_float]
+        L.orc_expf.restype = C.c_float
+        L.orc_expf_n.argtypes = [_P, _P, C.c_size_t]
+        L.orc_expf_n.restype = None
+        L.orc_rope_table.argtypes = [C.c_float, C.c_int, C.c_int, _P]
+        L.orc_rope_table.restype = None
+        L.orc_rope_f16.argtypes = [_P, C.c_int, C.c_int, _P, C.c_int]
+        L.orc_rope_f16.restype = None
+        for f in (L.orc_attention_ref, L.orc_attention_splitk):
+            f.argtypes = [_P, _P, _P, C.c_int, C.c_int, C.c_int, C.c_int, _P, _P]
+            f.restype = None
         L.orc_quantize_bitnet.argtypes = [_P, C.c_size_t, _P]
         L.orc_quantize_bitnet.restype = C.c_float
         L.orc_quantize_nt.argtypes = [_P, C.c_size_t, C.c_int, _P]
@@ -281,6 +292,53 @@ def argmax_f16(logits: np.ndarray) -> int:
     """argmax_local_k + argmax_final_k (cuda/ter_cuda_forward_bitnet.cu:454-495)."""
     lg = np.ascontiguousarray(logits, dtype=np.float16)
     return int(lib().orc_argmax_f16(_ptr(lg), lg.size))
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    """The attention softmax's binary32 exp (orc_expf)."""
+    xx = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    y = np.empty_like(xx)
+    lib().orc_expf_n(_ptr(xx), _ptr(y), xx.size)
+    return y.reshape(np.shape(x))
+
+
+def rope_table(theta: float, hd: int, n_pos: int) -> np.ndarray:
+    """NEOX RoPE (cos, sin) table [n_pos][hd/2][2] (rope_k's steps)."""
+    cs = np.empty((n_pos, hd // 2, 2), dtype=np.float32)
+    lib().orc_rope_table(C.c_float(theta), hd, n_pos, _ptr(cs))
+    return cs
+
+
+def rope_f16(v: np.ndarray, cs_pos: np.ndarray, neox: bool = True) -> np.ndarray:
+    """rope_k on fp16 head vectors v [n_heads][hd] with table row cs_pos [hd/2][2]."""
+    out = np.array(v, dtype=np.float16, copy=True, order="C")
+    nh, hd = out.shape
+    cp = np.ascontiguousarray(cs_pos, dtype=np.float32)
+    lib().orc_rope_f16(_ptr(out), nh, hd, _ptr(cp), 1 if neox else 0)
+    return out
+
+
+def _attention(fn, q, K, V):
+    qq = np.ascontiguousarray(q, dtype=np.float16)
+    KK = np.ascontiguousarray(K, dtype=np.float16)
+    VV = np.ascontiguousarray(V, dtype=np.float16)
+    nh, hd = qq.shape
+    seq, nkv, _ = KK.shape
+    o16 = np.empty((nh, hd), dtype=np.uint16)
+    o32 = np.empty((nh, hd), dtype=np.float32)
+    fn(_ptr(qq), _ptr(KK), _ptr(VV), nh, nkv, hd, seq, _ptr(o16), _ptr(o32))
+    return o16.view(np.float16), o32
+
+
+def attention_ref(q, K, V):
+    """attention_k (cuda/ter_cuda_forward_bitnet.cu:336-374): q fp16 [nh][hd],
+    K, V fp16 [seq][nkv][hd] -> (fp16 out [nh][hd], fp32 pre-rounding)."""
+    return _attention(lib().orc_attention_ref, q, K, V)
+
+
+def attention_splitk(q, K, V):
+    """The GPU kernel's chunked order (64-position chunks)."""
+    return _attention(lib().orc_attention_splitk, q, K, V)
 
 
 def quantize_bitnet(x: np.ndarray):

@@ -42,6 +42,22 @@
  *                                           that separates the lane-strided order
  *                                           and butterfly from a sequential sum,
  *                                           odd H.
+ *   orc_expf                             -- exp in double rounded to binary32 (max
+ *                                           error measured over dense samples),
+ *                                           exact special points.
+ *   orc_rope_table, orc_rope_f16         -- identity at position 0, the NEOX
+ *                                           pairing (k, k + hd/2) and the NORM
+ *                                           pairing (2k, 2k+1) on unit vectors,
+ *                                           norm preservation, table entries
+ *                                           against numpy's double cos/sin.
+ *   orc_attention_ref                    -- one position (out = v exactly), q = 0
+ *                                           (out = mean of v), a dominant score,
+ *                                           float64 softmax attention within the
+ *                                           rounding bound.
+ *   orc_attention_splitk                 -- orc_attention_ref within the rounding
+ *                                           bound; equal to it where the chunked
+ *                                           order reduces to the sequential one
+ *                                           (one position).
  *   orc_argmax_f16                       -- numpy argmax on unique maxima; on
  *                                           ties the closed-form rule of the
  *                                           two reduction trees; NaN / -inf never
@@ -503,6 +519,201 @@ int orc_argmax_f16(const uint16_t* logits, int N) {
     }
     orc_tree_max(best, idx, PARTS);
     return idx[0];
+}
+
+/* ------------------------------------------------------------------------ */
+/* exp for the attention softmax.  The reference calls CUDA's expf, whose   */
+/* exact results only its own GPU reproduces; this build uses one binary32  */
+/* algorithm, the same operation for operation here and in the kernel:      */
+/* Cody-Waite argument reduction x = n ln2 + r (ln2 split so that n ln2_hi  */
+/* is exact), e^r by the degree-7 Taylor polynomial in Horner form with     */
+/* fused multiply-adds (truncation < 6e-9 relative on |r| <= ln2/2), then   */
+/* the scale 2^n applied in two exact-or-once-rounded steps.                */
+/* ------------------------------------------------------------------------ */
+static float orc_pow2i(int e) {  /* 2^e for -126 <= e <= 127 */
+    const uint32_t b = (uint32_t)(e + 127) << 23;
+    float f;
+    memcpy(&f, &b, sizeof f);
+    return f;
+}
+
+float orc_expf(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return INFINITY;
+    if (x < -103.972084045410156f) return 0.0f;
+    const float n = rintf(x * 1.44269502162933349609375f);
+    float r = fmaf(-n, 0.693145751953125f, x);
+    r = fmaf(-n, 1.42860676533018704e-06f, r);
+    float p = 1.98412701e-04f;
+    p = fmaf(p, r, 1.38888892e-03f);
+    p = fmaf(p, r, 8.33333377e-03f);
+    p = fmaf(p, r, 4.16666679e-02f);
+    p = fmaf(p, r, 1.66666672e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    const int n1 = ni / 2, n2 = ni - n1;
+    return (p * orc_pow2i(n1)) * orc_pow2i(n2);
+}
+
+void orc_expf_n(const float* x, float* y, size_t n) {
+    for (size_t i = 0; i < n; ++i) y[i] = orc_expf(x[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* NEOX RoPE: rope_k, cuda/ter_cuda_forward_bitnet.cu:185-200 (pairs        */
+/* (v[k], v[k + hd/2]); tools/bitnet_pyfwd.py:83-94).  Table entry (p, k):  */
+/* freq = fl(1 / fl(theta^(2k/hd))), a = fl(p * freq), c = fl(cos a),      */
+/* s = fl(sin a): the reference's float steps, with its powf / cosf / sinf  */
+/* replaced by libm in double rounded once to binary32.                     */
+/* cs: [n_pos][hd/2][2] (cos, sin).                                         */
+/* ------------------------------------------------------------------------ */
+void orc_rope_table(float theta, int hd, int n_pos, float* cs) {
+    const int half = hd / 2;
+    for (int k = 0; k < half; ++k) {
+        const float e = (2.0f * (float)k) / (float)hd;
+        const float pw = (float)pow((double)theta, (double)e);
+        const float freq = 1.0f / pw;
+        for (int p = 0; p < n_pos; ++p) {
+            const float a = (float)p * freq;
+            cs[((size_t)p * half + k) * 2] = (float)cos((double)a);
+            cs[((size_t)p * half + k) * 2 + 1] = (float)sin((double)a);
+        }
+    }
+}
+
+/* Rotate n_heads fp16 head vectors in place with one position's table row
+ * cs_p [hd/2][2]: pair k is (v[k], v[k + hd/2]) for NEOX (BitNet, rope_k of
+ * cuda/ter_cuda_forward_bitnet.cu:185-200) or (v[2k], v[2k+1]) for NORM (the
+ * Llama forward's rope_k, cuda/ter_cuda_forward_packed.cu:64-76);
+ * r0 = v0*c - v1*s, r1 = v0*s + v1*c, each contracted as one fused
+ * multiply-add over the other product (fma(v0, c, -(v1 s)), fma(v0, s, v1 c):
+ * the fold LLVM applies to the reference's expression), rounded to fp16. */
+void orc_rope_f16(uint16_t* v, int n_heads, int hd, const float* cs_p, int neox) {
+    const int half = hd / 2;
+    for (int h = 0; h < n_heads; ++h)
+        for (int k = 0; k < half; ++k) {
+            uint16_t* a = v + (size_t)h * hd + (neox ? k : 2 * k);
+            uint16_t* b = neox ? a + half : a + 1;
+            const float c = cs_p[2 * k], sn = cs_p[2 * k + 1];
+            const float v0 = orc_half_to_float(*a), v1 = orc_half_to_float(*b);
+            const float r0 = fmaf(v0, c, -(v1 * sn));
+            const float r1 = fmaf(v0, sn, v1 * c);
+            *a = orc_float_to_half(r0);
+            *b = orc_float_to_half(r1);
+        }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Decode attention, reference order: attention_k,                           */
+/* cuda/ter_cuda_forward_bitnet.cu:336-374, for one token over seq cached    */
+/* positions.  q fp16 [nh][hd] (after RoPE); K, V fp16 [seq][nkv][hd]; query */
+/* head h reads KV head h * nkv / nh.                                        */
+/*   score_s = fl(dot_s * fl(1/sqrt(hd))), dot_s the fp32 sum over d in     */
+/*     order (products of fp16 values are exact, so contraction is moot;    */
+/*     the reference's rsqrtf is replaced by the correctly rounded value);   */
+/*   one thread: mx = max_s score_s; e_s = orc_expf(score_s - mx); sum over  */
+/*     s in order; p_s = e_s * (1 / sum);                                    */
+/*   out[d] = half(acc), acc = fma(p_s, v_sd, acc) over s in order.         */
+/* out32 (optional) receives acc.                                            */
+/* ------------------------------------------------------------------------ */
+static float orc_score(const uint16_t* q, const uint16_t* k, int hd, float inv_sqrt) {
+    float dot = 0.f;
+    for (int d = 0; d < hd; ++d) dot = fmaf(orc_half_to_float(q[d]), orc_half_to_float(k[d]), dot);
+    return dot * inv_sqrt;
+}
+
+void orc_attention_ref(const uint16_t* q, const uint16_t* K, const uint16_t* V, int nh, int nkv, int hd, int seq,
+                       uint16_t* out16, float* out32) {
+    const float inv_sqrt = (float)(1.0 / sqrt((double)hd));
+    float* p = (float*)malloc(sizeof(float) * (size_t)(seq > 0 ? seq : 1));
+    if (!p) return;
+    for (int h = 0; h < nh; ++h) {
+        const int g = h * nkv / nh;
+        for (int s = 0; s < seq; ++s)
+            p[s] = orc_score(q + (size_t)h * hd, K + ((size_t)s * nkv + g) * hd, hd, inv_sqrt);
+        float mx = p[0];
+        for (int s = 1; s < seq; ++s)
+            if (p[s] > mx) mx = p[s];
+        float sum = 0.f;
+        for (int s = 0; s < seq; ++s) {
+            p[s] = orc_expf(p[s] - mx);
+            sum += p[s];
+        }
+        const float inv = 1.f / sum;
+        for (int s = 0; s < seq; ++s) p[s] *= inv;
+        for (int d = 0; d < hd; ++d) {
+            float acc = 0.f;
+            for (int s = 0; s < seq; ++s) acc = fmaf(p[s], orc_half_to_float(V[((size_t)s * nkv + g) * hd + d]), acc);
+            if (out32) out32[(size_t)h * hd + d] = acc;
+            if (out16) out16[(size_t)h * hd + d] = orc_float_to_half(acc);
+        }
+    }
+    free(p);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Decode attention in this build's chunked order (the GPU kernel's):        */
+/* positions in chunks of 64; per chunk c and head: m_c = max score,         */
+/* e_s = orc_expf(score_s - m_c), l_c = the xor butterfly (o = 32 .. 1) over */
+/* the chunk's 64 lanes (lane i holds position 64c + i, 0 past seq),         */
+/* o_c[d] = fma(e_s, v_sd, .) over the chunk's positions in order; then over */
+/* chunks in order: w_c = orc_expf(m_c - M) (M = max_c m_c),                 */
+/* L = fma(l_c, w_c, L), O[d] = fma(o_c[d], w_c, O[d]); out[d] = half(O/L).  */
+/* Scores as orc_attention_ref.                                              */
+/* ------------------------------------------------------------------------ */
+void orc_attention_splitk(const uint16_t* q, const uint16_t* K, const uint16_t* V, int nh, int nkv, int hd, int seq,
+                          uint16_t* out16, float* out32) {
+    enum { CH = 64 };
+    const float inv_sqrt = (float)(1.0 / sqrt((double)hd));
+    const int nc = (seq + CH - 1) / CH;
+    float* m = (float*)malloc(sizeof(float) * (size_t)nc);
+    float* l = (float*)malloc(sizeof(float) * (size_t)nc);
+    float* o = (float*)malloc(sizeof(float) * (size_t)nc * (size_t)hd);
+    if (!m || !l || !o) {
+        free(m), free(l), free(o);
+        return;
+    }
+    for (int h = 0; h < nh; ++h) {
+        const int g = h * nkv / nh;
+        float M = -INFINITY;
+        for (int c = 0; c < nc; ++c) {
+            float sc[CH], e[CH], t[CH], u[CH];
+            const int s0 = c * CH;
+            const int n = seq - s0 < CH ? seq - s0 : CH;
+            float mc = -INFINITY;
+            for (int i = 0; i < n; ++i) {
+                sc[i] = orc_score(q + (size_t)h * hd, K + ((size_t)(s0 + i) * nkv + g) * hd, hd, inv_sqrt);
+                if (sc[i] > mc) mc = sc[i];
+            }
+            for (int i = 0; i < CH; ++i) e[i] = i < n ? orc_expf(sc[i] - mc) : 0.f;
+            for (int d = 0; d < hd; ++d) {
+                float acc = 0.f;
+                for (int i = 0; i < n; ++i)
+                    acc = fmaf(e[i], orc_half_to_float(V[((size_t)(s0 + i) * nkv + g) * hd + d]), acc);
+                o[(size_t)c * hd + d] = acc;
+            }
+            memcpy(t, e, sizeof t);
+            for (int w = CH / 2; w > 0; w >>= 1) {
+                for (int i = 0; i < CH; ++i) u[i] = t[i] + t[i ^ w];
+                memcpy(t, u, sizeof t);
+            }
+            m[c] = mc;
+            l[c] = t[0];
+            if (mc > M) M = mc;
+        }
+        float L = 0.f;
+        for (int c = 0; c < nc; ++c) L = fmaf(l[c], orc_expf(m[c] - M), L);
+        for (int d = 0; d < hd; ++d) {
+            float O = 0.f;
+            for (int c = 0; c < nc; ++c) O = fmaf(o[(size_t)c * hd + d], orc_expf(m[c] - M), O);
+            const float r = O / L;
+            if (out32) out32[(size_t)h * hd + d] = r;
+            if (out16) out16[(size_t)h * hd + d] = orc_float_to_half(r);
+        }
+    }
+    free(m), free(l), free(o);
 }
 
 /* ------------------------------------------------------------------------ */

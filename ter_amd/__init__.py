@@ -7,6 +7,7 @@ with ctypes.  See ter_amd.fabric for the host interface.
 from . import _lib  # noqa: F401
 from .fabric import (  # noqa: F401
     ArgmaxState,
+    Attention,
     GemmPlan,
     Handle,
     PackedTrits,
@@ -27,6 +28,6 @@ from .fabric import (  # noqa: F401
     synth_v11,
 )
 
-__all__ = ["ArgmaxState", "GemmPlan", "Handle", "PackedTrits", "Plan", "argmax_f16", "gemv", "lm_head_argmax",
+__all__ = ["ArgmaxState", "Attention", "GemmPlan", "Handle", "PackedTrits", "Plan", "argmax_f16", "gemv", "lm_head_argmax",
            "lm_head_f16", "mm_batched", "mm_packed_dispatch", "mm_packed_dispatch_f16", "mm_row", "quant_int8",
            "relu2_rmsnorm_quant", "rmsnorm_f16", "rmsnorm_quant", "synth_i8", "synth_v11"]

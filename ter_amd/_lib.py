@@ -38,6 +38,8 @@ X_F16_RMS = 3
 X_RELU2_RMS = 4
 LAYOUT_T16 = 16
 ARGMAX_STATE_BYTES = 16512
+ROPE_NORM = 0
+ROPE_NEOX = 1
 
 
 class WPK(C.Structure):
@@ -145,6 +147,11 @@ SIGNATURES = [
     ("ter_hip_lm_head_f16", C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
     ("ter_hip_argmax_f16", C.c_int, [_P, C.c_int32, _P, _P, _P]),
     ("ter_hip_lm_head_argmax", C.c_int, [_P, _P, C.c_float, _P, C.c_int32, C.c_int32, _P, _P, _P, _P, _P]),
+    ("ter_hip_attn_create", C.c_int, [C.POINTER(C.c_void_p), C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
+                                      C.c_int32]),
+    ("ter_hip_attn_decode", C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P]),
+    ("ter_hip_rope", C.c_int, [_P, _P, C.c_int32, _P, _P]),
+    ("ter_hip_attn_destroy", None, [_P]),
     ("ter_hip_create", _P, [C.c_int32]),
     ("ter_hip_destroy", None, [_P]),
     ("ter_hip_install_native", C.c_int, [_P, C.c_char_p, NATIVE_FN]),

@@ -8,6 +8,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cmath>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -281,6 +282,14 @@ struct ter_hip_plan {
     const int32_t* ranges_dev = nullptr;    //   [n_wg + 1] block ranges per workgroup
     int n_blocks = 0;
     uint64_t bytes = 0, macs = 0;
+};
+
+struct ter_hip_attn {
+    int nh = 0, nkv = 0, hd = 0, smax = 0;
+    bool neox = true;
+    float* rope = nullptr;      // [smax][hd/2][2]
+    float* part = nullptr;      // [nh][n_chunks][hd + 2]
+    unsigned* count = nullptr;  // [n_groups], zero at rest
 };
 
 struct ter_hip_handle {
@@ -953,6 +962,92 @@ int ter_hip_lm_head_argmax(const float* hidden, const uint16_t* gamma, float eps
                                   reinterpret_cast<unsigned long long*>(state), n_wg, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "lm_head launch");
     return TER_HIP_OK;
+}
+
+int ter_hip_attn_create(ter_hip_attn_t** out, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t s_max,
+                        float theta, int32_t rope_type) {
+    if (!out) return fail(TER_HIP_ERR_NULL, "null context pointer");
+    *out = nullptr;
+    if (n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads || !attn_supported_head_dim(head_dim) || s_max < 1 ||
+        s_max > attn_chunk() * attn_max_chunks())
+        return fail(TER_HIP_ERR_SHAPE, "attention shape nh=%d nkv=%d hd=%d smax=%d unsupported", n_heads, n_kv_heads,
+                    head_dim, s_max);
+    if (rope_type != TER_HIP_ROPE_NORM && rope_type != TER_HIP_ROPE_NEOX)
+        return fail(TER_HIP_ERR_PAYLOAD, "unknown RoPE type %d", rope_type);
+    if (!(theta > 0.f)) return fail(TER_HIP_ERR_SHAPE, "RoPE theta must be > 0");
+    const int half = head_dim / 2;
+    const int n_chunks = (s_max + attn_chunk() - 1) / attn_chunk();
+    const int groups = n_kv_heads * ((n_heads / n_kv_heads + 3) / 4);
+    // RoPE table: the reference's float steps (rope_k), powf / cosf / sinf
+    // replaced by libm in double rounded once to binary32
+    std::vector<float> tab;
+    try {
+        tab.resize((size_t)s_max * half * 2);
+    } catch (...) {
+        return fail(TER_HIP_ERR_ALLOC, "RoPE table");
+    }
+    for (int k = 0; k < half; ++k) {
+        const float e = (2.0f * (float)k) / (float)head_dim;
+        const float pw = (float)std::pow((double)theta, (double)e);
+        const float freq = 1.0f / pw;
+        for (int p = 0; p < s_max; ++p) {
+            const float ang = (float)p * freq;
+            tab[((size_t)p * half + k) * 2] = (float)std::cos((double)ang);
+            tab[((size_t)p * half + k) * 2 + 1] = (float)std::sin((double)ang);
+        }
+    }
+    ter_hip_attn* a = new (std::nothrow) ter_hip_attn();
+    if (!a) return fail(TER_HIP_ERR_ALLOC, "attention context");
+    a->nh = n_heads;
+    a->nkv = n_kv_heads;
+    a->hd = head_dim;
+    a->smax = s_max;
+    a->neox = rope_type == TER_HIP_ROPE_NEOX;
+    const size_t tb = tab.size() * sizeof(float);
+    const size_t pb = (size_t)n_heads * n_chunks * (head_dim + 2) * sizeof(float);
+    const size_t cb = (size_t)groups * sizeof(unsigned);
+    hipError_t e = hipMalloc(&a->rope, tb);
+    if (e == hipSuccess) e = hipMalloc(&a->part, pb);
+    if (e == hipSuccess) e = hipMalloc(&a->count, cb);
+    if (e == hipSuccess) e = hipMemcpy(a->rope, tab.data(), tb, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(a->count, 0, cb);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        ter_hip_attn_destroy(a);
+        return hip_fail(e, "attention context allocation");
+    }
+    *out = a;
+    return TER_HIP_OK;
+}
+
+int ter_hip_attn_decode(const ter_hip_attn_t* a, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                        uint16_t* k_cache, uint16_t* v_cache, const int32_t* pos_dev, uint16_t* out, void* stream) {
+    if (!a || !q || !k || !v || !k_cache || !v_cache || !pos_dev || !out) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (!aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(q, 2) || !aligned(k, 2) || !aligned(v, 2) ||
+        !aligned(out, 2) || !aligned(pos_dev, 4))
+        return fail(TER_HIP_ERR_ALIGN, "misaligned argument (caches need 16 bytes)");
+    hipError_t e = launch_attn_decode(q, k, v, k_cache, v_cache, pos_dev, out, a->rope, a->part, a->count, a->nh,
+                                      a->nkv, a->hd, a->smax, a->neox, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "attention launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_rope(const ter_hip_attn_t* a, uint16_t* x, int32_t n_heads, const int32_t* pos_dev, void* stream) {
+    if (!a || !x || !pos_dev) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (n_heads < 1) return fail(TER_HIP_ERR_SHAPE, "n_heads=%d", n_heads);
+    if (!aligned(x, 2) || !aligned(pos_dev, 4)) return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
+    hipError_t e =
+        launch_rope(x, n_heads, a->hd, a->rope, pos_dev, a->smax, a->neox, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "rope launch");
+    return TER_HIP_OK;
+}
+
+void ter_hip_attn_destroy(ter_hip_attn_t* a) {
+    if (!a) return;
+    (void)hipFree(a->rope);
+    (void)hipFree(a->part);
+    (void)hipFree(a->count);
+    delete a;
 }
 
 int ter_hip_synth_v11(uint8_t* v11_dev, int32_t K, int32_t N, uint64_t seed, uint32_t t0, uint32_t t1, void* stream) {

@@ -1,0 +1,364 @@
+// attention.hip -- one decode step's attention for one layer on gfx950:
+// RoPE of the new query and key, the KV-cache write of the new position, and
+// attention over all cached positions, in one launch.
+//
+// Reference (cuda/ter_cuda_forward_bitnet.cu, BitNet; the Llama forward
+// cuda/ter_cuda_forward_packed.cu has the same kernels with the NORM pairing):
+//   rope_k       :185-200   NEOX pairs (k, k + hd/2) (NORM: (2k, 2k+1))
+//   kv_copy_k    :204-214   K/V of the new position into [L][Smax][nkv*hd]
+//   attention_k  :336-374   one block per head, whole sequence, one thread's softmax
+//
+// The reference kernel runs the softmax and every output element as single
+// sequential chains over the sequence (2048 dependent steps at BitNet's
+// C5 context).  Here the positions are split into chunks of 64:
+//   - workgroup (head group, chunk): up to 4 query heads sharing one KV head
+//     (GQA), 4 waves, wave i = query head i, lane = position in the chunk;
+//   - scores exactly as the reference (fp32 dot over d in order, times
+//     1/sqrt(hd)); chunk max m_c, e_s = exp(score - m_c), l_c the xor
+//     butterfly over the wave, o_c[d] = sum over the chunk's positions in
+//     order of e_s v_sd (fused multiply-adds);
+//   - the last workgroup of a head group to finish combines the chunks in
+//     order: w_c = exp(m_c - M), L = sum l_c w_c, O = sum o_c w_c, out = O/L.
+// The K and V rows of the chunk are staged in LDS with coalesced 16-byte
+// loads issued before anything else; the new position's key and value come
+// from the projection outputs (RoPE applied here), not from the cache, which
+// this launch writes.
+//
+// Cross-workgroup exchange without fences: partials are written with
+// agent-scope atomic stores (written through to the coherence point), each
+// thread waits for its stores to complete, then one arrival is counted with
+// an agent-scope atomic add; the workgroup that counts last reads the
+// partials with agent-scope atomic loads.  The count returns to zero.
+#include <type_traits>
+
+#include "common.h"
+
+namespace terhip {
+namespace {
+
+constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = kAttnWaves * 64;
+constexpr int kChunk = 64;       // positions per chunk (one per lane)
+constexpr int kMaxChunks = 64;   // combine: one lane per chunk
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+struct AttnArgs {
+    const uint16_t* q;      // fp16 [nh][hd], before RoPE
+    const uint16_t* k;      // fp16 [nkv][hd], before RoPE
+    const uint16_t* v;      // fp16 [nkv][hd]
+    uint16_t* kc;           // fp16 [smax][nkv][hd] K cache of this layer
+    uint16_t* vc;           // fp16 [smax][nkv][hd] V cache of this layer
+    const int32_t* pos;     // device: the new token's position (< smax)
+    uint16_t* out;          // fp16 [nh][hd]
+    const float* rope;      // [smax][hd/2][2] (cos, sin)
+    float* part;            // [nh][n_chunks][hd + 2]: o_c[hd], m_c, l_c
+    unsigned* count;        // [n_groups], zero at rest
+    int nh, nkv, smax, n_chunks, neox, groups_per_kv;
+    float inv_sqrt;
+};
+
+// The softmax exp: Cody-Waite reduction, degree-7 Taylor polynomial in Horner
+// form, two-step scaling by 2^n.  The same operations as the oracle's
+// orc_expf, so both round identically (faithful: < 1 ulp from exp).
+__device__ __forceinline__ float pow2i(int e) { return __builtin_bit_cast(float, (unsigned)(e + 127) << 23); }
+
+__device__ __forceinline__ float attn_expf(float x) {
+#pragma clang fp contract(off)
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -103.972084045410156f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.42860676533018704e-06f, r);
+    float p = 1.98412701e-04f;
+    p = __builtin_fmaf(p, r, 1.38888892e-03f);
+    p = __builtin_fmaf(p, r, 8.33333377e-03f);
+    p = __builtin_fmaf(p, r, 4.16666679e-02f);
+    p = __builtin_fmaf(p, r, 1.66666672e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    const int n1 = ni / 2, n2 = ni - n1;
+    return (p * pow2i(n1)) * pow2i(n2);
+}
+
+// RoPE of one pair (x0, x1) with table entry (c, s): the reference's
+// v0*c - v1*s and v0*s + v1*c, each one fused multiply-add over the other
+// product, rounded to fp16.
+__device__ __forceinline__ void rope_pair(uint16_t& a, uint16_t& b, float c, float s) {
+#pragma clang fp contract(off)
+    const float v0 = half_bits_to_float(a), v1 = half_bits_to_float(b);
+    const float r0 = __builtin_fmaf(v0, c, -(v1 * s));
+    const float r1 = __builtin_fmaf(v0, s, v1 * c);
+    a = float_to_half_bits(r0);
+    b = float_to_half_bits(r1);
+}
+
+// Element indices of RoPE pair k of a head: NEOX (k, k + hd/2), NORM (2k, 2k+1).
+__device__ __forceinline__ void pair_index(int k, int hd, bool neox, int& i0, int& i1) {
+    i0 = neox ? k : 2 * k;
+    i1 = neox ? k + hd / 2 : 2 * k + 1;
+}
+
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
+#pragma clang fp contract(off)
+    constexpr int KROW = HD * 2 + 16;  // padded K row in LDS (bytes): conflict-free 16-byte reads
+    constexpr int VROW = HD * 2;
+    constexpr int HALF = HD / 2;
+    constexpr int DPT = HD / 64;       // output elements per thread
+    __shared__ __align__(16) unsigned char ks[kChunk * KROW];
+    __shared__ __align__(16) unsigned char vs[kChunk * VROW];
+    __shared__ __align__(16) float qs[kAttnWaves][HD];
+    __shared__ float es[kAttnWaves][kChunk];
+    __shared__ float cw[kAttnWaves][kMaxChunks];  // combine: w_c
+    __shared__ float cl[kAttnWaves][kMaxChunks];  // combine: l_c
+    __shared__ int last_flag;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = blockIdx.x / a.n_chunks, chunk = blockIdx.x - grp * a.n_chunks;
+    const int g = grp / a.groups_per_kv;                      // KV head
+    const int gs = a.nh / a.nkv;                              // query heads per KV head
+    const int h0 = g * gs + (grp - g * a.groups_per_kv) * kAttnWaves;
+    const int nhg = min(kAttnWaves, g * gs + gs - h0);        // query heads in this group
+    const int s0 = chunk * kChunk;
+    const int rows = min(kChunk, a.smax - s0);                // cache rows of this chunk
+    const long long row_stride = (long long)a.nkv * HD;        // halves between positions
+
+    // 1. K and V rows of the chunk, in flight before anything else (they do
+    // not depend on the position; rows past the sequence are zeroed below).
+    constexpr int kLoads = kChunk * VROW / 16 / kAttnThreads;  // 16-byte loads per thread per matrix
+    u32x4 kreg[kLoads], vreg[kLoads];
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int idx = tid + i * kAttnThreads;               // 16-byte piece
+        const int r = idx / (VROW / 16), cpart = idx - r * (VROW / 16);
+        kreg[i] = vreg[i] = u32x4{0u, 0u, 0u, 0u};
+        if (r < rows) {
+            const long long off = (long long)(s0 + r) * row_stride + (long long)g * HD + cpart * 8;
+            kreg[i] = *reinterpret_cast<const TER_GLOBAL u32x4*>(gptr(a.kc) + off);
+            vreg[i] = *reinterpret_cast<const TER_GLOBAL u32x4*>(gptr(a.vc) + off);
+        }
+    }
+    const int pos = *gptr(a.pos);
+    if (pos < 0 || pos >= a.smax) return;                     // (the whole grid: no output, no count)
+    const int seq = pos + 1;
+    const int n = max(0, min(kChunk, seq - s0));              // positions in this chunk
+    const bool has_pos = pos >= s0 && pos < s0 + kChunk;
+    const bool writer = has_pos && grp == g * a.groups_per_kv;  // one workgroup per KV head writes the cache
+
+    // 2. RoPE of the group's query heads into qs (as the fp16-rounded values).
+    const TER_GLOBAL float* tab = gptr(a.rope) + (long long)pos * HD;  // [hd/2][2] of this position
+    for (int idx = tid; idx < nhg * HALF; idx += kAttnThreads) {
+        const int i = idx / HALF, kk = idx - i * HALF;
+        int i0, i1;
+        pair_index(kk, HD, a.neox != 0, i0, i1);
+        const TER_GLOBAL uint16_t* qh = gptr(a.q) + (long long)(h0 + i) * HD;
+        uint16_t x0 = qh[i0], x1 = qh[i1];
+        rope_pair(x0, x1, tab[2 * kk], tab[2 * kk + 1]);
+        qs[i][i0] = half_bits_to_float(x0);
+        qs[i][i1] = half_bits_to_float(x1);
+    }
+    // stage K (padded rows) and V; rows past the sequence as zeros
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+        const int idx = tid + i * kAttnThreads;
+        const int r = idx / (VROW / 16), cpart = idx - r * (VROW / 16);
+        const bool live = r < n;
+        *reinterpret_cast<u32x4*>(ks + r * KROW + cpart * 16) = live ? kreg[i] : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(vs + r * VROW + cpart * 16) = live ? vreg[i] : u32x4{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+    // the new position: RoPE(k) and v from the projections (the cache holds
+    // the old contents until this launch writes it)
+    if (has_pos) {
+        const int r = pos - s0;
+        uint16_t* krow = reinterpret_cast<uint16_t*>(ks + r * KROW);
+        uint16_t* vrow = reinterpret_cast<uint16_t*>(vs + r * VROW);
+        const TER_GLOBAL uint16_t* kh = gptr(a.k) + (long long)g * HD;
+        const TER_GLOBAL uint16_t* vh = gptr(a.v) + (long long)g * HD;
+        for (int kk = tid; kk < HALF; kk += kAttnThreads) {
+            int i0, i1;
+            pair_index(kk, HD, a.neox != 0, i0, i1);
+            uint16_t x0 = kh[i0], x1 = kh[i1];
+            rope_pair(x0, x1, tab[2 * kk], tab[2 * kk + 1]);
+            krow[i0] = x0;
+            krow[i1] = x1;
+            if (writer) {
+                uint16_t* kd = a.kc + (long long)pos * row_stride + (long long)g * HD;
+                gptr(kd)[i0] = x0;
+                gptr(kd)[i1] = x1;
+            }
+        }
+        for (int d = tid; d < HD; d += kAttnThreads) {
+            const uint16_t x = vh[d];
+            vrow[d] = x;
+            if (writer) gptr(a.vc + (long long)pos * row_stride + (long long)g * HD)[d] = x;
+        }
+    }
+    __syncthreads();
+
+    // 3. scores: wave i = query head i, lane = position (the reference's dot order)
+    const bool head_ok = wave < nhg;
+    float score = -__builtin_inff();
+    if (head_ok && lane < n) {
+        float dot = 0.f;
+        const unsigned char* krow = ks + lane * KROW;
+#pragma unroll
+        for (int d8 = 0; d8 < HD; d8 += 8) {
+            const u32x4 kw = *reinterpret_cast<const u32x4*>(krow + d8 * 2);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                dot = __builtin_fmaf(qs[wave][d8 + 2 * j], half_bits_to_float((uint16_t)(kw[j] & 0xFFFFu)), dot);
+                dot = __builtin_fmaf(qs[wave][d8 + 2 * j + 1], half_bits_to_float((uint16_t)(kw[j] >> 16)), dot);
+            }
+        }
+        score = dot * a.inv_sqrt;
+    }
+    // 4. chunk softmax statistics per head
+    const float mc = wave_max_f(score);
+    const float e = lane < n ? attn_expf(score - mc) : 0.f;
+    float lsum = e;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) lsum = lsum + __shfl_xor(lsum, o);
+    es[wave][lane] = e;
+    __syncthreads();
+
+    // 5. output partials: thread (i, DPT consecutive d), positions in order
+    float acc[DPT];
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) acc[j] = 0.f;
+    const int d0 = DPT * lane;
+    if (head_ok) {
+        for (int s = 0; s < n; ++s) {
+            const float w = es[wave][s];
+            const uint16_t* vrow = reinterpret_cast<const uint16_t*>(vs + s * VROW) + d0;
+#pragma unroll
+            for (int j = 0; j < DPT; ++j) acc[j] = __builtin_fmaf(w, half_bits_to_float(vrow[j]), acc[j]);
+        }
+    }
+    // 6. publish the partials (written through), then count the arrival
+    if (head_ok && n > 0) {
+        float* P = a.part + ((long long)(h0 + wave) * a.n_chunks + chunk) * (HD + 2);
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) __hip_atomic_store(P + d0 + j, acc[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+            __hip_atomic_store(P + HD, mc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(P + HD + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are complete
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev =
+            __hip_atomic_fetch_add(a.count + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last_flag = prev == (unsigned)a.n_chunks - 1u;
+        if (last_flag) __hip_atomic_store(a.count + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last_flag || !head_ok) return;
+
+    // 7. combine (last workgroup of the group): chunks in order
+    const int nc = (seq + kChunk - 1) / kChunk;
+    const float* Ph = a.part + (long long)(h0 + wave) * a.n_chunks * (HD + 2);
+    float m_l = -__builtin_inff(), l_l = 0.f;
+    if (lane < nc) {
+        m_l = __hip_atomic_load(Ph + (long long)lane * (HD + 2) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        l_l = __hip_atomic_load(Ph + (long long)lane * (HD + 2) + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    const float M = wave_max_f(m_l);
+    cw[wave][lane] = lane < nc ? attn_expf(m_l - M) : 0.f;
+    cl[wave][lane] = l_l;
+    // (each wave reads only its own rows of cw / cl: a wave-local exchange)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+    float L = 0.f;
+    float O[DPT];
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) O[j] = 0.f;
+    for (int c = 0; c < nc; ++c) {
+        const float w = cw[wave][c];
+        L = __builtin_fmaf(cl[wave][c], w, L);
+        const float* Pc = Ph + (long long)c * (HD + 2) + d0;
+#pragma unroll
+        for (int j = 0; j < DPT; ++j)
+            O[j] = __builtin_fmaf(__hip_atomic_load(Pc + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), w, O[j]);
+    }
+    uint16_t* oh = a.out + (long long)(h0 + wave) * HD + d0;
+#pragma unroll
+    for (int j = 0; j < DPT; ++j) gptr(oh)[j] = float_to_half_bits(O[j] / L);
+}
+
+// Standalone RoPE on fp16 head vectors in place (rope_k), one thread per pair.
+__global__ void rope_kernel(uint16_t* v, int n_heads, int hd, const float* rope, const int32_t* pos_dev, int smax,
+                            int neox) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const int half = hd / 2;
+    if (idx >= n_heads * half) return;
+    const int h = idx / half, kk = idx - h * half;
+    const int pos = *gptr(pos_dev);
+    if (pos < 0 || pos >= smax) return;
+    int i0, i1;
+    pair_index(kk, hd, neox != 0, i0, i1);
+    uint16_t* vh = v + (long long)h * hd;
+    uint16_t x0 = gptr(vh)[i0], x1 = gptr(vh)[i1];
+    const TER_GLOBAL float* t = gptr(rope) + ((long long)pos * half + kk) * 2;
+    rope_pair(x0, x1, t[0], t[1]);
+    gptr(vh)[i0] = x0;
+    gptr(vh)[i1] = x1;
+}
+
+}  // namespace
+
+bool attn_supported_head_dim(int hd) { return hd == 64 || hd == 128; }
+int attn_chunk() { return kChunk; }
+int attn_max_chunks() { return kMaxChunks; }
+
+hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc,
+                              const int32_t* pos, uint16_t* out, const float* rope, float* part, unsigned* count,
+                              int nh, int nkv, int hd, int smax, bool neox, hipStream_t st) {
+    AttnArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.kc = kc;
+    a.vc = vc;
+    a.pos = pos;
+    a.out = out;
+    a.rope = rope;
+    a.part = part;
+    a.count = count;
+    a.nh = nh;
+    a.nkv = nkv;
+    a.smax = smax;
+    a.n_chunks = (smax + kChunk - 1) / kChunk;
+    a.neox = neox ? 1 : 0;
+    a.groups_per_kv = (nh / nkv + kAttnWaves - 1) / kAttnWaves;
+    a.inv_sqrt = (float)(1.0 / __builtin_sqrt((double)hd));
+    const dim3 grid(nkv * a.groups_per_kv * a.n_chunks), block(kAttnThreads);
+    if (hd == 128)
+        hipLaunchKernelGGL(attn_decode_kernel<128>, grid, block, 0, st, a);
+    else
+        hipLaunchKernelGGL(attn_decode_kernel<64>, grid, block, 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(uint16_t* v, int n_heads, int hd, const float* rope, const int32_t* pos, int smax, bool neox,
+                       hipStream_t st) {
+    const int n = n_heads * (hd / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3((n + 255) / 256), dim3(256), 0, st, v, n_heads, hd, rope, pos, smax,
+                       neox ? 1 : 0);
+    return hipGetLastError();
+}
+
+}  // namespace terhip

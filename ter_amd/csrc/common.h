@@ -108,6 +108,17 @@ hipError_t launch_argmax_f16(const uint16_t* logits, int n, int32_t* token_out, 
                              hipStream_t st);
 hipError_t launch_rmsnorm_f16_rows(const float* x, const uint16_t* gamma, float eps, int M, int H, uint16_t* y,
                                    hipStream_t st);
+// Decode attention (attention.hip): head_dim 64 or 128, chunks of
+// attn_chunk() positions, at most attn_max_chunks() chunks.
+bool attn_supported_head_dim(int hd);
+int attn_chunk();
+int attn_max_chunks();
+hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc,
+                              const int32_t* pos, uint16_t* out, const float* rope, float* part, unsigned* count,
+                              int nh, int nkv, int hd, int smax, bool neox, hipStream_t st);
+// Positions outside [0, smax) write nothing (both kernels).
+hipError_t launch_rope(uint16_t* v, int n_heads, int hd, const float* rope, const int32_t* pos, int smax, bool neox,
+                       hipStream_t st);
 // Rows per MFMA row block group: MB = 1, 2, 4, 8, 16 for M up to 16, 32, 64, 128, 256.
 int gemm_mb_of(int M);
 // vec: every x pointer 16-byte aligned and every ldx a multiple of 16.
@@ -157,8 +168,12 @@ __device__ inline float half_bits_to_float(uint16_t h) {
 }
 
 // binary32 -> binary16 in the default round-to-nearest-even mode (the
-// reference's __float2half of its fp16 outputs); overflow gives inf.
+// reference's __float2half of its fp16 outputs); overflow gives inf.  The
+// value is first pinned in a register as binary32: otherwise the compiler
+// may fold the producing multiply / fma into the conversion
+// (v_fma_mixlo_f16), rounding once to fp16 instead of to fp32 and then fp16.
 __device__ inline uint16_t float_to_half_bits(float f) {
+    asm volatile("" : "+v"(f));
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 

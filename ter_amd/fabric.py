@@ -387,6 +387,56 @@ def lm_head_argmax(hidden, gamma, token_embd, eps: float = 1e-5, token_out=None,
     return token_out
 
 
+class Attention:
+    """Decode-attention context (ter_hip_attn_*): RoPE + KV-cache write +
+    attention in one launch per layer (rope_k, kv_copy_k, attention_k,
+    cuda/ter_cuda_forward_bitnet.cu:185-214, 336-374)."""
+
+    def __init__(self, n_heads: int, n_kv_heads: int, head_dim: int, s_max: int, theta: float,
+                 neox: bool = True):
+        h = C.c_void_p()
+        L.check(L.lib().ter_hip_attn_create(C.byref(h), n_heads, n_kv_heads, head_dim, s_max, C.c_float(theta),
+                                            L.ROPE_NEOX if neox else L.ROPE_NORM), "ter_hip_attn_create")
+        self._h = h
+        self.n_heads, self.n_kv_heads, self.head_dim, self.s_max = n_heads, n_kv_heads, head_dim, s_max
+
+    def decode(self, q, k, v, k_cache, v_cache, pos_dev, out=None, stream=None):
+        """q fp16 [nh][hd], k, v fp16 [nkv][hd] (before RoPE); caches fp16
+        [s_max][nkv][hd]; pos_dev int32 [1].  Returns out fp16 [nh][hd]."""
+        torch = _torch()
+        for t, nm in ((q, "q"), (k, "k"), (v, "v"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+            if t.dtype != torch.float16 or not t.is_cuda:
+                raise TypeError(f"{nm} must be a CUDA float16 tensor")
+        if q.numel() != self.n_heads * self.head_dim or k.numel() != self.n_kv_heads * self.head_dim \
+                or v.numel() != k.numel():
+            raise ValueError("q, k or v has the wrong size")
+        if k_cache.numel() < self.s_max * self.n_kv_heads * self.head_dim or v_cache.numel() < k_cache.numel():
+            raise ValueError("caches must hold s_max positions")
+        if out is None:
+            out = torch.empty((self.n_heads, self.head_dim), dtype=torch.float16, device=q.device)
+        L.check(L.lib().ter_hip_attn_decode(self._h, q.data_ptr(), k.data_ptr(), v.data_ptr(), k_cache.data_ptr(),
+                                            v_cache.data_ptr(), pos_dev.data_ptr(), out.data_ptr(), _stream(stream)),
+                "ter_hip_attn_decode")
+        return out
+
+    def rope(self, x, pos_dev, stream=None):
+        """RoPE in place on fp16 head vectors x [n][hd]."""
+        n = x.numel() // self.head_dim
+        L.check(L.lib().ter_hip_rope(self._h, x.data_ptr(), n, pos_dev.data_ptr(), _stream(stream)), "ter_hip_rope")
+        return x
+
+    def close(self):
+        if getattr(self, "_h", None):
+            L.lib().ter_hip_attn_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Plan:
     """Many independent GEMVs in one launch (one work list).  `items` is a
     sequence of dicts: {w: PackedTrits, x: tensor, y?, acc?, y16?, resid?,

@@ -27,7 +27,7 @@ def declared_functions():
 
 def test_library_exports_every_declared_symbol():
     names = declared_functions()
-    assert len(names) == 35, names
+    assert len(names) == 39, names
     lib = L.lib()
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
@@ -174,6 +174,21 @@ def test_lm_head_validation_without_device():
     assert lib.ter_hip_lm_head_argmax(*bad) == L.ERR_ALIGN
     bad = list(args); bad[2] = float("nan")
     assert lib.ter_hip_lm_head_argmax(*bad) == L.ERR_SHAPE
+
+
+def test_attention_validation_without_device():
+    lib = L.lib()
+    h = C.c_void_p()
+    create = lib.ter_hip_attn_create
+    assert create(None, 20, 5, 128, 2048, 5e5, L.ROPE_NEOX) == L.ERR_NULL
+    assert create(C.byref(h), 20, 6, 128, 2048, 5e5, L.ROPE_NEOX) == L.ERR_SHAPE   # heads not a multiple
+    assert create(C.byref(h), 20, 5, 96, 2048, 5e5, L.ROPE_NEOX) == L.ERR_SHAPE    # head_dim
+    assert create(C.byref(h), 20, 5, 128, 4097, 5e5, L.ROPE_NEOX) == L.ERR_SHAPE   # > 64 chunks of 64
+    assert create(C.byref(h), 20, 5, 128, 2048, 5e5, 7) == L.ERR_PAYLOAD
+    assert create(C.byref(h), 20, 5, 128, 2048, 0.0, L.ROPE_NEOX) == L.ERR_SHAPE
+    fake = 1 << 20
+    assert lib.ter_hip_attn_decode(None, fake, fake, fake, fake, fake, fake, fake, None) == L.ERR_NULL
+    assert lib.ter_hip_rope(None, fake, 1, fake, None) == L.ERR_NULL
 
 
 def test_mm_row_rejects_non_int8_activations():

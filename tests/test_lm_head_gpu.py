@@ -50,6 +50,27 @@ def test_rmsnorm_f16_rows(cuda, H):
         assert (f16_bits(y[r]) == f16_bits(want)).all(), r
 
 
+def test_rmsnorm_f16_double_rounding(cuda):
+    """y = half(fp32((x * rms_inv) * gamma)): the product is rounded to fp32
+    first, as the reference's __float2half of a float expression; rounding
+    the exact product straight to fp16 differs where the fp32 value lands on
+    an fp16 tie.  64 rows of 2560 hold such elements (counted here)."""
+    import ter_amd as T
+    rng = np.random.default_rng(77)
+    H = 2560
+    X = (rng.standard_normal((64, H)) * 3).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, H).astype(np.float16)
+    y = host(T.rmsnorm_f16(dev(X), dev(g), 1e-5))
+    sensitive = 0
+    for r in range(64):
+        want, rinv = O.rmsnorm_f16(X[r], g, 1e-5)
+        assert (f16_bits(y[r]) == f16_bits(want)).all(), r
+        a = (X[r] * rinv).astype(np.float32)
+        exact = a.astype(np.float64) * g.astype(np.float64)
+        sensitive += int((exact.astype(np.float16) != exact.astype(np.float32).astype(np.float16)).sum())
+    assert sensitive > 0
+
+
 @pytest.mark.parametrize("H,V", [(2560, 1000), (2560, 4097), (2048, 300), (64, 33), (1000, 300), (2056, 129),
                                  (100, 50), (2561, 77), (8200, 50), (2, 5)],
                          ids=["bitnet-h", "odd-v", "llama-h", "one-group", "masked-groups", "partial-group",

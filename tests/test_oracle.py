@@ -519,3 +519,134 @@ def test_argmax_nan_and_minus_inf_never_win():
     assert O.argmax_f16(lg) == 777
     lg[900] = np.float16(np.inf)
     assert O.argmax_f16(lg) == 900
+
+
+# ---------------------------------------------------------------------------
+# Decode attention: NEOX RoPE (rope_k, cuda/ter_cuda_forward_bitnet.cu:185-200),
+# attention_k (:336-374) in the reference's order and in the chunked order the
+# GPU kernel uses, and the binary32 exp both use.
+# ---------------------------------------------------------------------------
+
+def test_expf_is_faithful_and_exact_at_special_points():
+    x = np.linspace(-103.9, 88.72, 1_000_001).astype(np.float32)
+    y = O.expf(x)
+    ref = np.exp(x.astype(np.float64))
+    normal = ref > 1.2e-38
+    ulp = np.abs(y[normal] - ref[normal]) / np.spacing(ref[normal].astype(np.float32)).astype(np.float64)
+    assert ulp.max() < 1.0  # faithful rounding everywhere in the normal range
+    sub = ~normal  # subnormal results: within one subnormal step
+    assert (np.abs(y[sub] - ref[sub]) <= 2.0 ** -149).all()
+    sp = O.expf(np.array([0.0, -0.0, np.inf, -np.inf, -200.0, 100.0], np.float32))
+    assert list(sp[:2]) == [1.0, 1.0] and sp[2] == np.inf and sp[3] == 0.0 and sp[4] == 0.0 and sp[5] == np.inf
+    assert np.isnan(O.expf(np.array([np.nan], np.float32))[0])
+
+
+def test_rope_table_steps():
+    theta, hd = 500000.0, 128
+    cs = O.rope_table(theta, hd, 3000)
+    assert (cs[0, :, 0] == 1.0).all() and (cs[0, :, 1] == 0.0).all()
+    p = np.arange(3000)
+    # pair 0: freq = 1, so a = p exactly
+    assert (cs[:, 0, 0] == np.cos(p.astype(np.float64)).astype(np.float32)).all()
+    assert (cs[:, 0, 1] == np.sin(p.astype(np.float64)).astype(np.float32)).all()
+    for k in (1, 17, 63):
+        pw = np.float32(np.float64(theta) ** np.float64(np.float32(2 * k) / np.float32(hd)))
+        freq = np.float32(1.0) / pw
+        a = (p.astype(np.float32) * freq).astype(np.float32)
+        assert (cs[:, k, 0] == np.cos(a.astype(np.float64)).astype(np.float32)).all()
+
+
+def test_rope_neox_pairs_k_with_k_plus_half():
+    """A unit vector e_k rotates into (c at k, s at k + hd/2): NEOX pairing,
+    not interleaved (2k, 2k+1).  Position 0 is the identity."""
+    hd = 128
+    cs = O.rope_table(500000.0, hd, 100)
+    rng = np.random.default_rng(31)
+    v = rng.standard_normal((3, hd)).astype(np.float16)
+    assert (O.rope_f16(v, cs[0]).view(np.uint16) == v.view(np.uint16)).all()
+    for k in (0, 5, 63):
+        e = np.zeros((1, hd), np.float16)
+        e[0, k] = 1.0
+        r = O.rope_f16(e, cs[77])
+        want = np.zeros(hd, np.float16)
+        want[k] = np.float16(cs[77, k, 0])
+        want[k + hd // 2] = np.float16(cs[77, k, 1])
+        assert (r[0] == want).all(), k  # value equality: the zero entries may come out as -0
+    # NORM pairing (the Llama forward): e_{2k} rotates into (c at 2k, s at 2k+1)
+    for k in (0, 31):
+        e = np.zeros((1, hd), np.float16)
+        e[0, 2 * k] = 1.0
+        r = O.rope_f16(e, cs[77], neox=False)
+        want = np.zeros(hd, np.float16)
+        want[2 * k] = np.float16(cs[77, k, 0])
+        want[2 * k + 1] = np.float16(cs[77, k, 1])
+        assert (r[0] == want).all(), k
+    # the rotation keeps each pair's norm (to fp16 rounding)
+    r = O.rope_f16(v, cs[99]).astype(np.float64)
+    n0 = v[:, :64].astype(np.float64) ** 2 + v[:, 64:].astype(np.float64) ** 2
+    n1 = r[:, :64] ** 2 + r[:, 64:] ** 2
+    assert np.allclose(n0, n1, rtol=3e-3, atol=1e-6)
+
+
+def _attention_f64(q, K, V):
+    nh, hd = q.shape
+    seq, nkv, _ = K.shape
+    out = np.empty((nh, hd))
+    bound = np.empty((nh, hd))
+    for h in range(nh):
+        g = h * nkv // nh
+        sc = (K[:, g, :].astype(np.float64) @ q[h].astype(np.float64)) / np.sqrt(hd)
+        p = np.exp(sc - sc.max())
+        p /= p.sum()
+        out[h] = p @ V[:, g, :].astype(np.float64)
+        bound[h] = p @ np.abs(V[:, g, :].astype(np.float64))
+    return out, bound
+
+
+def _kv(seed, seq, nh=20, nkv=5, hd=128):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((nh, hd)).astype(np.float16)
+    K = rng.standard_normal((seq, nkv, hd)).astype(np.float16)
+    V = rng.standard_normal((seq, nkv, hd)).astype(np.float16)
+    return q, K, V
+
+
+def test_attention_ref_closed_forms():
+    q, K, V = _kv(41, 1)
+    o16, o32 = O.attention_ref(q, K, V)
+    for h in range(20):  # one position: softmax weight exactly 1, out = v of its KV head
+        assert (o16[h].view(np.uint16) == V[0, h // 4].view(np.uint16)).all()
+    q0 = np.zeros_like(q)
+    q, K, V = _kv(42, 300)
+    o16, o32 = O.attention_ref(q0, K, V)  # equal scores: out = mean of v
+    mean = V.astype(np.float64).mean(axis=0)
+    for h in range(20):
+        assert np.abs(o32[h] - mean[h // 4]).max() < 1e-5
+    # GQA mapping: query head h reads KV head h * nkv / nh
+    qg, Kg, Vg = _kv(43, 50, nh=4, nkv=2)
+    Vg[:, 1, :] += np.float16(100)
+    o16, o32 = O.attention_ref(qg, Kg, Vg)
+    assert (o32[:2] < 50).all() and (o32[2:] > 50).all()
+
+
+@pytest.mark.parametrize("seq", [7, 64, 65, 300, 2048])
+def test_attention_orders_within_rounding_bound(seq):
+    """Both orders against float64 softmax attention: |err| <= 2e-6 * sum_s
+    p_s |v_sd| + 1e-7 (fp32 rounding of 2048-term sums and the exp's one
+    ulp); the fp16 outputs of the two orders differ by at most one ulp."""
+    q, K, V = _kv(seq, seq)
+    want, bound = _attention_f64(q, K, V)
+    r16, r32 = O.attention_ref(q, K, V)
+    s16, s32 = O.attention_splitk(q, K, V)
+    tol = 2e-6 * bound + 1e-7
+    assert (np.abs(r32 - want) <= tol).all()
+    assert (np.abs(s32 - want) <= tol).all()
+    d = np.abs(r16.view(np.uint16).astype(np.int64) - s16.view(np.uint16).astype(np.int64))
+    assert d.max() <= 1
+
+
+def test_attention_splitk_equals_ref_on_one_position():
+    q, K, V = _kv(44, 1)
+    a = O.attention_ref(q, K, V)
+    b = O.attention_splitk(q, K, V)
+    assert (a[1].view(np.uint32) == b[1].view(np.uint32)).all()
