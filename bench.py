@@ -526,6 +526,86 @@ def run_lm_head(args):
     }
 
 
+def run_attention(args):
+    """Decode attention of the C5 model (BitNet-2B-4T shape: 30 layers, 20
+    query / 5 KV heads, head_dim 128, NEOX RoPE theta 5e5) with the KV cache
+    filled to 2048 positions (N(0,1) fp16): one step = the 30 layers'
+    attention launches for the token at position 2047 (RoPE + cache write +
+    attention each), rotating over 2 copies of the whole cache (315 MB, beyond
+    the 256 MB Infinity Cache)."""
+    import numpy as np
+    import torch
+    import ter_amd as T
+    NL, NH, NKV, HD, S = 30, 20, 5, 128, 2048
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2048)
+    A = T.Attention(NH, NKV, HD, S, 500000.0, True)
+    caches = [[(torch.randn(S, NKV, HD, generator=g, device="cuda").to(torch.float16),
+                torch.randn(S, NKV, HD, generator=g, device="cuda").to(torch.float16)) for _ in range(NL)]
+              for _ in range(2)]
+    q = torch.randn(NH, HD, generator=g, device="cuda").to(torch.float16)
+    k = torch.randn(NKV, HD, generator=g, device="cuda").to(torch.float16)
+    v = torch.randn(NKV, HD, generator=g, device="cuda").to(torch.float16)
+    out = torch.empty(NH, HD, dtype=torch.float16, device="cuda")
+    pos = torch.full((1,), S - 1, dtype=torch.int32, device="cuda")
+
+    def token(c):
+        for kc, vc in caches[c]:
+            A.decode(q, k, v, kc, vc, pos, out)
+    rot = graph_of(lambda: [token(c) for c in range(2)])
+    settle(rot.replay)
+    for _ in range(max(1, args.warmup // 2)):
+        rot.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_start = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps // 2):
+        rot.replay()
+    for i in range(args.steps % 2):
+        token(i)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t_start) * 1e3 / args.steps
+    ev_tok = e0.elapsed_time(e1) / args.steps
+    layer_bytes = 2 * S * NKV * HD * 2 + NH * HD * 2 * 2 + 2 * NKV * HD * 2 * 2 + HD * 4
+    gbs = NL * layer_bytes / (ev_tok * 1e-3) / 1e9
+    log(f"[bench] attention: {ev_tok * 1e3:.2f} us/token (30 layers), {ev_tok * 1e3 / NL:.2f} us/layer, {gbs:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        qh, Kh, Vh = q.cpu().numpy(), caches[0][0][0].cpu().numpy(), caches[0][0][1].cpu().numpy()
+        n, t_cpu = 0, 0.0
+        t_begin = time.perf_counter()
+        while True:
+            t0 = time.perf_counter()
+            O.attention_ref(qh, Kh, Vh)
+            t_cpu += time.perf_counter() - t0
+            n += 1
+            if time.perf_counter() - t_begin > args.cpu_seconds:
+                break
+        cpu = dict(value=round(n * 2 * S * NKV * HD * 2 / t_cpu / 1e9, 3), unit="GB/s", cores=1, kind="port",
+                   sample=f"oracle orc_attention_ref (C restatement of attention_k's sequential order) on one layer "
+                          f"at 2048 positions, {n} runs, {t_cpu:.1f} s, 1 thread; GB/s of K/V read")
+        log(f"[bench] cpu baseline: {cpu}")
+    return {
+        "metric": "decode attention (RoPE + KV write + attention) over a 2048-position fp16 KV cache, HBM GB/s",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16", "data": "synthetic",
+        "config": {"workload": "C5 attention: bitnet-b1.58-2b-4t 30 layers, 20/5 heads, head_dim 128, NEOX RoPE "
+                               "theta 5e5, KV cache at 2048 positions, one launch per layer, 2 rotated cache copies",
+                   "us_per_token": round(ev_tok * 1e3, 2), "us_per_layer": round(ev_tok * 1e3 / NL, 3)},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("attn_decode_kernel", "bitnet_attention_2048"),
+                     "kernel": "attn_decode_kernel", "bytes_per_launch": layer_bytes,
+                     "mean_launch_us": round(ev_tok * 1e3 / NL, 3)},
+        "cpu_baseline": cpu,
+    }
+
+
 def run_copy(args):
     """A plain copy-shaped kernel of known size (torch.neg over 256 MiB of
     fp32: 256 MiB read, 256 MiB written per launch).  Its rocprofv3
@@ -549,7 +629,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", choices=["llama", "bitnet", "batched", "lm_head", "copy"], default="llama")
+    ap.add_argument("--config", choices=["llama", "bitnet", "batched", "lm_head", "attention", "copy"],
+                    default="llama")
     ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
     ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -569,6 +650,8 @@ def main():
         out = run_copy(args)
     elif args.config == "lm_head":
         out = run_lm_head(args)
+    elif args.config == "attention":
+        out = run_attention(args)
     else:
         cfg = LLAMA if args.config == "llama" else BITNET
         out = run_m1(args, cfg, fp32_x=(args.config == "bitnet"))

@@ -115,10 +115,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     constexpr int VROW = HD * 2;
     constexpr int HALF = HD / 2;
     constexpr int DPT = HD / 64;       // output elements per thread
+    static_assert(kAttnWaves * HALF <= kAttnThreads && HD <= kAttnThreads, "one RoPE pair / v element per thread");
     __shared__ __align__(16) unsigned char ks[kChunk * KROW];
     __shared__ __align__(16) unsigned char vs[kChunk * VROW];
-    __shared__ __align__(16) float qs[kAttnWaves][HD];
-    __shared__ float es[kAttnWaves][kChunk];
+    __shared__ __align__(16) uint16_t qs[kAttnWaves][HD];  // RoPE'd query heads (fp16, as the reference rounds them)
+    __shared__ __align__(16) float es[kAttnWaves][kChunk];
     __shared__ float cw[kAttnWaves][kMaxChunks];  // combine: w_c
     __shared__ float cl[kAttnWaves][kMaxChunks];  // combine: l_c
     __shared__ int last_flag;
@@ -149,6 +150,24 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
             vreg[i] = *reinterpret_cast<const TER_GLOBAL u32x4*>(gptr(a.vc) + off);
         }
     }
+    // the new token's q pair, k pair and v element of this thread (one each:
+    // nhg * hd/2 <= 256 query pairs), also before the position is known
+    const int qi = tid / HALF, qk = tid - qi * HALF;  // query head of the group, pair
+    int q0, q1;
+    pair_index(qk, HD, a.neox != 0, q0, q1);
+    const bool has_q = tid < nhg * HALF;
+    uint16_t qx0 = 0, qx1 = 0, kx0 = 0, kx1 = 0, vx = 0;
+    if (has_q) {
+        const TER_GLOBAL uint16_t* qh = gptr(a.q) + (long long)(h0 + qi) * HD;
+        qx0 = qh[q0];
+        qx1 = qh[q1];
+    }
+    if (tid < HALF) {  // pair tid of the KV head's key (same indices as q pair tid)
+        const TER_GLOBAL uint16_t* kh = gptr(a.k) + (long long)g * HD;
+        kx0 = kh[q0];
+        kx1 = kh[q1];
+    }
+    if (tid < HD) vx = gptr(a.v)[(long long)g * HD + tid];
     const int pos = *gptr(a.pos);
     if (pos < 0 || pos >= a.smax) return;                     // (the whole grid: no output, no count)
     const int seq = pos + 1;
@@ -158,15 +177,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 
     // 2. RoPE of the group's query heads into qs (as the fp16-rounded values).
     const TER_GLOBAL float* tab = gptr(a.rope) + (long long)pos * HD;  // [hd/2][2] of this position
-    for (int idx = tid; idx < nhg * HALF; idx += kAttnThreads) {
-        const int i = idx / HALF, kk = idx - i * HALF;
-        int i0, i1;
-        pair_index(kk, HD, a.neox != 0, i0, i1);
-        const TER_GLOBAL uint16_t* qh = gptr(a.q) + (long long)(h0 + i) * HD;
-        uint16_t x0 = qh[i0], x1 = qh[i1];
-        rope_pair(x0, x1, tab[2 * kk], tab[2 * kk + 1]);
-        qs[i][i0] = half_bits_to_float(x0);
-        qs[i][i1] = half_bits_to_float(x1);
+    const float rc = tab[2 * qk], rsn = tab[2 * qk + 1];
+    if (has_q) {
+        rope_pair(qx0, qx1, rc, rsn);
+        qs[qi][q0] = qx0;
+        qs[qi][q1] = qx1;
     }
     // stage K (padded rows) and V; rows past the sequence as zeros
 #pragma unroll
@@ -184,25 +199,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         const int r = pos - s0;
         uint16_t* krow = reinterpret_cast<uint16_t*>(ks + r * KROW);
         uint16_t* vrow = reinterpret_cast<uint16_t*>(vs + r * VROW);
-        const TER_GLOBAL uint16_t* kh = gptr(a.k) + (long long)g * HD;
-        const TER_GLOBAL uint16_t* vh = gptr(a.v) + (long long)g * HD;
-        for (int kk = tid; kk < HALF; kk += kAttnThreads) {
-            int i0, i1;
-            pair_index(kk, HD, a.neox != 0, i0, i1);
-            uint16_t x0 = kh[i0], x1 = kh[i1];
-            rope_pair(x0, x1, tab[2 * kk], tab[2 * kk + 1]);
-            krow[i0] = x0;
-            krow[i1] = x1;
+        if (tid < HALF) {  // pair tid: the same table entry as query pair tid
+            rope_pair(kx0, kx1, rc, rsn);
+            krow[q0] = kx0;
+            krow[q1] = kx1;
             if (writer) {
                 uint16_t* kd = a.kc + (long long)pos * row_stride + (long long)g * HD;
-                gptr(kd)[i0] = x0;
-                gptr(kd)[i1] = x1;
+                gptr(kd)[q0] = kx0;
+                gptr(kd)[q1] = kx1;
             }
         }
-        for (int d = tid; d < HD; d += kAttnThreads) {
-            const uint16_t x = vh[d];
-            vrow[d] = x;
-            if (writer) gptr(a.vc + (long long)pos * row_stride + (long long)g * HD)[d] = x;
+        if (tid < HD) {
+            vrow[tid] = vx;
+            if (writer) gptr(a.vc + (long long)pos * row_stride + (long long)g * HD)[tid] = vx;
         }
     }
     __syncthreads();
@@ -211,16 +220,28 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     const bool head_ok = wave < nhg;
     float score = -__builtin_inff();
     if (head_ok && lane < n) {
+        // blocks of 32 d: the block's K row and query values are read from
+        // LDS into registers together, then the 32-step chain runs
         float dot = 0.f;
         const unsigned char* krow = ks + lane * KROW;
+        const unsigned char* qrow = reinterpret_cast<const unsigned char*>(qs[wave]);
 #pragma unroll
-        for (int d8 = 0; d8 < HD; d8 += 8) {
-            const u32x4 kw = *reinterpret_cast<const u32x4*>(krow + d8 * 2);
+        for (int b = 0; b < HD; b += 32) {
+            u32x4 kw[4], qw[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                dot = __builtin_fmaf(qs[wave][d8 + 2 * j], half_bits_to_float((uint16_t)(kw[j] & 0xFFFFu)), dot);
-                dot = __builtin_fmaf(qs[wave][d8 + 2 * j + 1], half_bits_to_float((uint16_t)(kw[j] >> 16)), dot);
+            for (int i = 0; i < 4; ++i) {
+                kw[i] = *reinterpret_cast<const u32x4*>(krow + (b + 8 * i) * 2);
+                qw[i] = *reinterpret_cast<const u32x4*>(qrow + (b + 8 * i) * 2);
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    dot = __builtin_fmaf(half_bits_to_float((uint16_t)(qw[i][j] & 0xFFFFu)),
+                                         half_bits_to_float((uint16_t)(kw[i][j] & 0xFFFFu)), dot);
+                    dot = __builtin_fmaf(half_bits_to_float((uint16_t)(qw[i][j] >> 16)),
+                                         half_bits_to_float((uint16_t)(kw[i][j] >> 16)), dot);
+                }
         }
         score = dot * a.inv_sqrt;
     }
@@ -233,17 +254,39 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     es[wave][lane] = e;
     __syncthreads();
 
-    // 5. output partials: thread (i, DPT consecutive d), positions in order
+    // 5. output partials: thread (i, DPT consecutive d), positions in order.
+    // All 64 rows: past n, e = 0 and the V row is zero, so those steps add +0
+    // to an accumulator that is never -0 (exact no-ops), and the loop is
+    // unrolled with its LDS reads scheduled ahead.
     float acc[DPT];
 #pragma unroll
     for (int j = 0; j < DPT; ++j) acc[j] = 0.f;
     const int d0 = DPT * lane;
     if (head_ok) {
-        for (int s = 0; s < n; ++s) {
-            const float w = es[wave][s];
-            const uint16_t* vrow = reinterpret_cast<const uint16_t*>(vs + s * VROW) + d0;
+        // blocks of 16 positions: their weights and V values are read from
+        // LDS into registers together, then the block's steps run in order
 #pragma unroll
-            for (int j = 0; j < DPT; ++j) acc[j] = __builtin_fmaf(w, half_bits_to_float(vrow[j]), acc[j]);
+        for (int b = 0; b < kChunk; b += 16) {
+            float wv[16];
+            uint16_t vv[16][DPT];
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const float4 w4 = *reinterpret_cast<const float4*>(&es[wave][b + i]);
+                wv[i] = w4.x;
+                wv[i + 1] = w4.y;
+                wv[i + 2] = w4.z;
+                wv[i + 3] = w4.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint16_t* vrow = reinterpret_cast<const uint16_t*>(vs + (b + i) * VROW) + d0;
+#pragma unroll
+                for (int j = 0; j < DPT; ++j) vv[i][j] = vrow[j];
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+#pragma unroll
+                for (int j = 0; j < DPT; ++j) acc[j] = __builtin_fmaf(wv[i], half_bits_to_float(vv[i][j]), acc[j]);
         }
     }
     // 6. publish the partials (written through), then count the arrival
@@ -268,13 +311,30 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     __syncthreads();
     if (!last_flag || !head_ok) return;
 
-    // 7. combine (last workgroup of the group): chunks in order
+    // 7. combine (last workgroup of the group): chunks in order.  The
+    // partials are read with system-coherent (SC1) buffer loads, which miss
+    // any stale copy in this XCD's L2, all issued before the first is used.
     const int nc = (seq + kChunk - 1) / kChunk;
     const float* Ph = a.part + (long long)(h0 + wave) * a.n_chunks * (HD + 2);
+    const __amdgpu_buffer_rsrc_t pr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)Ph, 0, nc * (HD + 2) * 4, 0x00020000);
+    constexpr int kSC1 = 16;  // cache policy: system coherent
     float m_l = -__builtin_inff(), l_l = 0.f;
     if (lane < nc) {
-        m_l = __hip_atomic_load(Ph + (long long)lane * (HD + 2) + HD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        l_l = __hip_atomic_load(Ph + (long long)lane * (HD + 2) + HD + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        m_l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (lane * (HD + 2) + HD) * 4, 0, kSC1));
+        l_l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (lane * (HD + 2) + HD + 1) * 4, 0, kSC1));
+    }
+    float pv[kMaxChunks][DPT];  // o_c[d0 .. d0 + DPT) for every chunk (zeros past nc: out of range)
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+        if constexpr (DPT == 2) {
+            const unsigned long long w2 = __builtin_bit_cast(
+                unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(pr, (c * (HD + 2) + d0) * 4, 0, kSC1));
+            pv[c][0] = __builtin_bit_cast(float, (unsigned)w2);
+            pv[c][1] = __builtin_bit_cast(float, (unsigned)(w2 >> 32));
+        } else {
+            pv[c][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (c * (HD + 2) + d0) * 4, 0, kSC1));
+        }
     }
     const float M = wave_max_f(m_l);
     cw[wave][lane] = lane < nc ? attn_expf(m_l - M) : 0.f;
@@ -286,13 +346,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     float O[DPT];
 #pragma unroll
     for (int j = 0; j < DPT; ++j) O[j] = 0.f;
-    for (int c = 0; c < nc; ++c) {
+    // chunks past nc have w = 0 and o = 0 (out-of-range loads): exact no-ops
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
         const float w = cw[wave][c];
         L = __builtin_fmaf(cl[wave][c], w, L);
-        const float* Pc = Ph + (long long)c * (HD + 2) + d0;
 #pragma unroll
-        for (int j = 0; j < DPT; ++j)
-            O[j] = __builtin_fmaf(__hip_atomic_load(Pc + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), w, O[j]);
+        for (int j = 0; j < DPT; ++j) O[j] = __builtin_fmaf(pv[c][j], w, O[j]);
     }
     uint16_t* oh = a.out + (long long)(h0 + wave) * HD + d0;
 #pragma unroll
