@@ -606,6 +606,70 @@ def run_attention(args):
     }
 
 
+def run_decode(args):
+    """C5: end-to-end greedy decode of a random-init BitNet-2B-4T-shaped model
+    (30 layers, hidden 2560, 20/5 heads of 128, NEOX RoPE 5e5, relu^2 FFN
+    6912, tied fp16 token_embd 128256 x 2560) with the KV cache pre-filled to
+    2048 positions (N(0,1) fp16).  One step = one token: embedding, 30 layers
+    of five launches (Q/K/V plan, attention, o plan, gate/up plan, down plan)
+    and the fused RMSNorm + lm_head + argmax, replayed from one HIP graph."""
+    import torch
+    from ter_amd import bitnet as B
+    c = B.Shape()
+    t0 = time.perf_counter()
+    model = B.random_model(c, seed=5)
+    start, steps = 2048, args.steps
+    dec = B.Decoder(model, start + max(steps, args.warmup, 64) + 64)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(6)
+    for t in (dec.K, dec.V):
+        t.copy_(torch.randn(t.shape, generator=g, device="cuda").to(torch.float16))
+    graph = dec.capture()
+    log(f"[bench] decode: model + caches built in {time.perf_counter() - t0:.1f} s")
+
+    def run(n):
+        dec.pos.fill_(start)
+        dec.token.fill_(1)
+        for _ in range(n):
+            graph.replay()
+    run(args.warmup)
+    torch.cuda.synchronize()
+    dec.pos.fill_(start)
+    dec.token.fill_(1)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_start = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_tok = (time.perf_counter() - t_start) * 1e3 / steps
+    ev_tok = e0.elapsed_time(e1) / steps
+    shapes = B.proj_shapes(c)
+    w_bytes = sum(K * N // 4 for K, N in shapes.values()) * c.Nl
+    kv_bytes = 2 * (start + steps // 2) * c.Nkv * c.Hd * 2 * c.Nl
+    lm_bytes = c.V * c.H * 2
+    tok_bytes = w_bytes + kv_bytes + lm_bytes
+    log(f"[bench] decode: {ev_tok * 1e3:.1f} us/token (events), {1e3 / ms_tok:.0f} tokens/s (wall), "
+        f"{tok_bytes / (ev_tok * 1e-3) / 1e9:.0f} GB/s over {tok_bytes / 1e6:.0f} MB/token")
+    return {
+        "metric": "end-to-end greedy decode tokens/s (BitNet-2B-4T shape, KV 2048)",
+        "value": round(1e3 / ms_tok, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_tok, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "C5: random-init bitnet-b1.58-2b-4t-shaped decode, 30 layers, KV cache pre-filled "
+                               "to 2048 positions, one HIP graph per token",
+                   "launches_per_token": dec.launches_per_token(), "us_per_token": round(ev_tok * 1e3, 2),
+                   "bytes_per_token": tok_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(tok_bytes / (ev_tok * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(tok_bytes / (ev_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "whole step", "bytes_per_launch": tok_bytes,
+                     "mean_launch_us": round(ev_tok * 1e3, 2)},
+        "cpu_baseline": None,
+    }
+
+
 def run_copy(args):
     """A plain copy-shaped kernel of known size (torch.neg over 256 MiB of
     fp32: 256 MiB read, 256 MiB written per launch).  Its rocprofv3
@@ -629,7 +693,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", choices=["llama", "bitnet", "batched", "lm_head", "attention", "copy"],
+    ap.add_argument("--config", choices=["llama", "bitnet", "batched", "lm_head", "attention", "decode", "copy"],
                     default="llama")
     ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
     ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
@@ -652,6 +716,8 @@ def main():
         out = run_lm_head(args)
     elif args.config == "attention":
         out = run_attention(args)
+    elif args.config == "decode":
+        out = run_decode(args)
     else:
         cfg = LLAMA if args.config == "llama" else BITNET
         out = run_m1(args, cfg, fp32_x=(args.config == "bitnet"))

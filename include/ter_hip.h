@@ -312,11 +312,17 @@ int ter_hip_argmax_f16(const uint16_t* logits, int32_t N, int32_t* out_idx, uint
 /* The whole tail in ONE launch (rmsnorm_f32_in_k + mm_fp16_lm_head_k +
  * argmax, :890-911): hidden fp32 [H] -> x_norm -> logits -> *token_out.
  * x_norm_out (fp16 [H]) and logits_out (fp16 [V]) are optional copies;
- * token_out and state (as ter_hip_argmax_f16) are required.  H even;
- * hidden 8-byte and gamma 4-byte aligned. */
+ * token_out and state (as ter_hip_argmax_f16) are required.  pos_advance
+ * (optional, device int32) is incremented once the token is written: the
+ * step's inc_pos_k (:912).  H even; hidden 8-byte and gamma 4-byte aligned. */
 int ter_hip_lm_head_argmax(const float* hidden, const uint16_t* gamma, float eps,
                            const uint16_t* token_embd, int32_t H, int32_t V, uint16_t* x_norm_out,
-                           uint16_t* logits_out, int32_t* token_out, uint64_t* state, void* stream);
+                           uint16_t* logits_out, int32_t* token_out, uint64_t* state,
+                           int32_t* pos_advance, void* stream);
+/* The step's first kernel, token_embed_lookup_k (:220-231): hidden fp32 [H] =
+ * token_embd[*token_dev] widened (a token outside [0, V) writes nothing). */
+int ter_hip_embed_f16(const uint16_t* token_embd, int32_t V, int32_t H, const int32_t* token_dev,
+                      float* hidden, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Decode attention: RoPE + KV-cache write + attention, one launch per      */

@@ -13,6 +13,7 @@ from .fabric import (  # noqa: F401
     PackedTrits,
     Plan,
     argmax_f16,
+    embed_f16,
     gemv,
     lm_head_argmax,
     lm_head_f16,
@@ -28,6 +29,26 @@ from .fabric import (  # noqa: F401
     synth_v11,
 )
 
-__all__ = ["ArgmaxState", "Attention", "GemmPlan", "Handle", "PackedTrits", "Plan", "argmax_f16", "gemv", "lm_head_argmax",
-           "lm_head_f16", "mm_batched", "mm_packed_dispatch", "mm_packed_dispatch_f16", "mm_row", "quant_int8",
-           "relu2_rmsnorm_quant", "rmsnorm_f16", "rmsnorm_quant", "synth_i8", "synth_v11"]
+__all__ = [
+    "ArgmaxState",
+    "Attention",
+    "GemmPlan",
+    "Handle",
+    "PackedTrits",
+    "Plan",
+    "argmax_f16",
+    "embed_f16",
+    "gemv",
+    "lm_head_argmax",
+    "lm_head_f16",
+    "mm_batched",
+    "mm_packed_dispatch",
+    "mm_packed_dispatch_f16",
+    "mm_row",
+    "quant_int8",
+    "relu2_rmsnorm_quant",
+    "rmsnorm_f16",
+    "rmsnorm_quant",
+    "synth_i8",
+    "synth_v11",
+]

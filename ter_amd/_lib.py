@@ -146,7 +146,8 @@ SIGNATURES = [
     ("ter_hip_rmsnorm_f16", C.c_int, [_P, _P, C.c_float, C.c_int32, C.c_int32, _P, _P]),
     ("ter_hip_lm_head_f16", C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
     ("ter_hip_argmax_f16", C.c_int, [_P, C.c_int32, _P, _P, _P]),
-    ("ter_hip_lm_head_argmax", C.c_int, [_P, _P, C.c_float, _P, C.c_int32, C.c_int32, _P, _P, _P, _P, _P]),
+    ("ter_hip_lm_head_argmax", C.c_int, [_P, _P, C.c_float, _P, C.c_int32, C.c_int32, _P, _P, _P, _P, _P, _P]),
+    ("ter_hip_embed_f16", C.c_int, [_P, C.c_int32, C.c_int32, _P, _P, _P]),
     ("ter_hip_attn_create", C.c_int, [C.POINTER(C.c_void_p), C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
                                       C.c_int32]),
     ("ter_hip_attn_decode", C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P]),

@@ -922,7 +922,7 @@ int ter_hip_lm_head_f16(const uint16_t* x_norm, const uint16_t* token_embd, uint
     rc = pick_lm_head_wg(H, V, &n_wg);
     if (rc) return rc;
     hipError_t e = launch_lm_head(nullptr, nullptr, 0.f, x_norm, token_embd, H, V, nullptr, logits, nullptr, nullptr,
-                                  n_wg, static_cast<hipStream_t>(stream));
+                                  nullptr, n_wg, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "lm_head launch");
     return TER_HIP_OK;
 }
@@ -944,22 +944,34 @@ int ter_hip_argmax_f16(const uint16_t* logits, int32_t N, int32_t* out_idx, uint
     return TER_HIP_OK;
 }
 
+int ter_hip_embed_f16(const uint16_t* token_embd, int32_t V, int32_t H, const int32_t* token_dev, float* hidden,
+                      void* stream) {
+    if (!token_embd || !token_dev || !hidden) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (V < 1 || H < 1 || V > TER_HIP_N_MAX || H > TER_HIP_K_MAX) return fail(TER_HIP_ERR_SHAPE, "V=%d H=%d", V, H);
+    if (!aligned(token_embd, 2) || !aligned(token_dev, 4) || !aligned(hidden, 4))
+        return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
+    hipError_t e = launch_embed_f16(token_embd, V, H, token_dev, hidden, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "embedding launch");
+    return TER_HIP_OK;
+}
+
 int ter_hip_lm_head_argmax(const float* hidden, const uint16_t* gamma, float eps, const uint16_t* token_embd, int32_t H,
                            int32_t V, uint16_t* x_norm_out, uint16_t* logits_out, int32_t* token_out, uint64_t* state,
-                           void* stream) {
+                           int32_t* pos_advance, void* stream) {
     if (!hidden || !gamma || !token_out || !state) return fail(TER_HIP_ERR_NULL, "null argument");
     int rc = check_lm_head(token_embd, H, V);
     if (rc) return rc;
     if (H % 2) return fail(TER_HIP_ERR_SHAPE, "the fused RMSNorm prologue needs an even H (H=%d)", H);
     if (!aligned(hidden, 8) || !aligned(gamma, 4) || !aligned(x_norm_out, 4) || !aligned(logits_out, 2) ||
-        !aligned(token_out, 4) || !aligned(state, 8))
+        !aligned(token_out, 4) || !aligned(state, 8) || !aligned(pos_advance, 4))
         return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
     if (!(eps >= 0.f)) return fail(TER_HIP_ERR_SHAPE, "RMSNorm eps must be >= 0");
     int n_wg = 0;
     rc = pick_lm_head_wg(H, V, &n_wg);
     if (rc) return rc;
     hipError_t e = launch_lm_head(hidden, gamma, eps, nullptr, token_embd, H, V, x_norm_out, logits_out, token_out,
-                                  reinterpret_cast<unsigned long long*>(state), n_wg, static_cast<hipStream_t>(stream));
+                                  reinterpret_cast<unsigned long long*>(state), pos_advance, n_wg,
+                                  static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "lm_head launch");
     return TER_HIP_OK;
 }

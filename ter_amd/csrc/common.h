@@ -103,7 +103,8 @@ int lm_head_fast_nb(int H);
 int lm_head_max_wg_per_cu(int H);
 hipError_t launch_lm_head(const float* hidden, const uint16_t* gamma, float eps, const uint16_t* x16,
                           const uint16_t* emb, int H, int V, uint16_t* x_out, uint16_t* logits, int32_t* token_out,
-                          unsigned long long* state, int n_wg, hipStream_t st);
+                          unsigned long long* state, int32_t* pos_advance, int n_wg, hipStream_t st);
+hipError_t launch_embed_f16(const uint16_t* emb, int V, int H, const int32_t* token, float* hidden, hipStream_t st);
 hipError_t launch_argmax_f16(const uint16_t* logits, int n, int32_t* token_out, unsigned long long* state, int n_wg,
                              hipStream_t st);
 hipError_t launch_rmsnorm_f16_rows(const float* x, const uint16_t* gamma, float eps, int M, int H, uint16_t* y,

@@ -47,6 +47,7 @@ struct LmArgs {
     uint16_t* x_out;            // fp16 [H] copy of the normalized input or null
     uint16_t* logits;           // fp16 [V] or null
     int32_t* token_out;         // argmax index or null
+    int32_t* pos_advance;       // position incremented after the token is written, or null
     unsigned long long* state;  // argmax state, zero at rest (kArgGroups + 1 pairs)
     float eps;
     int H, V;
@@ -128,7 +129,7 @@ __device__ __forceinline__ bool arrive(unsigned long long* p, unsigned long long
 // about n_wg / kArgGroups arrivals; the last arrival writes the index.
 // Every thread of the workgroup must call it.
 __device__ void argmax_finish(unsigned long long key, unsigned long long* kred, unsigned long long* state,
-                              int32_t* token_out, int chunk) {
+                              int32_t* token_out, int chunk, int32_t* pos_advance) {
     key = wave_max64(key);
     if ((threadIdx.x & 63) == 0) kred[threadIdx.x >> 6] = key;
     __syncthreads();
@@ -141,8 +142,10 @@ __device__ void argmax_finish(unsigned long long key, unsigned long long* kred, 
         const unsigned in_group = (n_wg - g + kArgGroups - 1) / kArgGroups;
         unsigned long long bg, best;
         if (arrive(state + kArgStride * g, m, in_group, &bg) &&
-            arrive(state + kArgStride * kArgGroups, bg, groups, &best))
+            arrive(state + kArgStride * kArgGroups, bg, groups, &best)) {
             *gptr(token_out) = argmax_index(best, chunk);
+            if (pos_advance) *gptr(pos_advance) += 1;  // inc_pos_k: the step's last use of the position is done
+        }
     }
 }
 
@@ -324,7 +327,7 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_kernel(LmArgs a, int stage
         asm volatile("" ::: "memory");
         for (int i = lane; i < nrows; i += 64) gptr(a.logits)[r0 + i] = my_stage[i];
     }
-    if (a.token_out) argmax_finish(best, kred, a.state, a.token_out, chunk);
+    if (a.token_out) argmax_finish(best, kred, a.state, a.token_out, chunk, a.pos_advance);
 }
 
 // Any H off the fast path (not a multiple of 8, or above 4096): the reference's
@@ -371,7 +374,7 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_generic_kernel(LmArgs a, i
             if (a.token_out) best = umax64(best, argmax_key(h, (int)r, chunk));
         }
     }
-    if (a.token_out) argmax_finish(best, kred, a.state, a.token_out, chunk);
+    if (a.token_out) argmax_finish(best, kred, a.state, a.token_out, chunk, a.pos_advance);
 }
 
 // argmax of fp16 logits [N] (argmax_local_k + argmax_final_k semantics).
@@ -382,7 +385,17 @@ __global__ __launch_bounds__(kLmThreads) void argmax_kernel(const uint16_t* __re
     unsigned long long best = 0ull;
     for (long long i = (long long)blockIdx.x * kLmThreads + threadIdx.x; i < n; i += (long long)gridDim.x * kLmThreads)
         best = umax64(best, argmax_key(gptr(logits)[i], (int)i, chunk));
-    argmax_finish(best, kred, state, token_out, chunk);
+    argmax_finish(best, kred, state, token_out, chunk, nullptr);
+}
+
+// token_embed_lookup_k: hidden[i] = float(token_embd[token][i]) (exact
+// widening); a token outside [0, V) writes nothing.
+__global__ void embed_kernel(const uint16_t* __restrict__ emb, int V, int H, const int32_t* __restrict__ token,
+                             float* __restrict__ hidden) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int t = *gptr(token);
+    if (i >= H || t < 0 || t >= V) return;
+    gptr(hidden)[i] = half_bits_to_float(gptr(emb)[(long long)t * H + i]);
 }
 
 // rmsnorm_f32_in_k per row (256 threads): y = half((x * rms_inv) * gamma).
@@ -462,8 +475,9 @@ int lm_head_max_wg_per_cu(int H) {
 
 hipError_t launch_lm_head(const float* hidden, const uint16_t* gamma, float eps, const uint16_t* x16,
                           const uint16_t* emb, int H, int V, uint16_t* x_out, uint16_t* logits, int32_t* token_out,
-                          unsigned long long* state, int n_wg, hipStream_t st) {
+                          unsigned long long* state, int32_t* pos_advance, int n_wg, hipStream_t st) {
     LmArgs a{};
+    a.pos_advance = pos_advance;
     a.hidden = hidden;
     a.gamma = gamma;
     a.x16 = x16;
@@ -488,6 +502,11 @@ hipError_t launch_lm_head(const float* hidden, const uint16_t* gamma, float eps,
 hipError_t launch_argmax_f16(const uint16_t* logits, int n, int32_t* token_out, unsigned long long* state, int n_wg,
                              hipStream_t st) {
     hipLaunchKernelGGL(argmax_kernel, dim3(n_wg), dim3(kLmThreads), 0, st, logits, n, token_out, state);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_f16(const uint16_t* emb, int V, int H, const int32_t* token, float* hidden, hipStream_t st) {
+    hipLaunchKernelGGL(embed_kernel, dim3((H + 255) / 256), dim3(256), 0, st, emb, V, H, token, hidden);
     return hipGetLastError();
 }
 

@@ -366,8 +366,19 @@ def argmax_f16(logits, out_idx=None, state: Optional[ArgmaxState] = None, stream
     return out_idx
 
 
+def embed_f16(token_embd, token_dev, hidden=None, stream=None):
+    """token_embed_lookup_k: hidden fp32 [H] = token_embd[*token_dev] (fp16 [V][H])."""
+    torch = _torch()
+    V, H = token_embd.shape
+    if hidden is None:
+        hidden = torch.empty(H, dtype=torch.float32, device=token_embd.device)
+    L.check(L.lib().ter_hip_embed_f16(token_embd.data_ptr(), V, H, token_dev.data_ptr(), hidden.data_ptr(),
+                                      _stream(stream)), "ter_hip_embed_f16")
+    return hidden
+
+
 def lm_head_argmax(hidden, gamma, token_embd, eps: float = 1e-5, token_out=None, state: Optional[ArgmaxState] = None,
-                   x_norm_out=None, logits_out=None, stream=None):
+                   x_norm_out=None, logits_out=None, pos_advance=None, stream=None):
     """The decode step's tail in one launch (cuda/ter_cuda_forward_bitnet.cu:890-911):
     RMSNorm of fp32 hidden [H] -> fp16 lm_head over token_embd [V][H] -> argmax.
     Returns token_out (int32 [1])."""
@@ -383,7 +394,7 @@ def lm_head_argmax(hidden, gamma, token_embd, eps: float = 1e-5, token_out=None,
         state = ArgmaxState(hidden.device)
     L.check(L.lib().ter_hip_lm_head_argmax(hidden.data_ptr(), gamma.data_ptr(), C.c_float(eps), token_embd.data_ptr(),
                                            H, V, _ptr(x_norm_out), _ptr(logits_out), token_out.data_ptr(),
-                                           state.ptr(), _stream(stream)), "ter_hip_lm_head_argmax")
+                                           state.ptr(), _ptr(pos_advance), _stream(stream)), "ter_hip_lm_head_argmax")
     return token_out
 
 

@@ -27,7 +27,7 @@ def declared_functions():
 
 def test_library_exports_every_declared_symbol():
     names = declared_functions()
-    assert len(names) == 39, names
+    assert len(names) == 40, names
     lib = L.lib()
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
@@ -165,7 +165,7 @@ def test_lm_head_validation_without_device():
     assert lib.ter_hip_argmax_f16(fake, 0, fake, fake, None) == L.ERR_SHAPE
     assert lib.ter_hip_argmax_f16(fake, 10, fake, fake + 4, None) == L.ERR_ALIGN
     # fused tail: even H only, token_out and state required, alignment
-    args = [fake, fake, 1e-5, fake, 64, 10, None, None, fake, fake, None]
+    args = [fake, fake, 1e-5, fake, 64, 10, None, None, fake, fake, None, None]
     bad = list(args); bad[8] = None
     assert lib.ter_hip_lm_head_argmax(*bad) == L.ERR_NULL
     bad = list(args); bad[4] = 63
