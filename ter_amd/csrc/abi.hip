@@ -526,7 +526,7 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
     const GemvDesc d = make_desc(w, x, *out, 0);
     const long long total = (long long)d.n_strips * d.Ku;
     int n_wg = 0;
-    const int lds = gemv_lds_bytes(w->K);
+    const int lds = is_rms(x->kind) ? gemv_lds_bytes_rms(w->K) : gemv_lds_bytes(w->K);
     rc = pick_wg(total, 0, lds, &n_wg);
     if (rc) return rc;
     hipError_t e = launch_gemv(d, nullptr, nullptr, total, n_wg, lds, static_cast<hipStream_t>(stream));
@@ -611,7 +611,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         ds[(size_t)i] = make_desc(it.w, &it.x, o, tile);
         starts[(size_t)i] = tile;
         tile += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
-        const int lb = gemv_lds_bytes(it.w->K);
+        const int lb = is_rms(it.x.kind) ? gemv_lds_bytes_rms(it.w->K) : gemv_lds_bytes(it.w->K);
         if (lb > lds) lds = lb;
         bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.w->K * act_bytes(it.x.kind) +
                  (uint64_t)it.w->N * out_bytes(o);

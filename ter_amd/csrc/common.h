@@ -33,7 +33,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kGemvWaves = 4;             // waves per workgroup of the GEMV kernel
 constexpr int kGemvThreads = 64 * kGemvWaves;
 
-inline int32_t units_of(int32_t K) { return (K + kUnitK - 1) / kUnitK; }
+__host__ __device__ inline int32_t units_of(int32_t K) { return (K + kUnitK - 1) / kUnitK; }
 inline int32_t strips_of(int32_t N) { return (N + kStripCols - 1) / kStripCols; }
 inline size_t tile_stream_bytes(int32_t K, int32_t N) {
     return (size_t)strips_of(N) * (size_t)units_of(K) * kTileBytes;
@@ -260,7 +260,11 @@ __device__ inline float relu2_sum_sq_1024(const uint16_t* gate, const uint16_t* 
 
 // LDS bytes the GEMV kernel needs for a K: X (Ku*256 int8) + unit sums +
 // reduction scratch (one float per thread).
-inline int gemv_lds_bytes(int32_t K) { return units_of(K) * kUnitK + units_of(K) * 4 + kGemvThreads * 4; }
+__host__ __device__ inline int gemv_lds_bytes(int32_t K) { return units_of(K) * kUnitK + units_of(K) * 4 + kGemvThreads * 4; }
+// RMS activation kinds also stage the fp32 activations ([Ku*256] floats) at
+// this 16-byte aligned offset.
+__host__ __device__ inline int gemv_lds_xs32_offset(int32_t K) { return (gemv_lds_bytes(K) + 15) / 16 * 16; }
+inline int gemv_lds_bytes_rms(int32_t K) { return gemv_lds_xs32_offset(K) + units_of(K) * kUnitK * 4; }
 
 int device_cu_count(int device);
 // Resident GEMV workgroups per CU at this LDS size (0 if the query fails).

@@ -169,6 +169,24 @@ __device__ __forceinline__ void load_h16(const uint16_t* xh, int k, int K, float
     }
 }
 
+// 16 fp16 values at k as 8 packed dwords (zeros past K): half the registers
+// of load_h16 while the values wait.
+__device__ __forceinline__ void load_h16_raw(const uint16_t* xh, int k, int K, uint32_t (&w)[8]) {
+    if (((reinterpret_cast<uintptr_t>(xh + k) & 15u) == 0) && k + 16 <= K) {
+        const TER_GLOBAL u32x4* p = gptr(reinterpret_cast<const u32x4*>(xh + k));
+        const u32x4 a = p[0], b = p[1];
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lo = k + 2 * i < K ? gptr(xh)[k + 2 * i] : 0u;
+            const uint32_t hi = k + 2 * i + 1 < K ? gptr(xh)[k + 2 * i + 1] : 0u;
+            w[i] = lo | (hi << 16);
+        }
+    }
+}
+
 // relu^2(gate) * up on 16 elements at k (zeros past K).
 __device__ __forceinline__ void load_relu2_16(const uint16_t* g, const uint16_t* u, int k, int K, float (&v)[16]) {
     if ((((reinterpret_cast<uintptr_t>(g + k) | reinterpret_cast<uintptr_t>(u + k)) & 15u) == 0) && k + 16 <= K) {
@@ -247,7 +265,8 @@ __device__ __forceinline__ void x_prefetch(const GemvDesc& d, XPre& r) {
 // (cuda/ter_cuda_forward_bitnet.cu:258-309): x = relu^2(gate) * up and the
 // sum of squares in its 1024-thread order.  `owner` (the workgroup that starts the GEMV)
 // also writes the optional copies xq_out / xs_out.
-__device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* usum, float* red, bool owner) {
+__device__ __forceinline__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* usum, float* red, float* xs32,
+                         bool owner) {
 #pragma clang fp contract(off)
     const int K = d.K;
     const int nchunks = d.Ku * (kUnitK / 16);
@@ -264,14 +283,46 @@ __device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* u
     }
     const bool rms = d.x_kind != TER_HIP_X_F32;
     float rms_inv = 1.0f;
+    uint32_t g0[8], g1[8];
     if (rms) {
+        // gamma for the prefetched chunks, in flight during the reduction
+        if (c0 < nchunks) load_h16_raw(d.gamma, c0 * 16, K, g0);
+        if (c1 < nchunks) load_h16_raw(d.gamma, c1 * 16, K, g1);
+        // the (zero-padded) activations as fp32 in LDS, so the sum of squares
+        // reads them in the reference's strided order without a second pass
+        // over global memory
+        auto put16 = [&](int c, const float (&v)[16]) {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4)
+                *reinterpret_cast<f32x4*>(xs32 + c * 16 + i) = f32x4{v[i], v[i + 1], v[i + 2], v[i + 3]};
+        };
+        if (c0 < nchunks) put16(c0, r.v0);
+        if (c1 < nchunks) put16(c1, r.v1);
+        for (int c = tid + 2 * kGemvThreads; c < nchunks; c += kGemvThreads) {
+            float t[16];
+            load_x16f(d, c * 16, t);
+            put16(c, t);
+        }
+        __syncthreads();
         float ss;
         if (d.x_kind == TER_HIP_X_RELU2_RMS) {
-            ss = relu2_sum_sq_1024(static_cast<const uint16_t*>(d.x), d.up, K, red);
+            // 1024 virtual threads: element i goes to partial (i / 256) % 4 of thread i % 256
+            float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+            for (int i = tid; i < K; i += 4 * kGemvThreads) {
+                const float a = xs32[i];
+                const float b = i + 256 < K ? xs32[i + 256] : 0.f;
+                const float c = i + 512 < K ? xs32[i + 512] : 0.f;
+                const float e = i + 768 < K ? xs32[i + 768] : 0.f;
+                p0 = __builtin_fmaf(a, a, p0);
+                p1 = __builtin_fmaf(b, b, p1);  // past K: +0, which changes no sum
+                p2 = __builtin_fmaf(c, c, p2);
+                p3 = __builtin_fmaf(e, e, p3);
+            }
+            ss = tree_sum256((p0 + p2) + (p1 + p3), red);
         } else {
             float part = 0.f;
             for (int i = tid; i < K; i += kGemvThreads) {
-                const float v = x_at(d, i);
+                const float v = xs32[i];
                 part = __builtin_fmaf(v, v, part);
             }
             ss = tree_sum256(part, red);
@@ -279,13 +330,29 @@ __device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* u
         rms_inv = 1.0f / __builtin_sqrtf(ss / (float)K + d.eps);
     }
     float v0[16], v1[16];
+    if (rms) {
+        // the chunks come back from LDS, so the prefetch registers are free
+        // during the reduction
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        v0[i] = r.v0[i];
-        v1[i] = r.v1[i];
+        for (int i = 0; i < 16; i += 4) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(xs32 + (c0 < nchunks ? c0 : 0) * 16 + i);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(xs32 + (c1 < nchunks ? c1 : 0) * 16 + i);
+            v0[i] = a.x; v0[i + 1] = a.y; v0[i + 2] = a.z; v0[i + 3] = a.w;
+            v1[i] = b.x; v1[i + 1] = b.y; v1[i + 2] = b.z; v1[i + 3] = b.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int sh = 16 * (i & 1);
+            v0[i] = (v0[i] * rms_inv) * half_bits_to_float((uint16_t)(g0[i >> 1] >> sh));
+            v1[i] = (v1[i] * rms_inv) * half_bits_to_float((uint16_t)(g1[i >> 1] >> sh));
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            v0[i] = r.v0[i];
+            v1[i] = r.v1[i];
+        }
     }
-    if (rms && c0 < nchunks) rms_apply(d, c0 * 16, rms_inv, v0);
-    if (rms && c1 < nchunks) rms_apply(d, c1 * 16, rms_inv, v1);
     float m = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -294,8 +361,16 @@ __device__ float stage_x(const GemvDesc& d, const XPre& r, int8_t* lds_x, int* u
     }
     for (int c = tid + 2 * kGemvThreads; c < nchunks; c += kGemvThreads) {
         float t[16];
-        load_x16f(d, c * 16, t);
-        if (rms) rms_apply(d, c * 16, rms_inv, t);
+        if (rms) {
+#pragma unroll
+            for (int i = 0; i < 16; i += 4) {
+                const f32x4 f = *reinterpret_cast<const f32x4*>(xs32 + c * 16 + i);
+                t[i] = f[0]; t[i + 1] = f[1]; t[i + 2] = f[2]; t[i + 3] = f[3];
+            }
+            rms_apply(d, c * 16, rms_inv, t);
+        } else {
+            load_x16f(d, c * 16, t);
+        }
 #pragma unroll
         for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(t[i]));
     }
@@ -471,7 +546,7 @@ __device__ __forceinline__ void finish_fixups(const Fixups& f) {
 
 // One wave streams local tiles [la, la + n) of GEMV d; `wa` holds the first
 // batch already.  Returns the piece's fix-up adds, to be finished later.
-__device__ Fixups run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usum, float s, int la, int n,
+__device__ __forceinline__ Fixups run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usum, float s, int la, int n,
                             __amdgpu_buffer_rsrc_t rs, int voff, u32x4 (&wa)[kBatch]) {
     Piece p;
     p.st = la / d.Ku;
@@ -559,8 +634,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
         int8_t* lds_x = reinterpret_cast<int8_t*>(lds_raw);
         int* usum = reinterpret_cast<int*>(lds_raw + d.Ku * kUnitK);
         float* red = reinterpret_cast<float*>(lds_raw + d.Ku * kUnitK + d.Ku * 4);
+        float* xs32 = reinterpret_cast<float*>(lds_raw + gemv_lds_xs32_offset(d.K));
         __syncthreads();  // the previous segment is done with LDS
-        const float act = stage_x(d, xpre, lds_x, usum, red, t == d.tile0);
+        const float act = stage_x(d, xpre, lds_x, usum, red, xs32, t == d.tile0);
         __syncthreads();
         const float s = act * d.w_scale;  // x_scale * w_scale (forward.cpp:342)
         if (n > 0) {
