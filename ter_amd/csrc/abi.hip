@@ -163,6 +163,21 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip
 constexpr int kGemvWgPerCu = 2;
 constexpr long long kMaxPieceTiles = 1 << 20;
 
+// The activation kind shared by every item of a GEMV work list when each
+// qualifies for the kernel's vector prologue (K a multiple of 16; x, up and
+// gamma 16-byte aligned), else -1 (the general prologue).
+int gemv_vec_kind(const ter_hip_gemv_item_t* items, int n) {
+    auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    const int kind = items[0].x.kind;
+    for (int i = 0; i < n; ++i) {
+        const ter_hip_act_t& x = items[i].x;
+        if (x.kind != kind || items[i].w->K % 16 != 0 || !a16(x.data)) return -1;
+        if (x.kind == TER_HIP_X_RELU2_RMS && !a16(x.up)) return -1;
+        if (is_rms(x.kind) && !a16(x.gamma)) return -1;
+    }
+    return kind;
+}
+
 int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, int* n_wg) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -274,6 +289,7 @@ struct ter_hip_plan {
     long long total = 0;         // tiles (GEMV) or blocks (GEMM) of one launch
     int n_wg = 0;
     int lds_bytes = 0;           // GEMV
+    int vec_kind = -1;           // GEMV: common activation kind for the vector prologue, or -1
     int mb = 0;                  // GEMM row-block count
     bool vec = false;            // GEMM: 16-byte X rows
     bool stream = false;         // GEMM: streaming kernel (M <= 16), total counts tiles
@@ -529,7 +545,7 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
     const int lds = is_rms(x->kind) ? gemv_lds_bytes_rms(w->K) : gemv_lds_bytes(w->K);
     rc = pick_wg(total, 0, lds, &n_wg);
     if (rc) return rc;
-    hipError_t e = launch_gemv(d, nullptr, nullptr, total, n_wg, lds, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_gemv(d, nullptr, nullptr, total, n_wg, lds, -1, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return TER_HIP_OK;
 }
@@ -633,6 +649,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     p->total = tile;
     p->n_wg = n_wg;
     p->lds_bytes = lds;
+    p->vec_kind = gemv_vec_kind(items, n);
     p->bytes = bytes;
     p->macs = macs;
     *plan = p;
@@ -657,7 +674,7 @@ int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
     } else {
         GemvDesc none{};
         e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev, plan->total,
-                        plan->n_wg, plan->lds_bytes, static_cast<hipStream_t>(stream));
+                        plan->n_wg, plan->lds_bytes, plan->vec_kind, static_cast<hipStream_t>(stream));
     }
     if (e != hipSuccess) return hip_fail(e, "plan launch");
     return TER_HIP_OK;

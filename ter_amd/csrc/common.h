@@ -82,8 +82,10 @@ struct alignas(16) GemmDesc {
 // device descriptor table `list_dev` and `first_dev`, the index of each
 // workgroup's first descriptor (range g starts at total * g / n_wg); single
 // launches pass nullptr for both.
+// vec_kind: the activation kind of every GEMV of a work list that qualifies
+// for the vector prologue (gemv_vec_kind), else -1.
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const int32_t* first_dev,
-                       long long total_tiles, int n_wg, int lds_bytes, hipStream_t st);
+                       long long total_tiles, int n_wg, int lds_bytes, int vec_kind, hipStream_t st);
 hipError_t launch_pack_v11(const uint8_t* v11, uint8_t* t16, int K, int N, hipStream_t st);
 hipError_t launch_unpack_v11(const uint8_t* t16, uint8_t* v11, int K, int N, hipStream_t st);
 hipError_t launch_pack_i2s(const uint8_t* raw, uint8_t* t16, int K, int N, hipStream_t st);
@@ -259,8 +261,10 @@ __device__ inline float relu2_sum_sq_1024(const uint16_t* gate, const uint16_t* 
 #endif
 
 // LDS bytes the GEMV kernel needs for a K: X (Ku*256 int8) + unit sums +
-// reduction scratch (one float per thread).
-__host__ __device__ inline int gemv_lds_bytes(int32_t K) { return units_of(K) * kUnitK + units_of(K) * 4 + kGemvThreads * 4; }
+// reduction scratch (one float per thread, then one per wave).
+__host__ __device__ inline int gemv_lds_bytes(int32_t K) {
+    return units_of(K) * kUnitK + units_of(K) * 4 + (kGemvThreads + kGemvWaves) * 4;
+}
 // RMS activation kinds also stage the fp32 activations ([Ku*256] floats) at
 // this 16-byte aligned offset.
 __host__ __device__ inline int gemv_lds_xs32_offset(int32_t K) { return (gemv_lds_bytes(K) + 15) / 16 * 16; }

@@ -408,6 +408,288 @@ __device__ __forceinline__ float stage_x(const GemvDesc& d, const XPre& r, int8_
     return act;
 }
 
+// ---------------------------------------------------------------------------
+// Vector prologue.  When every GEMV of a launch has one activation kind, K a
+// multiple of 16 and 16-byte aligned vectors (the decode step's case), the
+// launch uses a kernel specialised on that kind: the activations (and gamma)
+// are read through buffer resources sized to K elements, so a 16-element
+// chunk is either loaded whole or reads as zeros past K, and no load sits
+// behind a branch.  All of them are issued before the weight batch and stay
+// raw in registers until staging, so the staging waits only for them and not
+// for the weights (a wave's loads complete in issue order).  Results are those
+// of stage_x.
+
+// Raw chunk registers: for chunk c0 = tid and c1 = tid + 256, the x words
+// (I8: a[0], a[1]; F16: a[0..1], a[2..3]; F32: a[0..3], a[4..7]; RELU2: gate
+// a[0..1], a[2..3] and up a[4..5], a[6..7]) and gamma's (g[0..1], g[2..3]).
+struct XRaw {
+    u32x4 a[8];
+    u32x4 g[4];
+};
+
+constexpr bool kind_rms(int kind) { return kind != TER_HIP_X_F32 && kind != TER_HIP_X_I8; }
+// Bytes of one x element of a kind (gate's for X_RELU2_RMS).
+constexpr int kind_bytes(int kind) {
+    return kind == TER_HIP_X_I8 ? 1 : ((kind == TER_HIP_X_F32 || kind == TER_HIP_X_F32_RMS) ? 4 : 2);
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t vec_rsrc(const void* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 vload(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// Loads of chunk c into a[j0 ..] (x) and a[j0 + 4 ..] (up).
+template <int kKind>
+__device__ __forceinline__ void vload_chunk(__amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t ru, int c, u32x4* a) {
+    constexpr int L = kind_bytes(kKind);  // dwordx4 loads per 16 elements
+#pragma unroll
+    for (int j = 0; j < L; ++j) a[j] = vload(rx, c * 16 * L + 16 * j);
+    if constexpr (kKind == TER_HIP_X_RELU2_RMS) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) a[4 + j] = vload(ru, c * 32 + 16 * j);
+    }
+}
+
+__device__ __forceinline__ void halves_to_float(const u32x4* w, float (&v)[16]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[8 * j + 2 * i] = half_bits_to_float((uint16_t)(w[j][i] & 0xFFFFu));
+            v[8 * j + 2 * i + 1] = half_bits_to_float((uint16_t)(w[j][i] >> 16));
+        }
+}
+
+// 16 activations of chunk registers a (layout of vload_chunk) as fp32.
+template <int kKind>
+__device__ __forceinline__ void unpack_chunk(const u32x4* a, float (&v)[16]) {
+    if constexpr (kKind == TER_HIP_X_F32 || kKind == TER_HIP_X_F32_RMS) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const unsigned w = a[j][i];  // (bit_cast of the element lvalue itself reads element 0)
+                v[4 * j + i] = __builtin_bit_cast(float, w);
+            }
+    } else if constexpr (kKind == TER_HIP_X_F16_RMS) {
+        halves_to_float(a, v);
+    } else {
+        float g[16], u[16];
+        halves_to_float(a, g);
+        halves_to_float(a + 4, u);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = relu2_mul(g[i], u[i]);
+    }
+}
+
+template <int kKind>
+__device__ __forceinline__ void x_prefetch_vec(const GemvDesc& d, XRaw& r) {
+    const int c0 = threadIdx.x, c1 = threadIdx.x + kGemvThreads;
+    const __amdgpu_buffer_rsrc_t rx = vec_rsrc(d.x, d.K * kind_bytes(kKind));
+    if constexpr (kKind == TER_HIP_X_I8) {
+        r.a[0] = vload(rx, c0 * 16);
+        r.a[1] = vload(rx, c1 * 16);
+        return;
+    }
+    const __amdgpu_buffer_rsrc_t ru = vec_rsrc(d.up, d.K * 2);
+    if constexpr (kKind == TER_HIP_X_F32 || kKind == TER_HIP_X_F32_RMS) {
+        vload_chunk<kKind>(rx, ru, c0, r.a);
+        vload_chunk<kKind>(rx, ru, c1, r.a + 4);
+    } else {
+        // two-load chunks: x (gate) in a[0..3], up in a[4..7]
+        u32x4 t[8];
+        vload_chunk<kKind>(rx, ru, c0, t);
+        r.a[0] = t[0];
+        r.a[1] = t[1];
+        if constexpr (kKind == TER_HIP_X_RELU2_RMS) {
+            r.a[4] = t[4];
+            r.a[5] = t[5];
+        }
+        vload_chunk<kKind>(rx, ru, c1, t);
+        r.a[2] = t[0];
+        r.a[3] = t[1];
+        if constexpr (kKind == TER_HIP_X_RELU2_RMS) {
+            r.a[6] = t[4];
+            r.a[7] = t[5];
+        }
+    }
+    if constexpr (kind_rms(kKind)) {
+        const __amdgpu_buffer_rsrc_t rg = vec_rsrc(d.gamma, d.K * 2);
+        r.g[0] = vload(rg, c0 * 32);
+        r.g[1] = vload(rg, c0 * 32 + 16);
+        r.g[2] = vload(rg, c1 * 32);
+        r.g[3] = vload(rg, c1 * 32 + 16);
+    }
+}
+
+// Chunk `which` (0: c0, 1: c1) of the prefetched registers as fp32.
+template <int kKind>
+__device__ __forceinline__ void prefetched_chunk(const XRaw& r, int which, float (&v)[16]) {
+    if constexpr (kKind == TER_HIP_X_F32 || kKind == TER_HIP_X_F32_RMS) {
+        unpack_chunk<kKind>(r.a + 4 * which, v);
+    } else {
+        u32x4 t[8];
+        t[0] = r.a[2 * which];
+        t[1] = r.a[2 * which + 1];
+        if constexpr (kKind == TER_HIP_X_RELU2_RMS) {
+            t[4] = r.a[4 + 2 * which];
+            t[5] = r.a[5 + 2 * which];
+        }
+        unpack_chunk<kKind>(t, v);
+    }
+}
+
+// Sum over 256 threads in the order of tree_sum256, with one barrier: every
+// wave reads all 256 partials and reduces levels 128 and 64 as
+// (v[l] + v[l + 128]) + (v[l + 64] + v[l + 192]), then the wave's own
+// levels 32 .. 1.  `red` must not be written again before a later barrier.
+__device__ __forceinline__ float tree_sum256_all(float v, float* red) {
+    const int t = threadIdx.x, l = t & 63;
+    red[t] = v;
+    __syncthreads();
+    float a = (red[l] + red[l + 128]) + (red[l + 64] + red[l + 192]);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) a = a + __shfl_down(a, s);
+    return __shfl(a, 0);
+}
+
+template <int kKind>
+__device__ __forceinline__ float stage_x_vec(const GemvDesc& d, const XRaw& r, int8_t* lds_x, int* usum, float* red,
+                                             float* xs32, bool owner) {
+#pragma clang fp contract(off)
+    const int K = d.K;
+    const int nchunks = d.Ku * (kUnitK / 16);
+    const int tid = threadIdx.x;
+    const int c0 = tid, c1 = tid + kGemvThreads;
+    const __amdgpu_buffer_rsrc_t rx = vec_rsrc(d.x, K * kind_bytes(kKind));
+    if constexpr (kKind == TER_HIP_X_I8) {
+        if (c0 < nchunks) put_chunk(c0, r.a[0], lds_x, usum);
+        if (c1 < nchunks) put_chunk(c1, r.a[1], lds_x, usum);
+        for (int c = tid + 2 * kGemvThreads; c < nchunks; c += kGemvThreads) put_chunk(c, vload(rx, c * 16), lds_x, usum);
+        return d.x_scale_dev ? *gptr(d.x_scale_dev) : d.x_scale;
+    } else {
+        const __amdgpu_buffer_rsrc_t ru = vec_rsrc(d.up, K * 2);
+        const __amdgpu_buffer_rsrc_t rg = vec_rsrc(d.gamma, K * 2);
+        constexpr bool rms = kind_rms(kKind);
+        float v0[16], v1[16];
+        prefetched_chunk<kKind>(r, 0, v0);
+        prefetched_chunk<kKind>(r, 1, v1);
+        // chunk c (beyond the prefetched two) as fp32, normalized for the RMS kinds
+        auto far_chunk = [&](int c, float rms_inv, float (&t)[16]) {
+            if constexpr (rms) {
+#pragma unroll
+                for (int i = 0; i < 16; i += 4) {
+                    const f32x4 f = *reinterpret_cast<const f32x4*>(xs32 + c * 16 + i);
+                    t[i] = f[0]; t[i + 1] = f[1]; t[i + 2] = f[2]; t[i + 3] = f[3];
+                }
+                const u32x4 gw[2] = {vload(rg, c * 32), vload(rg, c * 32 + 16)};
+                float g[16];
+                halves_to_float(gw, g);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) t[i] = (t[i] * rms_inv) * g[i];
+            } else {
+                u32x4 a[8];
+                vload_chunk<kKind>(rx, ru, c, a);
+                unpack_chunk<kKind>(a, t);
+            }
+        };
+        float rms_inv = 1.0f;
+        if constexpr (rms) {
+            auto put16 = [&](int c, const float (&v)[16]) {
+#pragma unroll
+                for (int i = 0; i < 16; i += 4)
+                    *reinterpret_cast<f32x4*>(xs32 + c * 16 + i) = f32x4{v[i], v[i + 1], v[i + 2], v[i + 3]};
+            };
+            if (c0 < nchunks) put16(c0, v0);
+            if (c1 < nchunks) put16(c1, v1);
+            for (int c = tid + 2 * kGemvThreads; c < nchunks; c += kGemvThreads) {
+                u32x4 a[8];
+                vload_chunk<kKind>(rx, ru, c, a);
+                float t[16];
+                unpack_chunk<kKind>(a, t);
+                put16(c, t);
+            }
+            __syncthreads();
+            float ss;
+            if constexpr (kKind == TER_HIP_X_RELU2_RMS) {
+                // 1024 virtual threads (relu2_sum_sq_1024's order)
+                float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+                for (int i = tid; i < K; i += 4 * kGemvThreads) {
+                    const float a = xs32[i];
+                    const float b = i + 256 < K ? xs32[i + 256] : 0.f;
+                    const float c = i + 512 < K ? xs32[i + 512] : 0.f;
+                    const float e = i + 768 < K ? xs32[i + 768] : 0.f;
+                    p0 = __builtin_fmaf(a, a, p0);
+                    p1 = __builtin_fmaf(b, b, p1);  // past K: +0, which changes no sum
+                    p2 = __builtin_fmaf(c, c, p2);
+                    p3 = __builtin_fmaf(e, e, p3);
+                }
+                ss = tree_sum256_all((p0 + p2) + (p1 + p3), red);
+            } else {
+                float part = 0.f;
+                for (int i = tid; i < K; i += kGemvThreads) {
+                    const float v = xs32[i];
+                    part = __builtin_fmaf(v, v, part);
+                }
+                ss = tree_sum256_all(part, red);
+            }
+            rms_inv = 1.0f / __builtin_sqrtf(ss / (float)K + d.eps);
+            float g0[16], g1[16];
+            halves_to_float(r.g, g0);
+            halves_to_float(r.g + 2, g1);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                v0[i] = (v0[i] * rms_inv) * g0[i];
+                v1[i] = (v1[i] * rms_inv) * g1[i];
+            }
+        }
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) m = fmaxf(m, fmaxf(fabsf(v0[i]), fabsf(v1[i])));  // zeros past the chunks
+        for (int c = tid + 2 * kGemvThreads; c < nchunks; c += kGemvThreads) {
+            float t[16];
+            far_chunk(c, rms_inv, t);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(t[i]));
+        }
+        m = wave_max(m);
+        float* wmax = red + kGemvThreads;  // apart from the sum's slots, which other waves may still read
+        if ((tid & 63) == 0) wmax[tid >> 6] = m;
+        __syncthreads();
+        m = wmax[0];
+#pragma unroll
+        for (int i = 1; i < kGemvWaves; ++i) m = fmaxf(m, wmax[i]);
+        const float amax = m + 1e-9f;
+        const float scale = 127.0f / amax;
+        const float act = 1.0f / scale;
+        for (int c = tid; c < nchunks; c += kGemvThreads) {
+            u32x4 q;
+            if (c == c0) {
+                q = pack_q16(v0, scale);
+            } else if (c == c1) {
+                q = pack_q16(v1, scale);
+            } else {
+                float t[16];
+                far_chunk(c, rms_inv, t);
+                q = pack_q16(t, scale);
+            }
+            put_chunk(c, q, lds_x, usum);
+            if (owner && d.xq_out) {
+                const int k = c * 16;
+                const unsigned qw[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (k + i < K) gptr(d.xq_out)[k + i] = (int8_t)((qw[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+            }
+        }
+        if (owner && tid == 0 && d.xs_out) *gptr(d.xs_out) = act;
+        return act;
+    }
+}
+
 __device__ __forceinline__ void emit(const GemvDesc& d, int col, int val, float s) { emit_out(d, col, val, s); }
 
 // Accumulate 1 tile (16 bytes of this lane) into the 4 column accumulators.
@@ -599,8 +881,9 @@ __device__ __forceinline__ Fixups run_piece(const GemvDesc& d, const int8_t* lds
 
 // kList: GEMVs come from the device table `list` (plan launches); otherwise
 // the single descriptor is a kernel argument.  Two instantiations keep the
-// descriptor in scalar registers either way.
-template <bool kList>
+// descriptor in scalar registers either way.  kKind >= 0: every GEMV has that
+// activation kind and qualifies for the vector prologue; -1: any kind.
+template <bool kList, int kKind>
 __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
                                                             const GemvDesc* __restrict__ list,
                                                             const int32_t* __restrict__ first,
@@ -628,7 +911,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(d.w + (long long)la * kTileBytes), 0, n * kTileBytes, 0x00020000);
         XPre xpre;
-        x_prefetch(d, xpre);          // activations first (see XPre)
+        XRaw xraw;
+        if constexpr (kKind < 0)
+            x_prefetch(d, xpre);      // activations first (see XPre)
+        else
+            x_prefetch_vec<kKind>(d, xraw);
         u32x4 wa[kBatch];
         load_batch(wa, rs, voff, 0);  // in flight while the activations are staged
         int8_t* lds_x = reinterpret_cast<int8_t*>(lds_raw);
@@ -636,7 +923,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
         float* red = reinterpret_cast<float*>(lds_raw + d.Ku * kUnitK + d.Ku * 4);
         float* xs32 = reinterpret_cast<float*>(lds_raw + gemv_lds_xs32_offset(d.K));
         __syncthreads();  // the previous segment is done with LDS
-        const float act = stage_x(d, xpre, lds_x, usum, red, xs32, t == d.tile0);
+        float act;
+        if constexpr (kKind < 0)
+            act = stage_x(d, xpre, lds_x, usum, red, xs32, t == d.tile0);
+        else
+            act = stage_x_vec<kKind>(d, xraw, lds_x, usum, red, xs32, t == d.tile0);
         __syncthreads();
         const float s = act * d.w_scale;  // x_scale * w_scale (forward.cpp:342)
         if (n > 0) {
@@ -655,19 +946,45 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
 
 int gemv_max_wg_per_cu(int lds_bytes) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel<true>, kGemvThreads, lds_bytes) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel<true, -1>, kGemvThreads, lds_bytes) !=
+        hipSuccess)
         return 0;
     return n;
 }
 
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const int32_t* first_dev,
-                       long long total_tiles, int n_wg, int lds_bytes, hipStream_t st) {
-    if (list_dev)
-        hipLaunchKernelGGL(gemv_t16_kernel<true>, dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, single, list_dev,
+                       long long total_tiles, int n_wg, int lds_bytes, int vec_kind, hipStream_t st) {
+    const dim3 grid(n_wg), block(kGemvThreads);
+    if (!list_dev) {
+        hipLaunchKernelGGL((gemv_t16_kernel<false, -1>), grid, block, lds_bytes, st, single, list_dev, first_dev,
+                           total_tiles, n_wg);
+        return hipGetLastError();
+    }
+    switch (vec_kind) {
+    case TER_HIP_X_I8:
+        hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_I8>), grid, block, lds_bytes, st, single, list_dev,
                            first_dev, total_tiles, n_wg);
-    else
-        hipLaunchKernelGGL(gemv_t16_kernel<false>, dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, single, list_dev,
+        break;
+    case TER_HIP_X_F32:
+        hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_F32>), grid, block, lds_bytes, st, single, list_dev,
                            first_dev, total_tiles, n_wg);
+        break;
+    case TER_HIP_X_F32_RMS:
+        hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_F32_RMS>), grid, block, lds_bytes, st, single,
+                           list_dev, first_dev, total_tiles, n_wg);
+        break;
+    case TER_HIP_X_F16_RMS:
+        hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_F16_RMS>), grid, block, lds_bytes, st, single,
+                           list_dev, first_dev, total_tiles, n_wg);
+        break;
+    case TER_HIP_X_RELU2_RMS:
+        hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_RELU2_RMS>), grid, block, lds_bytes, st, single,
+                           list_dev, first_dev, total_tiles, n_wg);
+        break;
+    default:
+        hipLaunchKernelGGL((gemv_t16_kernel<true, -1>), grid, block, lds_bytes, st, single, list_dev, first_dev,
+                           total_tiles, n_wg);
+    }
     return hipGetLastError();
 }
 
