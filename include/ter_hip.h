@@ -209,7 +209,10 @@ typedef struct ter_hip_gemv_item {
 typedef struct ter_hip_plan ter_hip_plan_t;
 
 /* Build a launch plan for `n` GEMVs (descriptor table copied to the device).
- * wg_per_cu <= 0 picks the default occupancy.  Items sharing a weight must not
+ * wg_per_cu <= 0 picks the default occupancy (2 workgroups per CU; 1 for
+ * small plans whose activations need a prologue).  When every item has the
+ * same activation kind, K % 16 == 0 and 16-byte aligned x / up / gamma, the
+ * plan launches the kernel specialised on that kind.  Items sharing a weight must not
  * appear twice in one plan, and no two items may write overlapping `resid`
  * ranges (TER_HIP_ERR_CONFLICT). */
 int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items, int32_t n,

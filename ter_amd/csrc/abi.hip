@@ -161,6 +161,12 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip
 // wave's piece would exceed kMaxPieceTiles (its buffer resource spans at most
 // 2^31 bytes).  wg_per_cu > 0 overrides (tuning).
 constexpr int kGemvWgPerCu = 2;
+// A launch whose activations need a prologue (any kind but X_I8) and that
+// has fewer tiles than this per workgroup at kGemvWgPerCu uses one workgroup
+// per CU: every workgroup repeats the prologue, and below this size halving
+// the repeats gains more than the second workgroup's overlap (decode-step
+// plans: 1600 - 8640 tiles).
+constexpr long long kSmallPlanTilesPerWg = 32;
 constexpr long long kMaxPieceTiles = 1 << 20;
 
 // The activation kind shared by every item of a GEMV work list when each
@@ -178,7 +184,7 @@ int gemv_vec_kind(const ter_hip_gemv_item_t* items, int n) {
     return kind;
 }
 
-int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, int* n_wg) {
+int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, bool prologue, int* n_wg) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
@@ -187,6 +193,7 @@ int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, int* n_wg) {
     const int fit = gemv_max_wg_per_cu(lds_bytes);
     if (fit <= 0) return fail(TER_HIP_ERR_SHAPE, "GEMV workgroup does not fit a CU (LDS %d bytes)", lds_bytes);
     int per_cu = wg_per_cu > 0 ? wg_per_cu : (kGemvWgPerCu < fit ? kGemvWgPerCu : fit);
+    if (wg_per_cu <= 0 && prologue && total_tiles < (long long)cus * kGemvWgPerCu * kSmallPlanTilesPerWg) per_cu = 1;
     long long g = (long long)cus * per_cu;
     const long long min_g = (total_tiles + kMaxPieceTiles * kGemvWaves - 1) / (kMaxPieceTiles * kGemvWaves);
     if (g < min_g) g = min_g;
@@ -543,7 +550,7 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
     const long long total = (long long)d.n_strips * d.Ku;
     int n_wg = 0;
     const int lds = is_rms(x->kind) ? gemv_lds_bytes_rms(w->K) : gemv_lds_bytes(w->K);
-    rc = pick_wg(total, 0, lds, &n_wg);
+    rc = pick_wg(total, 0, lds, x->kind != TER_HIP_X_I8, &n_wg);
     if (rc) return rc;
     hipError_t e = launch_gemv(d, nullptr, nullptr, total, n_wg, lds, -1, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
@@ -636,7 +643,9 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     int rc = check_resid_overlap(resid, inputs);
     if (rc) return rc;
     int n_wg = 0;
-    rc = pick_wg(tile, wg_per_cu, lds, &n_wg);
+    bool prologue = false;
+    for (int i = 0; i < n; ++i) prologue = prologue || items[i].x.kind != TER_HIP_X_I8;
+    rc = pick_wg(tile, wg_per_cu, lds, prologue, &n_wg);
     if (rc) return rc;
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
