@@ -184,6 +184,30 @@ int gemv_vec_kind(const ter_hip_gemv_item_t* items, int n) {
     return kind;
 }
 
+// Strip mode for work lists below kSmallPlanTilesPerWg tiles per workgroup at
+// the default occupancy and with at most two strips per CU (beyond that a
+// workgroup would walk several strips' units one after the other, and the
+// stream-K partition is faster: 2 x 432 strips of 10 units, 7.5 against
+// 8.0 us): one workgroup per strip up to one per CU (two for int8 inputs,
+// which have no prologue to repeat).
+int pick_strip_mode(long long total_tiles, long long total_strips, bool prologue, bool* strip_mode, int* n_wg) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const int cus = device_cu_count(dev);
+    if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
+    *strip_mode = total_tiles < (long long)cus * kGemvWgPerCu * kSmallPlanTilesPerWg &&
+                  total_strips <= (long long)cus * kGemvWgPerCu;
+    if (!*strip_mode) return TER_HIP_OK;
+    long long g = (long long)cus * (prologue ? 1 : kGemvWgPerCu);
+    if (g > total_strips) g = total_strips;
+    const long long min_g = (total_strips + kStripModeMaxStrips - 1) / kStripModeMaxStrips;
+    if (g < min_g) g = min_g;
+    if (g < 1) g = 1;
+    *n_wg = (int)g;
+    return TER_HIP_OK;
+}
+
 int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, bool prologue, int* n_wg) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -297,6 +321,8 @@ struct ter_hip_plan {
     int n_wg = 0;
     int lds_bytes = 0;           // GEMV
     int vec_kind = -1;           // GEMV: common activation kind for the vector prologue, or -1
+    bool strip_mode = false;     // GEMV: strip-mode kernel, total counts strips
+    int part_off = 0;            // GEMV strip mode: LDS offset of the partial sums
     int mb = 0;                  // GEMM row-block count
     bool vec = false;            // GEMM: 16-byte X rows
     bool stream = false;         // GEMM: streaming kernel (M <= 16), total counts tiles
@@ -612,8 +638,8 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     *plan = nullptr;
     if (n < 1) return fail(TER_HIP_ERR_SHAPE, "empty work list");
     std::vector<GemvDesc> ds((size_t)n);
-    std::vector<long long> starts((size_t)n);
-    long long tile = 0;
+    std::vector<long long> starts((size_t)n), strip_starts((size_t)n);
+    long long tile = 0, strips = 0;
     uint64_t bytes = 0, macs = 0;
     int lds = 0;
     Ranges resid, inputs;
@@ -632,8 +658,11 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         if (it.resid) resid.emplace_back((uintptr_t)it.resid, (uintptr_t)(it.resid + it.w->N));
         act_ranges(&it.x, 1, it.w->K, &inputs);
         ds[(size_t)i] = make_desc(it.w, &it.x, o, tile);
+        ds[(size_t)i].strip0 = strips;
         starts[(size_t)i] = tile;
+        strip_starts[(size_t)i] = strips;
         tile += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
+        strips += ds[(size_t)i].n_strips;
         const int lb = is_rms(it.x.kind) ? gemv_lds_bytes_rms(it.w->K) : gemv_lds_bytes(it.w->K);
         if (lb > lds) lds = lb;
         bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.w->K * act_bytes(it.x.kind) +
@@ -645,17 +674,36 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     int n_wg = 0;
     bool prologue = false;
     for (int i = 0; i < n; ++i) prologue = prologue || items[i].x.kind != TER_HIP_X_I8;
-    rc = pick_wg(tile, wg_per_cu, lds, prologue, &n_wg);
-    if (rc) return rc;
+    bool strip_mode = false;
+    int part_off = 0;
+    if (wg_per_cu <= 0) {
+        rc = pick_strip_mode(tile, strips, prologue, &strip_mode, &n_wg);
+        if (rc) return rc;
+    }
+    if (strip_mode) {
+        part_off = (lds + 15) / 16 * 16;
+        const long long per_wg = (strips + n_wg - 1) / n_wg;
+        const int lds_strip = part_off + (int)per_wg * kGemvWaves * kStripCols * 4;
+        if (gemv_max_wg_per_cu(lds_strip) > 0)
+            lds = lds_strip;
+        else
+            strip_mode = false;  // partial sums do not fit beside the activations: stream-K
+    }
+    if (!strip_mode) {
+        rc = pick_wg(tile, wg_per_cu, lds, prologue, &n_wg);
+        if (rc) return rc;
+    }
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
-    rc = upload_plan(p, ds, starts, tile, n_wg);
+    rc = strip_mode ? upload_plan(p, ds, strip_starts, strips, n_wg) : upload_plan(p, ds, starts, tile, n_wg);
     if (rc) {
         delete p;
         return rc;
     }
     p->n = n;
-    p->total = tile;
+    p->total = strip_mode ? strips : tile;
+    p->strip_mode = strip_mode;
+    p->part_off = part_off;
     p->n_wg = n_wg;
     p->lds_bytes = lds;
     p->vec_kind = gemv_vec_kind(items, n);
@@ -682,8 +730,13 @@ int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
                              plan->n_wg, plan->mb, plan->vec, static_cast<hipStream_t>(stream));
     } else {
         GemvDesc none{};
-        e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev, plan->total,
-                        plan->n_wg, plan->lds_bytes, plan->vec_kind, static_cast<hipStream_t>(stream));
+        if (plan->strip_mode)
+            e = launch_gemv_strips(static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev, plan->total,
+                                   plan->n_wg, plan->lds_bytes, plan->part_off, plan->vec_kind,
+                                   static_cast<hipStream_t>(stream));
+        else
+            e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev, plan->total,
+                            plan->n_wg, plan->lds_bytes, plan->vec_kind, static_cast<hipStream_t>(stream));
     }
     if (e != hipSuccess) return hip_fail(e, "plan launch");
     return TER_HIP_OK;

@@ -55,6 +55,7 @@ struct alignas(16) GemvDesc {
     float* resid;                // fp32 [N]: resid += float(half(y)), or null
     unsigned long long* fix;     // N fix-up slots, zero at rest
     long long tile0;             // first tile of this GEMV in the launch's stream
+    long long strip0;            // first strip of this GEMV in the launch's strip stream (strip mode)
     int32_t K, N, Ku, n_strips;
     float w_scale, x_scale;
     int32_t x_kind;
@@ -82,6 +83,12 @@ struct alignas(16) GemmDesc {
 // device descriptor table `list_dev` and `first_dev`, the index of each
 // workgroup's first descriptor (range g starts at total * g / n_wg); single
 // launches pass nullptr for both.
+// Strip mode (small work lists): workgroups take whole column strips of the
+// strip stream ([total_strips] over the list) and reduce the waves' partials
+// in LDS at part_off; at most kStripModeMaxStrips strips per workgroup.
+constexpr int kStripModeMaxStrips = 32;
+hipError_t launch_gemv_strips(const GemvDesc* list_dev, const int32_t* first_dev, long long total_strips, int n_wg,
+                              int lds_bytes, int part_off, int vec_kind, hipStream_t st);
 // vec_kind: the activation kind of every GEMV of a work list that qualifies
 // for the vector prologue (gemv_vec_kind), else -1.
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const int32_t* first_dev,

@@ -942,6 +942,126 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
     if (have_prev) finish_fixups(prev);
 }
 
+// Strip mode, for work lists too small to keep the chip busy with whole
+// strips per wave: workgroup g takes strips [S g / n_wg, S (g + 1) / n_wg) of
+// the list's strip stream (S strips), and each strip's Ku units are split
+// over the 4 waves (wave w: units [Ku w / 4, Ku (w + 1) / 4)).  A wave streams
+// its units of every strip of a segment as one list of tiles, keeps each
+// strip's partial column sums in LDS, and after a barrier wave j % 4 adds the
+// four partials of strip j (integer sums, so the result is the stream-K
+// kernel's) and writes the outputs.  No fix-up slots, no global atomics.
+template <int kKind>
+__global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(const GemvDesc* __restrict__ list,
+                                                                  const int32_t* __restrict__ first,
+                                                                  long long total, int n_wg, int part_off) {
+    extern __shared__ __align__(16) unsigned char lds_raw[];
+    int g = blockIdx.x;
+    if ((n_wg & 7) == 0) g = (g & 7) * (n_wg >> 3) + (g >> 3);  // keep neighbouring ranges on one XCD
+    const long long s_begin = total * g / n_wg;
+    const long long s_end = total * (g + 1) / n_wg;
+    if (s_begin >= s_end) return;
+    int di = first[g];
+    const int wave = uniform(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int voff = lane * 16;
+    int* part = reinterpret_cast<int*>(lds_raw + part_off);  // [strip][wave][16 columns]
+    long long sg = s_begin;
+    while (sg < s_end) {
+        const GemvDesc d = list[di];
+        const long long seg_end = min(s_end, d.strip0 + (long long)d.n_strips);
+        const int sa = (int)(sg - d.strip0);  // first strip of the segment within the GEMV
+        const int ns = (int)(seg_end - sg);
+        const int u0 = d.Ku * wave / kGemvWaves;
+        const int nw = d.Ku * (wave + 1) / kGemvWaves - u0;  // units per strip of this wave
+        const int n = nw * ns;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(d.w + (long long)sa * d.Ku * kTileBytes), 0, ns * d.Ku * kTileBytes, 0x00020000);
+        // tile i of the wave's list: strip i / nw, unit u0 + i % nw; tracked
+        // incrementally (jl, kl) for the loads, past n an out-of-range offset
+        int jl = 0, kl = 0;
+        auto next_off = [&]() {
+            const int off = jl < ns ? ((jl * d.Ku + u0 + kl) * kTileBytes) : 0x7FFFF000 - voff;
+            if (++kl == nw) {
+                kl = 0;
+                ++jl;
+            }
+            return off;
+        };
+        auto load_b = [&](u32x4 (&w)[kBatch]) {
+#pragma unroll
+            for (int i = 0; i < kBatch; ++i) w[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + next_off(), 0, 2);
+        };
+        XPre xpre;
+        XRaw xraw;
+        if constexpr (kKind < 0)
+            x_prefetch(d, xpre);
+        else
+            x_prefetch_vec<kKind>(d, xraw);
+        u32x4 wa[kBatch], wb[kBatch];
+        if (nw > 0) load_b(wa);
+        int8_t* lds_x = reinterpret_cast<int8_t*>(lds_raw);
+        int* usum = reinterpret_cast<int*>(lds_raw + d.Ku * kUnitK);
+        float* red = reinterpret_cast<float*>(lds_raw + d.Ku * kUnitK + d.Ku * 4);
+        float* xs32 = reinterpret_cast<float*>(lds_raw + gemv_lds_xs32_offset(d.K));
+        __syncthreads();  // the previous segment is done with LDS
+        float act;
+        if constexpr (kKind < 0)
+            act = stage_x(d, xpre, lds_x, usum, red, xs32, sg == d.strip0);
+        else
+            act = stage_x_vec<kKind>(d, xraw, lds_x, usum, red, xs32, sg == d.strip0);
+        __syncthreads();
+        const float s = act * d.w_scale;  // x_scale * w_scale (forward.cpp:342)
+        const int q = lane & 15;
+        const int pcol = (lane >> 4) * 4 + q;  // column within the strip of lanes q < 4
+        if (nw == 0) {
+            for (int j = 0; j < ns; ++j)
+                if (q < 4) part[(j * kGemvWaves + wave) * 16 + pcol] = 0;
+        } else {
+            int a1[4] = {0, 0, 0, 0}, a4[4] = {0, 0, 0, 0};
+            int corr = 0, j = 0, k = 0;
+            auto compute_b = [&](const u32x4 (&w)[kBatch], int i0) {
+#pragma unroll
+                for (int i = 0; i < kBatch; ++i) {
+                    if (i0 + i < n) {
+                        const int u = u0 + k;
+                        const u32x4 xv = *reinterpret_cast<const u32x4*>(lds_x + u * kUnitK + q * 16);
+                        corr += usum[u];
+                        dot_tile(w[i], xv, a1, a4);
+                        if (++k == nw) {
+                            const int v = reduce_strip(a1, a4, corr);
+                            if (q < 4) part[(j * kGemvWaves + wave) * 16 + pcol] = v;
+                            corr = 0;
+                            k = 0;
+                            ++j;
+                        }
+                    }
+                }
+            };
+            int i0 = 0;
+            while (true) {
+                load_b(wb);
+                compute_b(wa, i0);
+                i0 += kBatch;
+                if (i0 >= n) break;
+                load_b(wa);
+                compute_b(wb, i0);
+                i0 += kBatch;
+                if (i0 >= n) break;
+            }
+        }
+        __syncthreads();
+        for (int j = wave; j < ns; j += kGemvWaves) {
+            const int col = (sa + j) * kStripCols + lane;
+            if (lane < 16 && col < d.N) {
+                const int* pj = part + j * kGemvWaves * 16 + lane;
+                emit(d, col, ((pj[0] + pj[16]) + pj[32]) + pj[48], s);
+            }
+        }
+        sg = seg_end;
+        ++di;
+    }
+}
+
 }  // namespace
 
 int gemv_max_wg_per_cu(int lds_bytes) {
@@ -984,6 +1104,37 @@ hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const i
     default:
         hipLaunchKernelGGL((gemv_t16_kernel<true, -1>), grid, block, lds_bytes, st, single, list_dev, first_dev,
                            total_tiles, n_wg);
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_strips(const GemvDesc* list_dev, const int32_t* first_dev, long long total_strips, int n_wg,
+                              int lds_bytes, int part_off, int vec_kind, hipStream_t st) {
+    const dim3 grid(n_wg), block(kGemvThreads);
+    switch (vec_kind) {
+    case TER_HIP_X_I8:
+        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_I8>), grid, block, lds_bytes, st, list_dev, first_dev,
+                           total_strips, n_wg, part_off);
+        break;
+    case TER_HIP_X_F32:
+        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_F32>), grid, block, lds_bytes, st, list_dev, first_dev,
+                           total_strips, n_wg, part_off);
+        break;
+    case TER_HIP_X_F32_RMS:
+        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_F32_RMS>), grid, block, lds_bytes, st, list_dev, first_dev,
+                           total_strips, n_wg, part_off);
+        break;
+    case TER_HIP_X_F16_RMS:
+        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_F16_RMS>), grid, block, lds_bytes, st, list_dev, first_dev,
+                           total_strips, n_wg, part_off);
+        break;
+    case TER_HIP_X_RELU2_RMS:
+        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_RELU2_RMS>), grid, block, lds_bytes, st, list_dev,
+                           first_dev, total_strips, n_wg, part_off);
+        break;
+    default:
+        hipLaunchKernelGGL((gemv_strip_kernel<-1>), grid, block, lds_bytes, st, list_dev, first_dev, total_strips,
+                           n_wg, part_off);
     }
     return hipGetLastError();
 }

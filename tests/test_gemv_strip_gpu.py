@@ -1,0 +1,82 @@
+"""GPU parity of the GEMV kernel's strip mode: small work lists (fewer than
+32 tiles per workgroup at two workgroups per CU, at most two strips per CU)
+give each workgroup whole column strips, split each strip's 256-row units
+over its four waves and add the waves' partial column sums in LDS; stream-K
+fix-up slots are not used.
+
+Bar: int32 accumulators and fp32 outputs bit-exact against the oracle
+(mm_row's integer dot products, src/tx/forward.cpp:342-345), for strips
+with fewer units than waves, partial last strips, many strips per
+workgroup and workgroup ranges that cross GEMV boundaries.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def run_list(specs, seed, launches=2, fp32=False):
+    """specs: (K, N) per GEMV, int8 inputs (fp32 with the absmax prologue if
+    fp32); checks acc and y after each launch."""
+    import torch
+    import ter_amd as T
+    items, refs = [], []
+    for i, (K, N) in enumerate(specs):
+        v11 = O.v11_pack(O.rand_trits(seed + 17 * i, K, N, 0.4))
+        ws = 0.01 + 0.003 * i
+        W = T.PackedTrits.from_v11(v11, K, N, ws)
+        out = dict(y=torch.empty(N, dtype=torch.float32, device="cuda"),
+                   acc=torch.empty(N, dtype=torch.int32, device="cuda"))
+        if fp32:
+            x = (np.random.default_rng(seed + i).standard_normal(K) * 2).astype(np.float32)
+            items.append(dict(w=W, x=dev(x), **out))
+            rq, rs = O.quant_int8(x)
+            refs.append(O.gemv_v11(rq, rs, v11, ws, K, N))
+        else:
+            x = O.rand_int8(seed + 31 * i, K)
+            items.append(dict(w=W, x=dev(x), x_scale=0.02, **out))
+            refs.append(O.gemv_v11(x, np.float32(0.02), v11, ws, K, N))
+    plan = T.Plan(items)
+    for rep in range(launches):
+        for it in items:
+            it["acc"].fill_(-7)
+        plan.launch()
+        for it, (ra, ry) in zip(items, refs):
+            assert (host(it["acc"]) == ra).all(), (rep, it["w"].K, it["w"].N)
+            assert (host(it["y"]).view(np.int32) == np.asarray(ry, np.float32).view(np.int32)).all()
+    plan.close()
+
+
+@pytest.mark.parametrize("K", [256, 512, 768, 1024, 2560, 6912], ids=lambda k: f"K{k}")
+def test_units_per_wave(cuda, K):
+    """Ku = 1, 2, 3 (waves without units write zero partials), 4, 10, 27."""
+    run_list([(K, 300)], seed=K)
+
+
+@pytest.mark.parametrize("K", [256, 2560])
+def test_two_strips_per_workgroup(cuda, K):
+    """512 strips with a prologue (one workgroup per CU): two strips per
+    workgroup, one range crossing the boundary between the two GEMVs at an
+    odd strip, ragged N."""
+    run_list([(K, 16 * 255 - 4), (K, 16 * 257)], seed=5 + K, fp32=True)
+
+
+def test_decode_shaped_lists(cuda):
+    """The decode step's lists: Q/K/V, O, gate/up, down (BitNet-2B shapes)."""
+    run_list([(2560, 2560), (2560, 640), (2560, 640)], seed=11)
+    run_list([(2560, 2560)], seed=12)
+    run_list([(2560, 6912), (2560, 6912)], seed=13)  # stream-K (864 strips)
+    run_list([(6912, 2560)], seed=14)

@@ -2,7 +2,9 @@
 share one activation kind, with K a multiple of 16 and 16-byte aligned x / up
 / gamma, run a kernel specialised on that kind (branch-free buffer loads of
 the activations, issued before the weights).  The same items placed at an
-unaligned offset take the general prologue.
+unaligned offset take the general prologue.  Small lists run in strip mode
+(whole strips per workgroup, partials reduced in LDS) unless wg_per_cu is
+given, which selects the stream-K partition.
 
 Bar: both placements give int32 accumulators, fp32 outputs, the int8
 activation copy and its scale bit-exact against the oracle (quant_int8_k,
@@ -119,14 +121,15 @@ def test_vector_and_general_prologue(cuda, kind, K, N):
     import ter_amd as T
     case = make_case(kind, K, N, seed=K + N + len(kind))
     for offset in (0, 1):  # 0: vector prologue, 1: general prologue
-        it = item_of(kind, case, K, N, offset)
-        plan = T.Plan([it])
-        for rep in range(2):
-            it["acc"].fill_(-7)
-            it["y"].fill_(-7)
-            plan.launch()
-            check(kind, it, case, (offset, rep))
-        plan.close()
+        for wg in (0, 2):  # 0: strip mode (a small list), 2: stream-K
+            it = item_of(kind, case, K, N, offset)
+            plan = T.Plan([it], wg_per_cu=wg)
+            for rep in range(2):
+                it["acc"].fill_(-7)
+                it["y"].fill_(-7)
+                plan.launch()
+                check(kind, it, case, (offset, wg, rep))
+            plan.close()
 
 
 @pytest.mark.parametrize("kind", KINDS)
