@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -336,9 +337,10 @@ struct ter_hip_plan {
 struct ter_hip_attn {
     int nh = 0, nkv = 0, hd = 0, smax = 0;
     bool neox = true;
+    bool xcd_local = false;     // the XCD-local exchange (dispatch checked at creation)
     float* rope = nullptr;      // [smax][hd/2][2]
-    float* part = nullptr;      // [nh][n_chunks][hd + 2]
-    unsigned* count = nullptr;  // [n_groups], zero at rest
+    float* part = nullptr;      // [nh][n_chunks][attn_part_stride(hd)]
+    unsigned* count = nullptr;  // [n_groups][attn_count_stride()], zero at rest
 };
 
 struct ter_hip_handle {
@@ -1060,7 +1062,7 @@ int ter_hip_attn_create(ter_hip_attn_t** out, int32_t n_heads, int32_t n_kv_head
     if (!out) return fail(TER_HIP_ERR_NULL, "null context pointer");
     *out = nullptr;
     if (n_heads < 1 || n_kv_heads < 1 || n_heads % n_kv_heads || !attn_supported_head_dim(head_dim) || s_max < 1 ||
-        s_max > attn_chunk() * attn_max_chunks())
+        s_max > attn_chunk() * attn_max_chunks() || (long long)s_max * n_kv_heads * head_dim * 2 > 0x7FFFFFFFLL)
         return fail(TER_HIP_ERR_SHAPE, "attention shape nh=%d nkv=%d hd=%d smax=%d unsupported", n_heads, n_kv_heads,
                     head_dim, s_max);
     if (rope_type != TER_HIP_ROPE_NORM && rope_type != TER_HIP_ROPE_NEOX)
@@ -1095,12 +1097,22 @@ int ter_hip_attn_create(ter_hip_attn_t** out, int32_t n_heads, int32_t n_kv_head
     a->smax = s_max;
     a->neox = rope_type == TER_HIP_ROPE_NEOX;
     const size_t tb = tab.size() * sizeof(float);
-    const size_t pb = (size_t)n_heads * n_chunks * (head_dim + 2) * sizeof(float);
-    const size_t cb = (size_t)groups * sizeof(unsigned);
+    const size_t pb = (size_t)n_heads * n_chunks * attn_part_stride(head_dim) * sizeof(float);
+    const size_t cb = (size_t)groups * attn_count_stride() * sizeof(unsigned);
     hipError_t e = hipMalloc(&a->rope, tb);
     if (e == hipSuccess) e = hipMalloc(&a->part, pb);
     if (e == hipSuccess) e = hipMalloc(&a->count, cb);
     if (e == hipSuccess) e = hipMemcpy(a->rope, tab.data(), tb, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    // the XCD-local exchange needs blocks on XCD b % 8; the partial buffer
+    // serves as the probe's scratch (it holds no state between launches)
+    const int nb = attn_local_blocks(n_heads, n_kv_heads, s_max);
+    // (TER_HIP_ATTN_DEVICE_WIDE=1 in the environment keeps the device-wide form)
+    const char* dw = std::getenv("TER_HIP_ATTN_DEVICE_WIDE");
+    const bool want_local = !(dw && dw[0] == '1');
+    if (e == hipSuccess && want_local && (size_t)nb * sizeof(int) <= pb)
+        a->xcd_local = attn_xcd_round_robin(nb, reinterpret_cast<int*>(a->part), nullptr);
+    if (e == hipSuccess) e = hipGetLastError();
     if (e == hipSuccess) e = hipMemset(a->count, 0, cb);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -1118,7 +1130,7 @@ int ter_hip_attn_decode(const ter_hip_attn_t* a, const uint16_t* q, const uint16
         !aligned(out, 2) || !aligned(pos_dev, 4))
         return fail(TER_HIP_ERR_ALIGN, "misaligned argument (caches need 16 bytes)");
     hipError_t e = launch_attn_decode(q, k, v, k_cache, v_cache, pos_dev, out, a->rope, a->part, a->count, a->nh,
-                                      a->nkv, a->hd, a->smax, a->neox, static_cast<hipStream_t>(stream));
+                                      a->nkv, a->hd, a->smax, a->neox, a->xcd_local, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "attention launch");
     return TER_HIP_OK;
 }

@@ -24,12 +24,20 @@
 // from the projection outputs (RoPE applied here), not from the cache, which
 // this launch writes.
 //
-// Cross-workgroup exchange without fences: partials are written with
-// agent-scope atomic stores (written through to the coherence point), each
-// thread waits for its stores to complete, then one arrival is counted with
-// an agent-scope atomic add; the workgroup that counts last reads the
-// partials with agent-scope atomic loads.  The count returns to zero.
+// Cross-workgroup exchange without fences.  Each thread waits for its
+// partial stores to complete, then one arrival per workgroup is counted with
+// an atomic add; the workgroup that counts last reads the partials.  The
+// count returns to zero.  Two forms of it:
+//   - XCD-local (the default where it holds): workgroups are dispatched to
+//     the 8 XCDs round-robin by block index (checked once per context by
+//     attn_xcd_round_robin), so the blocks of a head group are laid out on one
+//     XCD and everything goes through that XCD's L2: plain stores, an L2
+//     atomic, loads that bypass only L1.  Counters and partial rows are
+//     padded to whole 256-byte lines so no line is shared by two XCDs.
+//   - device-wide: agent-scope atomic stores (written through), an
+//     agent-scope atomic add, system-coherent loads that bypass L2.
 #include <type_traits>
+#include <vector>
 
 #include "common.h"
 
@@ -40,6 +48,8 @@ constexpr int kAttnWaves = 4;
 constexpr int kAttnThreads = kAttnWaves * 64;
 constexpr int kChunk = 64;       // positions per chunk (one per lane)
 constexpr int kMaxChunks = 64;   // combine: one lane per chunk
+constexpr int kXcds = 8;         // XCDs of an MI355X, dispatched round-robin
+constexpr int kCountStride = 64; // arrival counters, one per 256-byte line
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -52,9 +62,9 @@ struct AttnArgs {
     const int32_t* pos;     // device: the new token's position (< smax)
     uint16_t* out;          // fp16 [nh][hd]
     const float* rope;      // [smax][hd/2][2] (cos, sin)
-    float* part;            // [nh][n_chunks][hd + 2]: o_c[hd], m_c, l_c
-    unsigned* count;        // [n_groups], zero at rest
-    int nh, nkv, smax, n_chunks, neox, groups_per_kv;
+    float* part;            // [nh][n_chunks][attn_part_stride(hd)]: o_c[hd], m_c, l_c
+    unsigned* count;        // [n_groups][kCountStride], zero at rest
+    int nh, nkv, smax, n_chunks, neox, groups_per_kv, n_groups;
     float inv_sqrt;
 };
 
@@ -108,9 +118,14 @@ __device__ __forceinline__ float wave_max_f(float v) {
     return v;
 }
 
-template <int HD>
+// Floats per chunk partial (o_c[hd], m_c, l_c) rounded up to whole 256-byte lines.
+constexpr int part_stride(int hd) { return (hd + 2 + 63) / 64 * 64; }
+
+// kLocal: the XCD-local exchange (grid laid out by XCD), else device-wide.
+template <int HD, bool kLocal>
 __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 #pragma clang fp contract(off)
+    constexpr int PST = part_stride(HD);
     constexpr int KROW = HD * 2 + 16;  // padded K row in LDS (bytes): conflict-free 16-byte reads
     constexpr int VROW = HD * 2;
     constexpr int HALF = HD / 2;
@@ -126,49 +141,58 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int grp = blockIdx.x / a.n_chunks, chunk = blockIdx.x - grp * a.n_chunks;
+    int grp, chunk;
+    if constexpr (kLocal) {  // block b on XCD b % 8: group (r / n_chunks) * 8 + b % 8, r = b / 8
+        const int x = blockIdx.x % kXcds, r = blockIdx.x / kXcds, gq = r / a.n_chunks;
+        grp = gq * kXcds + x;
+        chunk = r - gq * a.n_chunks;
+        if (grp >= a.n_groups) return;
+    } else {
+        grp = blockIdx.x / a.n_chunks;
+        chunk = blockIdx.x - grp * a.n_chunks;
+    }
     const int g = grp / a.groups_per_kv;                      // KV head
     const int gs = a.nh / a.nkv;                              // query heads per KV head
     const int h0 = g * gs + (grp - g * a.groups_per_kv) * kAttnWaves;
     const int nhg = min(kAttnWaves, g * gs + gs - h0);        // query heads in this group
     const int s0 = chunk * kChunk;
-    const int rows = min(kChunk, a.smax - s0);                // cache rows of this chunk
     const long long row_stride = (long long)a.nkv * HD;        // halves between positions
 
-    // 1. K and V rows of the chunk, in flight before anything else (they do
-    // not depend on the position; rows past the sequence are zeroed below).
+    // 1. The position (a scalar load), then the loads that depend on it or
+    // on nothing: this position's RoPE table entries and the new token's q
+    // pair, k pair and v element of this thread (one each: nhg * hd/2 <= 256
+    // query pairs), then the chunk's K and V rows.  A wave's vector loads
+    // complete in issue order, so the RoPE inputs arrive before the cache
+    // rows and the rotations overlap the cache reads.  The small loads are
+    // unconditional, at clamped in-range addresses (values a thread does not
+    // use are ignored), so no branch makes the compiler wait for them early.
+    const int pos = *gptr(a.pos);
+    const int pos_c = min(max(pos, 0), a.smax - 1);           // address only; checked below
+    const int qi = tid / HALF, qk = tid - qi * HALF;          // query head of the group, pair
+    int q0, q1;
+    pair_index(qk, HD, a.neox != 0, q0, q1);
+    const TER_GLOBAL float* tab = gptr(a.rope) + (long long)pos_c * HD;  // [hd/2][2] of this position
+    const float rc = tab[2 * qk], rsn = tab[2 * qk + 1];
+    const TER_GLOBAL uint16_t* qh = gptr(a.q) + (long long)min(h0 + qi, a.nh - 1) * HD;
+    uint16_t qx0 = qh[q0], qx1 = qh[q1];
+    const TER_GLOBAL uint16_t* kh = gptr(a.k) + (long long)g * HD;  // pair qk of the KV head's key
+    uint16_t kx0 = kh[q0], kx1 = kh[q1];
+    const uint16_t vx = gptr(a.v)[(long long)g * HD + min(tid, HD - 1)];
+    // cache rows through buffer resources sized to the cache: rows past smax
+    // read as zeros, and no load sits behind a branch
     constexpr int kLoads = kChunk * VROW / 16 / kAttnThreads;  // 16-byte loads per thread per matrix
+    const int cache_bytes = a.smax * (int)row_stride * 2;
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kc, 0, cache_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(a.vc, 0, cache_bytes, 0x00020000);
     u32x4 kreg[kLoads], vreg[kLoads];
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
         const int idx = tid + i * kAttnThreads;               // 16-byte piece
         const int r = idx / (VROW / 16), cpart = idx - r * (VROW / 16);
-        kreg[i] = vreg[i] = u32x4{0u, 0u, 0u, 0u};
-        if (r < rows) {
-            const long long off = (long long)(s0 + r) * row_stride + (long long)g * HD + cpart * 8;
-            kreg[i] = *reinterpret_cast<const TER_GLOBAL u32x4*>(gptr(a.kc) + off);
-            vreg[i] = *reinterpret_cast<const TER_GLOBAL u32x4*>(gptr(a.vc) + off);
-        }
+        const int off = ((s0 + r) * (int)row_stride + g * HD + cpart * 8) * 2;
+        kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
+        vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
     }
-    // the new token's q pair, k pair and v element of this thread (one each:
-    // nhg * hd/2 <= 256 query pairs), also before the position is known
-    const int qi = tid / HALF, qk = tid - qi * HALF;  // query head of the group, pair
-    int q0, q1;
-    pair_index(qk, HD, a.neox != 0, q0, q1);
-    const bool has_q = tid < nhg * HALF;
-    uint16_t qx0 = 0, qx1 = 0, kx0 = 0, kx1 = 0, vx = 0;
-    if (has_q) {
-        const TER_GLOBAL uint16_t* qh = gptr(a.q) + (long long)(h0 + qi) * HD;
-        qx0 = qh[q0];
-        qx1 = qh[q1];
-    }
-    if (tid < HALF) {  // pair tid of the KV head's key (same indices as q pair tid)
-        const TER_GLOBAL uint16_t* kh = gptr(a.k) + (long long)g * HD;
-        kx0 = kh[q0];
-        kx1 = kh[q1];
-    }
-    if (tid < HD) vx = gptr(a.v)[(long long)g * HD + tid];
-    const int pos = *gptr(a.pos);
     if (pos < 0 || pos >= a.smax) return;                     // (the whole grid: no output, no count)
     const int seq = pos + 1;
     const int n = max(0, min(kChunk, seq - s0));              // positions in this chunk
@@ -176,13 +200,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     const bool writer = has_pos && grp == g * a.groups_per_kv;  // one workgroup per KV head writes the cache
 
     // 2. RoPE of the group's query heads into qs (as the fp16-rounded values).
-    const TER_GLOBAL float* tab = gptr(a.rope) + (long long)pos * HD;  // [hd/2][2] of this position
-    const float rc = tab[2 * qk], rsn = tab[2 * qk + 1];
-    if (has_q) {
-        rope_pair(qx0, qx1, rc, rsn);
-        qs[qi][q0] = qx0;
-        qs[qi][q1] = qx1;
-    }
+    // (every thread: rows of heads past the group's hold values no wave reads,
+    // and an unconditional use keeps the q loads ahead of the cache rows)
+    rope_pair(qx0, qx1, rc, rsn);
+    qs[qi][q0] = qx0;
+    qs[qi][q1] = qx1;
     // stage K (padded rows) and V; rows past the sequence as zeros
 #pragma unroll
     for (int i = 0; i < kLoads; ++i) {
@@ -290,52 +312,52 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         }
     }
     // 6. publish the partials (written through), then count the arrival
+    constexpr int kScope = kLocal ? __HIP_MEMORY_SCOPE_WORKGROUP : __HIP_MEMORY_SCOPE_AGENT;
     if (head_ok && n > 0) {
-        float* P = a.part + ((long long)(h0 + wave) * a.n_chunks + chunk) * (HD + 2);
+        float* P = a.part + ((long long)(h0 + wave) * a.n_chunks + chunk) * PST;
 #pragma unroll
-        for (int j = 0; j < DPT; ++j) __hip_atomic_store(P + d0 + j, acc[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int j = 0; j < DPT; ++j) __hip_atomic_store(P + d0 + j, acc[j], __ATOMIC_RELAXED, kScope);
         if (lane == 0) {
-            __hip_atomic_store(P + HD, mc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(P + HD + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(P + HD, mc, __ATOMIC_RELAXED, kScope);
+            __hip_atomic_store(P + HD + 1, lsum, __ATOMIC_RELAXED, kScope);
         }
     }
     __builtin_amdgcn_s_waitcnt(0);  // this thread's stores are complete
     asm volatile("" ::: "memory");
     __syncthreads();
     if (tid == 0) {
-        const unsigned prev =
-            __hip_atomic_fetch_add(a.count + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned* cnt = a.count + grp * kCountStride;
+        const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, kScope);
         last_flag = prev == (unsigned)a.n_chunks - 1u;
-        if (last_flag) __hip_atomic_store(a.count + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (last_flag) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, kScope);
     }
     __syncthreads();
     if (!last_flag || !head_ok) return;
 
     // 7. combine (last workgroup of the group): chunks in order.  The
-    // partials are read with system-coherent (SC1) buffer loads, which miss
-    // any stale copy in this XCD's L2, all issued before the first is used.
+    // partials are read with buffer loads that miss any stale copy (L1 for
+    // the XCD-local exchange: SC0; L1 and this XCD's L2 otherwise: SC1), all
+    // issued before the first is used; chunks past nc are out of the
+    // buffer's range and read as zeros.
     const int nc = (seq + kChunk - 1) / kChunk;
-    const float* Ph = a.part + (long long)(h0 + wave) * a.n_chunks * (HD + 2);
-    const __amdgpu_buffer_rsrc_t pr =
-        __builtin_amdgcn_make_buffer_rsrc((void*)Ph, 0, nc * (HD + 2) * 4, 0x00020000);
-    constexpr int kSC1 = 16;  // cache policy: system coherent
-    float m_l = -__builtin_inff(), l_l = 0.f;
-    if (lane < nc) {
-        m_l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (lane * (HD + 2) + HD) * 4, 0, kSC1));
-        l_l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (lane * (HD + 2) + HD + 1) * 4, 0, kSC1));
-    }
+    const float* Ph = a.part + (long long)(h0 + wave) * a.n_chunks * PST;
+    const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc((void*)Ph, 0, nc * PST * 4, 0x00020000);
+    constexpr int kCoh = kLocal ? 1 : 16;  // cache policy: SC0 / SC1
+    const float m_raw = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (lane * PST + HD) * 4, 0, kCoh));
+    const float l_l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (lane * PST + HD + 1) * 4, 0, kCoh));
     float pv[kMaxChunks][DPT];  // o_c[d0 .. d0 + DPT) for every chunk (zeros past nc: out of range)
 #pragma unroll
     for (int c = 0; c < kMaxChunks; ++c) {
         if constexpr (DPT == 2) {
             const unsigned long long w2 = __builtin_bit_cast(
-                unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(pr, (c * (HD + 2) + d0) * 4, 0, kSC1));
+                unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(pr, (c * PST + d0) * 4, 0, kCoh));
             pv[c][0] = __builtin_bit_cast(float, (unsigned)w2);
             pv[c][1] = __builtin_bit_cast(float, (unsigned)(w2 >> 32));
         } else {
-            pv[c][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (c * (HD + 2) + d0) * 4, 0, kSC1));
+            pv[c][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (c * PST + d0) * 4, 0, kCoh));
         }
     }
+    const float m_l = lane < nc ? m_raw : -__builtin_inff();
     const float M = wave_max_f(m_l);
     cw[wave][lane] = lane < nc ? attn_expf(m_l - M) : 0.f;
     cl[wave][lane] = l_l;
@@ -378,15 +400,46 @@ __global__ void rope_kernel(uint16_t* v, int n_heads, int hd, const float* rope,
     gptr(vh)[i1] = x1;
 }
 
+// Records the XCD of every block (XCC_ID hardware register).
+__global__ void xcc_probe_kernel(int* out) {
+    if (threadIdx.x == 0) {
+        unsigned v;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+        out[blockIdx.x] = (int)(v & 0xFu);
+    }
+}
+
 }  // namespace
 
 bool attn_supported_head_dim(int hd) { return hd == 64 || hd == 128; }
+int attn_part_stride(int hd) { return part_stride(hd); }
+int attn_count_stride() { return kCountStride; }
+int attn_local_blocks(int nh, int nkv, int smax) {
+    const int groups = nkv * ((nh / nkv + kAttnWaves - 1) / kAttnWaves);
+    return kXcds * ((groups + kXcds - 1) / kXcds) * ((smax + kChunk - 1) / kChunk);
+}
+
+bool attn_xcd_round_robin(int n_blocks, int* scratch, hipStream_t st) {
+    std::vector<int> h((size_t)n_blocks);
+    for (int rep = 0; rep < 4; ++rep) {  // (a few launches: the mapping must hold every time)
+        hipLaunchKernelGGL(xcc_probe_kernel, dim3(n_blocks), dim3(64), 0, st, scratch);
+        if (hipGetLastError() != hipSuccess) return false;
+        if (hipMemcpyAsync(h.data(), scratch, sizeof(int) * (size_t)n_blocks, hipMemcpyDeviceToHost, st) !=
+                hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess)
+            return false;
+        for (int b = 0; b < n_blocks; ++b)
+            if (h[(size_t)b] != b % kXcds) return false;
+    }
+    return true;
+}
+
 int attn_chunk() { return kChunk; }
 int attn_max_chunks() { return kMaxChunks; }
 
 hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc,
                               const int32_t* pos, uint16_t* out, const float* rope, float* part, unsigned* count,
-                              int nh, int nkv, int hd, int smax, bool neox, hipStream_t st) {
+                              int nh, int nkv, int hd, int smax, bool neox, bool xcd_local, hipStream_t st) {
     AttnArgs a{};
     a.q = q;
     a.k = k;
@@ -404,12 +457,22 @@ hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16
     a.n_chunks = (smax + kChunk - 1) / kChunk;
     a.neox = neox ? 1 : 0;
     a.groups_per_kv = (nh / nkv + kAttnWaves - 1) / kAttnWaves;
+    a.n_groups = nkv * a.groups_per_kv;
     a.inv_sqrt = (float)(1.0 / __builtin_sqrt((double)hd));
-    const dim3 grid(nkv * a.groups_per_kv * a.n_chunks), block(kAttnThreads);
-    if (hd == 128)
-        hipLaunchKernelGGL(attn_decode_kernel<128>, grid, block, 0, st, a);
-    else
-        hipLaunchKernelGGL(attn_decode_kernel<64>, grid, block, 0, st, a);
+    const dim3 block(kAttnThreads);
+    if (xcd_local) {
+        const dim3 grid(attn_local_blocks(nh, nkv, smax));
+        if (hd == 128)
+            hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, block, 0, st, a);
+    } else {
+        const dim3 grid(a.n_groups * a.n_chunks);
+        if (hd == 128)
+            hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, block, 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, block, 0, st, a);
+    }
     return hipGetLastError();
 }
 

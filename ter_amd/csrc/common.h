@@ -123,9 +123,17 @@ hipError_t launch_rmsnorm_f16_rows(const float* x, const uint16_t* gamma, float 
 bool attn_supported_head_dim(int hd);
 int attn_chunk();
 int attn_max_chunks();
+// Partial buffer [nh][n_chunks][attn_part_stride(hd)] floats; arrival
+// counters [n_groups][attn_count_stride()] (zero at rest).
+int attn_part_stride(int hd);
+int attn_count_stride();
+// Grid of the XCD-local launch, and whether blocks 0 .. n_blocks - 1 land on
+// XCD b % 8 (probed with n_blocks ints of device scratch; false on any error).
+int attn_local_blocks(int nh, int nkv, int smax);
+bool attn_xcd_round_robin(int n_blocks, int* scratch, hipStream_t st);
 hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc,
                               const int32_t* pos, uint16_t* out, const float* rope, float* part, unsigned* count,
-                              int nh, int nkv, int hd, int smax, bool neox, hipStream_t st);
+                              int nh, int nkv, int hd, int smax, bool neox, bool xcd_local, hipStream_t st);
 // Positions outside [0, smax) write nothing (both kernels).
 hipError_t launch_rope(uint16_t* v, int n_heads, int hd, const float* rope, const int32_t* pos, int smax, bool neox,
                        hipStream_t st);

@@ -3,6 +3,9 @@ launch per layer; rope_k, kv_copy_k, attention_k of
 cuda/ter_cuda_forward_bitnet.cu:185-214, 336-374 and the Llama forward's
 NORM-pairing rope_k, cuda/ter_cuda_forward_packed.cu:64-76).
 
+The cross-workgroup exchange runs in both of its forms (XCD-local and
+device-wide).
+
 Bar: the fp16 outputs bit-exact against the oracle's chunked order
 (orc_attention_splitk), and within one fp16 ulp of the reference's sequential
 order (orc_attention_ref; both orders' fp32 values are within 2e-6 of
@@ -68,6 +71,20 @@ def test_bitnet_decode_attention(cuda, positions):
     """BitNet-2B: 20 query / 5 KV heads, head_dim 128, NEOX, theta 5e5,
     2048-position cache (the C5 context)."""
     run_decode(20, 5, 128, 2048, 500000.0, True, positions, seed=positions[0] + 1)
+
+
+@pytest.mark.parametrize("form", ["xcd-local", "device-wide"])
+def test_exchange_forms(cuda, monkeypatch, form):
+    """Both forms of the cross-workgroup exchange (the context picks the
+    XCD-local one when blocks land on XCD b % 8; TER_HIP_ATTN_DEVICE_WIDE=1
+    keeps the device-wide one): BitNet shape, then Llama's 8 groups (one per
+    XCD), over consecutive positions sharing one context."""
+    if form == "device-wide":
+        monkeypatch.setenv("TER_HIP_ATTN_DEVICE_WIDE", "1")
+    else:
+        monkeypatch.delenv("TER_HIP_ATTN_DEVICE_WIDE", raising=False)
+    run_decode(20, 5, 128, 2048, 500000.0, True, [5, 6, 7, 2047], seed=31)
+    run_decode(32, 8, 64, 1000, 500000.0, False, [0, 999], seed=32)
 
 
 def test_llama_decode_attention(cuda):
