@@ -343,6 +343,10 @@ typedef struct ter_hip_attn ter_hip_attn_t;
  * reference's K_cache / V_cache slice of one layer), RoPE base theta.
  * Holds the RoPE table (fl(1/fl(theta^(2k/hd))), positions times that, cos
  * and sin in double rounded once to binary32) and the chunk workspace.
+ * Creation runs a probe kernel once: when blocks are dispatched to the 8 XCDs
+ * round-robin by index, launches keep each head group's partial exchange in
+ * one XCD's L2; otherwise (or with TER_HIP_ATTN_DEVICE_WIDE=1 in the
+ * environment) they use a device-wide exchange.  Same results either way.
  * Contexts are not shared between streams: launches of one context must not
  * overlap in time. */
 int ter_hip_attn_create(ter_hip_attn_t** a, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
