@@ -615,9 +615,14 @@ def run_decode(args):
     and the fused RMSNorm + lm_head + argmax, replayed from one HIP graph."""
     import torch
     from ter_amd import bitnet as B
-    c = B.Shape()
     t0 = time.perf_counter()
-    model = B.random_model(c, seed=5)
+    if args.bin:  # a packed model file ('TERT', tools/convert_bitnet_to_packed.py)
+        from ter_amd.modelfile import load_bitnet
+        model = load_bitnet(args.bin)
+        c = model.shape
+    else:
+        c = B.Shape()
+        model = B.random_model(c, seed=5)
     start, steps = 2048, args.steps
     dec = B.Decoder(model, start + max(steps, args.warmup, 64) + 64)
     g = torch.Generator(device="cuda")
@@ -657,9 +662,10 @@ def run_decode(args):
         "metric": "end-to-end greedy decode tokens/s (BitNet-2B-4T shape, KV 2048)",
         "value": round(1e3 / ms_tok, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": args.warmup,
         "ms_per_step": round(ms_tok, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8", "data": "synthetic",
-        "config": {"workload": "C5: random-init bitnet-b1.58-2b-4t-shaped decode, 30 layers, KV cache pre-filled "
-                               "to 2048 positions, one HIP graph per token",
+        "dtype": "int8", "data": "synthetic" if not args.bin else "model file, synthetic KV cache",
+        "config": {"workload": ("C5: random-init bitnet-b1.58-2b-4t-shaped decode" if not args.bin else
+                                f"C5: decode of {os.path.basename(args.bin)}") +
+                               f", {c.Nl} layers, KV cache pre-filled to 2048 positions, one HIP graph per token",
                    "launches_per_token": dec.launches_per_token(), "us_per_token": round(ev_tok * 1e3, 2),
                    "bytes_per_token": tok_bytes},
         "roofline": {"bound": "hbm", "achieved": round(tok_bytes / (ev_tok * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
@@ -698,6 +704,7 @@ def main():
     ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
     ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--bin", default=None, help="--config decode: load this packed BitNet model file ('TERT')")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--quick", action="store_true", help="skip the per-GEMV / grouped launch modes")
     args = ap.parse_args()

@@ -45,6 +45,7 @@ extern "C" {
 #define TER_HIP_ERR_ALIGN     -8  /* device pointer misaligned                  */
 #define TER_HIP_ERR_FULL      -9  /* kernel table has no free slot             */
 #define TER_HIP_ERR_CONFLICT -10  /* a plan names one weight twice (shared fix-up slots) */
+#define TER_HIP_ERR_FILE     -11  /* model file: cannot open, bad header, size mismatch, short read */
 
 /* ---- limits ---- */
 #define TER_HIP_K_MAX      32768  /* activation vector staged in LDS (int8)    */
@@ -366,6 +367,67 @@ int ter_hip_attn_decode(const ter_hip_attn_t* a, const uint16_t* q, const uint16
 /* RoPE in place on fp16 head vectors x [n_heads][hd] at *pos_dev (rope_k). */
 int ter_hip_rope(const ter_hip_attn_t* a, uint16_t* x, int32_t n_heads, const int32_t* pos_dev, void* stream);
 void ter_hip_attn_destroy(ter_hip_attn_t* a);
+
+/* ---------------------------------------------------------------------- */
+/* Packed model files: the flat .bin blobs of tools/convert_bitnet_to_packed.py */
+/* ('TERT', read by load_model_from_bin, cuda/ter_cuda_forward_bitnet.cu     */
+/* :698-784) and tools/convert_llama_to_packed.py ('LLRT', read by           */
+/* load_model_from_bin, cuda/ter_cuda_forward_packed.cu:589-659).  Little     */
+/* endian: a 64-byte header, token_embd fp16 [V][H], output_norm fp32 [H],    */
+/* then per layer the fp32 norms (attn_norm [H], ffn_norm [H]; TERT also      */
+/* attn_sub_norm [H], ffn_sub_norm [F]) and the seven projections Wq Wk Wv Wo */
+/* Wgate Wup Wdown, each K*(N/4) v11 bytes followed by its fp32 scale.        */
+/* ---------------------------------------------------------------------- */
+#define TER_HIP_BIN_TERT 0x54455254u  /* BitNet b1.58 (sub-norms, relu^2 FFN) */
+#define TER_HIP_BIN_LLRT 0x4C4C5254u  /* Llama, ternarized per tensor         */
+
+typedef struct ter_hip_bin_header {
+    uint32_t magic, version;           /* TER_HIP_BIN_*, 1                    */
+    uint32_t H, F, Nl, V, Nh, Nkv, Hd, Smax;
+    float    rope_theta, eps;
+} ter_hip_bin_header_t;
+
+#define TER_HIP_BIN_F16   0  /* fp16 [n]: token_embd                          */
+#define TER_HIP_BIN_F32   1  /* fp32 [n]: a norm (the loaders convert to fp16) */
+#define TER_HIP_BIN_TRITS 2  /* v11 packed trits [K*(N/4)] + fp32 scale        */
+
+typedef struct ter_hip_bin_tensor {
+    char     name[24];   /* token_embd, output_norm, attn_norm, ffn_norm,
+                            attn_sub_norm, ffn_sub_norm, Wq .. Wdown          */
+    int32_t  layer;      /* -1 for token_embd and output_norm                  */
+    int32_t  kind;       /* TER_HIP_BIN_*                                      */
+    int64_t  offset;     /* file offset of the data                            */
+    int64_t  bytes;      /* data bytes (trits: without the scale)              */
+    int64_t  n;          /* elements (F16 / F32)                               */
+    int32_t  K, N;       /* TRITS: input rows, output columns                   */
+    float    scale;      /* TRITS: the per-tensor scale that follows the data   */
+} ter_hip_bin_tensor_t;
+
+typedef struct ter_hip_bin ter_hip_bin_t;
+
+/* Open a model file: checks magic and version (as the reference loaders),
+ * shapes (N a multiple of 4 for every projection), and that the file holds
+ * exactly the tensors the header implies; reads the projection scales and
+ * builds the tensor directory.  Host only (no device work). */
+int ter_hip_bin_open(const char* path, ter_hip_bin_t** bin, ter_hip_bin_header_t* header);
+/* Number of tensors and entry i of the directory (file order). */
+int32_t ter_hip_bin_count(const ter_hip_bin_t* bin);
+int ter_hip_bin_tensor(const ter_hip_bin_t* bin, int32_t i, ter_hip_bin_tensor_t* out);
+/* Index of the tensor `name` of `layer` (-1 for the model-level tensors),
+ * or TER_HIP_ERR_NOTFOUND. */
+int32_t ter_hip_bin_find(const ter_hip_bin_t* bin, const char* name, int32_t layer);
+/* Tensor i into host memory: F16 and TRITS as stored (TRITS without the
+ * scale); F32 as stored, or, with as_f16, rounded to fp16 (to nearest even,
+ * the loaders' __float2half of read_f32_to_half_device). */
+int ter_hip_bin_read_host(const ter_hip_bin_t* bin, int32_t i, void* dst, int32_t as_f16);
+/* Tensor i (F16, or F32 as fp16) into device memory [n] fp16. */
+int ter_hip_bin_upload_f16(const ter_hip_bin_t* bin, int32_t i, uint16_t* dst_dev, void* stream);
+/* Projection i into `w` (initialised by ter_hip_wpk_init for its K x N; the
+ * scale is set from the file): the v11 bytes go through v11_stage_dev
+ * (K*(N/4) device bytes) and ter_hip_pack_v11. */
+int ter_hip_bin_upload_wpk(const ter_hip_bin_t* bin, int32_t i, ter_hip_wpk_t* w, uint8_t* v11_stage_dev,
+                           void* stream);
+void ter_hip_bin_close(ter_hip_bin_t* bin);
 
 /* ---------------------------------------------------------------------- */
 /* K4-style handle + KernelTable native slot                               */

@@ -26,6 +26,7 @@ ERR_HIP = -7
 ERR_ALIGN = -8
 ERR_FULL = -9
 ERR_CONFLICT = -10
+ERR_FILE = -11
 
 K_MAX = 32768
 N_MAX = 1 << 24
@@ -40,6 +41,9 @@ LAYOUT_T16 = 16
 ARGMAX_STATE_BYTES = 16512
 ROPE_NORM = 0
 ROPE_NEOX = 1
+BIN_TERT = 0x54455254
+BIN_LLRT = 0x4C4C5254
+BIN_F16, BIN_F32, BIN_TRITS = 0, 1, 2
 
 
 class WPK(C.Structure):
@@ -105,6 +109,27 @@ class GemmItem(C.Structure):
     ]
 
 
+class BinHeader(C.Structure):
+    """ter_hip_bin_header_t -- the 64-byte header of a packed model file."""
+    _fields_ = [(n, C.c_uint32) for n in ("magic", "version", "H", "F", "Nl", "V", "Nh", "Nkv", "Hd", "Smax")] + [
+        ("rope_theta", C.c_float), ("eps", C.c_float)]
+
+
+class BinTensor(C.Structure):
+    """ter_hip_bin_tensor_t -- one entry of a model file's tensor directory."""
+    _fields_ = [
+        ("name", C.c_char * 24),
+        ("layer", C.c_int32),
+        ("kind", C.c_int32),
+        ("offset", C.c_int64),
+        ("bytes", C.c_int64),
+        ("n", C.c_int64),
+        ("K", C.c_int32),
+        ("N", C.c_int32),
+        ("scale", C.c_float),
+    ]
+
+
 class OpCounts(C.Structure):
     _fields_ = [
         ("total_ops", C.c_uint64),
@@ -153,6 +178,14 @@ SIGNATURES = [
     ("ter_hip_attn_decode", C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P]),
     ("ter_hip_rope", C.c_int, [_P, _P, C.c_int32, _P, _P]),
     ("ter_hip_attn_destroy", None, [_P]),
+    ("ter_hip_bin_open", C.c_int, [C.c_char_p, C.POINTER(C.c_void_p), C.POINTER(BinHeader)]),
+    ("ter_hip_bin_count", C.c_int32, [_P]),
+    ("ter_hip_bin_tensor", C.c_int, [_P, C.c_int32, C.POINTER(BinTensor)]),
+    ("ter_hip_bin_find", C.c_int32, [_P, C.c_char_p, C.c_int32]),
+    ("ter_hip_bin_read_host", C.c_int, [_P, C.c_int32, _P, C.c_int32]),
+    ("ter_hip_bin_upload_f16", C.c_int, [_P, C.c_int32, _P, _P]),
+    ("ter_hip_bin_upload_wpk", C.c_int, [_P, C.c_int32, C.POINTER(WPK), _P, _P]),
+    ("ter_hip_bin_close", None, [_P]),
     ("ter_hip_create", _P, [C.c_int32]),
     ("ter_hip_destroy", None, [_P]),
     ("ter_hip_install_native", C.c_int, [_P, C.c_char_p, NATIVE_FN]),

@@ -19,11 +19,9 @@
 #include "common.h"
 
 namespace terhip {
-namespace {
 
 thread_local std::string g_last_error;
 
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char* fmt, ...) {
     char buf[512];
     va_list ap;
@@ -37,6 +35,8 @@ int fail(int code, const char* fmt, ...) {
 int hip_fail(hipError_t e, const char* what) {
     return fail(TER_HIP_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
+
+namespace {
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 

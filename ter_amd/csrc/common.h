@@ -285,6 +285,11 @@ __host__ __device__ inline int gemv_lds_bytes(int32_t K) {
 __host__ __device__ inline int gemv_lds_xs32_offset(int32_t K) { return (gemv_lds_bytes(K) + 15) / 16 * 16; }
 inline int gemv_lds_bytes_rms(int32_t K) { return gemv_lds_xs32_offset(K) + units_of(K) * kUnitK * 4; }
 
+// Status helpers of the C-ABI (abi.hip): record the message returned by
+// ter_hip_last_error() and return `code` (TER_HIP_ERR_HIP for hip_fail).
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t e, const char* what);
+
 int device_cu_count(int device);
 // Resident GEMV workgroups per CU at this LDS size (0 if the query fails).
 int gemv_max_wg_per_cu(int lds_bytes);
