@@ -210,8 +210,9 @@ typedef struct ter_hip_gemv_item {
 typedef struct ter_hip_plan ter_hip_plan_t;
 
 /* Build a launch plan for `n` GEMVs (descriptor table copied to the device).
- * wg_per_cu <= 0 picks the default occupancy (2 workgroups per CU; 1 for
- * small plans whose activations need a prologue).  When every item has the
+ * wg_per_cu <= 0 picks the default launch shape (2 workgroups per CU, 4 for
+ * int8 lists that take the vector prologue; small lists: whole strips per
+ * workgroup, or 1 workgroup per CU when their activations need a prologue).  When every item has the
  * same activation kind, K % 16 == 0 and 16-byte aligned x / up / gamma, the
  * plan launches the kernel specialised on that kind.  Items sharing a weight must not
  * appear twice in one plan, and no two items may write overlapping `resid`

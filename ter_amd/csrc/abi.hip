@@ -162,6 +162,10 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip
 // wave's piece would exceed kMaxPieceTiles (its buffer resource spans at most
 // 2^31 bytes).  wg_per_cu > 0 overrides (tuning).
 constexpr int kGemvWgPerCu = 2;
+// Work lists of int8 GEMVs qualifying for the vector prologue run the int8
+// kernel (96 VGPRs): four workgroups per CU hide more latency there (C2
+// Llama sweep: 42.6 against 43.3 us at two); the other kinds keep two.
+constexpr int kGemvWgPerCuI8 = 4;
 // A launch whose activations need a prologue (any kind but X_I8) and that
 // has fewer tiles than this per workgroup at kGemvWgPerCu uses one workgroup
 // per CU: every workgroup repeats the prologue, and below this size halving
@@ -209,15 +213,16 @@ int pick_strip_mode(long long total_tiles, long long total_strips, bool prologue
     return TER_HIP_OK;
 }
 
-int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, bool prologue, int* n_wg) {
+int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, bool prologue, int vec_kind, int* n_wg) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     const int cus = device_cu_count(dev);
     if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
-    const int fit = gemv_max_wg_per_cu(lds_bytes);
+    const int fit = gemv_max_wg_per_cu(lds_bytes, vec_kind);
     if (fit <= 0) return fail(TER_HIP_ERR_SHAPE, "GEMV workgroup does not fit a CU (LDS %d bytes)", lds_bytes);
-    int per_cu = wg_per_cu > 0 ? wg_per_cu : (kGemvWgPerCu < fit ? kGemvWgPerCu : fit);
+    const int dflt = vec_kind == TER_HIP_X_I8 ? kGemvWgPerCuI8 : kGemvWgPerCu;
+    int per_cu = wg_per_cu > 0 ? wg_per_cu : (dflt < fit ? dflt : fit);
     if (wg_per_cu <= 0 && prologue && total_tiles < (long long)cus * kGemvWgPerCu * kSmallPlanTilesPerWg) per_cu = 1;
     long long g = (long long)cus * per_cu;
     const long long min_g = (total_tiles + kMaxPieceTiles * kGemvWaves - 1) / (kMaxPieceTiles * kGemvWaves);
@@ -578,7 +583,7 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
     const long long total = (long long)d.n_strips * d.Ku;
     int n_wg = 0;
     const int lds = is_rms(x->kind) ? gemv_lds_bytes_rms(w->K) : gemv_lds_bytes(w->K);
-    rc = pick_wg(total, 0, lds, x->kind != TER_HIP_X_I8, &n_wg);
+    rc = pick_wg(total, 0, lds, x->kind != TER_HIP_X_I8, -1, &n_wg);
     if (rc) return rc;
     hipError_t e = launch_gemv(d, nullptr, nullptr, total, n_wg, lds, -1, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
@@ -676,6 +681,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     int n_wg = 0;
     bool prologue = false;
     for (int i = 0; i < n; ++i) prologue = prologue || items[i].x.kind != TER_HIP_X_I8;
+    const int vec_kind = gemv_vec_kind(items, n);
     bool strip_mode = false;
     int part_off = 0;
     if (wg_per_cu <= 0) {
@@ -692,7 +698,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
             strip_mode = false;  // partial sums do not fit beside the activations: stream-K
     }
     if (!strip_mode) {
-        rc = pick_wg(tile, wg_per_cu, lds, prologue, &n_wg);
+        rc = pick_wg(tile, wg_per_cu, lds, prologue, vec_kind, &n_wg);
         if (rc) return rc;
     }
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
@@ -708,7 +714,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     p->part_off = part_off;
     p->n_wg = n_wg;
     p->lds_bytes = lds;
-    p->vec_kind = gemv_vec_kind(items, n);
+    p->vec_kind = vec_kind;
     p->bytes = bytes;
     p->macs = macs;
     *plan = p;

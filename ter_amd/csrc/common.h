@@ -292,6 +292,6 @@ int hip_fail(hipError_t e, const char* what);
 
 int device_cu_count(int device);
 // Resident GEMV workgroups per CU at this LDS size (0 if the query fails).
-int gemv_max_wg_per_cu(int lds_bytes);
+int gemv_max_wg_per_cu(int lds_bytes, int vec_kind = -1);
 
 }  // namespace terhip

@@ -1064,12 +1064,22 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(const GemvDesc
 
 }  // namespace
 
-int gemv_max_wg_per_cu(int lds_bytes) {
+int gemv_max_wg_per_cu(int lds_bytes, int vec_kind) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel<true, -1>, kGemvThreads, lds_bytes) !=
-        hipSuccess)
-        return 0;
-    return n;
+    hipError_t e;
+    switch (vec_kind) {
+    case TER_HIP_X_I8:
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel<true, TER_HIP_X_I8>, kGemvThreads,
+                                                         lds_bytes);
+        break;
+    case TER_HIP_X_F32:
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel<true, TER_HIP_X_F32>, kGemvThreads,
+                                                         lds_bytes);
+        break;
+    default:  // the general kernel needs the most registers of all
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_t16_kernel<true, -1>, kGemvThreads, lds_bytes);
+    }
+    return e == hipSuccess ? n : 0;
 }
 
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const int32_t* first_dev,
