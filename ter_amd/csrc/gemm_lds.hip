@@ -68,10 +68,11 @@ struct LCfg {
 };
 
 // The configuration per row-block count (M <= 16, 32, 64, 128), measured on the
-// BitNet-2B sweep: every wave covers all rows (RS = 1) and 4 strips, so a
-// block is 32 strips and X is staged once per 32 weight tiles; three stages
-// where the LDS allows two workgroups per CU (M <= 32), two above.
-using Cfg1 = LCfg<1, 4, 1, 3>;
+// BitNet-2B sweep: every wave covers all rows (RS = 1); 2 strips per wave at
+// M <= 16 (16-strip blocks, 60 KiB for three stages: two workgroups per CU,
+// 116.7 against 122.9 us with 4 strips and one), 4 above (32-strip blocks, X
+// staged once per 32 weight tiles); three stages up to M = 32, two above.
+using Cfg1 = LCfg<1, 2, 1, 3>;
 using Cfg2 = LCfg<2, 4, 1, 3>;
 using Cfg4 = LCfg<4, 4, 1, 2>;
 using Cfg8 = LCfg<8, 4, 1, 2>;
