@@ -153,6 +153,7 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip
     d.w_scale = w->scale;
     d.x_scale = x->scale;
     d.x_kind = x->kind;
+    d.stage32 = is_rms(x->kind) && gemv_stage32(w->K) ? 1 : 0;
     return d;
 }
 
@@ -183,6 +184,7 @@ int gemv_vec_kind(const ter_hip_gemv_item_t* items, int n) {
     for (int i = 0; i < n; ++i) {
         const ter_hip_act_t& x = items[i].x;
         if (x.kind != kind || items[i].w->K % 16 != 0 || !a16(x.data)) return -1;
+        if (is_rms(x.kind) && !gemv_stage32(items[i].w->K)) return -1;  // the vector prologue always stages
         if (x.kind == TER_HIP_X_RELU2_RMS && !a16(x.up)) return -1;
         if (is_rms(x.kind) && !a16(x.gamma)) return -1;
     }
@@ -582,7 +584,7 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
     const GemvDesc d = make_desc(w, x, *out, 0);
     const long long total = (long long)d.n_strips * d.Ku;
     int n_wg = 0;
-    const int lds = is_rms(x->kind) ? gemv_lds_bytes_rms(w->K) : gemv_lds_bytes(w->K);
+    const int lds = d.stage32 ? gemv_lds_bytes_rms(w->K) : gemv_lds_bytes(w->K);
     rc = pick_wg(total, 0, lds, x->kind != TER_HIP_X_I8, -1, &n_wg);
     if (rc) return rc;
     hipError_t e = launch_gemv(d, nullptr, nullptr, total, n_wg, lds, -1, static_cast<hipStream_t>(stream));
@@ -670,7 +672,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         strip_starts[(size_t)i] = strips;
         tile += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
         strips += ds[(size_t)i].n_strips;
-        const int lb = is_rms(it.x.kind) ? gemv_lds_bytes_rms(it.w->K) : gemv_lds_bytes(it.w->K);
+        const int lb = ds[(size_t)i].stage32 ? gemv_lds_bytes_rms(it.w->K) : gemv_lds_bytes(it.w->K);
         if (lb > lds) lds = lb;
         bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.w->K * act_bytes(it.x.kind) +
                  (uint64_t)it.w->N * out_bytes(o);

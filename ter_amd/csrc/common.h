@@ -56,6 +56,7 @@ struct alignas(16) GemvDesc {
     unsigned long long* fix;     // N fix-up slots, zero at rest
     long long tile0;             // first tile of this GEMV in the launch's stream
     long long strip0;            // first strip of this GEMV in the launch's strip stream (strip mode)
+    int32_t stage32;             // RMS kinds: fp32 activations staged in LDS (else re-read for the sums)
     int32_t K, N, Ku, n_strips;
     float w_scale, x_scale;
     int32_t x_kind;
@@ -284,6 +285,10 @@ __host__ __device__ inline int gemv_lds_bytes(int32_t K) {
 // this 16-byte aligned offset.
 __host__ __device__ inline int gemv_lds_xs32_offset(int32_t K) { return (gemv_lds_bytes(K) + 15) / 16 * 16; }
 inline int gemv_lds_bytes_rms(int32_t K) { return gemv_lds_xs32_offset(K) + units_of(K) * kUnitK * 4; }
+// LDS of one workgroup on gfx950, and whether an RMS kind at this K stages
+// its fp32 activations (the staging costs 4 bytes per element).
+constexpr int kLdsMax = 160 * 1024;
+inline bool gemv_stage32(int32_t K) { return gemv_lds_bytes_rms(K) <= kLdsMax; }
 
 // Status helpers of the C-ABI (abi.hip): record the message returned by
 // ter_hip_last_error() and return `code` (TER_HIP_ERR_HIP for hip_fail).

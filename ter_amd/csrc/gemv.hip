@@ -288,6 +288,21 @@ __device__ __forceinline__ float stage_x(const GemvDesc& d, const XPre& r, int8_
         // gamma for the prefetched chunks, in flight during the reduction
         if (c0 < nchunks) load_h16_raw(d.gamma, c0 * 16, K, g0);
         if (c1 < nchunks) load_h16_raw(d.gamma, c1 * 16, K, g1);
+        float ss;
+        if (!d.stage32) {
+            // K too large to stage fp32 activations beside the int8 ones: the
+            // strided sums re-read the inputs (L2-resident) in the same order
+            if (d.x_kind == TER_HIP_X_RELU2_RMS) {
+                ss = relu2_sum_sq_1024(static_cast<const uint16_t*>(d.x), d.up, K, red);
+            } else {
+                float part = 0.f;
+                for (int i = tid; i < K; i += kGemvThreads) {
+                    const float v = x_at(d, i);
+                    part = __builtin_fmaf(v, v, part);
+                }
+                ss = tree_sum256(part, red);
+            }
+        } else {
         // the (zero-padded) activations as fp32 in LDS, so the sum of squares
         // reads them in the reference's strided order without a second pass
         // over global memory
@@ -304,7 +319,6 @@ __device__ __forceinline__ float stage_x(const GemvDesc& d, const XPre& r, int8_
             put16(c, t);
         }
         __syncthreads();
-        float ss;
         if (d.x_kind == TER_HIP_X_RELU2_RMS) {
             // 1024 virtual threads: element i goes to partial (i / 256) % 4 of thread i % 256
             float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
@@ -327,10 +341,18 @@ __device__ __forceinline__ float stage_x(const GemvDesc& d, const XPre& r, int8_
             }
             ss = tree_sum256(part, red);
         }
+        }
         rms_inv = 1.0f / __builtin_sqrtf(ss / (float)K + d.eps);
     }
     float v0[16], v1[16];
-    if (rms) {
+    if (rms && !d.stage32) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int sh = 16 * (i & 1);
+            v0[i] = (r.v0[i] * rms_inv) * half_bits_to_float((uint16_t)(g0[i >> 1] >> sh));
+            v1[i] = (r.v1[i] * rms_inv) * half_bits_to_float((uint16_t)(g1[i >> 1] >> sh));
+        }
+    } else if (rms) {
         // the chunks come back from LDS, so the prefetch registers are free
         // during the reduction
 #pragma unroll
@@ -361,7 +383,7 @@ __device__ __forceinline__ float stage_x(const GemvDesc& d, const XPre& r, int8_
     }
     for (int c = tid + 2 * kGemvThreads; c < nchunks; c += kGemvThreads) {
         float t[16];
-        if (rms) {
+        if (rms && d.stage32) {
 #pragma unroll
             for (int i = 0; i < 16; i += 4) {
                 const f32x4 f = *reinterpret_cast<const f32x4*>(xs32 + c * 16 + i);
@@ -370,6 +392,7 @@ __device__ __forceinline__ float stage_x(const GemvDesc& d, const XPre& r, int8_
             rms_apply(d, c * 16, rms_inv, t);
         } else {
             load_x16f(d, c * 16, t);
+            if (rms) rms_apply(d, c * 16, rms_inv, t);
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) m = fmaxf(m, fabsf(t[i]));

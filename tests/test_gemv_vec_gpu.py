@@ -147,3 +147,19 @@ def test_vector_prologue_multi_item(cuda, kind, wg):
         for it, c in zip(items, cases):
             check(kind, it, c, (wg, rep, it["w"].K, it["w"].N))
     plan.close()
+
+
+@pytest.mark.parametrize("kind", ["f32_rms", "f16_rms", "relu2"])
+def test_rms_prologue_at_k_max(cuda, kind):
+    """K = 32768 (TER_HIP_K_MAX): the fp32 staging of the RMS prologue no
+    longer fits beside the int8 activations in LDS, so the sums of squares
+    re-read the inputs (same order); the list takes the general prologue."""
+    import ter_amd as T
+    K, N = 32768, 48
+    case = make_case(kind, K, N, seed=4242 + len(kind))
+    for wg in (0, 1):
+        it = item_of(kind, case, K, N, 0)
+        plan = T.Plan([it], wg_per_cu=wg)
+        plan.launch()
+        check(kind, it, case, wg)
+        plan.close()
