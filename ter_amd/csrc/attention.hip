@@ -112,9 +112,38 @@ __device__ __forceinline__ void pair_index(int k, int hd, bool neox, int& i0, in
     i1 = neox ? k + hd / 2 : 2 * k + 1;
 }
 
+__device__ __forceinline__ int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
+}
+
+// Max over the 64 lanes (every lane gets it): DPP inside each row of 16
+// lanes, then two cross-row exchanges (the max is exact in any order).
 __device__ __forceinline__ float wave_max_f(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+    v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+
+// The xor butterfly sum  for o = 32, 16, ..., 1: v += v[lane ^ o]  (every
+// lane ends with the same bits; each level adds the same two operands as the
+// lane-shuffle form, so the result is that form's).  Levels 8 .. 1 use DPP
+// inside a row of 16 lanes: xor 8 is a rotation by 8, xor 4 takes the row
+// shifted by 4 in one direction or the other, xor 2 and 1 are quad
+// permutations.
+__device__ __forceinline__ float xor_sum64(float v) {
+    v = v + __shfl_xor(v, 32);
+    v = v + __shfl_xor(v, 16);
+    v = v + dpp_f<0x128>(v);  // row_ror:8 (lane ^ 8 within the row)
+    const float up = dpp_f<0x104>(v), down = dpp_f<0x114>(v);  // row_shl:4 (lane + 4), row_shr:4 (lane - 4)
+    v = v + (((threadIdx.x & 4) == 0) ? up : down);
+    v = v + dpp_f<0x4E>(v);   // quad_perm [2,3,0,1] (lane ^ 2)
+    v = v + dpp_f<0xB1>(v);   // quad_perm [1,0,3,2] (lane ^ 1)
     return v;
 }
 
@@ -135,8 +164,6 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     __shared__ __align__(16) unsigned char vs[kChunk * VROW];
     __shared__ __align__(16) uint16_t qs[kAttnWaves][HD];  // RoPE'd query heads (fp16, as the reference rounds them)
     __shared__ __align__(16) float es[kAttnWaves][kChunk];
-    __shared__ float cw[kAttnWaves][kMaxChunks];  // combine: w_c
-    __shared__ float cl[kAttnWaves][kMaxChunks];  // combine: l_c
     __shared__ int last_flag;
 
     const int tid = threadIdx.x;
@@ -271,8 +298,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     const float mc = wave_max_f(score);
     const float e = lane < n ? attn_expf(score - mc) : 0.f;
     float lsum = e;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) lsum = lsum + __shfl_xor(lsum, o);
+    lsum = xor_sum64(lsum);
     es[wave][lane] = e;
     __syncthreads();
 
@@ -336,45 +362,61 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
 
     // 7. combine (last workgroup of the group): chunks in order.  The
     // partials are read with buffer loads that miss any stale copy (L1 for
-    // the XCD-local exchange: SC0; L1 and this XCD's L2 otherwise: SC1), all
-    // issued before the first is used; chunks past nc are out of the
-    // buffer's range and read as zeros.
+    // the XCD-local exchange: SC0; L1 and this XCD's L2 otherwise: SC1);
+    // chunks past nc are out of the buffer's range and read as zeros.  Lane c
+    // holds chunk c's (m_c, l_c); the output partials go in groups of 8
+    // chunks, the loads of one group in flight while the previous is added.
     const int nc = (seq + kChunk - 1) / kChunk;
     const float* Ph = a.part + (long long)(h0 + wave) * a.n_chunks * PST;
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc((void*)Ph, 0, nc * PST * 4, 0x00020000);
     constexpr int kCoh = kLocal ? 1 : 16;  // cache policy: SC0 / SC1
-    const float m_raw = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (lane * PST + HD) * 4, 0, kCoh));
-    const float l_l = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (lane * PST + HD + 1) * 4, 0, kCoh));
-    float pv[kMaxChunks][DPT];  // o_c[d0 .. d0 + DPT) for every chunk (zeros past nc: out of range)
+    constexpr int G = 8;                   // chunks per group
+    auto load_group = [&](int gi, float (&pg)[G][DPT]) {
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) {
-        if constexpr (DPT == 2) {
-            const unsigned long long w2 = __builtin_bit_cast(
-                unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(pr, (c * PST + d0) * 4, 0, kCoh));
-            pv[c][0] = __builtin_bit_cast(float, (unsigned)w2);
-            pv[c][1] = __builtin_bit_cast(float, (unsigned)(w2 >> 32));
-        } else {
-            pv[c][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, (c * PST + d0) * 4, 0, kCoh));
+        for (int c = 0; c < G; ++c) {
+            const int off = ((gi * G + c) * PST + d0) * 4;
+            if constexpr (DPT == 2) {
+                const unsigned long long w2 =
+                    __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(pr, off, 0, kCoh));
+                pg[c][0] = __builtin_bit_cast(float, (unsigned)w2);
+                pg[c][1] = __builtin_bit_cast(float, (unsigned)(w2 >> 32));
+            } else {
+                pg[c][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, kCoh));
+            }
         }
-    }
-    const float m_l = lane < nc ? m_raw : -__builtin_inff();
+    };
+    const unsigned long long ml =
+        __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(pr, (lane * PST + HD) * 4, 0, kCoh));
+    float pa[G][DPT], pb[G][DPT];
+    load_group(0, pa);
+    const float m_l = lane < nc ? __builtin_bit_cast(float, (unsigned)ml) : -__builtin_inff();
     const float M = wave_max_f(m_l);
-    cw[wave][lane] = lane < nc ? attn_expf(m_l - M) : 0.f;
-    cl[wave][lane] = l_l;
-    // (each wave reads only its own rows of cw / cl: a wave-local exchange)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_wave_barrier();
+    // lane c's weight and sum, read with v_readlane (a uniform lane per step)
+    const int w_bits = __builtin_bit_cast(int, lane < nc ? attn_expf(m_l - M) : 0.f);
+    const int l_bits = (int)(unsigned)(ml >> 32);
     float L = 0.f;
     float O[DPT];
 #pragma unroll
     for (int j = 0; j < DPT; ++j) O[j] = 0.f;
-    // chunks past nc have w = 0 and o = 0 (out-of-range loads): exact no-ops
+    // chunks past nc have w = 0 and o = 0: exact no-ops.  Two groups per
+    // step with no exit between them; at most 64 chunks, so every lane index
+    // read below is < 64.
+    auto add_group = [&](int gi, const float (&pg)[G][DPT]) {
 #pragma unroll
-    for (int c = 0; c < kMaxChunks; ++c) {
-        const float w = cw[wave][c];
-        L = __builtin_fmaf(cl[wave][c], w, L);
+        for (int c = 0; c < G; ++c) {
+            const int src = uniform_i(gi * G + c);
+            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(w_bits, src));
+            L = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(l_bits, src)), w, L);
 #pragma unroll
-        for (int j = 0; j < DPT; ++j) O[j] = __builtin_fmaf(pv[c][j], w, O[j]);
+            for (int j = 0; j < DPT; ++j) O[j] = __builtin_fmaf(pg[c][j], w, O[j]);
+        }
+    };
+    const int ng = (nc + G - 1) / G;
+    for (int gi = 0; gi < ng; gi += 2) {
+        load_group(gi + 1, pb);
+        add_group(gi, pa);
+        load_group(gi + 2, pa);
+        add_group(gi + 1, pb);
     }
     uint16_t* oh = a.out + (long long)(h0 + wave) * HD + d0;
 #pragma unroll
