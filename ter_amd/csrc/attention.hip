@@ -152,7 +152,7 @@ constexpr int part_stride(int hd) { return (hd + 2 + 63) / 64 * 64; }
 
 // kLocal: the XCD-local exchange (grid laid out by XCD), else device-wide.
 template <int HD, bool kLocal>
-__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a_in) {
 #pragma clang fp contract(off)
     constexpr int PST = part_stride(HD);
     constexpr int KROW = HD * 2 + 16;  // padded K row in LDS (bytes): conflict-free 16-byte reads
@@ -166,6 +166,13 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     __shared__ __align__(16) float es[kAttnWaves][kChunk];
     __shared__ int last_flag;
 
+    // Every kernel argument in one round of scalar loads: left to itself the
+    // compiler fetches them in several dependent rounds around the branches
+    // below, each a scalar-cache miss on the launch's critical path.
+    AttnArgs a = a_in;
+    asm volatile("" : "+s"(a.q), "+s"(a.k), "+s"(a.v), "+s"(a.kc), "+s"(a.vc), "+s"(a.pos), "+s"(a.out),
+                 "+s"(a.rope), "+s"(a.part), "+s"(a.count), "+s"(a.nh), "+s"(a.nkv), "+s"(a.smax),
+                 "+s"(a.n_chunks), "+s"(a.neox), "+s"(a.groups_per_kv), "+s"(a.n_groups), "+s"(a.inv_sqrt));
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int grp, chunk;
@@ -185,28 +192,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
     const int s0 = chunk * kChunk;
     const long long row_stride = (long long)a.nkv * HD;        // halves between positions
 
-    // 1. The position (a scalar load), then the loads that depend on it or
-    // on nothing: this position's RoPE table entries and the new token's q
-    // pair, k pair and v element of this thread (one each: nhg * hd/2 <= 256
-    // query pairs), then the chunk's K and V rows.  A wave's vector loads
-    // complete in issue order, so the RoPE inputs arrive before the cache
-    // rows and the rotations overlap the cache reads.  The small loads are
-    // unconditional, at clamped in-range addresses (values a thread does not
-    // use are ignored), so no branch makes the compiler wait for them early.
-    const int pos = *gptr(a.pos);
-    const int pos_c = min(max(pos, 0), a.smax - 1);           // address only; checked below
-    const int qi = tid / HALF, qk = tid - qi * HALF;          // query head of the group, pair
-    int q0, q1;
-    pair_index(qk, HD, a.neox != 0, q0, q1);
-    const TER_GLOBAL float* tab = gptr(a.rope) + (long long)pos_c * HD;  // [hd/2][2] of this position
-    const float rc = tab[2 * qk], rsn = tab[2 * qk + 1];
-    const TER_GLOBAL uint16_t* qh = gptr(a.q) + (long long)min(h0 + qi, a.nh - 1) * HD;
-    uint16_t qx0 = qh[q0], qx1 = qh[q1];
-    const TER_GLOBAL uint16_t* kh = gptr(a.k) + (long long)g * HD;  // pair qk of the KV head's key
-    uint16_t kx0 = kh[q0], kx1 = kh[q1];
-    const uint16_t vx = gptr(a.v)[(long long)g * HD + min(tid, HD - 1)];
-    // cache rows through buffer resources sized to the cache: rows past smax
-    // read as zeros, and no load sits behind a branch
+    // 1. The chunk's K and V rows first (they do not depend on the position;
+    // rows past smax are out of the buffers' range and read as zeros), with
+    // the position as a scalar load beside them; then this position's RoPE
+    // table entries and the new token's q pair, k pair and v element of this
+    // thread (one each: nhg * hd/2 <= 256 query pairs).  These small loads
+    // are unconditional, at clamped in-range addresses (values a thread does
+    // not use are ignored), so no branch makes the compiler wait for them
+    // early; they return right behind the cache rows.
     constexpr int kLoads = kChunk * VROW / 16 / kAttnThreads;  // 16-byte loads per thread per matrix
     const int cache_bytes = a.smax * (int)row_stride * 2;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(a.kc, 0, cache_bytes, 0x00020000);
@@ -220,6 +213,22 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a) {
         kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0);
         vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0);
     }
+    asm volatile("" ::: "memory");  // keeps the row loads ahead of the branch on the position
+    // the position through the scalar cache (invalidated at every launch;
+    // nothing in this launch writes it), so waiting for it waits for no
+    // vector load
+    const int pos = *(const __attribute__((address_space(4))) int32_t*)(size_t)a.pos;
+    const int pos_c = min(max(pos, 0), a.smax - 1);           // address only; checked below
+    const int qi = tid / HALF, qk = tid - qi * HALF;          // query head of the group, pair
+    int q0, q1;
+    pair_index(qk, HD, a.neox != 0, q0, q1);
+    const TER_GLOBAL float* tab = gptr(a.rope) + (long long)pos_c * HD;  // [hd/2][2] of this position
+    const float rc = tab[2 * qk], rsn = tab[2 * qk + 1];
+    const TER_GLOBAL uint16_t* qh = gptr(a.q) + (long long)min(h0 + qi, a.nh - 1) * HD;
+    uint16_t qx0 = qh[q0], qx1 = qh[q1];
+    const TER_GLOBAL uint16_t* kh = gptr(a.k) + (long long)g * HD;  // pair qk of the KV head's key
+    uint16_t kx0 = kh[q0], kx1 = kh[q1];
+    const uint16_t vx = gptr(a.v)[(long long)g * HD + min(tid, HD - 1)];
     if (pos < 0 || pos >= a.smax) return;                     // (the whole grid: no output, no count)
     const int seq = pos + 1;
     const int n = max(0, min(kChunk, seq - s0));              // positions in this chunk
