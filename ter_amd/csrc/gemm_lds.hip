@@ -64,6 +64,11 @@ struct LCfg {
     static constexpr int NI = XI + BS;                // load runs per stage, run q issued by wave q % 8
     static constexpr int NIW = NI / kLWaves;          // runs of waves >= NR ...
     static constexpr int NR = NI % kLWaves;           // ... and waves < NR issue one more
+    // Weight tiles transposed by 16-byte chunks in LDS: conflict-free operand
+    // reads, but each quarter-wave's load spans four 256-byte runs instead of
+    // one.  Measured on the BitNet-2B sweep: 2.8% faster at M = 128 (8 row
+    // blocks, bound by LDS reads), 2.7% slower at M = 16 (bound by the loads).
+    static constexpr bool TW = MBW >= 4;
     static_assert(NST >= 2 && NST <= 4, "stage count");
 };
 
@@ -133,9 +138,13 @@ __device__ __forceinline__ void issue_stage(int ldx, int Ku, int u, unsigned cha
             __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (TER_LDS void*)(stage + q * 1024), 16,
                                                      row * ldx + u * kUnitK + chunk * 16, 0, 0, 0);
         } else {
-            const int t = q - C::XI;  // tile (strip t of the block, unit u)
+            // tile (strip t of the block, unit u); with C::TW its 16-byte chunk
+            // (column quad cq, row group rq) at tile offset cq * 256 + rq * 16
+            // lands at LDS chunk 4 rq + cq (see compute_stage)
+            const int t = q - C::XI;
+            const int src = C::TW ? (lane & 3) * 256 + (lane >> 2) * 16 : lane * 16;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (TER_LDS void*)(stage + C::XB + t * 1024), 16,
-                                                     (t * Ku + u) * kTileBytes + lane * 16, 0, 0, 2 /* nt */);
+                                                     (t * Ku + u) * kTileBytes + src, 0, 0, 2 /* nt */);
         }
     }
 }
@@ -162,8 +171,12 @@ __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg
         }
 #pragma unroll
         for (int s = 0; s < C::S; ++s) {
-            const unsigned dw = *reinterpret_cast<const unsigned*>(
-                stage + C::XB + (sg * C::S + s) * kTileBytes + (j >> 2) * 256 + g * 16 + (j & 3) * 4 + ks * 64);
+            // column j, rows (4 ks + g) * 16 .. +15: tile offset (j >> 2) * 256 +
+            // (4 ks + g) * 16 + (j & 3) * 4.  With C::TW the load placed it at
+            // ks * 256 + lane * 4: the 64 lanes read 256 contiguous bytes, where
+            // in tile order four lanes share each bank.
+            const int off = C::TW ? ks * 256 + lane * 4 : (j >> 2) * 256 + (4 * ks + g) * 16 + (j & 3) * 4;
+            const unsigned dw = *reinterpret_cast<const unsigned*>(stage + C::XB + (sg * C::S + s) * kTileBytes + off);
             const i32x4 B = unpack_signed(dw);
 #pragma unroll
             for (int mb = 0; mb < C::MBW; ++mb)
