@@ -219,19 +219,25 @@ __global__ __launch_bounds__(kThreads) void gemm_t16_kernel(GemmDesc single, con
         for (int i = 0; i < MB; ++i)
             if (sch == 0) rsum[srow + 16 * i] = rs[i];
         __syncthreads();
+        // The output fields through an opaque copy: with one GEMM they are
+        // loop-invariant, and the compiler would otherwise hoist every row's
+        // output addresses and checks out of the block loop into registers.
+        GemmDesc o_d = d;
+        asm volatile("" : "+s"(o_d.N), "+s"(o_d.M), "+s"(o_d.y), "+s"(o_d.acc), "+s"(o_d.y16), "+s"(o_d.resid),
+                     "+s"(o_d.xs), "+s"(o_d.w_scale));
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const int col = (st0 + s) * kStripCols + j;
-            if (s < n_act && col < d.N) {
+            if (s < n_act && col < o_d.N) {
 #pragma unroll
                 for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int row = mb * 16 + g * 4 + e;
-                        if (row < d.M) {
+                        if (row < o_d.M) {
                             const int val = C[s][mb][e] - rsum[row];
-                            const long long o = (long long)row * d.N + col;
-                            emit_out(d, o, val, gptr(d.xs)[row] * d.w_scale);
+                            const long long o = (long long)row * o_d.N + col;
+                            emit_out(o_d, o, val, gptr(o_d.xs)[row] * o_d.w_scale);
                         }
                     }
                 }

@@ -283,8 +283,13 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
         ++it;
         c_stage = c_stage + 1 == C::NST ? 0 : c_stage + 1;
         if (++cu == bc.d.Ku) {
-            // epilogue of block cb
-            const GemmDesc& d = bc.d;
+            // epilogue of block cb.  The output fields through an opaque copy:
+            // with one GEMM they are loop-invariant, and the compiler would
+            // otherwise hoist every row's output addresses and checks out of
+            // the loop (at 8 row blocks, 136 VGPRs spilled to scratch)
+            GemmDesc d = bc.d;
+            asm volatile("" : "+s"(d.N), "+s"(d.M), "+s"(d.y), "+s"(d.acc), "+s"(d.y16), "+s"(d.resid),
+                         "+s"(d.w_scale));
             const float* xs_l = reinterpret_cast<const float*>(lds + C::XSO + (cb % C::NST) * 1024);
             // For the 8-row-block configuration (M > 64, occupancy already
             // fixed by its accumulators) fp32 / int32 outputs get a loop of
