@@ -404,14 +404,13 @@ def run_batched(args):
     tops = 2 * mac / (ev_plan * 1e-3) / 1e12
     hbm_bound = M <= 64
     # the kernel the library picks: M <= 16 streams when M rows of the widest X
-    # fit 64 KiB of LDS; otherwise M <= 128 takes the LDS-ring kernel
+    # fit 64 KiB of LDS; otherwise the LDS-ring kernel (16-byte aligned X rows:
+    # K here is a multiple of 16), above M = 128 over pieces of 128 rows
     ku = max(-(-K // 256) for _, K, _ in cfg["shapes"])
     if M <= 16 and M * (ku * 256 + 16) + 64 <= 65536:
         kernel = "gemm_stream_kernel"
-    elif M <= 128:
-        kernel = "gemm_lds_kernel"  # 16-byte aligned X rows (K here is a multiple of 16)
     else:
-        kernel = "gemm_t16_kernel"
+        kernel = "gemm_lds_kernel"
     return {
         "metric": f"batched packed-trit GEMM, M={M}, BitNet-2B sweep",
         "value": round(mac / (wall * 1e-3) / 1e9, 1), "unit": "GMAC/s", "n_gpus": 1, "steps": args.steps,

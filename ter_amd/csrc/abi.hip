@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cmath>
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -261,6 +262,22 @@ GemmDesc make_gemm_desc(const ter_hip_wpk_t* w, const int8_t* x, const float* xs
 }
 
 bool gemm_vec_ok(const GemmDesc& d) { return aligned(d.x, 16) && d.ldx % 16 == 0; }
+
+// Rows per piece of the LDS-ring GEMM (8 row blocks).  A GEMM with more rows
+// (prefill) whose X rows are 16-byte aligned is cut into pieces of this many
+// rows over the same weights, so the ring kernel serves it instead of the
+// register-staged kernel (M = 256 on the BitNet-2B sweep: about 2x the
+// M = 128 time, against 11x).
+constexpr int kRingRows = 128;
+
+bool ring_rows_ok(const int8_t* x, int K) { return aligned(x, 16) && K % 16 == 0; }
+
+// The outputs of rows r0.. of an [M][N] output set.
+ter_hip_out_t out_rows(const ter_hip_out_t& o, int r0, int N) {
+    const size_t off = (size_t)r0 * (size_t)N;
+    return ter_hip_out_t{o.y ? o.y + off : nullptr, o.acc ? o.acc + off : nullptr, o.y16 ? o.y16 + off : nullptr,
+                         o.resid ? o.resid + off : nullptr};
+}
 
 // GEMM workgroups: up to kGemmWgPerCu per CU (more weight bytes in flight
 // for the HBM-bound small-M blocks), capped by occupancy and by the block count.
@@ -841,6 +858,22 @@ int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, 
         xq = x->q_out;
         xs = x->scale_out;
     }
+    if (M > kRingRows && ring_rows_ok(xq, w->K)) {
+        // pieces of kRingRows rows, one LDS-ring launch each
+        const int mb = gemm_mb_of(kRingRows), lbs = gemm_lds_strips_per_block(mb);
+        for (int r0 = 0; r0 < M; r0 += kRingRows) {
+            const int m = std::min(kRingRows, M - r0);
+            const GemmDesc d = make_gemm_desc(w, xq + (size_t)r0 * w->K, xs + r0, m, out_rows(*out, r0, w->N), 0,
+                                              kWaves * gemm_strips_per_wave(mb), 0);
+            const int nb = (d.n_strips + lbs - 1) / lbs;
+            int n_wg = 0;
+            rc = pick_lds_wg(nb, mb, &n_wg);
+            if (rc) return rc;
+            const hipError_t e = launch_gemm_lds(d, nullptr, nullptr, nullptr, nb, n_wg, mb, st);
+            if (e != hipSuccess) return hip_fail(e, "gemm launch");
+        }
+        return TER_HIP_OK;
+    }
     const int mb = gemm_mb_of(M);
     const GemmDesc d = make_gemm_desc(w, xq, xs, M, *out, 0, kWaves * gemm_strips_per_wave(mb), 0);
     int n_wg = 0;
@@ -892,25 +925,37 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
         if (it.M > max_m) max_m = it.M;
     }
     if (int rc = check_resid_overlap(resid, inputs)) return rc;
-    const int mb = gemm_mb_of(max_m);  // one row-block count (and block width) per launch
+    // Items with more than kRingRows rows become pieces of kRingRows rows
+    // (one descriptor each) when every X qualifies for the LDS-ring kernel.
+    bool ring_all = true;
+    for (int i = 0; i < n; ++i) ring_all = ring_all && ring_rows_ok(items[i].x, items[i].w->K);
+    const int rows = max_m > kRingRows && ring_all ? kRingRows : TER_HIP_M_MAX;
+    const int mb = gemm_mb_of(std::min(max_m, rows));  // one row-block count (and block width) per launch
     const int per_block = kWaves * gemm_strips_per_wave(mb);
     long long tiles = 0;
     int max_k = 1;
-    std::vector<long long> block_starts((size_t)n), tile_starts((size_t)n);
+    ds.clear();
+    std::vector<long long> block_starts, tile_starts;
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemm_item_t& it = items[i];
         const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid};
-        ds[(size_t)i] = make_gemm_desc(it.w, it.x, it.x_scale_dev, it.M, o, blocks, per_block, tiles);
-        block_starts[(size_t)i] = blocks;
-        tile_starts[(size_t)i] = tiles;
-        blocks += ds[(size_t)i].n_blocks;
-        tiles += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
+        for (int r0 = 0; r0 < it.M; r0 += rows) {
+            const int m = std::min(rows, it.M - r0);
+            const GemmDesc d = make_gemm_desc(it.w, it.x + (size_t)r0 * it.w->K, it.x_scale_dev + r0, m,
+                                              out_rows(o, r0, it.w->N), blocks, per_block, tiles);
+            ds.push_back(d);
+            block_starts.push_back(blocks);
+            tile_starts.push_back(tiles);
+            blocks += d.n_blocks;
+            tiles += (long long)d.n_strips * d.Ku;
+            vec = vec && gemm_vec_ok(d);
+        }
         if (it.w->K > max_k) max_k = it.w->K;
-        vec = vec && gemm_vec_ok(ds[(size_t)i]);
         bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.M * it.w->K +
                  (uint64_t)it.M * it.w->N * out_bytes(o);
         macs += (uint64_t)it.M * (uint64_t)it.w->K * (uint64_t)it.w->N;
     }
+    n = (int)ds.size();
     int n_wg = 0;
     const int slds = gemm_stream_lds_bytes(max_m, max_k);
     const bool stream = max_m <= 16 && slds <= kGemmStreamLdsMax;

@@ -141,6 +141,18 @@ def test_gemm_plan_mixed(cuda):
 
 
 @pytest.mark.parametrize("specs", [
+    [(256, 2560, 640), (200, 512, 48), (130, 1024, 300), (8, 2048, 512)],
+    [(256, 512, 64), (140, 300, 20)],
+], ids=["row_pieces", "bytewise_x"])
+def test_gemm_plan_prefill(cuda, specs):
+    """M above 128: with every X 16-byte aligned (K a multiple of 16) each item
+    is cut into pieces of 128 rows for the LDS-ring kernel (a piece may hold
+    fewer rows); with a byte-wise X in the list the register-staged kernel
+    takes all rows at once."""
+    run_plan(specs, 500, (0,))
+
+
+@pytest.mark.parametrize("specs", [
     [(8, 2560, 640), (3, 300, 20), (16, 2048, 512), (1, 64, 16), (5, 6912, 256), (12, 1000, 100)],
     [(8, 2560, 640), (8, 2560, 2560), (1, 256, 16), (16, 512, 4000), (4, 6912, 2560)],
 ], ids=["bytewise_x", "vector_x"])
