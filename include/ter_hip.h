@@ -233,7 +233,9 @@ void ter_hip_plan_destroy(ter_hip_plan_t* plan);
 /* Y[m][j] = float(acc[m][j]) * (x_scale[m] * w->scale).  x->data is [M][K];
  * for X_F32 each row is quantized by absmax (quant_int8_k steps) into
  * `x->q_out` / `x->scale_out` (both REQUIRED for X_F32, [M][K] / [M]).  For
- * X_I8, x->scale_dev ([M]) is required. */
+ * X_I8, x->scale_dev ([M]) is required.  M up to TER_HIP_M_MAX; above 128
+ * rows, with the int8 rows 16-byte aligned and K % 16 == 0, the rows run in
+ * pieces of 128 (one launch each, on the same stream). */
 int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, float* y,
                  int32_t* acc, void* stream);
 /* ter_hip_gemm with every output form (ter_hip_out_t, [M][N] each). */
@@ -245,7 +247,9 @@ int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M,
  * projection).  X is int8 [M][K] (row stride K) with per-row device scales
  * x_scale_dev[M] (quantize fp32 rows with ter_hip_quant_int8 first).  The
  * plan is launched, queried and destroyed with ter_hip_plan_launch /
- * ter_hip_plan_stats / ter_hip_plan_destroy. */
+ * ter_hip_plan_stats / ter_hip_plan_destroy.  When some item has more than
+ * 128 rows and every x is 16-byte aligned with K % 16 == 0, each item is cut
+ * into pieces of 128 rows (one descriptor each, still one launch). */
 typedef struct ter_hip_gemm_item {
     const ter_hip_wpk_t* w;
     const int8_t*        x;            /* device int8 [M][K]                 */
