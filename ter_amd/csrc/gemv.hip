@@ -41,12 +41,15 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Tiles per batch (two batches per wave in flight): 6 for fp32 activations
-// and for the general prologue, 5 for the other kinds.  Measured with each
-// size everywhere: the int8 C2 sweep 42.6 against 42.9 us and the decode step
-// 1.168 against 1.194 ms per token with 5; the fp32 C3 sweep 90.5 against
-// 92.2 us with 6.
+// and for the general prologue, 5 for int8, 4 for the RMS kinds (the decode
+// step's small lists).  Measured: the int8 C2 sweep 42.6 against 42.9 us and
+// the decode step 1.168 against 1.194 ms per token with 5 rather than 6; the
+// fp32 C3 sweep 90.5 against 92.2 us with 6 rather than 5; the decode step
+// 1.166 against 1.171 ms with 4 rather than 5 for the RMS kinds.
 template <int kKind>
-constexpr int batch_of() { return kKind == TER_HIP_X_F32 || kKind < 0 ? 6 : 5; }
+constexpr int batch_of() {
+    return kKind == TER_HIP_X_F32 || kKind < 0 ? 6 : (kKind >= TER_HIP_X_F32_RMS ? 4 : 5);
+}
 
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
 __device__ __forceinline__ int row_sum16(int v) {
