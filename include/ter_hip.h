@@ -46,6 +46,7 @@ extern "C" {
 #define TER_HIP_ERR_FULL      -9  /* kernel table has no free slot             */
 #define TER_HIP_ERR_CONFLICT -10  /* a plan names one weight twice (shared fix-up slots) */
 #define TER_HIP_ERR_FILE     -11  /* model file: cannot open, bad header, size mismatch, short read */
+#define TER_HIP_ERR_FEWARGS  -12  /* a native slot got fewer arguments than it takes */
 
 /* ---- limits ---- */
 #define TER_HIP_K_MAX      32768  /* activation vector staged in LDS (int8)    */
@@ -65,6 +66,12 @@ extern "C" {
  * (cuda/ter_cuda_forward_bitnet.cu:258-309, launched <<<1,1024>>> at :884).
  * `data` is the fp16 gate [K], `up` the fp16 up projection [K]. */
 #define TER_HIP_X_RELU2_RMS 4
+/* int16 X[K] with a host or device activation scale: the reference host
+ * forward's 9-trit payloads (quantize(x_norm, {1,H}, 9) gives |x| <= 9841,
+ * src/tx/forward.cpp:400, src/numfmt/quantize.cpp:26-38); any int16 value is
+ * exact.  Single GEMVs only (ter_hip_gemv, ter_hip_gemv_out, ter_hip_mm_row);
+ * work lists and batched GEMMs refuse it (TER_HIP_ERR_PAYLOAD). */
+#define TER_HIP_X_I16 5
 
 /*
  * Packed ternary weight (replaces WPK, cuda/ter_cuda_forward_packed.cu:400).
@@ -75,8 +82,11 @@ extern "C" {
  * 16(L%16)+e, e = 4f+b at bits 8b+2f), followed by `N` 64-bit fix-up slots
  * (`fix`, zero at rest) used to combine split column strips.  The whole
  * buffer is `ter_hip_wpk_bytes(K, N)` bytes of device memory owned by the
- * caller.  `scale` is the per-tensor weight scale (Wt.scale; a ternary
- * payload {-m,0,+m} is stored as {-1,0,+1} with m folded into `scale`).
+ * caller.  `scale` is the per-tensor weight scale (Wt.scale).  A ternary
+ * payload {-m,0,+m} is stored as trits {-1,0,+1} with m in `mag` (1 for
+ * plain trits): the kernels keep the trit accumulator acc in int32 and form
+ * the reference's float((int64)(m * acc)) in the epilogue, so the fp32
+ * outputs are mm_row's bit for bit (src/tx/forward.cpp:333-345).
  */
 typedef struct ter_hip_wpk {
     uint8_t*  data;    /* device: tile stream, then fix-up slots            */
@@ -85,17 +95,18 @@ typedef struct ter_hip_wpk {
     int32_t   K, N;
     float     scale;
     int32_t   layout;  /* TER_HIP_LAYOUT_T16                                */
+    int32_t   mag;     /* trit magnitude m >= 1 (ter_hip_wpk_init sets 1)    */
 } ter_hip_wpk_t;
 
 #define TER_HIP_LAYOUT_T16 16
 
 /* Activation operand of one GEMV / GEMM. */
 typedef struct ter_hip_act {
-    const void*  data;       /* device: int8 (X_I8), fp32 (X_F32, X_F32_RMS) or fp16
-                                (X_F16_RMS; the gate for X_RELU2_RMS) [M][K]            */
+    const void*  data;       /* device: int8 (X_I8), int16 (X_I16), fp32 (X_F32, X_F32_RMS)
+                                or fp16 (X_F16_RMS; the gate for X_RELU2_RMS) [M][K]    */
     int32_t      kind;       /* TER_HIP_X_*                                            */
-    float        scale;      /* X_I8: host activation scale, used when scale_dev NULL  */
-    const float* scale_dev;  /* X_I8: device activation scale(s) ([M]), or NULL       */
+    float        scale;      /* X_I8, X_I16: host activation scale, used when scale_dev NULL */
+    const float* scale_dev;  /* X_I8, X_I16: device activation scale(s) ([M]), or NULL */
     int8_t*      q_out;      /* X_F32: optional device copy of the quantized X [M][K]  */
     float*       scale_out;  /* X_F32: optional device act scale(s) 1/scale ([M])     */
     const uint16_t* gamma;   /* RMS kinds: device fp16 RMSNorm weights [K]             */
@@ -155,9 +166,9 @@ int ter_hip_pack_i2s(ter_hip_wpk_t* w, const uint8_t* i2s_dev, void* stream);
 
 /* Host pack of a TritTensor payload (int32 [K][N] row-major, the orientation
  * mm_row reads, src/tx/forward.cpp:337) into `w` (synchronous upload).  The
- * payload must be ternary {-m, 0, +m} for one m > 0 (or all zero);
- * `w->scale` becomes scale * m.  Returns TER_HIP_ERR_PAYLOAD otherwise.
- * `magnitude_out` (optional) receives m. */
+ * payload must be ternary {-m, 0, +m} for one m > 0 (or all zero; then
+ * m = 1); `w->scale` becomes `scale` and `w->mag` m.  Returns
+ * TER_HIP_ERR_PAYLOAD otherwise.  `magnitude_out` (optional) receives m. */
 int ter_hip_pack_payload(ter_hip_wpk_t* w, const int32_t* payload_host, float scale,
                          int32_t* magnitude_out, void* stream);
 
@@ -187,13 +198,16 @@ int ter_hip_mm_packed_dispatch_f16(const int8_t* X, const float* scale_x_dev,
 
 /* Host-side mm_row contract (src/tx/forward.cpp:299-352): X is the host
  * TritTensor payload (int32 [rows][K]), `row` selects the row; out (host
- * fp32 [N]) = float(acc) * (x_scale * W.scale).  Every X value must fit int8
- * (TER_HIP_ERR_PAYLOAD otherwise -- no CPU fallback).  Synchronous.
- * `x_stage_dev` (K int8) and `y_stage_dev` (N fp32) are caller device
- * buffers used for the transfer. */
+ * fp32 [N]) = float(W.mag * acc) * (x_scale * W.scale), bit for bit the
+ * reference's float(int64 acc) * (Xt.scale * Wt.scale).  A row whose values
+ * fit int8 runs the int8 GEMV; one that fits int16 (the reference forward's
+ * 9-trit activations, |x| <= 9841) runs the int16 GEMV (TER_HIP_X_I16);
+ * anything wider is TER_HIP_ERR_PAYLOAD (no CPU fallback).  Synchronous.
+ * `x_stage_dev` (2*K bytes, 16-byte aligned) and `y_stage_dev` (N fp32) are
+ * caller device buffers used for the transfer. */
 int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale,
                    const ter_hip_wpk_t* W, int32_t N, float* out,
-                   int8_t* x_stage_dev, float* y_stage_dev, void* stream);
+                   void* x_stage_dev, float* y_stage_dev, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Work lists: many independent GEMVs in ONE launch (layer sweeps)          */
@@ -452,21 +466,29 @@ typedef struct {
     uint64_t tvmul;
 } ter_hip_op_counts_t;  /* same fields as ter_k4_op_counts_t */
 
-/* Creates a handle bound to HIP device `device` with the default slot
- * "tk_matmul_b_9t" (src/kernels/registry.cpp:18-20) installed as the native
- * packed GEMV.  Returns NULL on failure. */
+/* Name of the native packed GEMV/GEMM slot.  It is not the reference's
+ * "tk_matmul_b_9t" (src/kernels/registry.cpp:18-20): that name belongs to the
+ * 3-argument Sim kernel (R1 = X, R2 = W, R3 = Y, src/kernels/tk_matmul_b_9t.tasm),
+ * whose calls must keep reaching the Sim (ter_hip_call returns
+ * TER_HIP_ERR_NOTFOUND for it, the router's cue to fall through). */
+#define TER_HIP_SLOT_MATMUL "tk_matmul_t16"
+
+/* Creates a handle bound to HIP device `device` (-1: calls select no device)
+ * with the slot TER_HIP_SLOT_MATMUL installed as the native packed GEMV.
+ * Returns NULL on failure. */
 ter_hip_handle_t* ter_hip_create(int32_t device);
 void ter_hip_destroy(ter_hip_handle_t* h);
 /* Install (or replace) a named native slot.  Names longer than 31 chars are
  * truncated (KernelTable::kNameMax = 32).  TER_HIP_ERR_FULL after 32 slots. */
 int ter_hip_install_native(ter_hip_handle_t* h, const char* name, ter_hip_native_fn fn);
 /* Call a slot by name: -1 null, -2 unknown name, -4 n_args > 7
- * (src/k4/ter_k4.cpp:52-55); otherwise the slot's return value. */
+ * (src/k4/ter_k4.cpp:52-55); otherwise the slot's return value
+ * (TER_HIP_ERR_FEWARGS when a slot gets fewer arguments than it takes). */
 int ter_hip_call(ter_hip_handle_t* h, const char* name, const int64_t* args, size_t n_args);
 void ter_hip_op_counts(const ter_hip_handle_t* h, ter_hip_op_counts_t* out);
 void ter_hip_reset_counters(ter_hip_handle_t* h);
 
-/* Argument convention of the default "tk_matmul_b_9t" native slot:
+/* Argument convention of the TER_HIP_SLOT_MATMUL native slot:
  *   args[0] = (const ter_hip_wpk_t*) W
  *   args[1] = (const ter_hip_act_t*) X
  *   args[2] = (float*)   y   (device, may be 0)

@@ -1,7 +1,7 @@
 """ctypes bindings of libter_hip.so (the C-ABI declared in include/ter_hip.h).
 
-The library is loaded from the package directory (it is built in-tree by
-ter_amd/build.py) unless TER_HIP_LIB names another build of it.  Loading fails loudly when it is missing: there is no
+The library is always the in-tree build, ter_amd/libter_hip.so (built by
+ter_amd/build.py).  Loading fails loudly when it is missing: there is no
 Python or CPU fallback for any entry point.
 """
 from __future__ import annotations
@@ -10,9 +10,7 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-# TER_HIP_LIB may name another build of the same library (e.g. a tuning build);
-# by default the in-tree one is loaded.
-LIB_PATH = os.environ.get("TER_HIP_LIB") or os.path.join(HERE, "libter_hip.so")
+LIB_PATH = os.path.join(HERE, "libter_hip.so")
 
 # status codes (include/ter_hip.h)
 OK = 0
@@ -27,6 +25,7 @@ ERR_ALIGN = -8
 ERR_FULL = -9
 ERR_CONFLICT = -10
 ERR_FILE = -11
+ERR_FEWARGS = -12
 
 K_MAX = 32768
 N_MAX = 1 << 24
@@ -37,6 +36,8 @@ X_F32 = 1
 X_F32_RMS = 2
 X_F16_RMS = 3
 X_RELU2_RMS = 4
+X_I16 = 5
+SLOT_MATMUL = b"tk_matmul_t16"
 LAYOUT_T16 = 16
 ARGMAX_STATE_BYTES = 16512
 ROPE_NORM = 0
@@ -57,6 +58,7 @@ class WPK(C.Structure):
         ("N", C.c_int32),
         ("scale", C.c_float),
         ("layout", C.c_int32),
+        ("mag", C.c_int32),
     ]
 
 

@@ -47,6 +47,7 @@ int check_wpk(const ter_hip_wpk_t* w) {
     if (w->K < 1 || w->K > TER_HIP_K_MAX || w->N < 1 || w->N > TER_HIP_N_MAX)
         return fail(TER_HIP_ERR_SHAPE, "weight shape K=%d N=%d out of range", w->K, w->N);
     if (w->bytes < ter_hip_wpk_bytes(w->K, w->N)) return fail(TER_HIP_ERR_SHAPE, "weight buffer too small");
+    if (w->mag < 1) return fail(TER_HIP_ERR_PAYLOAD, "trit magnitude %d < 1", w->mag);
     return TER_HIP_OK;
 }
 
@@ -56,8 +57,11 @@ bool is_rms(int kind) {
 
 int check_act(const ter_hip_act_t* x, int M) {
     if (!x || !x->data) return fail(TER_HIP_ERR_NULL, "null activation");
-    if (x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_F32 && !is_rms(x->kind))
+    if (x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_F32 && x->kind != TER_HIP_X_I16 && !is_rms(x->kind))
         return fail(TER_HIP_ERR_PAYLOAD, "unknown activation kind %d", x->kind);
+    if (x->kind == TER_HIP_X_I16 && M != 1)
+        return fail(TER_HIP_ERR_PAYLOAD, "int16 activations run as single GEMVs only (M=%d)", M);
+    if (x->kind == TER_HIP_X_I16 && !aligned(x->data, 2)) return fail(TER_HIP_ERR_ALIGN, "int16 X misaligned");
     if ((x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS) && !aligned(x->data, 4))
         return fail(TER_HIP_ERR_ALIGN, "fp32 X misaligned");
     if ((x->kind == TER_HIP_X_F16_RMS || x->kind == TER_HIP_X_RELU2_RMS) && !aligned(x->data, 2))
@@ -91,6 +95,7 @@ unsigned act_bytes(int kind) {
         case TER_HIP_X_F32_RMS: return 6;
         case TER_HIP_X_F16_RMS: return 4;
         case TER_HIP_X_RELU2_RMS: return 6;
+        case TER_HIP_X_I16: return 2;
         default: return 1;
     }
 }
@@ -107,7 +112,7 @@ bool overlaps(const std::pair<uintptr_t, uintptr_t>& a, const std::pair<uintptr_
 // Device byte ranges an activation operand reads (M rows of K elements).
 void act_ranges(const ter_hip_act_t* x, int M, int K, Ranges* out) {
     const size_t n = (size_t)M * (size_t)K;
-    const size_t el = x->kind == TER_HIP_X_I8 ? 1 : (x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS ? 4 : 2);
+    const size_t el = x->kind == TER_HIP_X_I8 ? 1 : (x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS ? 4 : 2);  // I16, fp16: 2
     out->emplace_back((uintptr_t)x->data, (uintptr_t)x->data + n * el);
     if (x->kind == TER_HIP_X_RELU2_RMS && x->up) out->emplace_back((uintptr_t)x->up, (uintptr_t)(x->up + n));
 }
@@ -135,13 +140,14 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip
     GemvDesc d{};
     d.w = w->data;
     d.x = x->data;
-    d.x_scale_dev = x->kind == TER_HIP_X_I8 ? x->scale_dev : nullptr;
+    d.x_scale_dev = x->kind == TER_HIP_X_I8 || x->kind == TER_HIP_X_I16 ? x->scale_dev : nullptr;
     d.y = o.y;
     d.acc = o.acc;
     d.y16 = o.y16;
     d.resid = o.resid;
-    d.xq_out = x->kind != TER_HIP_X_I8 ? x->q_out : nullptr;
-    d.xs_out = x->kind != TER_HIP_X_I8 ? x->scale_out : nullptr;
+    const bool quantized = x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_I16;
+    d.xq_out = quantized ? x->q_out : nullptr;
+    d.xs_out = quantized ? x->scale_out : nullptr;
     d.gamma = is_rms(x->kind) ? x->gamma : nullptr;
     d.up = x->kind == TER_HIP_X_RELU2_RMS ? x->up : nullptr;
     d.eps = x->eps;
@@ -152,6 +158,7 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip
     d.Ku = units_of(w->K);
     d.n_strips = strips_of(w->N);
     d.w_scale = w->scale;
+    d.w_mag = w->mag;
     d.x_scale = x->scale;
     d.x_kind = x->kind;
     d.stage32 = is_rms(x->kind) && gemv_stage32(w->K) ? 1 : 0;
@@ -258,6 +265,7 @@ GemmDesc make_gemm_desc(const ter_hip_wpk_t* w, const int8_t* x, const float* xs
     d.ldx = w->K;
     d.n_blocks = (d.n_strips + per_block - 1) / per_block;
     d.w_scale = w->scale;
+    d.w_mag = w->mag;
     return d;
 }
 
@@ -427,6 +435,27 @@ int pick_lds_wg(long long blocks, int mb, int* n_wg) {
     return TER_HIP_OK;
 }
 
+// Int16-activation GEMV: whole strips per workgroup, two workgroups per CU
+// (one strip each for small N), at most kStripModeMaxStrips strips each.
+int launch_x16(const GemvDesc& d, hipStream_t st) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    const int cus = device_cu_count(dev);
+    if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
+    long long g = std::min<long long>((long long)cus * 2, d.n_strips);
+    const long long min_g = ((long long)d.n_strips + kStripModeMaxStrips - 1) / kStripModeMaxStrips;
+    if (g < min_g) g = min_g;
+    if (g >= 8) g -= g % 8;  // a multiple of 8 keeps neighbouring strips on one XCD
+    if (g < min_g) g += 8;
+    const int per_wg = (int)(((long long)d.n_strips + g - 1) / g);
+    const int lds = gemv_x16_lds_bytes(d.K, per_wg);
+    if (lds > kLdsMax) return fail(TER_HIP_ERR_SHAPE, "int16 GEMV needs %d bytes of LDS", lds);
+    e = launch_gemv_x16(d, (int)g, lds, st);
+    if (e != hipSuccess) return hip_fail(e, "int16 gemv launch");
+    return TER_HIP_OK;
+}
+
 // Device copy of an LDS-ring GEMM plan: descriptors, the block list, and the
 // per-workgroup block ranges, balanced by 256-row units: range g holds the
 // blocks whose first unit lies in [total * g / n_wg, total * (g + 1) / n_wg).
@@ -487,6 +516,7 @@ int ter_hip_wpk_init(ter_hip_wpk_t* w, void* dev_buf, size_t buf_bytes, int32_t 
     w->N = N;
     w->scale = scale;
     w->layout = TER_HIP_LAYOUT_T16;
+    w->mag = 1;
     return TER_HIP_OK;
 }
 
@@ -539,6 +569,7 @@ int ter_hip_pack_payload(ter_hip_wpk_t* w, const int32_t* payload, float scale, 
     for (size_t i = 0; i < n; ++i) {
         const int64_t a = payload[i] < 0 ? -(int64_t)payload[i] : (int64_t)payload[i];
         if (a == 0) continue;
+        if (a > 0x7FFFFFFFLL) return fail(TER_HIP_ERR_PAYLOAD, "payload magnitude %lld does not fit int32", (long long)a);
         if (m == 0) m = a;
         else if (a != m)
             return fail(TER_HIP_ERR_PAYLOAD, "payload not ternary: |%lld| vs |%lld| at %zu", (long long)a,
@@ -575,8 +606,9 @@ int ter_hip_pack_payload(ter_hip_wpk_t* w, const int32_t* payload, float scale, 
     if (e == hipSuccess) e = hipMemsetAsync(w->fix, 0, (size_t)N * sizeof(uint64_t), st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e != hipSuccess) return hip_fail(e, "payload upload");
-    w->scale = scale * (float)(m == 0 ? 1 : m);
-    if (magnitude_out) *magnitude_out = (int32_t)(m == 0 ? 1 : m);
+    w->scale = scale;
+    w->mag = (int32_t)(m == 0 ? 1 : m);
+    if (magnitude_out) *magnitude_out = w->mag;
     return TER_HIP_OK;
 }
 
@@ -599,6 +631,7 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
         if (rc) return rc;
     }
     const GemvDesc d = make_desc(w, x, *out, 0);
+    if (x->kind == TER_HIP_X_I16) return launch_x16(d, static_cast<hipStream_t>(stream));
     const long long total = (long long)d.n_strips * d.Ku;
     int n_wg = 0;
     const int lds = d.stage32 ? gemv_lds_bytes_rms(w->K) : gemv_lds_bytes(w->K);
@@ -633,23 +666,37 @@ int ter_hip_mm_packed_dispatch_f16(const int8_t* X, const float* scale_x_dev, co
 }
 
 int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale, const ter_hip_wpk_t* W, int32_t N,
-                   float* out, int8_t* x_stage_dev, float* y_stage_dev, void* stream) {
+                   float* out, void* x_stage_dev, float* y_stage_dev, void* stream) {
     if (!X || !W || !out || !x_stage_dev || !y_stage_dev) return fail(TER_HIP_ERR_NULL, "null argument");
     if (row < 0) return fail(TER_HIP_ERR_SHAPE, "negative row");
     if (W->K != K || W->N != N) return fail(TER_HIP_ERR_SHAPE, "K/N (%d,%d) do not match W (%d,%d)", K, N, W->K, W->N);
-    std::vector<int8_t> xb((size_t)K);
+    if (!aligned(x_stage_dev, 16)) return fail(TER_HIP_ERR_ALIGN, "x_stage_dev must be 16-byte aligned");
     const int32_t* xr = X + (size_t)row * (size_t)K;
+    int32_t lo = 0, hi = 0;
     for (int k = 0; k < K; ++k) {
-        if (xr[k] < -128 || xr[k] > 127)
-            return fail(TER_HIP_ERR_PAYLOAD, "X[%d]=%d does not fit int8 (no CPU fallback)", k, xr[k]);
-        xb[(size_t)k] = (int8_t)xr[k];
+        lo = std::min(lo, xr[k]);
+        hi = std::max(hi, xr[k]);
+    }
+    if (lo < -32768 || hi > 32767)
+        return fail(TER_HIP_ERR_PAYLOAD, "X values [%d, %d] do not fit int16 (no CPU fallback)", lo, hi);
+    const bool wide = lo < -128 || hi > 127;
+    std::vector<int8_t> xb;
+    std::vector<int16_t> xw;
+    try {
+        if (wide)
+            xw.assign(xr, xr + K);
+        else
+            xb.assign(xr, xr + K);
+    } catch (...) {
+        return fail(TER_HIP_ERR_ALLOC, "host staging allocation");
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
-    hipError_t e = hipMemcpyAsync(x_stage_dev, xb.data(), (size_t)K, hipMemcpyHostToDevice, st);
+    hipError_t e = wide ? hipMemcpyAsync(x_stage_dev, xw.data(), (size_t)K * 2, hipMemcpyHostToDevice, st)
+                        : hipMemcpyAsync(x_stage_dev, xb.data(), (size_t)K, hipMemcpyHostToDevice, st);
     if (e != hipSuccess) return hip_fail(e, "X upload");
     ter_hip_act_t x{};
     x.data = x_stage_dev;
-    x.kind = TER_HIP_X_I8;
+    x.kind = wide ? TER_HIP_X_I16 : TER_HIP_X_I8;
     x.scale = x_scale;
     int rc = ter_hip_gemv(W, &x, y_stage_dev, nullptr, stream);
     if (rc) return rc;
@@ -675,6 +722,8 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         if (rc) return rc;
         rc = check_act(&it.x, 1);
         if (rc) return rc;
+        if (it.x.kind == TER_HIP_X_I16)
+            return fail(TER_HIP_ERR_PAYLOAD, "item %d: int16 activations run as single GEMVs only", i);
         const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid};
         rc = check_out(&o);
         if (rc) return rc;
@@ -1225,7 +1274,7 @@ int ter_hip_synth_i8(int8_t* x_dev, int64_t n, uint64_t seed, int32_t lo, int32_
 // ---- K4-style handle + KernelTable native slot -------------------------
 
 static int native_matmul(ter_hip_handle_t* h, const int64_t* args, size_t n_args) {
-    if (n_args < 6) return fail(TER_HIP_ERR_NARGS, "tk_matmul_b_9t needs 6 args, got %zu", n_args);
+    if (n_args < 6) return fail(TER_HIP_ERR_FEWARGS, TER_HIP_SLOT_MATMUL " takes 6 args, got %zu", n_args);
     const ter_hip_wpk_t* w = reinterpret_cast<const ter_hip_wpk_t*>(static_cast<intptr_t>(args[0]));
     const ter_hip_act_t* x = reinterpret_cast<const ter_hip_act_t*>(static_cast<intptr_t>(args[1]));
     float* y = reinterpret_cast<float*>(static_cast<intptr_t>(args[2]));
@@ -1248,7 +1297,7 @@ ter_hip_handle_t* ter_hip_create(int32_t device) {
     if (!h) return nullptr;
     std::memset(h, 0, sizeof *h);
     h->device = device;
-    if (ter_hip_install_native(h, "tk_matmul_b_9t", native_matmul) != TER_HIP_OK) {
+    if (ter_hip_install_native(h, TER_HIP_SLOT_MATMUL, native_matmul) != TER_HIP_OK) {
         delete h;
         return nullptr;
     }

@@ -61,6 +61,7 @@ struct alignas(16) GemvDesc {
     float w_scale, x_scale;
     int32_t x_kind;
     float eps;                   // RMS kinds
+    int32_t w_mag;               // trit magnitude m of a {-m, 0, +m} payload (1 for plain trits)
 };
 
 // One GEMM (M > 1) of a work list.  Its blocks (4 column strips x all K each)
@@ -78,6 +79,7 @@ struct alignas(16) GemmDesc {
     int32_t K, N, Ku, n_strips;
     int32_t M, ldx, n_blocks;
     float w_scale;
+    int32_t w_mag;               // trit magnitude m of a {-m, 0, +m} payload (1 for plain trits)
 };
 
 // Host launchers (defined in the .hip files).  Work-list launches take the
@@ -94,6 +96,10 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const int32_t* first_dev
 // for the vector prologue (gemv_vec_kind), else -1.
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const int32_t* first_dev,
                        long long total_tiles, int n_wg, int lds_bytes, int vec_kind, hipStream_t st);
+// Single GEMV with int16 activations (gemv_x16.hip): whole strips per
+// workgroup, at most kStripModeMaxStrips of them.
+int gemv_x16_lds_bytes(int K, int strips_per_wg);
+hipError_t launch_gemv_x16(const GemvDesc& d, int n_wg, int lds_bytes, hipStream_t st);
 hipError_t launch_pack_v11(const uint8_t* v11, uint8_t* t16, int K, int N, hipStream_t st);
 hipError_t launch_unpack_v11(const uint8_t* t16, uint8_t* v11, int K, int N, hipStream_t st);
 hipError_t launch_pack_i2s(const uint8_t* raw, uint8_t* t16, int K, int N, hipStream_t st);
@@ -196,14 +202,23 @@ __device__ inline uint16_t float_to_half_bits(float f) {
     return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
-// Output element o of a GEMV / GEMM (GemvDesc or GemmDesc): acc, y =
-// float(acc) * s, y16 = half(y) (the reference's __float2half projection
-// output), resid += float(half(y)) (its add_k_f32 residual step).
+// The reference's accumulator as fp32: mm_row sums X * W in int64 over the
+// payload {-m, 0, +m} and converts once (src/tx/forward.cpp:333-345), so
+// float(acc) there is float(m * acc) here, rounded once from the exact int64
+// product (acc is the trit accumulator, |acc| < 2^31).
+__device__ __forceinline__ float acc_to_float(int val, int mag) {
+    return mag == 1 ? (float)val : (float)((long long)val * (long long)mag);
+}
+
+// Output element o of a GEMV / GEMM (GemvDesc or GemmDesc): acc (the trit
+// accumulator), y = float(m * acc) * s, y16 = half(y) (the reference's
+// __float2half projection output), resid += float(half(y)) (its add_k_f32
+// residual step).
 template <class D>
 __device__ __forceinline__ void emit_out(const D& d, long long o, int val, float s) {
 #pragma clang fp contract(off)
     if (d.acc) gptr(d.acc)[o] = val;
-    const float y = (float)val * s;
+    const float y = acc_to_float(val, d.w_mag) * s;
     if (d.y) gptr(d.y)[o] = y;
     if (d.y16 || d.resid) {
         const uint16_t h = float_to_half_bits(y);

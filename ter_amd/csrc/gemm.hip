@@ -224,7 +224,7 @@ __global__ __launch_bounds__(kThreads) void gemm_t16_kernel(GemmDesc single, con
         // output addresses and checks out of the block loop into registers.
         GemmDesc o_d = d;
         asm volatile("" : "+s"(o_d.N), "+s"(o_d.M), "+s"(o_d.y), "+s"(o_d.acc), "+s"(o_d.y16), "+s"(o_d.resid),
-                     "+s"(o_d.xs), "+s"(o_d.w_scale));
+                     "+s"(o_d.xs), "+s"(o_d.w_scale), "+s"(o_d.w_mag));
 #pragma unroll
         for (int s = 0; s < S; ++s) {
             const int col = (st0 + s) * kStripCols + j;

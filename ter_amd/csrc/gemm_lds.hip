@@ -289,7 +289,7 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
             // the loop (at 8 row blocks, 136 VGPRs spilled to scratch)
             GemmDesc d = bc.d;
             asm volatile("" : "+s"(d.N), "+s"(d.M), "+s"(d.y), "+s"(d.acc), "+s"(d.y16), "+s"(d.resid),
-                         "+s"(d.w_scale));
+                         "+s"(d.w_scale), "+s"(d.w_mag));
             const float* xs_l = reinterpret_cast<const float*>(lds + C::XSO + (cb % C::NST) * 1024);
             // For the 8-row-block configuration (M > 64, occupancy already
             // fixed by its accumulators) fp32 / int32 outputs get a loop of
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
                 }
             };
             if constexpr (C::MBW >= 8) {
-                if (!d.y16 && !d.resid)
+                if (!d.y16 && !d.resid && d.w_mag == 1)
                     epilogue(std::true_type{});
                 else
                     epilogue(std::false_type{});

@@ -844,7 +844,7 @@ struct Fixups {
     uint16_t* y16;
     float* resid;
     unsigned long long* fix;
-    int Ku;
+    int Ku, w_mag;
 };
 
 __device__ __forceinline__ void finish_fixups(const Fixups& f) {
@@ -856,6 +856,7 @@ __device__ __forceinline__ void finish_fixups(const Fixups& f) {
     d.resid = f.resid;
     d.fix = f.fix;
     d.Ku = f.Ku;
+    d.w_mag = f.w_mag;
     if (f.col_last >= 0) part_complete(d, f.col_last, f.o_last + f.w_last, f.s);
     if (f.col_first >= 0) part_complete(d, f.col_first, f.o_first + f.w_first, f.s);
 }
@@ -897,6 +898,7 @@ __device__ __forceinline__ Fixups run_piece(const GemvDesc& d, const int8_t* lds
     f.resid = d.resid;
     f.fix = d.fix;
     f.Ku = d.Ku;
+    f.w_mag = d.w_mag;
     if (p.u != p.u_start) {
         f.w_last = part_word(p.u - p.u_start, reduce_strip(p.a1, p.a4, p.corr));
         if (col_owner(d, p.st)) {

@@ -67,11 +67,15 @@ class PackedTrits:
         self.wpk = L.WPK()
         L.check(L.lib().ter_hip_wpk_init(C.byref(self.wpk), self.buf.data_ptr(), nbytes, self.K, self.N,
                                          float(scale)), "ter_hip_wpk_init")
-        self.magnitude = 1
 
     @property
     def scale(self) -> float:
         return self.wpk.scale
+
+    @property
+    def magnitude(self) -> int:
+        """m of a {-m, 0, +m} payload (1 for plain trits): y = float(m * acc) * scale."""
+        return self.wpk.mag
 
     @property
     def nbytes_packed(self) -> int:
@@ -108,7 +112,6 @@ class PackedTrits:
         m = C.c_int32(0)
         L.check(L.lib().ter_hip_pack_payload(C.byref(w.wpk), p.ctypes.data, float(scale), C.byref(m),
                                              _stream(stream)), "ter_hip_pack_payload")
-        w.magnitude = m.value
         return w
 
     def to_v11(self, stream=None):
@@ -144,8 +147,8 @@ def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=No
         a.eps = float(eps)
         a.q_out = _ptr(q_out)
         a.scale_out = _ptr(scale_out)
-    elif x.dtype == torch.int8:
-        a.kind = L.X_I8
+    elif x.dtype in (torch.int8, torch.int16):
+        a.kind = L.X_I8 if x.dtype == torch.int8 else L.X_I16
         a.scale = float(x_scale) if x_scale is not None else 1.0
         a.scale_dev = _ptr(x_scale_dev)
     elif x.dtype == torch.float32:
@@ -153,7 +156,7 @@ def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=No
         a.q_out = _ptr(q_out)
         a.scale_out = _ptr(scale_out)
     else:
-        raise TypeError(f"activations must be int8 or float32, got {x.dtype}")
+        raise TypeError(f"activations must be int8, int16 or float32, got {x.dtype}")
     return a
 
 
@@ -165,7 +168,7 @@ def _out(y, acc, y16, resid) -> L.Out:
 
 def gemv(W: PackedTrits, x, y=None, acc=None, x_scale: Optional[float] = None, x_scale_dev=None,
          q_out=None, scale_out=None, gamma=None, eps: float = 1e-5, up=None, y16=None, resid=None, stream=None):
-    """M = 1 GEMV.  x: int8 [K] (with x_scale or x_scale_dev) or fp32 [K]
+    """M = 1 GEMV.  x: int8 or int16 [K] (with x_scale or x_scale_dev) or fp32 [K]
     (absmax-quantized in the kernel prologue); with gamma (fp16 [K]), x fp32 or
     fp16 is RMS-normalized first (rmsnorm_quant_*_in_k steps), and with up as
     well, x is the fp16 gate and the prologue is relu2_mul_rmsnorm_quant_k.
@@ -214,11 +217,13 @@ def mm_packed_dispatch_f16(X, scale_x_dev, W: PackedTrits, out, K: int, N: int, 
 
 def mm_row(Xt_payload: np.ndarray, row: int, x_scale: float, W: PackedTrits, K: int, N: int) -> np.ndarray:
     """The mm_row contract (src/tx/forward.cpp:299-352): host TritTensor
-    payload X (int32 [rows][K]) -> host fp32 out[N].  X must fit int8."""
+    payload X (int32 [rows][K]) -> host fp32 out[N], bit for bit the
+    reference's.  Rows that fit int8 run the int8 GEMV, rows that fit int16
+    (the host forward's 9-trit activations) the int16 GEMV."""
     torch = _torch()
     X = np.ascontiguousarray(Xt_payload, dtype=np.int32)
     out = np.empty(N, dtype=np.float32)
-    xs = torch.empty(K, dtype=torch.int8, device=W.buf.device)
+    xs = torch.empty(2 * K, dtype=torch.int8, device=W.buf.device)
     ys = torch.empty(N, dtype=torch.float32, device=W.buf.device)
     L.check(L.lib().ter_hip_mm_row(X.ctypes.data, int(row), int(K), float(x_scale), C.byref(W.wpk), int(N),
                                    out.ctypes.data, xs.data_ptr(), ys.data_ptr(), _stream(None)),
@@ -557,11 +562,11 @@ class Handle:
 
     def matmul(self, W: PackedTrits, x, y=None, acc=None, x_scale=None, x_scale_dev=None, M: int = 1,
                q_out=None, scale_out=None, stream=None) -> int:
-        """Call the default "tk_matmul_b_9t" native slot."""
+        """Call the native packed-GEMV slot (TER_HIP_SLOT_MATMUL)."""
         a = _act(x, x_scale, x_scale_dev, q_out, scale_out)
         self._last_act = a
         args = [C.addressof(W.wpk), C.addressof(a), _ptr(y) or 0, _ptr(acc) or 0, _stream(stream) or 0, int(M)]
-        return self.call("tk_matmul_b_9t", args)
+        return self.call(L.SLOT_MATMUL.decode(), args)
 
     def op_counts(self) -> dict:
         c = L.OpCounts()

@@ -19,6 +19,13 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU")
+    # the tests check the in-tree library and nothing else
+    if os.environ.get("TER_HIP_LIB"):
+        raise pytest.UsageError("TER_HIP_LIB is set: the tests only load ter_amd/libter_hip.so")
+    from ter_amd import _lib
+    want = os.path.join(ROOT, "ter_amd", "libter_hip.so")
+    if os.path.realpath(_lib.LIB_PATH) != os.path.realpath(want):
+        raise pytest.UsageError(f"ter_amd._lib loads {_lib.LIB_PATH}, not the in-tree {want}")
 
 
 @pytest.fixture(scope="session")

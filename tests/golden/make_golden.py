@@ -14,6 +14,10 @@ Fixtures:
   i2s_block.npz       the hand-built i2_s block of tests/test_nt_dequant.cpp:37-61
   mm_row_random.npz   seeded random (X, W, scales) -> reference mm_row outputs, several shapes
   quantizers.npz      reference quantize(..., 9) and quantize_bitnet on seeded floats
+  mm_row_bitnet9.npz  the reference host forward's mm_row calls on BitNet weights: weights
+                      through quantize_bitnet and quantize(..., 9) (src/host/load_gguf.cpp:64-111:
+                      payload {-9841, 0, +9841}), activations through quantize(x, {1, K}, 9)
+                      (src/tx/forward.cpp:400: |x| <= 9841) -> reference mm_row outputs
 
 Run: python tests/golden/make_golden.py
 """
@@ -117,6 +121,35 @@ def quantizers():
     np.savez(os.path.join(HERE, "quantizers.npz"), x=x, q9=q9, s9=s9, qb=qb, sb=sb)
 
 
+# (K, N, seed): BitNet-2B's projection inputs (2560, 6912) and Llama's 2048.
+BITNET9_CASES = [(2560, 64, 31), (6912, 32, 37), (2048, 48, 41)]
+
+
+def mm_row_bitnet9():
+    arrays = {}
+    for i, (K, N, seed) in enumerate(BITNET9_CASES):
+        wf = O.rand_normal_f32(seed, K * N) * np.float32(0.02)
+        bn, sb = O.ref_quantize_bitnet(wf)                  # ternary {-1, 0, +1} and absmean scale
+        tmp = bn.astype(np.float32) * sb                    # the bitnet round trip of tensor_to_trit
+        W, ws = O.ref_quantize(tmp, 9)                      # payload {-9841, 0, +9841}
+        W = W.reshape(K, N)
+        mags = np.unique(np.abs(W[W != 0]))
+        assert mags.size == 1, mags
+        xf = O.rand_normal_f32(seed + 1, K)
+        X, xs = O.ref_quantize(xf, 9)                       # |x| <= 9841
+        out = ref_mm(X.reshape(1, K), float(xs), W, float(ws), 0)
+        arrays[f"c{i}_K"] = np.int32(K)
+        arrays[f"c{i}_N"] = np.int32(N)
+        arrays[f"c{i}_trits"] = np.sign(W).astype(np.int8)
+        arrays[f"c{i}_mag"] = np.int32(mags[0])
+        arrays[f"c{i}_ws"] = np.float32(ws)
+        arrays[f"c{i}_X"] = X.astype(np.int16)
+        arrays[f"c{i}_xs"] = np.float32(xs)
+        arrays[f"c{i}_out"] = out
+    arrays["n_cases"] = np.int32(len(BITNET9_CASES))
+    np.savez_compressed(os.path.join(HERE, "mm_row_bitnet9.npz"), **arrays)
+
+
 def main():
     if not O.ref_available():
         raise SystemExit("oracle/_ref is not built (make -C oracle ref needs the reference tree)")
@@ -125,6 +158,7 @@ def main():
     i2s_block()
     mm_row_random()
     quantizers()
+    mm_row_bitnet9()
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -191,24 +191,50 @@ def test_attention_validation_without_device():
     assert lib.ter_hip_rope(None, fake, 1, fake, None) == L.ERR_NULL
 
 
-def test_mm_row_rejects_non_int8_activations():
-    # The 9-trit host activations (+-9841, src/tx/forward.cpp:400) do not fit
-    # int8: the boundary refuses them instead of computing on the CPU.
+def test_mm_row_rejects_activations_beyond_int16():
+    # The 9-trit host activations (+-9841, src/tx/forward.cpp:400) run on the
+    # int16 GEMV; values that do not fit int16 (10+-trit payloads beyond
+    # 32767) are refused instead of computed on the CPU.  The staging buffer
+    # must be 16-byte aligned.
     import numpy as np
     lib = L.lib()
     w = L.WPK()
     fake = 1 << 20
     K, N = 64, 16
     assert lib.ter_hip_wpk_init(C.byref(w), fake, lib.ter_hip_wpk_bytes(K, N), K, N, 1.0) == L.OK
-    X = np.zeros((1, K), dtype=np.int32)
-    X[0, 5] = 9841
+    X = np.zeros((2, K), dtype=np.int32)
     out = np.zeros(N, dtype=np.float32)
-    rc = lib.ter_hip_mm_row(X.ctypes.data, 0, K, 1.0, C.byref(w), N, out.ctypes.data, fake, fake, None)
-    assert rc == L.ERR_PAYLOAD
-    assert b"int8" in lib.ter_hip_last_error()
-    X[0, 5] = -129
-    rc = lib.ter_hip_mm_row(X.ctypes.data, 0, K, 1.0, C.byref(w), N, out.ctypes.data, fake, fake, None)
-    assert rc == L.ERR_PAYLOAD
+    for bad in (32768, -32769, 88573):
+        X[1, 5] = bad
+        rc = lib.ter_hip_mm_row(X.ctypes.data, 1, K, 1.0, C.byref(w), N, out.ctypes.data, fake, fake, None)
+        assert rc == L.ERR_PAYLOAD
+        assert b"int16" in lib.ter_hip_last_error()
+    X[1, 5] = 9841
+    rc = lib.ter_hip_mm_row(X.ctypes.data, 1, K, 1.0, C.byref(w), N, out.ctypes.data, fake + 8, fake, None)
+    assert rc == L.ERR_ALIGN
+
+
+def test_int16_activations_are_single_gemv_only():
+    lib = L.lib()
+    w = L.WPK()
+    fake = 1 << 20
+    assert lib.ter_hip_wpk_init(C.byref(w), fake, lib.ter_hip_wpk_bytes(64, 16), 64, 16, 1.0) == L.OK
+    a = L.Act()
+    a.data = fake
+    a.kind = L.X_I16
+    a.scale_dev = fake
+    assert lib.ter_hip_gemm(C.byref(w), C.byref(a), 4, fake, None, None) == L.ERR_PAYLOAD
+    items = (L.GemvItem * 1)()
+    items[0].w = C.pointer(w)
+    items[0].x = a
+    items[0].y = fake
+    h = C.c_void_p()
+    assert lib.ter_hip_plan_create(C.byref(h), items, 1, 0) == L.ERR_PAYLOAD
+    a.data = fake + 1
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(a), fake, None, None) == L.ERR_ALIGN
+    w.mag = 0
+    a.data = fake
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(a), fake, None, None) == L.ERR_PAYLOAD
 
 
 def test_pack_payload_rejects_non_ternary_and_blocked():
@@ -283,14 +309,19 @@ def test_kernel_table_slots_and_codes():
     assert h
     try:
         args = (C.c_int64 * 8)(*range(8))
-        assert lib.ter_hip_call(None, b"tk_matmul_b_9t", args, 1) == L.ERR_NULL
+        assert lib.ter_hip_call(None, L.SLOT_MATMUL, args, 1) == L.ERR_NULL
         assert lib.ter_hip_call(h, None, args, 1) == L.ERR_NULL
         assert lib.ter_hip_call(h, b"no_such_kernel", args, 1) == L.ERR_NOTFOUND
-        assert lib.ter_hip_call(h, b"tk_matmul_b_9t", args, 8) == L.ERR_NARGS
-        # the default matmul slot validates its own arguments
+        assert lib.ter_hip_call(h, L.SLOT_MATMUL, args, 8) == L.ERR_NARGS
+        # the reference's own matmul name is the Sim's 3-argument kernel
+        # (r1 = X, r2 = W, r3 = Y: src/kernels/tk_matmul_b_9t.tasm): the
+        # native table does not claim it, so a router falls through to the Sim
+        sim_args = (C.c_int64 * 3)(100, 200, 300)
+        assert lib.ter_hip_call(h, b"tk_matmul_b_9t", sim_args, 3) == L.ERR_NOTFOUND
+        # the native matmul slot validates its own arguments
         zero = (C.c_int64 * 6)(0, 0, 0, 0, 0, 1)
-        assert lib.ter_hip_call(h, b"tk_matmul_b_9t", zero, 6) == L.ERR_NULL   # null W
-        assert lib.ter_hip_call(h, b"tk_matmul_b_9t", zero, 5) == L.ERR_NARGS  # too few
+        assert lib.ter_hip_call(h, L.SLOT_MATMUL, zero, 6) == L.ERR_NULL     # null W
+        assert lib.ter_hip_call(h, L.SLOT_MATMUL, zero, 5) == L.ERR_FEWARGS  # too few
         seen = []
 
         def native(hh, a, n):
@@ -301,7 +332,7 @@ def test_kernel_table_slots_and_codes():
         assert lib.ter_hip_install_native(h, b"tk_custom", cb) == L.OK
         assert lib.ter_hip_call(h, b"tk_custom", args, 7) == 42
         assert seen == [list(range(7))]
-        # 32 slots: 2 used (tk_matmul_b_9t, tk_custom) -> 30 more fit, then full
+        # 32 slots: 2 used (the matmul slot, tk_custom) -> 30 more fit, then full
         for i in range(30):
             assert lib.ter_hip_install_native(h, b"slot%02d" % i, cb) == L.OK
         assert lib.ter_hip_install_native(h, b"one_too_many", cb) == L.ERR_FULL
@@ -328,3 +359,24 @@ def test_kernel_table_name_truncation():
         assert lib.ter_hip_call(h, b"k" * 30, args, 0) == L.ERR_NOTFOUND
     finally:
         lib.ter_hip_destroy(h)
+
+
+def test_c99_caller_routes_reference_calls_to_the_sim(tmp_path):
+    """A strict C99 translation unit compiles against include/ter_hip.h,
+    links libter_hip.so and implements the ter_k4_call routing: the
+    reference's 3-argument tk_matmul_b_9t call reaches the Sim (stub)."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not installed")
+    L.lib()  # the library is built
+    exe = str(tmp_path / "k4_router")
+    libdir = os.path.dirname(L.LIB_PATH)
+    cmd = [gcc, "-std=c99", "-Wall", "-Wextra", "-Werror", "-pedantic", "-I", os.path.join(ROOT, "include"),
+           os.path.join(ROOT, "tests", "c", "k4_router.c"), "-L", libdir, "-lter_hip", f"-Wl,-rpath,{libdir}",
+           "-o", exe]
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    assert r.returncode == 0, r.stdout
+    r = subprocess.run([exe], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True, timeout=60)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stdout

@@ -109,20 +109,101 @@ def test_gemv_reference_fixtures(cuda, golden):
         assert int(host(acc)[0]) == int(m[xk].astype(np.int64) @ w[:, 0])
 
 
-def test_gemv_payload_magnitude_folded(cuda):
-    """A ternary payload {-m,0,+m} (e.g. 9-trit quantized BitNet weights,
-    src/host/load_gguf.cpp:111) is packed as {-1,0,+1} with m in the scale."""
+@pytest.mark.parametrize("K,N,m", [(100, 12, 9841), (2560, 640, 9841), (6912, 80, 9841), (2048, 48, 3)])
+def test_gemv_payload_magnitude(cuda, K, N, m):
+    """A ternary payload {-m,0,+m} (9-trit quantized BitNet weights,
+    src/host/load_gguf.cpp:111) is packed as {-1,0,+1} with m kept as an
+    integer: y = float(int64(m * acc)) * fl(xs * ws), bit for bit the
+    reference mm_row (src/tx/forward.cpp:333-345), also where m * acc is
+    beyond 2^24; every output form (fp32, fp16, residual) uses it."""
     import torch
     import ter_amd as T
-    K, N = 100, 12
-    w = O.rand_trits(3, K, N).astype(np.int32) * 9841
-    x = O.rand_int8(4, K)
-    W = T.PackedTrits.from_payload(w, 0.001)
-    assert W.magnitude == 9841
+    w = O.rand_trits(3 + K, K, N, 0.4).astype(np.int32) * m
+    x = O.rand_int8(4 + K, K)
+    xs, ws = 0.0173, 0.00071
+    W = T.PackedTrits.from_payload(w, ws)
+    assert W.magnitude == m and W.scale == np.float32(ws)
     acc = torch.empty(N, dtype=torch.int32, device="cuda")
-    T.gemv(W, dev(x), acc=acc, x_scale=1.0)
-    ref_acc, _ = O.mm_row(x.astype(np.int32)[None], 0, 1.0, w, 1.0)
-    assert (host(acc).astype(np.int64) * 9841 == ref_acc).all()
+    y = torch.empty(N, dtype=torch.float32, device="cuda")
+    T.gemv(W, dev(x), y=y, acc=acc, x_scale=xs)
+    ref_acc, ref_y = O.mm_row(x.astype(np.int32)[None], 0, xs, w, ws)
+    assert (host(acc).astype(np.int64) * m == ref_acc).all()
+    assert_f32_equal(host(y), ref_y)
+    if K >= 2048 and m > 1000:
+        assert np.abs(ref_acc).max() > 2 ** 24
+    # the fp16 and residual epilogues take the same y
+    y16 = torch.empty(N, dtype=torch.float16, device="cuda")
+    resid = dev(O.rand_normal_f32(5 + K, N))
+    r0 = host(resid).copy()
+    T.gemv(W, dev(x), y16=y16, resid=resid, x_scale=xs)
+    assert (host(y16).view(np.uint16) == O.float_to_half_bits(ref_y)).all()
+    assert (host(resid).view(np.int32) == O.residual_add_f16(r0, ref_y).view(np.int32)).all()
+
+
+def test_mm_row_bitnet9_golden(cuda, golden):
+    """The reference host forward's own mm_row calls on BitNet weights
+    (tests/golden/mm_row_bitnet9.npz, written by the reference build):
+    payload {-9841, 0, +9841} and 9-trit activations (|x| <= 9841, the
+    int16 GEMV) -- the fp32 outputs bit for bit."""
+    import ter_amd as T
+    g = golden("mm_row_bitnet9.npz")
+    for i in range(int(g["n_cases"])):
+        K, N = int(g[f"c{i}_K"]), int(g[f"c{i}_N"])
+        m = int(g[f"c{i}_mag"])
+        W = T.PackedTrits.from_payload(g[f"c{i}_trits"].astype(np.int32) * m, float(g[f"c{i}_ws"]))
+        X = g[f"c{i}_X"].astype(np.int32)
+        out = T.mm_row(np.stack([np.zeros(K, np.int32), X]), 1, float(g[f"c{i}_xs"]), W, K, N)
+        assert_f32_equal(out, g[f"c{i}_out"])
+
+
+def int16_case(K, N, seed, x, p0=1 / 3, xs=0.00013, ws=0.05, x_scale_dev=False):
+    import torch
+    import ter_amd as T
+    w = O.rand_trits(seed, K, N, p0).astype(np.int32)
+    W = T.PackedTrits.from_payload(w, ws)
+    acc = torch.empty(N, dtype=torch.int32, device="cuda")
+    y = torch.empty(N, dtype=torch.float32, device="cuda")
+    if x_scale_dev:
+        T.gemv(W, dev(x.astype(np.int16)), y=y, acc=acc, x_scale_dev=dev(np.array([xs], np.float32)))
+    else:
+        T.gemv(W, dev(x.astype(np.int16)), y=y, acc=acc, x_scale=xs)
+    ra, ry = O.mm_row(x.astype(np.int32)[None], 0, xs, w, ws)
+    assert (host(acc).astype(np.int64) == ra).all(), f"int16 acc mismatch K={K} N={N}"
+    assert_f32_equal(host(y), ry)
+
+
+@pytest.mark.parametrize("K,N", [(2560, 2560), (2560, 640), (6912, 2560), (2048, 8192), (1, 4), (17, 33),
+                                 (300, 20), (4112, 100), (32768, 48)])
+def test_gemv_int16_activations(cuda, K, N):
+    """int16 X (the host forward's 9-trit payloads, and the whole int16
+    range) on the int16 GEMV: exact accumulators and fp32 outputs."""
+    x = O.splitmix64(K * 31 + N, K)
+    x9 = (x % np.uint64(2 * 9841 + 1)).astype(np.int64) - 9841
+    int16_case(K, N, K + N, x9)
+    full = (x % np.uint64(65536)).astype(np.int64) - 32768
+    int16_case(K, N, K + N + 1, full, x_scale_dev=True)
+
+
+def test_gemv_int16_extremes(cuda):
+    """All -32768, all 32767 (the accumulator's largest magnitudes at
+    K = 32768: 2^30), alternating, and a misaligned (odd-element) vector."""
+    import torch
+    import ter_amd as T
+    K, N = 32768, 20
+    for fill in (-32768, 32767):
+        int16_case(K, N, 5, np.full(K, fill), p0=0.0)
+    alt = np.where(np.arange(K) % 2 == 0, 32767, -32768)
+    int16_case(K, N, 6, alt)
+    # one element off 16-byte alignment: the element-wise staging path
+    K2 = 1000
+    x = ((O.splitmix64(7, K2 + 1) % np.uint64(65536)).astype(np.int64) - 32768).astype(np.int16)
+    w = O.rand_trits(8, K2, N).astype(np.int32)
+    W = T.PackedTrits.from_payload(w, 0.5)
+    buf = dev(x)
+    acc = torch.empty(N, dtype=torch.int32, device="cuda")
+    T.gemv(W, buf[1:], acc=acc, x_scale=1.0)
+    ra, _ = O.mm_row(x[1:].astype(np.int32)[None], 0, 1.0, w, 1.0)
+    assert (host(acc).astype(np.int64) == ra).all()
 
 
 def test_gemv_fp32_prologue(cuda):

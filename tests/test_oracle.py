@@ -93,6 +93,31 @@ def test_mm_row_golden_random(golden):
             assert (acc2 == acc).all() and (out2.view(np.int32) == out.view(np.int32)).all()
 
 
+def test_mm_row_bitnet9_golden(golden):
+    """The host forward's mm_row calls on BitNet weights (payload {-9841, 0,
+    +9841}, 9-trit activations), written by the reference build: the
+    restatement reproduces them bit for bit, and they equal the closed form
+    float(int64 sum) * fl(xs * ws) with the accumulator beyond 2^24."""
+    g = golden("mm_row_bitnet9.npz")
+    for i in range(int(g["n_cases"])):
+        t = g[f"c{i}_trits"].astype(np.int64)
+        m = int(g[f"c{i}_mag"])
+        assert m == 9841
+        X = g[f"c{i}_X"].astype(np.int64)
+        assert np.abs(X).max() == 9841
+        xs, ws = g[f"c{i}_xs"], g[f"c{i}_ws"]
+        acc, out = O.mm_row(X[None].astype(np.int32), 0, float(xs), (t * m).astype(np.int32), float(ws))
+        assert (out.view(np.int32) == g[f"c{i}_out"].view(np.int32)).all(), i
+        want_acc = (X @ t) * m
+        assert (acc == want_acc).all()
+        assert np.abs(want_acc).max() > 2 ** 24  # float(acc) rounds: the int64 -> fp32 step matters
+        closed = want_acc.astype(np.float32) * np.float32(np.float32(xs) * np.float32(ws))
+        assert (closed.view(np.int32) == g[f"c{i}_out"].view(np.int32)).all(), i
+        # folding m into the scale instead is a different function
+        folded = (X @ t).astype(np.float32) * np.float32(np.float32(xs) * np.float32(np.float32(ws) * np.float32(m)))
+        assert (folded.view(np.int32) != g[f"c{i}_out"].view(np.int32)).any()
+
+
 def test_mm_row_zero_skip_and_signs():
     # X == 0 rows contribute nothing; negating X negates acc; W = 0 -> 0.
     K, N = 64, 8
