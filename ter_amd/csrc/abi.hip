@@ -874,8 +874,10 @@ int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, floa
     return ter_hip_gemm_out(w, x, M, &o, stream);
 }
 
-int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, const ter_hip_out_t* out,
-                     void* stream) {
+// ter_hip_gemm_out with the quantized rows of fp32 / fp16 activations in
+// q_ws [M][K] and s_ws [M] (unused for int8 X).
+static int gemm_out_ws(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, const ter_hip_out_t* out,
+                       int8_t* q_ws, float* s_ws, void* stream) {
     int rc = check_wpk(w);
     if (rc) return rc;
     if (M < 1 || M > TER_HIP_M_MAX) return fail(TER_HIP_ERR_SHAPE, "M=%d out of range [1,%d]", M, TER_HIP_M_MAX);
@@ -887,25 +889,25 @@ int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, 
     const int8_t* xq = static_cast<const int8_t*>(x->data);
     const float* xs = x->scale_dev;
     if (out->resid) {  // the GEMM reads int8 rows: X itself or the q_out workspace
-        const int8_t* xr = x->kind == TER_HIP_X_I8 ? xq : x->q_out;
+        const int8_t* xr = x->kind == TER_HIP_X_I8 ? xq : q_ws;
         const size_t mk = (size_t)M * (size_t)w->K;
         rc = check_resid_overlap({{(uintptr_t)out->resid, (uintptr_t)(out->resid + (size_t)M * w->N)}},
                                  {{(uintptr_t)xr, (uintptr_t)(xr + mk)}});
         if (rc) return rc;
     }
     if (x->kind != TER_HIP_X_I8) {
-        if (!x->q_out || !x->scale_out)
+        if (!q_ws || !s_ws)
             return fail(TER_HIP_ERR_NULL, "fp32/fp16 batched X needs q_out and scale_out workspaces");
         if (x->kind == TER_HIP_X_F32)
-            rc = ter_hip_quant_int8(static_cast<const float*>(x->data), M, w->K, x->q_out, x->scale_out, stream);
+            rc = ter_hip_quant_int8(static_cast<const float*>(x->data), M, w->K, q_ws, s_ws, stream);
         else if (x->kind == TER_HIP_X_RELU2_RMS)
             rc = ter_hip_relu2_rmsnorm_quant(static_cast<const uint16_t*>(x->data), x->up, x->gamma, x->eps, M, w->K,
-                                             x->q_out, x->scale_out, stream);
+                                             q_ws, s_ws, stream);
         else
-            rc = ter_hip_rmsnorm_quant(x->data, x->kind, x->gamma, x->eps, M, w->K, x->q_out, x->scale_out, stream);
+            rc = ter_hip_rmsnorm_quant(x->data, x->kind, x->gamma, x->eps, M, w->K, q_ws, s_ws, stream);
         if (rc) return rc;
-        xq = x->q_out;
-        xs = x->scale_out;
+        xq = q_ws;
+        xs = s_ws;
     }
     if (M > kRingRows && ring_rows_ok(xq, w->K)) {
         // pieces of kRingRows rows, one LDS-ring launch each
@@ -946,6 +948,12 @@ int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, 
     }
     if (e != hipSuccess) return hip_fail(e, "gemm launch");
     return TER_HIP_OK;
+}
+
+int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, const ter_hip_out_t* out,
+                     void* stream) {
+    if (!x) return fail(TER_HIP_ERR_NULL, "null activation");
+    return gemm_out_ws(w, x, M, out, x->q_out, x->scale_out, stream);
 }
 
 int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* items, int32_t n,
