@@ -216,6 +216,12 @@ def lib():
             raise RuntimeError(
                 f"{LIB_PATH} is missing: build it with `python -m ter_amd.build` "
                 "(there is no fallback path)")
+        # PyTorch ships its own HIP runtime (torch/lib/libamdhip64.so, soname
+        # libamdhip64.so.7).  Loaded first, it satisfies this library's
+        # libamdhip64.so.7 dependency, so both share one runtime; loaded after
+        # this library, torch would bring in a second runtime beside the
+        # /opt/rocm one, and this library's launches would find no device.
+        import torch  # noqa: F401
         L = C.CDLL(LIB_PATH)
         for name, res, args in SIGNATURES:
             f = getattr(L, name)
