@@ -256,6 +256,21 @@ int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, floa
 int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M,
                      const ter_hip_out_t* out, void* stream);
 
+/* ter_hip_gemm_out that allocates nothing and takes no workspace.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  fp32 / fp16 / RMS activations are quantized into a
+ * static device array of the library (one per GPU, TER_HIP_STATIC_Q_MAX
+ * bytes of rows plus TER_HIP_M_MAX scales, held until the process ends)
+ * instead of x->q_out / x->scale_out, which must be NULL; int8 X uses no
+ * workspace.  M * K above TER_HIP_STATIC_Q_MAX is TER_HIP_ERR_SHAPE.  Every
+ * call on a GPU shares that GPU's array: calls that overlap in time on one
+ * GPU (other streams, other threads) race on it.  Results are
+ * ter_hip_gemm_out's.  No hipMalloc, hipFree or allocating library call. */
+#define TER_HIP_STATIC_Q_MAX (4 << 20)
+int ter_hip_gemm_out_static(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M,
+                            const ter_hip_out_t* out, void* stream);
+
 /* Many independent GEMMs in ONE launch (batched decode / prefill over a
  * layer sweep; replaces one mm_bitnet_addonly_batched_k launch per
  * projection).  X is int8 [M][K] (row stride K) with per-row device scales

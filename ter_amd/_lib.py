@@ -30,6 +30,7 @@ ERR_FEWARGS = -12
 K_MAX = 32768
 N_MAX = 1 << 24
 M_MAX = 256
+STATIC_Q_MAX = 4 << 20
 
 X_I8 = 0
 X_F32 = 1
@@ -165,6 +166,7 @@ SIGNATURES = [
     ("ter_hip_plan_destroy", None, [_P]),
     ("ter_hip_gemm", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, _P, _P, _P]),
     ("ter_hip_gemm_out", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, C.POINTER(Out), _P]),
+    ("ter_hip_gemm_out_static", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, C.POINTER(Out), _P]),
     ("ter_hip_gemm_plan_create", C.c_int, [C.POINTER(C.c_void_p), C.POINTER(GemmItem), C.c_int32, C.c_int32]),
     ("ter_hip_quant_int8", C.c_int, [_P, C.c_int32, C.c_int32, _P, _P, _P]),
     ("ter_hip_pack_i2s", C.c_int, [C.POINTER(WPK), _P, _P]),

@@ -456,6 +456,36 @@ int launch_x16(const GemvDesc& d, hipStream_t st) {
     return TER_HIP_OK;
 }
 
+// Workspace of ter_hip_gemm_out_static: the quantized rows (int8
+// [M][K], at most TER_HIP_STATIC_Q_MAX bytes) followed by their scales
+// (fp32 [M], M <= TER_HIP_M_MAX).  One copy per GPU, held until the process
+// ends; host code reaches it only through the address hipGetSymbolAddress
+// returns for the current device (the array's name is a host-side stand-in).
+constexpr size_t kScratchScaleOff = TER_HIP_STATIC_Q_MAX;
+constexpr size_t kScratchBytes = kScratchScaleOff + TER_HIP_M_MAX * sizeof(float);
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+static std::mutex g_scratch_mu;
+static std::vector<void*> g_scratch_ptr;  // per device; null until looked up on it
+
+// The current device's address of `scratch`, looked up once per device.
+static int scratch_of_current_device(unsigned char** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if ((int)g_scratch_ptr.size() <= dev) g_scratch_ptr.resize((size_t)dev + 1, nullptr);
+    if (!g_scratch_ptr[(size_t)dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(TER_HIP_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[(size_t)dev] = p;
+    }
+    *out = static_cast<unsigned char*>(g_scratch_ptr[(size_t)dev]);
+    return TER_HIP_OK;
+}
+
 // Device copy of an LDS-ring GEMM plan: descriptors, the block list, and the
 // per-workgroup block ranges, balanced by 256-row units: range g holds the
 // blocks whose first unit lies in [total * g / n_wg, total * (g + 1) / n_wg).
@@ -954,6 +984,25 @@ int ter_hip_gemm_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, 
                      void* stream) {
     if (!x) return fail(TER_HIP_ERR_NULL, "null activation");
     return gemm_out_ws(w, x, M, out, x->q_out, x->scale_out, stream);
+}
+
+int ter_hip_gemm_out_static(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, const ter_hip_out_t* out,
+                            void* stream) {
+    int rc = check_wpk(w);
+    if (rc) return rc;
+    if (!x) return fail(TER_HIP_ERR_NULL, "null activation");
+    if (x->q_out || x->scale_out)
+        return fail(TER_HIP_ERR_SHAPE, "ter_hip_gemm_out_static takes no q_out / scale_out (its workspace is static)");
+    if (M < 1 || M > TER_HIP_M_MAX) return fail(TER_HIP_ERR_SHAPE, "M=%d out of range [1,%d]", M, TER_HIP_M_MAX);
+    if ((long long)M * w->K > (long long)TER_HIP_STATIC_Q_MAX)
+        return fail(TER_HIP_ERR_SHAPE, "M*K = %lld exceeds the static workspace (%d bytes)", (long long)M * w->K,
+                    TER_HIP_STATIC_Q_MAX);
+    if (x->kind == TER_HIP_X_I8) return gemm_out_ws(w, x, M, out, nullptr, nullptr, stream);  // no workspace used
+    unsigned char* ws = nullptr;
+    rc = scratch_of_current_device(&ws);
+    if (rc) return rc;
+    return gemm_out_ws(w, x, M, out, reinterpret_cast<int8_t*>(ws), reinterpret_cast<float*>(ws + kScratchScaleOff),
+                       stream);
 }
 
 int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* items, int32_t n,
