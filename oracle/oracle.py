@@ -93,6 +93,14 @@ def lib():
         L.orc_dequant_i2s.restype = None
         L.orc_i2s_to_v11.argtypes = [_P, C.c_int, C.c_int, _P]
         L.orc_i2s_to_v11.restype = C.c_int
+        L.orc_gemv_i8w.argtypes = [_P, C.c_float, _P, C.c_float, C.c_int, C.c_int, _P, _P]
+        L.orc_gemv_i8w.restype = None
+        L.orc_gemm_i8w.argtypes = [_P, _P, C.c_int, _P, C.c_float, C.c_int, C.c_int, _P, _P]
+        L.orc_gemm_i8w.restype = None
+        L.orc_v11_to_i8.argtypes = [_P, C.c_int, C.c_int, _P]
+        L.orc_v11_to_i8.restype = C.c_int
+        L.orc_rand_trits.argtypes = [C.c_uint64, C.c_int, C.c_int, C.c_uint64, C.c_uint64, _P]
+        L.orc_rand_trits.restype = None
         L.orc_mm_row_tvmac.argtypes = [C.c_int, C.c_int]
         L.orc_mm_row_tvmac.restype = C.c_uint64
         _lib = L
@@ -183,6 +191,55 @@ def gemv_v11(x: np.ndarray, xs: float, v11: np.ndarray, ws: float, K: int, N: in
     out = np.empty(N, dtype=np.float32)
     lib().orc_gemv_v11(_ptr(x), float(xs), _ptr(b), float(ws), K, N, _ptr(acc), _ptr(out))
     return acc, out
+
+
+def gemv_i8w(x: np.ndarray, xs: float, W: np.ndarray, ws: float):
+    """mm_row's int path at int8 width: int8 x[K] times int8 W [K][N] ->
+    (int32 acc[N], fp32 out[N] = float(acc) * (xs * ws))."""
+    x = np.ascontiguousarray(x, dtype=np.int8)
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    K, N = W.shape
+    assert x.size == K
+    acc = np.empty(N, dtype=np.int32)
+    out = np.empty(N, dtype=np.float32)
+    lib().orc_gemv_i8w(_ptr(x), float(xs), _ptr(W), float(ws), K, N, _ptr(acc), _ptr(out))
+    return acc, out
+
+
+def gemm_i8w(X: np.ndarray, xs: np.ndarray, W: np.ndarray, ws: float):
+    """gemv_i8w per row of int8 X [M][K] with per-row scales xs[M]."""
+    X = np.ascontiguousarray(X, dtype=np.int8)
+    xs = np.ascontiguousarray(xs, dtype=np.float32)
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    M, K = X.shape
+    N = W.shape[1]
+    acc = np.empty((M, N), dtype=np.int32)
+    out = np.empty((M, N), dtype=np.float32)
+    lib().orc_gemm_i8w(_ptr(X), _ptr(xs), M, _ptr(W), float(ws), K, N, _ptr(acc), _ptr(out))
+    return acc, out
+
+
+def v11_to_i8(v11: np.ndarray, K: int, N: int) -> np.ndarray:
+    """v11 bytes -> int8 trits [K][N] (v11_unpack at int8 width)."""
+    b = np.ascontiguousarray(v11, dtype=np.uint8)
+    out = np.empty((K, N), dtype=np.int8)
+    assert lib().orc_v11_to_i8(_ptr(b), K, N, _ptr(out)) == 0
+    return out
+
+
+def synth_thresholds(p_zero: float):
+    """(t0, t1) of rand_trits / ter_hip_synth_v11 for P(0) = p_zero."""
+    t0 = int(round(p_zero * 2 ** 32))
+    t1 = t0 + int(round((1.0 - p_zero) / 2.0 * 2 ** 32))
+    return t0, min(t1, 2 ** 32 - 1)
+
+
+def rand_trits_c(seed: int, K: int, N: int, p_zero: float = 1.0 / 3.0) -> np.ndarray:
+    """rand_trits in C (same stream and mapping), for full-size inputs."""
+    t0, t1 = synth_thresholds(p_zero)
+    out = np.empty((K, N), dtype=np.int8)
+    lib().orc_rand_trits(seed & _M64, K, N, t0, t1, _ptr(out))
+    return out
 
 
 def gemm_v11(X: np.ndarray, xs: np.ndarray, v11: np.ndarray, ws: float, K: int, N: int):

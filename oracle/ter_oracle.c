@@ -26,6 +26,11 @@
  *                                           tests/test_kernel_matmul_b_small.cpp.
  *   orc_mm_row_blocked                   -- oracle/_ref.
  *   orc_gemv_v11                         -- equality with orc_mm_row on unpacked W.
+ *   orc_gemv_i8w / orc_gemm_i8w          -- equality with orc_mm_row (int64 accumulators,
+ *                                           fp32 outputs) on random and ragged cases.
+ *   orc_v11_to_i8                        -- equality with orc_v11_unpack.
+ *   orc_rand_trits                       -- (an input generator, not a reference
+ *                                           function) equality with oracle.rand_trits.
  *   orc_quant_int8                       -- closed-form tie / zero / amax cases.
  *   orc_float_to_half                    -- numpy's IEEE binary16 rounding on
  *                                           edge sets and random patterns.
@@ -205,6 +210,91 @@ void orc_gemv_v11(const int8_t* x, float xs, const uint8_t* v11, float ws, int K
             if (acc_out) acc_out[4 * jb + s2] = acc[s2];
             if (out) out[4 * jb + s2] = (float)acc[s2] * s;
         }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* mm_row's integer path (src/tx/forward.cpp:331-346) at int8 width: x int8  */
+/* [K], W int8 [K][N] row-major (the payload orientation), the reference's   */
+/* k-outer / j-inner loop with zero rows of x skipped, int32 accumulators    */
+/* (exact: |acc| <= 128 * K < 2^31); out = float(acc) * (xs * ws).  The j    */
+/* loop vectorizes as the reference's does; threads split the columns       */
+/* (integer sums are exact in any split).  The checker of full-size lists.  */
+/* ------------------------------------------------------------------------ */
+void orc_gemv_i8w(const int8_t* x, float xs, const int8_t* W, float ws, int K, int N, int32_t* acc_out,
+                  float* out) {
+    const float s = xs * ws;
+    enum { CB = 256 };  /* columns per thread chunk */
+    #pragma omp parallel for schedule(static)
+    for (int j0 = 0; j0 < N; j0 += CB) {
+        const int j1 = j0 + CB < N ? j0 + CB : N;
+        int32_t acc[CB];
+        for (int j = j0; j < j1; ++j) acc[j - j0] = 0;
+        for (int k = 0; k < K; ++k) {
+            const int32_t xv = x[k];
+            if (xv == 0) continue;
+            const int8_t* w_row = W + (size_t)k * (size_t)N;
+            for (int j = j0; j < j1; ++j) acc[j - j0] += xv * (int32_t)w_row[j];
+        }
+        for (int j = j0; j < j1; ++j) {
+            if (acc_out) acc_out[j] = acc[j - j0];
+            if (out) out[j] = (float)acc[j - j0] * s;
+        }
+    }
+}
+
+/* orc_gemv_i8w per row of X [M][K] with per-row scales xs[M] (the batched   */
+/* semantics below); threads split the rows.                                 */
+void orc_gemm_i8w(const int8_t* X, const float* xs, int M, const int8_t* W, float ws, int K, int N,
+                  int32_t* acc_out, float* out) {
+    const float* sx = xs;
+    #pragma omp parallel for schedule(dynamic, 1)
+    for (int m = 0; m < M; ++m) {
+        const float s = sx[m] * ws;
+        int32_t* acc = (int32_t*)calloc((size_t)N, sizeof(int32_t));
+        const int8_t* xr = X + (size_t)m * (size_t)K;
+        for (int k = 0; k < K; ++k) {
+            const int32_t xv = xr[k];
+            if (xv == 0) continue;
+            const int8_t* w_row = W + (size_t)k * (size_t)N;
+            for (int j = 0; j < N; ++j) acc[j] += xv * (int32_t)w_row[j];
+        }
+        for (int j = 0; j < N; ++j) {
+            if (acc_out) acc_out[(size_t)m * N + j] = acc[j];
+            if (out) out[(size_t)m * N + j] = (float)acc[j] * s;
+        }
+        free(acc);
+    }
+}
+
+/* orc_v11_unpack at int8 width. */
+int orc_v11_to_i8(const uint8_t* v11, int K, int N, int8_t* w_kn) {
+    if (K <= 0 || N <= 0 || (N % 4) != 0) return -5;
+    const int NB = N / 4;
+    #pragma omp parallel for schedule(static)
+    for (int k = 0; k < K; ++k)
+        for (int jb = 0; jb < NB; ++jb) {
+            const unsigned b = v11[(size_t)jb * K + k];
+            for (int s2 = 0; s2 < 4; ++s2) w_kn[(size_t)k * N + (size_t)(4 * jb + s2)] = (int8_t)orc_code_to_trit(b >> (2 * s2));
+        }
+    return 0;
+}
+
+/* Test-input generator (not a reference function): trits [K][N] from the    */
+/* counter-based splitmix64 stream of oracle.rand_trits, which             */
+/* ter_hip_synth_v11 draws on the device -- element i = k*N + n takes state  */
+/* seed + (i+1) * 0x9E3779B97F4A7C15; u = top 32 bits of the mixed value;   */
+/* trit 0 if u < t0, +1 if u < t1, else -1.                                 */
+void orc_rand_trits(uint64_t seed, int K, int N, uint64_t t0, uint64_t t1, int8_t* out) {
+    const size_t n = (size_t)K * (size_t)N;
+    #pragma omp parallel for schedule(static)
+    for (size_t i = 0; i < n; ++i) {
+        uint64_t z = seed + (uint64_t)(i + 1) * 0x9E3779B97F4A7C15ULL;
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+        z = z ^ (z >> 31);
+        const uint64_t u = z >> 32;
+        out[i] = (int8_t)(u < t0 ? 0 : (u < t1 ? 1 : -1));
     }
 }
 
@@ -437,6 +527,7 @@ void orc_rmsnorm_f16(const float* x, const uint16_t* gamma, int H, float eps, ui
 /* acc_out (optional) receives lane 0's fp32 value.                          */
 /* ------------------------------------------------------------------------ */
 void orc_lm_head_f16(const uint16_t* x, const uint16_t* e, int H, int V, uint16_t* logits, float* acc_out) {
+    #pragma omp parallel for schedule(static)  /* rows are independent; each keeps its own order */
     for (int v = 0; v < V; ++v) {
         const uint16_t* row = e + (size_t)v * (size_t)H;
         float lane[32];

@@ -24,8 +24,10 @@ def oracle_step(hm, tok, pos, K, V, table):
     hidden = hm["emb"][tok].astype(np.float32)
     for l, lay in enumerate(hm["layers"]):
         def mm(x_q, x_s, nm):
-            v11, ws, Kd, Nd = lay[nm]
-            return O.gemv_v11(x_q, x_s, v11, ws, Kd, Nd)[1]
+            w, ws, Kd, Nd = lay[nm]
+            if w.dtype == np.int8:  # trits [K][N] (host_model_i8)
+                return O.gemv_i8w(x_q, x_s, w, ws)[1]
+            return O.gemv_v11(x_q, x_s, w, ws, Kd, Nd)[1]
         xq, xs, _ = O.rmsnorm_quant(hidden, lay["attn_norm"], c.eps)
         q = half_of(mm(xq, xs, "Wq")).reshape(c.Nh, c.Hd)
         k = half_of(mm(xq, xs, "Wk")).reshape(c.Nkv, c.Hd)
@@ -57,3 +59,23 @@ def host_model(m):
     return dict(shape=m.shape, layers=layers, emb=host(m.token_embd), out_norm=host(m.output_norm))
 
 
+
+
+def host_model_i8(m, seed, p_zero=0.4):
+    """host_model for a random_model(shape, seed, p_zero): the projections as
+    int8 trits [K][N] regenerated on the host from random_model's seeds (the
+    splitmix64 stream ter_hip_synth_v11 draws), not read back from the
+    device; norms and the token embedding copied from the device."""
+    from ter_amd import bitnet as B
+    shapes = B.proj_shapes(m.shape)
+    layers = []
+    for l, lay in enumerate(m.layers):
+        d = {}
+        for i, nm in enumerate(B.PROJ):
+            K, N = shapes[nm]
+            s = seed * 1_000_003 + l * 101 + i
+            d[nm] = (O.rand_trits_c(s, K, N, p_zero), lay.W[nm].scale, K, N)
+        d.update(attn_norm=host(lay.attn_norm), attn_sub_norm=host(lay.attn_sub_norm), ffn_norm=host(lay.ffn_norm),
+                 ffn_sub_norm=host(lay.ffn_sub_norm))
+        layers.append(d)
+    return dict(shape=m.shape, layers=layers, emb=host(m.token_embd), out_norm=host(m.output_norm))

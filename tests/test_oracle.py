@@ -118,6 +118,31 @@ def test_mm_row_bitnet9_golden(golden):
         assert (folded.view(np.int32) != g[f"c{i}_out"].view(np.int32)).any()
 
 
+@pytest.mark.parametrize("K,N,p0", [(1, 1, 0.0), (27, 5, 0.4), (300, 20, 1 / 3), (2560, 640, 0.4),
+                                     (6912, 300, 0.4), (1000, 1, 0.0)])
+def test_int8_width_checkers_equal_mm_row(K, N, p0):
+    """orc_gemv_i8w / orc_gemm_i8w (the fast checkers of full-size lists)
+    equal orc_mm_row, which is pinned to the reference build; v11_to_i8
+    equals v11_unpack; the C trit stream equals rand_trits."""
+    W = O.rand_trits(K * 3 + N, K, N, p0)
+    assert (O.rand_trits_c(K * 3 + N, K, N, p0) == W).all()
+    X = O.rand_int8(K + N, 3 * K).reshape(3, K)
+    X[1, ::3] = 0                      # zero skip
+    X[2, :] = -128                     # extreme
+    xs = np.array([0.0312, 0.5, 1e-3], np.float32)
+    ws = np.float32(0.047)
+    acc, out = O.gemm_i8w(X, xs, W, ws)
+    for r in range(3):
+        ra, ry = O.mm_row(X.astype(np.int32), r, float(xs[r]), W.astype(np.int32), float(ws))
+        assert (acc[r].astype(np.int64) == ra).all(), r
+        assert (out[r].view(np.int32) == ry.view(np.int32)).all(), r
+        a1, y1 = O.gemv_i8w(X[r], float(xs[r]), W, float(ws))
+        assert (a1 == acc[r]).all() and (y1.view(np.int32) == out[r].view(np.int32)).all()
+    if N % 4 == 0:
+        v = O.v11_pack(W)
+        assert (O.v11_to_i8(v, K, N) == O.v11_unpack(v, K, N)).all()
+
+
 def test_mm_row_zero_skip_and_signs():
     # X == 0 rows contribute nothing; negating X negates acc; W = 0 -> 0.
     K, N = 64, 8
