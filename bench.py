@@ -344,6 +344,10 @@ def run_m1(args, cfg, fp32_x: bool):
         },
         "hbm_gbs": round(achieved_gbs, 1),
         "hbm_frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+        # the same bytes over the wall-clock step time `value` uses (it also
+        # holds the host's launch and synchronize latency of the timed region)
+        "hbm_gbs_wall": round(bytes_alg / (ms_step * 1e-3) / 1e9, 1),
+        "hbm_frac_wall": round(bytes_alg / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "lane_gmacs": round(lane_macs(cfg) / (ms_step * 1e-3) / 1e9, 1),
         "roofline": {
             "bound": "hbm",
@@ -355,6 +359,8 @@ def run_m1(args, cfg, fp32_x: bool):
             "kernel": "gemv_t16_kernel",
             "bytes_per_launch": bytes_alg,
             "mean_launch_us": round(ev_mean * 1e3, 3),
+            "timer": "HIP events on the launch stream over the timed region (value: wall clock)",
+            "frac_wall": round(bytes_alg / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         },
         "cpu_baseline": cpu,
         "modes": modes,
@@ -692,6 +698,127 @@ def run_decode(args):
     }
 
 
+# Per-shape table: the reference bench's five shapes
+# (cuda/ter_cuda_forward_packed_v13_bench.cu:422-428, the packed lm_head
+# included) and BitNet-2B's four.
+SHAPES = [("llama Wq/Wo", 2048, 2048), ("llama Wk/Wv", 2048, 512), ("llama Wgate/Wup", 2048, 8192),
+          ("llama Wdown", 8192, 2048), ("packed lm_head", 2048, 128256),
+          ("bitnet Wq/Wo", 2560, 2560), ("bitnet Wk/Wv", 2560, 640), ("bitnet Wgate/Wup", 2560, 6912),
+          ("bitnet Wdown", 6912, 2560)]
+
+
+def run_shapes(args):
+    """One GEMV shape at a time, cache-cold: each shape's weights are
+    rotated over enough seeded copies to span >= 512 MB (twice the Infinity
+    Cache).  Per shape:
+      single  -- the mm_packed_dispatch path, one launch per GEMV: each
+                 launch bracketed by its own HIP events, median of `steps`
+                 launches after 20 warmups (the reference's bench_one method,
+                 cuda/ter_cuda_forward_packed_v13_bench.cu:377-404), and the
+                 mean per launch of the same launches replayed back to back
+                 from a HIP graph;
+      list    -- the same copies as ONE work-list launch (median of launches).
+    GB/s counts packed bytes K*N/4 (the reference's convention, :399-401);
+    alg_gbs adds X and Y; lane GMAC/s uses ceil(K/27)*27*N."""
+    import torch
+    import ter_amd as T
+    rows = []
+    x_cache = {}
+    for label, K, N in SHAPES:
+        wbytes = K * N // 4
+        copies = max(2, -(-512_000_000 // wbytes))
+        Ws = [T.PackedTrits.from_v11(T.synth_v11(K, N, seed=900_000 + K + N + c), K, N, scale_of(c + 1))
+              for c in range(copies)]
+        if K not in x_cache:
+            x_cache[K] = T.synth_i8(K, seed=K)
+        x = x_cache[K]
+        xs = torch.full((1,), 0.0312, dtype=torch.float32, device="cuda")
+        y = torch.empty(N, dtype=torch.float32, device="cuda")
+        fns = [lambda W=W: T.mm_packed_dispatch(x, xs, W, y, K, N) for W in Ws]
+        settle(fns[0], 0.2)
+        _, mean_ev, med_ev = time_launches(fns, args.steps, 20)
+        n_graph = min(len(fns), 512)
+        g = graph_of(lambda: [f() for f in fns[:n_graph]])
+        _, g_ev, _ = time_launches([g.replay], max(10, args.steps // 50), 2)
+        graph_us = g_ev * 1e3 / n_graph
+        ys = [torch.empty(N, dtype=torch.float32, device="cuda") for _ in range(copies)]
+        plan = T.Plan([dict(w=W, x=x, x_scale=0.0312, y=yy) for W, yy in zip(Ws, ys)])
+        _, l_mean, l_med = time_launches([plan.launch], max(20, args.steps // 10), 3)
+        list_us = l_med * 1e3 / copies
+        lane = ((K + 26) // 27) * 27 * N
+        alg = wbytes + K + 4 * N
+
+        def fig(us):
+            return dict(us=round(us, 3), gbs=round(wbytes / (us * 1e-6) / 1e9, 1),
+                        alg_gbs=round(alg / (us * 1e-6) / 1e9, 1),
+                        frac_hbm=round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                        gmacs=round(K * N / (us * 1e-6) / 1e9, 1), lane_gmacs=round(lane / (us * 1e-6) / 1e9, 1))
+        row = dict(shape=label, K=K, N=N, copies=copies, single_median=fig(med_ev * 1e3),
+                   single_graph=fig(graph_us), list=fig(list_us), list_launch_us=round(l_med * 1e3, 2))
+        rows.append(row)
+        log(f"[bench] {label:16s} K={K:5d} N={N:6d}: single median {med_ev * 1e3:7.2f} us "
+            f"({row['single_median']['gbs']:7.1f} GB/s), graph {graph_us:7.2f} us, list {list_us:7.3f} us/GEMV "
+            f"({row['list']['gbs']:7.1f} GB/s, {100 * row['list']['frac_hbm']:.1f}%)")
+        del Ws, ys, plan, g, fns
+        torch.cuda.empty_cache()
+    best = max(rows, key=lambda r: r["list"]["frac_hbm"])
+    return {
+        "metric": "per-shape packed-trit GEMV (M=1): GB/s of packed weights, single launch and work list",
+        "value": best["list"]["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 20,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "per-shape table: the reference bench's 5 shapes + BitNet-2B's 4, int8 X, "
+                               "weights rotated over >= 512 MB of copies per shape"},
+        "shapes": rows,
+    }
+
+
+def run_floors(args):
+    """Floors of the M=1 path on this GPU: an empty launch, the smallest
+    GEMV (one 1 KiB tile, K=256, N=16), and a pure streaming read of the C2
+    sweep's packed bytes (243 MB, rotated over 4 buffers) with the C2 work
+    list's own partition (workgroup count of its plan) -- the ceiling of the
+    GEMV's streaming on the same bytes."""
+    import torch
+    import ter_amd as T
+    out = {}
+    g = graph_of(lambda: [T.noop() for _ in range(256)])
+    _, ev, _ = time_launches([g.replay], 50, 5)
+    out["empty_launch_us"] = round(ev * 1e3 / 256, 3)
+    _, ev1, med1 = time_launches([T.noop], 500, 20)
+    out["empty_launch_events_median_us"] = round(med1 * 1e3, 3)
+    W = T.PackedTrits.from_v11(T.synth_v11(256, 16, seed=3), 256, 16, 0.5)
+    x = T.synth_i8(256, seed=4)
+    xs = torch.full((1,), 0.5, dtype=torch.float32, device="cuda")
+    y = torch.empty(16, dtype=torch.float32, device="cuda")
+    g = graph_of(lambda: [T.mm_packed_dispatch(x, xs, W, y, 256, 16) for _ in range(256)])
+    _, ev, _ = time_launches([g.replay], 50, 5)
+    out["gemv_1kib_us"] = round(ev * 1e3 / 256, 3)
+    _, _, med = time_launches([lambda: T.mm_packed_dispatch(x, xs, W, y, 256, 16)], 500, 20)
+    out["gemv_1kib_events_median_us"] = round(med * 1e3, 3)
+    # pure read of the C2 packed bytes with the C2 plan's partition
+    sw = Sweep(LLAMA, 1, False)
+    plan = T.Plan(sw.items(0))
+    n_wg = plan.n_wg
+    nbytes = sum(K * N // 4 for _, K, N in LLAMA["shapes"]) * LLAMA["layers"]
+    del plan, sw
+    bufs = [torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(4)]
+    sink = torch.empty(4 * n_wg, dtype=torch.int32, device="cuda")
+    g = graph_of(lambda: [T.read_probe(b, nbytes, n_wg, sink) for b in bufs])
+    settle(g.replay)
+    _, ev, _ = time_launches([g.replay], max(25, args.steps // 4), 5)
+    us = ev * 1e3 / 4
+    out["c2_read_probe"] = dict(bytes=nbytes, n_wg=n_wg, us=round(us, 2), gbs=round(nbytes / (us * 1e-6) / 1e9, 1),
+                                frac_hbm=round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+    log(f"[bench] floors: {out}")
+    return {
+        "metric": "floors of the M=1 path: empty launch, 1 KiB GEMV, pure read of the C2 bytes",
+        "value": out["c2_read_probe"]["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": 5,
+        "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic", "config": {"workload": "floors"}, "floors": out,
+    }
+
+
 def run_copy(args):
     """A plain copy-shaped kernel of known size (torch.neg over 256 MiB of
     fp32: 256 MiB read, 256 MiB written per launch).  Its rocprofv3
@@ -715,8 +842,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--config", choices=["llama", "bitnet", "batched", "lm_head", "attention", "decode", "copy"],
-                    default="llama")
+    ap.add_argument("--config", choices=["llama", "bitnet", "batched", "lm_head", "attention", "decode", "copy",
+                                         "shapes", "floors"], default="llama")
     ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
     ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -735,6 +862,10 @@ def main():
         out = run_batched(args)
     elif args.config == "copy":
         out = run_copy(args)
+    elif args.config == "shapes":
+        out = run_shapes(args)
+    elif args.config == "floors":
+        out = run_floors(args)
     elif args.config == "lm_head":
         out = run_lm_head(args)
     elif args.config == "attention":

@@ -532,6 +532,17 @@ int ter_hip_synth_v11(uint8_t* v11_dev, int32_t K, int32_t N, uint64_t seed,
 int ter_hip_synth_i8(int8_t* x_dev, int64_t n, uint64_t seed, int32_t lo, int32_t hi,
                      void* stream);
 
+/* Measurement utilities (the floors bench.py reports beside the GEMV).
+ * ter_hip_noop: one launch of an empty kernel (the launch floor).
+ * ter_hip_read_probe: a pure streaming read of `bytes` (a multiple of 1024)
+ * of device memory at `buf`, split as the GEMV splits its tile stream (n_wg
+ * equal contiguous ranges, neighbouring ranges on one XCD, 4 waves per
+ * workgroup with nontemporal 16-byte loads); `sink` receives 4 * n_wg
+ * device words folded from the data.  No arithmetic: the ceiling of the
+ * GEMV's streaming on the same bytes. */
+int ter_hip_noop(void* stream);
+int ter_hip_read_probe(const void* buf, size_t bytes, int32_t n_wg, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,7 +21,9 @@ from .fabric import (  # noqa: F401
     mm_packed_dispatch,
     mm_packed_dispatch_f16,
     mm_row,
+    noop,
     quant_int8,
+    read_probe,
     relu2_rmsnorm_quant,
     rmsnorm_f16,
     rmsnorm_quant,
@@ -45,7 +47,9 @@ __all__ = [
     "mm_packed_dispatch",
     "mm_packed_dispatch_f16",
     "mm_row",
+    "noop",
     "quant_int8",
+    "read_probe",
     "relu2_rmsnorm_quant",
     "rmsnorm_f16",
     "rmsnorm_quant",

@@ -198,6 +198,8 @@ SIGNATURES = [
     ("ter_hip_reset_counters", None, [_P]),
     ("ter_hip_synth_v11", C.c_int, [_P, C.c_int32, C.c_int32, C.c_uint64, C.c_uint32, C.c_uint32, _P]),
     ("ter_hip_synth_i8", C.c_int, [_P, C.c_int64, C.c_uint64, C.c_int32, C.c_int32, _P]),
+    ("ter_hip_noop", C.c_int, [_P]),
+    ("ter_hip_read_probe", C.c_int, [_P, C.c_size_t, C.c_int32, _P, _P]),
 ]
 
 _lib = None

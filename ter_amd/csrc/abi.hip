@@ -1328,6 +1328,24 @@ int ter_hip_synth_i8(int8_t* x_dev, int64_t n, uint64_t seed, int32_t lo, int32_
     return TER_HIP_OK;
 }
 
+int ter_hip_noop(void* stream) {
+    hipError_t e = launch_noop(static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "noop launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_read_probe(const void* buf, size_t bytes, int32_t n_wg, uint32_t* sink, void* stream) {
+    if (!buf || !sink) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (bytes == 0 || bytes % kTileBytes || bytes / kTileBytes > (size_t)n_wg * kGemvWaves * (1u << 20))
+        return fail(TER_HIP_ERR_SHAPE, "bytes %zu: a nonzero multiple of 1024, at most 1 GiB per wave", bytes);
+    if (n_wg < 1) return fail(TER_HIP_ERR_SHAPE, "n_wg=%d", n_wg);
+    if (!aligned(buf, 16) || !aligned(sink, 4)) return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
+    hipError_t e = launch_read_probe(static_cast<const uint8_t*>(buf), (long long)(bytes / kTileBytes), n_wg,
+                                     reinterpret_cast<unsigned*>(sink), static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "read probe launch");
+    return TER_HIP_OK;
+}
+
 // ---- K4-style handle + KernelTable native slot -------------------------
 
 static int native_matmul(ter_hip_handle_t* h, const int64_t* args, size_t n_args) {

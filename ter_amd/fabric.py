@@ -601,6 +601,18 @@ def synth_v11(K: int, N: int, seed: int, p_zero: float = 1.0 / 3.0, device="cuda
     return out
 
 
+def noop(stream=None):
+    """One empty kernel launch (the launch floor)."""
+    L.check(L.lib().ter_hip_noop(_stream(stream)), "ter_hip_noop")
+
+
+def read_probe(buf, nbytes: int, n_wg: int, sink, stream=None):
+    """Pure streaming read of nbytes of `buf` with the GEMV's partition over
+    n_wg workgroups (a measurement ceiling; sink: int32 [4 * n_wg])."""
+    L.check(L.lib().ter_hip_read_probe(buf.data_ptr(), int(nbytes), int(n_wg), sink.data_ptr(), _stream(stream)),
+            "ter_hip_read_probe")
+
+
 def synth_i8(n: int, seed: int, lo: int = -127, hi: int = 127, device="cuda", stream=None):
     torch = _torch()
     out = torch.empty(n, dtype=torch.int8, device=device)
