@@ -209,6 +209,24 @@ int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale,
                    const ter_hip_wpk_t* W, int32_t N, float* out,
                    void* x_stage_dev, float* y_stage_dev, void* stream);
 
+/* The per-block branch of mm_row (src/tx/forward.cpp:308-330), for weights
+ * whose TritTensor carries block_scales: W is the payload {-m, 0, +m} packed
+ * by ter_hip_pack_payload, block_scales_dev the device fp32 scales
+ * [ceil(K*N / block_size)] (block b covers the row-major payload elements
+ * [b*bs, (b+1)*bs), as the reference indexes them).  out (host fp32 [N]) =
+ * float(facc * double(x_scale)), facc the reference's double sum over k in
+ * increasing order of x[k] * W[k][j] * block_scales[(k*N + j) / bs], bit for
+ * bit.  W.scale is not used (the reference's branch ignores Wt.scale).  X as
+ * ter_hip_mm_row (the row must fit int16), and every |x| * W.mag must be
+ * below 2^29 so each term is exact in double (TER_HIP_ERR_PAYLOAD
+ * otherwise; the reference's 9-trit activations and weights give at most
+ * 9841^2).  Synchronous; x_stage_dev 2*K bytes (16-byte aligned),
+ * y_stage_dev N fp32. */
+int ter_hip_mm_row_blocked(const int32_t* X, int32_t row, int32_t K, float x_scale,
+                           const ter_hip_wpk_t* W, int32_t N, const float* block_scales_dev,
+                           int64_t block_size, float* out, void* x_stage_dev, float* y_stage_dev,
+                           void* stream);
+
 /* ---------------------------------------------------------------------- */
 /* Work lists: many independent GEMVs in ONE launch (layer sweeps)          */
 /* ---------------------------------------------------------------------- */

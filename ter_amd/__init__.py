@@ -21,6 +21,7 @@ from .fabric import (  # noqa: F401
     mm_packed_dispatch,
     mm_packed_dispatch_f16,
     mm_row,
+    mm_row_blocked,
     noop,
     quant_int8,
     read_probe,
@@ -47,6 +48,7 @@ __all__ = [
     "mm_packed_dispatch",
     "mm_packed_dispatch_f16",
     "mm_row",
+    "mm_row_blocked",
     "noop",
     "quant_int8",
     "read_probe",

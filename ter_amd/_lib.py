@@ -160,6 +160,8 @@ SIGNATURES = [
     ("ter_hip_mm_packed_dispatch", C.c_int, [_P, _P, C.POINTER(WPK), _P, C.c_int32, C.c_int32, _P]),
     ("ter_hip_mm_packed_dispatch_f16", C.c_int, [_P, _P, C.POINTER(WPK), _P, C.c_int32, C.c_int32, _P]),
     ("ter_hip_mm_row", C.c_int, [_P, C.c_int32, C.c_int32, C.c_float, C.POINTER(WPK), C.c_int32, _P, _P, _P, _P]),
+    ("ter_hip_mm_row_blocked", C.c_int, [_P, C.c_int32, C.c_int32, C.c_float, C.POINTER(WPK), C.c_int32, _P,
+                                         C.c_int64, _P, _P, _P, _P]),
     ("ter_hip_plan_create", C.c_int, [C.POINTER(C.c_void_p), C.POINTER(GemvItem), C.c_int32, C.c_int32]),
     ("ter_hip_plan_launch", C.c_int, [_P, _P]),
     ("ter_hip_plan_stats", C.c_int, [_P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_int32)]),

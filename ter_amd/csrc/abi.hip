@@ -736,6 +736,46 @@ int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale, cons
     return TER_HIP_OK;
 }
 
+int ter_hip_mm_row_blocked(const int32_t* X, int32_t row, int32_t K, float x_scale, const ter_hip_wpk_t* W, int32_t N,
+                           const float* block_scales_dev, int64_t block_size, float* out, void* x_stage_dev,
+                           float* y_stage_dev, void* stream) {
+    if (!X || !W || !out || !x_stage_dev || !y_stage_dev || !block_scales_dev)
+        return fail(TER_HIP_ERR_NULL, "null argument");
+    int rc = check_wpk(W);
+    if (rc) return rc;
+    if (row < 0) return fail(TER_HIP_ERR_SHAPE, "negative row");
+    if (W->K != K || W->N != N) return fail(TER_HIP_ERR_SHAPE, "K/N (%d,%d) do not match W (%d,%d)", K, N, W->K, W->N);
+    if (block_size < 1) return fail(TER_HIP_ERR_SHAPE, "block_size %lld < 1", (long long)block_size);
+    if (!aligned(x_stage_dev, 16) || !aligned(y_stage_dev, 4) || !aligned(block_scales_dev, 4))
+        return fail(TER_HIP_ERR_ALIGN, "misaligned staging or scale buffer");
+    const int32_t* xr = X + (size_t)row * (size_t)K;
+    int32_t lo = 0, hi = 0;
+    for (int k = 0; k < K; ++k) {
+        lo = std::min(lo, xr[k]);
+        hi = std::max(hi, xr[k]);
+    }
+    if (lo < -32768 || hi > 32767)
+        return fail(TER_HIP_ERR_PAYLOAD, "X values [%d, %d] do not fit int16 (no CPU fallback)", lo, hi);
+    const long long amax = std::max(-(long long)lo, (long long)hi);
+    if (amax * (long long)W->mag >= (1LL << 29))
+        return fail(TER_HIP_ERR_PAYLOAD, "|x| * m = %lld * %d reaches 2^29: the double terms would round", amax, W->mag);
+    std::vector<int16_t> xw;
+    try {
+        xw.assign(xr, xr + K);
+    } catch (...) {
+        return fail(TER_HIP_ERR_ALLOC, "host staging allocation");
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    hipError_t e = hipMemcpyAsync(x_stage_dev, xw.data(), (size_t)K * 2, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess)
+        e = launch_mm_row_blocked(W->data, K, N, W->mag, static_cast<const int16_t*>(x_stage_dev), block_scales_dev,
+                                  (long long)block_size, x_scale, y_stage_dev, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, y_stage_dev, (size_t)N * sizeof(float), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) return hip_fail(e, "blocked mm_row");
+    return TER_HIP_OK;
+}
+
 int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items, int32_t n, int32_t wg_per_cu) {
     if (!plan || !items) return fail(TER_HIP_ERR_NULL, "null plan or items");
     *plan = nullptr;

@@ -101,6 +101,9 @@ hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const i
 int gemv_x16_lds_bytes(int K, int strips_per_wg);
 hipError_t launch_gemv_x16(const GemvDesc& d, int n_wg, int lds_bytes, hipStream_t st);
 hipError_t launch_pack_v11(const uint8_t* v11, uint8_t* t16, int K, int N, hipStream_t st);
+// The per-block branch of mm_row (blocked.hip): one thread per column.
+hipError_t launch_mm_row_blocked(const uint8_t* w, int K, int N, int mag, const int16_t* x, const float* bsc,
+                                 long long bs, float xs, float* out, hipStream_t st);
 // Measurement kernels (probe.hip).
 hipError_t launch_noop(hipStream_t st);
 hipError_t launch_read_probe(const uint8_t* buf, long long tiles, int n_wg, unsigned* sink, hipStream_t st);

@@ -231,6 +231,26 @@ def mm_row(Xt_payload: np.ndarray, row: int, x_scale: float, W: PackedTrits, K: 
     return out
 
 
+def mm_row_blocked(Xt_payload: np.ndarray, row: int, x_scale: float, W: PackedTrits, K: int, N: int,
+                   block_scales, block_size: int) -> np.ndarray:
+    """The per-block branch of mm_row (src/tx/forward.cpp:308-330): W's
+    TritTensor carries block_scales (fp32 [ceil(K*N / block_size)], here a
+    CUDA tensor or a host array); host fp32 out[N], bit for bit the
+    reference's double accumulation."""
+    torch = _torch()
+    X = np.ascontiguousarray(Xt_payload, dtype=np.int32)
+    if isinstance(block_scales, np.ndarray):
+        block_scales = torch.from_numpy(np.ascontiguousarray(block_scales, dtype=np.float32)).to(W.buf.device)
+    _require_cuda(block_scales, "block_scales", torch.float32, -(-K * N // int(block_size)))
+    out = np.empty(N, dtype=np.float32)
+    xs = torch.empty(2 * K, dtype=torch.int8, device=W.buf.device)
+    ys = torch.empty(N, dtype=torch.float32, device=W.buf.device)
+    L.check(L.lib().ter_hip_mm_row_blocked(X.ctypes.data, int(row), int(K), float(x_scale), C.byref(W.wpk), int(N),
+                                           block_scales.data_ptr(), int(block_size), out.ctypes.data, xs.data_ptr(),
+                                           ys.data_ptr(), _stream(None)), "ter_hip_mm_row_blocked")
+    return out
+
+
 def quant_int8(x, q=None, scale_out=None, stream=None):
     """Per-row absmax int8 quantization of fp32 x [M][K] (quant_int8_k steps)."""
     torch = _torch()

@@ -14,6 +14,9 @@ Fixtures:
   i2s_block.npz       the hand-built i2_s block of tests/test_nt_dequant.cpp:37-61
   mm_row_random.npz   seeded random (X, W, scales) -> reference mm_row outputs, several shapes
   quantizers.npz      reference quantize(..., 9) and quantize_bitnet on seeded floats
+  mm_row_blocked.npz  the per-block branch of the reference mm_row (src/tx/forward.cpp:308-330):
+                      payload {-9841, 0, +9841}, per-block fp32 scales (some zero), block sizes
+                      that do and do not divide N, 9-trit activations -> reference outputs
   mm_row_bitnet9.npz  the reference host forward's mm_row calls on BitNet weights: weights
                       through quantize_bitnet and quantize(..., 9) (src/host/load_gguf.cpp:64-111:
                       payload {-9841, 0, +9841}), activations through quantize(x, {1, K}, 9)
@@ -150,6 +153,37 @@ def mm_row_bitnet9():
     np.savez_compressed(os.path.join(HERE, "mm_row_bitnet9.npz"), **arrays)
 
 
+# (K, N, block_size, seed)
+BLOCKED_CASES = [(2560, 64, 4096, 51), (6912, 32, 1000, 53), (300, 20, 7, 57), (256, 16, 256 * 16, 59)]
+
+
+def mm_row_blocked():
+    arrays = {}
+    for i, (K, N, bs, seed) in enumerate(BLOCKED_CASES):
+        t = O.rand_trits(seed, K, N, 0.4)
+        W = t.astype(np.int32) * 9841
+        nb = -(-K * N // bs)
+        u = (O.splitmix64(seed + 7, nb) >> np.uint64(40)).astype(np.float64) / float(1 << 24)
+        bsc = (1e-6 + 2e-6 * u).astype(np.float32)
+        bsc[::5] = 0.0  # blocks whose scale is zero (all-zero blocks of quantize_blocked)
+        xf = O.rand_normal_f32(seed + 1, K)
+        X, xs = O.ref_quantize(xf, 9)
+        r = O.RefMmRow(X.reshape(1, K), float(xs), W, 1.0, bsc, bs)
+        out = r.run(0).copy()
+        r.close()
+        arrays[f"c{i}_K"] = np.int32(K)
+        arrays[f"c{i}_N"] = np.int32(N)
+        arrays[f"c{i}_bs"] = np.int64(bs)
+        arrays[f"c{i}_trits"] = t.astype(np.int8)
+        arrays[f"c{i}_mag"] = np.int32(9841)
+        arrays[f"c{i}_bsc"] = bsc
+        arrays[f"c{i}_X"] = X.astype(np.int16)
+        arrays[f"c{i}_xs"] = np.float32(xs)
+        arrays[f"c{i}_out"] = out
+    arrays["n_cases"] = np.int32(len(BLOCKED_CASES))
+    np.savez_compressed(os.path.join(HERE, "mm_row_blocked.npz"), **arrays)
+
+
 def main():
     if not O.ref_available():
         raise SystemExit("oracle/_ref is not built (make -C oracle ref needs the reference tree)")
@@ -159,6 +193,7 @@ def main():
     mm_row_random()
     quantizers()
     mm_row_bitnet9()
+    mm_row_blocked()
     for f in sorted(os.listdir(HERE)):
         if f.endswith(".npz"):
             print(f, os.path.getsize(os.path.join(HERE, f)))

@@ -156,6 +156,33 @@ def test_mm_row_bitnet9_golden(cuda, golden):
         assert_f32_equal(out, g[f"c{i}_out"])
 
 
+def test_mm_row_blocked_golden(cuda, golden):
+    """The per-block branch of mm_row (src/tx/forward.cpp:308-330) on the
+    GPU against the reference build's outputs (tests/golden/mm_row_blocked.npz):
+    block sizes that do and do not divide N, zero-scale blocks -- bit for bit."""
+    import ter_amd as T
+    g = golden("mm_row_blocked.npz")
+    for i in range(int(g["n_cases"])):
+        K, N, bs = int(g[f"c{i}_K"]), int(g[f"c{i}_N"]), int(g[f"c{i}_bs"])
+        m = int(g[f"c{i}_mag"])
+        W = T.PackedTrits.from_payload(g[f"c{i}_trits"].astype(np.int32) * m, 1.0)
+        X = g[f"c{i}_X"].astype(np.int32)
+        out = T.mm_row_blocked(np.stack([X, X[::-1]]), 0, float(g[f"c{i}_xs"]), W, K, N, g[f"c{i}_bsc"], bs)
+        assert_f32_equal(out, g[f"c{i}_out"])
+
+
+def test_mm_row_blocked_refuses_inexact_terms(cuda):
+    """|x| * m at 2^29 or beyond would make the double terms round: refused."""
+    import ter_amd as T
+    K, N = 64, 16
+    W = T.PackedTrits.from_payload(O.rand_trits(1, K, N).astype(np.int32) * 32767, 1.0)
+    X = np.zeros((1, K), np.int32)
+    X[0, 3] = 16385  # 16385 * 32767 >= 2^29
+    with pytest.raises(T._lib.TerHipError) as e:
+        T.mm_row_blocked(X, 0, 1.0, W, K, N, np.ones(K * N, np.float32), 1)
+    assert e.value.code == T._lib.ERR_PAYLOAD
+
+
 def int16_case(K, N, seed, x, p0=1 / 3, xs=0.00013, ws=0.05, x_scale_dev=False):
     import torch
     import ter_amd as T

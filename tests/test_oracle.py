@@ -143,6 +143,31 @@ def test_int8_width_checkers_equal_mm_row(K, N, p0):
         assert (O.v11_to_i8(v, K, N) == O.v11_unpack(v, K, N)).all()
 
 
+def test_mm_row_blocked_golden(golden):
+    """The per-block branch written by the reference build
+    (tests/golden/mm_row_blocked.npz): the restatement reproduces it bit for
+    bit, and so does the closed form -- every term x * W * s is exact in
+    double here (|x| * m <= 9841^2 < 2^29), so only the in-order additions,
+    the final multiply and the conversion round."""
+    g = golden("mm_row_blocked.npz")
+    for i in range(int(g["n_cases"])):
+        K, N, bs = int(g[f"c{i}_K"]), int(g[f"c{i}_N"]), int(g[f"c{i}_bs"])
+        W = g[f"c{i}_trits"].astype(np.int32) * int(g[f"c{i}_mag"])
+        X = g[f"c{i}_X"].astype(np.int32)
+        bsc = g[f"c{i}_bsc"]
+        out = O.mm_row_blocked(X[None], 0, float(g[f"c{i}_xs"]), W, bsc, bs)
+        assert (out.view(np.int32) == g[f"c{i}_out"].view(np.int32)).all(), i
+        assert np.abs(X).max() * 9841 < 2 ** 29
+        flat = np.arange(K * N, dtype=np.int64).reshape(K, N) // bs
+        terms = (X[:, None].astype(np.float64) * W.astype(np.float64)) * bsc[flat].astype(np.float64)
+        facc = np.zeros(N, np.float64)
+        for k in range(K):
+            if X[k] != 0:
+                facc = facc + terms[k]
+        closed = (facc * np.float64(g[f"c{i}_xs"])).astype(np.float32)
+        assert (closed.view(np.int32) == g[f"c{i}_out"].view(np.int32)).all(), i
+
+
 def test_mm_row_zero_skip_and_signs():
     # X == 0 rows contribute nothing; negating X negates acc; W = 0 -> 0.
     K, N = 64, 8
