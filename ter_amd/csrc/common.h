@@ -21,7 +21,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/ter_hip.h"
+#include "ter_hip.h"
 
 namespace terhip {
 
@@ -156,11 +156,23 @@ int gemm_mb_of(int M);
 hipError_t launch_gemm_list(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
                             long long total_blocks, int n_wg, int mb, bool vec, hipStream_t st);
 // Streaming GEMM for M <= 16 (whole X of a GEMM staged in LDS, whole strips
-// per wave, no per-unit barrier).  lds_bytes = streaming_lds_bytes(max M, max K).
-inline int gemm_stream_lds_bytes(int M, int K) { return M * (units_of(K) * kUnitK + 16) + 16 * 4; }
-constexpr int kGemmStreamLdsMax = 64 * 1024;
+// per wave, no per-unit barrier).  LDS (for the plan's widest M and K): the X
+// image, M rows of Ku * 16 chunks + one padding chunk each (16 bytes per
+// chunk), at [0, gemm_stream_zero_off); a zero row of Ku * 256 bytes; 16 row
+// sums; the waves' tile slots.
+inline int gemm_stream_zero_off(int M, int K) { return M * (units_of(K) * (kUnitK / 16) + 1) * 16; }
+// Each of the workgroup's 4 waves turns its tiles into MFMA operand order through two 1 KiB slots.
+constexpr int gemm_stream_slot_bytes() { return 4 * 2 * kTileBytes; }
+inline int gemm_stream_lds_bytes(int M, int K) {
+    return gemm_stream_zero_off(M, K) + units_of(K) * kUnitK + 64 + gemm_stream_slot_bytes();
+}
+constexpr int kGemmStreamXMax = 64 * 1024;   // the X image (its staging registers hold 64 KiB)
+constexpr int kGemmStreamLdsMax = 80 * 1024; // in all: two workgroups per CU
+inline bool gemm_stream_fits(int M, int K) {
+    return M <= 16 && gemm_stream_zero_off(M, K) <= kGemmStreamXMax && gemm_stream_lds_bytes(M, K) <= kGemmStreamLdsMax;
+}
 hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
-                              long long total_tiles, int n_wg, int lds_bytes, bool vec, hipStream_t st);
+                              long long total_tiles, int n_wg, int lds_bytes, int zero_off, bool vec, hipStream_t st);
 int gemm_stream_max_wg_per_cu(int lds_bytes);
 
 // Resident GEMM workgroups per CU for row-block count mb (0 if the query fails).

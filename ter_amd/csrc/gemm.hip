@@ -252,37 +252,87 @@ __global__ __launch_bounds__(kThreads) void gemm_t16_kernel(GemmDesc single, con
 // Streaming variant for M <= 16 (one MFMA row block).  The work list is one
 // stream of tiles cut into equal contiguous ranges per workgroup, like the
 // M = 1 GEMV; a workgroup owns the strips whose first tile lies in its range.
-// Per GEMM segment it stages the whole X[0:M][0:Ku*256] in LDS once (plus
-// per-row sums), then each wave streams the tiles of a contiguous run of
-// whole strips with two batches of tiles in registers and no further
-// barrier.  A strip's 16 x 16 MFMA accumulator is written when its last
-// unit is in.
-constexpr int kSBatch = 4;
+// Per GEMM segment it stages the whole X[0:M][0:Ku*256] in LDS once, then
+// each wave streams the tiles of a contiguous run of whole strips with two
+// batches of tiles in registers and no further barrier.  A strip's 16 x 16
+// MFMA accumulator is written when its last unit is in.
+//
+// Staging.  The LDS image of X is a sequence of 16-byte chunks, row r's
+// chunk c at index r * (Ku * 16 + 1) + c (one padding chunk per row, so the
+// 16 rows an A operand reads fall on distinct banks).  Every thread loads
+// its (at most kStageChunks) chunks into registers at once through a buffer
+// resource (chunks past the end read zeros, so no load is predicated), then
+// the segment's first weight batch is issued, then the chunks are written
+// to LDS: the writes wait only for the X loads (older than the weights), in
+// one L2 round trip for the whole X.  Row sums are gathered on the way (the
+// u = w + 1 codes feed the MFMA as they are, 7 bit operations per 16 trits,
+// and the epilogue subtracts sum_k X[m][k]); the lanes of rows >= M read a
+// zero row kept after the X image instead of masking their A operands.
+constexpr int kSWaves = 4;                  // waves per workgroup (all sharing one X image)
+constexpr int kSThreads = 64 * kSWaves;
+constexpr int kStageChunks = 65536 / 16 / kSThreads;  // chunks per thread: the 64 KiB LDS limit
+constexpr int kSBatch = 6;                  // tiles per batch, two batches per wave in flight
 
-template <bool kVec>
-__device__ __forceinline__ void stage_rows(const GemmDesc& d, int8_t* lx, int ldl, int* rsum) {
-    const int per_row = d.Ku * (kUnitK / 16);  // 16-byte chunks per row
-    const int nch = d.M * per_row;
+// Chunks of one staged row (Ku * 16) plus its padding chunk.
+__device__ __forceinline__ int stream_row_chunks(int Ku) { return Ku * (kUnitK / 16) + 1; }
+
+// This thread's chunks of X (16-byte aligned rows), in registers.
+struct XStage {
+    u32x4 v[kStageChunks];
+};
+
+__device__ __forceinline__ void stage_load(const GemmDesc& d, XStage& x) {
+    const int per = stream_row_chunks(d.Ku) - 1;
+    const int nch = d.M * per;
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)d.x, 0, d.M * d.ldx, 0x00020000);
-    if (threadIdx.x < 16) rsum[threadIdx.x] = 0;
-    __syncthreads();
-    for (int c = threadIdx.x; c < nch; c += kThreads) {
-        const int row = c / per_row, ch = c - row * per_row;
-        const u32x4 v = load_x16<kVec>(d, xr, row, ch * 16);
-        *reinterpret_cast<u32x4*>(lx + row * ldl + ch * 16) = v;
-        // per_row is a multiple of 16, so the 16 lanes of a DPP row share `row`
-        const int s = row_sum16(sum_bytes(v));
-        if ((threadIdx.x & 15) == 0) atomicAdd(rsum + row, s);
+#pragma unroll
+    for (int i = 0; i < kStageChunks; ++i) {
+        const int c = threadIdx.x + kSThreads * i;
+        const int row = c / per, ch = c - row * per;
+        x.v[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, c < nch ? row * d.ldx + ch * 16 : 0x7FFFFFF0, 0, 0);
     }
 }
 
-__device__ __forceinline__ void stream_load(unsigned (&w)[kSBatch][4], __amdgpu_buffer_rsrc_t rs, int woff, int i0) {
+// Write the staged chunks to LDS and add their bytes into rsum[row] (zero
+// before the call).  per = Ku * 16 is a multiple of 16 and a thread's chunks
+// are tid + 256 i, so the 16 lanes of a DPP row hold chunks of one row.
+__device__ __forceinline__ void stage_store(const GemmDesc& d, const XStage& x, int8_t* lx, int* rsum) {
+    const int rc = stream_row_chunks(d.Ku), per = rc - 1;
+    const int nch = d.M * per;
 #pragma unroll
-    for (int i = 0; i < kSBatch; ++i) {
-        const int toff = woff + (i0 + i) * kTileBytes;  // range-checked: zeros past the wave's tiles
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) w[i][ks] = __builtin_amdgcn_raw_buffer_load_b32(rs, toff + ks * 64, 0, 2);
+    for (int i = 0; i < kStageChunks; ++i) {
+        const int c = threadIdx.x + kSThreads * i;
+        const int row = c / per, ch = c - row * per;
+        if (c < nch) {
+            *reinterpret_cast<u32x4*>(lx + (row * rc + ch) * 16) = x.v[i];
+            const int sm = row_sum16(sum_bytes(x.v[i]));
+            if ((threadIdx.x & 15) == 0) atomicAdd(rsum + row, sm);
+        }
     }
+}
+
+// Byte-wise staging from registers (rows not 16-byte aligned), row sums too.
+__device__ __forceinline__ void stage_rows_bytes(const GemmDesc& d, int8_t* lx, int* rsum) {
+    const int rc = stream_row_chunks(d.Ku);
+    const int nch = d.M * (rc - 1);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)d.x, 0, d.M * d.ldx, 0x00020000);
+    for (int c = threadIdx.x; c < nch; c += kSThreads) {
+        const int row = c / (rc - 1), ch = c - row * (rc - 1);
+        const u32x4 v = load_x16<false>(d, xr, row, ch * 16);
+        *reinterpret_cast<u32x4*>(lx + (row * rc + ch) * 16) = v;
+        const int sm = row_sum16(sum_bytes(v));
+        if ((threadIdx.x & 15) == 0) atomicAdd(rsum + row, sm);
+    }
+}
+
+// A batch of NB tiles: one 16-byte load per lane and tile, lane L taking
+// bytes [16 L, 16 L + 16) of the contiguous 1 KiB tile (the GEMV's loads).
+template <int NB>
+__device__ __forceinline__ void stream_load(u32x4 (&w)[NB], __amdgpu_buffer_rsrc_t rs, int i0) {
+    const int voff = (threadIdx.x & 63) * 16;
+#pragma unroll
+    for (int i = 0; i < NB; ++i)  // range-checked: zeros past the wave's tiles
+        w[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + (i0 + i) * kTileBytes, 0, 2 /* nt */);
 }
 
 struct StreamState {
@@ -290,21 +340,31 @@ struct StreamState {
     i32x4 C;
 };
 
-__device__ __forceinline__ void stream_compute(const GemmDesc& d, const unsigned (&w)[kSBatch][4], int i0, int n,
-                                               const int8_t* arow, bool arow_ok, int st_base, const int* rsum,
-                                               const float (&xsr)[4], StreamState& p) {
+// Reduce tiles [i0, min(i0 + NB, n)) of the wave's run.  Each tile goes
+// through the wave's two 1 KiB LDS slots (tile order in, MFMA B order out):
+// lane (j, g) takes, for slab ks, the dword of column j over rows
+// 64 ks + 16 g .. +15 at tile offset (j >> 2) * 256 + (4 ks + g) * 16 + (j & 3) * 4.
+// A wave's LDS operations run in order, so the slot written for tile i + 1
+// while tile i is read back never overtakes the reads of tile i - 1.
+template <int NB>
+__device__ __forceinline__ void stream_compute(const GemmDesc& d, const u32x4 (&w)[NB], int i0, int n,
+                                               const int8_t* arow, unsigned char* slot, int st_base,
+                                               const int (&rs)[4], const float (&xsr)[4], StreamState& p) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
+    const int roff = (j >> 2) * 256 + g * 16 + (j & 3) * 4;
+    *reinterpret_cast<u32x4*>(slot + lane * 16) = w[0];
 #pragma unroll
-    for (int i = 0; i < kSBatch; ++i) {
+    for (int i = 0; i < NB; ++i) {
+        if (i + 1 < NB) *reinterpret_cast<u32x4*>(slot + ((i + 1) & 1) * kTileBytes + lane * 16) = w[i + 1];
         if (i0 + i < n) {
+            const unsigned char* ts = slot + (i & 1) * kTileBytes + roff;
             const int8_t* ab = arow + p.u * kUnitK + g * 16;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                i32x4 A = *reinterpret_cast<const i32x4*>(ab + ks * 64);
-                if (!arow_ok) A = i32x4{0, 0, 0, 0};
-                const unsigned dw = w[i][ks];
+                const i32x4 A = *reinterpret_cast<const i32x4*>(ab + ks * 64);
+                const unsigned dw = *reinterpret_cast<const unsigned*>(ts + ks * 64);
                 const i32x4 B = i32x4{(int)(dw & 0x03030303u), (int)((dw >> 2) & 0x03030303u),
                                       (int)((dw >> 4) & 0x03030303u), (int)((dw >> 6) & 0x03030303u)};
                 p.C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, p.C, 0, 0, 0);
@@ -315,11 +375,7 @@ __device__ __forceinline__ void stream_compute(const GemmDesc& d, const unsigned
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int row = g * 4 + e;
-                        if (row < d.M) {
-                            const int val = p.C[e] - rsum[row];
-                            const long long o = (long long)row * d.N + col;
-                            emit_out(d, o, val, xsr[e]);
-                        }
+                        if (row < d.M) emit_out(d, (long long)row * d.N + col, p.C[e] - rs[e], xsr[e]);
                     }
                 }
                 p.C = i32x4{0, 0, 0, 0};
@@ -331,10 +387,13 @@ __device__ __forceinline__ void stream_compute(const GemmDesc& d, const unsigned
 }
 
 template <bool kList, bool kVec>
-__global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GemmDesc single, const GemmDesc* __restrict__ list,
+__global__ __launch_bounds__(kSThreads) void gemm_stream_kernel(GemmDesc single, const GemmDesc* __restrict__ list,
                                                                const int32_t* __restrict__ first, long long total,
-                                                               int n_wg) {
+                                                               int n_wg, int zero_off, int zero_bytes) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
+    // the zero row (Ku * 256 bytes of the widest GEMM) after the X images
+    for (int c = threadIdx.x; c < zero_bytes / 16; c += kSThreads)
+        *reinterpret_cast<u32x4*>(lds_raw + zero_off + c * 16) = u32x4{0u, 0u, 0u, 0u};
     int gi = blockIdx.x;
     if ((n_wg & 7) == 0) gi = (gi & 7) * (n_wg >> 3) + (gi >> 3);
     const long long t_begin = total * gi / n_wg;
@@ -344,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GemmDesc single, 
     const int lane = threadIdx.x & 63;
     const int wave = uniform(threadIdx.x >> 6);
     const int g = lane >> 4, j = lane & 15;
-    const int woff = (j >> 2) * 256 + g * 16 + (j & 3) * 4;
+    unsigned char* slot = lds_raw + zero_off + zero_bytes + 64 + wave * 2 * kTileBytes;  // this wave's 2 tiles
     long long t = t_begin;
     while (t < t_end) {
         const GemmDesc d = kList ? list[di] : single;
@@ -353,36 +412,54 @@ __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GemmDesc single, 
         // the strips whose first tile lies in [la, lb)
         const int st_a = (la + d.Ku - 1) / d.Ku, st_b = (lb + d.Ku - 1) / d.Ku;
         const int ns = st_b - st_a;
-        const int w_a = st_a + ns * wave / kWaves, w_b = st_a + ns * (wave + 1) / kWaves;
+        const int w_a = st_a + ns * wave / kSWaves, w_b = st_a + ns * (wave + 1) / kSWaves;
         const int n = (w_b - w_a) * d.Ku;  // this wave's tiles
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(d.w + (long long)w_a * d.Ku * kTileBytes), 0, n * kTileBytes, 0x00020000);
-        unsigned wa[kSBatch][4], wb[kSBatch][4];
-        stream_load(wa, rs, woff, 0);  // in flight while X is staged
-        const int ldl = d.Ku * kUnitK + 16;
-        int8_t* lx = reinterpret_cast<int8_t*>(lds_raw);
-        int* rsum = reinterpret_cast<int*>(lds_raw + d.M * ldl);
+        const int rc = stream_row_chunks(d.Ku);
+        unsigned char* lx = lds_raw;
+        // rows 4g .. 4g + 3's scales in one load, rows past M reading zeros
+        const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void*)d.xs, 0, d.M * 4, 0x00020000);
+        const u32x4 xsw = __builtin_amdgcn_raw_buffer_load_b128(sr, g * 16, 0, 0);
+        u32x4 wa[kSBatch], wb[kSBatch];
+        int* rsum = reinterpret_cast<int*>(lds_raw + zero_off + zero_bytes);
+        if constexpr (kVec) {
+            XStage xst;
+            stage_load(d, xst);           // X first: its writes below wait for nothing else
+            stream_load(wa, rs, 0);
+            __syncthreads();              // the previous segment is done with LDS
+            if (threadIdx.x < 16) rsum[threadIdx.x] = 0;
+            __syncthreads();
+            if (ns > 0) stage_store(d, xst, reinterpret_cast<int8_t*>(lx), rsum);
+        } else {
+            stream_load(wa, rs, 0);
+            __syncthreads();
+            if (threadIdx.x < 16) rsum[threadIdx.x] = 0;
+            __syncthreads();
+            if (ns > 0) stage_rows_bytes(d, reinterpret_cast<int8_t*>(lx), rsum);
+        }
         float xsr[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int row = g * 4 + e;
-            xsr[e] = row < d.M ? gptr(d.xs)[row] * d.w_scale : 0.f;
+            const unsigned b = xsw[e];  // (bit_cast of the element lvalue itself reads element 0)
+            xsr[e] = __builtin_bit_cast(float, b) * d.w_scale;
         }
-        __syncthreads();  // the previous segment is done with LDS
-        if (ns > 0) stage_rows<kVec>(d, lx, ldl, rsum);
         __syncthreads();
         if (n > 0) {
-            const bool arow_ok = j < d.M;
-            const int8_t* arow = lx + (arow_ok ? j : 0) * ldl;
+            // rows >= M read the zero row (their outputs are not written)
+            const int8_t* arow = reinterpret_cast<const int8_t*>(lx) + (j < d.M ? j * rc * 16 : zero_off);
+            int rsr[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rsr[e] = rsum[g * 4 + e];
             StreamState p{0, 0, i32x4{0, 0, 0, 0}};
             int i0 = 0;
             while (true) {
-                stream_load(wb, rs, woff, i0 + kSBatch);
-                stream_compute(d, wa, i0, n, arow, arow_ok, w_a, rsum, xsr, p);
+                stream_load(wb, rs, i0 + kSBatch);
+                stream_compute(d, wa, i0, n, arow, slot, w_a, rsr, xsr, p);
                 i0 += kSBatch;
                 if (i0 >= n) break;
-                stream_load(wa, rs, woff, i0 + kSBatch);
-                stream_compute(d, wb, i0, n, arow, arow_ok, w_a, rsum, xsr, p);
+                stream_load(wa, rs, i0 + kSBatch);
+                stream_compute(d, wb, i0, n, arow, slot, w_a, rsr, xsr, p);
                 i0 += kSBatch;
                 if (i0 >= n) break;
             }
@@ -392,11 +469,29 @@ __global__ __launch_bounds__(kThreads) void gemm_stream_kernel(GemmDesc single, 
     }
 }
 
+// Dynamic LDS above the 64 KiB default for every instantiation; once per process.
+hipError_t allow_stream_lds() {
+    static hipError_t done = [] {
+        hipError_t e = hipSuccess;
+        const void* fns[] = {reinterpret_cast<const void*>(&gemm_stream_kernel<true, true>),
+                             reinterpret_cast<const void*>(&gemm_stream_kernel<true, false>),
+                             reinterpret_cast<const void*>(&gemm_stream_kernel<false, true>),
+                             reinterpret_cast<const void*>(&gemm_stream_kernel<false, false>)};
+        for (const void* f : fns)
+            if (e == hipSuccess) e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kGemmStreamLdsMax);
+        return e;
+    }();
+    return done;
+}
+
 template <bool kList, bool kVec>
 hipError_t launch_stream_t(const GemmDesc& single, const GemmDesc* list, const int32_t* first, long long total, int n_wg,
-                           int lds, hipStream_t st) {
-    hipLaunchKernelGGL((gemm_stream_kernel<kList, kVec>), dim3(n_wg), dim3(kThreads), lds, st, single, list, first,
-                       total, n_wg);
+                           int lds, int zero_off, hipStream_t st) {
+    const hipError_t e = allow_stream_lds();
+    if (e != hipSuccess) return e;
+    // LDS: the X image [0, zero_off), the zero row, 16 row sums, the waves' tile slots
+    hipLaunchKernelGGL((gemm_stream_kernel<kList, kVec>), dim3(n_wg), dim3(kSThreads), lds, st, single, list, first,
+                       total, n_wg, zero_off, lds - zero_off - 64 - gemm_stream_slot_bytes());
     return hipGetLastError();
 }
 
@@ -450,20 +545,22 @@ int gemm_max_wg_per_cu(int mb) {
 }
 
 int gemm_stream_max_wg_per_cu(int lds_bytes) {
+    if (allow_stream_lds() != hipSuccess) return 0;
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_stream_kernel<true, true>, kThreads, lds_bytes) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_stream_kernel<true, true>, kSThreads, lds_bytes) !=
         hipSuccess)
         return 0;
     return n;
 }
 
 hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
-                              long long total_tiles, int n_wg, int lds_bytes, bool vec, hipStream_t st) {
+                              long long total_tiles, int n_wg, int lds_bytes, int zero_off, bool vec, hipStream_t st) {
     if (list_dev)
-        return vec ? launch_stream_t<true, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st)
-                   : launch_stream_t<true, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st);
-    return vec ? launch_stream_t<false, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st)
-               : launch_stream_t<false, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st);
+        return vec ? launch_stream_t<true, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, zero_off, st)
+                   : launch_stream_t<true, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, zero_off,
+                                                  st);
+    return vec ? launch_stream_t<false, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, zero_off, st)
+               : launch_stream_t<false, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, zero_off, st);
 }
 
 int gemm_mb_of(int M) {
