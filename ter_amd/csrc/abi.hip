@@ -363,6 +363,7 @@ struct ter_hip_plan {
     bool lds = false;            // GEMM: LDS-ring kernel (M <= 128 where streaming does not apply)
     const GemmBlock* blocks_dev = nullptr;  // LDS-ring: [n_blocks] blocks, then
     const int32_t* ranges_dev = nullptr;    //   [n_wg + 1] block ranges per workgroup
+    const long long* wg_ranges_dev = nullptr;  // GEMV stream-K: [n_wg + 1] tile ranges per workgroup
     int n_blocks = 0;
     uint64_t bytes = 0, macs = 0;
 };
@@ -387,36 +388,61 @@ struct ter_hip_handle {
 };
 
 // Device copy of a plan: the descriptors, followed by the index of each
-// workgroup's first descriptor (the kernels cut `total` units into n_wg
-// ranges, range g starting at total * g / n_wg; starts[i] is descriptor i's
-// first unit, strictly increasing).
+// workgroup's first descriptor.  The kernels cut `total` units into n_wg
+// ranges, range g starting at total * g / n_wg, or at ranges[g] when a range
+// table is given (then uploaded after `first`); starts[i] is descriptor i's
+// first unit, strictly increasing.
 template <typename Desc>
 int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<long long>& starts, long long total,
-                int n_wg) {
+                int n_wg, const std::vector<long long>* ranges = nullptr) {
     std::vector<int32_t> first((size_t)n_wg);
     size_t di = 0;
     for (int g = 0; g < n_wg; ++g) {
-        const long long t = total * g / n_wg;
+        const long long t = ranges ? (*ranges)[(size_t)g] : total * g / n_wg;
         while (di + 1 < starts.size() && starts[di + 1] <= t) ++di;
         first[(size_t)g] = (int32_t)di;
     }
     const size_t db = sizeof(Desc) * ds.size();
-    hipError_t e = hipMalloc(&p->descs_dev, db + sizeof(int32_t) * (size_t)n_wg);
+    const size_t fb = (sizeof(int32_t) * (size_t)n_wg + 7) / 8 * 8;
+    const size_t rb = ranges ? sizeof(long long) * ranges->size() : 0;
+    hipError_t e = hipMalloc(&p->descs_dev, db + fb + rb);
     if (e != hipSuccess) {
         p->descs_dev = nullptr;
         return hip_fail(e, "plan descriptor allocation");
     }
-    e = hipMemcpy(p->descs_dev, ds.data(), db, hipMemcpyHostToDevice);
-    if (e == hipSuccess)
-        e = hipMemcpy(static_cast<char*>(p->descs_dev) + db, first.data(), sizeof(int32_t) * (size_t)n_wg,
-                      hipMemcpyHostToDevice);
+    char* base = static_cast<char*>(p->descs_dev);
+    e = hipMemcpy(base, ds.data(), db, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(base + db, first.data(), sizeof(int32_t) * (size_t)n_wg, hipMemcpyHostToDevice);
+    if (e == hipSuccess && ranges) e = hipMemcpy(base + db + fb, ranges->data(), rb, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         (void)hipFree(p->descs_dev);
         p->descs_dev = nullptr;
         return hip_fail(e, "plan descriptor upload");
     }
-    p->first_dev = reinterpret_cast<const int32_t*>(static_cast<const char*>(p->descs_dev) + db);
+    p->first_dev = reinterpret_cast<const int32_t*>(base + db);
+    p->wg_ranges_dev = ranges ? reinterpret_cast<const long long*>(base + db + fb) : nullptr;
     return TER_HIP_OK;
+}
+
+// Workgroup tile ranges of a stream-K GEMV plan: range g nominally starts at
+// total * g / n_wg; each interior start moves to the nearest strip edge of
+// the GEMV holding it when snap_ranges allows (common.h), so that most
+// workgroups share no strip with a neighbour.  Nondecreasing, ranges[0] = 0,
+// ranges[n_wg] = total.
+std::vector<long long> plan_ranges(const std::vector<GemvDesc>& ds, const std::vector<long long>& starts,
+                                   long long total, int n_wg) {
+    std::vector<long long> r((size_t)n_wg + 1);
+    size_t di = 0;
+    r[0] = 0;
+    r[(size_t)n_wg] = total;
+    for (int g = 1; g < n_wg; ++g) {
+        long long t = total * g / n_wg;
+        while (di + 1 < starts.size() && starts[di + 1] <= t) ++di;
+        const int Ku = ds[di].Ku;
+        if (snap_ranges(Ku, total, n_wg)) t = starts[di] + strip_edge_near(t - starts[di], Ku);
+        r[(size_t)g] = t < r[(size_t)g - 1] ? r[(size_t)g - 1] : t;
+    }
+    return r;
 }
 
 // LDS-ring GEMM (M <= 128, 16-byte aligned X): resident workgroups per
@@ -665,10 +691,10 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
     if (x->kind == TER_HIP_X_I16) return launch_x16(d, static_cast<hipStream_t>(stream));
     const long long total = (long long)d.n_strips * d.Ku;
     int n_wg = 0;
-    const int lds = d.stage32 ? gemv_lds_bytes_rms(w->K) : gemv_lds_bytes(w->K);
+    const int lds = gemv_t16_lds_bytes(w->K, d.stage32 != 0);
     rc = pick_wg(total, 0, lds, x->kind != TER_HIP_X_I8, -1, &n_wg);
     if (rc) return rc;
-    hipError_t e = launch_gemv(d, nullptr, nullptr, total, n_wg, lds, -1, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_gemv(d, nullptr, nullptr, nullptr, total, n_wg, lds, -1, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "gemv launch");
     return TER_HIP_OK;
 }
@@ -809,7 +835,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         strip_starts[(size_t)i] = strips;
         tile += (long long)ds[(size_t)i].n_strips * ds[(size_t)i].Ku;
         strips += ds[(size_t)i].n_strips;
-        const int lb = ds[(size_t)i].stage32 ? gemv_lds_bytes_rms(it.w->K) : gemv_lds_bytes(it.w->K);
+        const int lb = gemv_t16_lds_bytes(it.w->K, ds[(size_t)i].stage32 != 0);
         if (lb > lds) lds = lb;
         bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.w->K * act_bytes(it.x.kind) +
                  (uint64_t)it.w->N * out_bytes(o);
@@ -842,7 +868,12 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     }
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
-    rc = strip_mode ? upload_plan(p, ds, strip_starts, strips, n_wg) : upload_plan(p, ds, starts, tile, n_wg);
+    if (strip_mode) {
+        rc = upload_plan(p, ds, strip_starts, strips, n_wg);
+    } else {
+        const std::vector<long long> ranges = plan_ranges(ds, starts, tile, n_wg);
+        rc = upload_plan(p, ds, starts, tile, n_wg, &ranges);
+    }
     if (rc) {
         delete p;
         return rc;
@@ -882,8 +913,9 @@ int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
                                    plan->n_wg, plan->lds_bytes, plan->part_off, plan->vec_kind,
                                    static_cast<hipStream_t>(stream));
         else
-            e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev, plan->total,
-                            plan->n_wg, plan->lds_bytes, plan->vec_kind, static_cast<hipStream_t>(stream));
+            e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev,
+                            plan->wg_ranges_dev, plan->total, plan->n_wg, plan->lds_bytes, plan->vec_kind,
+                            static_cast<hipStream_t>(stream));
     }
     if (e != hipSuccess) return hip_fail(e, "plan launch");
     return TER_HIP_OK;

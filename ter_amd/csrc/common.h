@@ -94,8 +94,13 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const int32_t* first_dev
                               int lds_bytes, int part_off, int vec_kind, hipStream_t st);
 // vec_kind: the activation kind of every GEMV of a work list that qualifies
 // for the vector prologue (gemv_vec_kind), else -1.
+// ranges_dev: [n_wg + 1] tile ranges of the workgroups of a work list (range
+// g = [ranges[g], ranges[g + 1]), ends on strip edges where plan_ranges could
+// put them there); single launches pass nullptr and cut total * g / n_wg,
+// moved to the nearest strip edge under the same rule.
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const int32_t* first_dev,
-                       long long total_tiles, int n_wg, int lds_bytes, int vec_kind, hipStream_t st);
+                       const long long* ranges_dev, long long total_tiles, int n_wg, int lds_bytes, int vec_kind,
+                       hipStream_t st);
 // Single GEMV with int16 activations (gemv_x16.hip): whole strips per
 // workgroup, at most kStripModeMaxStrips of them.
 int gemv_x16_lds_bytes(int K, int strips_per_wg);
@@ -317,11 +322,36 @@ __host__ __device__ inline int gemv_lds_bytes(int32_t K) {
 // RMS activation kinds also stage the fp32 activations ([Ku*256] floats) at
 // this 16-byte aligned offset.
 __host__ __device__ inline int gemv_lds_xs32_offset(int32_t K) { return (gemv_lds_bytes(K) + 15) / 16 * 16; }
-inline int gemv_lds_bytes_rms(int32_t K) { return gemv_lds_xs32_offset(K) + units_of(K) * kUnitK * 4; }
+__host__ __device__ inline int gemv_lds_bytes_rms(int32_t K) {
+    return gemv_lds_xs32_offset(K) + units_of(K) * kUnitK * 4;
+}
+// Workgroup ranges of the stream-K GEMV kernel end at strip edges where that
+// moves them by at most a quarter of the mean range (2 Ku n_wg <= total):
+// then the strips at a workgroup's range ends are not shared with another
+// workgroup and need no global fix-up.  (Uneven ranges cost nothing here:
+// the workgroups of a launch share the HBM stream, measured flat for ranges
+// up to 3:1 apart.)  strip_edge_near: the strip edge nearest to local tile
+// `local` of a GEMV (the upper edge is within the GEMV when local is).
+__host__ __device__ inline bool snap_ranges(int Ku, long long total, int n_wg) {
+    return 2LL * Ku * n_wg <= total;
+}
+__host__ __device__ inline long long strip_edge_near(long long local, int Ku) {
+    const long long lo = local - local % Ku;
+    return local - lo <= Ku / 2 ? lo : lo + Ku;
+}
+// The stream-K kernel's slots, after the staging area, for the strips its
+// waves share: per wave its first and last strip of a segment, each as a
+// strip index, a unit count and the 16 column sums.
+constexpr int kGemvSlotInts = 2 + kStripCols;
+constexpr int kGemvSlotBytes = 2 * kGemvWaves * kGemvSlotInts * 4;
+__host__ __device__ inline int gemv_lds_slots_offset(int32_t K, bool stage32) {
+    return ((stage32 ? gemv_lds_bytes_rms(K) : gemv_lds_bytes(K)) + 15) / 16 * 16;
+}
+inline int gemv_t16_lds_bytes(int32_t K, bool stage32) { return gemv_lds_slots_offset(K, stage32) + kGemvSlotBytes; }
 // LDS of one workgroup on gfx950, and whether an RMS kind at this K stages
 // its fp32 activations (the staging costs 4 bytes per element).
 constexpr int kLdsMax = 160 * 1024;
-inline bool gemv_stage32(int32_t K) { return gemv_lds_bytes_rms(K) <= kLdsMax; }
+inline bool gemv_stage32(int32_t K) { return gemv_t16_lds_bytes(K, true) <= kLdsMax; }
 
 // Status helpers of the C-ABI (abi.hip): record the message returned by
 // ter_hip_last_error() and return `code` (TER_HIP_ERR_HIP for hip_fail).

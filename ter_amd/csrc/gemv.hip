@@ -861,11 +861,19 @@ __device__ __forceinline__ void finish_fixups(const Fixups& f) {
     if (f.col_first >= 0) part_complete(d, f.col_first, f.o_first + f.w_first, f.s);
 }
 
+// The strips of a piece not complete within it (at most its first and its
+// last), with the column sums of lanes q < 4; st = -1: none.
+struct Partials {
+    int st_first, units_first, val_first;
+    int st_last, units_last, val_last;
+};
+
 // One wave streams local tiles [la, la + n) of GEMV d; `wa` holds the first
-// batch already.  Returns the piece's fix-up adds, to be finished later.
+// batch already.  Strips complete within the piece are written; the others
+// are returned.
 template <int NB>
-__device__ __forceinline__ Fixups run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usum, float s, int la, int n,
-                            __amdgpu_buffer_rsrc_t rs, int voff, u32x4 (&wa)[NB]) {
+__device__ __forceinline__ Partials run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usum, float s, int la,
+                                              int n, __amdgpu_buffer_rsrc_t rs, int voff, u32x4 (&wa)[NB]) {
     Piece p;
     p.st = la / d.Ku;
     p.u = la - p.st * d.Ku;
@@ -887,7 +895,31 @@ __device__ __forceinline__ Fixups run_piece(const GemvDesc& d, const int8_t* lds
         i0 += NB;
         if (i0 >= n) break;
     }
-    // Strips shared with neighbouring pieces: add both partials.
+    Partials r;
+    r.st_first = p.has_first ? p.first_st : -1;
+    r.units_first = p.first_units;
+    r.val_first = p.first_val;
+    r.st_last = -1;
+    r.units_last = r.val_last = 0;
+    if (p.u != p.u_start) {
+        r.st_last = p.st;
+        r.units_last = p.u - p.u_start;
+        r.val_last = reduce_strip(p.a1, p.a4, p.corr);
+    }
+    return r;
+}
+
+// After a segment: every wave has put its Partials in the slots (slot 2 w:
+// first, 2 w + 1: last) and passed a barrier.  The first slot holding a strip
+// adds the partials of every slot holding it (integer sums, so the result is
+// the same in any order).  A strip with all Ku units is written; one that
+// also spans another workgroup's range (a range end not on a strip edge) goes
+// to the global fix-up slot with one atomic per column, whose result is
+// examined later (finish_fixups).
+__device__ __forceinline__ Fixups combine_partials(const GemvDesc& d, const int* slots, float s) {
+    const int wave = uniform(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int c = (lane >> 4) * 4 + (lane & 15);  // column within the strip of lanes q < 4
     Fixups f;
     f.o_last = f.w_last = f.o_first = f.w_first = 0;
     f.col_last = f.col_first = -1;
@@ -899,37 +931,65 @@ __device__ __forceinline__ Fixups run_piece(const GemvDesc& d, const int8_t* lds
     f.fix = d.fix;
     f.Ku = d.Ku;
     f.w_mag = d.w_mag;
-    if (p.u != p.u_start) {
-        f.w_last = part_word(p.u - p.u_start, reduce_strip(p.a1, p.a4, p.corr));
-        if (col_owner(d, p.st)) {
-            f.col_last = strip_col(p.st);
-            f.o_last = part_add(d, f.col_last, f.w_last);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int me = 2 * wave + k;
+        const int st = uniform(slots[me * kGemvSlotInts]);
+        if (st < 0) continue;
+        bool lead = true;
+        for (int j = 0; j < me; ++j) lead = lead && slots[j * kGemvSlotInts] != st;
+        if (!uniform(lead ? 1 : 0)) continue;
+        int units = 0, val = 0;
+        for (int j = me; j < 2 * kGemvWaves; ++j) {
+            const int* sl = slots + j * kGemvSlotInts;
+            if (sl[0] == st) {
+                units += sl[1];
+                val += (lane & 15) < 4 ? sl[2 + (c & 15)] : 0;
+            }
         }
-    }
-    if (p.has_first) {
-        f.w_first = part_word(p.first_units, p.first_val);
-        if (col_owner(d, p.first_st)) {
-            f.col_first = strip_col(p.first_st);
+        units = uniform(units);
+        if (!col_owner(d, st)) continue;
+        if (units == d.Ku) {
+            emit(d, strip_col(st), val, s);
+        } else if (k == 0) {
+            f.col_first = strip_col(st);
+            f.w_first = part_word(units, val);
             f.o_first = part_add(d, f.col_first, f.w_first);
+        } else {
+            f.col_last = strip_col(st);
+            f.w_last = part_word(units, val);
+            f.o_last = part_add(d, f.col_last, f.w_last);
         }
     }
     return f;
 }
 
-// kList: GEMVs come from the device table `list` (plan launches); otherwise
-// the single descriptor is a kernel argument.  Two instantiations keep the
-// descriptor in scalar registers either way.  kKind >= 0: every GEMV has that
-// activation kind and qualifies for the vector prologue; -1: any kind.
+// kList: GEMVs come from the device table `list` (plan launches) with the
+// workgroup ranges `ranges`; otherwise the single descriptor is a kernel
+// argument.  Two instantiations keep the descriptor in scalar registers
+// either way.  kKind >= 0: every GEMV has that activation kind and qualifies
+// for the vector prologue; -1: any kind.
 template <bool kList, int kKind>
 __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
                                                             const GemvDesc* __restrict__ list,
                                                             const int32_t* __restrict__ first,
+                                                            const long long* __restrict__ ranges,
                                                             long long total, int n_wg) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     int g = blockIdx.x;
     if ((n_wg & 7) == 0) g = (g & 7) * (n_wg >> 3) + (g >> 3);  // keep neighbouring ranges on one XCD
-    const long long t_begin = total * g / n_wg;
-    const long long t_end = total * (g + 1) / n_wg;
+    long long t_begin, t_end;
+    if constexpr (kList) {
+        t_begin = ranges[g];
+        t_end = ranges[g + 1];
+    } else {
+        t_begin = total * g / n_wg;
+        t_end = total * (g + 1) / n_wg;
+        if (snap_ranges(single.Ku, total, n_wg)) {
+            t_begin = strip_edge_near(t_begin, single.Ku);
+            t_end = strip_edge_near(t_end, single.Ku);
+        }
+    }
     if (t_begin >= t_end) return;
 
     int di = kList ? first[g] : 0;  // the descriptor holding tile t_begin
@@ -959,6 +1019,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
         int* usum = reinterpret_cast<int*>(lds_raw + d.Ku * kUnitK);
         float* red = reinterpret_cast<float*>(lds_raw + d.Ku * kUnitK + d.Ku * 4);
         float* xs32 = reinterpret_cast<float*>(lds_raw + gemv_lds_xs32_offset(d.K));
+        int* slots = reinterpret_cast<int*>(lds_raw + gemv_lds_slots_offset(d.K, d.stage32 != 0));
         __syncthreads();  // the previous segment is done with LDS
         float act;
         if constexpr (kKind < 0)
@@ -967,12 +1028,30 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
             act = stage_x_vec<kKind>(d, xraw, lds_x, usum, red, xs32, t == d.tile0);
         __syncthreads();
         const float s = act * d.w_scale;  // x_scale * w_scale (forward.cpp:342)
-        if (n > 0) {
-            const Fixups f = run_piece(d, lds_x, usum, s, la, n, rs, voff, wa);
-            if (have_prev) finish_fixups(prev);
-            prev = f;
-            have_prev = true;
+        Partials pr;
+        pr.st_first = pr.st_last = -1;
+        pr.units_first = pr.val_first = pr.units_last = pr.val_last = 0;
+        if (n > 0) pr = run_piece(d, lds_x, usum, s, la, n, rs, voff, wa);
+        {
+            const int lane = threadIdx.x & 63;
+            int* sl = slots + 2 * wave * kGemvSlotInts;
+            if (lane == 0) {
+                sl[0] = pr.st_first;
+                sl[1] = pr.units_first;
+                sl[kGemvSlotInts] = pr.st_last;
+                sl[kGemvSlotInts + 1] = pr.units_last;
+            }
+            if ((lane & 15) < 4) {
+                const int c = (lane >> 4) * 4 + (lane & 15);
+                sl[2 + c] = pr.val_first;
+                sl[kGemvSlotInts + 2 + c] = pr.val_last;
+            }
         }
+        __syncthreads();
+        const Fixups f = combine_partials(d, slots, s);
+        if (have_prev) finish_fixups(prev);
+        prev = f;
+        have_prev = true;
         t = seg_end;
         ++di;
     }
@@ -1121,37 +1200,38 @@ int gemv_max_wg_per_cu(int lds_bytes, int vec_kind) {
 }
 
 hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const int32_t* first_dev,
-                       long long total_tiles, int n_wg, int lds_bytes, int vec_kind, hipStream_t st) {
+                       const long long* ranges_dev, long long total_tiles, int n_wg, int lds_bytes, int vec_kind,
+                       hipStream_t st) {
     const dim3 grid(n_wg), block(kGemvThreads);
     if (!list_dev) {
         hipLaunchKernelGGL((gemv_t16_kernel<false, -1>), grid, block, lds_bytes, st, single, list_dev, first_dev,
-                           total_tiles, n_wg);
+                           ranges_dev, total_tiles, n_wg);
         return hipGetLastError();
     }
     switch (vec_kind) {
     case TER_HIP_X_I8:
         hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_I8>), grid, block, lds_bytes, st, single, list_dev,
-                           first_dev, total_tiles, n_wg);
+                           first_dev, ranges_dev, total_tiles, n_wg);
         break;
     case TER_HIP_X_F32:
         hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_F32>), grid, block, lds_bytes, st, single, list_dev,
-                           first_dev, total_tiles, n_wg);
+                           first_dev, ranges_dev, total_tiles, n_wg);
         break;
     case TER_HIP_X_F32_RMS:
         hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_F32_RMS>), grid, block, lds_bytes, st, single,
-                           list_dev, first_dev, total_tiles, n_wg);
+                           list_dev, first_dev, ranges_dev, total_tiles, n_wg);
         break;
     case TER_HIP_X_F16_RMS:
         hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_F16_RMS>), grid, block, lds_bytes, st, single,
-                           list_dev, first_dev, total_tiles, n_wg);
+                           list_dev, first_dev, ranges_dev, total_tiles, n_wg);
         break;
     case TER_HIP_X_RELU2_RMS:
         hipLaunchKernelGGL((gemv_t16_kernel<true, TER_HIP_X_RELU2_RMS>), grid, block, lds_bytes, st, single,
-                           list_dev, first_dev, total_tiles, n_wg);
+                           list_dev, first_dev, ranges_dev, total_tiles, n_wg);
         break;
     default:
         hipLaunchKernelGGL((gemv_t16_kernel<true, -1>), grid, block, lds_bytes, st, single, list_dev, first_dev,
-                           total_tiles, n_wg);
+                           ranges_dev, total_tiles, n_wg);
     }
     return hipGetLastError();
 }

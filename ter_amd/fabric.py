@@ -473,6 +473,14 @@ class Attention:
             pass
 
 
+def _held(it: dict) -> list:
+    """What a plan built from item `it` must keep alive: the device table
+    holds raw pointers into the weight buffer (as it was when the plan was
+    built) and into every tensor of the item, so none of them may be freed
+    while the plan can still be launched."""
+    return [it["w"], it["w"].buf] + [v for k, v in it.items() if k != "w" and hasattr(v, "data_ptr")]
+
+
 class Plan:
     """Many independent GEMVs in one launch (one work list).  `items` is a
     sequence of dicts: {w: PackedTrits, x: tensor, y?, acc?, y16?, resid?,
@@ -491,7 +499,7 @@ class Plan:
             arr[i].acc = _ptr(it.get("acc"))
             arr[i].y16 = _ptr(it.get("y16"))
             arr[i].resid = _ptr(it.get("resid"))
-            self._keep.append(W)
+            self._keep.extend(_held(it))
         h = C.c_void_p()
         L.check(L.lib().ter_hip_plan_create(C.byref(h), arr, n, int(wg_per_cu)), "ter_hip_plan_create")
         self._h = h
@@ -538,7 +546,7 @@ class GemmPlan:
             arr[i].acc = _ptr(it.get("acc"))
             arr[i].y16 = _ptr(it.get("y16"))
             arr[i].resid = _ptr(it.get("resid"))
-            self._keep.append(W)
+            self._keep.extend(_held(it))
         h = C.c_void_p()
         L.check(L.lib().ter_hip_gemm_plan_create(C.byref(h), arr, n, int(wg_per_cu)), "ter_hip_gemm_plan_create")
         self._h = h

@@ -363,6 +363,69 @@ def test_plan_worklist_mixed(cuda, wg_per_cu):
         assert int(host(fix).astype(np.int64).sum()) == 0
 
 
+@pytest.mark.parametrize("wg_per_cu", [1, 2])
+def test_plan_ranges_on_strip_edges(cuda, wg_per_cu):
+    """Work-list workgroup ranges: 8 GEMVs of K = 8192 (32 tiles per strip),
+    16384 tiles.  One workgroup per CU puts the range ends on strip edges
+    (mean range 64 tiles, two strips; each wave's piece of 16 tiles is half a
+    strip, so the waves' partials meet in LDS); two per CU leave them inside
+    strips (mean 32 tiles), so strips also span workgroups (global fix-up).
+    Bit-exact against the oracle on two launches in a row, slots clean."""
+    import torch
+    import ter_amd as T
+    K, N = 8192, 1024
+    items, refs = [], []
+    for i in range(8):
+        v11 = O.v11_pack(O.rand_trits(900 + i, K, N))
+        W = T.PackedTrits.from_v11(v11, K, N, 0.02 * (i + 1))
+        x = O.rand_int8(950 + i, K)
+        acc = torch.empty(N, dtype=torch.int32, device="cuda")
+        y = torch.empty(N, dtype=torch.float32, device="cuda")
+        items.append(dict(w=W, x=dev(x), x_scale=0.25, y=y, acc=acc))
+        refs.append(O.gemv_v11(x, 0.25, v11, 0.02 * (i + 1), K, N))
+    plan = T.Plan(items, wg_per_cu=wg_per_cu)
+    for rep in range(2):
+        for it in items:
+            it["acc"].fill_(-7)
+            it["y"].fill_(-7)
+        plan.launch()
+        for it, (ra, ry) in zip(items, refs):
+            assert (host(it["acc"]) == ra).all(), (rep, wg_per_cu)
+            assert_f32_equal(host(it["y"]), ry)
+    for it in items:
+        fix = it["w"].buf[it["w"].buf.numel() - 8 * N:]
+        assert int(host(fix).astype(np.int64).sum()) == 0
+
+
+def test_single_gemv_ranges_on_strip_edges(cuda):
+    """A single GEMV large enough that its workgroup ranges move to strip
+    edges inside the kernel (K = 2048, N = 65536: 32768 tiles)."""
+    gemv_case(2048, 65536, seed=4242)
+
+
+def test_plan_keeps_its_tensors_alive(cuda):
+    """A plan holds every tensor whose address it copied: outputs passed as
+    temporaries stay allocated and receive the results."""
+    import gc
+    import weakref
+    import torch
+    import ter_amd as T
+    K, N = 2048, 512
+    v11 = O.v11_pack(O.rand_trits(77, K, N))
+    x = O.rand_int8(78, K)
+    W = T.PackedTrits.from_v11(v11, K, N, 0.5)
+    plan = T.Plan([dict(w=W, x=dev(x), x_scale=1.0, acc=torch.empty(N, dtype=torch.int32, device="cuda"))])
+    refs = [weakref.ref(t) for t in plan._keep if isinstance(t, torch.Tensor)]
+    del W
+    gc.collect()
+    torch.cuda.empty_cache()
+    assert all(r() is not None for r in refs)
+    plan.launch()
+    acc = [t for t in plan._keep if isinstance(t, torch.Tensor) and t.dtype == torch.int32][0]
+    ra, _ = O.gemv_v11(x, 1.0, v11, 0.5, K, N)
+    assert (host(acc) == ra).all()
+
+
 def test_handle_native_slot_counts(cuda):
     import torch
     import ter_amd as T
