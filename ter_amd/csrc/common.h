@@ -347,7 +347,14 @@ constexpr int kGemvSlotBytes = 2 * kGemvWaves * kGemvSlotInts * 4;
 __host__ __device__ inline int gemv_lds_slots_offset(int32_t K, bool stage32) {
     return ((stage32 ? gemv_lds_bytes_rms(K) : gemv_lds_bytes(K)) + 15) / 16 * 16;
 }
-inline int gemv_t16_lds_bytes(int32_t K, bool stage32) { return gemv_lds_slots_offset(K, stage32) + kGemvSlotBytes; }
+// Then per wave the column sums of the first kGemvOutStrips strips completed
+// within its piece (consecutive strips), written after its streaming loop so
+// that no store is issued among the weight loads.
+constexpr int kGemvOutStrips = 16;
+constexpr int kGemvOutBytes = kGemvWaves * kGemvOutStrips * kStripCols * 4;
+inline int gemv_t16_lds_bytes(int32_t K, bool stage32) {
+    return gemv_lds_slots_offset(K, stage32) + kGemvSlotBytes + kGemvOutBytes;
+}
 // LDS of one workgroup on gfx950, and whether an RMS kind at this K stages
 // its fp32 activations (the staging costs 4 bytes per element).
 constexpr int kLdsMax = 160 * 1024;

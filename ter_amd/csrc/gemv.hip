@@ -798,14 +798,16 @@ struct Piece {
     int st, u, u_start, corr;
     int first_val, first_units, first_st;  // the leading partial strip, combined after the loop
     bool has_first;
+    int nout;  // strips completed within the piece so far
     int a1[4], a4[4];
 };
 
 // Reduce tiles [i0, min(i0 + NB, n)) of the piece from registers `w`.
 template <int NB>
 __device__ __forceinline__ void compute_batch(const GemvDesc& d, const u32x4 (&w)[NB], int i0, int n,
-                                              const int8_t* lds_x, const int* usum, float s, Piece& p) {
+                                              const int8_t* lds_x, const int* usum, float s, Piece& p, int* obuf) {
     const int q = threadIdx.x & 15;
+    const int c = (threadIdx.x & 63) >> 4 << 2 | q;  // column within the strip of lanes q < 4
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
         if (i0 + i < n) {
@@ -816,7 +818,8 @@ __device__ __forceinline__ void compute_batch(const GemvDesc& d, const u32x4 (&w
             if (p.u == d.Ku) {
                 const int val = reduce_strip(p.a1, p.a4, p.corr);
                 if (p.u_start == 0) {
-                    if (col_owner(d, p.st)) emit(d, strip_col(p.st), val, s);
+                    if (q < 4) obuf[p.nout * kStripCols + c] = val;  // fewer than kGemvOutStrips per chunk
+                    ++p.nout;
                 } else {
                     p.first_val = val;
                     p.first_units = p.u - p.u_start;
@@ -873,7 +876,7 @@ struct Partials {
 // are returned.
 template <int NB>
 __device__ __forceinline__ Partials run_piece(const GemvDesc& d, const int8_t* lds_x, const int* usum, float s, int la,
-                                              int n, __amdgpu_buffer_rsrc_t rs, int voff, u32x4 (&wa)[NB]) {
+                                              int n, __amdgpu_buffer_rsrc_t rs, int voff, u32x4 (&wa)[NB], int* obuf) {
     Piece p;
     p.st = la / d.Ku;
     p.u = la - p.st * d.Ku;
@@ -881,19 +884,47 @@ __device__ __forceinline__ Partials run_piece(const GemvDesc& d, const int8_t* l
     p.corr = 0;
     p.first_val = p.first_units = p.first_st = 0;
     p.has_first = false;
+    p.nout = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) p.a1[j] = p.a4[j] = 0;
+    // The piece streams in chunks of C tiles, a whole number of double
+    // batches and at most 15 Ku, so that a chunk completes at most 15 strips
+    // (buffered in obuf); their outputs are written between chunks, and the
+    // streaming loop itself issues no memory operation but the weight loads
+    // (a store or another load among them makes the compiler drain every
+    // load at the loop head).  The next chunk's first batch is in flight
+    // meanwhile.
+    const int C = 2 * NB * max(1, (kGemvOutStrips - 1) * d.Ku / (2 * NB));
+    int st_full = p.u == 0 ? p.st : p.st + 1;  // strip of the next buffered completion
     u32x4 wb[NB];
     int i0 = 0;
     while (true) {
-        load_batch(wb, rs, voff, i0 + NB);
-        compute_batch(d, wa, i0, n, lds_x, usum, s, p);
-        i0 += NB;
+        const int cend = min(n, i0 + C);
+        while (true) {
+            load_batch(wb, rs, voff, i0 + NB);
+            compute_batch(d, wa, i0, n, lds_x, usum, s, p, obuf);
+            i0 += NB;
+            if (i0 >= cend) break;  // only at the piece's end (cend < n is a whole double batch)
+            load_batch(wa, rs, voff, i0 + NB);
+            compute_batch(d, wb, i0, n, lds_x, usum, s, p, obuf);
+            i0 += NB;
+            if (i0 >= cend) break;
+        }
+        // the chunk's completed strips, four per store across the wave's 64
+        // lanes (256 contiguous output bytes); a wave reads back only its own
+        // LDS writes
+        for (int j0 = 0; j0 < p.nout; j0 += 4) {
+            const int j = j0 + ((threadIdx.x & 63) >> 4);
+            const int col = (st_full + j) * kStripCols + (threadIdx.x & 15);
+            if (j < p.nout && col < d.N) emit(d, col, obuf[j * kStripCols + (threadIdx.x & 15)], s);
+        }
+        p.nout = 0;
+        st_full = p.u_start != 0 ? p.st + 1 : p.st;
         if (i0 >= n) break;
-        load_batch(wa, rs, voff, i0 + NB);
-        compute_batch(d, wb, i0, n, lds_x, usum, s, p);
-        i0 += NB;
-        if (i0 >= n) break;
+        // Another chunk: let the outputs (and a residual's read) complete
+        // first, so the streaming loop never starts with them pending (the
+        // compiler would then drain all loads at every loop head).
+        __builtin_amdgcn_s_waitcnt(0);
     }
     Partials r;
     r.st_first = p.has_first ? p.first_st : -1;
@@ -1020,6 +1051,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
         float* red = reinterpret_cast<float*>(lds_raw + d.Ku * kUnitK + d.Ku * 4);
         float* xs32 = reinterpret_cast<float*>(lds_raw + gemv_lds_xs32_offset(d.K));
         int* slots = reinterpret_cast<int*>(lds_raw + gemv_lds_slots_offset(d.K, d.stage32 != 0));
+        int* obuf = reinterpret_cast<int*>(lds_raw + gemv_lds_slots_offset(d.K, d.stage32 != 0) + kGemvSlotBytes) +
+                    wave * kGemvOutStrips * kStripCols;
         __syncthreads();  // the previous segment is done with LDS
         float act;
         if constexpr (kKind < 0)
@@ -1031,7 +1064,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
         Partials pr;
         pr.st_first = pr.st_last = -1;
         pr.units_first = pr.val_first = pr.units_last = pr.val_last = 0;
-        if (n > 0) pr = run_piece(d, lds_x, usum, s, la, n, rs, voff, wa);
+        if (n > 0) pr = run_piece(d, lds_x, usum, s, la, n, rs, voff, wa, obuf);
         {
             const int lane = threadIdx.x & 63;
             int* sl = slots + 2 * wave * kGemvSlotInts;
