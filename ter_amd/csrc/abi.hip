@@ -811,7 +811,8 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     std::vector<long long> starts((size_t)n), strip_starts((size_t)n);
     long long tile = 0, strips = 0;
     uint64_t bytes = 0, macs = 0;
-    int lds = 0;
+    int lds = 0;        // the stream-K kernel's (staging, slots and output buffers)
+    int lds_stage = 0;  // the staging area, all the strip-mode kernel needs beside its partial sums
     Ranges resid, inputs;
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemv_item_t& it = items[i];
@@ -837,6 +838,8 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         strips += ds[(size_t)i].n_strips;
         const int lb = gemv_t16_lds_bytes(it.w->K, ds[(size_t)i].stage32 != 0);
         if (lb > lds) lds = lb;
+        const int ls = gemv_lds_slots_offset(it.w->K, ds[(size_t)i].stage32 != 0);  // the staging area alone
+        if (ls > lds_stage) lds_stage = ls;
         bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.w->K * act_bytes(it.x.kind) +
                  (uint64_t)it.w->N * out_bytes(o);
         macs += (uint64_t)it.w->K * (uint64_t)it.w->N;
@@ -854,7 +857,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         if (rc) return rc;
     }
     if (strip_mode) {
-        part_off = (lds + 15) / 16 * 16;
+        part_off = (lds_stage + 15) / 16 * 16;
         const long long per_wg = (strips + n_wg - 1) / n_wg;
         const int lds_strip = part_off + (int)per_wg * kGemvWaves * kStripCols * 4;
         if (gemv_max_wg_per_cu(lds_strip) > 0)

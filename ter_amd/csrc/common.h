@@ -332,8 +332,17 @@ __host__ __device__ inline int gemv_lds_bytes_rms(int32_t K) {
 // the workgroups of a launch share the HBM stream, measured flat for ranges
 // up to 3:1 apart.)  strip_edge_near: the strip edge nearest to local tile
 // `local` of a GEMV (the upper edge is within the GEMV when local is).
+// Both apply to launches whose waves stream at least kCombineMinTiles tiles
+// each (combine_mode); for smaller pieces the workgroup barrier and the range
+// imbalance cost more than the atomics, and each wave adds its partial strips
+// to the global slots itself (decode-step lists: 34 tiles per workgroup,
+// 7.55 against 8.17 us per launch).
+constexpr long long kCombineMinTiles = 32;
+__host__ __device__ inline bool combine_mode(long long total, int n_wg) {
+    return total >= (long long)n_wg * kGemvWaves * kCombineMinTiles;
+}
 __host__ __device__ inline bool snap_ranges(int Ku, long long total, int n_wg) {
-    return 2LL * Ku * n_wg <= total;
+    return combine_mode(total, n_wg) && 2LL * Ku * n_wg <= total;
 }
 __host__ __device__ inline long long strip_edge_near(long long local, int Ku) {
     const long long lo = local - local % Ku;

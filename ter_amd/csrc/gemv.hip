@@ -947,10 +947,7 @@ __device__ __forceinline__ Partials run_piece(const GemvDesc& d, const int8_t* l
 // also spans another workgroup's range (a range end not on a strip edge) goes
 // to the global fix-up slot with one atomic per column, whose result is
 // examined later (finish_fixups).
-__device__ __forceinline__ Fixups combine_partials(const GemvDesc& d, const int* slots, float s) {
-    const int wave = uniform(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int c = (lane >> 4) * 4 + (lane & 15);  // column within the strip of lanes q < 4
+__device__ __forceinline__ Fixups no_fixups(const GemvDesc& d, float s) {
     Fixups f;
     f.o_last = f.w_last = f.o_first = f.w_first = 0;
     f.col_last = f.col_first = -1;
@@ -962,6 +959,31 @@ __device__ __forceinline__ Fixups combine_partials(const GemvDesc& d, const int*
     f.fix = d.fix;
     f.Ku = d.Ku;
     f.w_mag = d.w_mag;
+    return f;
+}
+
+// Small pieces (no combine_mode): the wave adds its own partial strips to the
+// global fix-up slots.
+__device__ __forceinline__ Fixups partials_to_slots(const GemvDesc& d, const Partials& pr, float s) {
+    Fixups f = no_fixups(d, s);
+    if (pr.st_first >= 0 && col_owner(d, pr.st_first)) {
+        f.col_first = strip_col(pr.st_first);
+        f.w_first = part_word(pr.units_first, pr.val_first);
+        f.o_first = part_add(d, f.col_first, f.w_first);
+    }
+    if (pr.st_last >= 0 && col_owner(d, pr.st_last)) {
+        f.col_last = strip_col(pr.st_last);
+        f.w_last = part_word(pr.units_last, pr.val_last);
+        f.o_last = part_add(d, f.col_last, f.w_last);
+    }
+    return f;
+}
+
+__device__ __forceinline__ Fixups combine_partials(const GemvDesc& d, const int* slots, float s) {
+    const int wave = uniform(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int c = (lane >> 4) * 4 + (lane & 15);  // column within the strip of lanes q < 4
+    Fixups f = no_fixups(d, s);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int me = 2 * wave + k;
@@ -1010,7 +1032,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
     int g = blockIdx.x;
     if ((n_wg & 7) == 0) g = (g & 7) * (n_wg >> 3) + (g >> 3);  // keep neighbouring ranges on one XCD
     long long t_begin, t_end;
+    int di = 0;  // the descriptor holding tile t_begin
     if constexpr (kList) {
+        // all three loads issued together, ahead of the range test
+        di = first[g];
         t_begin = ranges[g];
         t_end = ranges[g + 1];
     } else {
@@ -1021,9 +1046,12 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
             t_end = strip_edge_near(t_end, single.Ku);
         }
     }
-    if (t_begin >= t_end) return;
+    // (di < 0, a null list and total < 0 never happen: they keep first[g]
+    // among the loads above and the list pointer and total in the first
+    // round of argument loads, so the descriptor is the third round)
+    if (t_begin >= t_end || di < 0 || (kList && list == nullptr) || total < 0) return;
 
-    int di = kList ? first[g] : 0;  // the descriptor holding tile t_begin
+    const bool combine = combine_mode(total, n_wg);  // the waves' partial strips meet in LDS
     const int wave = uniform(threadIdx.x >> 6);
     const int voff = (threadIdx.x & 63) * 16;
     long long t = t_begin;
@@ -1065,7 +1093,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
         pr.st_first = pr.st_last = -1;
         pr.units_first = pr.val_first = pr.units_last = pr.val_last = 0;
         if (n > 0) pr = run_piece(d, lds_x, usum, s, la, n, rs, voff, wa, obuf);
-        {
+        Fixups f;
+        if (!combine) {
+            f = partials_to_slots(d, pr, s);
+        } else {
             const int lane = threadIdx.x & 63;
             int* sl = slots + 2 * wave * kGemvSlotInts;
             if (lane == 0) {
@@ -1079,9 +1110,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
                 sl[2 + c] = pr.val_first;
                 sl[kGemvSlotInts + 2 + c] = pr.val_last;
             }
+            __syncthreads();
+            f = combine_partials(d, slots, s);
         }
-        __syncthreads();
-        const Fixups f = combine_partials(d, slots, s);
         if (have_prev) finish_fixups(prev);
         prev = f;
         have_prev = true;

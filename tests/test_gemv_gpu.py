@@ -363,19 +363,19 @@ def test_plan_worklist_mixed(cuda, wg_per_cu):
         assert int(host(fix).astype(np.int64).sum()) == 0
 
 
-@pytest.mark.parametrize("wg_per_cu", [1, 2])
-def test_plan_ranges_on_strip_edges(cuda, wg_per_cu):
-    """Work-list workgroup ranges: 8 GEMVs of K = 8192 (32 tiles per strip),
-    16384 tiles.  One workgroup per CU puts the range ends on strip edges
-    (mean range 64 tiles, two strips; each wave's piece of 16 tiles is half a
-    strip, so the waves' partials meet in LDS); two per CU leave them inside
-    strips (mean 32 tiles), so strips also span workgroups (global fix-up).
-    Bit-exact against the oracle on two launches in a row, slots clean."""
+@pytest.mark.parametrize("K,N,count,wg_per_cu", [
+    (6912, 1024, 20, 1),   # 34560 tiles / 256 workgroups: ranges on strip edges, waves' partials meet in LDS
+    (20480, 496, 16, 1),   # 80-tile strips: too long to move range ends (LDS + global fix-up at range ends)
+    (6912, 1024, 20, 2),   # 17 tiles per wave: each wave adds its partial strips to the global slots
+])
+def test_plan_partitions(cuda, K, N, count, wg_per_cu):
+    """The three ways a work list's strips are completed (combine_mode and
+    snap_ranges): bit-exact against the oracle on two launches in a row, and
+    the global fix-up slots clean afterwards."""
     import torch
     import ter_amd as T
-    K, N = 8192, 1024
     items, refs = [], []
-    for i in range(8):
+    for i in range(count):
         v11 = O.v11_pack(O.rand_trits(900 + i, K, N))
         W = T.PackedTrits.from_v11(v11, K, N, 0.02 * (i + 1))
         x = O.rand_int8(950 + i, K)
@@ -390,7 +390,7 @@ def test_plan_ranges_on_strip_edges(cuda, wg_per_cu):
             it["y"].fill_(-7)
         plan.launch()
         for it, (ra, ry) in zip(items, refs):
-            assert (host(it["acc"]) == ra).all(), (rep, wg_per_cu)
+            assert (host(it["acc"]) == ra).all(), (rep, K, N, wg_per_cu)
             assert_f32_equal(host(it["y"]), ry)
     for it in items:
         fix = it["w"].buf[it["w"].buf.numel() - 8 * N:]
@@ -399,8 +399,9 @@ def test_plan_ranges_on_strip_edges(cuda, wg_per_cu):
 
 def test_single_gemv_ranges_on_strip_edges(cuda):
     """A single GEMV large enough that its workgroup ranges move to strip
-    edges inside the kernel (K = 2048, N = 65536: 32768 tiles)."""
-    gemv_case(2048, 65536, seed=4242)
+    edges inside the kernel (K = 2048, N = 262144: 131072 tiles, 32 per wave
+    at 1024 workgroups)."""
+    gemv_case(2048, 262144, seed=4242)
 
 
 def test_plan_keeps_its_tensors_alive(cuda):
