@@ -359,7 +359,7 @@ struct ter_hip_plan {
     int mb = 0;                  // GEMM row-block count
     bool vec = false;            // GEMM: 16-byte X rows
     bool stream = false;         // GEMM: streaming kernel (M <= 16), total counts tiles
-    int zero_off = 0;            // GEMM streaming kernel: LDS offset of its zero row
+
     bool lds = false;            // GEMM: LDS-ring kernel (M <= 128 where streaming does not apply)
     const GemmBlock* blocks_dev = nullptr;  // LDS-ring: [n_blocks] blocks, then
     const int32_t* ranges_dev = nullptr;    //   [n_wg + 1] block ranges per workgroup
@@ -904,7 +904,7 @@ int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
     } else if (plan->gemm && plan->stream) {
         GemmDesc none{};
         e = launch_gemm_stream(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->first_dev, plan->total,
-                               plan->n_wg, plan->lds_bytes, plan->zero_off, plan->vec, static_cast<hipStream_t>(stream));
+                               plan->n_wg, plan->lds_bytes, plan->vec, static_cast<hipStream_t>(stream));
     } else if (plan->gemm) {
         GemmDesc none{};
         e = launch_gemm_list(none, static_cast<const GemmDesc*>(plan->descs_dev), plan->first_dev, plan->total,
@@ -1035,13 +1035,13 @@ static int gemm_out_ws(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M
     const GemmDesc d = make_gemm_desc(w, xq, xs, M, *out, 0, kWaves * gemm_strips_per_wave(mb), 0);
     int n_wg = 0;
     hipError_t e;
-    const int slds = gemm_stream_lds_bytes(M, w->K);
+    const int slds = gemm_stream_lds_want(M, w->K);
     const int lbs = gemm_vec_ok(d) ? gemm_lds_strips_per_block(mb) : 0;
-    if (gemm_stream_fits(M, w->K)) {
+    if (gemm_stream_item_fits(M, w->K, slds)) {
         const long long tiles = (long long)d.n_strips * d.Ku;
         rc = pick_stream_wg(tiles, slds, 0, &n_wg);
         if (rc) return rc;
-        e = launch_gemm_stream(d, nullptr, nullptr, tiles, n_wg, slds, gemm_stream_zero_off(M, w->K), gemm_vec_ok(d), st);
+        e = launch_gemm_stream(d, nullptr, nullptr, tiles, n_wg, slds, gemm_vec_ok(d), st);
     } else if (lbs > 0) {
         const int nb = (d.n_strips + lbs - 1) / lbs;
         rc = pick_lds_wg(nb, mb, &n_wg);
@@ -1115,7 +1115,6 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     const int mb = gemm_mb_of(std::min(max_m, rows));  // one row-block count (and block width) per launch
     const int per_block = kWaves * gemm_strips_per_wave(mb);
     long long tiles = 0;
-    int max_k = 1;
     ds.clear();
     std::vector<long long> block_starts, tile_starts;
     for (int i = 0; i < n; ++i) {
@@ -1132,15 +1131,16 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
             tiles += (long long)d.n_strips * d.Ku;
             vec = vec && gemm_vec_ok(d);
         }
-        if (it.w->K > max_k) max_k = it.w->K;
         bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.M * it.w->K +
                  (uint64_t)it.M * it.w->N * out_bytes(o);
         macs += (uint64_t)it.M * (uint64_t)it.w->K * (uint64_t)it.w->N;
     }
     n = (int)ds.size();
     int n_wg = 0;
-    const int slds = gemm_stream_lds_bytes(max_m, max_k);
-    const bool stream = gemm_stream_fits(max_m, max_k);
+    int slds = 0;  // the streaming kernel's LDS: the most any item wants
+    for (int i = 0; i < n; ++i) slds = std::max(slds, gemm_stream_lds_want(ds[(size_t)i].M, ds[(size_t)i].K));
+    bool stream = true;
+    for (int i = 0; i < n && stream; ++i) stream = gemm_stream_item_fits(ds[(size_t)i].M, ds[(size_t)i].K, slds);
     const int lbs = !stream && vec ? gemm_lds_strips_per_block(mb) : 0;
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
@@ -1173,7 +1173,7 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     p->stream = stream;
     p->total = stream ? tiles : blocks;
     p->lds_bytes = stream ? slds : 0;
-    p->zero_off = stream ? gemm_stream_zero_off(max_m, max_k) : 0;
+
     p->n_wg = n_wg;
     p->mb = mb;
     p->vec = vec;

@@ -161,23 +161,49 @@ int gemm_mb_of(int M);
 hipError_t launch_gemm_list(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
                             long long total_blocks, int n_wg, int mb, bool vec, hipStream_t st);
 // Streaming GEMM for M <= 16 (whole X of a GEMM staged in LDS, whole strips
-// per wave, no per-unit barrier).  LDS (for the plan's widest M and K): the X
-// image, M rows of Ku * 16 chunks + one padding chunk each (16 bytes per
-// chunk), at [0, gemm_stream_zero_off); a zero row of Ku * 256 bytes; 16 row
-// sums; the waves' tile slots.
-inline int gemm_stream_zero_off(int M, int K) { return M * (units_of(K) * (kUnitK / 16) + 1) * 16; }
-// Each of the workgroup's 4 waves turns its tiles into MFMA operand order through two 1 KiB slots.
+// per wave, no per-unit barrier).  Each GEMM segment lays out the launch's
+// LDS for its own M and K: the X image, M rows of Ku * 16 chunks + one
+// padding chunk each (16 bytes per chunk), at [0, gemm_stream_zero_off); a
+// zero row of Ku * 256 bytes; 16 row sums; the waves' tile slots (each of the
+// 4 waves turns its tiles into MFMA operand order through two 1 KiB slots);
+// 16 row scales; then each wave's output buffer, as many whole strips as the
+// rest of the launch's LDS holds (up to kGemmStreamOutMax): the int32 results
+// of completed strips (M rows x 16 columns), written out between chunks of
+// the wave's tiles, so that no store is issued among the weight loads.  A
+// GEMM's X at K = 2560 leaves room for a whole run of strips (one write-out
+// per run); the stores cost about 10 us at M = 8 on the BitNet sweep
+// wherever they go, and 6 us more when split over five write-outs per run.
+__host__ __device__ inline int gemm_stream_zero_off(int M, int K) { return M * (units_of(K) * (kUnitK / 16) + 1) * 16; }
 constexpr int gemm_stream_slot_bytes() { return 4 * 2 * kTileBytes; }
-inline int gemm_stream_lds_bytes(int M, int K) {
-    return gemm_stream_zero_off(M, K) + units_of(K) * kUnitK + 64 + gemm_stream_slot_bytes();
+__host__ __device__ inline int gemm_stream_out_off(int M, int K) {
+    return gemm_stream_zero_off(M, K) + units_of(K) * kUnitK + 64 + gemm_stream_slot_bytes() + 64;
 }
 constexpr int kGemmStreamXMax = 64 * 1024;   // the X image (its staging registers hold 64 KiB)
 constexpr int kGemmStreamLdsMax = 80 * 1024; // in all: two workgroups per CU
-inline bool gemm_stream_fits(int M, int K) {
-    return M <= 16 && gemm_stream_zero_off(M, K) <= kGemmStreamXMax && gemm_stream_lds_bytes(M, K) <= kGemmStreamLdsMax;
+constexpr int kGemmStreamBatch = 6;          // tiles per batch (two batches per wave in flight)
+constexpr int kGemmStreamOutMax = 32;        // strips per output buffer at most
+// Strips of each wave's output buffer for a segment of this M and K in `lds` bytes.
+__host__ __device__ inline int gemm_stream_out_strips(int M, int K, int lds) {
+    const int left = lds - gemm_stream_out_off(M, K);
+    const int s = left > 0 ? left / (4 * M * kStripCols * 4) : 0;
+    return s < kGemmStreamOutMax ? s : kGemmStreamOutMax;
 }
+// A chunk is at least one double batch and completes at most
+// floor(chunk / Ku) + 1 strips, so a buffer needs floor(2 batch / Ku) + 1.
+__host__ __device__ inline int gemm_stream_out_need(int Ku) { return 2 * kGemmStreamBatch / Ku + 1; }
+// The LDS a GEMM of this M and K would take (full buffers), capped.
+inline int gemm_stream_lds_want(int M, int K) {
+    const int w = gemm_stream_out_off(M, K) + 4 * kGemmStreamOutMax * M * kStripCols * 4;
+    return w < kGemmStreamLdsMax ? w : kGemmStreamLdsMax;
+}
+// Whether a GEMM of this M and K streams in a launch of `lds` bytes.
+inline bool gemm_stream_item_fits(int M, int K, int lds) {
+    return M <= 16 && gemm_stream_zero_off(M, K) <= kGemmStreamXMax &&
+           gemm_stream_out_strips(M, K, lds) >= gemm_stream_out_need(units_of(K));
+}
+// lds_bytes: the launch's LDS (the largest gemm_stream_lds_want of the list).
 hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
-                              long long total_tiles, int n_wg, int lds_bytes, int zero_off, bool vec, hipStream_t st);
+                              long long total_tiles, int n_wg, int lds_bytes, bool vec, hipStream_t st);
 int gemm_stream_max_wg_per_cu(int lds_bytes);
 
 // Resident GEMM workgroups per CU for row-block count mb (0 if the query fails).

@@ -271,7 +271,7 @@ __global__ __launch_bounds__(kThreads) void gemm_t16_kernel(GemmDesc single, con
 constexpr int kSWaves = 4;                  // waves per workgroup (all sharing one X image)
 constexpr int kSThreads = 64 * kSWaves;
 constexpr int kStageChunks = 65536 / 16 / kSThreads;  // chunks per thread: the 64 KiB LDS limit
-constexpr int kSBatch = 6;                  // tiles per batch, two batches per wave in flight
+constexpr int kSBatch = kGemmStreamBatch;   // tiles per batch, two batches per wave in flight
 
 // Chunks of one staged row (Ku * 16) plus its padding chunk.
 __device__ __forceinline__ int stream_row_chunks(int Ku) { return Ku * (kUnitK / 16) + 1; }
@@ -337,6 +337,7 @@ __device__ __forceinline__ void stream_load(u32x4 (&w)[NB], __amdgpu_buffer_rsrc
 
 struct StreamState {
     int strip, u;
+    int nbuf;  // completed strips in the wave's output buffer
     i32x4 C;
 };
 
@@ -348,8 +349,8 @@ struct StreamState {
 // while tile i is read back never overtakes the reads of tile i - 1.
 template <int NB>
 __device__ __forceinline__ void stream_compute(const GemmDesc& d, const u32x4 (&w)[NB], int i0, int n,
-                                               const int8_t* arow, unsigned char* slot, int st_base,
-                                               const int (&rs)[4], const float (&xsr)[4], StreamState& p) {
+                                               const int8_t* arow, unsigned char* slot, int* obuf, int out_rows,
+                                               const int (&rs)[4], StreamState& p) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
@@ -370,17 +371,17 @@ __device__ __forceinline__ void stream_compute(const GemmDesc& d, const u32x4 (&
                 p.C = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, p.C, 0, 0, 0);
             }
             if (++p.u == d.Ku) {
-                const int col = (st_base + p.strip) * kStripCols + j;
-                if (col < d.N) {
+                // the strip's results into the output buffer (rows of 16 columns)
+                int* ob = obuf + p.nbuf * out_rows * kStripCols;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int row = g * 4 + e;
-                        if (row < d.M) emit_out(d, (long long)row * d.N + col, p.C[e] - rs[e], xsr[e]);
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    const int row = g * 4 + e;
+                    if (row < d.M) ob[row * kStripCols + j] = p.C[e] - rs[e];
                 }
                 p.C = i32x4{0, 0, 0, 0};
                 p.u = 0;
                 ++p.strip;
+                ++p.nbuf;
             }
         }
     }
@@ -389,11 +390,8 @@ __device__ __forceinline__ void stream_compute(const GemmDesc& d, const u32x4 (&
 template <bool kList, bool kVec>
 __global__ __launch_bounds__(kSThreads) void gemm_stream_kernel(GemmDesc single, const GemmDesc* __restrict__ list,
                                                                const int32_t* __restrict__ first, long long total,
-                                                               int n_wg, int zero_off, int zero_bytes) {
+                                                               int n_wg, int lds_bytes) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    // the zero row (Ku * 256 bytes of the widest GEMM) after the X images
-    for (int c = threadIdx.x; c < zero_bytes / 16; c += kSThreads)
-        *reinterpret_cast<u32x4*>(lds_raw + zero_off + c * 16) = u32x4{0u, 0u, 0u, 0u};
     int gi = blockIdx.x;
     if ((n_wg & 7) == 0) gi = (gi & 7) * (n_wg >> 3) + (gi >> 3);
     const long long t_begin = total * gi / n_wg;
@@ -403,7 +401,6 @@ __global__ __launch_bounds__(kSThreads) void gemm_stream_kernel(GemmDesc single,
     const int lane = threadIdx.x & 63;
     const int wave = uniform(threadIdx.x >> 6);
     const int g = lane >> 4, j = lane & 15;
-    unsigned char* slot = lds_raw + zero_off + zero_bytes + 64 + wave * 2 * kTileBytes;  // this wave's 2 tiles
     long long t = t_begin;
     while (t < t_end) {
         const GemmDesc d = kList ? list[di] : single;
@@ -418,31 +415,44 @@ __global__ __launch_bounds__(kSThreads) void gemm_stream_kernel(GemmDesc single,
             (void*)(d.w + (long long)w_a * d.Ku * kTileBytes), 0, n * kTileBytes, 0x00020000);
         const int rc = stream_row_chunks(d.Ku);
         unsigned char* lx = lds_raw;
+        // this segment's LDS layout (common.h, gemm_stream_out_off)
+        const int zero_off = gemm_stream_zero_off(d.M, d.K);
+        const int out_off = gemm_stream_out_off(d.M, d.K);
+        const int out_strips = gemm_stream_out_strips(d.M, d.K, lds_bytes);
+        unsigned char* slot = lds_raw + zero_off + d.Ku * kUnitK + 64 + wave * 2 * kTileBytes;  // this wave's 2 tiles
+        int* obuf = reinterpret_cast<int*>(lds_raw + out_off) + wave * out_strips * d.M * kStripCols;
         // rows 4g .. 4g + 3's scales in one load, rows past M reading zeros
         const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc((void*)d.xs, 0, d.M * 4, 0x00020000);
         const u32x4 xsw = __builtin_amdgcn_raw_buffer_load_b128(sr, g * 16, 0, 0);
         u32x4 wa[kSBatch], wb[kSBatch];
-        int* rsum = reinterpret_cast<int*>(lds_raw + zero_off + zero_bytes);
+        int* rsum = reinterpret_cast<int*>(lds_raw + zero_off + d.Ku * kUnitK);
+        // the zero row read by the A operands of rows >= M, and the row sums
+        auto clear = [&]() {
+            for (int c = threadIdx.x; c < d.Ku * (kUnitK / 16); c += kSThreads)
+                *reinterpret_cast<u32x4*>(lds_raw + zero_off + c * 16) = u32x4{0u, 0u, 0u, 0u};
+            if (threadIdx.x < 16) rsum[threadIdx.x] = 0;
+        };
         if constexpr (kVec) {
             XStage xst;
             stage_load(d, xst);           // X first: its writes below wait for nothing else
             stream_load(wa, rs, 0);
             __syncthreads();              // the previous segment is done with LDS
-            if (threadIdx.x < 16) rsum[threadIdx.x] = 0;
+            clear();
             __syncthreads();
             if (ns > 0) stage_store(d, xst, reinterpret_cast<int8_t*>(lx), rsum);
         } else {
             stream_load(wa, rs, 0);
             __syncthreads();
-            if (threadIdx.x < 16) rsum[threadIdx.x] = 0;
+            clear();
             __syncthreads();
             if (ns > 0) stage_rows_bytes(d, reinterpret_cast<int8_t*>(lx), rsum);
         }
-        float xsr[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const unsigned b = xsw[e];  // (bit_cast of the element lvalue itself reads element 0)
-            xsr[e] = __builtin_bit_cast(float, b) * d.w_scale;
+        // the rows' output scales x_scale[r] * w_scale for the flushes: lane
+        // 16 g + e of wave 0 writes row 4 g + e (its xsw holds rows 4 g .. 4 g + 3)
+        float* xs_l = reinterpret_cast<float*>(lds_raw + out_off - 64);
+        if (wave == 0 && j < 4) {
+            const unsigned b = j == 0 ? xsw[0] : (j == 1 ? xsw[1] : (j == 2 ? xsw[2] : xsw[3]));
+            xs_l[g * 4 + j] = __builtin_bit_cast(float, b) * d.w_scale;
         }
         __syncthreads();
         if (n > 0) {
@@ -451,16 +461,47 @@ __global__ __launch_bounds__(kSThreads) void gemm_stream_kernel(GemmDesc single,
             int rsr[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) rsr[e] = rsum[g * 4 + e];
-            StreamState p{0, 0, i32x4{0, 0, 0, 0}};
+            StreamState p{0, 0, 0, i32x4{0, 0, 0, 0}};
+            // Chunks of C tiles (whole double batches, at most (S - 1) Ku, so
+            // at most S strips complete in one), their strips written between
+            // chunks while the next chunk's first batch is in flight.
+            const int C = 2 * kSBatch * max(1, (out_strips - 1) * d.Ku / (2 * kSBatch));
+            int st_flush = 0;  // the run's strip index of the buffer's first strip
             int i0 = 0;
             while (true) {
-                stream_load(wb, rs, i0 + kSBatch);
-                stream_compute(d, wa, i0, n, arow, slot, w_a, rsr, xsr, p);
-                i0 += kSBatch;
-                if (i0 >= n) break;
-                stream_load(wa, rs, i0 + kSBatch);
-                stream_compute(d, wb, i0, n, arow, slot, w_a, rsr, xsr, p);
-                i0 += kSBatch;
+                const int cend = min(n, i0 + C);
+                while (true) {
+                    stream_load(wb, rs, i0 + kSBatch);
+                    stream_compute(d, wa, i0, n, arow, slot, obuf, d.M, rsr, p);
+                    i0 += kSBatch;
+                    if (i0 >= cend) break;  // only at the run's end (cend < n is a whole double batch)
+                    stream_load(wa, rs, i0 + kSBatch);
+                    stream_compute(d, wb, i0, n, arow, slot, obuf, d.M, rsr, p);
+                    i0 += kSBatch;
+                    if (i0 >= cend) break;
+                }
+                // The next chunk's first batch (wa) is in flight: wait for it
+                // before the stores, so that no wait after them is for a load
+                // issued before them (a load wait with stores pending drains
+                // every store too; the one after these is for the batch
+                // issued right behind them and overlaps their completion).
+                if (i0 < n) {
+#pragma unroll
+                    for (int i = 0; i < kSBatch; ++i) asm volatile("" :: "v"(wa[i]));
+                }
+                // four buffered strips of one row per store (256 contiguous bytes);
+                // a wave reads back only its own LDS writes
+                for (int s0 = 0; s0 < p.nbuf; s0 += 4) {
+                    const int sb = s0 + (lane >> 4);
+                    const int col = (w_a + st_flush + sb) * kStripCols + (lane & 15);
+                    if (sb < p.nbuf && col < d.N) {
+                        const int* ob = obuf + sb * d.M * kStripCols + (lane & 15);
+                        for (int row = 0; row < d.M; ++row)
+                            emit_out(d, (long long)row * d.N + col, ob[row * kStripCols], xs_l[row]);
+                    }
+                }
+                st_flush = p.strip;
+                p.nbuf = 0;
                 if (i0 >= n) break;
             }
         }
@@ -486,12 +527,11 @@ hipError_t allow_stream_lds() {
 
 template <bool kList, bool kVec>
 hipError_t launch_stream_t(const GemmDesc& single, const GemmDesc* list, const int32_t* first, long long total, int n_wg,
-                           int lds, int zero_off, hipStream_t st) {
+                           int lds_bytes, hipStream_t st) {
     const hipError_t e = allow_stream_lds();
     if (e != hipSuccess) return e;
-    // LDS: the X image [0, zero_off), the zero row, 16 row sums, the waves' tile slots
-    hipLaunchKernelGGL((gemm_stream_kernel<kList, kVec>), dim3(n_wg), dim3(kSThreads), lds, st, single, list, first,
-                       total, n_wg, zero_off, lds - zero_off - 64 - gemm_stream_slot_bytes());
+    hipLaunchKernelGGL((gemm_stream_kernel<kList, kVec>), dim3(n_wg), dim3(kSThreads), lds_bytes, st, single, list,
+                       first, total, n_wg, lds_bytes);
     return hipGetLastError();
 }
 
@@ -554,13 +594,12 @@ int gemm_stream_max_wg_per_cu(int lds_bytes) {
 }
 
 hipError_t launch_gemm_stream(const GemmDesc& single, const GemmDesc* list_dev, const int32_t* first_dev,
-                              long long total_tiles, int n_wg, int lds_bytes, int zero_off, bool vec, hipStream_t st) {
+                              long long total_tiles, int n_wg, int lds_bytes, bool vec, hipStream_t st) {
     if (list_dev)
-        return vec ? launch_stream_t<true, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, zero_off, st)
-                   : launch_stream_t<true, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, zero_off,
-                                                  st);
-    return vec ? launch_stream_t<false, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, zero_off, st)
-               : launch_stream_t<false, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, zero_off, st);
+        return vec ? launch_stream_t<true, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st)
+                   : launch_stream_t<true, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st);
+    return vec ? launch_stream_t<false, true>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st)
+               : launch_stream_t<false, false>(single, list_dev, first_dev, total_tiles, n_wg, lds_bytes, st);
 }
 
 int gemm_mb_of(int M) {

@@ -157,9 +157,22 @@ def test_gemm_plan_prefill(cuda, specs):
     [(8, 2560, 640), (8, 2560, 2560), (1, 256, 16), (16, 512, 4000), (4, 6912, 2560)],
 ], ids=["bytewise_x", "vector_x"])
 def test_gemm_plan_small_m(cuda, specs):
-    """M <= 16 plans run the streamed kernel: a workgroup's tile range may
-    start or end inside a strip or a GEMM, at several launch shapes."""
+    """Small-M plans with a K = 6912 item: 16 rows of it do not fit the
+    streamed kernel's LDS, so these run the LDS-ring kernel (ragged M, K and
+    N, byte-wise and vector X), at several launch shapes."""
     run_plan(specs, 700, (0, 1, 2))
+
+
+@pytest.mark.parametrize("specs", [
+    [(2, 256, 1 << 20)],                   # Ku = 1: 16-strip output buffers, 12-tile chunks, ~64 strips per wave
+    [(8, 2560, 131064), (8, 6912, 2560)],  # M = 8 beside K = 6912: 5-strip buffers, 36-tile chunks, ragged last strip
+], ids=["ku1_long_runs", "m8_bitnet_k"])
+def test_gemm_stream_chunks(cuda, specs):
+    """The streamed kernel (M <= 16 where the X image and the output buffers
+    fit): at one workgroup per CU each wave's run spans several chunks, so
+    completed strips are buffered in LDS and written between chunks many
+    times per wave."""
+    run_plan(specs, 1300, (1,))
 
 
 @pytest.mark.parametrize("M", [8, 32, 128])
