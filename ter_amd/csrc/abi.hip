@@ -691,8 +691,25 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
     if (x->kind == TER_HIP_X_I16) return launch_x16(d, static_cast<hipStream_t>(stream));
     const long long total = (long long)d.n_strips * d.Ku;
     int n_wg = 0;
+    const bool prologue = x->kind != TER_HIP_X_I8;
+    // small GEMVs: strip mode, as for a plan (whole strips per workgroup,
+    // the waves' partials added in LDS, no fix-up slots)
+    bool strip_mode = false;
+    rc = pick_strip_mode(total, d.n_strips, prologue, &strip_mode, &n_wg);
+    if (rc) return rc;
+    if (strip_mode) {
+        const int part_off = (gemv_lds_slots_offset(w->K, d.stage32 != 0) + 15) / 16 * 16;
+        const long long per_wg = (d.n_strips + n_wg - 1) / n_wg;
+        const int lds_strip = part_off + (int)per_wg * kGemvWaves * kStripCols * 4;
+        if (gemv_max_wg_per_cu(lds_strip) > 0) {
+            const hipError_t e = launch_gemv_strips_single(d, d.n_strips, n_wg, lds_strip, part_off,
+                                                           static_cast<hipStream_t>(stream));
+            if (e != hipSuccess) return hip_fail(e, "gemv launch");
+            return TER_HIP_OK;
+        }
+    }
     const int lds = gemv_t16_lds_bytes(w->K, d.stage32 != 0);
-    rc = pick_wg(total, 0, lds, x->kind != TER_HIP_X_I8, -1, &n_wg);
+    rc = pick_wg(total, 0, lds, prologue, -1, &n_wg);
     if (rc) return rc;
     hipError_t e = launch_gemv(d, nullptr, nullptr, nullptr, total, n_wg, lds, -1, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "gemv launch");

@@ -92,6 +92,9 @@ struct alignas(16) GemmDesc {
 constexpr int kStripModeMaxStrips = 32;
 hipError_t launch_gemv_strips(const GemvDesc* list_dev, const int32_t* first_dev, long long total_strips, int n_wg,
                               int lds_bytes, int part_off, int vec_kind, hipStream_t st);
+// The same for one GEMV whose descriptor is a kernel argument (any activation kind).
+hipError_t launch_gemv_strips_single(const GemvDesc& d, long long total_strips, int n_wg, int lds_bytes, int part_off,
+                                     hipStream_t st);
 // vec_kind: the activation kind of every GEMV of a work list that qualifies
 // for the vector prologue (gemv_vec_kind), else -1.
 // ranges_dev: [n_wg + 1] tile ranges of the workgroups of a work list (range

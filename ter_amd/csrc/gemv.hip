@@ -1130,8 +1130,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
 // strip's partial column sums in LDS, and after a barrier wave j % 4 adds the
 // four partials of strip j (integer sums, so the result is the stream-K
 // kernel's) and writes the outputs.  No fix-up slots, no global atomics.
-template <int kKind>
-__global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(const GemvDesc* __restrict__ list,
+template <bool kList, int kKind>
+__global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc single, const GemvDesc* __restrict__ list,
                                                                   const int32_t* __restrict__ first,
                                                                   long long total, int n_wg, int part_off) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -1140,14 +1140,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(const GemvDesc
     const long long s_begin = total * g / n_wg;
     const long long s_end = total * (g + 1) / n_wg;
     if (s_begin >= s_end) return;
-    int di = first[g];
+    int di = kList ? first[g] : 0;
     const int wave = uniform(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int voff = lane * 16;
     int* part = reinterpret_cast<int*>(lds_raw + part_off);  // [strip][wave][16 columns]
     long long sg = s_begin;
     while (sg < s_end) {
-        const GemvDesc d = list[di];
+        const GemvDesc d = kList ? list[di] : single;
         const long long seg_end = min(s_end, d.strip0 + (long long)d.n_strips);
         const int sa = (int)(sg - d.strip0);  // first strip of the segment within the GEMV
         const int ns = (int)(seg_end - sg);
@@ -1305,29 +1305,36 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const int32_t* first_dev
     const dim3 grid(n_wg), block(kGemvThreads);
     switch (vec_kind) {
     case TER_HIP_X_I8:
-        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_I8>), grid, block, lds_bytes, st, list_dev, first_dev,
-                           total_strips, n_wg, part_off);
+        hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_I8>), grid, block, lds_bytes, st, GemvDesc{},
+                           list_dev, first_dev, total_strips, n_wg, part_off);
         break;
     case TER_HIP_X_F32:
-        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_F32>), grid, block, lds_bytes, st, list_dev, first_dev,
-                           total_strips, n_wg, part_off);
+        hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F32>), grid, block, lds_bytes, st, GemvDesc{},
+                           list_dev, first_dev, total_strips, n_wg, part_off);
         break;
     case TER_HIP_X_F32_RMS:
-        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_F32_RMS>), grid, block, lds_bytes, st, list_dev, first_dev,
-                           total_strips, n_wg, part_off);
+        hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F32_RMS>), grid, block, lds_bytes, st, GemvDesc{},
+                           list_dev, first_dev, total_strips, n_wg, part_off);
         break;
     case TER_HIP_X_F16_RMS:
-        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_F16_RMS>), grid, block, lds_bytes, st, list_dev, first_dev,
-                           total_strips, n_wg, part_off);
+        hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F16_RMS>), grid, block, lds_bytes, st, GemvDesc{},
+                           list_dev, first_dev, total_strips, n_wg, part_off);
         break;
     case TER_HIP_X_RELU2_RMS:
-        hipLaunchKernelGGL((gemv_strip_kernel<TER_HIP_X_RELU2_RMS>), grid, block, lds_bytes, st, list_dev,
-                           first_dev, total_strips, n_wg, part_off);
+        hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_RELU2_RMS>), grid, block, lds_bytes, st, GemvDesc{},
+                           list_dev, first_dev, total_strips, n_wg, part_off);
         break;
     default:
-        hipLaunchKernelGGL((gemv_strip_kernel<-1>), grid, block, lds_bytes, st, list_dev, first_dev, total_strips,
-                           n_wg, part_off);
+        hipLaunchKernelGGL((gemv_strip_kernel<true, -1>), grid, block, lds_bytes, st, GemvDesc{},
+                           list_dev, first_dev, total_strips, n_wg, part_off);
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_strips_single(const GemvDesc& d, long long total_strips, int n_wg, int lds_bytes, int part_off,
+                                     hipStream_t st) {
+    hipLaunchKernelGGL((gemv_strip_kernel<false, -1>), dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, d, nullptr,
+                       nullptr, total_strips, n_wg, part_off);
     return hipGetLastError();
 }
 
