@@ -14,15 +14,21 @@
 // Pipeline.  NST stages of LDS, each holding one unit's X rows and weight
 // tiles, are filled by buffer_load_dwordx4 ... lds (64 lanes x 16 bytes = one
 // 1 KiB LDS run per instruction; no registers involved) NST - 1 units ahead
-// of the MFMAs.  Per unit: wait for this wave's loads of the unit (explicit
-// vmcnt), barrier (every wave's loads landed, and every wave is done reading
-// the stage about to be refilled), issue the loads of unit + NST - 1, then
-// the MFMAs.  A wave's loads complete in issue order, so waiting until no
-// more operations are outstanding than the younger stages' loads guarantees
-// the stage has landed.  That holds with the epilogue's stores in flight too
-// (stores may complete out of order with respect to loads, but a wait that
-// leaves only the younger loads outstanding waits for them as well), so a
-// block's epilogue needs no drain.
+// of the MFMAs.  Per unit: the issuing waves wait for their loads of the unit
+// (explicit vmcnt), barrier (every load landed, and every compute wave is
+// done reading the stage about to be refilled), the issuing waves issue the
+// loads of unit + NST - 1, the compute waves run the MFMAs.  A wave's loads
+// complete in issue order, so waiting until no more operations are
+// outstanding than the younger stages' loads guarantees the stage has landed.
+// That holds with the epilogue's stores in flight too (stores may complete
+// out of order with respect to loads, but a wait that leaves only the younger
+// loads outstanding waits for them as well), so a block's epilogue needs no
+// drain.  Up to M = 32 (PW > 0) four producer waves issue all the loads and
+// the 8 compute waves issue none: the memory pipeline accepts only so many
+// loads in flight, and a wave that stalls at its loads holds back nothing
+// behind it in issue order (measured at M = 32: 154 -> 145 us per C4 launch).
+// Above, the 8 compute waves' registers leave no room for more waves, and
+// they issue the loads themselves after the barrier.
 //
 // Operands.  X rows sit in LDS as 256-byte rows whose 16-byte chunks are
 // XOR-swizzled by the row's low 4 bits (chunk c of row r at position
@@ -34,6 +40,11 @@
 // each 2-bit code u = w + 1 straight to the signed int8 w with one v_perm_b32
 // per 4 trits (a byte table {-1, 0, +1, 0} indexed by u), and issues
 // v_mfma_i32_16x16x64_i8.  Signed weights need no activation-sum correction.
+// The A operands are read a few steps ahead of their MFMAs.
+//
+// Epilogue.  fp32 / int32 outputs (N a multiple of 4) are transposed in
+// quads of lanes (DPP) so that each lane stores 4 consecutive columns of one
+// row with one 16-byte store; other output forms go element by element.
 #include <type_traits>
 
 #include "common.h"
@@ -48,11 +59,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 constexpr int kLWaves = 8;
-constexpr int kLThreads = 64 * kLWaves;
 
-template <int MBW_, int S_, int RS_, int NST_>
+// PW producer waves (0: the 8 compute waves issue the loads themselves).
+template <int MBW_, int S_, int RS_, int NST_, int PW_ = 0>
 struct LCfg {
-    static constexpr int MBW = MBW_, S = S_, RS = RS_, NST = NST_;
+    static constexpr int MBW = MBW_, S = S_, RS = RS_, NST = NST_, PW = PW_;
+    static constexpr int THREADS = 64 * (kLWaves + PW);
+    static constexpr int IW = PW > 0 ? PW : kLWaves;  // waves that issue the loads
     static constexpr int MB = RS * MBW;               // row blocks of 16
     static constexpr int SG = kLWaves / RS;           // strip groups
     static constexpr int BS = SG * S;                 // strips per block
@@ -61,9 +74,9 @@ struct LCfg {
     static constexpr int XSO = NST * STB;             // row-scale slots: NST x 1 KiB
     static constexpr int LDS = XSO + NST * 1024;
     static constexpr int XI = XB / 1024;              // 1 KiB load runs of X per stage
-    static constexpr int NI = XI + BS;                // load runs per stage, run q issued by wave q % 8
-    static constexpr int NIW = NI / kLWaves;          // runs of waves >= NR ...
-    static constexpr int NR = NI % kLWaves;           // ... and waves < NR issue one more
+    static constexpr int NI = XI + BS;                // load runs per stage, run q issued by issuer q % IW
+    static constexpr int NIW = NI / IW;               // runs of issuers >= NR ...
+    static constexpr int NR = NI % IW;                // ... and issuers < NR issue one more
     // Weight tiles transposed by 16-byte chunks in LDS: conflict-free operand
     // reads, but each quarter-wave's load spans four 256-byte runs instead of
     // one.  Measured on the BitNet-2B sweep: 2.8% faster at M = 128 (8 row
@@ -77,9 +90,15 @@ struct LCfg {
 // M <= 16 (16-strip blocks, 60 KiB for three stages: two workgroups per CU,
 // 116.7 against 122.9 us with 4 strips and one), 4 above (32-strip blocks, X
 // staged once per 32 weight tiles); three stages up to M = 32, two above.
-using Cfg1 = LCfg<1, 2, 1, 3>;
-using Cfg2 = LCfg<2, 4, 1, 3>;
-using Cfg4 = LCfg<4, 4, 1, 2>;
+#ifndef TER_LDS_PW
+#define TER_LDS_PW 4
+#endif
+using Cfg1 = LCfg<1, 2, 1, 3, TER_LDS_PW>;
+using Cfg2 = LCfg<2, 4, 1, 3, TER_LDS_PW>;
+#ifndef TER_LDS_PW4
+#define TER_LDS_PW4 0
+#endif
+using Cfg4 = LCfg<4, 4, 1, 2, TER_LDS_PW4>;
 using Cfg8 = LCfg<8, 4, 1, 2>;
 
 // s_waitcnt immediate (gfx9 family): vmcnt(n), expcnt and lgkmcnt not waited on.
@@ -112,40 +131,41 @@ __device__ __forceinline__ void wait_stage_n(int behind) {
 }
 
 template <class C>
-__device__ __forceinline__ void wait_stage(int behind, int wave) {
-    if (C::NR != 0 && wave < C::NR)
+__device__ __forceinline__ void wait_stage(int behind, int issuer) {
+    if (C::NR != 0 && issuer < C::NR)
         wait_stage_n<C, C::NIW + 1>(behind);
     else
         wait_stage_n<C, C::NIW>(behind);
 }
 
-// Issue this wave's share of the loads of unit u of the block starting at
-// strip st0 into `stage`.  xr covers X (M * ldx bytes: rows >= M read zeros);
-// wr covers the block's strips (strips past the matrix read zeros).
+// Load runs an issuing wave issues per stage (at most; run q of the stage is
+// issued by issuer q % IW).
 template <class C>
-__device__ __forceinline__ void issue_stage(int ldx, int Ku, int u, unsigned char* stage,
-                                            __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr, int wave,
-                                            int lane) {
-#pragma unroll
-    for (int r = 0; r < C::NIW + (C::NR != 0); ++r) {
-        const int q = wave + kLWaves * r;  // wave-uniform
-        if (C::NR != 0 && q >= C::NI) break;
-        if (q < C::XI) {
-            // rows 4q .. 4q+3: lane -> row 4q + lane / 16, stored chunk lane % 16
-            const int row = 4 * q + (lane >> 4);
-            const int chunk = (lane & 15) ^ (row & 15);
-            // (resource, LDS run, bytes per lane, vector offset, scalar offset, immediate offset, cache policy)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (TER_LDS void*)(stage + q * 1024), 16,
-                                                     row * ldx + u * kUnitK + chunk * 16, 0, 0, 0);
-        } else {
-            // tile (strip t of the block, unit u); with C::TW its 16-byte chunk
-            // (column quad cq, row group rq) at tile offset cq * 256 + rq * 16
-            // lands at LDS chunk 4 rq + cq (see compute_stage)
-            const int t = q - C::XI;
-            const int src = C::TW ? (lane & 3) * 256 + (lane >> 2) * 16 : lane * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (TER_LDS void*)(stage + C::XB + t * 1024), 16,
-                                                     (t * Ku + u) * kTileBytes + src, 0, 0, 2 /* nt */);
-        }
+constexpr int runs_per_wave() { return C::NIW + (C::NR != 0); }
+
+// Issue the issuing wave's r-th load run of unit u of the block starting at strip
+// st0 into `stage`.  xr covers X (M * ldx bytes: rows >= M read zeros); wr
+// covers the block's strips (strips past the matrix read zeros).
+template <class C>
+__device__ __forceinline__ void issue_run(int r, int ldx, int Ku, int u, unsigned char* stage,
+                                          __amdgpu_buffer_rsrc_t xr, __amdgpu_buffer_rsrc_t wr, int issuer, int lane) {
+    const int q = issuer + C::IW * r;  // wave-uniform
+    if (C::NR != 0 && q >= C::NI) return;
+    if (q < C::XI) {
+        // rows 4q .. 4q+3: lane -> row 4q + lane / 16, stored chunk lane % 16
+        const int row = 4 * q + (lane >> 4);
+        const int chunk = (lane & 15) ^ (row & 15);
+        // (resource, LDS run, bytes per lane, vector offset, scalar offset, immediate offset, cache policy)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (TER_LDS void*)(stage + q * 1024), 16,
+                                                 row * ldx + u * kUnitK + chunk * 16, 0, 0, 0);
+    } else {
+        // tile (strip t of the block, unit u); with C::TW its 16-byte chunk
+        // (column quad cq, row group rq) at tile offset cq * 256 + rq * 16
+        // lands at LDS chunk 4 rq + cq (see compute_stage)
+        const int t = q - C::XI;
+        const int src = C::TW ? (lane & 3) * 256 + (lane >> 2) * 16 : lane * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (TER_LDS void*)(stage + C::XB + t * 1024), 16,
+                                                 (t * Ku + u) * kTileBytes + src, 0, 0, 2 /* nt */);
     }
 }
 
@@ -157,18 +177,45 @@ __device__ __forceinline__ i32x4 unpack_signed(unsigned dw) {
                  (int)__builtin_amdgcn_perm(0u, kT, (dw >> 4) & kM), (int)__builtin_amdgcn_perm(0u, kT, (dw >> 6) & kM)};
 }
 
+// 4 x 4 transpose within each quad of lanes: lane 4 a + b returns element c
+// = element b of lane 4 a + c (two exchange rounds, partner lane b ^ 1 then
+// b ^ 2, each taking the elements whose index bit differs from the lane's).
+__device__ __forceinline__ i32x4 quad_transpose(i32x4 v, int lane) {
+    const bool o1 = lane & 1, o2 = lane & 2;
+    const int p0 = __builtin_amdgcn_mov_dpp(v[1], 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    const int p1 = __builtin_amdgcn_mov_dpp(v[0], 0xB1, 0xF, 0xF, false);
+    const int p2 = __builtin_amdgcn_mov_dpp(v[3], 0xB1, 0xF, 0xF, false);
+    const int p3 = __builtin_amdgcn_mov_dpp(v[2], 0xB1, 0xF, 0xF, false);
+    const int a0 = o1 ? p0 : v[0], a1 = o1 ? v[1] : p1, a2 = o1 ? p2 : v[2], a3 = o1 ? v[3] : p3;
+    const int q0 = __builtin_amdgcn_mov_dpp(a2, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    const int q1 = __builtin_amdgcn_mov_dpp(a3, 0x4E, 0xF, 0xF, false);
+    const int q2 = __builtin_amdgcn_mov_dpp(a0, 0x4E, 0xF, 0xF, false);
+    const int q3 = __builtin_amdgcn_mov_dpp(a1, 0x4E, 0xF, 0xF, false);
+    return i32x4{o2 ? q0 : a0, o2 ? q1 : a1, o2 ? a2 : q2, o2 ? a3 : q3};
+}
+
+// A operands read this many (slab, row block) steps ahead of their MFMAs.
+#ifndef TER_LDS_APF
+#define TER_LDS_APF 3
+#endif
+constexpr int kAPrefetch = TER_LDS_APF;
+
+// One stage: 4 slabs of 64 rows x MBW row blocks = 4 MBW steps, each one A
+// operand (ds_read_b128) feeding S MFMAs.  The stage's weight dwords (4 x S
+// ds_read_b32) are read first; then step t's MFMAs run while the A operand of
+// step t + kAPrefetch is in flight (a wave's LDS reads return in order, so
+// the wait before step t's MFMAs leaves the younger reads outstanding).  The
+// scheduling fences keep the compiler from pulling the reads down next to
+// their MFMAs, which exposed the LDS latency on every step.
 template <class C>
 __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg, int sg, int lane,
                                               i32x4 (&acc)[C::S][C::MBW]) {
     const int j = lane & 15, g = lane >> 4;
+    // (two steps ahead at 8 row blocks, whose accumulators leave no room for a third)
+    constexpr int KS = 4, T = KS * C::MBW, P = C::MBW >= 8 ? 2 : (kAPrefetch < T ? kAPrefetch : T);
+    unsigned dw[KS][C::S];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-        i32x4 A[C::MBW];
-#pragma unroll
-        for (int mb = 0; mb < C::MBW; ++mb) {
-            const int row = (rg * C::MBW + mb) * 16 + j;  // row % 16 == j
-            A[mb] = *reinterpret_cast<const i32x4*>(stage + row * kUnitK + (((ks * 4 + g) ^ j) * 16));
-        }
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int s = 0; s < C::S; ++s) {
             // column j, rows (4 ks + g) * 16 .. +15: tile offset (j >> 2) * 256 +
@@ -176,12 +223,31 @@ __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg
             // ks * 256 + lane * 4: the 64 lanes read 256 contiguous bytes, where
             // in tile order four lanes share each bank.
             const int off = C::TW ? ks * 256 + lane * 4 : (j >> 2) * 256 + (4 * ks + g) * 16 + (j & 3) * 4;
-            const unsigned dw = *reinterpret_cast<const unsigned*>(stage + C::XB + (sg * C::S + s) * kTileBytes + off);
-            const i32x4 B = unpack_signed(dw);
-#pragma unroll
-            for (int mb = 0; mb < C::MBW; ++mb)
-                acc[s][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mb], B, acc[s][mb], 0, 0, 0);
+            dw[ks][s] = *reinterpret_cast<const unsigned*>(stage + C::XB + (sg * C::S + s) * kTileBytes + off);
         }
+    auto a_at = [&](int t) {
+        const int ks = t / C::MBW, mb = t % C::MBW;
+        const int row = (rg * C::MBW + mb) * 16 + j;  // row % 16 == j
+        return *reinterpret_cast<const i32x4*>(stage + row * kUnitK + (((ks * 4 + g) ^ j) * 16));
+    };
+    i32x4 A[P];
+#pragma unroll
+    for (int t = 0; t < P; ++t) A[t] = a_at(t);
+    i32x4 B[C::S];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int ks = t / C::MBW, mb = t % C::MBW;
+        if (mb == 0) {
+#pragma unroll
+            for (int s = 0; s < C::S; ++s) B[s] = unpack_signed(dw[ks][s]);
+        }
+        const i32x4 a = A[t % P];
+        if (t + P < T) A[t % P] = a_at(t + P);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < C::S; ++s)
+            acc[s][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[s], acc[s][mb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -206,7 +272,7 @@ __device__ __forceinline__ BlockRef block_at(const GemmDesc& single, const GemmD
 }
 
 template <class C, bool kList>
-__global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, const GemmDesc* __restrict__ list,
+__global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, const GemmDesc* __restrict__ list,
                                                              const GemmBlock* __restrict__ blocks,
                                                              const int32_t* __restrict__ ranges, int n_blocks,
                                                              int n_wg) {
@@ -225,6 +291,8 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
     if (b_lo >= b_hi) return;
     const int lane = threadIdx.x & 63;
     const int wave = uniform(threadIdx.x >> 6);
+    const bool producer = C::PW > 0 && wave >= kLWaves;  // wave-uniform
+    const int issuer = C::PW > 0 ? wave - kLWaves : wave;  // index among the issuing waves
     const int rg = wave / C::SG, sg = wave % C::SG;
     const int j = lane & 15, g = lane >> 4;
 
@@ -240,18 +308,24 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
                                                  ns * r.d.Ku * kTileBytes, 0x00020000);
     };
     __amdgpu_buffer_rsrc_t xr = rsrc_x(bi.d), wr = rsrc_w(bi);
-    // Block ib's row scales go to LDS slot ib % NST with its first unit (wave 0,
-    // one extra load: an extra operation only makes the stage waits stricter).
-    // The issue side runs at most NST - 1 units ahead, so a slot is refilled
-    // only after the block that used it has finished.
-    auto issue_next = [&]() {
-        if (iu == 0 && wave == 0) {
+    // Block ib's row scales go to LDS slot ib % NST with its first unit
+    // (issuer 0, one extra load: an extra operation only makes the stage waits
+    // stricter).  The issue side runs at most NST - 1 units ahead, so a slot
+    // is refilled only after the block that used it has finished.
+    auto issue_scales = [&]() {
+        if (iu == 0 && issuer == 0) {
             const __amdgpu_buffer_rsrc_t sr =
                 __builtin_amdgcn_make_buffer_rsrc((void*)bi.d.xs, 0, bi.d.M * 4, 0x00020000);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(sr, (TER_LDS void*)(lds + C::XSO + (ib % C::NST) * 1024), 16,
                                                      lane * 16, 0, 0, 0);
         }
-        issue_stage<C>(bi.d.ldx, bi.d.Ku, iu, lds + i_stage * C::STB, xr, wr, wave, lane);
+    };
+    // this wave's loads of the next stage, then advance to the stage after it
+    auto issue_next = [&]() {
+        issue_scales();
+#pragma unroll
+        for (int r = 0; r < runs_per_wave<C>(); ++r)
+            issue_run<C>(r, bi.d.ldx, bi.d.Ku, iu, lds + i_stage * C::STB, xr, wr, issuer, lane);
         ++n_issued;
         i_stage = i_stage + 1 == C::NST ? 0 : i_stage + 1;
         if (++iu == bi.d.Ku) {
@@ -263,9 +337,32 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
             }
         }
     };
+    if (C::PW == 0 || producer) {
 #pragma unroll
-    for (int p = 0; p < C::NST - 1; ++p)
-        if (ib < b_hi) issue_next();
+        for (int p = 0; p < C::NST - 1; ++p)
+            if (ib < b_hi) issue_next();
+    }
+    if (producer) {
+        // Producer waves: wait for their loads of stage it, meet the compute
+        // waves at the stage's barrier, then issue the stage that refills the
+        // slot the compute waves have just left.  A producer that stalls at
+        // its loads (the memory pipeline accepts only so many in flight)
+        // holds back no MFMA; the compute waves wait only when the data is
+        // late.  Same stage count and barrier count as the compute waves.
+        int cb = b_lo, cu = 0, it = 0, cku = block_at<kList>(single, list, blocks, cb, C::BS).d.Ku;
+        while (true) {
+            wait_stage<C>(n_issued - it - 1, issuer);
+            lds_barrier();
+            if (ib < b_hi) issue_next();
+            ++it;
+            if (++cu == cku) {
+                if (++cb >= b_hi) break;
+                cku = block_at<kList>(single, list, blocks, cb, C::BS).d.Ku;
+                cu = 0;
+            }
+        }
+        return;
+    }
 
     // compute side
     int cb = b_lo, cu = 0, it = 0, c_stage = 0;
@@ -276,9 +373,9 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
 #pragma unroll
         for (int mb = 0; mb < C::MBW; ++mb) acc[s][mb] = i32x4{0, 0, 0, 0};
     while (true) {
-        wait_stage<C>(n_issued - it - 1, wave);
+        if (C::PW == 0) wait_stage<C>(n_issued - it - 1, issuer);
         lds_barrier();
-        if (ib < b_hi) issue_next();
+        if (C::PW == 0 && ib < b_hi) issue_next();
         compute_stage<C>(lds + c_stage * C::STB, rg, sg, lane, acc);
         ++it;
         c_stage = c_stage + 1 == C::NST ? 0 : c_stage + 1;
@@ -291,44 +388,32 @@ __global__ __launch_bounds__(kLThreads) void gemm_lds_kernel(GemmDesc single, co
             asm volatile("" : "+s"(d.N), "+s"(d.M), "+s"(d.y), "+s"(d.acc), "+s"(d.y16), "+s"(d.resid),
                          "+s"(d.w_scale), "+s"(d.w_mag));
             const float* xs_l = reinterpret_cast<const float*>(lds + C::XSO + (cb % C::NST) * 1024);
-            // For the 8-row-block configuration (M > 64, occupancy already
-            // fixed by its accumulators) fp32 / int32 outputs get a loop of
-            // their own: the fp16 and residual checks per element cost ~3% at
-            // M = 128.  Smaller configurations keep one loop (a second copy
-            // costs them a wave of occupancy).
-            auto epilogue = [&](auto plain_tag) {
-                constexpr bool kPlain = decltype(plain_tag)::value;
+            // fp32 / int32 outputs with N a multiple of 4 go out 16 bytes per
+            // lane: the address unit takes a store in about the same time
+            // whatever its width (4 lanes per cycle), and dword stores of a
+            // block's outputs cost more of it than the block's loads.
+            const bool vec_out = !d.y16 && !d.resid && d.w_mag == 1 && (d.N & 3) == 0 &&
+                                 ((reinterpret_cast<uintptr_t>(d.y) | reinterpret_cast<uintptr_t>(d.acc)) & 15) == 0;
+            if (vec_out) {
 #pragma unroll
                 for (int mb = 0; mb < C::MBW; ++mb) {
-                    const f32x4 xq = *reinterpret_cast<const f32x4*>(xs_l + (rg * C::MBW + mb) * 16 + g * 4);
+                    // after the transpose lane (j, g) holds row 4 g + j % 4 of
+                    // the row block, columns 4 (j / 4) .. +3 of each strip
+                    const int row = (rg * C::MBW + mb) * 16 + g * 4 + (lane & 3);
+                    const float sc = xs_l[row] * d.w_scale;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int row = (rg * C::MBW + mb) * 16 + g * 4 + e;
-                        if (row < d.M) {
-                            const float sc = xq[e] * d.w_scale;
-#pragma unroll
-                            for (int s = 0; s < C::S; ++s) {
-                                const int col = (bc.st0 + sg * C::S + s) * kStripCols + j;
-                                if (col < d.N) {
-                                    const long long o = (long long)row * d.N + col;
-                                    const int val = acc[s][mb][e];
-                                    if constexpr (kPlain) {
-                                        if (d.acc) gptr(d.acc)[o] = val;
-                                        if (d.y) gptr(d.y)[o] = (float)val * sc;
-                                    } else {
-                                        emit_out(d, o, val, sc);
-                                    }
-                                }
-                            }
+                    for (int s = 0; s < C::S; ++s) {
+                        i32x4 v = quad_transpose(acc[s][mb], lane);
+                        const int col = (bc.st0 + sg * C::S + s) * kStripCols + (j & ~3);
+                        if (row < d.M && col < d.N) {
+                            const long long o = (long long)row * d.N + col;
+                            if (d.acc) *reinterpret_cast<TER_GLOBAL i32x4*>(gptr(d.acc) + o) = v;
+                            if (d.y)
+                                *reinterpret_cast<TER_GLOBAL f32x4*>(gptr(d.y) + o) =
+                                    f32x4{(float)v[0] * sc, (float)v[1] * sc, (float)v[2] * sc, (float)v[3] * sc};
                         }
                     }
                 }
-            };
-            if constexpr (C::MBW >= 8) {
-                if (!d.y16 && !d.resid && d.w_mag == 1)
-                    epilogue(std::true_type{});
-                else
-                    epilogue(std::false_type{});
             } else {
 #pragma unroll
                 for (int mb = 0; mb < C::MBW; ++mb) {
@@ -379,10 +464,10 @@ hipError_t launch_cfg(const GemmDesc& single, const GemmDesc* list, const GemmBl
     const hipError_t e = allow_lds<C>();
     if (e != hipSuccess) return e;
     if (list)
-        hipLaunchKernelGGL((gemm_lds_kernel<C, true>), dim3(n_wg), dim3(kLThreads), C::LDS, st, single, list, blocks,
+        hipLaunchKernelGGL((gemm_lds_kernel<C, true>), dim3(n_wg), dim3(C::THREADS), C::LDS, st, single, list, blocks,
                            ranges, n_blocks, n_wg);
     else
-        hipLaunchKernelGGL((gemm_lds_kernel<C, false>), dim3(n_wg), dim3(kLThreads), C::LDS, st, single, list,
+        hipLaunchKernelGGL((gemm_lds_kernel<C, false>), dim3(n_wg), dim3(C::THREADS), C::LDS, st, single, list,
                            blocks, ranges, n_blocks, n_wg);
     return hipGetLastError();
 }
@@ -391,7 +476,7 @@ template <class C>
 int occupancy_cfg() {
     if (allow_lds<C>() != hipSuccess) return 0;
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_lds_kernel<C, true>, kLThreads, C::LDS) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemm_lds_kernel<C, true>, C::THREADS, C::LDS) != hipSuccess)
         return 0;
     return n;
 }
