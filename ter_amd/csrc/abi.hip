@@ -200,11 +200,10 @@ int gemv_vec_kind(const ter_hip_gemv_item_t* items, int n) {
 }
 
 // Strip mode for work lists below kSmallPlanTilesPerWg tiles per workgroup at
-// the default occupancy and with at most two strips per CU (beyond that a
-// workgroup would walk several strips' units one after the other, and the
-// stream-K partition is faster: 2 x 432 strips of 10 units, 7.5 against
-// 8.0 us): one workgroup per strip up to one per CU (two for int8 inputs,
-// which have no prologue to repeat).
+// the default occupancy and with at most four strips per CU (the decode
+// step's gate/up list, 2 x 432 strips of 10 units, included: 1.168 -> 1.147 ms
+// per C5 token against its stream-K partition): one workgroup per strip up to
+// one per CU (two for int8 inputs, which have no prologue to repeat).
 int pick_strip_mode(long long total_tiles, long long total_strips, bool prologue, bool* strip_mode, int* n_wg) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -212,7 +211,7 @@ int pick_strip_mode(long long total_tiles, long long total_strips, bool prologue
     const int cus = device_cu_count(dev);
     if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
     *strip_mode = total_tiles < (long long)cus * kGemvWgPerCu * kSmallPlanTilesPerWg &&
-                  total_strips <= (long long)cus * kGemvWgPerCu;
+                  total_strips <= (long long)cus * 4;
     if (!*strip_mode) return TER_HIP_OK;
     long long g = (long long)cus * (prologue ? 1 : kGemvWgPerCu);
     if (g > total_strips) g = total_strips;

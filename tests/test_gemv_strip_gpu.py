@@ -1,5 +1,5 @@
 """GPU parity of the GEMV kernel's strip mode: small work lists (fewer than
-32 tiles per workgroup at two workgroups per CU, at most two strips per CU)
+32 tiles per workgroup at two workgroups per CU, at most four strips per CU)
 give each workgroup whole column strips, split each strip's 256-row units
 over its four waves and add the waves' partial column sums in LDS; stream-K
 fix-up slots are not used.
@@ -74,9 +74,21 @@ def test_two_strips_per_workgroup(cuda, K):
     run_list([(K, 16 * 255 - 4), (K, 16 * 257)], seed=5 + K, fp32=True)
 
 
+@pytest.mark.parametrize("K", [512, 2560])
+def test_four_strips_per_workgroup(cuda, K):
+    """1000 strips with a prologue (one workgroup per CU): three or four
+    strips per workgroup, ranges crossing the boundaries between three GEMVs
+    at odd strips, ragged N."""
+    run_list([(K, 16 * 333 - 4), (K, 16 * 334), (K, 16 * 333 + 4)], seed=7 + K, fp32=True)
+
+
 def test_decode_shaped_lists(cuda):
-    """The decode step's lists: Q/K/V, O, gate/up, down (BitNet-2B shapes)."""
+    """The decode step's lists: Q/K/V, O, gate/up (864 strips: strip mode),
+    down (BitNet-2B shapes); and a list just past strip mode (1056 strips:
+    stream-K)."""
     run_list([(2560, 2560), (2560, 640), (2560, 640)], seed=11)
     run_list([(2560, 2560)], seed=12)
-    run_list([(2560, 6912), (2560, 6912)], seed=13)  # stream-K (864 strips)
+    run_list([(2560, 6912), (2560, 6912)], seed=13)
+    run_list([(2560, 6912), (2560, 6912)], seed=15, fp32=True)
     run_list([(6912, 2560)], seed=14)
+    run_list([(2560, 8448), (2560, 8448)], seed=16)
