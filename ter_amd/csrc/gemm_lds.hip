@@ -81,7 +81,19 @@ struct LCfg {
     // reads, but each quarter-wave's load spans four 256-byte runs instead of
     // one.  Measured on the BitNet-2B sweep: 2.8% faster at M = 128 (8 row
     // blocks, bound by LDS reads), 2.7% slower at M = 16 (bound by the loads).
-    static constexpr bool TW = MBW >= 4;
+#ifndef TER_LDS_TW_MB
+#define TER_LDS_TW_MB 4
+#endif
+    static constexpr bool TW = MBW >= TER_LDS_TW_MB;
+    // Up to 2 row blocks the weights enter the MFMAs as their unsigned codes
+    // u = w + 1 (7 bit operations per 16 trits instead of 11 for the signed
+    // table lookup) and one more MFMA per A operand sums the rows of X
+    // against all-ones, subtracted in the epilogue: there each weight dword
+    // feeds only MBW MFMAs, and its unpacking bounds the compute waves.
+#ifndef TER_LDS_UC_MB
+#define TER_LDS_UC_MB 2
+#endif
+    static constexpr bool UC = MBW <= TER_LDS_UC_MB;
     static_assert(NST >= 2 && NST <= 4, "stage count");
 };
 
@@ -177,6 +189,13 @@ __device__ __forceinline__ i32x4 unpack_signed(unsigned dw) {
                  (int)__builtin_amdgcn_perm(0u, kT, (dw >> 4) & kM), (int)__builtin_amdgcn_perm(0u, kT, (dw >> 6) & kM)};
 }
 
+// The 16 trits of one T16 dword as their unsigned codes u = w + 1 in MFMA B
+// operand order (byte b of word f: row 4 f + b); T16 fields hold 0, 1 or 2.
+__device__ __forceinline__ i32x4 unpack_u(unsigned dw) {
+    const unsigned kM = 0x03030303u;
+    return i32x4{(int)(dw & kM), (int)((dw >> 2) & kM), (int)((dw >> 4) & kM), (int)((dw >> 6) & kM)};
+}
+
 // 4 x 4 transpose within each quad of lanes: lane 4 a + b returns element c
 // = element b of lane 4 a + c (two exchange rounds, partner lane b ^ 1 then
 // b ^ 2, each taking the elements whose index bit differs from the lane's).
@@ -209,7 +228,7 @@ constexpr int kAPrefetch = TER_LDS_APF;
 // their MFMAs, which exposed the LDS latency on every step.
 template <class C>
 __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg, int sg, int lane,
-                                              i32x4 (&acc)[C::S][C::MBW]) {
+                                              i32x4 (&acc)[C::S][C::MBW], i32x4 (&rsum)[C::MBW]) {
     const int j = lane & 15, g = lane >> 4;
     // (two steps ahead at 8 row blocks, whose accumulators leave no room for a third)
     constexpr int KS = 4, T = KS * C::MBW, P = C::MBW >= 8 ? 2 : (kAPrefetch < T ? kAPrefetch : T);
@@ -239,7 +258,7 @@ __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg
         const int ks = t / C::MBW, mb = t % C::MBW;
         if (mb == 0) {
 #pragma unroll
-            for (int s = 0; s < C::S; ++s) B[s] = unpack_signed(dw[ks][s]);
+            for (int s = 0; s < C::S; ++s) B[s] = C::UC ? unpack_u(dw[ks][s]) : unpack_signed(dw[ks][s]);
         }
         const i32x4 a = A[t % P];
         if (t + P < T) A[t % P] = a_at(t + P);
@@ -247,6 +266,10 @@ __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg
 #pragma unroll
         for (int s = 0; s < C::S; ++s)
             acc[s][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[s], acc[s][mb], 0, 0, 0);
+        if constexpr (C::UC) {
+            const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
+            rsum[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ones, rsum[mb], 0, 0, 0);
+        }
         __builtin_amdgcn_sched_barrier(0);
     }
 }
@@ -368,15 +391,18 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
     int cb = b_lo, cu = 0, it = 0, c_stage = 0;
     BlockRef bc = block_at<kList>(single, list, blocks, cb, C::BS);
     i32x4 acc[C::S][C::MBW];
+    i32x4 rsum[C::MBW];  // row sums of X (C::UC only)
 #pragma unroll
     for (int s = 0; s < C::S; ++s)
 #pragma unroll
         for (int mb = 0; mb < C::MBW; ++mb) acc[s][mb] = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int mb = 0; mb < C::MBW; ++mb) rsum[mb] = i32x4{0, 0, 0, 0};
     while (true) {
         if (C::PW == 0) wait_stage<C>(n_issued - it - 1, issuer);
         lds_barrier();
         if (C::PW == 0 && ib < b_hi) issue_next();
-        compute_stage<C>(lds + c_stage * C::STB, rg, sg, lane, acc);
+        compute_stage<C>(lds + c_stage * C::STB, rg, sg, lane, acc, rsum);
         ++it;
         c_stage = c_stage + 1 == C::NST ? 0 : c_stage + 1;
         if (++cu == bc.d.Ku) {
@@ -384,6 +410,16 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
             // with one GEMM they are loop-invariant, and the compiler would
             // otherwise hoist every row's output addresses and checks out of
             // the loop (at 8 row blocks, 136 VGPRs spilled to scratch)
+            if constexpr (C::UC) {
+                // sum_k x u = sum_k x w + sum_k x (padding rows hold u = 1 and
+                // cancel too); the row sums are the same in every column
+#pragma unroll
+                for (int s = 0; s < C::S; ++s)
+#pragma unroll
+                    for (int mb = 0; mb < C::MBW; ++mb) acc[s][mb] -= rsum[mb];
+#pragma unroll
+                for (int mb = 0; mb < C::MBW; ++mb) rsum[mb] = i32x4{0, 0, 0, 0};
+            }
             GemmDesc d = bc.d;
             asm volatile("" : "+s"(d.N), "+s"(d.M), "+s"(d.y), "+s"(d.acc), "+s"(d.y16), "+s"(d.resid),
                          "+s"(d.w_scale), "+s"(d.w_mag));
