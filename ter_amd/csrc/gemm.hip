@@ -35,6 +35,7 @@ namespace {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int row_sum16(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
@@ -489,15 +490,42 @@ __global__ __launch_bounds__(kSThreads) void gemm_stream_kernel(GemmDesc single,
 #pragma unroll
                     for (int i = 0; i < kSBatch; ++i) asm volatile("" :: "v"(wa[i]));
                 }
-                // four buffered strips of one row per store (256 contiguous bytes);
-                // a wave reads back only its own LDS writes
-                for (int s0 = 0; s0 < p.nbuf; s0 += 4) {
-                    const int sb = s0 + (lane >> 4);
-                    const int col = (w_a + st_flush + sb) * kStripCols + (lane & 15);
-                    if (sb < p.nbuf && col < d.N) {
-                        const int* ob = obuf + sb * d.M * kStripCols + (lane & 15);
-                        for (int row = 0; row < d.M; ++row)
-                            emit_out(d, (long long)row * d.N + col, ob[row * kStripCols], xs_l[row]);
+                // A wave reads back only its own LDS writes.  fp32 / int32
+                // outputs with N a multiple of 4: lane (row r0 + lane / 16,
+                // strip s0 + lane % 16 / 4, columns 4 (lane % 4) .. +3), 16
+                // bytes per lane, four rows of four strips per store (the
+                // address unit takes a store in about the same time whatever
+                // its width).  Other forms: four strips of one row per store.
+                const bool vec_out = !d.y16 && !d.resid && (d.N & 3) == 0 &&
+                                     ((reinterpret_cast<uintptr_t>(d.y) | reinterpret_cast<uintptr_t>(d.acc)) & 15) == 0;
+                if (vec_out) {
+                    for (int s0 = 0; s0 < p.nbuf; s0 += 4) {
+                        const int sb = s0 + ((lane & 15) >> 2);
+                        const int col = (w_a + st_flush + sb) * kStripCols + (lane & 3) * 4;
+                        for (int r0 = 0; r0 < d.M; r0 += 4) {
+                            const int row = r0 + (lane >> 4);
+                            if (sb < p.nbuf && row < d.M && col < d.N) {
+                                const i32x4 v = *reinterpret_cast<const i32x4*>(obuf + (sb * d.M + row) * kStripCols +
+                                                                                (lane & 3) * 4);
+                                const long long o = (long long)row * d.N + col;
+                                const float sc = xs_l[row];
+                                if (d.acc) *reinterpret_cast<TER_GLOBAL i32x4*>(gptr(d.acc) + o) = v;
+                                if (d.y)
+                                    *reinterpret_cast<TER_GLOBAL f32x4*>(gptr(d.y) + o) =
+                                        f32x4{acc_to_float(v[0], d.w_mag) * sc, acc_to_float(v[1], d.w_mag) * sc,
+                                              acc_to_float(v[2], d.w_mag) * sc, acc_to_float(v[3], d.w_mag) * sc};
+                            }
+                        }
+                    }
+                } else {
+                    for (int s0 = 0; s0 < p.nbuf; s0 += 4) {
+                        const int sb = s0 + (lane >> 4);
+                        const int col = (w_a + st_flush + sb) * kStripCols + (lane & 15);
+                        if (sb < p.nbuf && col < d.N) {
+                            const int* ob = obuf + sb * d.M * kStripCols + (lane & 15);
+                            for (int row = 0; row < d.M; ++row)
+                                emit_out(d, (long long)row * d.N + col, ob[row * kStripCols], xs_l[row]);
+                        }
                     }
                 }
                 st_flush = p.strip;

@@ -428,7 +428,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
             // lane: the address unit takes a store in about the same time
             // whatever its width (4 lanes per cycle), and dword stores of a
             // block's outputs cost more of it than the block's loads.
-            const bool vec_out = !d.y16 && !d.resid && d.w_mag == 1 && (d.N & 3) == 0 &&
+            const bool vec_out = !d.y16 && !d.resid && (d.N & 3) == 0 &&
                                  ((reinterpret_cast<uintptr_t>(d.y) | reinterpret_cast<uintptr_t>(d.acc)) & 15) == 0;
             if (vec_out) {
 #pragma unroll
@@ -446,7 +446,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
                             if (d.acc) *reinterpret_cast<TER_GLOBAL i32x4*>(gptr(d.acc) + o) = v;
                             if (d.y)
                                 *reinterpret_cast<TER_GLOBAL f32x4*>(gptr(d.y) + o) =
-                                    f32x4{(float)v[0] * sc, (float)v[1] * sc, (float)v[2] * sc, (float)v[3] * sc};
+                                    f32x4{acc_to_float(v[0], d.w_mag) * sc, acc_to_float(v[1], d.w_mag) * sc,
+                                          acc_to_float(v[2], d.w_mag) * sc, acc_to_float(v[3], d.w_mag) * sc};
                         }
                     }
                 }
