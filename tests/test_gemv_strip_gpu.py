@@ -82,6 +82,15 @@ def test_four_strips_per_workgroup(cuda, K):
     run_list([(K, 16 * 333 - 4), (K, 16 * 334), (K, 16 * 333 + 4)], seed=7 + K, fp32=True)
 
 
+@pytest.mark.parametrize("fp32", [False, True], ids=["int8", "fp32"])
+def test_descriptor_table_lists(cuda, fp32):
+    """Strip-mode lists of four, five and six GEMVs (descriptor table lookups
+    across several GEMV boundaries), ragged N."""
+    run_list([(2560, 640 + 16 * i - (4 if i % 2 else 0)) for i in range(4)], seed=21, fp32=fp32)
+    run_list([(2560, 640 + 16 * i - (4 if i % 2 else 0)) for i in range(5)], seed=22, fp32=fp32)
+    run_list([(1024, 300 + 32 * i) for i in range(6)], seed=23, fp32=fp32)
+
+
 def test_decode_shaped_lists(cuda):
     """The decode step's lists: Q/K/V, O, gate/up (864 strips: strip mode),
     down (BitNet-2B shapes); and a list just past strip mode (1056 strips:
