@@ -115,7 +115,7 @@ typedef struct ter_hip_act {
 } ter_hip_act_t;
 
 /* Outputs of one GEMV / GEMM; any subset, at least one non-NULL.  With
- * y = float(acc) * (x_scale * w->scale):
+ * y = float(m * acc) * (x_scale * w->scale), m = w->mag (1 for plain trits):
  *   y     fp32 [M][N]
  *   acc   int32 [M][N]
  *   y16   fp16 bits [M][N] = half(y), round to nearest even: the reference's
@@ -176,7 +176,7 @@ int ter_hip_pack_payload(ter_hip_wpk_t* w, const int32_t* payload_host, float sc
 /* M = 1 decode GEMV                                                       */
 /* ---------------------------------------------------------------------- */
 
-/* y[j] = float(acc[j]) * (x_scale * w->scale), acc[j] = sum_k x[k] * w[k][j].
+/* y[j] = float(m * acc[j]) * (x_scale * w->scale), acc[j] = sum_k x[k] * w[k][j], m = w->mag.
  * y (fp32 [N]) and acc (int32 [N]) are optional device outputs (at least one). */
 int ter_hip_gemv(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int32_t* acc,
                  void* stream);
@@ -262,7 +262,7 @@ void ter_hip_plan_destroy(ter_hip_plan_t* plan);
 /* mm_packed_batched, cuda/ter_cuda_addonly_batched.cu:31-124)              */
 /* ---------------------------------------------------------------------- */
 
-/* Y[m][j] = float(acc[m][j]) * (x_scale[m] * w->scale).  x->data is [M][K];
+/* Y[m][j] = float(w->mag * acc[m][j]) * (x_scale[m] * w->scale).  x->data is [M][K];
  * for X_F32 each row is quantized by absmax (quant_int8_k steps) into
  * `x->q_out` / `x->scale_out` (both REQUIRED for X_F32, [M][K] / [M]).  For
  * X_I8, x->scale_dev ([M]) is required.  M up to TER_HIP_M_MAX; above 128

@@ -4,7 +4,7 @@
 // cuda/ter_cuda_packed_batched.cu:26-83; mm_bitnet_addonly_batched_k<M>,
 // cuda/ter_cuda_addonly_batched.cu:31-124; the wmma s4 mm_int4_tc*).
 // Semantics: acc[m][j] = sum_k X[m][k] w[k][j] (exact int32) and
-// y[m][j] = float(acc[m][j]) * (x_scale[m] * w_scale)
+// y[m][j] = float(mag * acc[m][j]) * (x_scale[m] * w_scale), mag the payload magnitude
 // (cuda/ter_cuda_addonly_batched.cu:117-123).
 //
 // Input is the same T16 tile stream as the GEMV (common.h).  Work is a list

@@ -2,7 +2,7 @@
 // fed through an LDS ring by direct global->LDS loads.
 //
 // Same semantics as gemm.hip (cuda/ter_cuda_addonly_batched.cu:117-123):
-// acc[m][j] = sum_k X[m][k] w[k][j] in exact int32, y = float(acc) * (xs[m] * w_scale).
+// acc[m][j] = sum_k X[m][k] w[k][j] in exact int32, y = float(mag * acc) * (xs[m] * w_scale).
 //
 // Work.  A block is BS consecutive column strips of one GEMM (all M rows,
 // all K).  The blocks of a launch are split over the workgroups in contiguous

@@ -5,7 +5,7 @@
 // cuda/ter_cuda_forward_bitnet.cu:497-559; v12/v13 variants) with one
 // kernel that streams the T16 tile layout (common.h).  Results are the
 // reference's: acc[j] = sum_k x[k] * w[k][j] in exact integers and
-// y[j] = float(acc[j]) * (x_scale * w_scale) (src/tx/forward.cpp:342-345,
+// y[j] = float(mag * acc[j]) * (x_scale * w_scale), mag the payload magnitude (src/tx/forward.cpp:342-345,
 // cuda/ter_cuda_forward_packed.cu:353,393).
 //
 // Work distribution.  All GEMVs of a launch form one stream of 1 KiB tiles.
