@@ -23,12 +23,11 @@
 // That holds with the epilogue's stores in flight too (stores may complete
 // out of order with respect to loads, but a wait that leaves only the younger
 // loads outstanding waits for them as well), so a block's epilogue needs no
-// drain.  Up to M = 32 (PW > 0) four producer waves issue all the loads and
-// the 8 compute waves issue none: the memory pipeline accepts only so many
-// loads in flight, and a wave that stalls at its loads holds back nothing
-// behind it in issue order (measured at M = 32: 154 -> 145 us per C4 launch).
-// Above, the 8 compute waves' registers leave no room for more waves, and
-// they issue the loads themselves after the barrier.
+// drain.  Four producer waves (PW > 0) issue all the loads and the 8 compute
+// waves issue none: the memory pipeline accepts only so many loads in
+// flight, and a wave that stalls at its loads holds back nothing behind it
+// in issue order (measured at M = 32: 154 -> 145 us per C4 launch).  With
+// PW = 0 the compute waves issue the loads themselves after the barrier.
 //
 // Operands.  X rows sit in LDS as 256-byte rows whose 16-byte chunks are
 // XOR-swizzled by the row's low 4 bits (chunk c of row r at position
@@ -95,23 +94,38 @@ struct LCfg {
 #endif
     static constexpr bool UC = MBW <= TER_LDS_UC_MB;
     static_assert(NST >= 2 && NST <= 4, "stage count");
+    static_assert(LDS <= kLdsMax, "LDS budget");
 };
 
-// The configuration per row-block count (M <= 16, 32, 64, 128), measured on the
-// BitNet-2B sweep: every wave covers all rows (RS = 1); 2 strips per wave at
-// M <= 16 (16-strip blocks, 60 KiB for three stages: two workgroups per CU,
-// 116.7 against 122.9 us with 4 strips and one), 4 above (32-strip blocks, X
-// staged once per 32 weight tiles); three stages up to M = 32, two above.
+// The configuration per row-block count (M <= 16, 32, 64, 128) as
+// (MBW, S, RS, NST, PW), measured on the BitNet-2B sweep (C4): every wave
+// covers all rows (RS = 1) and four producer waves issue the loads.  At 64
+// and 128 rows the blocks are 16 strips (2 per wave): the compute waves'
+// accumulators then fit 168 VGPRs, which leaves room for the producers, and
+// the smaller stages a third ring stage (M = 128: 325 -> 284 us against
+// 32-strip blocks of 8 compute waves that issued their own loads; M = 64:
+// 200 -> 180 us); 32-strip blocks at M = 32 (2 per wave: 142 against 138 us);
+// four stages at M = 16 (124 -> 120 us).  (Each can be overridden at build
+// time.)
 #ifndef TER_LDS_PW
 #define TER_LDS_PW 4
 #endif
-using Cfg1 = LCfg<1, 2, 1, 3, TER_LDS_PW>;
-using Cfg2 = LCfg<2, 4, 1, 3, TER_LDS_PW>;
-#ifndef TER_LDS_PW4
-#define TER_LDS_PW4 0
+#ifndef TER_LDS_CFG1
+#define TER_LDS_CFG1 1, 2, 1, 4, TER_LDS_PW
 #endif
-using Cfg4 = LCfg<4, 4, 1, 2, TER_LDS_PW4>;
-using Cfg8 = LCfg<8, 4, 1, 2>;
+#ifndef TER_LDS_CFG2
+#define TER_LDS_CFG2 2, 4, 1, 3, TER_LDS_PW
+#endif
+using Cfg1 = LCfg<TER_LDS_CFG1>;
+using Cfg2 = LCfg<TER_LDS_CFG2>;
+#ifndef TER_LDS_CFG4
+#define TER_LDS_CFG4 4, 2, 1, 3, 4
+#endif
+#ifndef TER_LDS_CFG8
+#define TER_LDS_CFG8 8, 2, 1, 3, 4
+#endif
+using Cfg4 = LCfg<TER_LDS_CFG4>;
+using Cfg8 = LCfg<TER_LDS_CFG8>;
 
 // s_waitcnt immediate (gfx9 family): vmcnt(n), expcnt and lgkmcnt not waited on.
 template <int N>
