@@ -112,8 +112,6 @@ __device__ __forceinline__ void pair_index(int k, int hd, bool neox, int& i0, in
     i1 = neox ? k + hd / 2 : 2 * k + 1;
 }
 
-__device__ __forceinline__ int uniform_i(int v) { return __builtin_amdgcn_readfirstlane(v); }
-
 template <int kCtrl>
 __device__ __forceinline__ float dpp_f(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
@@ -373,31 +371,35 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a_in
     // partials are read with buffer loads that miss any stale copy (L1 for
     // the XCD-local exchange: SC0; L1 and this XCD's L2 otherwise: SC1);
     // chunks past nc are out of the buffer's range and read as zeros.  Lane c
-    // holds chunk c's (m_c, l_c); the output partials go in groups of 8
-    // chunks, the loads of one group in flight while the previous is added.
+    // holds chunk c's (m_c, l_c).  Every load is issued before the first
+    // add (groups of 8 chunks, each group behind a wave-uniform test of nc),
+    // so the chain waits for one round trip, not one per group.
     const int nc = (seq + kChunk - 1) / kChunk;
     const float* Ph = a.part + (long long)(h0 + wave) * a.n_chunks * PST;
     const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc((void*)Ph, 0, nc * PST * 4, 0x00020000);
     constexpr int kCoh = kLocal ? 1 : 16;  // cache policy: SC0 / SC1
     constexpr int G = 8;                   // chunks per group
-    auto load_group = [&](int gi, float (&pg)[G][DPT]) {
-#pragma unroll
-        for (int c = 0; c < G; ++c) {
-            const int off = ((gi * G + c) * PST + d0) * 4;
-            if constexpr (DPT == 2) {
-                const unsigned long long w2 =
-                    __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(pr, off, 0, kCoh));
-                pg[c][0] = __builtin_bit_cast(float, (unsigned)w2);
-                pg[c][1] = __builtin_bit_cast(float, (unsigned)(w2 >> 32));
-            } else {
-                pg[c][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, kCoh));
-            }
-        }
-    };
+    constexpr int NG = kMaxChunks / G;
     const unsigned long long ml =
         __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(pr, (lane * PST + HD) * 4, 0, kCoh));
-    float pa[G][DPT], pb[G][DPT];
-    load_group(0, pa);
+    float pg[NG][G][DPT];
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi) {
+        if (gi * G < nc) {
+#pragma unroll
+            for (int c = 0; c < G; ++c) {
+                const int off = ((gi * G + c) * PST + d0) * 4;
+                if constexpr (DPT == 2) {
+                    const unsigned long long w2 = __builtin_bit_cast(
+                        unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(pr, off, 0, kCoh));
+                    pg[gi][c][0] = __builtin_bit_cast(float, (unsigned)w2);
+                    pg[gi][c][1] = __builtin_bit_cast(float, (unsigned)(w2 >> 32));
+                } else {
+                    pg[gi][c][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, off, 0, kCoh));
+                }
+            }
+        }
+    }
     const float m_l = lane < nc ? __builtin_bit_cast(float, (unsigned)ml) : -__builtin_inff();
     const float M = wave_max_f(m_l);
     // lane c's weight and sum, read with v_readlane (a uniform lane per step)
@@ -407,25 +409,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a_in
     float O[DPT];
 #pragma unroll
     for (int j = 0; j < DPT; ++j) O[j] = 0.f;
-    // chunks past nc have w = 0 and o = 0: exact no-ops.  Two groups per
-    // step with no exit between them; at most 64 chunks, so every lane index
-    // read below is < 64.
-    auto add_group = [&](int gi, const float (&pg)[G][DPT]) {
+    // chunks past nc in the last group have w = 0 and o = 0: exact no-ops;
+    // at most 64 chunks, so every lane index read below is < 64
 #pragma unroll
-        for (int c = 0; c < G; ++c) {
-            const int src = uniform_i(gi * G + c);
-            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(w_bits, src));
-            L = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(l_bits, src)), w, L);
+    for (int gi = 0; gi < NG; ++gi) {
+        if (gi * G < nc) {
 #pragma unroll
-            for (int j = 0; j < DPT; ++j) O[j] = __builtin_fmaf(pg[c][j], w, O[j]);
+            for (int c = 0; c < G; ++c) {
+                const int src = gi * G + c;
+                const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(w_bits, src));
+                L = __builtin_fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(l_bits, src)), w, L);
+#pragma unroll
+                for (int j = 0; j < DPT; ++j) O[j] = __builtin_fmaf(pg[gi][c][j], w, O[j]);
+            }
         }
-    };
-    const int ng = (nc + G - 1) / G;
-    for (int gi = 0; gi < ng; gi += 2) {
-        load_group(gi + 1, pb);
-        add_group(gi, pa);
-        load_group(gi + 2, pa);
-        add_group(gi + 1, pb);
     }
     uint16_t* oh = a.out + (long long)(h0 + wave) * HD + d0;
 #pragma unroll
