@@ -13,6 +13,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <queue>
 #include <new>
 #include <string>
 #include <vector>
@@ -512,17 +513,49 @@ static int scratch_of_current_device(unsigned char** out) {
     return TER_HIP_OK;
 }
 
-// Device copy of an LDS-ring GEMM plan: descriptors, the block list, and the
-// per-workgroup block ranges, balanced by 256-row units: range g holds the
-// blocks whose first unit lies in [total * g / n_wg, total * (g + 1) / n_wg).
-int upload_lds_plan(ter_hip_plan* p, const std::vector<GemmDesc>& ds, const std::vector<GemmBlock>& blocks,
-                    const std::vector<long long>& unit0, long long total_units, int n_wg) {
+// Device copy of an LDS-ring GEMM plan: descriptors, the block list in
+// workgroup order, and the per-workgroup block ranges.  Range g holds
+// workgroup g's blocks in the order it runs them.  The blocks are dealt out
+// largest first, each to the workgroup that would be free first (list
+// scheduling; ties to the lowest workgroup).  The order is a stable sort by
+// estimated cost, so blocks of one size stay in list order, and neighbouring
+// blocks run at about the same time on neighbouring workgroups, which the
+// kernel places on one XCD: the weight runs and output rows in flight at
+// any moment lie close together in memory.  The cost of a block of ns
+// strips over Ku 256-row units, in units of one full stage: Ku (0.3 + 0.7 ns
+// / bs) (a stage's barrier and X rows cost the same at any width), plus one
+// for the epilogue.  Against contiguous ranges balanced by units (the
+// largest range 15% above the mean at 16 rows, 37% at 32 rows) this keeps
+// every range within about 5% of the mean.
+int upload_lds_plan(ter_hip_plan* p, const std::vector<GemmDesc>& ds, const std::vector<GemmBlock>& blocks_in,
+                    int bs, int n_wg) {
+    const size_t nb = blocks_in.size();
+    std::vector<double> cost(nb);
+    for (size_t b = 0; b < nb; ++b) {
+        const GemmDesc& d = ds[(size_t)blocks_in[b].desc];
+        const int ns = std::min(bs, d.n_strips - blocks_in[b].strip0);
+        cost[b] = d.Ku * (0.3 + 0.7 * ns / bs) + 1.0;
+    }
+    std::vector<int32_t> order(nb);
+    for (size_t b = 0; b < nb; ++b) order[b] = (int32_t)b;
+    std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t b) { return cost[(size_t)a] > cost[(size_t)b]; });
+    std::vector<std::vector<int32_t>> per_wg((size_t)n_wg);
+    using Slot = std::pair<double, int>;  // (time the workgroup is free, workgroup)
+    std::priority_queue<Slot, std::vector<Slot>, std::greater<Slot>> free_at;
+    for (int g = 0; g < n_wg; ++g) free_at.push(Slot{0.0, g});
+    for (const int32_t b : order) {
+        Slot s = free_at.top();
+        free_at.pop();
+        per_wg[(size_t)s.second].push_back(b);
+        s.first += cost[(size_t)b];
+        free_at.push(s);
+    }
+    std::vector<GemmBlock> blocks;
+    blocks.reserve(nb);
     std::vector<int32_t> ranges((size_t)n_wg + 1);
-    size_t b = 0;
-    for (int g = 0; g <= n_wg; ++g) {
-        const long long t = total_units * g / n_wg;
-        while (b < blocks.size() && unit0[b] < t) ++b;
-        ranges[(size_t)g] = (int32_t)b;
+    for (int g = 0; g < n_wg; ++g) {
+        ranges[(size_t)g] = (int32_t)blocks.size();
+        for (const int32_t b : per_wg[(size_t)g]) blocks.push_back(blocks_in[(size_t)b]);
     }
     ranges[(size_t)n_wg] = (int32_t)blocks.size();
     const size_t db = sizeof(GemmDesc) * ds.size(), bb = sizeof(GemmBlock) * blocks.size();
@@ -1162,19 +1195,12 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
     int rc;
     if (lbs > 0) {
-        // LDS-ring kernel: blocks of lbs strips, balanced by units
+        // LDS-ring kernel: blocks of lbs strips, dealt out by list scheduling
         std::vector<GemmBlock> bl;
-        std::vector<long long> unit0;
-        long long units = 0;
-        for (int i = 0; i < n; ++i) {
-            for (int st = 0; st < ds[(size_t)i].n_strips; st += lbs) {
-                bl.push_back(GemmBlock{i, st});
-                unit0.push_back(units);
-                units += ds[(size_t)i].Ku;
-            }
-        }
+        for (int i = 0; i < n; ++i)
+            for (int st = 0; st < ds[(size_t)i].n_strips; st += lbs) bl.push_back(GemmBlock{i, st});
         rc = pick_lds_wg((long long)bl.size(), mb, &n_wg);
-        if (!rc) rc = upload_lds_plan(p, ds, bl, unit0, units, n_wg);
+        if (!rc) rc = upload_lds_plan(p, ds, bl, lbs, n_wg);
     } else {
         rc = stream ? pick_stream_wg(tiles, slds, wg_per_cu, &n_wg) : pick_gemm_wg(blocks, mb, wg_per_cu, &n_wg);
         if (!rc) rc = stream ? upload_plan(p, ds, tile_starts, tiles, n_wg) : upload_plan(p, ds, block_starts, blocks, n_wg);

@@ -93,7 +93,7 @@ struct LCfg {
 #define TER_LDS_UC_MB 2
 #endif
     static constexpr bool UC = MBW <= TER_LDS_UC_MB;
-    static_assert(NST >= 2 && NST <= 4, "stage count");
+    static_assert(NST >= 2 && NST <= 8, "stage count");
     static_assert(LDS <= kLdsMax, "LDS budget");
 };
 
@@ -145,14 +145,15 @@ __device__ __forceinline__ void lds_barrier() {
 // Wait until this wave's loads of the unit `behind` stages older than the
 // newest issued one have landed: `behind` = stages issued after it (0..NST-2),
 // each holding N of this wave's loads.
-template <class C, int N>
+template <class C, int N, int B = C::NST - 2>
 __device__ __forceinline__ void wait_stage_n(int behind) {
-    if (C::NST >= 4 && behind >= 2) {
-        wait_vm<(C::NST >= 4 ? 2 : 0) * N>();
-    } else if (C::NST >= 3 && behind >= 1) {
-        wait_vm<N>();
-    } else {
+    if constexpr (B == 0) {
         wait_vm<0>();
+    } else {
+        if (behind >= B)
+            wait_vm<B * N>();
+        else
+            wait_stage_n<C, N, B - 1>(behind);
     }
 }
 
