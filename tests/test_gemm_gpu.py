@@ -163,6 +163,16 @@ def test_gemm_plan_small_m(cuda, specs):
     run_plan(specs, 700, (0, 1, 2))
 
 
+@pytest.mark.parametrize("M", [16, 32, 128])
+def test_gemm_plan_list_schedule(cuda, M):
+    """LDS-ring plans whose blocks the host deals out largest first: K = 6912
+    blocks (27 units) first, then K = 2560, then many one-unit blocks (K =
+    256) back to back at the end of each workgroup's list, partial blocks at
+    every ragged N, at several launch shapes (each a different schedule)."""
+    run_plan([(M, 6912, 2560), (M, 256, 640), (M, 256, 48), (M, 512, 4000), (M, 256, 1024), (M, 2560, 256),
+              (M, 256, 4096)], 1300 + M, (0, 1, 2))
+
+
 @pytest.mark.parametrize("specs", [
     [(2, 256, 1 << 20)],                   # Ku = 1: 16-strip output buffers, 12-tile chunks, ~64 strips per wave
     [(8, 2560, 131064), (8, 6912, 2560)],  # M = 8 beside K = 6912: 5-strip buffers, 36-tile chunks, ragged last strip
