@@ -53,6 +53,7 @@ namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 #define TER_LDS __attribute__((address_space(3)))
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -445,7 +446,31 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
             // block's outputs cost more of it than the block's loads.
             const bool vec_out = !d.y16 && !d.resid && (d.N & 3) == 0 &&
                                  ((reinterpret_cast<uintptr_t>(d.y) | reinterpret_cast<uintptr_t>(d.acc)) & 15) == 0;
-            if (vec_out) {
+            // The common form, fp32 y only with payload magnitude 1 and an
+            // output of at most 2 GiB: buffer stores at 32-bit offsets, lanes
+            // outside the matrix sent to offset 2^31, past the buffer's range
+            // (the hardware drops them), so no store needs a branch or a
+            // 64-bit address (the general form below takes 20 or more
+            // instructions a store, and the matrix cores idle meanwhile).
+            const bool fast_y = vec_out && d.y && !d.acc && d.w_mag == 1 && (long long)d.M * d.N <= (1LL << 29);
+            if (fast_y) {
+                const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+                    (void*)d.y, 0, (int)((unsigned)d.M * (unsigned)d.N * 4u), 0x00020000);
+#pragma unroll
+                for (int mb = 0; mb < C::MBW; ++mb) {
+                    const int row = (rg * C::MBW + mb) * 16 + g * 4 + (lane & 3);
+                    const float sc = xs_l[row] * d.w_scale;
+                    const unsigned row_off = (unsigned)row * (unsigned)d.N;
+#pragma unroll
+                    for (int s = 0; s < C::S; ++s) {
+                        const i32x4 v = quad_transpose(acc[s][mb], lane);
+                        const int col = (bc.st0 + sg * C::S + s) * kStripCols + (j & ~3);
+                        const unsigned off = row < d.M && col < d.N ? (row_off + (unsigned)col) * 4u : 0x80000000u;
+                        const f32x4 y = f32x4{(float)v[0] * sc, (float)v[1] * sc, (float)v[2] * sc, (float)v[3] * sc};
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, y), yr, (int)off, 0, 0);
+                    }
+                }
+            } else if (vec_out) {
 #pragma unroll
                 for (int mb = 0; mb < C::MBW; ++mb) {
                     // after the transpose lane (j, g) holds row 4 g + j % 4 of

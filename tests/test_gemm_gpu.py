@@ -105,9 +105,10 @@ def test_quant_int8_kernel(cuda):
     assert (host(s).view(np.int32) == rs.view(np.int32)).all()
 
 
-def run_plan(specs, seed, wgs):
+def run_plan(specs, seed, wgs, with_acc=True):
     """Build a GemmPlan over `specs`, launch it twice per launch shape and
-    compare every item with the oracle (outputs poisoned between launches)."""
+    compare every item with the oracle (outputs poisoned between launches).
+    with_acc=False: fp32 outputs only (the kernels' store path for that form)."""
     import torch
     import ter_amd as T
     items, refs = [], []
@@ -117,18 +118,20 @@ def run_plan(specs, seed, wgs):
         xs = (0.002 * (np.arange(M) + 1 + i)).astype(np.float32)
         W = T.PackedTrits.from_v11(v11, K, N, 0.03 + 0.01 * i)
         y = torch.empty((M, N), dtype=torch.float32, device="cuda")
-        acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+        acc = torch.empty((M, N), dtype=torch.int32, device="cuda") if with_acc else None
         items.append(dict(w=W, x=dev(X), x_scale_dev=dev(xs), y=y, acc=acc))
         refs.append(O.gemm_v11(X, xs, v11, 0.03 + 0.01 * i, K, N))
     for wg_per_cu in wgs:
         plan = T.GemmPlan(items, wg_per_cu=wg_per_cu)
         for rep in range(2):
             for it in items:
-                it["acc"].fill_(-9)
+                if with_acc:
+                    it["acc"].fill_(-9)
                 it["y"].fill_(-9)
             plan.launch()
             for it, (ra, ry) in zip(items, refs):
-                assert (host(it["acc"]) == ra).all(), (wg_per_cu, rep, it["w"].K, it["w"].N)
+                if with_acc:
+                    assert (host(it["acc"]) == ra).all(), (wg_per_cu, rep, it["w"].K, it["w"].N)
                 assert_f32_equal(host(it["y"]), ry)
         plan.close()
 
@@ -163,14 +166,17 @@ def test_gemm_plan_small_m(cuda, specs):
     run_plan(specs, 700, (0, 1, 2))
 
 
-@pytest.mark.parametrize("M", [16, 32, 128])
-def test_gemm_plan_list_schedule(cuda, M):
+@pytest.mark.parametrize("M", [16, 32, 100, 128])
+@pytest.mark.parametrize("with_acc", [True, False], ids=["y_and_acc", "y_only"])
+def test_gemm_plan_list_schedule(cuda, M, with_acc):
     """LDS-ring plans whose blocks the host deals out largest first: K = 6912
     blocks (27 units) first, then K = 2560, then many one-unit blocks (K =
     256) back to back at the end of each workgroup's list, partial blocks at
-    every ragged N, at several launch shapes (each a different schedule)."""
+    every ragged N, ragged M (100 rows: lanes past the last row store
+    nothing), with and without int32 outputs (fp32 outputs alone take the
+    branch-free store path)."""
     run_plan([(M, 6912, 2560), (M, 256, 640), (M, 256, 48), (M, 512, 4000), (M, 256, 1024), (M, 2560, 256),
-              (M, 256, 4096)], 1300 + M, (0, 1, 2))
+              (M, 256, 4096)], 1300 + M, (0,), with_acc)
 
 
 @pytest.mark.parametrize("specs", [
