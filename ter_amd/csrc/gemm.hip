@@ -36,6 +36,7 @@ namespace {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int row_sum16(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);
@@ -498,7 +499,29 @@ __global__ __launch_bounds__(kSThreads) void gemm_stream_kernel(GemmDesc single,
                 // its width).  Other forms: four strips of one row per store.
                 const bool vec_out = !d.y16 && !d.resid && (d.N & 3) == 0 &&
                                      ((reinterpret_cast<uintptr_t>(d.y) | reinterpret_cast<uintptr_t>(d.acc)) & 15) == 0;
-                if (vec_out) {
+                // fp32 y only, payload magnitude 1, output of at most 2 GiB:
+                // buffer stores at 32-bit offsets, lanes outside the matrix
+                // sent to offset 2^31, past the buffer's range (dropped), so
+                // no store needs a branch or a 64-bit address
+                const bool fast_y = vec_out && d.y && !d.acc && d.w_mag == 1 && (long long)d.M * d.N <= (1LL << 29);
+                if (fast_y) {
+                    const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
+                        (void*)d.y, 0, (int)((unsigned)d.M * (unsigned)d.N * 4u), 0x00020000);
+                    for (int s0 = 0; s0 < p.nbuf; s0 += 4) {
+                        const int sb = s0 + ((lane & 15) >> 2);
+                        const int col = (w_a + st_flush + sb) * kStripCols + (lane & 3) * 4;
+                        for (int r0 = 0; r0 < d.M; r0 += 4) {
+                            const int row = r0 + (lane >> 4);
+                            const bool ok = sb < p.nbuf && row < d.M && col < d.N;
+                            const i32x4 v = *reinterpret_cast<const i32x4*>(
+                                obuf + (min(sb, p.nbuf - 1) * d.M + min(row, d.M - 1)) * kStripCols + (lane & 3) * 4);
+                            const float sc = xs_l[min(row, d.M - 1)];
+                            const unsigned off = ok ? ((unsigned)row * (unsigned)d.N + (unsigned)col) * 4u : 0x80000000u;
+                            const f32x4 y = f32x4{(float)v[0] * sc, (float)v[1] * sc, (float)v[2] * sc, (float)v[3] * sc};
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, y), yr, (int)off, 0, 0);
+                        }
+                    }
+                } else if (vec_out) {
                     for (int s0 = 0; s0 < p.nbuf; s0 += 4) {
                         const int sb = s0 + ((lane & 15) >> 2);
                         const int col = (w_a + st_flush + sb) * kStripCols + (lane & 3) * 4;

@@ -182,13 +182,15 @@ def test_gemm_plan_list_schedule(cuda, M, with_acc):
 @pytest.mark.parametrize("specs", [
     [(2, 256, 1 << 20)],                   # Ku = 1: 16-strip output buffers, 12-tile chunks, ~64 strips per wave
     [(8, 2560, 131064), (8, 6912, 2560)],  # M = 8 beside K = 6912: 5-strip buffers, 36-tile chunks, ragged last strip
-], ids=["ku1_long_runs", "m8_bitnet_k"])
-def test_gemm_stream_chunks(cuda, specs):
+    [(3, 2560, 6000), (7, 2048, 1000), (16, 512, 4096)],  # ragged M: lanes past the last row store nothing
+], ids=["ku1_long_runs", "m8_bitnet_k", "ragged_m"])
+@pytest.mark.parametrize("with_acc", [True, False], ids=["y_and_acc", "y_only"])
+def test_gemm_stream_chunks(cuda, specs, with_acc):
     """The streamed kernel (M <= 16 where the X image and the output buffers
     fit): at one workgroup per CU each wave's run spans several chunks, so
     completed strips are buffered in LDS and written between chunks many
-    times per wave."""
-    run_plan(specs, 1300, (1,))
+    times per wave; fp32 outputs alone take the branch-free store path."""
+    run_plan(specs, 1300, (1,), with_acc)
 
 
 @pytest.mark.parametrize("M", [8, 32, 128])
