@@ -1348,7 +1348,7 @@ int ter_hip_attn_create(ter_hip_attn_t** out, int32_t n_heads, int32_t n_kv_head
     if (!(theta > 0.f)) return fail(TER_HIP_ERR_SHAPE, "RoPE theta must be > 0");
     const int half = head_dim / 2;
     const int n_chunks = (s_max + attn_chunk() - 1) / attn_chunk();
-    const int groups = n_kv_heads * ((n_heads / n_kv_heads + 3) / 4);
+    const int groups = attn_head_groups(n_heads, n_kv_heads);
     // RoPE table: the reference's float steps (rope_k), powf / cosf / sinf
     // replaced by libm in double rounded once to binary32
     std::vector<float> tab;

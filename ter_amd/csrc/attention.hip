@@ -44,7 +44,7 @@
 namespace terhip {
 namespace {
 
-constexpr int kAttnWaves = 4;
+constexpr int kAttnWaves = 4;  // query heads per workgroup (one wave each)
 constexpr int kAttnThreads = kAttnWaves * 64;
 constexpr int kChunk = 64;       // positions per chunk (one per lane)
 constexpr int kMaxChunks = 64;   // combine: one lane per chunk
@@ -462,8 +462,10 @@ __global__ void xcc_probe_kernel(int* out) {
 bool attn_supported_head_dim(int hd) { return hd == 64 || hd == 128; }
 int attn_part_stride(int hd) { return part_stride(hd); }
 int attn_count_stride() { return kCountStride; }
+int attn_head_groups(int nh, int nkv) { return nkv * ((nh / nkv + kAttnWaves - 1) / kAttnWaves); }
+
 int attn_local_blocks(int nh, int nkv, int smax) {
-    const int groups = nkv * ((nh / nkv + kAttnWaves - 1) / kAttnWaves);
+    const int groups = attn_head_groups(nh, nkv);
     return kXcds * ((groups + kXcds - 1) / kXcds) * ((smax + kChunk - 1) / kChunk);
 }
 

@@ -151,6 +151,7 @@ int attn_count_stride();
 // Grid of the XCD-local launch, and whether blocks 0 .. n_blocks - 1 land on
 // XCD b % 8 (probed with n_blocks ints of device scratch; false on any error).
 int attn_local_blocks(int nh, int nkv, int smax);
+int attn_head_groups(int nh, int nkv);  // workgroup head groups: query heads sharing a KV head, by kAttnWaves
 bool attn_xcd_round_robin(int n_blocks, int* scratch, hipStream_t st);
 hipError_t launch_attn_decode(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc,
                               const int32_t* pos, uint16_t* out, const float* rope, float* part, unsigned* count,
