@@ -527,6 +527,7 @@ static int scratch_of_current_device(unsigned char** out) {
 // for the epilogue.  Against contiguous ranges balanced by units (the
 // largest range 15% above the mean at 16 rows, 37% at 32 rows) this keeps
 // every range within about 5% of the mean.
+constexpr long long kRingMinBlocksPerCu = 4;
 int upload_lds_plan(ter_hip_plan* p, const std::vector<GemmDesc>& ds, const std::vector<GemmBlock>& blocks_in,
                     int bs, int n_wg) {
     const size_t nb = blocks_in.size();
@@ -1190,7 +1191,22 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     for (int i = 0; i < n; ++i) slds = std::max(slds, gemm_stream_lds_want(ds[(size_t)i].M, ds[(size_t)i].K));
     bool stream = true;
     for (int i = 0; i < n && stream; ++i) stream = gemm_stream_item_fits(ds[(size_t)i].M, ds[(size_t)i].K, slds);
-    const int lbs = !stream && vec ? gemm_lds_strips_per_block(mb) : 0;
+    // The LDS-ring kernel where the streamed one does not fit, and also
+    // where the list holds at least kRingMinBlocksPerCu of its blocks per CU:
+    // dealt out by list scheduling it beats the streamed kernel on large
+    // lists (C4 at 8 rows: 95.3 against 101.7 us; at 4 rows 88.7 against
+    // 95.5 us), while a short list needs the streamed kernel's split of K
+    // to fill the GPU (a ring block covers all of K for its strips).
+    int lbs = vec ? gemm_lds_strips_per_block(mb) : 0;
+    if (lbs > 0 && stream) {
+        long long ring_blocks = 0;
+        for (int i = 0; i < n; ++i) ring_blocks += (ds[(size_t)i].n_strips + lbs - 1) / lbs;
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return fail(TER_HIP_ERR_HIP, "hipGetDevice");
+        const int cus = device_cu_count(dev);
+        if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
+        if (ring_blocks < (long long)cus * kRingMinBlocksPerCu) lbs = 0;
+    }
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
     int rc;

@@ -180,16 +180,20 @@ def test_gemm_plan_list_schedule(cuda, M, with_acc):
 
 
 @pytest.mark.parametrize("specs", [
-    [(2, 256, 1 << 20)],                   # Ku = 1: 16-strip output buffers, 12-tile chunks, ~64 strips per wave
-    [(8, 2560, 131064), (8, 6912, 2560)],  # M = 8 beside K = 6912: 5-strip buffers, 36-tile chunks, ragged last strip
+    [(2, 256, 245760)],                    # Ku = 1: 16-strip output buffers, 12-tile chunks, 15 strips per wave
+    [(8, 2560, 12000), (8, 6912, 2560)],   # M = 8 beside K = 6912: 5-strip buffers, 36-tile chunks, ragged last strip
     [(3, 2560, 6000), (7, 2048, 1000), (16, 512, 4096)],  # ragged M: lanes past the last row store nothing
-], ids=["ku1_long_runs", "m8_bitnet_k", "ragged_m"])
+    [(2, 256, 1 << 20)],                   # as long as these lists are, the LDS ring takes them (>= 4 blocks per CU)
+    [(8, 2560, 262144), (8, 6912, 2560)],
+], ids=["ku1_long_runs", "m8_bitnet_k", "ragged_m", "ring_ku1", "ring_m8"])
 @pytest.mark.parametrize("with_acc", [True, False], ids=["y_and_acc", "y_only"])
 def test_gemm_stream_chunks(cuda, specs, with_acc):
     """The streamed kernel (M <= 16 where the X image and the output buffers
-    fit): at one workgroup per CU each wave's run spans several chunks, so
-    completed strips are buffered in LDS and written between chunks many
-    times per wave; fp32 outputs alone take the branch-free store path."""
+    fit, and the list too short for the LDS ring): at one workgroup per CU each
+    wave's run spans several chunks, so completed strips are buffered in LDS
+    and written between chunks many times per wave; fp32 outputs alone take
+    the branch-free store path.  The last two lists are long enough (at least
+    4 ring blocks per CU on MI355X's 256 CUs) for the LDS ring."""
     run_plan(specs, 1300, (1,), with_acc)
 
 
