@@ -424,12 +424,13 @@ def run_batched(args):
     gbs = plan.bytes / (ev_plan * 1e-3) / 1e9
     tops = 2 * mac / (ev_plan * 1e-3) / 1e12
     hbm_bound = M <= 64
-    # the kernel the library picks (common.h, gemm_stream_item_fits): M <= 16
-    # streams when M rows of each X fit 64 KiB of LDS and the launch's LDS (the
-    # largest want of the list, at most 80 KiB) leaves each GEMM an output
-    # buffer of 12 // Ku + 1 strips; otherwise the LDS-ring kernel (16-byte
-    # aligned X rows: K here is a multiple of 16), above M = 128 over pieces
-    # of 128 rows
+    # the kernel the library picks (common.h, gemm_stream_item_fits, and
+    # ter_hip_gemm_plan_create): M <= 16 streams when M rows of each X fit 64
+    # KiB of LDS, the launch's LDS (the largest want of the list, at most 80
+    # KiB) leaves each GEMM an output buffer of 12 // Ku + 1 strips, and the
+    # list holds fewer than 4 LDS-ring blocks (16 strips; 32 at M <= 32) per
+    # CU; otherwise the LDS-ring kernel (16-byte aligned X rows: K here is a
+    # multiple of 16), above M = 128 over pieces of 128 rows
     def out_off(K):
         ku = -(-K // 256)
         return M * (ku * 16 + 1) * 16 + ku * 256 + 64 + 8192 + 64
@@ -437,7 +438,10 @@ def run_batched(args):
     fits = all(M <= 16 and M * (-(-K // 256) * 16 + 1) * 16 <= 65536 and
                min(32, max(0, lds - out_off(K)) // (4 * M * 64)) >= 12 // -(-K // 256) + 1
                for _, K, _ in cfg["shapes"])
-    kernel = "gemm_stream_kernel" if fits else "gemm_lds_kernel"
+    bs = 32 if 16 < M <= 32 else 16
+    ring_blocks = cfg["layers"] * sum(-(-(-(-N // 16)) // bs) for _, _, N in cfg["shapes"])
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    kernel = "gemm_stream_kernel" if fits and ring_blocks < 4 * cus else "gemm_lds_kernel"
     return {
         "metric": f"batched packed-trit GEMM, M={M}, BitNet-2B sweep",
         "value": round(mac / (wall * 1e-3) / 1e9, 1), "unit": "GMAC/s", "n_gpus": 1, "steps": args.steps,
