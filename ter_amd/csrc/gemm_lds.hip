@@ -454,6 +454,11 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
             // instructions a store, and the matrix cores idle meanwhile).
             const bool fast_y = vec_out && d.y && !d.acc && d.w_mag == 1 && (long long)d.M * d.N <= (1LL << 29);
             if (fast_y) {
+                // nontemporal stores at one row block per wave (M <= 16 rows:
+                // C4 M = 16 101.7 -> 97.8 us, M = 8 93.9 -> 90.5 us); with more
+                // row blocks they cost (M = 32 120.4 -> 124.6 us, M = 128
+                // 254.5 -> 264.4 us), so those keep the default policy
+                constexpr int kYPolicy = C::MBW == 1 ? 2 : 0;
                 const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
                     (void*)d.y, 0, (int)((unsigned)d.M * (unsigned)d.N * 4u), 0x00020000);
 #pragma unroll
@@ -467,7 +472,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
                         const int col = (bc.st0 + sg * C::S + s) * kStripCols + (j & ~3);
                         const unsigned off = row < d.M && col < d.N ? (row_off + (unsigned)col) * 4u : 0x80000000u;
                         const f32x4 y = f32x4{(float)v[0] * sc, (float)v[1] * sc, (float)v[2] * sc, (float)v[3] * sc};
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, y), yr, (int)off, 0, 0);
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, y), yr, (int)off, 0, kYPolicy);
                     }
                 }
             } else if (vec_out) {
