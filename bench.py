@@ -703,7 +703,7 @@ def run_decode(args):
                      "mean_launch_us": round(ev_tok * 1e3, 2)},
         "cpu_baseline": None,
     }
-
+# Per-shape table: the reference bench's five shapes
 
 # Per-shape table: the reference bench's five shapes
 # (cuda/ter_cuda_forward_packed_v13_bench.cu:422-428, the packed lm_head
