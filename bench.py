@@ -703,9 +703,9 @@ def run_decode(args):
                      "mean_launch_us": round(ev_tok * 1e3, 2)},
         "cpu_baseline": None,
     }
-# Per-shape table: the reference bench's five shapes
 
-# Per-shape table: the reference bench's five shapes
+
+# Per-shape table: the reference bench's five shapes
 # (cuda/ter_cuda_forward_packed_v13_bench.cu:422-428, the packed lm_head
 # included) and BitNet-2B's four.
 SHAPES = [("llama Wq/Wo", 2048, 2048), ("llama Wk/Wv", 2048, 512), ("llama Wgate/Wup", 2048, 8192),
