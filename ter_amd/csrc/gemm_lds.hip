@@ -95,6 +95,7 @@ struct LCfg {
 #endif
     static constexpr bool UC = MBW <= TER_LDS_UC_MB;
     static_assert(NST >= 2 && NST <= 8, "stage count");
+    static_assert(S % 2 == 0, "the fp32 epilogue stores strips in pairs");
     static_assert(LDS <= kLdsMax, "LDS budget");
 };
 
@@ -454,25 +455,44 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
             // instructions a store, and the matrix cores idle meanwhile).
             const bool fast_y = vec_out && d.y && !d.acc && d.w_mag == 1 && (long long)d.M * d.N <= (1LL << 29);
             if (fast_y) {
-                // nontemporal stores at one row block per wave (M <= 16 rows:
-                // C4 M = 16 101.7 -> 97.8 us, M = 8 93.9 -> 90.5 us); with more
-                // row blocks they cost (M = 32 120.4 -> 124.6 us, M = 128
-                // 254.5 -> 264.4 us), so those keep the default policy
-                constexpr int kYPolicy = C::MBW == 1 ? 2 : 0;
+                // Strips in pairs (2 t, 2 t + 1), whole 128-byte lines per
+                // store: after the transpose lane (j, g) holds row 4 g + j % 4
+                // of the row block, columns 4 (j / 4) .. +3 of a strip; the
+                // swap of 16-lane rows between the pair (odd rows of the
+                // first with even rows of the second) leaves in the first
+                // rows 8 (g / 2) + j % 4 and in the second 8 (g / 2) + 4 +
+                // j % 4, of strip 2 t + g % 2, so a store covers 8 rows x 2
+                // strips.  Nontemporal: with whole lines it pays at every row
+                // count (C4: M = 128 265.3 -> 255.0 us, M = 32 121.1 -> 119.7,
+                // M = 16 98.1 -> 96.1, M = 8 90.4 -> 89.8), where half lines
+                // made it cost from two row blocks per wave on.
                 const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
                     (void*)d.y, 0, (int)((unsigned)d.M * (unsigned)d.N * 4u), 0x00020000);
 #pragma unroll
                 for (int mb = 0; mb < C::MBW; ++mb) {
-                    const int row = (rg * C::MBW + mb) * 16 + g * 4 + (lane & 3);
-                    const float sc = xs_l[row] * d.w_scale;
-                    const unsigned row_off = (unsigned)row * (unsigned)d.N;
 #pragma unroll
-                    for (int s = 0; s < C::S; ++s) {
-                        const i32x4 v = quad_transpose(acc[s][mb], lane);
-                        const int col = (bc.st0 + sg * C::S + s) * kStripCols + (j & ~3);
-                        const unsigned off = row < d.M && col < d.N ? (row_off + (unsigned)col) * 4u : 0x80000000u;
-                        const f32x4 y = f32x4{(float)v[0] * sc, (float)v[1] * sc, (float)v[2] * sc, (float)v[3] * sc};
-                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, y), yr, (int)off, 0, kYPolicy);
+                    for (int t = 0; t < C::S / 2; ++t) {
+                        i32x4 v[2] = {quad_transpose(acc[2 * t][mb], lane), quad_transpose(acc[2 * t + 1][mb], lane)};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const auto sw = __builtin_amdgcn_permlane16_swap((unsigned)v[0][e], (unsigned)v[1][e],
+                                                                             false, false);
+                            v[0][e] = (int)sw[0];
+                            v[1][e] = (int)sw[1];
+                        }
+                        const int col = (bc.st0 + sg * C::S + 2 * t + (g & 1)) * kStripCols + (j & ~3);
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const int row = (rg * C::MBW + mb) * 16 + (g >> 1) * 8 + h * 4 + (lane & 3);
+                            const float sc = xs_l[row] * d.w_scale;
+                            const unsigned off = row < d.M && col < d.N
+                                                     ? ((unsigned)row * (unsigned)d.N + (unsigned)col) * 4u
+                                                     : 0x80000000u;
+                            const f32x4 y = f32x4{(float)v[h][0] * sc, (float)v[h][1] * sc, (float)v[h][2] * sc,
+                                                  (float)v[h][3] * sc};
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, y), yr, (int)off, 0,
+                                                                   2 /* nt */);
+                        }
                     }
                 }
             } else if (vec_out) {
