@@ -227,7 +227,12 @@ def lib():
         # libamdhip64.so.7 dependency, so both share one runtime; loaded after
         # this library, torch would bring in a second runtime beside the
         # /opt/rocm one, and this library's launches would find no device.
-        import torch  # noqa: F401
+        # Without torch installed the library loads alone against the system
+        # runtime (the C-ABI needs nothing from torch).
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         for name, res, args in SIGNATURES:
             f = getattr(L, name)

@@ -1039,6 +1039,8 @@ static int gemm_out_ws(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M
     if (M < 1 || M > TER_HIP_M_MAX) return fail(TER_HIP_ERR_SHAPE, "M=%d out of range [1,%d]", M, TER_HIP_M_MAX);
     rc = check_act(x, M);
     if (rc) return rc;
+    if (x->kind == TER_HIP_X_I16)  // the GEMM kernels take int8 rows; int16 rows run as single GEMVs only
+        return fail(TER_HIP_ERR_PAYLOAD, "int16 activations run as single GEMVs only (ter_hip_gemv / ter_hip_mm_row)");
     rc = check_out(out);
     if (rc) return rc;
     hipStream_t st = static_cast<hipStream_t>(stream);
@@ -1123,7 +1125,8 @@ int ter_hip_gemm_out_static(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int3
     if ((long long)M * w->K > (long long)TER_HIP_STATIC_Q_MAX)
         return fail(TER_HIP_ERR_SHAPE, "M*K = %lld exceeds the static workspace (%d bytes)", (long long)M * w->K,
                     TER_HIP_STATIC_Q_MAX);
-    if (x->kind == TER_HIP_X_I8) return gemm_out_ws(w, x, M, out, nullptr, nullptr, stream);  // no workspace used
+    if (x->kind == TER_HIP_X_I8 || x->kind == TER_HIP_X_I16)  // no workspace used (int16 rows are refused there)
+        return gemm_out_ws(w, x, M, out, nullptr, nullptr, stream);
     unsigned char* ws = nullptr;
     rc = scratch_of_current_device(&ws);
     if (rc) return rc;
@@ -1167,9 +1170,11 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     long long tiles = 0;
     ds.clear();
     std::vector<long long> block_starts, tile_starts;
+    std::vector<int> piece0;  // first descriptor of each item (its pieces follow)
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemm_item_t& it = items[i];
         const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid};
+        piece0.push_back((int)ds.size());
         for (int r0 = 0; r0 < it.M; r0 += rows) {
             const int m = std::min(rows, it.M - r0);
             const GemmDesc d = make_gemm_desc(it.w, it.x + (size_t)r0 * it.w->K, it.x_scale_dev + r0, m,
@@ -1211,10 +1216,19 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
     int rc;
     if (lbs > 0) {
-        // LDS-ring kernel: blocks of lbs strips, dealt out by list scheduling
+        // LDS-ring kernel: blocks of lbs strips, dealt out by list scheduling.
+        // The pieces of an item read the same weights: their blocks of one
+        // strip range are listed next to each other, so the scheduler hands
+        // them out together to neighbouring workgroups on one XCD (equal cost,
+        // adjacent in the stable order) and the pieces after the first find
+        // the weight runs in that XCD's L2 instead of reading them again.
         std::vector<GemmBlock> bl;
-        for (int i = 0; i < n; ++i)
-            for (int st = 0; st < ds[(size_t)i].n_strips; st += lbs) bl.push_back(GemmBlock{i, st});
+        piece0.push_back(n);
+        for (size_t it = 0; it + 1 < piece0.size(); ++it) {
+            const int d0 = piece0[it], d1 = piece0[it + 1];
+            for (int st = 0; st < ds[(size_t)d0].n_strips; st += lbs)
+                for (int i = d0; i < d1; ++i) bl.push_back(GemmBlock{i, st});
+        }
         rc = pick_lds_wg((long long)bl.size(), mb, &n_wg);
         if (!rc) rc = upload_lds_plan(p, ds, bl, lbs, n_wg);
     } else {

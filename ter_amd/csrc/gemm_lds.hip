@@ -5,11 +5,16 @@
 // acc[m][j] = sum_k X[m][k] w[k][j] in exact int32, y = float(mag * acc) * (xs[m] * w_scale).
 //
 // Work.  A block is BS consecutive column strips of one GEMM (all M rows,
-// all K).  The blocks of a launch are split over the workgroups in contiguous
-// ranges balanced by 256-row units (a block costs Ku units), consecutive
-// ranges on one XCD.  A workgroup (8 waves) walks its blocks unit by unit:
-// for unit u of block b it needs X[0:M, u] (M x 256 int8) and the BS weight
-// tiles (strip, u) of the block, 1 KiB each.
+// all K).  The host deals the blocks of a launch out to the workgroups by
+// list scheduling (upload_lds_plan in abi.hip: largest estimated cost first,
+// each to the workgroup free first; the pieces of a GEMM cut into 128-row
+// pieces side by side, so they read the same weights at the same time), and
+// stores each workgroup's blocks as one range of the block list in the order
+// it runs them; workgroups with neighbouring ranges sit on one XCD.  A single
+// GEMM (no list) splits its blocks into equal contiguous ranges.  A
+// workgroup (8 compute waves) walks its blocks unit by unit: for unit u of
+// block b it needs X[0:M, u] (M x 256 int8) and the BS weight tiles
+// (strip, u) of the block, 1 KiB each.
 //
 // Pipeline.  NST stages of LDS, each holding one unit's X rows and weight
 // tiles, are filled by buffer_load_dwordx4 ... lds (64 lanes x 16 bytes = one
@@ -35,15 +40,25 @@
 // The wave grid is RS row groups x (8 / RS) strip groups; a wave holds
 // MBW x S accumulators (MBW row blocks of 16 x S strips).  Per 64-row slab a
 // wave reads MBW A operands (ds_read_b128) and S weight dwords (ds_read_b32,
-// lane = column j + 16 * k-group g, one dword = 16 trits of column j), expands
-// each 2-bit code u = w + 1 straight to the signed int8 w with one v_perm_b32
-// per 4 trits (a byte table {-1, 0, +1, 0} indexed by u), and issues
-// v_mfma_i32_16x16x64_i8.  Signed weights need no activation-sum correction.
-// The A operands are read a few steps ahead of their MFMAs.
+// lane = column j + 16 * k-group g, one dword = 16 trits of column j) and
+// issues v_mfma_i32_16x16x64_i8.  From 3 row blocks per wave on, each 2-bit
+// code u = w + 1 becomes the signed int8 w with one v_perm_b32 per 4 trits
+// (a byte table {-1, 0, +1, 0} indexed by u) and needs no correction.  Up to
+// 2 row blocks (C::UC) the MFMAs take the unsigned codes u themselves (7 bit
+// operations per 16 trits instead of 11), and one more MFMA per A operand
+// against all-ones sums the rows of X; the epilogue subtracts that row sum
+// (sum_k x u = sum_k x w + sum_k x, and the padding rows past K, which hold
+// u = 1, cancel the same way).  The A operands are read a few steps ahead of
+// their MFMAs.
 //
-// Epilogue.  fp32 / int32 outputs (N a multiple of 4) are transposed in
-// quads of lanes (DPP) so that each lane stores 4 consecutive columns of one
-// row with one 16-byte store; other output forms go element by element.
+// Epilogue.  The common output form (fp32 y only, payload magnitude 1, N a
+// multiple of 4) transposes each accumulator in quads of lanes (DPP), pairs
+// the two strips of a wave with v_permlane16_swap so that every store covers
+// whole 128-byte lines (8 rows x 2 strips), and stores them nontemporally
+// through a buffer resource at 32-bit offsets (lanes outside the matrix
+// store past its range, which the hardware drops: no branch).  Other fp32 /
+// int32 outputs with N a multiple of 4 store 4 consecutive columns of one
+// row per lane; fp16 and residual outputs go element by element.
 #include <type_traits>
 
 #include "common.h"

@@ -224,6 +224,13 @@ def test_int16_activations_are_single_gemv_only():
     a.kind = L.X_I16
     a.scale_dev = fake
     assert lib.ter_hip_gemm(C.byref(w), C.byref(a), 4, fake, None, None) == L.ERR_PAYLOAD
+    # one int16 row through the GEMM entry points is refused the same way
+    # (not sent to the fp32 / RMS quantizers, which would ask for q_out)
+    assert lib.ter_hip_gemm(C.byref(w), C.byref(a), 1, fake, None, None) == L.ERR_PAYLOAD
+    o = L.Out()
+    o.y = fake
+    assert lib.ter_hip_gemm_out(C.byref(w), C.byref(a), 1, C.byref(o), None) == L.ERR_PAYLOAD
+    assert lib.ter_hip_gemm_out_static(C.byref(w), C.byref(a), 1, C.byref(o), None) == L.ERR_PAYLOAD
     items = (L.GemvItem * 1)()
     items[0].w = C.pointer(w)
     items[0].x = a
