@@ -11,9 +11,13 @@ Cache), so every step streams its weights from HBM.
 
 Also reported (not `value`): the same sweep as one launch per GEMV (112
 launches) and as 4 launches per layer grouped like a decode step
-({q,k,v}, {o}, {gate,up}, {down}); the C3 BitNet-2B sweep (fp32 activations
-quantized in the kernel prologue) with --config bitnet; the C4 batched GEMM
-with --config batched --m M.
+({q,k,v}, {o}, {gate,up}, {down}); and, under "extras" in the same JSON line
+(unless --no-extras), the other benched workloads measured in the same run:
+C3 (the BitNet-2B sweep, fp32 activations quantized in the kernel prologue),
+C4 (the batched GEMM at M = 8, 32, 128), C5 (the end-to-end decode, its
+lm_head tail and attention), the per-shape table and the host mm_row route.
+Each also runs alone: --config bitnet | batched --m M | decode | lm_head |
+attention | shapes | mm_row.
 
 value = MACs of the sweep / (time per step); roofline.achieved = algorithmic
 bytes per launch (packed W K*N/4 + X + Y 4N, summed over the sweep) / mean
@@ -705,6 +709,138 @@ def run_decode(args):
     }
 
 
+def run_mm_row(args):
+    """The reference host forward's own route through the fabric: mm_row
+    (src/tx/forward.cpp:299-352) called synchronously 7 times per layer
+    (:400-403, 499, 524-525, 549) on BitNet-2B-4T's projection shapes, with
+    the host forward's operands: weights as the TritTensor payload
+    {-9841, 0, +9841} (quantize(..., 9) of ternary GGUF weights,
+    src/host/load_gguf.cpp:46,111) and 9-trit activation rows, |x| <= 9841
+    (quantize(x_norm, {1, H}, 9), src/tx/forward.cpp:400).  Those rows do
+    not fit int8, so every call runs the int16 GEMV (gemv_x16_kernel).
+    Per shape:
+      call_us   -- one ter_hip_mm_row call through the C-ABI as the host
+                   forward makes it (host int32 row in, host fp32 out:
+                   range check, upload, kernel, download, synchronize);
+                   median of the calls' wall times;
+      kernel    -- the int16 GEMV alone on a device-resident row, weights
+                   rotated over >= 512 MB of copies (HBM-cold), the mean
+                   per launch of up to 512 launches replayed back to back
+                   from a HIP graph; GB/s of packed weights K*N/4;
+    cpu_baseline: the reference's own mm_row (oracle/_ref, 1 thread) on
+    the same payloads and rows, its outputs compared bit for bit with the
+    GPU's."""
+    import ctypes as C
+    import numpy as np
+    import torch
+    import ter_amd as T
+    from ter_amd import _lib as L
+    lib = L.lib()
+    M9 = 9841
+    rows = []
+    ctx = []
+    st = torch.cuda.current_stream().cuda_stream
+    for i, (nm, K, N) in enumerate(BITNET["shapes"]):
+        rng = np.random.default_rng(4200 + i)
+        trits = rng.choice(np.array([-1, 0, 1], dtype=np.int32), size=(K, N), p=[0.3, 0.4, 0.3])
+        payload = trits * M9
+        ws = float(scale_of(4200 + i)) / M9
+        W = T.PackedTrits.from_payload(payload, ws)
+        X = np.clip(np.rint(rng.standard_normal((1, K)) * (M9 / 4)), -M9, M9).astype(np.int32)
+        xs = 1.0 / M9
+        xstage = torch.empty(2 * K, dtype=torch.int8, device="cuda")
+        ystage = torch.empty(N, dtype=torch.float32, device="cuda")
+        out = np.empty(N, dtype=np.float32)
+
+        def call(W=W, X=X, K=K, N=N, xs=xs, out=out, xstage=xstage, ystage=ystage):
+            return lib.ter_hip_mm_row(X.ctypes.data, 0, K, xs, C.byref(W.wpk), N, out.ctypes.data,
+                                      xstage.data_ptr(), ystage.data_ptr(), st)
+        for _ in range(5):
+            L.check(call(), "ter_hip_mm_row")
+        n_calls = max(50, args.steps)
+        tw = []
+        for _ in range(n_calls):
+            t0 = time.perf_counter()
+            rc = call()
+            tw.append(time.perf_counter() - t0)
+            if rc:
+                L.check(rc, "ter_hip_mm_row")
+        tw.sort()
+        call_us = tw[len(tw) // 2] * 1e6
+        # the kernel alone: int16 row on the device, weights rotated HBM-cold
+        wbytes = K * N // 4
+        copies = max(2, -(-512_000_000 // wbytes))
+        Ws = [T.PackedTrits.from_v11(T.synth_v11(K, N, seed=7000 + 31 * i + c, p_zero=0.4), K, N, ws)
+              for c in range(copies)]
+        x16 = torch.from_numpy(X[0].astype(np.int16)).cuda()
+        fns = [lambda Wc=Wc: T.gemv(Wc, x16, y=ystage, x_scale=xs) for Wc in Ws]
+        n_graph = min(len(fns), 512)
+        g = graph_of(lambda: [f() for f in fns[:n_graph]])
+        settle(g.replay, 0.2)
+        _, g_ev, _ = time_launches([g.replay], max(10, args.steps // 50), 2)
+        k_us = g_ev * 1e3 / n_graph
+        row = dict(shape=nm, K=K, N=N, call_us=round(call_us, 2), call_p90_us=round(tw[int(len(tw) * 0.9)] * 1e6, 2),
+                   kernel_us=round(k_us, 3), kernel_gbs=round(wbytes / (k_us * 1e-6) / 1e9, 1),
+                   kernel_frac_hbm=round((wbytes + 2 * K + 4 * N) / (k_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+        rows.append(row)
+        log(f"[bench] mm_row {nm:6s} K={K} N={N}: call {call_us:8.2f} us, int16 GEMV {k_us:6.2f} us "
+            f"({row['kernel_gbs']:.0f} GB/s)")
+        ctx.append((nm, K, N, X, xs, payload, ws, out.copy()))
+        del Ws, fns, g
+        torch.cuda.empty_cache()
+    layer_call_us = sum(r["call_us"] for r in rows)
+    layer_kernel_us = sum(r["kernel_us"] for r in rows)
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+        use_ref = O.ref_available()
+        runners, ok = [], True
+        for nm, K, N, X, xs, payload, ws, gpu_out in ctx:
+            if use_ref:
+                r = O.RefMmRow(X, xs, payload, ws)
+                runners.append((K, N, lambda r=r: r.run(0), gpu_out))
+            else:
+                runners.append((K, N, lambda X=X, xs=xs, P=payload, ws=ws: O.mm_row(X, 0, xs, P, ws)[1], gpu_out))
+        t_cpu, done, macs_done, reps = 0.0, 0, 0, 0
+        t_begin = time.perf_counter()
+        while True:
+            for K, N, run, gpu_out in runners:
+                t0 = time.perf_counter()
+                got = run()
+                t_cpu += time.perf_counter() - t0
+                done += 1
+                macs_done += K * N
+                if reps == 0:
+                    ok = ok and bool((got.view(np.int32) == gpu_out.view(np.int32)).all())
+            reps += 1
+            if time.perf_counter() - t_begin > args.cpu_seconds:
+                break
+        cpu = dict(value=round(t_cpu / done * 7 * 1e3, 3), unit="ms per layer (7 mm_row calls)", cores=1,
+                   kind="reference" if use_ref else "port", gmacs=round(macs_done / t_cpu / 1e9, 3),
+                   sample=f"the 7 calls of one layer, {reps} passes, {t_cpu:.1f} s of mm_row time, int32 payload "
+                          f"{{-9841,0,+9841}}, 9-trit rows, 1 thread",
+                   matches_gpu_bitexact=ok)
+        log(f"[bench] cpu baseline: {cpu}")
+    del ctx
+    return {
+        "metric": "host mm_row route: synchronous ter_hip_mm_row calls per BitNet-2B layer (9-trit rows)",
+        "value": round(layer_call_us, 2), "unit": "us per layer (7 calls)", "n_gpus": 1, "steps": args.steps,
+        "warmup": 5, "ms_per_step": round(layer_call_us * 1e-3, 5), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int16", "data": "synthetic",
+        "config": {"workload": "mm_row host route: bitnet-b1.58-2b-4t projection shapes, payload {-9841,0,+9841}, "
+                               "9-trit activation rows (int16 GEMV), host buffers in and out"},
+        "layer_kernel_us": round(layer_kernel_us, 2), "shapes": rows,
+        "roofline": {"bound": "hbm", "achieved": round(sum(K * N // 4 for _, K, N in BITNET["shapes"]) /
+                                                      (layer_kernel_us * 1e-6) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(sum(K * N // 4 + 2 * K + 4 * N for _, K, N in BITNET["shapes"]) /
+                                   (layer_kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "gemv_x16_kernel",
+                     "bytes_per_launch": None, "mean_launch_us": round(layer_kernel_us / 7, 3)},
+        "cpu_baseline": cpu,
+    }
+
+
 # Per-shape table: the reference bench's five shapes
 # (cuda/ter_cuda_forward_packed_v13_bench.cu:422-428, the packed lm_head
 # included) and BitNet-2B's four.
@@ -844,19 +980,104 @@ def run_copy(args):
             "config": {"workload": "copy", "read_bytes_per_launch": nbytes, "write_bytes_per_launch": nbytes}}
 
 
+def run_extras(args):
+    """The other benched workloads, measured in the same run as the C2
+    headline and reported beside it (never as `value`): C3 (the BitNet-2B
+    sweep, fp32 X quantized in the kernel prologue, with the reference
+    mm_row on layer 0 checked bit for bit), C4 at M = 8, 32 and 128, the C5
+    decode, its lm_head tail and attention, the per-shape table (single
+    launch and work list), and the host mm_row route.  Each runs with the
+    same --steps / --warmup as the headline and frees its device memory
+    before the next; one that fails is recorded with its error and the
+    rest still run."""
+    import copy
+    import gc
+    import torch
+    ex = {}
+
+    def sub(**kw):
+        a = copy.copy(args)
+        a.__dict__.update(kw)
+        return a
+
+    def rnd(v, n=4):
+        return None if v is None else round(v, n)
+
+    def do(name, fn, keep):
+        t0 = time.perf_counter()
+        try:
+            r = keep(fn())
+        except Exception as e:  # recorded, the other workloads still run
+            r = {"error": f"{type(e).__name__}: {e}"}
+        gc.collect()
+        torch.cuda.empty_cache()
+        r["run_s"] = round(time.perf_counter() - t0, 1)
+        ex[name] = r
+        log(f"[bench] extra {name}: {r}")
+
+    def keep_m1(r):
+        rf = r["roofline"]
+        return dict(workload=r["config"]["workload"], gmacs=r["value"], ms_per_step=r["ms_per_step"],
+                    launch_us_events=rf["mean_launch_us"], hbm_gbs=rf["achieved"], hbm_frac=rf["frac"],
+                    hbm_frac_wall=rf["frac_wall"], bytes_per_launch=rf["bytes_per_launch"], traffic=rf["traffic"],
+                    cpu_baseline=r["cpu_baseline"])
+    do("c3_bitnet_sweep", lambda: run_m1(sub(quick=True, cpu_seconds=min(args.cpu_seconds, 6.0)), BITNET, True),
+       keep_m1)
+
+    def keep_b(r):
+        rf = r["roofline"]
+        return dict(workload=r["config"]["workload"], kernel=rf["kernel"], gemm_launch_us=r["gemm_launch_us"],
+                    step_us=r["step_us"], hbm_gbs=r["hbm_gbs"], hbm_frac=rnd(r["hbm_gbs"] / HBM_PEAK_GBS),
+                    int8_tops=r["mfma_tops"], int8_frac=r["mfma_frac"], roofline_bound=rf["bound"],
+                    roofline_frac=rf["frac"], bytes_per_launch=rf["bytes_per_launch"], traffic=rf["traffic"])
+    for m in (8, 32, 128):
+        do(f"c4_batched_m{m}", lambda m=m: run_batched(sub(m=m)), keep_b)
+
+    def keep_dec(r):
+        c = r["config"]
+        return dict(workload=c["workload"], tokens_per_s_wall=r["value"], ms_per_token_wall=r["ms_per_step"],
+                    us_per_token_events=c["us_per_token"], launches_per_token=c["launches_per_token"],
+                    bytes_per_token=c["bytes_per_token"], hbm_frac=r["roofline"]["frac"])
+    do("c5_decode", lambda: run_decode(sub(bin=None)), keep_dec)
+
+    def keep_tail(r):
+        rf = r["roofline"]
+        return dict(workload=r["config"]["workload"], launch_us_events=rf["mean_launch_us"], hbm_gbs=rf["achieved"],
+                    hbm_frac=rf["frac"], three_launch_us=r.get("three_launch_us"))
+    do("c5_lm_head", lambda: run_lm_head(sub(no_cpu=True, quick=True)), keep_tail)
+    do("c5_attention", lambda: run_attention(sub(no_cpu=True)), keep_tail)
+
+    def keep_shapes(r):
+        return dict(workload=r["config"]["workload"],
+                    shapes=[dict(shape=x["shape"], K=x["K"], N=x["N"], single_median_us=x["single_median"]["us"],
+                                 single_graph_us=x["single_graph"]["us"], single_graph_gbs=x["single_graph"]["gbs"],
+                                 list_us=x["list"]["us"], list_gbs=x["list"]["gbs"],
+                                 list_frac_hbm=x["list"]["frac_hbm"], list_gmacs=x["list"]["gmacs"])
+                            for x in r["shapes"]])
+    do("per_shape", lambda: run_shapes(args), keep_shapes)
+
+    def keep_mmrow(r):
+        return dict(workload=r["config"]["workload"], layer_call_us=r["value"], layer_kernel_us=r["layer_kernel_us"],
+                    kernel_frac_hbm=r["roofline"]["frac"], shapes=r["shapes"], cpu_baseline=r["cpu_baseline"])
+    do("mm_row_host_route", lambda: run_mm_row(sub(cpu_seconds=min(args.cpu_seconds, 6.0))), keep_mmrow)
+    return ex
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", choices=["llama", "bitnet", "batched", "lm_head", "attention", "decode", "copy",
-                                         "shapes", "floors"], default="llama")
+                                         "shapes", "floors", "mm_row"], default="llama")
     ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
     ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--bin", default=None, help="--config decode: load this packed BitNet model file ('TERT')")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--quick", action="store_true", help="skip the per-GEMV / grouped launch modes")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default config: skip the other workloads reported under 'extras'")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -879,9 +1100,13 @@ def main():
         out = run_attention(args)
     elif args.config == "decode":
         out = run_decode(args)
+    elif args.config == "mm_row":
+        out = run_mm_row(args)
     else:
         cfg = LLAMA if args.config == "llama" else BITNET
         out = run_m1(args, cfg, fp32_x=(args.config == "bitnet"))
+        if args.config == "llama" and not args.no_extras:
+            out["extras"] = run_extras(args)
     print(json.dumps(out), flush=True)
 
 

@@ -203,8 +203,12 @@ int ter_hip_mm_packed_dispatch_f16(const int8_t* X, const float* scale_x_dev,
  * fit int8 runs the int8 GEMV; one that fits int16 (the reference forward's
  * 9-trit activations, |x| <= 9841) runs the int16 GEMV (TER_HIP_X_I16);
  * anything wider is TER_HIP_ERR_PAYLOAD (no CPU fallback).  Synchronous.
- * `x_stage_dev` (2*K bytes, 16-byte aligned) and `y_stage_dev` (N fp32) are
- * caller device buffers used for the transfer. */
+ * `x_stage_dev` (2*K bytes, 16-byte aligned) receives the row on the device.
+ * The library narrows the row into its own page-locked host buffer and the
+ * GEMV writes its outputs into another (one pair per device, grown on demand
+ * and held until the process ends; calls are serialized on them), so a call
+ * is one upload, one kernel and one synchronize; `y_stage_dev` (N fp32) is
+ * used only where page-locked memory cannot be had (pageable copies). */
 int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale,
                    const ter_hip_wpk_t* W, int32_t N, float* out,
                    void* x_stage_dev, float* y_stage_dev, void* stream);

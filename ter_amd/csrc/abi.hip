@@ -513,6 +513,66 @@ static int scratch_of_current_device(unsigned char** out) {
     return TER_HIP_OK;
 }
 
+// Host staging of the synchronous mm_row calls: page-locked buffers, one
+// pair per device, grown on demand and held until the process ends.  The
+// row is narrowed straight into page-locked memory, so its upload is one DMA
+// with no bounce through the runtime's own staging, and the GEMV writes its
+// fp32 outputs straight into page-locked host memory (coherent: the writes
+// reach host memory by the end of the kernel), so no download copy follows.
+// Callers hold g_stage_mu for the whole call (the reference's mm_row is never
+// called concurrently; calls from several threads are serialized).
+struct MmRowStage {
+    void* x = nullptr;
+    size_t xcap = 0;
+    float* y = nullptr;      // host address
+    float* y_dev = nullptr;  // the same memory as the device addresses it
+    size_t ycap = 0;
+};
+static std::mutex g_stage_mu;
+static std::vector<MmRowStage> g_stage;
+
+static size_t grown(size_t want) {
+    size_t c = 64 * 1024;
+    while (c < want) c *= 2;
+    return c;
+}
+
+// The device's staging with room for xbytes and ybytes; false when pinned
+// memory cannot be had (the caller then takes the pageable path).
+static bool mm_row_stage(int dev, size_t xbytes, size_t ybytes, MmRowStage** out) {
+    if ((int)g_stage.size() <= dev) g_stage.resize((size_t)dev + 1);
+    MmRowStage& s = g_stage[(size_t)dev];
+    if (s.xcap < xbytes) {
+        if (s.x) (void)hipHostFree(s.x);
+        s.x = nullptr;
+        s.xcap = 0;
+        const size_t c = grown(xbytes);
+        if (hipHostMalloc(&s.x, c, hipHostMallocDefault) != hipSuccess) {
+            s.x = nullptr;
+            return false;
+        }
+        s.xcap = c;
+    }
+    if (s.ycap < ybytes) {
+        if (s.y) (void)hipHostFree(s.y);
+        s.y = s.y_dev = nullptr;
+        s.ycap = 0;
+        const size_t c = grown(ybytes);
+        void* h = nullptr;
+        void* d = nullptr;
+        if (hipHostMalloc(&h, c, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) return false;
+        if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess || !d || ((uintptr_t)d & 15u) != 0) {
+            (void)hipHostFree(h);
+            return false;
+        }
+        s.y = static_cast<float*>(h);
+        s.y_dev = static_cast<float*>(d);
+        s.ycap = c;
+    }
+    *out = &s;
+    return true;
+}
+
 // Device copy of an LDS-ring GEMM plan: descriptors, the block list in
 // workgroup order, and the per-workgroup block ranges.  Range g holds
 // workgroup g's blocks in the order it runs them.  The blocks are dealt out
@@ -787,6 +847,34 @@ int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale, cons
     if (lo < -32768 || hi > 32767)
         return fail(TER_HIP_ERR_PAYLOAD, "X values [%d, %d] do not fit int16 (no CPU fallback)", lo, hi);
     const bool wide = lo < -128 || hi > 127;
+    const size_t xbytes = (size_t)K * (wide ? 2 : 1);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    ter_hip_act_t x{};
+    x.data = x_stage_dev;
+    x.kind = wide ? TER_HIP_X_I16 : TER_HIP_X_I8;
+    x.scale = x_scale;
+    std::lock_guard<std::mutex> lk(g_stage_mu);
+    MmRowStage* sg = nullptr;
+    if (mm_row_stage(dev, xbytes, (size_t)N * sizeof(float), &sg)) {
+        // pinned path: the row narrowed straight into page-locked memory, one
+        // DMA up, the GEMV's outputs written into page-locked host memory
+        if (wide)
+            for (int k = 0; k < K; ++k) static_cast<int16_t*>(sg->x)[k] = (int16_t)xr[k];
+        else
+            for (int k = 0; k < K; ++k) static_cast<int8_t*>(sg->x)[k] = (int8_t)xr[k];
+        e = hipMemcpyAsync(x_stage_dev, sg->x, xbytes, hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) return hip_fail(e, "X upload");
+        int rc = ter_hip_gemv(W, &x, sg->y_dev, nullptr, stream);
+        if (rc) return rc;
+        e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return hip_fail(e, "mm_row synchronize");
+        std::memcpy(out, sg->y, (size_t)N * sizeof(float));
+        return TER_HIP_OK;
+    }
+    // no pinned staging: pageable copies through the caller's device buffers
     std::vector<int8_t> xb;
     std::vector<int16_t> xw;
     try {
@@ -797,14 +885,9 @@ int ter_hip_mm_row(const int32_t* X, int32_t row, int32_t K, float x_scale, cons
     } catch (...) {
         return fail(TER_HIP_ERR_ALLOC, "host staging allocation");
     }
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    hipError_t e = wide ? hipMemcpyAsync(x_stage_dev, xw.data(), (size_t)K * 2, hipMemcpyHostToDevice, st)
-                        : hipMemcpyAsync(x_stage_dev, xb.data(), (size_t)K, hipMemcpyHostToDevice, st);
+    e = wide ? hipMemcpyAsync(x_stage_dev, xw.data(), xbytes, hipMemcpyHostToDevice, st)
+             : hipMemcpyAsync(x_stage_dev, xb.data(), xbytes, hipMemcpyHostToDevice, st);
     if (e != hipSuccess) return hip_fail(e, "X upload");
-    ter_hip_act_t x{};
-    x.data = x_stage_dev;
-    x.kind = wide ? TER_HIP_X_I16 : TER_HIP_X_I8;
-    x.scale = x_scale;
     int rc = ter_hip_gemv(W, &x, y_stage_dev, nullptr, stream);
     if (rc) return rc;
     e = hipMemcpyAsync(out, y_stage_dev, (size_t)N * sizeof(float), hipMemcpyDeviceToHost, st);

@@ -35,13 +35,20 @@ __device__ __forceinline__ unsigned row_sum16_u(unsigned v) {
     return v;
 }
 
-// 16 int16 activations at k (zeros past K), split into the hi plane (signed
-// bytes x >> 8) and the lo plane (bytes x & 255); returns their sum.
-__device__ __forceinline__ int split16(const int16_t* x, int k, int K, u32x4& hi, u32x4& lo) {
+// 16 int16 activations at k, read through a buffer resource that covers
+// the K elements of X (elements past K read zeros), split into the hi plane
+// (signed bytes x >> 8) and the lo plane (bytes x & 255); returns their sum.
+// kVec (X 16-byte aligned, K a multiple of 16): two 16-byte loads, each
+// chunk wholly inside X or wholly past it.  Otherwise 16 two-byte loads.
+// Either way every load is unconditional: no branch joins loaded values
+// (at such a join the compiler waited for every load in flight, the weight
+// batch issued before the staging included).
+template <bool kVec>
+__device__ __forceinline__ int split16(__amdgpu_buffer_rsrc_t xr, int k, u32x4& hi, u32x4& lo) {
     int v[16];
-    if (((reinterpret_cast<uintptr_t>(x + k) & 15u) == 0) && k + 16 <= K) {
-        const TER_GLOBAL u32x4* p = gptr(reinterpret_cast<const u32x4*>(x + k));
-        const u32x4 a = p[0], b = p[1];
+    if constexpr (kVec) {
+        const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(xr, 2 * k, 0, 0);
+        const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(xr, 2 * k + 16, 0, 0);
         const unsigned w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -50,7 +57,8 @@ __device__ __forceinline__ int split16(const int16_t* x, int k, int K, u32x4& hi
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = k + i < K ? (int)gptr(x)[k + i] : 0;
+        for (int i = 0; i < 16; ++i)
+            v[i] = (int)(int16_t)__builtin_amdgcn_raw_buffer_load_b16(xr, 2 * (k + i), 0, 0);
     }
     unsigned h[4], l[4];
     int sum = 0;
@@ -89,6 +97,7 @@ __device__ __forceinline__ void dot_tile_x16(const u32x4& w, const u32x4& hi, co
     }
 }
 
+template <bool kVec>
 __global__ __launch_bounds__(kGemvThreads) void gemv_x16_kernel(GemvDesc d, int n_wg, int part_off) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     int g = blockIdx.x;
@@ -131,11 +140,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_x16_kernel(GemvDesc d, int 
     uint8_t* lds_lo = reinterpret_cast<uint8_t*>(lds_raw + Ku * kUnitK);
     int* usum = reinterpret_cast<int*>(lds_raw + 2 * Ku * kUnitK);
     int* part = reinterpret_cast<int*>(lds_raw + part_off);  // [strip][wave][16 columns]
-    const int16_t* xp = static_cast<const int16_t*>(d.x);
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc((void*)d.x, 0, 2 * d.K, 0x00020000);
     const int nchunks = Ku * (kUnitK / 16);
     for (int c = tid; c < nchunks; c += kGemvThreads) {
         u32x4 hi, lo;
-        const int sum = split16(xp, c * 16, d.K, hi, lo);
+        const int sum = split16<kVec>(xr, c * 16, hi, lo);
         *reinterpret_cast<u32x4*>(lds_hi + c * 16) = hi;
         *reinterpret_cast<u32x4*>(lds_lo + c * 16) = lo;
         const unsigned us = row_sum16_u((unsigned)sum);
@@ -215,8 +224,12 @@ int gemv_x16_lds_bytes(int K, int strips_per_wg) {
 }
 
 hipError_t launch_gemv_x16(const GemvDesc& d, int n_wg, int lds_bytes, hipStream_t st) {
-    hipLaunchKernelGGL(gemv_x16_kernel, dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, d, n_wg,
-                       gemv_x16_part_off(d.K));
+    if ((reinterpret_cast<uintptr_t>(d.x) & 15u) == 0 && d.K % 16 == 0)
+        hipLaunchKernelGGL(gemv_x16_kernel<true>, dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, d, n_wg,
+                           gemv_x16_part_off(d.K));
+    else
+        hipLaunchKernelGGL(gemv_x16_kernel<false>, dim3(n_wg), dim3(kGemvThreads), lds_bytes, st, d, n_wg,
+                           gemv_x16_part_off(d.K));
     return hipGetLastError();
 }
 
