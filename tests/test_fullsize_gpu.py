@@ -1,5 +1,9 @@
 """The benchmarked configurations checked at the size they are benchmarked.
 
+C2: the Llama-3.2-1B sweep at M = 1 -- the exact 16 x 7 int8 work list that
+    `bench.py` launches for its headline (bench.Sweep with the bench's own
+    seeds, int8 activations over the full [-127, 127]), every output column
+    of every one of the 112 GEMVs against the oracle.
 C3: the BitNet-2B sweep at M = 1 -- the exact 30 x 7 fp32 work list that
     `bench.py --config bitnet` launches (bench.Sweep, bench's default launch
     shape), every output column of every GEMV against the oracle.
@@ -29,6 +33,38 @@ def host(t):
     import torch
     torch.cuda.synchronize()
     return t.cpu().numpy()
+
+
+def test_llama_sweep_full_size(cuda):
+    """C2: 112 GEMVs, int8 X, one launch (the headline's work list)."""
+    import bench
+    import ter_amd as T
+    cfg = bench.LLAMA
+    sw = bench.Sweep(cfg, 1, fp32_x=False)
+    plan = T.Plan(sw.items(0))
+    assert plan.bytes == bench.alg_bytes(cfg, False)
+    first = None
+    for rep in range(2):  # a second launch: fix-up slots left clean by the first
+        plan.launch()
+        ys = {(l, nm): host(sw.y[l][nm]).copy() for l in range(cfg["layers"]) for nm, _, _ in cfg["shapes"]}
+        if first is None:
+            first = ys
+        else:
+            assert all((ys[k].view(np.int32) == first[k].view(np.int32)).all() for k in ys), "relaunch differs"
+    xs = {}
+    for l in range(cfg["layers"]):
+        for nm, K, N in cfg["shapes"]:
+            W, _, seed = sw.copies[0][l][nm]
+            key = (l, bench.X_OF[nm])
+            if key not in xs:
+                xs[key] = host(sw.x[l][bench.X_OF[nm]])
+            x = xs[key]
+            Wt = O.rand_trits_c(seed, K, N, cfg["p_zero"])
+            _, want = O.gemv_i8w(x, 0.0312, Wt, W.scale)
+            got = first[(l, nm)]
+            assert (got.view(np.int32) == want.view(np.int32)).all(), (l, nm)
+    allx = np.concatenate(list(xs.values()))
+    assert allx.min() == -127 and allx.max() == 127  # the config's full activation range
 
 
 def test_bitnet_sweep_full_size(cuda):
@@ -63,8 +99,9 @@ def test_bitnet_sweep_full_size(cuda):
 
 @pytest.mark.parametrize("M", [8, 32, 128])
 def test_bitnet_batched_full_size(cuda, M):
-    """C4: 30 layers x 7 GEMMs at M rows in one plan launch (streamed kernel
-    at M = 8, LDS ring at 32 and 128), after the per-row quantizers."""
+    """C4: 30 layers x 7 GEMMs at M rows in one plan launch (the LDS-ring
+    kernel at every M: the 210-GEMM list holds more than 4 ring blocks per
+    CU even at M = 8), after the per-row quantizers."""
     import torch
     import bench
     wl = bench.Batched(M)

@@ -57,6 +57,61 @@ def _run(lib, fn, W, a, M, N):
     return y.cpu().numpy(), acc.cpu().numpy()
 
 
+def _capture_static(lib, W, a, M, N, y, acc):
+    """A HIP graph holding one ter_hip_gemm_out_static call (torch's global
+    capture mode, under which an allocation on any thread is an error)."""
+    import torch
+    o = L.Out()
+    o.y, o.acc = y.data_ptr(), acc.data_ptr()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, capture_error_mode="global"):
+        st = torch.cuda.current_stream().cuda_stream
+        rc = lib.ter_hip_gemm_out_static(C.byref(W.wpk), C.byref(a), M, C.byref(o), st)
+    L.check(rc, "ter_hip_gemm_out_static under capture")
+    return g
+
+
+@pytest.mark.gpu
+def test_static_gemm_under_graph_capture(cuda):
+    """Captured into a HIP graph: first before any eager call of the entry
+    point in this process (its first call on the device looks up the static
+    workspace's address inside the capture; this test runs before the other
+    GPU test of this file, and no other test file reaches that lookup), then
+    again after eager calls.  Every replay, with eager calls of other inputs
+    through the same workspace and synchronizations between the replays, is
+    bit-identical to ter_hip_gemm_out with caller workspaces."""
+    import torch
+    import ter_amd as T
+    lib = L.lib()
+    M, K, N = 32, 2560, 640
+    W = T.PackedTrits.from_v11(O.v11_pack(O.rand_trits(91, K, N, 0.4)), K, N, 0.023)
+    X1 = torch.from_numpy(O.rand_normal_f32(92, M * K).reshape(M, K)).cuda()
+    X2 = torch.from_numpy(O.rand_normal_f32(93, M * K).reshape(M, K) * 3).cuda()
+    q = torch.empty((M, K), dtype=torch.int8, device="cuda")
+    s = torch.empty(M, dtype=torch.float32, device="cuda")
+    want1 = _run(lib, "ter_hip_gemm_out", W, _act(L.X_F32, X1.data_ptr(), q_out=q.data_ptr(),
+                                                  scale_out=s.data_ptr()), M, N)
+    want2 = _run(lib, "ter_hip_gemm_out", W, _act(L.X_F32, X2.data_ptr(), q_out=q.data_ptr(),
+                                                  scale_out=s.data_ptr()), M, N)
+    for phase in ("first call under capture", "after eager calls"):
+        print(f"static GEMM capture: {phase}", flush=True)
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+        g = _capture_static(lib, W, _act(L.X_F32, X1.data_ptr()), M, N, y, acc)
+        for rep in range(3):
+            y.fill_(float("nan"))
+            acc.fill_(-1)
+            g.replay()
+            torch.cuda.synchronize()
+            assert (acc.cpu().numpy() == want1[1]).all(), (phase, rep)
+            assert (y.cpu().numpy().view(np.int32) == want1[0].view(np.int32)).all(), (phase, rep)
+            # eager work through the same static workspace between replays
+            sy, sa = _run(lib, "ter_hip_gemm_out_static", W, _act(L.X_F32, X2.data_ptr()), M, N)
+            assert (sa == want2[1]).all() and (sy.view(np.int32) == want2[0].view(np.int32)).all(), (phase, rep)
+        del g
+
+
 @pytest.mark.gpu
 def test_static_gemm_matches_workspace_entry(cuda):
     import torch
