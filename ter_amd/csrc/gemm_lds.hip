@@ -76,9 +76,12 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 constexpr int kLWaves = 8;
 
 // PW producer waves (0: the 8 compute waves issue the loads themselves).
-template <int MBW_, int S_, int RS_, int NST_, int PW_ = 0>
+template <int MBW_, int S_, int RS_, int NST_, int PW_ = 0, int FS_ = 0>
 struct LCfg {
     static constexpr int MBW = MBW_, S = S_, RS = RS_, NST = NST_, PW = PW_;
+    // FS: stage hand-over through LDS counters instead of a workgroup
+    // barrier per unit (needs producer waves)
+    static constexpr bool FS = FS_ != 0 && PW > 0;
     static constexpr int THREADS = 64 * (kLWaves + PW);
     static constexpr int IW = PW > 0 ? PW : kLWaves;  // waves that issue the loads
     static constexpr int MB = RS * MBW;               // row blocks of 16
@@ -87,7 +90,8 @@ struct LCfg {
     static constexpr int XB = MB * 16 * kUnitK;       // X bytes per stage
     static constexpr int STB = XB + BS * kTileBytes;  // bytes per stage
     static constexpr int XSO = NST * STB;             // row-scale slots: NST x 1 KiB
-    static constexpr int LDS = XSO + NST * 1024;
+    static constexpr int FLO = XSO + NST * 1024;      // stage counters: ready[NST], freed[NST]
+    static constexpr int LDS = FLO + 64;
     static constexpr int XI = XB / 1024;              // 1 KiB load runs of X per stage
     static constexpr int NI = XI + BS;                // load runs per stage, run q issued by issuer q % IW
     static constexpr int NIW = NI / IW;               // runs of issuers >= NR ...
@@ -122,8 +126,10 @@ struct LCfg {
 // the smaller stages a third ring stage (M = 128: 325 -> 284 us against
 // 32-strip blocks of 8 compute waves that issued their own loads; M = 64:
 // 200 -> 180 us); 32-strip blocks at M = 32 (2 per wave: 142 against 138 us);
-// four stages at M = 16 (124 -> 120 us).  (Each can be overridden at build
-// time.)
+// four stages at M = 16 (124 -> 120 us).  FS (the sixth field): at M = 32
+// the stages change hands through LDS counters instead of a barrier per unit
+// (123.2 -> 117.4 us); at 8, 16, 64, 128 and 256 rows the barrier is as fast
+// or 1-2% faster.  (Each can be overridden at build time.)
 #ifndef TER_LDS_PW
 #define TER_LDS_PW 4
 #endif
@@ -131,7 +137,7 @@ struct LCfg {
 #define TER_LDS_CFG1 1, 2, 1, 4, TER_LDS_PW
 #endif
 #ifndef TER_LDS_CFG2
-#define TER_LDS_CFG2 2, 4, 1, 3, TER_LDS_PW
+#define TER_LDS_CFG2 2, 4, 1, 3, TER_LDS_PW, 1
 #endif
 using Cfg1 = LCfg<TER_LDS_CFG1>;
 using Cfg2 = LCfg<TER_LDS_CFG2>;
@@ -157,6 +163,47 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+}
+
+// Stage hand-over without a workgroup barrier (PW > 0).  Two monotonic
+// counters per ring stage in LDS: ready[s] counts the producers' "my loads
+// of the unit in stage s have landed" signals (PW per use of the stage),
+// freed[s] the compute waves' "done reading stage s" signals (kLWaves per
+// use).  A compute wave waits for ready of its next unit only; a producer
+// waits for freed of the stage it is about to refill only.  So no wave
+// waits for the slowest of the others at every stage, and a stage is freed
+// as soon as its last operand is read, before the MFMAs on it finish.  LDS
+// operations of one wave execute in order, and a producer signals only
+// after its direct-to-LDS loads have landed (vmcnt), so a wave that sees a
+// count has the data (or the free slot) it stands for.  Every wait gives up
+// after kSpinCap polls (the kernel then ends with wrong results instead of
+// hanging; the parity tests would show it).
+//
+// The counter accesses are written as inline ds instructions: for a plain
+// LDS access the compiler first waits for every direct-to-LDS load in
+// flight (it cannot tell that the counters do not alias the ring), which in
+// a producer would drain the whole pipeline at every signal.
+constexpr int kSpinCap = 1 << 18;
+
+__device__ __forceinline__ unsigned lds_off(unsigned char* p) {
+    return (unsigned)reinterpret_cast<uintptr_t>((TER_LDS unsigned char*)p);
+}
+
+__device__ __forceinline__ void spin_ge(unsigned char* lds_byte, unsigned target) {
+    const unsigned a = lds_off(lds_byte);
+    for (int n = 0; n < kSpinCap; ++n) {
+        unsigned v;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
+        if ((unsigned)__builtin_amdgcn_readfirstlane((int)v) >= target) break;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ void signal_one(unsigned char* lds_byte, int lane) {
+    const unsigned a = lds_off(lds_byte);
+    asm volatile("" ::: "memory");
+    if (lane == 0) asm volatile("ds_add_u32 %0, %1" : : "v"(a), "v"(1u) : "memory");
 }
 
 // Wait until this wave's loads of the unit `behind` stages older than the
@@ -260,7 +307,8 @@ constexpr int kAPrefetch = TER_LDS_APF;
 // their MFMAs, which exposed the LDS latency on every step.
 template <class C>
 __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg, int sg, int lane,
-                                              i32x4 (&acc)[C::S][C::MBW], i32x4 (&rsum)[C::MBW]) {
+                                              i32x4 (&acc)[C::S][C::MBW], i32x4 (&rsum)[C::MBW],
+                                              unsigned char* freed) {
     const int j = lane & 15, g = lane >> 4;
     // (two steps ahead at 8 row blocks, whose accumulators leave no room for a third)
     constexpr int KS = 4, T = KS * C::MBW, P = C::MBW >= 8 ? 2 : (kAPrefetch < T ? kAPrefetch : T);
@@ -284,6 +332,9 @@ __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg
     i32x4 A[P];
 #pragma unroll
     for (int t = 0; t < P; ++t) A[t] = a_at(t);
+    // the stage's last operand read issued: hand the stage back (freed is
+    // null where the caller signals later)
+    if (P >= T && freed) signal_one(freed, lane);
     i32x4 B[C::S];
 #pragma unroll
     for (int t = 0; t < T; ++t) {
@@ -294,6 +345,7 @@ __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg
         }
         const i32x4 a = A[t % P];
         if (t + P < T) A[t % P] = a_at(t + P);
+        if (t + P == T - 1 && freed) signal_one(freed, lane);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < C::S; ++s)
@@ -392,18 +444,50 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
             }
         }
     };
+    unsigned char* const ready = lds + C::FLO;             // ready[NST]
+    unsigned char* const freed = lds + C::FLO + 4 * C::NST;  // freed[NST]
+    if (C::FS) {
+        if (threadIdx.x < 2 * C::NST) reinterpret_cast<unsigned*>(ready)[threadIdx.x] = 0u;
+        __syncthreads();
+    }
     if (C::PW == 0 || producer) {
 #pragma unroll
         for (int p = 0; p < C::NST - 1; ++p)
             if (ib < b_hi) issue_next();
     }
+    if (C::FS && producer) {
+        // Producer waves, unit j: wait for their loads of unit j (vmcnt) and
+        // signal it ready; then refill the stage unit j - 1 used with unit
+        // j + NST - 1 once every compute wave has freed it.  A producer that
+        // stalls at its loads (the memory pipeline accepts only so many in
+        // flight) holds back no MFMA; the compute waves wait only when the
+        // data is late.
+        int cb = b_lo, cu = 0, j = 0, js = 0, cku = block_at<kList>(single, list, blocks, cb, C::BS).d.Ku;
+        while (true) {
+            wait_stage<C>(n_issued - j - 1, issuer);
+            signal_one(ready + 4 * js, lane);
+            if (ib < b_hi) {
+                if (j >= 1) {
+                    const int jp = j - 1, sp = js == 0 ? C::NST - 1 : js - 1;
+                    spin_ge(freed + 4 * sp, (unsigned)(kLWaves * (jp / C::NST + 1)));
+                }
+                issue_next();
+            }
+            ++j;
+            js = js + 1 == C::NST ? 0 : js + 1;
+            if (++cu == cku) {
+                if (++cb >= b_hi) break;
+                cku = block_at<kList>(single, list, blocks, cb, C::BS).d.Ku;
+                cu = 0;
+            }
+        }
+        return;
+    }
     if (producer) {
-        // Producer waves: wait for their loads of stage it, meet the compute
-        // waves at the stage's barrier, then issue the stage that refills the
-        // slot the compute waves have just left.  A producer that stalls at
-        // its loads (the memory pipeline accepts only so many in flight)
-        // holds back no MFMA; the compute waves wait only when the data is
-        // late.  Same stage count and barrier count as the compute waves.
+        // Producer waves with a workgroup barrier per unit: wait for their
+        // loads of unit it, meet the compute waves at the unit's barrier, then
+        // issue the unit that refills the stage the compute waves have just
+        // left.  Same unit count and barrier count as the compute waves.
         int cb = b_lo, cu = 0, it = 0, cku = block_at<kList>(single, list, blocks, cb, C::BS).d.Ku;
         while (true) {
             wait_stage<C>(n_issued - it - 1, issuer);
@@ -431,10 +515,20 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
 #pragma unroll
     for (int mb = 0; mb < C::MBW; ++mb) rsum[mb] = i32x4{0, 0, 0, 0};
     while (true) {
-        if (C::PW == 0) wait_stage<C>(n_issued - it - 1, issuer);
-        lds_barrier();
-        if (C::PW == 0 && ib < b_hi) issue_next();
-        compute_stage<C>(lds + c_stage * C::STB, rg, sg, lane, acc, rsum);
+        const bool last_unit = cu + 1 == bc.d.Ku;
+        if constexpr (C::FS) {
+            spin_ge(ready + 4 * c_stage, (unsigned)(C::PW * (it / C::NST + 1)));
+            // the block's last unit is freed after its epilogue has read the
+            // row scales (the slot they sit in is refilled NST blocks on)
+            compute_stage<C>(lds + c_stage * C::STB, rg, sg, lane, acc, rsum,
+                             last_unit ? nullptr : freed + 4 * c_stage);
+        } else {
+            if (C::PW == 0) wait_stage<C>(n_issued - it - 1, issuer);
+            lds_barrier();
+            if (C::PW == 0 && ib < b_hi) issue_next();
+            compute_stage<C>(lds + c_stage * C::STB, rg, sg, lane, acc, rsum, nullptr);
+        }
+        const int done_stage = c_stage;
         ++it;
         c_stage = c_stage + 1 == C::NST ? 0 : c_stage + 1;
         if (++cu == bc.d.Ku) {
@@ -549,6 +643,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
                     }
                 }
             }
+            if constexpr (C::FS) signal_one(freed + 4 * done_stage, lane);
 #pragma unroll
             for (int s = 0; s < C::S; ++s)
 #pragma unroll
