@@ -563,6 +563,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
             // 64-bit address (the general form below takes 20 or more
             // instructions a store, and the matrix cores idle meanwhile).
             const bool fast_y = vec_out && d.y && !d.acc && d.w_mag == 1 && (long long)d.M * d.N <= (1LL << 29);
+            bool freed_early = false;  // (FS) the stage freed before the stores
             if (fast_y) {
                 // Strips in pairs (2 t, 2 t + 1), whole 128-byte lines per
                 // store: after the transpose lane (j, g) holds row 4 g + j % 4
@@ -577,6 +578,18 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
                 // made it cost from two row blocks per wave on.
                 const __amdgpu_buffer_rsrc_t yr = __builtin_amdgcn_make_buffer_rsrc(
                     (void*)d.y, 0, (int)((unsigned)d.M * (unsigned)d.N * 4u), 0x00020000);
+                // this lane's row scales first, then the stage is free
+                float scl[C::MBW][2];
+#pragma unroll
+                for (int mb = 0; mb < C::MBW; ++mb)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        scl[mb][h] = xs_l[(rg * C::MBW + mb) * 16 + (g >> 1) * 8 + h * 4 + (lane & 3)] * d.w_scale;
+                if constexpr (C::FS) {
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    signal_one(freed + 4 * done_stage, lane);
+                    freed_early = true;
+                }
 #pragma unroll
                 for (int mb = 0; mb < C::MBW; ++mb) {
 #pragma unroll
@@ -593,7 +606,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
 #pragma unroll
                         for (int h = 0; h < 2; ++h) {
                             const int row = (rg * C::MBW + mb) * 16 + (g >> 1) * 8 + h * 4 + (lane & 3);
-                            const float sc = xs_l[row] * d.w_scale;
+                            const float sc = scl[mb][h];
                             const unsigned off = row < d.M && col < d.N
                                                      ? ((unsigned)row * (unsigned)d.N + (unsigned)col) * 4u
                                                      : 0x80000000u;
@@ -643,7 +656,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
                     }
                 }
             }
-            if constexpr (C::FS) signal_one(freed + 4 * done_stage, lane);
+            if (C::FS && !freed_early) signal_one(freed + 4 * done_stage, lane);
 #pragma unroll
             for (int s = 0; s < C::S; ++s)
 #pragma unroll
