@@ -176,6 +176,10 @@ constexpr int kGemvWgPerCu = 2;
 // kernel (96 VGPRs): four workgroups per CU hide more latency there (C2
 // Llama sweep: 42.6 against 43.3 us at two); the other kinds keep two.
 constexpr int kGemvWgPerCuI8 = 4;
+// fp32 activations (the in-kernel absmax prologue; that kernel fits three
+// waves per SIMD): three workgroups per CU (C3 BitNet sweep: 86.3 against
+// 87.0 us at two, 91.4 at four, the fourth waiting for a free slot).
+constexpr int kGemvWgPerCuF32 = 3;
 // A launch whose activations need a prologue (any kind but X_I8) and that
 // has fewer tiles than this per workgroup at kGemvWgPerCu uses one workgroup
 // per CU: every workgroup repeats the prologue, and below this size halving
@@ -231,7 +235,8 @@ int pick_wg(long long total_tiles, int wg_per_cu, int lds_bytes, bool prologue, 
     if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
     const int fit = gemv_max_wg_per_cu(lds_bytes, vec_kind);
     if (fit <= 0) return fail(TER_HIP_ERR_SHAPE, "GEMV workgroup does not fit a CU (LDS %d bytes)", lds_bytes);
-    const int dflt = vec_kind == TER_HIP_X_I8 ? kGemvWgPerCuI8 : kGemvWgPerCu;
+    const int dflt = vec_kind == TER_HIP_X_I8 ? kGemvWgPerCuI8
+                     : (vec_kind == TER_HIP_X_F32 ? kGemvWgPerCuF32 : kGemvWgPerCu);
     int per_cu = wg_per_cu > 0 ? wg_per_cu : (dflt < fit ? dflt : fit);
     if (wg_per_cu <= 0 && prologue && total_tiles < (long long)cus * kGemvWgPerCu * kSmallPlanTilesPerWg) per_cu = 1;
     long long g = (long long)cus * per_cu;

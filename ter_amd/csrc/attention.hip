@@ -68,31 +68,9 @@ struct AttnArgs {
     float inv_sqrt;
 };
 
-// The softmax exp: Cody-Waite reduction, degree-7 Taylor polynomial in Horner
-// form, two-step scaling by 2^n.  The same operations as the oracle's
-// orc_expf, so both round identically (faithful: < 1 ulp from exp).
-__device__ __forceinline__ float pow2i(int e) { return __builtin_bit_cast(float, (unsigned)(e + 127) << 23); }
-
-__device__ __forceinline__ float attn_expf(float x) {
-#pragma clang fp contract(off)
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return __builtin_inff();
-    if (x < -103.972084045410156f) return 0.0f;
-    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
-    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
-    r = __builtin_fmaf(-n, 1.42860676533018704e-06f, r);
-    float p = 1.98412701e-04f;
-    p = __builtin_fmaf(p, r, 1.38888892e-03f);
-    p = __builtin_fmaf(p, r, 8.33333377e-03f);
-    p = __builtin_fmaf(p, r, 4.16666679e-02f);
-    p = __builtin_fmaf(p, r, 1.66666672e-01f);
-    p = __builtin_fmaf(p, r, 0.5f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    const int ni = (int)n;
-    const int n1 = ni / 2, n2 = ni - n1;
-    return (p * pow2i(n1)) * pow2i(n2);
-}
+// The softmax exp is ter_expf (common.h), the same operations as the oracle's
+// orc_expf, so both round identically.
+__device__ __forceinline__ float attn_expf(float x) { return ter_expf(x); }
 
 // RoPE of one pair (x0, x1) with table entry (c, s): the reference's
 // v0*c - v1*s and v0*s + v1*c, each one fused multiply-add over the other

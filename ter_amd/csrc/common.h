@@ -280,6 +280,33 @@ __device__ __forceinline__ void emit_out(const D& d, long long o, int val, float
     }
 }
 
+// exp(x) of this build (the reference calls CUDA's expf): Cody-Waite
+// reduction with a two-constant ln 2, degree-7 Taylor polynomial in Horner
+// form, two-step scaling by 2^n.  Faithful (< 1 ulp from exp); the oracle's
+// orc_expf runs the same operations, so both round identically.
+__device__ inline float ter_pow2i(int e) { return __builtin_bit_cast(float, (unsigned)(e + 127) << 23); }
+
+__device__ inline float ter_expf(float x) {
+#pragma clang fp contract(off)
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -103.972084045410156f) return 0.0f;
+    const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.42860676533018704e-06f, r);
+    float p = 1.98412701e-04f;
+    p = __builtin_fmaf(p, r, 1.38888892e-03f);
+    p = __builtin_fmaf(p, r, 8.33333377e-03f);
+    p = __builtin_fmaf(p, r, 4.16666679e-02f);
+    p = __builtin_fmaf(p, r, 1.66666672e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const int ni = (int)n;
+    const int n1 = ni / 2, n2 = ni - n1;
+    return (p * ter_pow2i(n1)) * ter_pow2i(n2);
+}
+
 // relu^2(gate) * up of relu2_mul_rmsnorm_quant_k
 // (cuda/ter_cuda_forward_bitnet.cu:273-276): the square rounds first, then
 // the product.

@@ -51,6 +51,14 @@ constexpr int batch_of() {
     return kKind == TER_HIP_X_F32 || kKind < 0 ? 6 : (kKind >= TER_HIP_X_F32_RMS ? 4 : 5);
 }
 
+// Waves per SIMD the stream-K kernel is compiled for: 4 for int8 X (the
+// workgroups of its default launch, kGemvWgPerCuI8 = 4 per CU, all resident),
+// otherwise whatever the registers allow.
+template <int kKind>
+constexpr int gemv_waves_per_eu() {
+    return kKind == TER_HIP_X_I8 ? 4 : 1;
+}
+
 // Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
 __device__ __forceinline__ int row_sum16(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, true);   // quad_perm [1,0,3,2]
@@ -979,41 +987,80 @@ __device__ __forceinline__ Fixups partials_to_slots(const GemvDesc& d, const Par
     return f;
 }
 
-__device__ __forceinline__ Fixups combine_partials(const GemvDesc& d, const int* slots, float s) {
-    const int wave = uniform(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    const int c = (lane >> 4) * 4 + (lane & 15);  // column within the strip of lanes q < 4
-    Fixups f = no_fixups(d, s);
+// Combine mode: the strips a segment's waves share meet in LDS slots without
+// a workgroup barrier.  The segment's boundaries b_0 .. b_4 (local tiles:
+// the workgroup's start, the wave boundaries, its end) are known to every
+// wave; a strip holding boundary b strictly inside gets slot b, or the slot
+// of the lowest boundary inside the same strip.  Slot j = [unit count, 16
+// column sums], zeroed while the activations are staged.  A wave adds its
+// partial column sums (ds_add), then its unit count with one workgroup-scope
+// acquire-release add; the add that brings the count to the strip's units
+// within the segment completes it: that wave reads the sums and writes the
+// column (all Ku units here), or adds it to the global fix-up slot (the strip
+// continues in another workgroup's range).  Integer sums, so the result does
+// not depend on which wave completes.
+constexpr int kSlotInts = 1 + kStripCols;
+static_assert((kGemvWaves + 1) * kSlotInts * 4 <= kGemvSlotBytes, "combine slots fit the slot area");
+
+struct SegBounds {
+    int b[kGemvWaves + 1];  // local tiles of the segment's boundaries
+    int Ku;
+};
+
+// Slot of the partial strip `st` holding boundary `from` strictly inside it:
+// the lowest boundary of the run of boundaries inside that strip.  (Constant
+// indices only, so the bounds stay in scalar registers.)
+__device__ __forceinline__ int strip_slot(const SegBounds& sb, int from, int st) {
+    int j = from;
+    bool run = true;
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        const int me = 2 * wave + k;
-        const int st = uniform(slots[me * kGemvSlotInts]);
-        if (st < 0) continue;
-        bool lead = true;
-        for (int j = 0; j < me; ++j) lead = lead && slots[j * kGemvSlotInts] != st;
-        if (!uniform(lead ? 1 : 0)) continue;
-        int units = 0, val = 0;
-        for (int j = me; j < 2 * kGemvWaves; ++j) {
-            const int* sl = slots + j * kGemvSlotInts;
-            if (sl[0] == st) {
-                units += sl[1];
-                val += (lane & 15) < 4 ? sl[2 + (c & 15)] : 0;
-            }
-        }
-        units = uniform(units);
-        if (!col_owner(d, st)) continue;
-        if (units == d.Ku) {
-            emit(d, strip_col(st), val, s);
-        } else if (k == 0) {
-            f.col_first = strip_col(st);
-            f.w_first = part_word(units, val);
-            f.o_first = part_add(d, f.col_first, f.w_first);
-        } else {
-            f.col_last = strip_col(st);
-            f.w_last = part_word(units, val);
-            f.o_last = part_add(d, f.col_last, f.w_last);
+    for (int w = kGemvWaves - 1; w >= 0; --w) {
+        if (w < from) {
+            const bool in = sb.b[w] % sb.Ku != 0 && sb.b[w] / sb.Ku == st;
+            if (run && in)
+                j = w;
+            else
+                run = false;
         }
     }
+    return j;
+}
+
+__device__ __forceinline__ void slot_finish(const GemvDesc& d, int* slots, const SegBounds& sb, int from, int st,
+                                            int units, int val, float s, int& col_out, unsigned long long& w_out,
+                                            unsigned long long& o_out) {
+    const int lane = threadIdx.x & 63;
+    const int c = (lane >> 4) * 4 + (lane & 15);  // column within the strip of lanes q < 4
+    int* sl = slots + strip_slot(sb, from, st) * kSlotInts;
+    const int lo = st * sb.Ku > sb.b[0] ? st * sb.Ku : sb.b[0];
+    const int hi = (st + 1) * sb.Ku < sb.b[kGemvWaves] ? (st + 1) * sb.Ku : sb.b[kGemvWaves];
+    const int expect = hi - lo;  // units of the strip within the segment
+    if ((lane & 15) < 4) __hip_atomic_fetch_add(sl + 1 + c, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(sl, units, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    old = uniform(old);
+    if (old + units != expect) return;
+    const int tot = (lane & 15) < 4 ? __hip_atomic_load(sl + 1 + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) : 0;
+    if (!col_owner(d, st)) return;
+    if (expect == d.Ku) {
+        emit(d, strip_col(st), tot, s);
+    } else {
+        col_out = strip_col(st);
+        w_out = part_word(expect, tot);
+        o_out = part_add(d, col_out, w_out);
+    }
+}
+
+__device__ __forceinline__ Fixups combine_partials(const GemvDesc& d, int* slots, const SegBounds& sb,
+                                                   const Partials& pr, float s) {
+    const int wave = uniform(threadIdx.x >> 6);
+    Fixups f = no_fixups(d, s);
+    if (pr.st_first >= 0)
+        slot_finish(d, slots, sb, wave, pr.st_first, pr.units_first, pr.val_first, s, f.col_first, f.w_first,
+                    f.o_first);
+    if (pr.st_last >= 0)
+        slot_finish(d, slots, sb, wave + 1, pr.st_last, pr.units_last, pr.val_last, s, f.col_last, f.w_last,
+                    f.o_last);
     return f;
 }
 
@@ -1023,7 +1070,8 @@ __device__ __forceinline__ Fixups combine_partials(const GemvDesc& d, const int*
 // either way.  kKind >= 0: every GEMV has that activation kind and qualifies
 // for the vector prologue; -1: any kind.
 template <bool kList, int kKind>
-__global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
+__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(gemv_waves_per_eu<kKind>())))
+void gemv_t16_kernel(GemvDesc single,
                                                             const GemvDesc* __restrict__ list,
                                                             const int32_t* __restrict__ first,
                                                             const long long* __restrict__ ranges,
@@ -1087,6 +1135,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
             act = stage_x(d, xpre, lds_x, usum, red, xs32, t == d.tile0);
         else
             act = stage_x_vec<kKind>(d, xraw, lds_x, usum, red, xs32, t == d.tile0);
+        if (combine && threadIdx.x < (kGemvWaves + 1) * kSlotInts) slots[threadIdx.x] = 0;
         __syncthreads();
         const float s = act * d.w_scale;  // x_scale * w_scale (forward.cpp:342)
         Partials pr;
@@ -1097,21 +1146,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_t16_kernel(GemvDesc single,
         if (!combine) {
             f = partials_to_slots(d, pr, s);
         } else {
-            const int lane = threadIdx.x & 63;
-            int* sl = slots + 2 * wave * kGemvSlotInts;
-            if (lane == 0) {
-                sl[0] = pr.st_first;
-                sl[1] = pr.units_first;
-                sl[kGemvSlotInts] = pr.st_last;
-                sl[kGemvSlotInts + 1] = pr.units_last;
-            }
-            if ((lane & 15) < 4) {
-                const int c = (lane >> 4) * 4 + (lane & 15);
-                sl[2 + c] = pr.val_first;
-                sl[kGemvSlotInts + 2 + c] = pr.val_last;
-            }
-            __syncthreads();
-            f = combine_partials(d, slots, s);
+            SegBounds sb;
+            sb.Ku = d.Ku;
+#pragma unroll
+            for (int w = 0; w <= kGemvWaves; ++w) sb.b[w] = (int)(t + nseg * w / kGemvWaves - d.tile0);
+            f = combine_partials(d, slots, sb, pr, s);
         }
         if (have_prev) finish_fixups(prev);
         prev = f;
