@@ -102,8 +102,8 @@ __device__ __forceinline__ float wave_max_f(float v) {
     v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
     v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
     v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
-    v = fmaxf(v, __shfl_xor(v, 16));
-    return fmaxf(v, __shfl_xor(v, 32));
+    v = fmaxf(v, lane_xor16(v));
+    return fmaxf(v, lane_xor32(v));
 }
 
 // The xor butterfly sum  for o = 32, 16, ..., 1: v += v[lane ^ o]  (every
@@ -113,8 +113,8 @@ __device__ __forceinline__ float wave_max_f(float v) {
 // shifted by 4 in one direction or the other, xor 2 and 1 are quad
 // permutations.
 __device__ __forceinline__ float xor_sum64(float v) {
-    v = v + __shfl_xor(v, 32);
-    v = v + __shfl_xor(v, 16);
+    v = v + lane_xor32(v);
+    v = v + lane_xor16(v);
     v = v + dpp_f<0x128>(v);  // row_ror:8 (lane ^ 8 within the row)
     const float up = dpp_f<0x104>(v), down = dpp_f<0x114>(v);  // row_shl:4 (lane + 4), row_shr:4 (lane - 4)
     v = v + (((threadIdx.x & 4) == 0) ? up : down);

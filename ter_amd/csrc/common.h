@@ -316,6 +316,39 @@ __device__ inline float relu2_mul(float g, float u) {
     return r * u;
 }
 
+// Cross-row lane exchanges of gfx950 (no LDS round trip): the value of lane
+// l ^ 32 (v_permlane32_swap) and of lane l ^ 16 (v_permlane16_swap).
+__device__ __forceinline__ float lane_xor32(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor16(float v) {
+    const unsigned u = __builtin_bit_cast(unsigned, v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+}
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, true));
+}
+
+// The shuffle-down tree of a wave (for s = 32, 16, ..., 1: a[l] += a[l + s])
+// as seen by lane 0, returned to every lane: the same two operands at each
+// level for every lane that lane 0's sum depends on (lanes l < s), so the bits
+// are those of the __shfl_down form.  Levels 32 and 16 use the permlane
+// swaps, 8 .. 1 DPP row_shl inside the row.
+__device__ __forceinline__ float tree_down64(float a) {
+    a = a + lane_xor32(a);
+    a = a + lane_xor16(a);
+    a = a + dpp_move_f<0x108>(a);  // row_shl:8 (lane + 8)
+    a = a + dpp_move_f<0x104>(a);  // row_shl:4
+    a = a + dpp_move_f<0x102>(a);  // row_shl:2
+    a = a + dpp_move_f<0x101>(a);  // row_shl:1
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, a), 0));
+}
+
 // Sum of one value per thread of a 256-thread block, paired exactly as the
 // reference's shared-memory tree (for s = 128, 64, ..., 1: partial[t] +=
 // partial[t + s]): shared memory for the two cross-wave levels, lane shuffles
@@ -328,9 +361,7 @@ __device__ inline float tree_sum256(float v, float* red) {
     if (t < 128) red[t] = red[t] + red[t + 128];
     __syncthreads();
     if (t < 64) {
-        float a = red[t] + red[t + 64];
-#pragma unroll
-        for (int s = 32; s >= 1; s >>= 1) a = a + __shfl_down(a, s);
+        const float a = tree_down64(red[t] + red[t + 64]);
         if (t == 0) red[0] = a;
     }
     __syncthreads();

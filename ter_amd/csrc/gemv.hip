@@ -79,8 +79,8 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmax_dpp<0x4E>(v);
     v = fmax_dpp<0x141>(v);
     v = fmax_dpp<0x140>(v);
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
+    v = fmaxf(v, lane_xor16(v));
+    v = fmaxf(v, lane_xor32(v));
     return v;
 }
 
@@ -590,10 +590,7 @@ __device__ __forceinline__ float tree_sum256_all(float v, float* red) {
     const int t = threadIdx.x, l = t & 63;
     red[t] = v;
     __syncthreads();
-    float a = (red[l] + red[l + 128]) + (red[l + 64] + red[l + 192]);
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) a = a + __shfl_down(a, s);
-    return __shfl(a, 0);
+    return tree_down64((red[l] + red[l + 128]) + (red[l + 64] + red[l + 192]));
 }
 
 template <int kKind>
