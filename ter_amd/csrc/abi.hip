@@ -369,6 +369,7 @@ struct ter_hip_plan {
     const GemmBlock* blocks_dev = nullptr;  // LDS-ring: [n_blocks] blocks, then
     const int32_t* ranges_dev = nullptr;    //   [n_wg + 1] block ranges per workgroup
     const long long* wg_ranges_dev = nullptr;  // GEMV stream-K: [n_wg + 1] tile ranges per workgroup
+    const void* wg_desc_dev = nullptr;         // GEMV strip mode: [n_wg] copies of each workgroup's first descriptor
     int n_blocks = 0;
     uint64_t bytes = 0, macs = 0;
 };
@@ -399,7 +400,7 @@ struct ter_hip_handle {
 // first unit, strictly increasing.
 template <typename Desc>
 int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<long long>& starts, long long total,
-                int n_wg, const std::vector<long long>* ranges = nullptr) {
+                int n_wg, const std::vector<long long>* ranges = nullptr, bool wg_copies = false) {
     std::vector<int32_t> first((size_t)n_wg);
     size_t di = 0;
     for (int g = 0; g < n_wg; ++g) {
@@ -410,7 +411,13 @@ int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<
     const size_t db = sizeof(Desc) * ds.size();
     const size_t fb = (sizeof(int32_t) * (size_t)n_wg + 7) / 8 * 8;
     const size_t rb = ranges ? sizeof(long long) * ranges->size() : 0;
-    hipError_t e = hipMalloc(&p->descs_dev, db + fb + rb);
+    // wg_copies: then each workgroup's first descriptor once more, in workgroup order
+    const size_t cb0 = (db + fb + rb + 15) / 16 * 16;
+    std::vector<Desc> copies;
+    if (wg_copies)
+        for (int g = 0; g < n_wg; ++g) copies.push_back(ds[(size_t)first[(size_t)g]]);
+    const size_t cb = sizeof(Desc) * copies.size();
+    hipError_t e = hipMalloc(&p->descs_dev, cb0 + cb);
     if (e != hipSuccess) {
         p->descs_dev = nullptr;
         return hip_fail(e, "plan descriptor allocation");
@@ -419,6 +426,7 @@ int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<
     e = hipMemcpy(base, ds.data(), db, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemcpy(base + db, first.data(), sizeof(int32_t) * (size_t)n_wg, hipMemcpyHostToDevice);
     if (e == hipSuccess && ranges) e = hipMemcpy(base + db + fb, ranges->data(), rb, hipMemcpyHostToDevice);
+    if (e == hipSuccess && cb) e = hipMemcpy(base + cb0, copies.data(), cb, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         (void)hipFree(p->descs_dev);
         p->descs_dev = nullptr;
@@ -426,6 +434,7 @@ int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<
     }
     p->first_dev = reinterpret_cast<const int32_t*>(base + db);
     p->wg_ranges_dev = ranges ? reinterpret_cast<const long long*>(base + db + fb) : nullptr;
+    p->wg_desc_dev = cb ? base + cb0 : nullptr;
     return TER_HIP_OK;
 }
 
@@ -1010,7 +1019,8 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
     if (strip_mode) {
-        rc = upload_plan(p, ds, strip_starts, strips, n_wg);
+        for (size_t i = 0; i < ds.size(); ++i) ds[i].self = (int32_t)i;
+        rc = upload_plan(p, ds, strip_starts, strips, n_wg, nullptr, true);
     } else {
         const std::vector<long long> ranges = plan_ranges(ds, starts, tile, n_wg);
         rc = upload_plan(p, ds, starts, tile, n_wg, &ranges);
@@ -1050,7 +1060,8 @@ int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
     } else {
         GemvDesc none{};
         if (plan->strip_mode)
-            e = launch_gemv_strips(static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev, plan->total,
+            e = launch_gemv_strips(static_cast<const GemvDesc*>(plan->descs_dev),
+                                   static_cast<const GemvDesc*>(plan->wg_desc_dev), plan->total,
                                    plan->n_wg, plan->lds_bytes, plan->part_off, plan->vec_kind,
                                    static_cast<hipStream_t>(stream));
         else

@@ -62,6 +62,7 @@ struct alignas(16) GemvDesc {
     int32_t x_kind;
     float eps;                   // RMS kinds
     int32_t w_mag;               // trit magnitude m of a {-m, 0, +m} payload (1 for plain trits)
+    int32_t self;                // index of this descriptor in its plan's list (strip-mode plans)
 };
 
 // One GEMM (M > 1) of a work list.  Its blocks (4 column strips x all K each)
@@ -90,7 +91,7 @@ struct alignas(16) GemmDesc {
 // strip stream ([total_strips] over the list) and reduce the waves' partials
 // in LDS at part_off; at most kStripModeMaxStrips strips per workgroup.
 constexpr int kStripModeMaxStrips = 32;
-hipError_t launch_gemv_strips(const GemvDesc* list_dev, const int32_t* first_dev, long long total_strips, int n_wg,
+hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_dev, long long total_strips, int n_wg,
                               int lds_bytes, int part_off, int vec_kind, hipStream_t st);
 // The same for one GEMV whose descriptor is a kernel argument (any activation kind).
 hipError_t launch_gemv_strips_single(const GemvDesc& d, long long total_strips, int n_wg, int lds_bytes, int part_off,

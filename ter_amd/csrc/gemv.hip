@@ -1168,7 +1168,7 @@ void gemv_t16_kernel(GemvDesc single,
 // kernel's) and writes the outputs.  No fix-up slots, no global atomics.
 template <bool kList, int kKind>
 __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc single, const GemvDesc* __restrict__ list,
-                                                                  const int32_t* __restrict__ first,
+                                                                  const GemvDesc* __restrict__ wg_desc,
                                                                   long long total, int n_wg, int part_off) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
     int g = blockIdx.x;
@@ -1176,14 +1176,18 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc singl
     const long long s_begin = total * g / n_wg;
     const long long s_end = total * (g + 1) / n_wg;
     if (s_begin >= s_end) return;
-    int di = kList ? first[g] : 0;
+    int di = 0;
     const int wave = uniform(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int voff = lane * 16;
     int* part = reinterpret_cast<int*>(lds_raw + part_off);  // [strip][wave][16 columns]
     long long sg = s_begin;
     while (sg < s_end) {
-        const GemvDesc d = kList ? list[di] : single;
+        // A plan's first segment reads the copy of its descriptor kept for
+        // this workgroup (one round of loads instead of an index, then the
+        // descriptor); later segments follow the list.
+        const GemvDesc d = kList ? *(sg == s_begin ? wg_desc + g : list + di) : single;
+        if constexpr (kList) di = d.self;
         const long long seg_end = min(s_end, d.strip0 + (long long)d.n_strips);
         const int sa = (int)(sg - d.strip0);  // first strip of the segment within the GEMV
         const int ns = (int)(seg_end - sg);
@@ -1336,33 +1340,33 @@ hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const i
     return hipGetLastError();
 }
 
-hipError_t launch_gemv_strips(const GemvDesc* list_dev, const int32_t* first_dev, long long total_strips, int n_wg,
+hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_dev, long long total_strips, int n_wg,
                               int lds_bytes, int part_off, int vec_kind, hipStream_t st) {
     const dim3 grid(n_wg), block(kGemvThreads);
     switch (vec_kind) {
     case TER_HIP_X_I8:
         hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_I8>), grid, block, lds_bytes, st, GemvDesc{},
-                           list_dev, first_dev, total_strips, n_wg, part_off);
+                           list_dev, wg_desc_dev, total_strips, n_wg, part_off);
         break;
     case TER_HIP_X_F32:
         hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F32>), grid, block, lds_bytes, st, GemvDesc{},
-                           list_dev, first_dev, total_strips, n_wg, part_off);
+                           list_dev, wg_desc_dev, total_strips, n_wg, part_off);
         break;
     case TER_HIP_X_F32_RMS:
         hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F32_RMS>), grid, block, lds_bytes, st, GemvDesc{},
-                           list_dev, first_dev, total_strips, n_wg, part_off);
+                           list_dev, wg_desc_dev, total_strips, n_wg, part_off);
         break;
     case TER_HIP_X_F16_RMS:
         hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F16_RMS>), grid, block, lds_bytes, st, GemvDesc{},
-                           list_dev, first_dev, total_strips, n_wg, part_off);
+                           list_dev, wg_desc_dev, total_strips, n_wg, part_off);
         break;
     case TER_HIP_X_RELU2_RMS:
         hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_RELU2_RMS>), grid, block, lds_bytes, st, GemvDesc{},
-                           list_dev, first_dev, total_strips, n_wg, part_off);
+                           list_dev, wg_desc_dev, total_strips, n_wg, part_off);
         break;
     default:
         hipLaunchKernelGGL((gemv_strip_kernel<true, -1>), grid, block, lds_bytes, st, GemvDesc{},
-                           list_dev, first_dev, total_strips, n_wg, part_off);
+                           list_dev, wg_desc_dev, total_strips, n_wg, part_off);
     }
     return hipGetLastError();
 }
