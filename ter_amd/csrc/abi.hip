@@ -361,6 +361,7 @@ struct ter_hip_plan {
     int vec_kind = -1;           // GEMV: common activation kind for the vector prologue, or -1
     bool strip_mode = false;     // GEMV: strip-mode kernel, total counts strips
     int part_off = 0;            // GEMV strip mode: LDS offset of the partial sums
+    bool strided = false;        // GEMV strip mode: the strided RMS prologue (gemv_strided_ok for every item)
     int mb = 0;                  // GEMM row-block count
     bool vec = false;            // GEMM: 16-byte X rows
     bool stream = false;         // GEMM: streaming kernel (M <= 16), total counts tiles
@@ -805,7 +806,7 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
     rc = pick_strip_mode(total, d.n_strips, prologue, &strip_mode, &n_wg);
     if (rc) return rc;
     if (strip_mode) {
-        const int part_off = (gemv_lds_slots_offset(w->K, d.stage32 != 0) + 15) / 16 * 16;
+        const int part_off = (gemv_strip_part_off(w->K, d.stage32 != 0) + 15) / 16 * 16;
         const long long per_wg = (d.n_strips + n_wg - 1) / n_wg;
         const int lds_strip = part_off + (int)per_wg * kGemvWaves * kStripCols * 4;
         if (gemv_max_wg_per_cu(lds_strip) > 0) {
@@ -985,7 +986,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         strips += ds[(size_t)i].n_strips;
         const int lb = gemv_t16_lds_bytes(it.w->K, ds[(size_t)i].stage32 != 0);
         if (lb > lds) lds = lb;
-        const int ls = gemv_lds_slots_offset(it.w->K, ds[(size_t)i].stage32 != 0);  // the staging area alone
+        const int ls = gemv_strip_part_off(it.w->K, ds[(size_t)i].stage32 != 0);  // the staging area alone
         if (ls > lds_stage) lds_stage = ls;
         bytes += (uint64_t)it.w->K * (uint64_t)it.w->N / 4 + (uint64_t)it.w->K * act_bytes(it.x.kind) +
                  (uint64_t)it.w->N * out_bytes(o);
@@ -1033,6 +1034,11 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     p->total = strip_mode ? strips : tile;
     p->strip_mode = strip_mode;
     p->part_off = part_off;
+    if (strip_mode && vec_kind >= 0) {
+        bool ok = true;
+        for (const GemvDesc& d : ds) ok = ok && gemv_strided_ok(vec_kind, d.K, d.stage32 != 0);
+        p->strided = ok;
+    }
     p->n_wg = n_wg;
     p->lds_bytes = lds;
     p->vec_kind = vec_kind;
@@ -1062,7 +1068,7 @@ int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
         if (plan->strip_mode)
             e = launch_gemv_strips(static_cast<const GemvDesc*>(plan->descs_dev),
                                    static_cast<const GemvDesc*>(plan->wg_desc_dev), plan->total,
-                                   plan->n_wg, plan->lds_bytes, plan->part_off, plan->vec_kind,
+                                   plan->n_wg, plan->lds_bytes, plan->part_off, plan->vec_kind, plan->strided,
                                    static_cast<hipStream_t>(stream));
         else
             e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev,

@@ -92,7 +92,10 @@ struct alignas(16) GemmDesc {
 // in LDS at part_off; at most kStripModeMaxStrips strips per workgroup.
 constexpr int kStripModeMaxStrips = 32;
 hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_dev, long long total_strips, int n_wg,
-                              int lds_bytes, int part_off, int vec_kind, hipStream_t st);
+                              int lds_bytes, int part_off, int vec_kind, bool strided, hipStream_t st);
+// Whether a strip-mode list of this activation kind and K runs the strided
+// RMS prologue (gemv.hip: stage_x_strided).
+bool gemv_strided_ok(int vec_kind, int32_t K, bool stage32);
 // The same for one GEMV whose descriptor is a kernel argument (any activation kind).
 hipError_t launch_gemv_strips_single(const GemvDesc& d, long long total_strips, int n_wg, int lds_bytes, int part_off,
                                      hipStream_t st);
@@ -444,6 +447,12 @@ constexpr int kGemvSlotInts = 2 + kStripCols;
 constexpr int kGemvSlotBytes = 2 * kGemvWaves * kGemvSlotInts * 4;
 __host__ __device__ inline int gemv_lds_slots_offset(int32_t K, bool stage32) {
     return ((stage32 ? gemv_lds_bytes_rms(K) : gemv_lds_bytes(K)) + 15) / 16 * 16;
+}
+// Strip mode: the staging area, then (RMS kinds staging fp32) the fp16 gamma
+// [Ku*256] of the one-barrier prologue; the partial sums follow at this
+// 16-byte aligned offset.
+__host__ __device__ inline int gemv_strip_part_off(int32_t K, bool stage32) {
+    return gemv_lds_slots_offset(K, stage32) + (stage32 ? units_of(K) * kUnitK * 2 : 0);
 }
 // Then per wave the column sums of the first kGemvOutStrips strips completed
 // within its piece (consecutive strips), written after its streaming loop so

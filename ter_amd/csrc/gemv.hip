@@ -727,6 +727,132 @@ __device__ __forceinline__ float stage_x_vec(const GemvDesc& d, const XRaw& r, i
     }
 }
 
+// Strided prologue of the RMS kinds in strip mode (the decode step's plans).
+// Thread t reads the values t + 256 j of x (and up) and gamma straight from
+// memory (range-checked buffer loads: zeros past K), for j < kMaxStridedKu:
+// those are exactly the values of its partial sum of squares in the
+// reference's order (X_RELU2_RMS: virtual threads t + 256 (j mod 4)), so the
+// sum needs no staging round.  The values also go to LDS (xs32, gs16) for the
+// quantization.  Then, with two workgroup barriers where stage_x_vec has
+// four: the partials meet in `red` (barrier), every wave forms the block tree
+// (tree_sum256_all's operands) and the absmax of its threads' normalized
+// values; the wave maxima meet (barrier); each wave quantizes only its own
+// units [u0, u1), the ones its GEMV loop reads (rows r of the wave take units
+// u0 + r, u0 + r + 4, ...), so a wave-level fence orders them before the loop.
+// Results are stage_x_vec's bit for bit.  Needs Ku <= kMaxStridedKu and the
+// fp32 staging (stage32); gs16: fp16 gamma [Ku*256] in LDS.
+template <int kKind>
+constexpr int max_strided_ku() {
+    return kKind == TER_HIP_X_RELU2_RMS ? 32 : 16;
+}
+
+template <int kKind>
+struct XStrided {
+    static constexpr int J = max_strided_ku<kKind>();
+    unsigned x[J];  // fp32 bits (X_F32_RMS) or fp16 bits (X_F16_RMS, gate of X_RELU2_RMS)
+    unsigned u[kKind == TER_HIP_X_RELU2_RMS ? J : 1];  // up (fp16 bits)
+    unsigned g[J];  // gamma (fp16 bits)
+};
+
+template <int kKind>
+__device__ __forceinline__ void x_prefetch_strided(const GemvDesc& d, XStrided<kKind>& r) {
+    constexpr int J = XStrided<kKind>::J;
+    const int t = threadIdx.x;
+    const __amdgpu_buffer_rsrc_t rx = vec_rsrc(d.x, d.K * kind_bytes(kKind));
+    const __amdgpu_buffer_rsrc_t rg = vec_rsrc(d.gamma, d.K * 2);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int i = t + 256 * j;
+        if constexpr (kKind == TER_HIP_X_F32_RMS)
+            r.x[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, 4 * i, 0, 0);
+        else
+            r.x[j] = __builtin_amdgcn_raw_buffer_load_b16(rx, 2 * i, 0, 0);
+    }
+    if constexpr (kKind == TER_HIP_X_RELU2_RMS) {
+        const __amdgpu_buffer_rsrc_t ru = vec_rsrc(d.up, d.K * 2);
+#pragma unroll
+        for (int j = 0; j < J; ++j) r.u[j] = __builtin_amdgcn_raw_buffer_load_b16(ru, 2 * (t + 256 * j), 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < J; ++j) r.g[j] = __builtin_amdgcn_raw_buffer_load_b16(rg, 2 * (t + 256 * j), 0, 0);
+}
+
+template <int kKind>
+__device__ __forceinline__ float stage_x_strided(const GemvDesc& d, const XStrided<kKind>& r, int8_t* lds_x,
+                                                 int* usum, float* red, float* xs32, uint16_t* gs16, int u0, int u1,
+                                                 bool owner) {
+#pragma clang fp contract(off)
+    constexpr int J = XStrided<kKind>::J;
+    constexpr int NP = kKind == TER_HIP_X_RELU2_RMS ? 4 : 1;
+    const int K = d.K, Ku = d.Ku;
+    const int t = threadIdx.x, lane = t & 63;
+    float x[J];
+    float P[NP];
+#pragma unroll
+    for (int k = 0; k < NP; ++k) P[k] = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        if constexpr (kKind == TER_HIP_X_F32_RMS)
+            x[j] = __builtin_bit_cast(float, r.x[j]);
+        else if constexpr (kKind == TER_HIP_X_F16_RMS)
+            x[j] = half_bits_to_float((uint16_t)r.x[j]);
+        else
+            x[j] = relu2_mul(half_bits_to_float((uint16_t)r.x[j]), half_bits_to_float((uint16_t)r.u[j]));
+        P[j % NP] = __builtin_fmaf(x[j], x[j], P[j % NP]);  // past K: fma(0, 0, p) = p
+        if (j < Ku) {
+            xs32[t + 256 * j] = x[j];
+            gs16[t + 256 * j] = (uint16_t)r.g[j];
+        }
+    }
+    red[t] = NP == 4 ? (P[0] + P[NP == 4 ? 2 : 0]) + (P[NP == 4 ? 1 : 0] + P[NP == 4 ? 3 : 0]) : P[0];
+    __syncthreads();
+    const float ss = tree_down64((red[lane] + red[lane + 128]) + (red[lane + 64] + red[lane + 192]));
+    const float rms_inv = 1.0f / __builtin_sqrtf(ss / (float)K + d.eps);
+    float mx = 0.f;  // zeros past K
+#pragma unroll
+    for (int j = 0; j < J; ++j) mx = fmaxf(mx, fabsf((x[j] * rms_inv) * half_bits_to_float((uint16_t)r.g[j])));
+    mx = wave_max(mx);
+    float* wmax = red + kGemvThreads;  // apart from the partials, which other waves may still read
+    if (lane == 0) wmax[t >> 6] = mx;
+    __syncthreads();
+    mx = wmax[0];
+#pragma unroll
+    for (int i = 1; i < kGemvWaves; ++i) mx = fmaxf(mx, wmax[i]);
+    const float amax = mx + 1e-9f;
+    const float scale = 127.0f / amax;
+    const float act = 1.0f / scale;
+    const int row = lane >> 4, qd = lane & 15;
+    for (int u = u0 + row; u < u1; u += 4) {
+        const int c = u * 16 + qd;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const f32x4 f = *reinterpret_cast<const f32x4*>(xs32 + c * 16 + i);
+            v[i] = f[0]; v[i + 1] = f[1]; v[i + 2] = f[2]; v[i + 3] = f[3];
+        }
+        const u32x4 gw[2] = {*reinterpret_cast<const u32x4*>(gs16 + c * 16),
+                             *reinterpret_cast<const u32x4*>(gs16 + c * 16 + 8)};
+        float g[16];
+        halves_to_float(gw, g);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = (v[i] * rms_inv) * g[i];
+        const u32x4 qv = pack_q16(v, scale);
+        *reinterpret_cast<u32x4*>(lds_x + c * 16) = qv;
+        const int su = row_sum16(sum_bytes(qv));
+        if (qd == 0) usum[u] = su;
+        if (owner && d.xq_out) {
+            const int k = c * 16;
+            const unsigned qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (k + i < K) gptr(d.xq_out)[k + i] = (int8_t)((qw[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+        }
+    }
+    if (owner && t == 0 && d.xs_out) *gptr(d.xs_out) = act;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    return act;
+}
+
 __device__ __forceinline__ void emit(const GemvDesc& d, int col, int val, float s) { emit_out(d, col, val, s); }
 
 // Accumulate 1 tile (16 bytes of this lane) into the 4 column accumulators.
@@ -1166,7 +1292,7 @@ void gemv_t16_kernel(GemvDesc single,
 // strip's partial column sums in LDS, and after a barrier wave j % 4 adds the
 // four partials of strip j (integer sums, so the result is the stream-K
 // kernel's) and writes the outputs.  No fix-up slots, no global atomics.
-template <bool kList, int kKind>
+template <bool kList, int kKind, bool kStrided = false>
 __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc single, const GemvDesc* __restrict__ list,
                                                                   const GemvDesc* __restrict__ wg_desc,
                                                                   long long total, int n_wg, int part_off) {
@@ -1214,8 +1340,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc singl
         };
         XPre xpre;
         XRaw xraw;
+        XStrided<kStrided ? kKind : TER_HIP_X_F32_RMS> xst;
         if constexpr (kKind < 0)
             x_prefetch(d, xpre);
+        else if constexpr (kStrided)
+            x_prefetch_strided<kKind>(d, xst);
         else
             x_prefetch_vec<kKind>(d, xraw);
         u32x4 wa[NB], wb[NB];
@@ -1226,11 +1355,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc singl
         float* xs32 = reinterpret_cast<float*>(lds_raw + gemv_lds_xs32_offset(d.K));
         __syncthreads();  // the previous segment is done with LDS
         float act;
-        if constexpr (kKind < 0)
+        if constexpr (kKind < 0) {
             act = stage_x(d, xpre, lds_x, usum, red, xs32, sg == d.strip0);
-        else
+            __syncthreads();
+        } else if constexpr (kStrided) {
+            uint16_t* gs16 = reinterpret_cast<uint16_t*>(lds_raw + gemv_lds_slots_offset(d.K, true));
+            act = stage_x_strided<kKind>(d, xst, lds_x, usum, red, xs32, gs16, u0, u0 + nw, sg == d.strip0);
+        } else {
             act = stage_x_vec<kKind>(d, xraw, lds_x, usum, red, xs32, sg == d.strip0);
-        __syncthreads();
+            __syncthreads();
+        }
         const float s = act * d.w_scale;  // x_scale * w_scale (forward.cpp:342)
         const int q = lane & 15;
         const int pcol = (lane >> 4) * 4 + q;  // column within the strip of lanes q < 4
@@ -1341,8 +1475,26 @@ hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const i
 }
 
 hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_dev, long long total_strips, int n_wg,
-                              int lds_bytes, int part_off, int vec_kind, hipStream_t st) {
+                              int lds_bytes, int part_off, int vec_kind, bool strided, hipStream_t st) {
     const dim3 grid(n_wg), block(kGemvThreads);
+    if (strided) {
+        switch (vec_kind) {
+        case TER_HIP_X_F32_RMS:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F32_RMS, true>), grid, block, lds_bytes, st,
+                               GemvDesc{}, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
+        case TER_HIP_X_F16_RMS:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F16_RMS, true>), grid, block, lds_bytes, st,
+                               GemvDesc{}, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
+        case TER_HIP_X_RELU2_RMS:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_RELU2_RMS, true>), grid, block, lds_bytes, st,
+                               GemvDesc{}, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
+        default:
+            return hipErrorInvalidValue;
+        }
+    }
     switch (vec_kind) {
     case TER_HIP_X_I8:
         hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_I8>), grid, block, lds_bytes, st, GemvDesc{},
@@ -1369,6 +1521,16 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_
                            list_dev, wg_desc_dev, total_strips, n_wg, part_off);
     }
     return hipGetLastError();
+}
+
+bool gemv_strided_ok(int vec_kind, int32_t K, bool stage32) {
+    const int ku = units_of(K);
+    switch (vec_kind) {
+    case TER_HIP_X_F32_RMS: return stage32 && ku <= max_strided_ku<TER_HIP_X_F32_RMS>();
+    case TER_HIP_X_F16_RMS: return stage32 && ku <= max_strided_ku<TER_HIP_X_F16_RMS>();
+    case TER_HIP_X_RELU2_RMS: return stage32 && ku <= max_strided_ku<TER_HIP_X_RELU2_RMS>();
+    default: return false;
+    }
 }
 
 hipError_t launch_gemv_strips_single(const GemvDesc& d, long long total_strips, int n_wg, int lds_bytes, int part_off,
