@@ -1004,10 +1004,14 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         rc = pick_strip_mode(tile, strips, prologue, &strip_mode, &n_wg);
         if (rc) return rc;
     }
+    bool strided = false;
     if (strip_mode) {
         part_off = (lds_stage + 15) / 16 * 16;
+        strided = vec_kind >= 0;
+        for (const GemvDesc& d : ds) strided = strided && gemv_strided_ok(vec_kind, d.K, d.stage32 != 0);
+        const int waves = strided ? gemv_strided_waves(vec_kind) : kGemvWaves;
         const long long per_wg = (strips + n_wg - 1) / n_wg;
-        const int lds_strip = part_off + (int)per_wg * kGemvWaves * kStripCols * 4;
+        const int lds_strip = part_off + (int)per_wg * waves * kStripCols * 4;
         if (gemv_max_wg_per_cu(lds_strip) > 0)
             lds = lds_strip;
         else
@@ -1034,11 +1038,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     p->total = strip_mode ? strips : tile;
     p->strip_mode = strip_mode;
     p->part_off = part_off;
-    if (strip_mode && vec_kind >= 0) {
-        bool ok = true;
-        for (const GemvDesc& d : ds) ok = ok && gemv_strided_ok(vec_kind, d.K, d.stage32 != 0);
-        p->strided = ok;
-    }
+    p->strided = strip_mode && strided;
     p->n_wg = n_wg;
     p->lds_bytes = lds;
     p->vec_kind = vec_kind;

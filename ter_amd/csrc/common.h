@@ -96,6 +96,9 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_
 // Whether a strip-mode list of this activation kind and K runs the strided
 // RMS prologue (gemv.hip: stage_x_strided).
 bool gemv_strided_ok(int vec_kind, int32_t K, bool stage32);
+// Waves per workgroup of that prologue's kernel (its strips' partial sums
+// take [strip][waves][16] ints of LDS).
+int gemv_strided_waves(int vec_kind);
 // The same for one GEMV whose descriptor is a kernel argument (any activation kind).
 hipError_t launch_gemv_strips_single(const GemvDesc& d, long long total_strips, int n_wg, int lds_bytes, int part_off,
                                      hipStream_t st);
@@ -449,10 +452,14 @@ __host__ __device__ inline int gemv_lds_slots_offset(int32_t K, bool stage32) {
     return ((stage32 ? gemv_lds_bytes_rms(K) : gemv_lds_bytes(K)) + 15) / 16 * 16;
 }
 // Strip mode: the staging area, then (RMS kinds staging fp32) the fp16 gamma
-// [Ku*256] of the one-barrier prologue; the partial sums follow at this
-// 16-byte aligned offset.
+// [Ku*256] and the partials of the strided prologue; the strips' partial
+// sums follow.
+__host__ __device__ inline int gemv_strip_red_offset(int32_t K) {
+    return gemv_lds_slots_offset(K, true) + units_of(K) * kUnitK * 2;
+}
+constexpr int kStripRedBytes = (1024 + 16) * 4;  // the strided prologue's partials and wave maxima
 __host__ __device__ inline int gemv_strip_part_off(int32_t K, bool stage32) {
-    return gemv_lds_slots_offset(K, stage32) + (stage32 ? units_of(K) * kUnitK * 2 : 0);
+    return stage32 ? gemv_strip_red_offset(K) + kStripRedBytes : gemv_lds_slots_offset(K, false);
 }
 // Then per wave the column sums of the first kGemvOutStrips strips completed
 // within its piece (consecutive strips), written after its streaming loop so

@@ -745,79 +745,155 @@ template <int kKind>
 constexpr int max_strided_ku() {
     return kKind == TER_HIP_X_RELU2_RMS ? 32 : 16;
 }
-
+// Waves per workgroup of the strided strip kernel: 8 for X_RELU2_RMS (its
+// prologue over F values and the 27-unit strips of the down projection keep
+// one wave per SIMD busy for microseconds; a second wave per SIMD shares
+// both), 4 for the 256-thread kinds, whose partials are the 256 threads'.
+#ifndef TER_STRIDED_RELU2_WAVES
+#define TER_STRIDED_RELU2_WAVES 8
+#endif
 template <int kKind>
+constexpr int strided_waves() {
+    return kKind == TER_HIP_X_RELU2_RMS ? TER_STRIDED_RELU2_WAVES : 4;
+}
+
+// Registers of the strided prologue.  The 256-thread kinds: x and gamma of
+// values t + T j.  X_RELU2_RMS: thread t owns the V = 1024 / T consecutive
+// virtual threads V t .. V t + V - 1 and reads their values V t + 1024 j as
+// one V-half vector each (gate, up and gamma: V = 4 a dwordx2, V = 2 a dword).
+template <int kKind, int kW>
 struct XStrided {
-    static constexpr int J = max_strided_ku<kKind>();
-    unsigned x[J];  // fp32 bits (X_F32_RMS) or fp16 bits (X_F16_RMS, gate of X_RELU2_RMS)
-    unsigned u[kKind == TER_HIP_X_RELU2_RMS ? J : 1];  // up (fp16 bits)
-    unsigned g[J];  // gamma (fp16 bits)
+    static constexpr int T = 64 * kW;
+    static constexpr bool R2 = kKind == TER_HIP_X_RELU2_RMS;
+    static constexpr int V = R2 ? 1024 / T : 1;                                  // values per load
+    static constexpr int J = max_strided_ku<kKind>() * kUnitK / (R2 ? 1024 : T);  // loads per operand
+    static constexpr int DW = R2 ? (V + 1) / 2 : 1;                               // dwords per load
+    unsigned x[J][DW];  // fp32 bits (X_F32_RMS) or fp16 bits (X_F16_RMS; gate of X_RELU2_RMS, V halves)
+    unsigned u[R2 ? J : 1][DW];  // up (X_RELU2_RMS)
+    unsigned g[J][DW];  // gamma (fp16 bits)
 };
 
-template <int kKind>
-__device__ __forceinline__ void x_prefetch_strided(const GemvDesc& d, XStrided<kKind>& r) {
-    constexpr int J = XStrided<kKind>::J;
+template <int DW>
+__device__ __forceinline__ void load_halves(__amdgpu_buffer_rsrc_t r, int off, unsigned (&o)[DW]) {
+    if constexpr (DW == 2) {
+        typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+        const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+        o[0] = v.x;
+        o[1] = v.y;
+    } else {
+        o[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    }
+}
+
+template <int kKind, int kW>
+__device__ __forceinline__ void x_prefetch_strided(const GemvDesc& d, XStrided<kKind, kW>& r) {
+    using XS = XStrided<kKind, kW>;
+    constexpr int J = XS::J, T = XS::T;
     const int t = threadIdx.x;
     const __amdgpu_buffer_rsrc_t rx = vec_rsrc(d.x, d.K * kind_bytes(kKind));
     const __amdgpu_buffer_rsrc_t rg = vec_rsrc(d.gamma, d.K * 2);
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int i = t + 256 * j;
-        if constexpr (kKind == TER_HIP_X_F32_RMS)
-            r.x[j] = __builtin_amdgcn_raw_buffer_load_b32(rx, 4 * i, 0, 0);
-        else
-            r.x[j] = __builtin_amdgcn_raw_buffer_load_b16(rx, 2 * i, 0, 0);
-    }
-    if constexpr (kKind == TER_HIP_X_RELU2_RMS) {
+    if constexpr (XS::R2) {
+        // (a vector past K reads as zeros: K is a multiple of 16, so a vector
+        // is either inside or wholly past it)
         const __amdgpu_buffer_rsrc_t ru = vec_rsrc(d.up, d.K * 2);
 #pragma unroll
-        for (int j = 0; j < J; ++j) r.u[j] = __builtin_amdgcn_raw_buffer_load_b16(ru, 2 * (t + 256 * j), 0, 0);
-    }
+        for (int j = 0; j < J; ++j) load_halves(rx, 2 * (XS::V * t + 1024 * j), r.x[j]);
 #pragma unroll
-    for (int j = 0; j < J; ++j) r.g[j] = __builtin_amdgcn_raw_buffer_load_b16(rg, 2 * (t + 256 * j), 0, 0);
+        for (int j = 0; j < J; ++j) load_halves(ru, 2 * (XS::V * t + 1024 * j), r.u[j]);
+#pragma unroll
+        for (int j = 0; j < J; ++j) load_halves(rg, 2 * (XS::V * t + 1024 * j), r.g[j]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int i = t + T * j;
+            if constexpr (kKind == TER_HIP_X_F32_RMS)
+                r.x[j][0] = __builtin_amdgcn_raw_buffer_load_b32(rx, 4 * i, 0, 0);
+            else
+                r.x[j][0] = __builtin_amdgcn_raw_buffer_load_b16(rx, 2 * i, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < J; ++j) r.g[j][0] = __builtin_amdgcn_raw_buffer_load_b16(rg, 2 * (t + T * j), 0, 0);
+    }
 }
 
-template <int kKind>
-__device__ __forceinline__ float stage_x_strided(const GemvDesc& d, const XStrided<kKind>& r, int8_t* lds_x,
+// Strided prologue of the RMS kinds in strip mode (the decode step's plans).
+// Every thread reads straight from memory (range-checked buffer loads: zeros
+// past K) the values of its own partial sums of squares in the reference's
+// order: the 256 threads' partials for X_F32_RMS / X_F16_RMS (thread t: the
+// values t + 256 j), the 1024 virtual threads' for X_RELU2_RMS (thread t of
+// T: virtual threads V t .. V t + V - 1, V = 1024 / T, values v + 1024 j),
+// each a fused multiply-add chain over increasing j.  So the sum needs no
+// staging round; the values also go to LDS (xs32, gs16) for the
+// quantization.  Then, with two workgroup barriers where stage_x_vec has
+// four: the partials meet in `red` (barrier), every wave forms
+// tree_sum256_all's operands (the 1024 virtual partials of a thread t' of 256
+// paired as (p(t') + p(t' + 512)) + (p(t' + 256) + p(t' + 768)) first) and
+// the absmax of its threads' normalized values; the wave maxima meet
+// (barrier); each wave quantizes only its own units [u0, u1), the ones its
+// GEMV loop reads (rows r of the wave take units u0 + r, u0 + r + 4, ...), so
+// a wave-level fence orders them before the loop.  Results are stage_x_vec's
+// bit for bit.  Needs Ku <= max_strided_ku and the fp32 staging (stage32);
+// gs16: fp16 gamma [Ku*256], red: 1024 + 16 floats.
+template <int kKind, int kW>
+__device__ __forceinline__ float stage_x_strided(const GemvDesc& d, const XStrided<kKind, kW>& r, int8_t* lds_x,
                                                  int* usum, float* red, float* xs32, uint16_t* gs16, int u0, int u1,
                                                  bool owner) {
 #pragma clang fp contract(off)
-    constexpr int J = XStrided<kKind>::J;
-    constexpr int NP = kKind == TER_HIP_X_RELU2_RMS ? 4 : 1;
+    using XS = XStrided<kKind, kW>;
+    constexpr int J = XS::J, T = XS::T, V = XS::V;
+    static_assert(XS::R2 ? (T == 256 || T == 512) : T == 256, "thread count");
     const int K = d.K, Ku = d.Ku;
     const int t = threadIdx.x, lane = t & 63;
-    float x[J];
-    float P[NP];
+    float x[J][V], gm[J][V];
+    float P[V];
 #pragma unroll
-    for (int k = 0; k < NP; ++k) P[k] = 0.f;
+    for (int e = 0; e < V; ++e) P[e] = 0.f;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-        if constexpr (kKind == TER_HIP_X_F32_RMS)
-            x[j] = __builtin_bit_cast(float, r.x[j]);
-        else if constexpr (kKind == TER_HIP_X_F16_RMS)
-            x[j] = half_bits_to_float((uint16_t)r.x[j]);
-        else
-            x[j] = relu2_mul(half_bits_to_float((uint16_t)r.x[j]), half_bits_to_float((uint16_t)r.u[j]));
-        P[j % NP] = __builtin_fmaf(x[j], x[j], P[j % NP]);  // past K: fma(0, 0, p) = p
-        if (j < Ku) {
-            xs32[t + 256 * j] = x[j];
-            gs16[t + 256 * j] = (uint16_t)r.g[j];
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+            const uint16_t gh = (uint16_t)(r.g[j][e >> 1] >> (16 * (e & 1)));
+            gm[j][e] = half_bits_to_float(XS::R2 ? gh : (uint16_t)r.g[j][0]);
+            if constexpr (kKind == TER_HIP_X_F32_RMS) {
+                x[j][e] = __builtin_bit_cast(float, r.x[j][0]);
+            } else if constexpr (kKind == TER_HIP_X_F16_RMS) {
+                x[j][e] = half_bits_to_float((uint16_t)r.x[j][0]);
+            } else {
+                const uint16_t xh = (uint16_t)(r.x[j][e >> 1] >> (16 * (e & 1)));
+                const uint16_t uh = (uint16_t)(r.u[j][e >> 1] >> (16 * (e & 1)));
+                x[j][e] = relu2_mul(half_bits_to_float(xh), half_bits_to_float(uh));
+            }
+            P[e] = __builtin_fmaf(x[j][e], x[j][e], P[e]);  // past K: fma(0, 0, p) = p
+            const int i = XS::R2 ? V * t + e + 1024 * j : t + T * j;
+            if (i < Ku * kUnitK) {  // the staged range
+                xs32[i] = x[j][e];
+                gs16[i] = XS::R2 ? gh : (uint16_t)r.g[j][0];
+            }
         }
     }
-    red[t] = NP == 4 ? (P[0] + P[NP == 4 ? 2 : 0]) + (P[NP == 4 ? 1 : 0] + P[NP == 4 ? 3 : 0]) : P[0];
+#pragma unroll
+    for (int e = 0; e < V; ++e) red[XS::R2 ? V * t + e : t] = P[e];
     __syncthreads();
-    const float ss = tree_down64((red[lane] + red[lane + 128]) + (red[lane + 64] + red[lane + 192]));
+    auto q = [&](int i) {
+        if constexpr (XS::R2)
+            return (red[i] + red[i + 512]) + (red[i + 256] + red[i + 768]);
+        else
+            return red[i];
+    };
+    const float ss = tree_down64((q(lane) + q(lane + 128)) + (q(lane + 64) + q(lane + 192)));
     const float rms_inv = 1.0f / __builtin_sqrtf(ss / (float)K + d.eps);
     float mx = 0.f;  // zeros past K
 #pragma unroll
-    for (int j = 0; j < J; ++j) mx = fmaxf(mx, fabsf((x[j] * rms_inv) * half_bits_to_float((uint16_t)r.g[j])));
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int e = 0; e < V; ++e) mx = fmaxf(mx, fabsf((x[j][e] * rms_inv) * gm[j][e]));
     mx = wave_max(mx);
-    float* wmax = red + kGemvThreads;  // apart from the partials, which other waves may still read
+    float* wmax = red + (XS::R2 ? 1024 : T);  // apart from the partials, which other waves may still read
     if (lane == 0) wmax[t >> 6] = mx;
     __syncthreads();
     mx = wmax[0];
 #pragma unroll
-    for (int i = 1; i < kGemvWaves; ++i) mx = fmaxf(mx, wmax[i]);
+    for (int i = 1; i < kW; ++i) mx = fmaxf(mx, wmax[i]);
     const float amax = mx + 1e-9f;
     const float scale = 127.0f / amax;
     const float act = 1.0f / scale;
@@ -1292,8 +1368,8 @@ void gemv_t16_kernel(GemvDesc single,
 // strip's partial column sums in LDS, and after a barrier wave j % 4 adds the
 // four partials of strip j (integer sums, so the result is the stream-K
 // kernel's) and writes the outputs.  No fix-up slots, no global atomics.
-template <bool kList, int kKind, bool kStrided = false>
-__global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc single, const GemvDesc* __restrict__ list,
+template <bool kList, int kKind, bool kStrided = false, int kW = kGemvWaves>
+__global__ __launch_bounds__(64 * kW) void gemv_strip_kernel(GemvDesc single, const GemvDesc* __restrict__ list,
                                                                   const GemvDesc* __restrict__ wg_desc,
                                                                   long long total, int n_wg, int part_off) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
@@ -1317,8 +1393,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc singl
         const long long seg_end = min(s_end, d.strip0 + (long long)d.n_strips);
         const int sa = (int)(sg - d.strip0);  // first strip of the segment within the GEMV
         const int ns = (int)(seg_end - sg);
-        const int u0 = d.Ku * wave / kGemvWaves;
-        const int nw = d.Ku * (wave + 1) / kGemvWaves - u0;  // units per strip of this wave
+        static_assert(kW == kGemvWaves || kStrided, "other wave counts run the strided prologue only");
+        const int u0 = d.Ku * wave / kW;
+        const int nw = d.Ku * (wave + 1) / kW - u0;  // units per strip of this wave
         const int n = nw * ns;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(d.w + (long long)sa * d.Ku * kTileBytes), 0, ns * d.Ku * kTileBytes, 0x00020000);
@@ -1340,11 +1417,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc singl
         };
         XPre xpre;
         XRaw xraw;
-        XStrided<kStrided ? kKind : TER_HIP_X_F32_RMS> xst;
+        XStrided<kStrided ? kKind : TER_HIP_X_F32_RMS, kStrided ? kW : kGemvWaves> xst;
         if constexpr (kKind < 0)
             x_prefetch(d, xpre);
         else if constexpr (kStrided)
-            x_prefetch_strided<kKind>(d, xst);
+            x_prefetch_strided<kKind, kW>(d, xst);
         else
             x_prefetch_vec<kKind>(d, xraw);
         u32x4 wa[NB], wb[NB];
@@ -1360,7 +1437,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc singl
             __syncthreads();
         } else if constexpr (kStrided) {
             uint16_t* gs16 = reinterpret_cast<uint16_t*>(lds_raw + gemv_lds_slots_offset(d.K, true));
-            act = stage_x_strided<kKind>(d, xst, lds_x, usum, red, xs32, gs16, u0, u0 + nw, sg == d.strip0);
+            float* red_s = reinterpret_cast<float*>(lds_raw + gemv_strip_red_offset(d.K));
+            act = stage_x_strided<kKind, kW>(d, xst, lds_x, usum, red_s, xs32, gs16, u0, u0 + nw, sg == d.strip0);
         } else {
             act = stage_x_vec<kKind>(d, xraw, lds_x, usum, red, xs32, sg == d.strip0);
             __syncthreads();
@@ -1370,7 +1448,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc singl
         const int pcol = (lane >> 4) * 4 + q;  // column within the strip of lanes q < 4
         if (nw == 0) {
             for (int j = 0; j < ns; ++j)
-                if (q < 4) part[(j * kGemvWaves + wave) * 16 + pcol] = 0;
+                if (q < 4) part[(j * kW + wave) * 16 + pcol] = 0;
         } else {
             int a1[4] = {0, 0, 0, 0}, a4[4] = {0, 0, 0, 0};
             int corr = 0, j = 0, k = 0;
@@ -1384,7 +1462,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc singl
                         dot_tile(w[i], xv, a1, a4);
                         if (++k == nw) {
                             const int v = reduce_strip(a1, a4, corr);
-                            if (q < 4) part[(j * kGemvWaves + wave) * 16 + pcol] = v;
+                            if (q < 4) part[(j * kW + wave) * 16 + pcol] = v;
                             corr = 0;
                             k = 0;
                             ++j;
@@ -1405,11 +1483,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_strip_kernel(GemvDesc singl
             }
         }
         __syncthreads();
-        for (int j = wave; j < ns; j += kGemvWaves) {
+        for (int j = wave; j < ns; j += kW) {
             const int col = (sa + j) * kStripCols + lane;
             if (lane < 16 && col < d.N) {
-                const int* pj = part + j * kGemvWaves * 16 + lane;
-                emit(d, col, ((pj[0] + pj[16]) + pj[32]) + pj[48], s);
+                const int* pj = part + j * kW * 16 + lane;
+                int v = pj[0];
+#pragma unroll
+                for (int w = 1; w < kW; ++w) v += pj[16 * w];
+                emit(d, col, v, s);
             }
         }
         sg = seg_end;
@@ -1488,8 +1569,9 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_
                                GemvDesc{}, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
             return hipGetLastError();
         case TER_HIP_X_RELU2_RMS:
-            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_RELU2_RMS, true>), grid, block, lds_bytes, st,
-                               GemvDesc{}, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_RELU2_RMS, true, strided_waves<TER_HIP_X_RELU2_RMS>()>),
+                               grid, dim3(64 * strided_waves<TER_HIP_X_RELU2_RMS>()), lds_bytes, st, GemvDesc{},
+                               list_dev, wg_desc_dev, total_strips, n_wg, part_off);
             return hipGetLastError();
         default:
             return hipErrorInvalidValue;
@@ -1521,6 +1603,10 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_
                            list_dev, wg_desc_dev, total_strips, n_wg, part_off);
     }
     return hipGetLastError();
+}
+
+int gemv_strided_waves(int vec_kind) {
+    return vec_kind == TER_HIP_X_RELU2_RMS ? strided_waves<TER_HIP_X_RELU2_RMS>() : kGemvWaves;
 }
 
 bool gemv_strided_ok(int vec_kind, int32_t K, bool stage32) {
