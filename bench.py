@@ -15,9 +15,10 @@ launches) and as 4 launches per layer grouped like a decode step
 (unless --no-extras), the other benched workloads measured in the same run:
 C3 (the BitNet-2B sweep, fp32 activations quantized in the kernel prologue),
 C4 (the batched GEMM at M = 8, 32, 128), C5 (the end-to-end decode, its
-lm_head tail and attention), the per-shape table and the host mm_row route.
+lm_head tail and attention), the Llama-3.2-1B decode of the reference's
+packed forward bench, the per-shape table and the host mm_row route.
 Each also runs alone: --config bitnet | batched --m M | decode | lm_head |
-attention | shapes | mm_row.
+attention | llama_decode | shapes | mm_row.
 
 value = MACs of the sweep / (time per step); roofline.achieved = algorithmic
 bytes per launch (packed W K*N/4 + X + Y 4N, summed over the sweep) / mean
@@ -715,6 +716,81 @@ def run_decode(args):
     }
 
 
+def run_llama_decode(args):
+    """The Llama-3.2-1B decode of the reference's packed forward bench
+    (cuda/ter_cuda_forward_packed.cu:680-760): random-init weights (16 layers,
+    H 2048, F 8192, 32/8 heads of 64, NORM RoPE 5e5, SiLU FFN, the ternary
+    lm_head over V 128256), greedy tokens in runs of 32 starting at position
+    4 with token 1 (its n_gen = 32 after 4 warm-up tokens).  One step = one
+    token: embedding, 16 layers of five launches, the lm_head GEMV and the
+    argmax, replayed from one HIP graph; each run of 32 first resets the
+    position and token on the device (counted in the time).  Also timed: the
+    same model with the lm_head tied to the fp16 token_embd (the real-weight
+    path, :547-554)."""
+    import torch
+    from ter_amd import llama as LM
+    run_len, start = 32, 4
+    steps = max(run_len, (args.steps + run_len - 1) // run_len * run_len)
+    warm = max(run_len, (args.warmup + run_len - 1) // run_len * run_len)
+    c = LM.Shape()
+    out = {}
+    for tied in (False, True):
+        t0 = time.perf_counter()
+        model = LM.random_model(c, seed=9, tied=tied)
+        dec = LM.Decoder(model, start + run_len + 64)
+        graph = dec.capture()
+        log(f"[bench] llama decode ({'tied' if tied else 'ternary'} lm_head): built in {time.perf_counter() - t0:.1f} s")
+
+        def run(n):
+            for i in range(n):
+                if i % run_len == 0:
+                    dec.pos.fill_(start)
+                    dec.token.fill_(1)
+                graph.replay()
+        run(warm)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_start = time.perf_counter()
+        e0.record()
+        run(steps)
+        e1.record()
+        torch.cuda.synchronize()
+        ms_tok = (time.perf_counter() - t_start) * 1e3 / steps
+        ev_tok = e0.elapsed_time(e1) / steps
+        shapes = LM.proj_shapes(c)
+        w_bytes = sum(K * N // 4 for K, N in shapes.values()) * c.Nl
+        kv_bytes = 2 * (start + run_len // 2) * c.Nkv * c.Hd * 2 * c.Nl
+        lm_bytes = c.V * c.H * 2 if tied else c.V * c.H // 4 + c.V * 2
+        tok_bytes = w_bytes + kv_bytes + lm_bytes
+        out["tied" if tied else "ternary"] = dict(
+            tokens_per_s_wall=round(1e3 / ms_tok, 1), ms_per_token_wall=round(ms_tok, 5),
+            us_per_token_events=round(ev_tok * 1e3, 2), launches_per_token=dec.launches_per_token(),
+            bytes_per_token=tok_bytes, hbm_gbs=round(tok_bytes / (ev_tok * 1e-3) / 1e9, 1),
+            hbm_frac=round(tok_bytes / (ev_tok * 1e-3) / 1e9 / HBM_PEAK_GBS, 4))
+        log(f"[bench] llama decode ({'tied' if tied else 'ternary'} lm_head): {ev_tok * 1e3:.1f} us/token (events), "
+            f"{1e3 / ms_tok:.0f} tokens/s (wall), {tok_bytes / (ev_tok * 1e-3) / 1e9:.0f} GB/s over "
+            f"{tok_bytes / 1e6:.0f} MB/token")
+        dec.close()
+        del dec, model, graph
+        torch.cuda.empty_cache()
+    r = out["ternary"]
+    return {
+        "metric": "end-to-end greedy decode tokens/s (Llama-3.2-1B shape, ternary lm_head, positions 4-35)",
+        "value": r["tokens_per_s_wall"], "unit": "tokens/s", "n_gpus": 1, "steps": steps, "warmup": warm,
+        "ms_per_step": r["ms_per_token_wall"], "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "random-init Llama-3.2-1B-shaped decode (the reference's packed forward bench), "
+                               "runs of 32 tokens from position 4, one HIP graph per token",
+                   "launches_per_token": r["launches_per_token"], "us_per_token": r["us_per_token_events"],
+                   "bytes_per_token": r["bytes_per_token"], "tied_lm_head": out["tied"],
+                   "reference_published": "425 tokens/s, RTX 3090 (README.md:11)"},
+        "roofline": {"bound": "hbm", "achieved": r["hbm_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": r["hbm_frac"], "traffic": None, "kernel": "whole step",
+                     "bytes_per_launch": r["bytes_per_token"], "mean_launch_us": r["us_per_token_events"]},
+        "cpu_baseline": None,
+    }
+
+
 def run_mm_row(args):
     """The reference host forward's own route through the fabric: mm_row
     (src/tx/forward.cpp:299-352) called synchronously 7 times per layer
@@ -991,7 +1067,7 @@ def run_extras(args):
     headline and reported beside it (never as `value`): C3 (the BitNet-2B
     sweep, fp32 X quantized in the kernel prologue, with the reference
     mm_row on layer 0 checked bit for bit), C4 at M = 8, 32 and 128, the C5
-    decode, its lm_head tail and attention, the per-shape table (single
+    decode, its lm_head tail and attention, the Llama-3.2-1B decode, the per-shape table (single
     launch and work list), and the host mm_row route.  Each runs with the
     same --steps / --warmup as the headline and frees its device memory
     before the next; one that fails is recorded with its error and the
@@ -1046,6 +1122,15 @@ def run_extras(args):
                     bytes_per_token=c["bytes_per_token"], hbm_frac=r["roofline"]["frac"])
     do("c5_decode", lambda: run_decode(sub(bin=None)), keep_dec)
 
+    def keep_llama(r):
+        c = r["config"]
+        return dict(workload=c["workload"], tokens_per_s_wall=r["value"], ms_per_token_wall=r["ms_per_step"],
+                    us_per_token_events=c["us_per_token"], launches_per_token=c["launches_per_token"],
+                    bytes_per_token=c["bytes_per_token"], hbm_frac=r["roofline"]["frac"],
+                    tied_lm_head=c["tied_lm_head"], reference_published=c["reference_published"])
+    do("llama_decode", lambda: run_llama_decode(sub(steps=min(args.steps, 256), warmup=min(args.warmup, 64))),
+       keep_llama)
+
     def keep_tail(r):
         rf = r["roofline"]
         return dict(workload=r["config"]["workload"], launch_us_events=rf["mean_launch_us"], hbm_gbs=rf["achieved"],
@@ -1075,7 +1160,7 @@ def main():
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", choices=["llama", "bitnet", "batched", "lm_head", "attention", "decode", "copy",
-                                         "shapes", "floors", "mm_row"], default="llama")
+                                         "shapes", "floors", "mm_row", "llama_decode"], default="llama")
     ap.add_argument("--m", type=int, default=8, help="rows for --config batched")
     ap.add_argument("--copies", type=int, default=4, help="rotated weight copies (HBM-cold)")
     ap.add_argument("--no-cpu", action="store_true")
@@ -1108,6 +1193,8 @@ def main():
         out = run_decode(args)
     elif args.config == "mm_row":
         out = run_mm_row(args)
+    elif args.config == "llama_decode":
+        out = run_llama_decode(args)
     else:
         cfg = LLAMA if args.config == "llama" else BITNET
         out = run_m1(args, cfg, fp32_x=(args.config == "bitnet"))

@@ -72,6 +72,18 @@ extern "C" {
  * exact.  Single GEMVs only (ter_hip_gemv, ter_hip_gemv_out, ter_hip_mm_row);
  * work lists and batched GEMMs refuse it (TER_HIP_ERR_PAYLOAD). */
 #define TER_HIP_X_I16 5
+/* fp16 X[K]: absmax -> int8 inside the kernel prologue, the Llama forward's
+ * quant_int8_k on its fp16 attention output before Wo
+ * (cuda/ter_cuda_forward_packed.cu:40-62, launched at :536). */
+#define TER_HIP_X_F16 6
+/* silu(gate) * up, then absmax -> int8: the Llama forward's fused
+ * silu_mul_quant_k in front of the FFN down projection
+ * (cuda/ter_cuda_forward_packed.cu:312-344, launched <<<1,1024>>> at :545).
+ * `data` is the fp16 gate [K], `up` the fp16 up projection [K].  The exp is
+ * this build's (faithful, the oracle's orc_expf), not CUDA's expf.
+ * TER_HIP_X_F16 and TER_HIP_X_SILU_MUL are single GEMVs and work lists
+ * only; batched GEMMs refuse them (TER_HIP_ERR_PAYLOAD). */
+#define TER_HIP_X_SILU_MUL 7
 
 /*
  * Packed ternary weight (replaces WPK, cuda/ter_cuda_forward_packed.cu:400).
@@ -103,7 +115,8 @@ typedef struct ter_hip_wpk {
 /* Activation operand of one GEMV / GEMM. */
 typedef struct ter_hip_act {
     const void*  data;       /* device: int8 (X_I8), int16 (X_I16), fp32 (X_F32, X_F32_RMS)
-                                or fp16 (X_F16_RMS; the gate for X_RELU2_RMS) [M][K]    */
+                                or fp16 (X_F16, X_F16_RMS; the gate for X_RELU2_RMS and
+                                X_SILU_MUL) [M][K]                                       */
     int32_t      kind;       /* TER_HIP_X_*                                            */
     float        scale;      /* X_I8, X_I16: host activation scale, used when scale_dev NULL */
     const float* scale_dev;  /* X_I8, X_I16: device activation scale(s) ([M]), or NULL */
@@ -111,7 +124,7 @@ typedef struct ter_hip_act {
     float*       scale_out;  /* X_F32: optional device act scale(s) 1/scale ([M])     */
     const uint16_t* gamma;   /* RMS kinds: device fp16 RMSNorm weights [K]             */
     float        eps;        /* RMS kinds: RMSNorm epsilon                             */
-    const uint16_t* up;      /* X_RELU2_RMS: device fp16 up projection [M][K]         */
+    const uint16_t* up;      /* X_RELU2_RMS, X_SILU_MUL: device fp16 up projection [M][K] */
 } ter_hip_act_t;
 
 /* Outputs of one GEMV / GEMM; any subset, at least one non-NULL.  With
@@ -126,12 +139,18 @@ typedef struct ter_hip_act {
  *         projection followed by add_k_f32 into the residual stream
  *         (cuda/ter_cuda_forward_bitnet.cu:51-54, :876, :887).  A plain
  *         read-modify-write: no other work of the same launch may target the
- *         same elements. */
+ *         same elements.
+ *   resid16 fp16 bits [M][N], updated in place: resid16 = half(float(resid16)
+ *         + float(half(y))), the projection followed by add_k into the Llama
+ *         forward's fp16 residual stream (cuda/ter_cuda_forward_packed.cu:115-118,
+ *         :538, :548); the same rule as resid.  GEMVs and GEMV work lists
+ *         only: the batched GEMMs refuse it (TER_HIP_ERR_PAYLOAD). */
 typedef struct ter_hip_out {
     float*    y;
     int32_t*  acc;
     uint16_t* y16;
     float*    resid;
+    uint16_t* resid16;
 } ter_hip_out_t;
 
 /* ---------------------------------------------------------------------- */
@@ -241,6 +260,7 @@ typedef struct ter_hip_gemv_item {
     int32_t*             acc;  /* int32 [N] or NULL */
     uint16_t*            y16;  /* fp16 [N] or NULL (ter_hip_out_t)            */
     float*               resid;/* fp32 [N] residual, += half(y), or NULL      */
+    uint16_t*            resid16; /* fp16 [N] residual, += half(y), or NULL   */
 } ter_hip_gemv_item_t;
 
 typedef struct ter_hip_plan ter_hip_plan_t;
@@ -310,6 +330,7 @@ typedef struct ter_hip_gemm_item {
     int32_t*             acc;          /* int32 [M][N] or NULL               */
     uint16_t*            y16;          /* fp16 [M][N] or NULL                */
     float*               resid;        /* fp32 [M][N] residual or NULL       */
+    uint16_t*            resid16;      /* NULL: fp16 residuals are GEMV-only */
 } ter_hip_gemm_item_t;
 
 int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* items, int32_t n,
@@ -369,6 +390,12 @@ int ter_hip_lm_head_f16(const uint16_t* x_norm, const uint16_t* token_embd, uint
 #define TER_HIP_ARGMAX_STATE_BYTES 16512
 int ter_hip_argmax_f16(const uint16_t* logits, int32_t N, int32_t* out_idx, uint64_t* state,
                        void* stream);
+/* ter_hip_argmax_f16 followed by inc_pos_k: the tail of the Llama forward's
+ * bench mode (cuda/ter_cuda_forward_packed.cu:555-559, after the packed
+ * lm_head GEMV of :541-545).  pos_advance (device int32, required) is
+ * incremented once the token is written. */
+int ter_hip_argmax_f16_step(const uint16_t* logits, int32_t N, int32_t* out_idx, uint64_t* state,
+                            int32_t* pos_advance, void* stream);
 /* The whole tail in ONE launch (rmsnorm_f32_in_k + mm_fp16_lm_head_k +
  * argmax, :890-911): hidden fp32 [H] -> x_norm -> logits -> *token_out.
  * x_norm_out (fp16 [H]) and logits_out (fp16 [V]) are optional copies;
@@ -383,6 +410,18 @@ int ter_hip_lm_head_argmax(const float* hidden, const uint16_t* gamma, float eps
  * token_embd[*token_dev] widened (a token outside [0, V) writes nothing). */
 int ter_hip_embed_f16(const uint16_t* token_embd, int32_t V, int32_t H, const int32_t* token_dev,
                       float* hidden, void* stream);
+/* The Llama forward's tail and first kernel, on its fp16 residual stream
+ * (cuda/ter_cuda_forward_packed.cu:505-560): ter_hip_lm_head_argmax_h16 is
+ * ter_hip_lm_head_argmax with hidden16 fp16 [H] (rmsnorm_k, :27-37, then
+ * mm_fp16_lm_head_k and the argmax, :550-557; hidden16 4-byte aligned), and
+ * ter_hip_embed_h16 writes hidden16 fp16 [H] = token_embd[*token_dev]
+ * (token_embed_lookup_k, :99-106; a token outside [0, V) writes nothing). */
+int ter_hip_lm_head_argmax_h16(const uint16_t* hidden16, const uint16_t* gamma, float eps,
+                               const uint16_t* token_embd, int32_t H, int32_t V, uint16_t* x_norm_out,
+                               uint16_t* logits_out, int32_t* token_out, uint64_t* state,
+                               int32_t* pos_advance, void* stream);
+int ter_hip_embed_h16(const uint16_t* token_embd, int32_t V, int32_t H, const int32_t* token_dev,
+                      uint16_t* hidden16, void* stream);
 
 /* ---------------------------------------------------------------------- */
 /* Decode attention: RoPE + KV-cache write + attention, one launch per      */

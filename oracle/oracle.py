@@ -68,6 +68,12 @@ def lib():
         L.orc_relu2_rmsnorm_quant.restype = None
         L.orc_residual_add_f16.argtypes = [_P, _P, C.c_int]
         L.orc_residual_add_f16.restype = None
+        L.orc_residual_add_h16.argtypes = [_P, _P, C.c_int]
+        L.orc_residual_add_h16.restype = None
+        L.orc_silu_mul.argtypes = [C.c_uint16, C.c_uint16]
+        L.orc_silu_mul.restype = C.c_float
+        L.orc_silu_mul_quant.argtypes = [_P, _P, C.c_int, _P, _P, _P]
+        L.orc_silu_mul_quant.restype = None
         L.orc_rmsnorm_f16.argtypes = [_P, _P, C.c_int, C.c_float, _P, _P]
         L.orc_rmsnorm_f16.restype = None
         L.orc_lm_head_f16.argtypes = [_P, _P, C.c_int, C.c_int, _P, _P]
@@ -320,6 +326,28 @@ def residual_add_f16(hidden: np.ndarray, y: np.ndarray) -> np.ndarray:
     yy = np.ascontiguousarray(y, dtype=np.float32)
     lib().orc_residual_add_f16(_ptr(h), _ptr(yy), h.size)
     return h
+
+
+def residual_add_h16(hidden: np.ndarray, y: np.ndarray) -> np.ndarray:
+    """add_k (cuda/ter_cuda_forward_packed.cu:113-116) after an fp16 GEMV
+    output: fp16 hidden + half(y), rounded to fp16."""
+    h = np.array(hidden, dtype=np.float16, copy=True)
+    yy = np.ascontiguousarray(y, dtype=np.float32)
+    lib().orc_residual_add_h16(_ptr(h), _ptr(yy), h.size)
+    return h
+
+
+def silu_mul_quant(gate: np.ndarray, up: np.ndarray):
+    """silu_mul_quant_k (cuda/ter_cuda_forward_packed.cu:312-344): fp16 gate,
+    up [F] -> (int8 [F], act_scale, fp32 silu(gate) * up [F])."""
+    g = np.ascontiguousarray(gate, dtype=np.float16)
+    u = np.ascontiguousarray(up, dtype=np.float16)
+    F = g.size
+    q = np.empty(F, dtype=np.int8)
+    s = np.zeros(1, dtype=np.float32)
+    v = np.empty(F, dtype=np.float32)
+    lib().orc_silu_mul_quant(_ptr(g), _ptr(u), F, _ptr(q), _ptr(s), _ptr(v))
+    return q, s[0], v
 
 
 def rmsnorm_f16(x: np.ndarray, gamma: np.ndarray, eps: float = 1e-5):

@@ -40,6 +40,14 @@
  *                                           1024-thread order reduces to it,
  *                                           a summation-order case.
  *   orc_residual_add_f16                 -- orc_float_to_half / orc_half_to_float.
+ *   orc_residual_add_h16                 -- numpy's binary16 addition (one correctly
+ *                                           rounded add) of hidden and half(y).
+ *   orc_silu_mul / orc_silu_mul_quant    -- closed forms (g = 0 or u = 0 gives 0,
+ *                                           large g gives g * u exactly, very
+ *                                           negative g gives 0), float64
+ *                                           g * sigmoid(g) * u within the rounding
+ *                                           bound, odd symmetry of silu(g) - g/2,
+ *                                           the quantizer against orc_quant_int8.
  *   orc_rmsnorm_f16                      -- rms_inv equal to orc_rmsnorm_quant's (one
  *                                           reference order), constant-input closed
  *                                           form, fp16 rounding of the product.
@@ -488,6 +496,47 @@ void orc_relu2_rmsnorm_quant(const uint16_t* gate, const uint16_t* up, const uin
 /* ------------------------------------------------------------------------ */
 void orc_residual_add_f16(float* hidden, const float* y, int n) {
     for (int i = 0; i < n; ++i) hidden[i] = hidden[i] + orc_half_to_float(orc_float_to_half(y[i]));
+}
+
+/* ------------------------------------------------------------------------ */
+/* Residual add into an fp16 hidden state: add_k,                            */
+/* cuda/ter_cuda_forward_packed.cu:113-116, after the GEMV wrote an fp16     */
+/* output: hidden[i] = half(float(hidden[i]) + float(half(y[i]))).  binary32 */
+/* has more than 2*11+1 significand bits, so the two roundings equal one     */
+/* correctly rounded binary16 addition.                                      */
+/* ------------------------------------------------------------------------ */
+void orc_residual_add_h16(uint16_t* hidden, const float* y, int n) {
+    for (int i = 0; i < n; ++i) {
+        const float a = orc_half_to_float(hidden[i]);
+        const float b = orc_half_to_float(orc_float_to_half(y[i]));
+        hidden[i] = orc_float_to_half(a + b);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* SiLU(gate) * up + int8 quantizer: silu_mul_quant_k,                       */
+/* cuda/ter_cuda_forward_packed.cu:312-344, launched <<<1,1024>>> (:535).    */
+/* gate and up fp16; v_i = (g_i / (1 + expf(-g_i))) * u_i kept in binary32   */
+/* (the kernel's shared-memory copy is float, never rounded to fp16); then   */
+/* the quant_int8_k steps on v (amax + 1e-9f, 127 / amax, round to nearest   */
+/* even, clamp).  expf is orc_expf.  v_out (may be NULL) receives v.         */
+/* ------------------------------------------------------------------------ */
+float orc_expf(float x); /* defined with the attention softmax below */
+
+float orc_silu_mul(uint16_t g16, uint16_t u16) {
+    const float g = orc_half_to_float(g16), u = orc_half_to_float(u16);
+    const float d = 1.0f + orc_expf(-g);
+    const float sg = g / d;
+    return sg * u;
+}
+
+void orc_silu_mul_quant(const uint16_t* gate, const uint16_t* up, int F, int8_t* q, float* act_scale, float* v_out) {
+    float* v = (float*)malloc(sizeof(float) * (size_t)(F > 0 ? F : 1));
+    if (!v) return;
+    for (int i = 0; i < F; ++i) v[i] = orc_silu_mul(gate[i], up[i]);
+    orc_quant_int8(v, F, q, act_scale);
+    if (v_out) memcpy(v_out, v, sizeof(float) * (size_t)F);
+    free(v);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -14,6 +14,7 @@ from .fabric import (  # noqa: F401
     Plan,
     argmax_f16,
     embed_f16,
+    embed_h16,
     gemv,
     lm_head_argmax,
     lm_head_f16,
@@ -41,6 +42,7 @@ __all__ = [
     "Plan",
     "argmax_f16",
     "embed_f16",
+    "embed_h16",
     "gemv",
     "lm_head_argmax",
     "lm_head_f16",

@@ -38,6 +38,8 @@ X_F32_RMS = 2
 X_F16_RMS = 3
 X_RELU2_RMS = 4
 X_I16 = 5
+X_F16 = 6
+X_SILU_MUL = 7
 SLOT_MATMUL = b"tk_matmul_t16"
 LAYOUT_T16 = 16
 ARGMAX_STATE_BYTES = 16512
@@ -85,6 +87,7 @@ class Out(C.Structure):
         ("acc", C.c_void_p),
         ("y16", C.c_void_p),
         ("resid", C.c_void_p),
+        ("resid16", C.c_void_p),
     ]
 
 
@@ -96,6 +99,7 @@ class GemvItem(C.Structure):
         ("acc", C.c_void_p),
         ("y16", C.c_void_p),
         ("resid", C.c_void_p),
+        ("resid16", C.c_void_p),
     ]
 
 
@@ -109,6 +113,7 @@ class GemmItem(C.Structure):
         ("acc", C.c_void_p),
         ("y16", C.c_void_p),
         ("resid", C.c_void_p),
+        ("resid16", C.c_void_p),
     ]
 
 
@@ -177,8 +182,11 @@ SIGNATURES = [
     ("ter_hip_rmsnorm_f16", C.c_int, [_P, _P, C.c_float, C.c_int32, C.c_int32, _P, _P]),
     ("ter_hip_lm_head_f16", C.c_int, [_P, _P, _P, C.c_int32, C.c_int32, _P]),
     ("ter_hip_argmax_f16", C.c_int, [_P, C.c_int32, _P, _P, _P]),
+    ("ter_hip_argmax_f16_step", C.c_int, [_P, C.c_int32, _P, _P, _P, _P]),
     ("ter_hip_lm_head_argmax", C.c_int, [_P, _P, C.c_float, _P, C.c_int32, C.c_int32, _P, _P, _P, _P, _P, _P]),
     ("ter_hip_embed_f16", C.c_int, [_P, C.c_int32, C.c_int32, _P, _P, _P]),
+    ("ter_hip_lm_head_argmax_h16", C.c_int, [_P, _P, C.c_float, _P, C.c_int32, C.c_int32, _P, _P, _P, _P, _P, _P]),
+    ("ter_hip_embed_h16", C.c_int, [_P, C.c_int32, C.c_int32, _P, _P, _P]),
     ("ter_hip_attn_create", C.c_int, [C.POINTER(C.c_void_p), C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_float,
                                       C.c_int32]),
     ("ter_hip_attn_decode", C.c_int, [_P, _P, _P, _P, _P, _P, _P, _P, _P]),

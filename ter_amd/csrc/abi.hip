@@ -56,19 +56,28 @@ bool is_rms(int kind) {
     return kind == TER_HIP_X_F32_RMS || kind == TER_HIP_X_F16_RMS || kind == TER_HIP_X_RELU2_RMS;
 }
 
+// Kinds whose prologue runs only inside the GEMV kernels (no batched row
+// quantizer): int16 rows, the fp16 absmax and the silu(gate) * up kinds.
+bool gemv_only_kind(int kind) {
+    return kind == TER_HIP_X_I16 || kind == TER_HIP_X_F16 || kind == TER_HIP_X_SILU_MUL;
+}
+
 int check_act(const ter_hip_act_t* x, int M) {
     if (!x || !x->data) return fail(TER_HIP_ERR_NULL, "null activation");
-    if (x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_F32 && x->kind != TER_HIP_X_I16 && !is_rms(x->kind))
+    if (x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_F32 && !gemv_only_kind(x->kind) && !is_rms(x->kind))
         return fail(TER_HIP_ERR_PAYLOAD, "unknown activation kind %d", x->kind);
-    if (x->kind == TER_HIP_X_I16 && M != 1)
-        return fail(TER_HIP_ERR_PAYLOAD, "int16 activations run as single GEMVs only (M=%d)", M);
+    if (gemv_only_kind(x->kind) && M != 1)
+        return fail(TER_HIP_ERR_PAYLOAD, "activation kind %d runs as single GEMVs and GEMV work lists only (M=%d)",
+                    x->kind, M);
     if (x->kind == TER_HIP_X_I16 && !aligned(x->data, 2)) return fail(TER_HIP_ERR_ALIGN, "int16 X misaligned");
     if ((x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS) && !aligned(x->data, 4))
         return fail(TER_HIP_ERR_ALIGN, "fp32 X misaligned");
-    if ((x->kind == TER_HIP_X_F16_RMS || x->kind == TER_HIP_X_RELU2_RMS) && !aligned(x->data, 2))
+    if ((x->kind == TER_HIP_X_F16_RMS || x->kind == TER_HIP_X_RELU2_RMS || x->kind == TER_HIP_X_F16 ||
+         x->kind == TER_HIP_X_SILU_MUL) &&
+        !aligned(x->data, 2))
         return fail(TER_HIP_ERR_ALIGN, "fp16 X misaligned");
-    if (x->kind == TER_HIP_X_RELU2_RMS) {
-        if (!x->up) return fail(TER_HIP_ERR_NULL, "relu2 activation without up");
+    if (x->kind == TER_HIP_X_RELU2_RMS || x->kind == TER_HIP_X_SILU_MUL) {
+        if (!x->up) return fail(TER_HIP_ERR_NULL, "gated activation without up");
         if (!aligned(x->up, 2)) return fail(TER_HIP_ERR_ALIGN, "fp16 up misaligned");
     }
     if (is_rms(x->kind)) {
@@ -82,8 +91,10 @@ int check_act(const ter_hip_act_t* x, int M) {
 }
 
 int check_out(const ter_hip_out_t* o) {
-    if (!o || (!o->y && !o->acc && !o->y16 && !o->resid)) return fail(TER_HIP_ERR_NULL, "no output buffer");
-    if (!aligned(o->y, 4) || !aligned(o->acc, 4) || !aligned(o->y16, 2) || !aligned(o->resid, 4))
+    if (!o || (!o->y && !o->acc && !o->y16 && !o->resid && !o->resid16))
+        return fail(TER_HIP_ERR_NULL, "no output buffer");
+    if (!aligned(o->y, 4) || !aligned(o->acc, 4) || !aligned(o->y16, 2) || !aligned(o->resid, 4) ||
+        !aligned(o->resid16, 2))
         return fail(TER_HIP_ERR_ALIGN, "output buffer misaligned");
     return TER_HIP_OK;
 }
@@ -97,11 +108,13 @@ unsigned act_bytes(int kind) {
         case TER_HIP_X_F16_RMS: return 4;
         case TER_HIP_X_RELU2_RMS: return 6;
         case TER_HIP_X_I16: return 2;
+        case TER_HIP_X_F16: return 2;
+        case TER_HIP_X_SILU_MUL: return 4;
         default: return 1;
     }
 }
 unsigned out_bytes(const ter_hip_out_t& o) {
-    return (o.y ? 4u : 0u) + (o.acc ? 4u : 0u) + (o.y16 ? 2u : 0u) + (o.resid ? 8u : 0u);
+    return (o.y ? 4u : 0u) + (o.acc ? 4u : 0u) + (o.y16 ? 2u : 0u) + (o.resid ? 8u : 0u) + (o.resid16 ? 4u : 0u);
 }
 
 typedef std::vector<std::pair<uintptr_t, uintptr_t>> Ranges;
@@ -115,7 +128,8 @@ void act_ranges(const ter_hip_act_t* x, int M, int K, Ranges* out) {
     const size_t n = (size_t)M * (size_t)K;
     const size_t el = x->kind == TER_HIP_X_I8 ? 1 : (x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS ? 4 : 2);  // I16, fp16: 2
     out->emplace_back((uintptr_t)x->data, (uintptr_t)x->data + n * el);
-    if (x->kind == TER_HIP_X_RELU2_RMS && x->up) out->emplace_back((uintptr_t)x->up, (uintptr_t)(x->up + n));
+    if ((x->kind == TER_HIP_X_RELU2_RMS || x->kind == TER_HIP_X_SILU_MUL) && x->up)
+        out->emplace_back((uintptr_t)x->up, (uintptr_t)(x->up + n));
 }
 
 // Residual targets of one launch must not overlap one another or any input
@@ -146,11 +160,12 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip
     d.acc = o.acc;
     d.y16 = o.y16;
     d.resid = o.resid;
+    d.resid16 = o.resid16;
     const bool quantized = x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_I16;
     d.xq_out = quantized ? x->q_out : nullptr;
     d.xs_out = quantized ? x->scale_out : nullptr;
     d.gamma = is_rms(x->kind) ? x->gamma : nullptr;
-    d.up = x->kind == TER_HIP_X_RELU2_RMS ? x->up : nullptr;
+    d.up = x->kind == TER_HIP_X_RELU2_RMS || x->kind == TER_HIP_X_SILU_MUL ? x->up : nullptr;
     d.eps = x->eps;
     d.fix = reinterpret_cast<unsigned long long*>(w->fix);
     d.tile0 = tile0;
@@ -197,6 +212,7 @@ int gemv_vec_kind(const ter_hip_gemv_item_t* items, int n) {
     for (int i = 0; i < n; ++i) {
         const ter_hip_act_t& x = items[i].x;
         if (x.kind != kind || items[i].w->K % 16 != 0 || !a16(x.data)) return -1;
+        if (gemv_only_kind(x.kind)) return -1;  // the general prologue
         if (is_rms(x.kind) && !gemv_stage32(items[i].w->K)) return -1;  // the vector prologue always stages
         if (x.kind == TER_HIP_X_RELU2_RMS && !a16(x.up)) return -1;
         if (is_rms(x.kind) && !a16(x.gamma)) return -1;
@@ -289,7 +305,7 @@ bool ring_rows_ok(const int8_t* x, int K) { return aligned(x, 16) && K % 16 == 0
 ter_hip_out_t out_rows(const ter_hip_out_t& o, int r0, int N) {
     const size_t off = (size_t)r0 * (size_t)N;
     return ter_hip_out_t{o.y ? o.y + off : nullptr, o.acc ? o.acc + off : nullptr, o.y16 ? o.y16 + off : nullptr,
-                         o.resid ? o.resid + off : nullptr};
+                         o.resid ? o.resid + off : nullptr, o.resid16 ? o.resid16 + off : nullptr};
 }
 
 // GEMM workgroups: up to kGemmWgPerCu per CU (more weight bytes in flight
@@ -778,7 +794,7 @@ int ter_hip_pack_payload(ter_hip_wpk_t* w, const int32_t* payload, float scale, 
 }
 
 int ter_hip_gemv(const ter_hip_wpk_t* w, const ter_hip_act_t* x, float* y, int32_t* acc, void* stream) {
-    const ter_hip_out_t o{y, acc, nullptr, nullptr};
+    const ter_hip_out_t o{y, acc, nullptr, nullptr, nullptr};
     return ter_hip_gemv_out(w, x, &o, stream);
 }
 
@@ -789,10 +805,12 @@ int ter_hip_gemv_out(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_h
     if (rc) return rc;
     rc = check_out(out);
     if (rc) return rc;
-    if (out->resid) {
-        Ranges in;
+    if (out->resid || out->resid16) {
+        Ranges in, rr;
         act_ranges(x, 1, w->K, &in);
-        rc = check_resid_overlap({{(uintptr_t)out->resid, (uintptr_t)(out->resid + w->N)}}, in);
+        if (out->resid) rr.emplace_back((uintptr_t)out->resid, (uintptr_t)(out->resid + w->N));
+        if (out->resid16) rr.emplace_back((uintptr_t)out->resid16, (uintptr_t)(out->resid16 + w->N));
+        rc = check_resid_overlap(rr, in);
         if (rc) return rc;
     }
     const GemvDesc d = make_desc(w, x, *out, 0);
@@ -843,7 +861,7 @@ int ter_hip_mm_packed_dispatch_f16(const int8_t* X, const float* scale_x_dev, co
     x.data = X;
     x.kind = TER_HIP_X_I8;
     x.scale_dev = scale_x_dev;
-    const ter_hip_out_t o{nullptr, nullptr, out, nullptr};
+    const ter_hip_out_t o{nullptr, nullptr, out, nullptr, nullptr};
     return ter_hip_gemv_out(W, &x, &o, stream);
 }
 
@@ -970,13 +988,14 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         if (rc) return rc;
         if (it.x.kind == TER_HIP_X_I16)
             return fail(TER_HIP_ERR_PAYLOAD, "item %d: int16 activations run as single GEMVs only", i);
-        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid};
+        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid, it.resid16};
         rc = check_out(&o);
         if (rc) return rc;
         for (int k = 0; k < i; ++k)
             if (items[k].w->fix == it.w->fix)
                 return fail(TER_HIP_ERR_CONFLICT, "weight of item %d repeats item %d", i, k);
         if (it.resid) resid.emplace_back((uintptr_t)it.resid, (uintptr_t)(it.resid + it.w->N));
+        if (it.resid16) resid.emplace_back((uintptr_t)it.resid16, (uintptr_t)(it.resid16 + it.w->N));
         act_ranges(&it.x, 1, it.w->K, &inputs);
         ds[(size_t)i] = make_desc(it.w, &it.x, o, tile);
         ds[(size_t)i].strip0 = strips;
@@ -1131,7 +1150,7 @@ int ter_hip_quant_int8(const float* x, int32_t M, int32_t K, int8_t* q, float* s
 }
 
 int ter_hip_gemm(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M, float* y, int32_t* acc, void* stream) {
-    const ter_hip_out_t o{y, acc, nullptr, nullptr};
+    const ter_hip_out_t o{y, acc, nullptr, nullptr, nullptr};
     return ter_hip_gemm_out(w, x, M, &o, stream);
 }
 
@@ -1144,10 +1163,11 @@ static int gemm_out_ws(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M
     if (M < 1 || M > TER_HIP_M_MAX) return fail(TER_HIP_ERR_SHAPE, "M=%d out of range [1,%d]", M, TER_HIP_M_MAX);
     rc = check_act(x, M);
     if (rc) return rc;
-    if (x->kind == TER_HIP_X_I16)  // the GEMM kernels take int8 rows; int16 rows run as single GEMVs only
-        return fail(TER_HIP_ERR_PAYLOAD, "int16 activations run as single GEMVs only (ter_hip_gemv / ter_hip_mm_row)");
+    if (gemv_only_kind(x->kind))  // the GEMM kernels take int8 rows from the batched quantizers
+        return fail(TER_HIP_ERR_PAYLOAD, "activation kind %d runs as single GEMVs and GEMV work lists only", x->kind);
     rc = check_out(out);
     if (rc) return rc;
+    if (out->resid16) return fail(TER_HIP_ERR_PAYLOAD, "fp16 residual outputs: GEMVs only");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int8_t* xq = static_cast<const int8_t*>(x->data);
     const float* xs = x->scale_dev;
@@ -1257,9 +1277,10 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
         if (!it.x || !it.x_scale_dev) return fail(TER_HIP_ERR_NULL, "item %d: null X or X scales", i);
         if (it.M < 1 || it.M > TER_HIP_M_MAX)
             return fail(TER_HIP_ERR_SHAPE, "item %d: M=%d out of range [1,%d]", i, it.M, TER_HIP_M_MAX);
-        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid};
+        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid, nullptr};
         rc = check_out(&o);
         if (rc) return rc;
+        if (it.resid16) return fail(TER_HIP_ERR_PAYLOAD, "item %d: fp16 residual outputs: GEMVs only", i);
         if (it.resid) resid.emplace_back((uintptr_t)it.resid, (uintptr_t)(it.resid + (size_t)it.M * it.w->N));
         inputs.emplace_back((uintptr_t)it.x, (uintptr_t)(it.x + (size_t)it.M * it.w->K));
         if (it.M > max_m) max_m = it.M;
@@ -1278,7 +1299,7 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     std::vector<int> piece0;  // first descriptor of each item (its pieces follow)
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemm_item_t& it = items[i];
-        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid};
+        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid, nullptr};
         piece0.push_back((int)ds.size());
         for (int r0 = 0; r0 < it.M; r0 += rows) {
             const int m = std::min(rows, it.M - r0);
@@ -1415,16 +1436,18 @@ int ter_hip_lm_head_f16(const uint16_t* x_norm, const uint16_t* token_embd, uint
     int n_wg = 0;
     rc = pick_lm_head_wg(H, V, &n_wg);
     if (rc) return rc;
-    hipError_t e = launch_lm_head(nullptr, nullptr, 0.f, x_norm, token_embd, H, V, nullptr, logits, nullptr, nullptr,
+    hipError_t e = launch_lm_head(nullptr, nullptr, nullptr, 0.f, x_norm, token_embd, H, V, nullptr, logits, nullptr, nullptr,
                                   nullptr, n_wg, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "lm_head launch");
     return TER_HIP_OK;
 }
 
-int ter_hip_argmax_f16(const uint16_t* logits, int32_t N, int32_t* out_idx, uint64_t* state, void* stream) {
+static int argmax_any(const uint16_t* logits, int32_t N, int32_t* out_idx, uint64_t* state, int32_t* pos_advance,
+                      void* stream) {
     if (!logits || !out_idx || !state) return fail(TER_HIP_ERR_NULL, "null argument");
     if (N < 1 || N > TER_HIP_N_MAX) return fail(TER_HIP_ERR_SHAPE, "N=%d out of range", N);
-    if (!aligned(logits, 2) || !aligned(out_idx, 4) || !aligned(state, 8)) return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
+    if (!aligned(logits, 2) || !aligned(out_idx, 4) || !aligned(state, 8) || !aligned(pos_advance, 4))
+        return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
@@ -1432,10 +1455,20 @@ int ter_hip_argmax_f16(const uint16_t* logits, int32_t N, int32_t* out_idx, uint
     if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
     long long g = ((long long)N + 1023) / 1024;  // about 4 elements per thread
     if (g > cus) g = cus;
-    e = launch_argmax_f16(logits, N, out_idx, reinterpret_cast<unsigned long long*>(state), (int)g,
+    e = launch_argmax_f16(logits, N, out_idx, reinterpret_cast<unsigned long long*>(state), pos_advance, (int)g,
                           static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "argmax launch");
     return TER_HIP_OK;
+}
+
+int ter_hip_argmax_f16(const uint16_t* logits, int32_t N, int32_t* out_idx, uint64_t* state, void* stream) {
+    return argmax_any(logits, N, out_idx, state, nullptr, stream);
+}
+
+int ter_hip_argmax_f16_step(const uint16_t* logits, int32_t N, int32_t* out_idx, uint64_t* state,
+                            int32_t* pos_advance, void* stream) {
+    if (!pos_advance) return fail(TER_HIP_ERR_NULL, "null argument");
+    return argmax_any(logits, N, out_idx, state, pos_advance, stream);
 }
 
 int ter_hip_embed_f16(const uint16_t* token_embd, int32_t V, int32_t H, const int32_t* token_dev, float* hidden,
@@ -1449,24 +1482,53 @@ int ter_hip_embed_f16(const uint16_t* token_embd, int32_t V, int32_t H, const in
     return TER_HIP_OK;
 }
 
-int ter_hip_lm_head_argmax(const float* hidden, const uint16_t* gamma, float eps, const uint16_t* token_embd, int32_t H,
-                           int32_t V, uint16_t* x_norm_out, uint16_t* logits_out, int32_t* token_out, uint64_t* state,
-                           int32_t* pos_advance, void* stream) {
-    if (!hidden || !gamma || !token_out || !state) return fail(TER_HIP_ERR_NULL, "null argument");
+// The fused tail over an fp32 (hidden) or fp16 (hidden16) residual stream.
+static int lm_head_argmax_any(const float* hidden, const uint16_t* hidden16, const uint16_t* gamma, float eps,
+                              const uint16_t* token_embd, int32_t H, int32_t V, uint16_t* x_norm_out,
+                              uint16_t* logits_out, int32_t* token_out, uint64_t* state, int32_t* pos_advance,
+                              void* stream) {
+    if ((!hidden && !hidden16) || !gamma || !token_out || !state) return fail(TER_HIP_ERR_NULL, "null argument");
     int rc = check_lm_head(token_embd, H, V);
     if (rc) return rc;
     if (H % 2) return fail(TER_HIP_ERR_SHAPE, "the fused RMSNorm prologue needs an even H (H=%d)", H);
-    if (!aligned(hidden, 8) || !aligned(gamma, 4) || !aligned(x_norm_out, 4) || !aligned(logits_out, 2) ||
-        !aligned(token_out, 4) || !aligned(state, 8) || !aligned(pos_advance, 4))
+    if (!aligned(hidden, 8) || !aligned(hidden16, 4) || !aligned(gamma, 4) || !aligned(x_norm_out, 4) ||
+        !aligned(logits_out, 2) || !aligned(token_out, 4) || !aligned(state, 8) || !aligned(pos_advance, 4))
         return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
     if (!(eps >= 0.f)) return fail(TER_HIP_ERR_SHAPE, "RMSNorm eps must be >= 0");
     int n_wg = 0;
     rc = pick_lm_head_wg(H, V, &n_wg);
     if (rc) return rc;
-    hipError_t e = launch_lm_head(hidden, gamma, eps, nullptr, token_embd, H, V, x_norm_out, logits_out, token_out,
-                                  reinterpret_cast<unsigned long long*>(state), pos_advance, n_wg,
+    hipError_t e = launch_lm_head(hidden, hidden16, gamma, eps, nullptr, token_embd, H, V, x_norm_out, logits_out,
+                                  token_out, reinterpret_cast<unsigned long long*>(state), pos_advance, n_wg,
                                   static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "lm_head launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_lm_head_argmax(const float* hidden, const uint16_t* gamma, float eps, const uint16_t* token_embd, int32_t H,
+                           int32_t V, uint16_t* x_norm_out, uint16_t* logits_out, int32_t* token_out, uint64_t* state,
+                           int32_t* pos_advance, void* stream) {
+    if (!hidden) return fail(TER_HIP_ERR_NULL, "null argument");
+    return lm_head_argmax_any(hidden, nullptr, gamma, eps, token_embd, H, V, x_norm_out, logits_out, token_out, state,
+                              pos_advance, stream);
+}
+
+int ter_hip_lm_head_argmax_h16(const uint16_t* hidden16, const uint16_t* gamma, float eps, const uint16_t* token_embd,
+                               int32_t H, int32_t V, uint16_t* x_norm_out, uint16_t* logits_out, int32_t* token_out,
+                               uint64_t* state, int32_t* pos_advance, void* stream) {
+    if (!hidden16) return fail(TER_HIP_ERR_NULL, "null argument");
+    return lm_head_argmax_any(nullptr, hidden16, gamma, eps, token_embd, H, V, x_norm_out, logits_out, token_out,
+                              state, pos_advance, stream);
+}
+
+int ter_hip_embed_h16(const uint16_t* token_embd, int32_t V, int32_t H, const int32_t* token_dev, uint16_t* hidden16,
+                      void* stream) {
+    if (!token_embd || !token_dev || !hidden16) return fail(TER_HIP_ERR_NULL, "null argument");
+    if (V < 1 || H < 1 || V > TER_HIP_N_MAX || H > TER_HIP_K_MAX) return fail(TER_HIP_ERR_SHAPE, "V=%d H=%d", V, H);
+    if (!aligned(token_embd, 2) || !aligned(token_dev, 4) || !aligned(hidden16, 2))
+        return fail(TER_HIP_ERR_ALIGN, "misaligned argument");
+    hipError_t e = launch_embed_h16(token_embd, V, H, token_dev, hidden16, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "embedding launch");
     return TER_HIP_OK;
 }
 

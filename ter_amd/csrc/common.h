@@ -19,6 +19,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <type_traits>
 #include <stdint.h>
 
 #include "ter_hip.h"
@@ -53,6 +54,7 @@ struct alignas(16) GemvDesc {
     const uint16_t* up;          // X_RELU2_RMS: fp16 up projection [K]
     uint16_t* y16;               // fp16 [N] = half(y) or null
     float* resid;                // fp32 [N]: resid += float(half(y)), or null
+    uint16_t* resid16;           // fp16 [N]: resid16 = half(float(resid16) + float(half(y))), or null
     unsigned long long* fix;     // N fix-up slots, zero at rest
     long long tile0;             // first tile of this GEMV in the launch's stream
     long long strip0;            // first strip of this GEMV in the launch's strip stream (strip mode)
@@ -138,12 +140,17 @@ hipError_t launch_rmsnorm_quant_rows(const void* x, const uint16_t* up, int kind
 // zero at rest) is needed when token_out is set.
 int lm_head_fast_nb(int H);
 int lm_head_max_wg_per_cu(int H);
-hipError_t launch_lm_head(const float* hidden, const uint16_t* gamma, float eps, const uint16_t* x16,
-                          const uint16_t* emb, int H, int V, uint16_t* x_out, uint16_t* logits, int32_t* token_out,
-                          unsigned long long* state, int32_t* pos_advance, int n_wg, hipStream_t st);
+// The RMSNorm prologue reads hidden (fp32) or hidden16 (fp16); with neither,
+// x16 is the normalized input.
+hipError_t launch_lm_head(const float* hidden, const uint16_t* hidden16, const uint16_t* gamma, float eps,
+                          const uint16_t* x16, const uint16_t* emb, int H, int V, uint16_t* x_out, uint16_t* logits,
+                          int32_t* token_out, unsigned long long* state, int32_t* pos_advance, int n_wg,
+                          hipStream_t st);
 hipError_t launch_embed_f16(const uint16_t* emb, int V, int H, const int32_t* token, float* hidden, hipStream_t st);
-hipError_t launch_argmax_f16(const uint16_t* logits, int n, int32_t* token_out, unsigned long long* state, int n_wg,
-                             hipStream_t st);
+hipError_t launch_embed_h16(const uint16_t* emb, int V, int H, const int32_t* token, uint16_t* hidden16,
+                            hipStream_t st);
+hipError_t launch_argmax_f16(const uint16_t* logits, int n, int32_t* token_out, unsigned long long* state,
+                             int32_t* pos_advance, int n_wg, hipStream_t st);
 hipError_t launch_rmsnorm_f16_rows(const float* x, const uint16_t* gamma, float eps, int M, int H, uint16_t* y,
                                    hipStream_t st);
 // Decode attention (attention.hip): head_dim 64 or 128, chunks of
@@ -272,18 +279,28 @@ __device__ __forceinline__ float acc_to_float(int val, int mag) {
 
 // Output element o of a GEMV / GEMM (GemvDesc or GemmDesc): acc (the trit
 // accumulator), y = float(m * acc) * s, y16 = half(y) (the reference's
-// __float2half projection output), resid += float(half(y)) (its add_k_f32
-// residual step).
+// __float2half projection output), resid += float(half(y)) (BitNet's
+// add_k_f32 residual step into its fp32 stream) and, for GEMVs, resid16 =
+// half(float(resid16) + float(half(y))) (the Llama forward's add_k into its
+// fp16 stream, cuda/ter_cuda_forward_packed.cu:115-118).
 template <class D>
 __device__ __forceinline__ void emit_out(const D& d, long long o, int val, float s) {
 #pragma clang fp contract(off)
     if (d.acc) gptr(d.acc)[o] = val;
     const float y = acc_to_float(val, d.w_mag) * s;
     if (d.y) gptr(d.y)[o] = y;
-    if (d.y16 || d.resid) {
+    constexpr bool kR16 = std::is_same<D, GemvDesc>::value;
+    bool half_out = d.y16 || d.resid;
+    if constexpr (kR16) half_out = half_out || d.resid16;
+    if (half_out) {
         const uint16_t h = float_to_half_bits(y);
         if (d.y16) gptr(d.y16)[o] = h;
         if (d.resid) gptr(d.resid)[o] = gptr(d.resid)[o] + half_bits_to_float(h);
+        if constexpr (kR16) {
+            if (d.resid16)
+                gptr(d.resid16)[o] =
+                    float_to_half_bits(half_bits_to_float(gptr(d.resid16)[o]) + half_bits_to_float(h));
+        }
     }
 }
 
@@ -312,6 +329,15 @@ __device__ inline float ter_expf(float x) {
     const int ni = (int)n;
     const int n1 = ni / 2, n2 = ni - n1;
     return (p * ter_pow2i(n1)) * ter_pow2i(n2);
+}
+
+// silu(gate) * up of silu_mul_quant_k (cuda/ter_cuda_forward_packed.cu:322-326):
+// g / (1 + exp(-g)) with this build's exp, then the product, each rounded
+// (the division correctly rounded, as nvcc's default division is).
+__device__ inline float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+    const float sg = g / (1.0f + ter_expf(-g));
+    return sg * u;
 }
 
 // relu^2(gate) * up of relu2_mul_rmsnorm_quant_k

@@ -227,13 +227,24 @@ __device__ __forceinline__ void load_relu2_16(const uint16_t* g, const uint16_t*
     }
 }
 
-// 16 activations of an fp32-family input (fp32, fp16 for X_F16_RMS, or
-// relu^2(gate) * up for X_RELU2_RMS) as fp32.
+// silu(gate) * up on 16 elements at k (zeros past K).
+__device__ __forceinline__ void load_silu16(const uint16_t* g, const uint16_t* u, int k, int K, float (&v)[16]) {
+    float gv[16], uv[16];
+    load_h16(g, k, K, gv);
+    load_h16(u, k, K, uv);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = silu_mul(gv[i], uv[i]);  // past K: silu(0) * 0 = 0
+}
+
+// 16 activations of an fp32-family input (fp32, fp16 for X_F16 / X_F16_RMS,
+// relu^2(gate) * up for X_RELU2_RMS, silu(gate) * up for X_SILU_MUL) as fp32.
 __device__ __forceinline__ void load_x16f(const GemvDesc& d, int k, float (&v)[16]) {
-    if (d.x_kind == TER_HIP_X_F16_RMS) {
+    if (d.x_kind == TER_HIP_X_F16_RMS || d.x_kind == TER_HIP_X_F16) {
         load_h16(static_cast<const uint16_t*>(d.x), k, d.K, v);
     } else if (d.x_kind == TER_HIP_X_RELU2_RMS) {
         load_relu2_16(static_cast<const uint16_t*>(d.x), d.up, k, d.K, v);
+    } else if (d.x_kind == TER_HIP_X_SILU_MUL) {
+        load_silu16(static_cast<const uint16_t*>(d.x), d.up, k, d.K, v);
     } else {
         const float* xf = static_cast<const float*>(d.x);
         load_f16(xf, k, d.K, (reinterpret_cast<uintptr_t>(xf) & 15u) == 0, v);
@@ -243,7 +254,7 @@ __device__ __forceinline__ void load_x16f(const GemvDesc& d, int k, float (&v)[1
 __device__ __forceinline__ float x_at(const GemvDesc& d, int i) {
     if (d.x_kind == TER_HIP_X_F32_RMS) return gptr(static_cast<const float*>(d.x))[i];
     const float h = half_bits_to_float(gptr(static_cast<const uint16_t*>(d.x))[i]);
-    return d.x_kind == TER_HIP_X_F16_RMS ? h : relu2_mul(h, half_bits_to_float(gptr(d.up)[i]));
+    return d.x_kind == TER_HIP_X_F16_RMS ? h : relu2_mul(h, half_bits_to_float(gptr(d.up)[i]));  // (RMS kinds only)
 }
 
 // RMSNorm of the RMS kinds: n = (x * rms_inv) * gamma on 16 values at k.
@@ -298,7 +309,7 @@ __device__ __forceinline__ float stage_x(const GemvDesc& d, const XPre& r, int8_
             put_chunk(c, load_i16(xp, c * 16, K, vec_ok), lds_x, usum);
         return d.x_scale_dev ? *gptr(d.x_scale_dev) : d.x_scale;
     }
-    const bool rms = d.x_kind != TER_HIP_X_F32;
+    const bool rms = d.x_kind == TER_HIP_X_F32_RMS || d.x_kind == TER_HIP_X_F16_RMS || d.x_kind == TER_HIP_X_RELU2_RMS;
     float rms_inv = 1.0f;
     uint32_t g0[8], g1[8];
     if (rms) {
@@ -1053,6 +1064,7 @@ struct Fixups {
     int32_t* acc;
     uint16_t* y16;
     float* resid;
+    uint16_t* resid16;
     unsigned long long* fix;
     int Ku, w_mag;
 };
@@ -1064,6 +1076,7 @@ __device__ __forceinline__ void finish_fixups(const Fixups& f) {
     d.acc = f.acc;
     d.y16 = f.y16;
     d.resid = f.resid;
+    d.resid16 = f.resid16;
     d.fix = f.fix;
     d.Ku = f.Ku;
     d.w_mag = f.w_mag;
@@ -1163,6 +1176,7 @@ __device__ __forceinline__ Fixups no_fixups(const GemvDesc& d, float s) {
     f.acc = d.acc;
     f.y16 = d.y16;
     f.resid = d.resid;
+    f.resid16 = d.resid16;
     f.fix = d.fix;
     f.Ku = d.Ku;
     f.w_mag = d.w_mag;

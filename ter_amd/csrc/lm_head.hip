@@ -41,6 +41,7 @@ constexpr unsigned kOob = 0x80000000u;  // voffset past any resource: the load r
 
 struct LmArgs {
     const float* hidden;        // fp32 [H] residual stream (RMSNorm prologue) or null
+    const uint16_t* hidden16;   // fp16 [H] residual stream (the Llama forward's; RMSNorm prologue) or null
     const uint16_t* gamma;      // fp16 [H] RMSNorm weights (with hidden)
     const uint16_t* x16;        // fp16 [H] normalized input (without hidden)
     const uint16_t* emb;        // fp16 [V][H]
@@ -153,13 +154,37 @@ __device__ void argmax_finish(unsigned long long key, unsigned long long* kred, 
 // H/2 (H even).  With hidden: rmsnorm_f32_in_k's steps (256 strided partial
 // sums of squares with fused multiply-adds, the reference tree,
 // rms_inv = 1 / sqrt(ss / H + eps) correctly rounded,
-// y = half((x * rms_inv) * gamma)).  Workgroup 0 writes the optional copy.
+// y = half((x * rms_inv) * gamma)).  With hidden16 the same steps on the
+// fp16 values, widened exactly (rmsnorm_k, cuda/ter_cuda_forward_packed.cu:27-37).
+// Workgroup 0 writes the optional copy.
 __device__ void stage_x_pairs(const LmArgs& a, uint32_t* xs, int npad, float* red) {
 #pragma clang fp contract(off)
     const int tid = threadIdx.x;
     const int n2 = a.H >> 1;
     const bool owner = blockIdx.x == 0 && a.x_out != nullptr;
-    if (a.hidden) {
+    if (a.hidden16) {
+        const TER_GLOBAL uint16_t* h = gptr(a.hidden16);
+        float part = 0.f;
+        for (int i = tid; i < a.H; i += kLmThreads) {
+            const float v = half_bits_to_float(h[i]);
+            part = __builtin_fmaf(v, v, part);
+        }
+        const float rms_inv = 1.0f / __builtin_sqrtf(tree_sum256(part, red) / (float)a.H + a.eps);
+        for (int i = tid; i < npad; i += kLmThreads) {
+            uint32_t w = 0;
+            if (i < n2) {
+                const uint32_t hw = gptr(reinterpret_cast<const uint32_t*>(a.hidden16))[i];
+                const uint32_t gw = gptr(reinterpret_cast<const uint32_t*>(a.gamma))[i];
+                const uint16_t y0 = float_to_half_bits((half_bits_to_float((uint16_t)(hw & 0xFFFFu)) * rms_inv) *
+                                                       half_bits_to_float((uint16_t)(gw & 0xFFFFu)));
+                const uint16_t y1 = float_to_half_bits((half_bits_to_float((uint16_t)(hw >> 16)) * rms_inv) *
+                                                       half_bits_to_float((uint16_t)(gw >> 16)));
+                w = (uint32_t)y0 | ((uint32_t)y1 << 16);
+                if (owner) gptr(reinterpret_cast<uint32_t*>(a.x_out))[i] = w;
+            }
+            xs[i] = w;
+        }
+    } else if (a.hidden) {
         const TER_GLOBAL float* h = gptr(a.hidden);
         float part = 0.f;
         for (int i = tid; i < a.H; i += kLmThreads) part = __builtin_fmaf(h[i], h[i], part);
@@ -379,13 +404,14 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_generic_kernel(LmArgs a, i
 
 // argmax of fp16 logits [N] (argmax_local_k + argmax_final_k semantics).
 __global__ __launch_bounds__(kLmThreads) void argmax_kernel(const uint16_t* __restrict__ logits, int n,
-                                                            int32_t* token_out, unsigned long long* state) {
+                                                            int32_t* token_out, unsigned long long* state,
+                                                            int32_t* pos_advance) {
     __shared__ unsigned long long kred[kLmWaves];
     const int chunk = argmax_chunk(n);
     unsigned long long best = 0ull;
     for (long long i = (long long)blockIdx.x * kLmThreads + threadIdx.x; i < n; i += (long long)gridDim.x * kLmThreads)
         best = umax64(best, argmax_key(gptr(logits)[i], (int)i, chunk));
-    argmax_finish(best, kred, state, token_out, chunk, nullptr);
+    argmax_finish(best, kred, state, token_out, chunk, pos_advance);
 }
 
 // token_embed_lookup_k: hidden[i] = float(token_embd[token][i]) (exact
@@ -396,6 +422,16 @@ __global__ void embed_kernel(const uint16_t* __restrict__ emb, int V, int H, con
     const int t = *gptr(token);
     if (i >= H || t < 0 || t >= V) return;
     gptr(hidden)[i] = half_bits_to_float(gptr(emb)[(long long)t * H + i]);
+}
+
+// token_embed_lookup_k (cuda/ter_cuda_forward_packed.cu:99-106): the token's
+// fp16 row into the fp16 hidden stream (a token outside [0, V) writes nothing).
+__global__ void embed16_kernel(const uint16_t* __restrict__ emb, int V, int H, const int32_t* __restrict__ token,
+                               uint16_t* __restrict__ hidden16) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const int t = *gptr(token);
+    if (i >= H || t < 0 || t >= V) return;
+    gptr(hidden16)[i] = gptr(emb)[(long long)t * H + i];
 }
 
 // rmsnorm_f32_in_k per row (256 threads): y = half((x * rms_inv) * gamma).
@@ -473,12 +509,14 @@ int lm_head_max_wg_per_cu(int H) {
     return e == hipSuccess ? n : 0;
 }
 
-hipError_t launch_lm_head(const float* hidden, const uint16_t* gamma, float eps, const uint16_t* x16,
-                          const uint16_t* emb, int H, int V, uint16_t* x_out, uint16_t* logits, int32_t* token_out,
-                          unsigned long long* state, int32_t* pos_advance, int n_wg, hipStream_t st) {
+hipError_t launch_lm_head(const float* hidden, const uint16_t* hidden16, const uint16_t* gamma, float eps,
+                          const uint16_t* x16, const uint16_t* emb, int H, int V, uint16_t* x_out, uint16_t* logits,
+                          int32_t* token_out, unsigned long long* state, int32_t* pos_advance, int n_wg,
+                          hipStream_t st) {
     LmArgs a{};
     a.pos_advance = pos_advance;
     a.hidden = hidden;
+    a.hidden16 = hidden16;
     a.gamma = gamma;
     a.x16 = x16;
     a.emb = emb;
@@ -499,14 +537,20 @@ hipError_t launch_lm_head(const float* hidden, const uint16_t* gamma, float eps,
     return hipGetLastError();
 }
 
-hipError_t launch_argmax_f16(const uint16_t* logits, int n, int32_t* token_out, unsigned long long* state, int n_wg,
-                             hipStream_t st) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(n_wg), dim3(kLmThreads), 0, st, logits, n, token_out, state);
+hipError_t launch_argmax_f16(const uint16_t* logits, int n, int32_t* token_out, unsigned long long* state,
+                             int32_t* pos_advance, int n_wg, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(n_wg), dim3(kLmThreads), 0, st, logits, n, token_out, state, pos_advance);
     return hipGetLastError();
 }
 
 hipError_t launch_embed_f16(const uint16_t* emb, int V, int H, const int32_t* token, float* hidden, hipStream_t st) {
     hipLaunchKernelGGL(embed_kernel, dim3((H + 255) / 256), dim3(256), 0, st, emb, V, H, token, hidden);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_h16(const uint16_t* emb, int V, int H, const int32_t* token, uint16_t* hidden16,
+                            hipStream_t st) {
+    hipLaunchKernelGGL(embed16_kernel, dim3((H + 255) / 256), dim3(256), 0, st, emb, V, H, token, hidden16);
     return hipGetLastError();
 }
 

@@ -127,8 +127,14 @@ def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=No
     a = L.Act()
     a.data = x.data_ptr()
     if up is not None and gamma is None:
-        raise TypeError("up (relu^2(gate) * up activations) needs gamma")
-    if gamma is not None:
+        # silu(gate) * up, then absmax quantization (silu_mul_quant_k)
+        if x.dtype != torch.float16 or up.dtype != torch.float16 or not up.is_cuda or up.shape != x.shape:
+            raise TypeError("silu activations: gate and up must be CUDA float16 tensors of one shape")
+        a.kind = L.X_SILU_MUL
+        a.up = up.data_ptr()
+        a.q_out = _ptr(q_out)
+        a.scale_out = _ptr(scale_out)
+    elif gamma is not None:
         # fused RMSNorm (fp16 gamma) + absmax quantization in the prologue
         if gamma.dtype != torch.float16 or not gamma.is_cuda:
             raise TypeError("gamma must be a CUDA float16 tensor")
@@ -151,39 +157,43 @@ def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=No
         a.kind = L.X_I8 if x.dtype == torch.int8 else L.X_I16
         a.scale = float(x_scale) if x_scale is not None else 1.0
         a.scale_dev = _ptr(x_scale_dev)
-    elif x.dtype == torch.float32:
-        a.kind = L.X_F32
+    elif x.dtype in (torch.float32, torch.float16):
+        # absmax quantization in the prologue (quant_int8_k)
+        a.kind = L.X_F32 if x.dtype == torch.float32 else L.X_F16
         a.q_out = _ptr(q_out)
         a.scale_out = _ptr(scale_out)
     else:
-        raise TypeError(f"activations must be int8, int16 or float32, got {x.dtype}")
+        raise TypeError(f"activations must be int8, int16, float32 or float16, got {x.dtype}")
     return a
 
 
-def _out(y, acc, y16, resid) -> L.Out:
+def _out(y, acc, y16, resid, resid16=None) -> L.Out:
     o = L.Out()
-    o.y, o.acc, o.y16, o.resid = _ptr(y), _ptr(acc), _ptr(y16), _ptr(resid)
+    o.y, o.acc, o.y16, o.resid, o.resid16 = _ptr(y), _ptr(acc), _ptr(y16), _ptr(resid), _ptr(resid16)
     return o
 
 
 def gemv(W: PackedTrits, x, y=None, acc=None, x_scale: Optional[float] = None, x_scale_dev=None,
-         q_out=None, scale_out=None, gamma=None, eps: float = 1e-5, up=None, y16=None, resid=None, stream=None):
-    """M = 1 GEMV.  x: int8 or int16 [K] (with x_scale or x_scale_dev) or fp32 [K]
-    (absmax-quantized in the kernel prologue); with gamma (fp16 [K]), x fp32 or
-    fp16 is RMS-normalized first (rmsnorm_quant_*_in_k steps), and with up as
-    well, x is the fp16 gate and the prologue is relu2_mul_rmsnorm_quant_k.
-    Outputs: y fp32, acc int32, y16 fp16 = half(y), resid fp32 += half(y);
-    y is allocated when none is given.  Returns (y, acc)."""
+         q_out=None, scale_out=None, gamma=None, eps: float = 1e-5, up=None, y16=None, resid=None, resid16=None,
+         stream=None):
+    """M = 1 GEMV.  x: int8 or int16 [K] (with x_scale or x_scale_dev), or fp32 /
+    fp16 [K] (absmax-quantized in the kernel prologue, quant_int8_k); with gamma
+    (fp16 [K]), x fp32 or fp16 is RMS-normalized first (rmsnorm_quant_*_in_k
+    steps), and with up as well, x is the fp16 gate and the prologue is
+    relu2_mul_rmsnorm_quant_k; with up but no gamma, silu_mul_quant_k.
+    Outputs: y fp32, acc int32, y16 fp16 = half(y), resid fp32 += half(y),
+    resid16 fp16 = half(resid16 + half(y)); y is allocated when none is given.
+    Returns (y, acc)."""
     torch = _torch()
     _require_cuda(x, "x", None, W.K)
-    if y is None and acc is None and y16 is None and resid is None:
+    if y is None and acc is None and y16 is None and resid is None and resid16 is None:
         y = torch.empty(W.N, dtype=torch.float32, device=x.device)
     a = _act(x, x_scale, x_scale_dev, q_out, scale_out, gamma, eps, up)
-    if y16 is None and resid is None:
+    if y16 is None and resid is None and resid16 is None:
         L.check(L.lib().ter_hip_gemv(C.byref(W.wpk), C.byref(a), _ptr(y), _ptr(acc), _stream(stream)),
                 "ter_hip_gemv")
     else:
-        o = _out(y, acc, y16, resid)
+        o = _out(y, acc, y16, resid, resid16)
         L.check(L.lib().ter_hip_gemv_out(C.byref(W.wpk), C.byref(a), C.byref(o), _stream(stream)),
                 "ter_hip_gemv_out")
     return y, acc
@@ -376,9 +386,11 @@ class ArgmaxState:
         return self.t.data_ptr()
 
 
-def argmax_f16(logits, out_idx=None, state: Optional[ArgmaxState] = None, stream=None):
+def argmax_f16(logits, out_idx=None, state: Optional[ArgmaxState] = None, pos_advance=None, stream=None):
     """argmax of fp16 logits with the reference's index (ties included):
-    argmax_local_k + argmax_final_k (cuda/ter_cuda_forward_bitnet.cu:454-495)."""
+    argmax_local_k + argmax_final_k (cuda/ter_cuda_forward_bitnet.cu:454-495);
+    with pos_advance (device int32 [1]) also inc_pos_k
+    (cuda/ter_cuda_forward_packed.cu:559)."""
     torch = _torch()
     if logits.dtype != torch.float16:
         raise TypeError("logits must be float16")
@@ -386,8 +398,14 @@ def argmax_f16(logits, out_idx=None, state: Optional[ArgmaxState] = None, stream
         out_idx = torch.empty(1, dtype=torch.int32, device=logits.device)
     if state is None:
         state = ArgmaxState(logits.device)
-    L.check(L.lib().ter_hip_argmax_f16(logits.data_ptr(), logits.numel(), out_idx.data_ptr(), state.ptr(),
-                                       _stream(stream)), "ter_hip_argmax_f16")
+    if pos_advance is None:
+        L.check(L.lib().ter_hip_argmax_f16(logits.data_ptr(), logits.numel(), out_idx.data_ptr(), state.ptr(),
+                                           _stream(stream)), "ter_hip_argmax_f16")
+    else:
+        if pos_advance.dtype != torch.int32:
+            raise TypeError("pos_advance must be int32")
+        L.check(L.lib().ter_hip_argmax_f16_step(logits.data_ptr(), logits.numel(), out_idx.data_ptr(), state.ptr(),
+                                                pos_advance.data_ptr(), _stream(stream)), "ter_hip_argmax_f16_step")
     return out_idx
 
 
@@ -402,24 +420,37 @@ def embed_f16(token_embd, token_dev, hidden=None, stream=None):
     return hidden
 
 
-def lm_head_argmax(hidden, gamma, token_embd, eps: float = 1e-5, token_out=None, state: Optional[ArgmaxState] = None,
-                   x_norm_out=None, logits_out=None, pos_advance=None, stream=None):
-    """The decode step's tail in one launch (cuda/ter_cuda_forward_bitnet.cu:890-911):
-    RMSNorm of fp32 hidden [H] -> fp16 lm_head over token_embd [V][H] -> argmax.
-    Returns token_out (int32 [1])."""
+def embed_h16(token_embd, token_dev, hidden16=None, stream=None):
+    """token_embed_lookup_k of the Llama forward: hidden16 fp16 [H] = token_embd[*token_dev]."""
     torch = _torch()
     V, H = token_embd.shape
-    if hidden.dtype != torch.float32 or hidden.numel() != H:
-        raise TypeError("hidden must be float32 [H]")
+    if hidden16 is None:
+        hidden16 = torch.empty(H, dtype=torch.float16, device=token_embd.device)
+    L.check(L.lib().ter_hip_embed_h16(token_embd.data_ptr(), V, H, token_dev.data_ptr(), hidden16.data_ptr(),
+                                      _stream(stream)), "ter_hip_embed_h16")
+    return hidden16
+
+
+def lm_head_argmax(hidden, gamma, token_embd, eps: float = 1e-5, token_out=None, state: Optional[ArgmaxState] = None,
+                   x_norm_out=None, logits_out=None, pos_advance=None, stream=None):
+    """The decode step's tail in one launch (cuda/ter_cuda_forward_bitnet.cu:890-911,
+    cuda/ter_cuda_forward_packed.cu:550-557): RMSNorm of hidden [H] (fp32, or
+    the Llama forward's fp16 stream) -> fp16 lm_head over token_embd [V][H] ->
+    argmax.  Returns token_out (int32 [1])."""
+    torch = _torch()
+    V, H = token_embd.shape
+    if hidden.dtype not in (torch.float32, torch.float16) or hidden.numel() != H:
+        raise TypeError("hidden must be float32 or float16 [H]")
     if gamma.dtype != torch.float16 or token_embd.dtype != torch.float16:
         raise TypeError("gamma and token_embd must be float16")
     if token_out is None:
         token_out = torch.empty(1, dtype=torch.int32, device=hidden.device)
     if state is None:
         state = ArgmaxState(hidden.device)
-    L.check(L.lib().ter_hip_lm_head_argmax(hidden.data_ptr(), gamma.data_ptr(), C.c_float(eps), token_embd.data_ptr(),
-                                           H, V, _ptr(x_norm_out), _ptr(logits_out), token_out.data_ptr(),
-                                           state.ptr(), _ptr(pos_advance), _stream(stream)), "ter_hip_lm_head_argmax")
+    fn = "ter_hip_lm_head_argmax" if hidden.dtype == torch.float32 else "ter_hip_lm_head_argmax_h16"
+    L.check(getattr(L.lib(), fn)(hidden.data_ptr(), gamma.data_ptr(), C.c_float(eps), token_embd.data_ptr(),
+                                 H, V, _ptr(x_norm_out), _ptr(logits_out), token_out.data_ptr(),
+                                 state.ptr(), _ptr(pos_advance), _stream(stream)), fn)
     return token_out
 
 
@@ -484,7 +515,7 @@ def _held(it: dict) -> list:
 class Plan:
     """Many independent GEMVs in one launch (one work list).  `items` is a
     sequence of dicts: {w: PackedTrits, x: tensor, y?, acc?, y16?, resid?,
-    x_scale?, x_scale_dev?, q_out?, scale_out?, gamma?, eps?, up?}."""
+    resid16?, x_scale?, x_scale_dev?, q_out?, scale_out?, gamma?, eps?, up?}."""
 
     def __init__(self, items: Sequence[dict], wg_per_cu: int = 0):
         n = len(items)
@@ -499,6 +530,7 @@ class Plan:
             arr[i].acc = _ptr(it.get("acc"))
             arr[i].y16 = _ptr(it.get("y16"))
             arr[i].resid = _ptr(it.get("resid"))
+            arr[i].resid16 = _ptr(it.get("resid16"))
             self._keep.extend(_held(it))
         h = C.c_void_p()
         L.check(L.lib().ter_hip_plan_create(C.byref(h), arr, n, int(wg_per_cu)), "ter_hip_plan_create")

@@ -3,7 +3,9 @@ forward_token_dev order, cuda/ter_cuda_forward_bitnet.cu:848-913), shared by
 the end-to-end decode tests: embedding, per layer the RMSNorm + quantization,
 Q/K/V, RoPE, the chunked attention, the sub-norm, O with the residual add,
 the FFN norm, gate/up, relu^2 sub-norm, down with the residual add; then the
-final norm, the fp16 lm_head and the argmax.  Test infrastructure only."""
+final norm, the fp16 lm_head and the argmax.  llama_oracle_step is the same
+for the Llama forward (cuda/ter_cuda_forward_packed.cu:505-560).  Test
+infrastructure only."""
 import numpy as np
 
 from oracle import oracle as O
@@ -79,3 +81,69 @@ def host_model_i8(m, seed, p_zero=0.4):
                  ffn_sub_norm=host(lay.ffn_sub_norm))
         layers.append(d)
     return dict(shape=m.shape, layers=layers, emb=host(m.token_embd), out_norm=host(m.output_norm))
+
+
+def _mm(wt, x_q, x_s):
+    w, ws, Kd, Nd = wt
+    if w.dtype == np.int8:  # trits [K][N]
+        return O.gemv_i8w(x_q, x_s, w, ws)[1]
+    return O.gemv_v11(x_q, x_s, w, ws, Kd, Nd)[1]
+
+
+def llama_oracle_step(hm, tok, pos, K, V, table):
+    """The oracle's chain of one Llama decode step (forward_token_dev,
+    cuda/ter_cuda_forward_packed.cu:505-560) on the fp16 hidden stream:
+    embedding; per layer rmsnorm_quant_fp16_in_k, Q/K/V, NORM RoPE, the
+    chunked attention, quant_int8_k of the fp16 attention output, O with
+    add_k, rmsnorm_quant_fp16_in_k, gate/up, silu_mul_quant_k, down with
+    add_k; then the tail: the ternary lm_head behind the fused norm + quant
+    (bench mode, hm["lm_head"]) or rmsnorm_k + the fp16 lm_head over the
+    tied token_embd; the argmax.  Writes the new cache rows into K and V."""
+    c = hm["shape"]
+    hidden = hm["emb"][tok].astype(np.float16)
+    for l, lay in enumerate(hm["layers"]):
+        xq, xs, _ = O.rmsnorm_quant(hidden, lay["attn_norm"], c.eps)
+        q = half_of(_mm(lay["Wq"], xq, xs)).reshape(c.Nh, c.Hd)
+        k = half_of(_mm(lay["Wk"], xq, xs)).reshape(c.Nkv, c.Hd)
+        v = half_of(_mm(lay["Wv"], xq, xs)).reshape(c.Nkv, c.Hd)
+        qr = O.rope_f16(q, table[pos], False)
+        K[l, pos] = O.rope_f16(k, table[pos], False)
+        V[l, pos] = v
+        att, _ = O.attention_splitk(qr, K[l, :pos + 1], V[l, :pos + 1])
+        aq, as_ = O.quant_int8(att.reshape(-1).astype(np.float32))
+        hidden = O.residual_add_h16(hidden, _mm(lay["Wo"], aq, as_))
+        fq, fs, _ = O.rmsnorm_quant(hidden, lay["ffn_norm"], c.eps)
+        g16, u16 = half_of(_mm(lay["Wgate"], fq, fs)), half_of(_mm(lay["Wup"], fq, fs))
+        dq, ds, _ = O.silu_mul_quant(g16, u16)
+        hidden = O.residual_add_h16(hidden, _mm(lay["Wdown"], dq, ds))
+    if hm.get("lm_head") is None:
+        xn, _ = O.rmsnorm_f16(hidden.astype(np.float32), hm["out_norm"], c.eps)
+        logits, _ = O.lm_head_f16(xn, hm["emb"])
+    else:
+        hq, hs, _ = O.rmsnorm_quant(hidden, hm["out_norm"], c.eps)
+        logits = half_of(_mm(hm["lm_head"], hq, hs))
+    return O.argmax_f16(logits), hidden
+
+
+def llama_host_model(m, seed=None, p_zero=0.4):
+    """The host copy of a llama.Model: projections read back as v11 bytes, or,
+    with `seed` (a llama.random_model's), regenerated on the host as int8
+    trits from the seeds the device drew (ter_hip_synth_v11's splitmix64
+    stream); norms and the token embedding copied from the device."""
+    from ter_amd import llama as LM
+    shapes = LM.proj_shapes(m.shape)
+
+    def wt(W, K, N, s):
+        if seed is None:
+            return (host(W.to_v11()), W.scale, K, N)
+        return (O.rand_trits_c(s, K, N, p_zero), W.scale, K, N)
+
+    layers = []
+    for l, lay in enumerate(m.layers):
+        d = {nm: wt(lay.W[nm], *shapes[nm], LM.weight_seed(seed or 0, l, i)) for i, nm in enumerate(LM.PROJ)}
+        d.update(attn_norm=host(lay.attn_norm), ffn_norm=host(lay.ffn_norm))
+        layers.append(d)
+    head = None
+    if m.lm_head is not None:
+        head = wt(m.lm_head, m.shape.H, m.shape.V, LM.weight_seed(seed or 0, -1, 0))
+    return dict(shape=m.shape, layers=layers, emb=host(m.token_embd), out_norm=host(m.output_norm), lm_head=head)

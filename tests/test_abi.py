@@ -27,7 +27,7 @@ def declared_functions():
 
 def test_library_exports_every_declared_symbol():
     names = declared_functions()
-    assert len(names) == 52, names
+    assert len(names) == 55, names
     lib = L.lib()
     missing = [n for n in names if not hasattr(lib, n)]
     assert not missing, missing
@@ -71,8 +71,27 @@ def test_gemv_validation_without_device():
     assert lib.ter_hip_gemv(C.byref(w), None, fake, None, None) == L.ERR_NULL
     assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_NULL  # x.data null
     x.data = fake
-    x.kind = 7
+    x.kind = 99
     assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_PAYLOAD
+    # silu(gate) * up needs up; fp16 kinds 2-byte aligned; both are GEMV-only
+    x.kind = L.X_SILU_MUL
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_NULL
+    x.up = fake + 1
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_ALIGN
+    x.up = None
+    x.kind, x.data = L.X_F16, fake + 1
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_ALIGN
+    x.data = fake
+    assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 4, fake, None, None) == L.ERR_PAYLOAD
+    assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 1, fake, None, None) == L.ERR_PAYLOAD
+    # fp16 residual outputs: 2-byte aligned, GEMVs only
+    o = L.Out()
+    o.resid16 = fake + 1
+    assert lib.ter_hip_gemv_out(C.byref(w), C.byref(x), C.byref(o), None) == L.ERR_ALIGN
+    o.resid16 = fake
+    xi = L.Act()
+    xi.data, xi.kind, xi.scale_dev = fake, L.X_I8, fake
+    assert lib.ter_hip_gemm_out(C.byref(w), C.byref(xi), 4, C.byref(o), None) == L.ERR_PAYLOAD
     x.kind = L.X_I8
     assert lib.ter_hip_gemv(C.byref(w), C.byref(x), None, None, None) == L.ERR_NULL  # no output
     x.kind = L.X_F32

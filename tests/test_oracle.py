@@ -538,6 +538,75 @@ def test_residual_add_rounds_projection_to_half():
     assert got[1] == np.inf and got[2] == -np.inf
 
 
+def test_residual_add_h16_is_one_binary16_addition():
+    """add_k (cuda/ter_cuda_forward_packed.cu:113-116): fp16 hidden + half(y),
+    against numpy's binary16 addition, overflow and signed zero included."""
+    rng = np.random.default_rng(18)
+    h = (rng.standard_normal(8192) * 30).astype(np.float16)
+    y = (rng.standard_normal(8192) * 30).astype(np.float32)
+    h[:5] = [65504.0, -65504.0, 0.5, -0.0, 1.0]
+    y[:5] = [64.0, -64.0, -0.5, 0.0, 2.0 ** -12 + 2.0 ** -30]
+    got = O.residual_add_h16(h, y)
+    with np.errstate(over="ignore"):
+        want = h + y.astype(np.float16)
+    assert (got.view(np.uint16) == want.view(np.uint16)).all()
+    assert got[0] == np.inf and got[1] == -np.inf and got[2] == 0
+    assert got[4] == np.float16(1.0) + np.float16(2.0 ** -12)  # y rounds first, then the sum
+    # a plausible slip, adding y in fp32 without rounding it to fp16 first, differs here
+    h2, y2 = np.array([1.0], np.float16), np.array([2.0 ** -11 + 2.0 ** -13], np.float32)
+    assert O.residual_add_h16(h2, y2)[0] == np.float16(1.0) + np.float16(y2[0])
+
+
+def _silu_mul_f64(g, u):
+    g, u = np.float64(g), np.float64(u)
+    return g / (1.0 + np.exp(-g)) * u
+
+
+def test_silu_mul_closed_forms():
+    """silu_mul_quant_k (cuda/ter_cuda_forward_packed.cu:322-325): g = 0 or
+    u = 0 give 0; g >= 17 gives g * u exactly (expf(-g) < 2^-24 vanishes in
+    1 + expf(-g)); g <= -104 gives (-)0 (expf underflow is not needed: g / inf)."""
+    f = lambda g, u: O.lib().orc_silu_mul(int(np.float16(g).view(np.uint16)), int(np.float16(u).view(np.uint16)))
+    assert f(0.0, 5.0) == 0.0 and f(3.0, 0.0) == 0.0
+    for g in (17.0, 20.0, 100.0, 6.0e4):
+        for u in (1.0, -2.5, 0.125):
+            assert f(g, u) == np.float32(np.float16(g)) * np.float32(np.float16(u))
+    for g in (-104.0, -2000.0, -6.0e4):
+        assert f(g, 3.0) == 0.0
+    assert f(1.0, 1.0) == np.float32(1.0 / (1.0 + np.float32(np.exp(np.float32(-1.0)))))
+
+
+def test_silu_mul_within_rounding_bound_and_odd_part():
+    """fp32 silu(g) * u against float64 on every finite-range fp16 gate value
+    of interest: a few ulp (exp within 1 ulp, then three roundings).
+    silu(g) - silu(-g) = g (sigmoid(g) + sigmoid(-g) = 1): a dropped minus
+    sign or a sigmoid without the g factor breaks it."""
+    rng = np.random.default_rng(19)
+    g = np.concatenate([np.linspace(-30, 30, 20001), rng.standard_normal(20000) * 4]).astype(np.float16)
+    u = rng.uniform(-3, 3, g.size).astype(np.float16)
+    _, _, v = O.silu_mul_quant(g, u)
+    want = _silu_mul_f64(g.astype(np.float64), u.astype(np.float64))
+    err = np.abs(v.astype(np.float64) - want)
+    assert (err <= 4 * np.spacing(np.abs(want).astype(np.float32)).astype(np.float64) + 1e-38).all()
+    ones = np.ones(g.size, np.float16)
+    _, _, vp = O.silu_mul_quant(g, ones)
+    _, _, vn = O.silu_mul_quant(-g, ones)
+    gf = g.astype(np.float64)
+    # up to the fp32 rounding of each term
+    assert np.abs((vp.astype(np.float64) - vn) - gf).max() <= 1e-5 * np.abs(gf).max()
+
+
+def test_silu_mul_quant_is_quant_int8_of_silu():
+    rng = np.random.default_rng(20)
+    g = (rng.standard_normal(8192) * 3).astype(np.float16)
+    u = rng.standard_normal(8192).astype(np.float16)
+    q, s, v = O.silu_mul_quant(g, u)
+    q2, s2 = O.quant_int8(v)
+    assert (q == q2).all() and s == s2
+    i = int(np.argmax(np.abs(v)))
+    assert abs(int(q[i])) == 127
+
+
 # ---------------------------------------------------------------------------
 # lm_head tail of the decode step: rmsnorm_f32_in_k (:37-47), mm_fp16_lm_head_k
 # (:388-429), argmax_local_k / argmax_final_k (:454-495) of
