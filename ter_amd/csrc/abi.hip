@@ -56,6 +56,11 @@ bool is_rms(int kind) {
     return kind == TER_HIP_X_F32_RMS || kind == TER_HIP_X_F16_RMS || kind == TER_HIP_X_RELU2_RMS;
 }
 
+// Kinds whose GEMV descriptor stages fp32 activations in LDS where K allows:
+// the RMS kinds (their sum of squares reads them) and the fp16 absmax kinds
+// (the strided strip prologue quantizes from them).
+bool stages32(int kind) { return is_rms(kind) || kind == TER_HIP_X_F16 || kind == TER_HIP_X_SILU_MUL; }
+
 // Kinds whose prologue runs only inside the GEMV kernels (no batched row
 // quantizer): int16 rows, the fp16 absmax and the silu(gate) * up kinds.
 bool gemv_only_kind(int kind) {
@@ -177,7 +182,7 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip
     d.w_mag = w->mag;
     d.x_scale = x->scale;
     d.x_kind = x->kind;
-    d.stage32 = is_rms(x->kind) && gemv_stage32(w->K) ? 1 : 0;
+    d.stage32 = stages32(x->kind) && gemv_stage32(w->K) ? 1 : 0;
     return d;
 }
 
@@ -205,16 +210,18 @@ constexpr long long kMaxPieceTiles = 1 << 20;
 
 // The activation kind shared by every item of a GEMV work list when each
 // qualifies for the kernel's vector prologue (K a multiple of 16; x, up and
-// gamma 16-byte aligned), else -1 (the general prologue).
+// gamma 16-byte aligned; the staged kinds' fp32 staging fits), else -1 (the
+// general prologue).  X_F16 and X_SILU_MUL have a vector prologue only in
+// strip mode (strided); elsewhere their kind launches the general kernel.
 int gemv_vec_kind(const ter_hip_gemv_item_t* items, int n) {
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     const int kind = items[0].x.kind;
     for (int i = 0; i < n; ++i) {
         const ter_hip_act_t& x = items[i].x;
         if (x.kind != kind || items[i].w->K % 16 != 0 || !a16(x.data)) return -1;
-        if (gemv_only_kind(x.kind)) return -1;  // the general prologue
-        if (is_rms(x.kind) && !gemv_stage32(items[i].w->K)) return -1;  // the vector prologue always stages
-        if (x.kind == TER_HIP_X_RELU2_RMS && !a16(x.up)) return -1;
+        if (x.kind == TER_HIP_X_I16) return -1;  // the general prologue
+        if (stages32(x.kind) && !gemv_stage32(items[i].w->K)) return -1;  // the vector prologues always stage
+        if ((x.kind == TER_HIP_X_RELU2_RMS || x.kind == TER_HIP_X_SILU_MUL) && !a16(x.up)) return -1;
         if (is_rms(x.kind) && !a16(x.gamma)) return -1;
     }
     return kind;

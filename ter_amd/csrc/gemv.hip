@@ -754,39 +754,50 @@ __device__ __forceinline__ float stage_x_vec(const GemvDesc& d, const XRaw& r, i
 // fp32 staging (stage32); gs16: fp16 gamma [Ku*256] in LDS.
 template <int kKind>
 constexpr int max_strided_ku() {
-    return kKind == TER_HIP_X_RELU2_RMS ? 32 : 16;
+    return kKind == TER_HIP_X_RELU2_RMS || kKind == TER_HIP_X_SILU_MUL ? 32 : 16;
 }
-// Waves per workgroup of the strided strip kernel: 8 for X_RELU2_RMS (its
-// prologue over F values and the 27-unit strips of the down projection keep
-// one wave per SIMD busy for microseconds; a second wave per SIMD shares
-// both), 4 for the 256-thread kinds, whose partials are the 256 threads'.
+// Waves per workgroup of the strided strip kernel: 8 for the down
+// projections' kinds X_RELU2_RMS and X_SILU_MUL (their prologue over F values
+// and the 27- or 32-unit strips keep one wave per SIMD busy for
+// microseconds; a second wave per SIMD shares both), 4 for the 256-thread
+// kinds, whose partials are the 256 threads'.
 #ifndef TER_STRIDED_RELU2_WAVES
 #define TER_STRIDED_RELU2_WAVES 8
 #endif
 template <int kKind>
 constexpr int strided_waves() {
-    return kKind == TER_HIP_X_RELU2_RMS ? TER_STRIDED_RELU2_WAVES : 4;
+    return kKind == TER_HIP_X_RELU2_RMS || kKind == TER_HIP_X_SILU_MUL ? TER_STRIDED_RELU2_WAVES : 4;
 }
 
 // Registers of the strided prologue.  The 256-thread kinds: x and gamma of
 // values t + T j.  X_RELU2_RMS: thread t owns the V = 1024 / T consecutive
 // virtual threads V t .. V t + V - 1 and reads their values V t + 1024 j as
 // one V-half vector each (gate, up and gamma: V = 4 a dwordx2, V = 2 a dword).
+// The absmax kinds X_F16 and X_SILU_MUL (no sum, so no order to keep): x (and
+// up) of values 8 t + 8 T j, 8 halves per dwordx4.
 template <int kKind, int kW>
 struct XStrided {
     static constexpr int T = 64 * kW;
     static constexpr bool R2 = kKind == TER_HIP_X_RELU2_RMS;
-    static constexpr int V = R2 ? 1024 / T : 1;                                  // values per load
-    static constexpr int J = max_strided_ku<kKind>() * kUnitK / (R2 ? 1024 : T);  // loads per operand
-    static constexpr int DW = R2 ? (V + 1) / 2 : 1;                               // dwords per load
-    unsigned x[J][DW];  // fp32 bits (X_F32_RMS) or fp16 bits (X_F16_RMS; gate of X_RELU2_RMS, V halves)
-    unsigned u[R2 ? J : 1][DW];  // up (X_RELU2_RMS)
-    unsigned g[J][DW];  // gamma (fp16 bits)
+    static constexpr bool ABS = kKind == TER_HIP_X_F16 || kKind == TER_HIP_X_SILU_MUL;
+    static constexpr bool UP = R2 || kKind == TER_HIP_X_SILU_MUL;
+    static constexpr int V = R2 ? 1024 / T : (ABS ? 8 : 1);                                  // values per load
+    static constexpr int J = max_strided_ku<kKind>() * kUnitK / (R2 ? 1024 : (ABS ? 8 * T : T));  // loads per operand
+    static constexpr int DW = R2 ? (V + 1) / 2 : (ABS ? 4 : 1);                               // dwords per load
+    unsigned x[J][DW];  // fp32 bits (X_F32_RMS) or fp16 bits (X_F16_RMS, X_F16; the gate of X_RELU2_RMS / X_SILU_MUL)
+    unsigned u[UP ? J : 1][DW];  // up (X_RELU2_RMS, X_SILU_MUL)
+    unsigned g[ABS ? 1 : J][DW];  // gamma (fp16 bits; the RMS kinds)
 };
 
 template <int DW>
 __device__ __forceinline__ void load_halves(__amdgpu_buffer_rsrc_t r, int off, unsigned (&o)[DW]) {
-    if constexpr (DW == 2) {
+    if constexpr (DW == 4) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+        o[0] = v.x;
+        o[1] = v.y;
+        o[2] = v.z;
+        o[3] = v.w;
+    } else if constexpr (DW == 2) {
         typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
         const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
         o[0] = v.x;
@@ -802,6 +813,17 @@ __device__ __forceinline__ void x_prefetch_strided(const GemvDesc& d, XStrided<k
     constexpr int J = XS::J, T = XS::T;
     const int t = threadIdx.x;
     const __amdgpu_buffer_rsrc_t rx = vec_rsrc(d.x, d.K * kind_bytes(kKind));
+    if constexpr (XS::ABS) {
+        // (K is a multiple of 16: a vector is either inside K or reads as zeros)
+#pragma unroll
+        for (int j = 0; j < J; ++j) load_halves(rx, 2 * (8 * t + 8 * T * j), r.x[j]);
+        if constexpr (XS::UP) {
+            const __amdgpu_buffer_rsrc_t ru = vec_rsrc(d.up, d.K * 2);
+#pragma unroll
+            for (int j = 0; j < J; ++j) load_halves(ru, 2 * (8 * t + 8 * T * j), r.u[j]);
+        }
+        return;
+    }
     const __amdgpu_buffer_rsrc_t rg = vec_rsrc(d.gamma, d.K * 2);
     if constexpr (XS::R2) {
         // (a vector past K reads as zeros: K is a multiple of 16, so a vector
@@ -923,6 +945,76 @@ __device__ __forceinline__ float stage_x_strided(const GemvDesc& d, const XStrid
         halves_to_float(gw, g);
 #pragma unroll
         for (int i = 0; i < 16; ++i) v[i] = (v[i] * rms_inv) * g[i];
+        const u32x4 qv = pack_q16(v, scale);
+        *reinterpret_cast<u32x4*>(lds_x + c * 16) = qv;
+        const int su = row_sum16(sum_bytes(qv));
+        if (qd == 0) usum[u] = su;
+        if (owner && d.xq_out) {
+            const int k = c * 16;
+            const unsigned qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (k + i < K) gptr(d.xq_out)[k + i] = (int8_t)((qw[i >> 2] >> (8 * (i & 3))) & 0xFFu);
+        }
+    }
+    if (owner && t == 0 && d.xs_out) *gptr(d.xs_out) = act;
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    return act;
+}
+
+// Strided prologue of the absmax kinds in strip mode: X_F16 (quant_int8_k on
+// an fp16 vector, cuda/ter_cuda_forward_packed.cu:40-62) and X_SILU_MUL
+// (silu_mul_quant_k, :312-344).  Each thread turns the 8 t + 8 T j values it
+// loaded into fp32 (silu(gate) * up), writes them to LDS (xs32) and folds
+// their absmax; the wave maxima meet (one workgroup barrier, which also
+// publishes xs32); each wave quantizes only its own units [u0, u1), as in
+// stage_x_strided.  The maximum is order-free, so the results are stage_x's
+// bit for bit.  Needs Ku <= max_strided_ku and the fp32 staging; red: kW floats.
+template <int kKind, int kW>
+__device__ __forceinline__ float stage_x_abs_strided(const GemvDesc& d, const XStrided<kKind, kW>& r, int8_t* lds_x,
+                                                     int* usum, float* red, float* xs32, int u0, int u1, bool owner) {
+#pragma clang fp contract(off)
+    using XS = XStrided<kKind, kW>;
+    constexpr int J = XS::J, T = XS::T;
+    const int K = d.K, Ku = d.Ku;
+    const int t = threadIdx.x, lane = t & 63;
+    float mx = 0.f;  // zeros past K
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float x = half_bits_to_float((uint16_t)(r.x[j][e >> 1] >> (16 * (e & 1))));
+            if constexpr (kKind == TER_HIP_X_SILU_MUL)
+                v[e] = silu_mul(x, half_bits_to_float((uint16_t)(r.u[j][e >> 1] >> (16 * (e & 1)))));
+            else
+                v[e] = x;  // past K: silu(0) * 0 = 0
+            mx = fmaxf(mx, fabsf(v[e]));
+        }
+        const int i = 8 * t + 8 * T * j;
+        if (i < Ku * kUnitK) {  // the staged range (a multiple of 8)
+            *reinterpret_cast<f32x4*>(xs32 + i) = f32x4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<f32x4*>(xs32 + i + 4) = f32x4{v[4], v[5], v[6], v[7]};
+        }
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[t >> 6] = mx;
+    __syncthreads();
+    mx = red[0];
+#pragma unroll
+    for (int i = 1; i < kW; ++i) mx = fmaxf(mx, red[i]);
+    const float amax = mx + 1e-9f;
+    const float scale = 127.0f / amax;
+    const float act = 1.0f / scale;
+    const int row = lane >> 4, qd = lane & 15;
+    for (int u = u0 + row; u < u1; u += 4) {
+        const int c = u * 16 + qd;
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+            const f32x4 f = *reinterpret_cast<const f32x4*>(xs32 + c * 16 + i);
+            v[i] = f[0]; v[i + 1] = f[1]; v[i + 2] = f[2]; v[i + 3] = f[3];
+        }
         const u32x4 qv = pack_q16(v, scale);
         *reinterpret_cast<u32x4*>(lds_x + c * 16) = qv;
         const int su = row_sum16(sum_bytes(qv));
@@ -1452,7 +1544,11 @@ __global__ __launch_bounds__(64 * kW) void gemv_strip_kernel(GemvDesc single, co
         } else if constexpr (kStrided) {
             uint16_t* gs16 = reinterpret_cast<uint16_t*>(lds_raw + gemv_lds_slots_offset(d.K, true));
             float* red_s = reinterpret_cast<float*>(lds_raw + gemv_strip_red_offset(d.K));
-            act = stage_x_strided<kKind, kW>(d, xst, lds_x, usum, red_s, xs32, gs16, u0, u0 + nw, sg == d.strip0);
+            if constexpr (XStrided<kKind, kW>::ABS)
+                act = stage_x_abs_strided<kKind, kW>(d, xst, lds_x, usum, red_s, xs32, u0, u0 + nw, sg == d.strip0);
+            else
+                act = stage_x_strided<kKind, kW>(d, xst, lds_x, usum, red_s, xs32, gs16, u0, u0 + nw,
+                                                 sg == d.strip0);
         } else {
             act = stage_x_vec<kKind>(d, xraw, lds_x, usum, red, xs32, sg == d.strip0);
             __syncthreads();
@@ -1587,6 +1683,16 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_
                                grid, dim3(64 * strided_waves<TER_HIP_X_RELU2_RMS>()), lds_bytes, st, GemvDesc{},
                                list_dev, wg_desc_dev, total_strips, n_wg, part_off);
             return hipGetLastError();
+        case TER_HIP_X_F16:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F16, true, strided_waves<TER_HIP_X_F16>()>),
+                               grid, dim3(64 * strided_waves<TER_HIP_X_F16>()), lds_bytes, st, GemvDesc{},
+                               list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
+        case TER_HIP_X_SILU_MUL:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_SILU_MUL, true, strided_waves<TER_HIP_X_SILU_MUL>()>),
+                               grid, dim3(64 * strided_waves<TER_HIP_X_SILU_MUL>()), lds_bytes, st, GemvDesc{},
+                               list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
         default:
             return hipErrorInvalidValue;
         }
@@ -1620,7 +1726,12 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_
 }
 
 int gemv_strided_waves(int vec_kind) {
-    return vec_kind == TER_HIP_X_RELU2_RMS ? strided_waves<TER_HIP_X_RELU2_RMS>() : kGemvWaves;
+    switch (vec_kind) {
+    case TER_HIP_X_RELU2_RMS: return strided_waves<TER_HIP_X_RELU2_RMS>();
+    case TER_HIP_X_SILU_MUL: return strided_waves<TER_HIP_X_SILU_MUL>();
+    case TER_HIP_X_F16: return strided_waves<TER_HIP_X_F16>();
+    default: return kGemvWaves;
+    }
 }
 
 bool gemv_strided_ok(int vec_kind, int32_t K, bool stage32) {
@@ -1629,6 +1740,8 @@ bool gemv_strided_ok(int vec_kind, int32_t K, bool stage32) {
     case TER_HIP_X_F32_RMS: return stage32 && ku <= max_strided_ku<TER_HIP_X_F32_RMS>();
     case TER_HIP_X_F16_RMS: return stage32 && ku <= max_strided_ku<TER_HIP_X_F16_RMS>();
     case TER_HIP_X_RELU2_RMS: return stage32 && ku <= max_strided_ku<TER_HIP_X_RELU2_RMS>();
+    case TER_HIP_X_F16: return stage32 && ku <= max_strided_ku<TER_HIP_X_F16>();
+    case TER_HIP_X_SILU_MUL: return stage32 && ku <= max_strided_ku<TER_HIP_X_SILU_MUL>();
     default: return false;
     }
 }

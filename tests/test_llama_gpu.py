@@ -122,6 +122,39 @@ def test_gemv_resid16_epilogue(cuda, K, N, ws):
         assert np.isinf(want.astype(np.float32)).any()
 
 
+@pytest.mark.parametrize("kind,K,N", [("f16", 2048, 2048), ("f16", 4112, 256), ("f16", 777, 64),
+                                      ("silu", 8192, 2048), ("silu", 9000, 512), ("silu", 1000, 128),
+                                      ("silu", 512, 256)],
+                         ids=["f16-strided", "f16-beyond-strided", "f16-ragged", "silu-strided", "silu-beyond-strided",
+                              "silu-ragged", "silu-small"])
+def test_plan_absmax_prologues(cuda, kind, K, N):
+    """Work-list plans of the fp16 absmax kinds: the strided strip prologue
+    (K a multiple of 16 within its unit limit), and the general one past the
+    limit or for ragged K; the quantized copy from the plan's owner."""
+    import torch
+    import ter_amd as T
+    rng = np.random.default_rng(K * 7 + N)
+    x = (rng.standard_normal(K) * 0.7).astype(np.float16)
+    u = (rng.standard_normal(K) * 2.0).astype(np.float16)
+    v11, W = weight(K * 11 + N, K, N, 0.03)
+    q = torch.empty(K, dtype=torch.int8, device="cuda")
+    s = torch.empty(1, dtype=torch.float32, device="cuda")
+    y16 = torch.empty(N, dtype=torch.float16, device="cuda")
+    it = dict(w=W, x=dev(x), y16=y16, q_out=q, scale_out=s)
+    if kind == "silu":
+        it["up"] = dev(u)
+        rq, rs, _ = O.silu_mul_quant(x, u)
+    else:
+        rq, rs = O.quant_int8(x.astype(np.float32))
+    plan = T.Plan([it])
+    for _ in range(2):  # a relaunch sees the same inputs
+        plan.launch()
+        assert (host(q) == rq).all(), np.flatnonzero(host(q) != rq)[:8]
+        assert host(s)[0].view(np.int32) == np.float32(rs).view(np.int32)
+        assert_f16_equal(y16, O.gemv_v11(rq, rs, v11, 0.03, K, N)[1])
+    plan.close()
+
+
 # ---------------------------------------------------------------------------
 # One Llama layer's projection chain (:513-539)
 # ---------------------------------------------------------------------------
