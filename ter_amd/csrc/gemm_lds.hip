@@ -100,6 +100,10 @@ struct LCfg {
     // reads, but each quarter-wave's load spans four 256-byte runs instead of
     // one.  Measured on the BitNet-2B sweep: 2.8% faster at M = 128 (8 row
     // blocks, bound by LDS reads), 2.7% slower at M = 16 (bound by the loads).
+    // Without it the tiles keep their runs with the row groups XOR-swizzled
+    // (see issue_run), also conflict-free; from 4 row blocks on the transposed
+    // layout is still 1-3% faster (C4 M = 64 162.4 against 167.4 us, M = 128
+    // 259.3 against 262.4, M = 256 488.8 against 498.1).
 #ifndef TER_LDS_TW_MB
 #define TER_LDS_TW_MB 4
 #endif
@@ -250,11 +254,14 @@ __device__ __forceinline__ void issue_run(int r, int ldx, int Ku, int u, unsigne
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (TER_LDS void*)(stage + q * 1024), 16,
                                                  row * ldx + u * kUnitK + chunk * 16, 0, 0, 0);
     } else {
-        // tile (strip t of the block, unit u); with C::TW its 16-byte chunk
-        // (column quad cq, row group rq) at tile offset cq * 256 + rq * 16
-        // lands at LDS chunk 4 rq + cq (see compute_stage)
+        // tile (strip t of the block, unit u); its 16-byte chunk (column quad
+        // cq, row group rq) at tile offset cq * 256 + rq * 16 lands at LDS
+        // chunk 4 rq + cq with C::TW, else at chunk 16 cq + (rq ^ 4 cq) (each
+        // quarter-wave still loads one contiguous 256-byte run; see
+        // compute_stage)
         const int t = q - C::XI;
-        const int src = C::TW ? (lane & 3) * 256 + (lane >> 2) * 16 : lane * 16;
+        const int src = C::TW ? (lane & 3) * 256 + (lane >> 2) * 16
+                              : (lane >> 4) * 256 + ((lane & 15) ^ (4 * (lane >> 4))) * 16;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (TER_LDS void*)(stage + C::XB + t * 1024), 16,
                                                  (t * Ku + u) * kTileBytes + src, 0, 0, 2 /* nt */);
     }
@@ -319,9 +326,14 @@ __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg
         for (int s = 0; s < C::S; ++s) {
             // column j, rows (4 ks + g) * 16 .. +15: tile offset (j >> 2) * 256 +
             // (4 ks + g) * 16 + (j & 3) * 4.  With C::TW the load placed it at
-            // ks * 256 + lane * 4: the 64 lanes read 256 contiguous bytes, where
-            // in tile order four lanes share each bank.
-            const int off = C::TW ? ks * 256 + lane * 4 : (j >> 2) * 256 + (4 * ks + g) * 16 + (j & 3) * 4;
+            // ks * 256 + lane * 4: the 64 lanes read 256 contiguous bytes.
+            // Otherwise the row groups of column quad cq sit XOR-swizzled by
+            // 4 cq, so the four quads' dwords of one row group fall on
+            // different banks: the 64 lanes hit 64 banks, where in tile order
+            // four lanes shared each (C4 M = 16 99.0 -> 95.5 us, M = 32
+            // 120.0 -> 118.3 us; M = 8 unchanged).
+            const int off = C::TW ? ks * 256 + lane * 4
+                                  : (j >> 2) * 256 + ((4 * ks + g) ^ (4 * (j >> 2))) * 16 + (j & 3) * 4;
             dw[ks][s] = *reinterpret_cast<const unsigned*>(stage + C::XB + (sg * C::S + s) * kTileBytes + off);
         }
     auto a_at = [&](int t) {
