@@ -279,6 +279,16 @@ int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream);
 /* Algorithmic bytes (packed W + X + Y) and MACs of one launch of the plan. */
 int ter_hip_plan_stats(const ter_hip_plan_t* plan, uint64_t* bytes, uint64_t* macs,
                        int32_t* n_wg);
+/* How a GEMV plan runs (no counterpart in the reference; for tuning and
+ * tests): *mode = TER_HIP_PLAN_STRIPS (whole column strips per workgroup)
+ * | TER_HIP_PLAN_STRIDED (the strided prologue) | TER_HIP_PLAN_SHARED (one
+ * activation vector and back-to-back tile streams, e.g. weights grouped in
+ * one allocation in item order: the first loads need no descriptor); 0 for
+ * the stream-K partition and for GEMM plans. */
+#define TER_HIP_PLAN_STRIPS 1
+#define TER_HIP_PLAN_STRIDED 2
+#define TER_HIP_PLAN_SHARED 4
+int ter_hip_plan_mode(const ter_hip_plan_t* plan, int32_t* mode);
 void ter_hip_plan_destroy(ter_hip_plan_t* plan);
 
 /* ---------------------------------------------------------------------- */

@@ -16,6 +16,7 @@ from .fabric import (  # noqa: F401
     embed_f16,
     embed_h16,
     gemv,
+    group_contiguous,
     lm_head_argmax,
     lm_head_f16,
     mm_batched,

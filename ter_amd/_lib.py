@@ -40,6 +40,7 @@ X_RELU2_RMS = 4
 X_I16 = 5
 X_F16 = 6
 X_SILU_MUL = 7
+PLAN_STRIPS, PLAN_STRIDED, PLAN_SHARED = 1, 2, 4  # ter_hip_plan_mode flags
 SLOT_MATMUL = b"tk_matmul_t16"
 LAYOUT_T16 = 16
 ARGMAX_STATE_BYTES = 16512
@@ -170,6 +171,7 @@ SIGNATURES = [
     ("ter_hip_plan_create", C.c_int, [C.POINTER(C.c_void_p), C.POINTER(GemvItem), C.c_int32, C.c_int32]),
     ("ter_hip_plan_launch", C.c_int, [_P, _P]),
     ("ter_hip_plan_stats", C.c_int, [_P, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_int32)]),
+    ("ter_hip_plan_mode", C.c_int, [_P, C.POINTER(C.c_int32)]),
     ("ter_hip_plan_destroy", None, [_P]),
     ("ter_hip_gemm", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, _P, _P, _P]),
     ("ter_hip_gemm_out", C.c_int, [C.POINTER(WPK), C.POINTER(Act), C.c_int32, C.POINTER(Out), _P]),

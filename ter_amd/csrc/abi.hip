@@ -385,6 +385,8 @@ struct ter_hip_plan {
     bool strip_mode = false;     // GEMV: strip-mode kernel, total counts strips
     int part_off = 0;            // GEMV strip mode: LDS offset of the partial sums
     bool strided = false;        // GEMV strip mode: the strided RMS prologue (gemv_strided_ok for every item)
+    bool shared = false;         // GEMV strided strip mode: one activation, back-to-back tile streams
+    GemvDesc shared_desc{};      //   its kernel argument (shared_plan_desc)
     int mb = 0;                  // GEMM row-block count
     bool vec = false;            // GEMM: 16-byte X rows
     bool stream = false;         // GEMM: streaming kernel (M <= 16), total counts tiles
@@ -424,7 +426,7 @@ struct ter_hip_handle {
 // first unit, strictly increasing.
 template <typename Desc>
 int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<long long>& starts, long long total,
-                int n_wg, const std::vector<long long>* ranges = nullptr, bool wg_copies = false) {
+                int n_wg, const std::vector<long long>* ranges = nullptr, int wg_copies = 0) {
     std::vector<int32_t> first((size_t)n_wg);
     size_t di = 0;
     for (int g = 0; g < n_wg; ++g) {
@@ -435,11 +437,18 @@ int upload_plan(ter_hip_plan* p, const std::vector<Desc>& ds, const std::vector<
     const size_t db = sizeof(Desc) * ds.size();
     const size_t fb = (sizeof(int32_t) * (size_t)n_wg + 7) / 8 * 8;
     const size_t rb = ranges ? sizeof(long long) * ranges->size() : 0;
-    // wg_copies: then each workgroup's first descriptor once more, in workgroup order
+    // wg_copies 1: then each workgroup's first descriptor once more, in
+    // workgroup order; 2: its first and the next (the last one repeated), in
+    // block order (block b runs workgroup range (b % 8) (n_wg / 8) + b / 8
+    // when 8 divides n_wg, else b)
     const size_t cb0 = (db + fb + rb + 15) / 16 * 16;
     std::vector<Desc> copies;
-    if (wg_copies)
-        for (int g = 0; g < n_wg; ++g) copies.push_back(ds[(size_t)first[(size_t)g]]);
+    for (int b = 0; wg_copies > 0 && b < n_wg; ++b) {
+        const int g = wg_copies > 1 && n_wg % 8 == 0 ? (b % 8) * (n_wg / 8) + b / 8 : b;
+        const size_t f = (size_t)first[(size_t)g];
+        copies.push_back(ds[f]);
+        if (wg_copies > 1) copies.push_back(ds[f + 1 < ds.size() ? f + 1 : f]);
+    }
     const size_t cb = sizeof(Desc) * copies.size();
     hipError_t e = hipMalloc(&p->descs_dev, cb0 + cb);
     if (e != hipSuccess) {
@@ -976,6 +985,49 @@ int ter_hip_mm_row_blocked(const int32_t* X, int32_t row, int32_t K, float x_sca
     return TER_HIP_OK;
 }
 
+// A strided strip-mode list whose GEMVs all read one activation vector (same
+// pointers, kind, K, norm) with no quantized copies requested, whose tile
+// streams follow each other in memory in list order, and where no
+// workgroup's range spans more than two GEMVs: the descriptor the kernel
+// takes as its argument (the activation, the first stream's base, strip0 0,
+// the list's strip count).  Returns false for any other list.
+bool shared_plan_desc(const std::vector<GemvDesc>& ds, long long strips, int n_wg, GemvDesc* out) {
+    const GemvDesc& a = ds[0];
+    // every workgroup's strips [S g / n_wg, S (g + 1) / n_wg) within two GEMVs
+    size_t di = 0;
+    for (int g = 0; g < n_wg; ++g) {
+        const long long s0 = strips * g / n_wg, s1 = strips * (g + 1) / n_wg;
+        if (s0 >= s1) continue;
+        while (di + 1 < ds.size() && ds[di + 1].strip0 <= s0) ++di;
+        size_t dl = di;
+        while (dl + 1 < ds.size() && ds[dl + 1].strip0 <= s1 - 1) ++dl;
+        if (dl > di + 1) return false;
+    }
+    for (const GemvDesc& d : ds) {
+        if (d.x != a.x || d.x_kind != a.x_kind || d.up != a.up || d.gamma != a.gamma || d.eps != a.eps ||
+            d.K != a.K || d.Ku != a.Ku || d.stage32 != a.stage32 || d.xq_out || d.xs_out || d.x_scale_dev)
+            return false;
+        if (d.w != a.w + d.strip0 * (long long)a.Ku * kTileBytes) return false;
+    }
+    GemvDesc s{};
+    s.w = a.w;
+    s.x = a.x;
+    s.up = a.up;
+    s.gamma = a.gamma;
+    s.eps = a.eps;
+    s.K = a.K;
+    s.Ku = a.Ku;
+    s.N = a.N;
+    s.stage32 = a.stage32;
+    s.x_kind = a.x_kind;
+    s.x_scale = a.x_scale;
+    s.w_mag = a.w_mag;
+    s.strip0 = 0;
+    s.n_strips = (int32_t)strips;
+    *out = s;
+    return true;
+}
+
 int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items, int32_t n, int32_t wg_per_cu) {
     if (!plan || !items) return fail(TER_HIP_ERR_NULL, "null plan or items");
     *plan = nullptr;
@@ -1049,9 +1101,11 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     }
     ter_hip_plan* p = new (std::nothrow) ter_hip_plan();
     if (!p) return fail(TER_HIP_ERR_ALLOC, "plan allocation");
+    GemvDesc shared_desc{};
+    const bool shared = strip_mode && strided && shared_plan_desc(ds, strips, n_wg, &shared_desc);
     if (strip_mode) {
         for (size_t i = 0; i < ds.size(); ++i) ds[i].self = (int32_t)i;
-        rc = upload_plan(p, ds, strip_starts, strips, n_wg, nullptr, true);
+        rc = upload_plan(p, ds, strip_starts, strips, n_wg, nullptr, shared ? 2 : 1);
     } else {
         const std::vector<long long> ranges = plan_ranges(ds, starts, tile, n_wg);
         rc = upload_plan(p, ds, starts, tile, n_wg, &ranges);
@@ -1065,6 +1119,8 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
     p->strip_mode = strip_mode;
     p->part_off = part_off;
     p->strided = strip_mode && strided;
+    p->shared = shared;
+    p->shared_desc = shared_desc;
     p->n_wg = n_wg;
     p->lds_bytes = lds;
     p->vec_kind = vec_kind;
@@ -1095,13 +1151,21 @@ int ter_hip_plan_launch(const ter_hip_plan_t* plan, void* stream) {
             e = launch_gemv_strips(static_cast<const GemvDesc*>(plan->descs_dev),
                                    static_cast<const GemvDesc*>(plan->wg_desc_dev), plan->total,
                                    plan->n_wg, plan->lds_bytes, plan->part_off, plan->vec_kind, plan->strided,
-                                   static_cast<hipStream_t>(stream));
+                                   plan->shared ? &plan->shared_desc : nullptr, static_cast<hipStream_t>(stream));
         else
             e = launch_gemv(none, static_cast<const GemvDesc*>(plan->descs_dev), plan->first_dev,
                             plan->wg_ranges_dev, plan->total, plan->n_wg, plan->lds_bytes, plan->vec_kind,
                             static_cast<hipStream_t>(stream));
     }
     if (e != hipSuccess) return hip_fail(e, "plan launch");
+    return TER_HIP_OK;
+}
+
+int ter_hip_plan_mode(const ter_hip_plan_t* plan, int32_t* mode) {
+    if (!plan || !mode) return fail(TER_HIP_ERR_NULL, "null plan or mode");
+    *mode = plan->gemm ? 0
+                       : (plan->strip_mode ? TER_HIP_PLAN_STRIPS : 0) | (plan->strided ? TER_HIP_PLAN_STRIDED : 0) |
+                             (plan->shared ? TER_HIP_PLAN_SHARED : 0);
     return TER_HIP_OK;
 }
 

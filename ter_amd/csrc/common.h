@@ -93,8 +93,13 @@ struct alignas(16) GemmDesc {
 // strip stream ([total_strips] over the list) and reduce the waves' partials
 // in LDS at part_off; at most kStripModeMaxStrips strips per workgroup.
 constexpr int kStripModeMaxStrips = 32;
+// shared (strided lists only, else null): the activation every GEMV of the
+// list reads and the base of their back-to-back tile streams (w, strip0 0,
+// n_strips the list's), passed as the kernel argument so that the first
+// loads need no descriptor.
 hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_dev, long long total_strips, int n_wg,
-                              int lds_bytes, int part_off, int vec_kind, bool strided, hipStream_t st);
+                              int lds_bytes, int part_off, int vec_kind, bool strided, const GemvDesc* shared,
+                              hipStream_t st);
 // Whether a strip-mode list of this activation kind and K runs the strided
 // RMS prologue (gemv.hip: stage_x_strided).
 bool gemv_strided_ok(int vec_kind, int32_t K, bool stage32);

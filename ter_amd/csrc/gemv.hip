@@ -1474,15 +1474,42 @@ void gemv_t16_kernel(GemvDesc single,
 // strip's partial column sums in LDS, and after a barrier wave j % 4 adds the
 // four partials of strip j (integer sums, so the result is the stream-K
 // kernel's) and writes the outputs.  No fix-up slots, no global atomics.
-template <bool kList, int kKind, bool kStrided = false, int kW = kGemvWaves>
+template <bool kList, int kKind, bool kStrided = false, int kW = kGemvWaves, bool kShared = false>
 __global__ __launch_bounds__(64 * kW) void gemv_strip_kernel(GemvDesc single, const GemvDesc* __restrict__ list,
                                                                   const GemvDesc* __restrict__ wg_desc,
                                                                   long long total, int n_wg, int part_off) {
     extern __shared__ __align__(16) unsigned char lds_raw[];
-    int g = blockIdx.x;
-    if ((n_wg & 7) == 0) g = (g & 7) * (n_wg >> 3) + (g >> 3);  // keep neighbouring ranges on one XCD
-    const long long s_begin = total * g / n_wg;
-    const long long s_end = total * (g + 1) / n_wg;
+    const int b = blockIdx.x;
+    // kShared (strided lists): every GEMV of the list reads the one
+    // activation vector `single` describes, and their tile streams follow
+    // each other in memory from single.w (strip s at single.w + s Ku KiB).
+    // Then the activation and weight loads need nothing but the kernel
+    // arguments, and go out in the first round of loads after them, together
+    // with the workgroup's descriptors, which only the outputs wait for.
+    // The range is one segment; it spans at most two GEMVs, whose
+    // descriptors wg_desc holds per block index (2 b: the first, 2 b + 1:
+    // the next), so their loads need no argument but the table's address.
+    static_assert(!kShared || (kList && kStrided), "shared lists run the strided prologue");
+    GemvDesc e0{}, e1{};
+    if constexpr (kShared) {
+        e0 = wg_desc[2 * b];
+        e1 = wg_desc[2 * b + 1];
+        // every argument in one round of loads (an asm statement before the
+        // descriptor loads would make them vector loads)
+        asm volatile("" ::"s"(total), "s"(n_wg), "s"(single.w), "s"(single.x), "s"(single.gamma), "s"(single.up),
+                     "s"(single.K), "s"(single.Ku), "s"(single.eps), "s"(single.stage32), "s"(single.strip0));
+    }
+    const int g = (n_wg & 7) == 0 ? (b & 7) * (n_wg >> 3) + (b >> 3) : b;  // neighbouring ranges on one XCD
+    long long s_begin, s_end;
+    if (total < (1LL << 20) && n_wg <= (1 << 11)) {
+        // 32-bit division (a 64-bit one is about 150 scalar instructions)
+        const unsigned t = (unsigned)total, n = (unsigned)n_wg;
+        s_begin = t * (unsigned)g / n;
+        s_end = t * (unsigned)(g + 1) / n;
+    } else {
+        s_begin = total * g / n_wg;
+        s_end = total * (g + 1) / n_wg;
+    }
     if (s_begin >= s_end) return;
     int di = 0;
     const int wave = uniform(threadIdx.x >> 6);
@@ -1494,9 +1521,9 @@ __global__ __launch_bounds__(64 * kW) void gemv_strip_kernel(GemvDesc single, co
         // A plan's first segment reads the copy of its descriptor kept for
         // this workgroup (one round of loads instead of an index, then the
         // descriptor); later segments follow the list.
-        const GemvDesc d = kList ? *(sg == s_begin ? wg_desc + g : list + di) : single;
+        const GemvDesc d = kShared ? single : (kList ? *(sg == s_begin ? wg_desc + g : list + di) : single);
         if constexpr (kList) di = d.self;
-        const long long seg_end = min(s_end, d.strip0 + (long long)d.n_strips);
+        const long long seg_end = kShared ? s_end : min(s_end, d.strip0 + (long long)d.n_strips);
         const int sa = (int)(sg - d.strip0);  // first strip of the segment within the GEMV
         const int ns = (int)(seg_end - sg);
         static_assert(kW == kGemvWaves || kStrided, "other wave counts run the strided prologue only");
@@ -1532,6 +1559,13 @@ __global__ __launch_bounds__(64 * kW) void gemv_strip_kernel(GemvDesc single, co
             x_prefetch_vec<kKind>(d, xraw);
         u32x4 wa[NB], wb[NB];
         if (nw > 0) load_b(wa);
+        if constexpr (kShared) {
+            // the descriptors the outputs need, in flight with the activation
+            // and weight loads (left alone the compiler issues them at the
+            // outputs, one more round trip at the end)
+            asm volatile("" ::"s"(e0.y), "s"(e0.y16), "s"(e0.resid), "s"(e0.resid16), "s"(e0.acc),
+                         "s"(e1.y), "s"(e1.y16), "s"(e1.resid), "s"(e1.resid16), "s"(e1.acc));
+        }
         int8_t* lds_x = reinterpret_cast<int8_t*>(lds_raw);
         int* usum = reinterpret_cast<int*>(lds_raw + d.Ku * kUnitK);
         float* red = reinterpret_cast<float*>(lds_raw + d.Ku * kUnitK + d.Ku * 4);
@@ -1593,14 +1627,35 @@ __global__ __launch_bounds__(64 * kW) void gemv_strip_kernel(GemvDesc single, co
             }
         }
         __syncthreads();
-        for (int j = wave; j < ns; j += kW) {
-            const int col = (sa + j) * kStripCols + lane;
-            if (lane < 16 && col < d.N) {
-                const int* pj = part + j * kW * 16 + lane;
-                int v = pj[0];
+        if constexpr (kShared) {
+            // each strip's own GEMV: the workgroup's first or the next
+            auto emit_strip = [&](const GemvDesc& e, int j) {
+                const int col = (int)(sg + j - e.strip0) * kStripCols + lane;
+                if (lane < 16 && col < e.N) {
+                    const int* pj = part + j * kW * 16 + lane;
+                    int v = pj[0];
 #pragma unroll
-                for (int w = 1; w < kW; ++w) v += pj[16 * w];
-                emit(d, col, v, s);
+                    for (int w = 1; w < kW; ++w) v += pj[16 * w];
+                    emit(e, col, v, act * e.w_scale);
+                }
+            };
+            const long long b = e0.strip0 + (long long)e0.n_strips;
+            for (int j = wave; j < ns; j += kW) {
+                if (sg + j < b)
+                    emit_strip(e0, j);
+                else
+                    emit_strip(e1, j);
+            }
+        } else {
+            for (int j = wave; j < ns; j += kW) {
+                const int col = (sa + j) * kStripCols + lane;
+                if (lane < 16 && col < d.N) {
+                    const int* pj = part + j * kW * 16 + lane;
+                    int v = pj[0];
+#pragma unroll
+                    for (int w = 1; w < kW; ++w) v += pj[16 * w];
+                    emit(d, col, v, s);
+                }
             }
         }
         sg = seg_end;
@@ -1666,31 +1721,64 @@ hipError_t launch_gemv(const GemvDesc& single, const GemvDesc* list_dev, const i
 }
 
 hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_dev, long long total_strips, int n_wg,
-                              int lds_bytes, int part_off, int vec_kind, bool strided, hipStream_t st) {
+                              int lds_bytes, int part_off, int vec_kind, bool strided, const GemvDesc* shared,
+                              hipStream_t st) {
     const dim3 grid(n_wg), block(kGemvThreads);
+    if (strided && shared) {
+        switch (vec_kind) {
+        case TER_HIP_X_F32_RMS:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F32_RMS, true, kGemvWaves, true>), grid, block,
+                               lds_bytes, st, *shared, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
+        case TER_HIP_X_F16_RMS:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F16_RMS, true, kGemvWaves, true>), grid, block,
+                               lds_bytes, st, *shared, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
+        case TER_HIP_X_RELU2_RMS:
+            hipLaunchKernelGGL(
+                (gemv_strip_kernel<true, TER_HIP_X_RELU2_RMS, true, strided_waves<TER_HIP_X_RELU2_RMS>(), true>),
+                grid, dim3(64 * strided_waves<TER_HIP_X_RELU2_RMS>()), lds_bytes, st, *shared, list_dev, wg_desc_dev,
+                total_strips, n_wg, part_off);
+            return hipGetLastError();
+        case TER_HIP_X_F16:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F16, true, strided_waves<TER_HIP_X_F16>(), true>),
+                               grid, dim3(64 * strided_waves<TER_HIP_X_F16>()), lds_bytes, st, *shared, list_dev,
+                               wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
+        case TER_HIP_X_SILU_MUL:
+            hipLaunchKernelGGL(
+                (gemv_strip_kernel<true, TER_HIP_X_SILU_MUL, true, strided_waves<TER_HIP_X_SILU_MUL>(), true>),
+                grid, dim3(64 * strided_waves<TER_HIP_X_SILU_MUL>()), lds_bytes, st, *shared, list_dev, wg_desc_dev,
+                total_strips, n_wg, part_off);
+            return hipGetLastError();
+        default:
+            return hipErrorInvalidValue;
+        }
+    }
     if (strided) {
+        const GemvDesc sh{};
         switch (vec_kind) {
         case TER_HIP_X_F32_RMS:
             hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F32_RMS, true>), grid, block, lds_bytes, st,
-                               GemvDesc{}, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+                               sh, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
             return hipGetLastError();
         case TER_HIP_X_F16_RMS:
             hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F16_RMS, true>), grid, block, lds_bytes, st,
-                               GemvDesc{}, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+                               sh, list_dev, wg_desc_dev, total_strips, n_wg, part_off);
             return hipGetLastError();
         case TER_HIP_X_RELU2_RMS:
             hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_RELU2_RMS, true, strided_waves<TER_HIP_X_RELU2_RMS>()>),
-                               grid, dim3(64 * strided_waves<TER_HIP_X_RELU2_RMS>()), lds_bytes, st, GemvDesc{},
+                               grid, dim3(64 * strided_waves<TER_HIP_X_RELU2_RMS>()), lds_bytes, st, sh,
                                list_dev, wg_desc_dev, total_strips, n_wg, part_off);
             return hipGetLastError();
         case TER_HIP_X_F16:
             hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_F16, true, strided_waves<TER_HIP_X_F16>()>),
-                               grid, dim3(64 * strided_waves<TER_HIP_X_F16>()), lds_bytes, st, GemvDesc{},
+                               grid, dim3(64 * strided_waves<TER_HIP_X_F16>()), lds_bytes, st, sh,
                                list_dev, wg_desc_dev, total_strips, n_wg, part_off);
             return hipGetLastError();
         case TER_HIP_X_SILU_MUL:
             hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_SILU_MUL, true, strided_waves<TER_HIP_X_SILU_MUL>()>),
-                               grid, dim3(64 * strided_waves<TER_HIP_X_SILU_MUL>()), lds_bytes, st, GemvDesc{},
+                               grid, dim3(64 * strided_waves<TER_HIP_X_SILU_MUL>()), lds_bytes, st, sh,
                                list_dev, wg_desc_dev, total_strips, n_wg, part_off);
             return hipGetLastError();
         default:

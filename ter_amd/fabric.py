@@ -122,6 +122,40 @@ class PackedTrits:
         return out
 
 
+def group_contiguous(ws: Sequence[PackedTrits]) -> List[PackedTrits]:
+    """The weights `ws` (one K) copied into one device allocation, their tile
+    streams back to back in the given order and their fix-up slots after all
+    of them; returns views into it (same shapes, scales and magnitudes).  A
+    strip-mode plan whose items read one activation vector and whose weights
+    are such a group, in the same order, starts its activation and weight
+    loads from the launch's arguments instead of waiting for its descriptors
+    (the decode steps group each layer's Q/K/V and gate/up this way)."""
+    torch = _torch()
+    if not ws or len({w.K for w in ws}) != 1:
+        raise ValueError("group_contiguous needs weights of one K")
+    lib = L.lib()
+    stream_b = [int(lib.ter_hip_wpk_bytes(w.K, w.N)) - 8 * w.N for w in ws]
+    total = sum(stream_b) + sum(8 * w.N for w in ws)
+    buf = torch.empty(total, dtype=torch.uint8, device=ws[0].buf.device)
+    out = []
+    off, foff = 0, sum(stream_b)
+    for w, sb in zip(ws, stream_b):
+        buf[off:off + sb].copy_(w.buf[:sb])
+        buf[foff:foff + 8 * w.N].zero_()  # fix-up slots, zero at rest
+        v = PackedTrits.__new__(PackedTrits)
+        v.K, v.N, v.buf = w.K, w.N, buf
+        v.wpk = L.WPK()
+        v.wpk.data = buf.data_ptr() + off
+        v.wpk.bytes = lib.ter_hip_wpk_bytes(w.K, w.N)
+        v.wpk.fix = buf.data_ptr() + foff
+        v.wpk.K, v.wpk.N, v.wpk.scale = w.K, w.N, w.scale
+        v.wpk.layout, v.wpk.mag = w.wpk.layout, w.wpk.mag
+        out.append(v)
+        off += sb
+        foff += 8 * w.N
+    return out
+
+
 def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=None, eps=1e-5, up=None) -> L.Act:
     torch = _torch()
     a = L.Act()
@@ -538,6 +572,9 @@ class Plan:
         b, m, g = C.c_uint64(), C.c_uint64(), C.c_int32()
         L.check(L.lib().ter_hip_plan_stats(self._h, C.byref(b), C.byref(m), C.byref(g)), "ter_hip_plan_stats")
         self.bytes, self.macs, self.n_wg = b.value, m.value, g.value
+        md = C.c_int32()
+        L.check(L.lib().ter_hip_plan_mode(self._h, C.byref(md)), "ter_hip_plan_mode")
+        self.mode = md.value  # TER_HIP_PLAN_* flags
 
     def launch(self, stream=None):
         L.check(L.lib().ter_hip_plan_launch(self._h, _stream(stream)), "ter_hip_plan_launch")

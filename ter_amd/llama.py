@@ -149,6 +149,11 @@ class Decoder:
         self.plans = []
         for lay in model.layers:
             W = lay.W
+            # Q/K/V and gate/up as one allocation each (views replace the
+            # model's weights): their plans then load the activation and the
+            # weights from the launch's arguments (fabric.group_contiguous)
+            W["Wq"], W["Wk"], W["Wv"] = F.group_contiguous([W["Wq"], W["Wk"], W["Wv"]])
+            W["Wgate"], W["Wup"] = F.group_contiguous([W["Wgate"], W["Wup"]])
             qkv = F.Plan([dict(w=W["Wq"], x=self.hidden, gamma=lay.attn_norm, eps=c.eps, y16=self.q),
                           dict(w=W["Wk"], x=self.hidden, gamma=lay.attn_norm, eps=c.eps, y16=self.k),
                           dict(w=W["Wv"], x=self.hidden, gamma=lay.attn_norm, eps=c.eps, y16=self.v)])

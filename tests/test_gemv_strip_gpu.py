@@ -101,3 +101,63 @@ def test_decode_shaped_lists(cuda):
     run_list([(2560, 6912), (2560, 6912)], seed=15, fp32=True)
     run_list([(6912, 2560)], seed=14)
     run_list([(2560, 8448), (2560, 8448)], seed=16)
+
+
+@pytest.mark.parametrize("kind", ["f32-rms", "f16-rms", "relu2", "f16", "silu"])
+@pytest.mark.parametrize("order", ["grouped", "reordered"])
+def test_shared_activation_plans(cuda, kind, order):
+    """Strided strip-mode lists whose GEMVs read one activation vector: with
+    the weights grouped in one allocation in item order (fabric.group_contiguous)
+    the plan takes the activation and weight streams from the launch's
+    arguments (TER_HIP_PLAN_SHARED), workgroup ranges crossing GEMV
+    boundaries included; listed in another order it runs the per-segment
+    path.  Outputs, fp16 copies and accumulators bit-exact either way, over
+    two launches."""
+    import torch
+    import ter_amd as T
+    from ter_amd import _lib as L
+    K = {"f32-rms": 2560, "f16-rms": 2048, "relu2": 6912, "f16": 2048, "silu": 8192}[kind]
+    Ns = [4000, 48, 2000] if kind in ("f32-rms", "f16-rms") else [1024, 528]
+    rng = np.random.default_rng(K + len(Ns))
+    gm = rng.uniform(0.5, 1.5, K).astype(np.float16)
+    if kind == "f32-rms":
+        x = (rng.standard_normal(K) * 3).astype(np.float32)
+    else:
+        x = (rng.standard_normal(K) * 1.5).astype(np.float16)
+    up = (rng.standard_normal(K) * 1.5).astype(np.float16)
+    if kind in ("f32-rms", "f16-rms"):
+        rq, rs, _ = O.rmsnorm_quant(x, gm, 1e-5)
+    elif kind == "relu2":
+        rq, rs, _ = O.relu2_rmsnorm_quant(x, up, gm, 1e-5)
+    elif kind == "f16":
+        rq, rs = O.quant_int8(x.astype(np.float32))
+    else:
+        rq, rs, _ = O.silu_mul_quant(x, up)
+    v11s = [O.v11_pack(O.rand_trits(K * 3 + 7 * i, K, N, 0.4)) for i, N in enumerate(Ns)]
+    Ws = [T.PackedTrits.from_v11(v, K, N, 0.01 * (i + 1)) for i, (v, N) in enumerate(zip(v11s, Ns))]
+    Ws = T.group_contiguous(Ws)
+    idx = list(range(len(Ns))) if order == "grouped" else list(range(len(Ns)))[::-1]
+    dx, dg, du = dev(x), dev(gm), dev(up)
+    items = []
+    for i in idx:
+        it = dict(w=Ws[i], x=dx, y=torch.empty(Ns[i], dtype=torch.float32, device="cuda"),
+                  acc=torch.empty(Ns[i], dtype=torch.int32, device="cuda"),
+                  y16=torch.empty(Ns[i], dtype=torch.float16, device="cuda"))
+        if kind in ("f32-rms", "f16-rms", "relu2"):
+            it.update(gamma=dg, eps=1e-5)
+        if kind in ("relu2", "silu"):
+            it["up"] = du
+        items.append(it)
+    plan = T.Plan(items)
+    assert plan.mode & L.PLAN_STRIPS and plan.mode & L.PLAN_STRIDED, plan.mode
+    assert bool(plan.mode & L.PLAN_SHARED) == (order == "grouped" or len(Ns) == 1), plan.mode
+    for rep in range(2):
+        for it in items:
+            it["acc"].fill_(-7)
+        plan.launch()
+        for i, it in zip(idx, items):
+            ra, ry = O.gemv_v11(rq, rs, v11s[i], 0.01 * (i + 1), K, Ns[i])
+            assert (host(it["acc"]) == ra).all(), (rep, i)
+            assert (host(it["y"]).view(np.int32) == ry.view(np.int32)).all(), (rep, i)
+            assert (host(it["y16"]).view(np.uint16) == O.float_to_half_bits(ry)).all(), (rep, i)
+    plan.close()
