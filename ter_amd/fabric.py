@@ -123,16 +123,17 @@ class PackedTrits:
 
 
 def group_contiguous(ws: Sequence[PackedTrits]) -> List[PackedTrits]:
-    """The weights `ws` (one K) copied into one device allocation, their tile
-    streams back to back in the given order and their fix-up slots after all
-    of them; returns views into it (same shapes, scales and magnitudes).  A
-    strip-mode plan whose items read one activation vector and whose weights
+    """The weights `ws` copied into one device allocation, their tile streams
+    back to back in the given order and their fix-up slots after all of them;
+    returns views into it (same shapes, scales and magnitudes).  A strip-mode
+    plan whose items read one activation vector (so one K) and whose weights
     are such a group, in the same order, starts its activation and weight
     loads from the launch's arguments instead of waiting for its descriptors
-    (the decode steps group each layer's Q/K/V and gate/up this way)."""
+    (the decode steps group each layer's Q/K/V and gate/up this way); a
+    stream-K plan over such a group reads one contiguous weight stream."""
     torch = _torch()
-    if not ws or len({w.K for w in ws}) != 1:
-        raise ValueError("group_contiguous needs weights of one K")
+    if not ws:
+        raise ValueError("group_contiguous needs at least one weight")
     lib = L.lib()
     stream_b = [int(lib.ter_hip_wpk_bytes(w.K, w.N)) - 8 * w.N for w in ws]
     total = sum(stream_b) + sum(8 * w.N for w in ws)
