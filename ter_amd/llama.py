@@ -146,14 +146,17 @@ class Decoder:
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.argmax = F.ArgmaxState(dev)
         self.attn = F.Attention(c.Nh, c.Nkv, c.Hd, s_max, c.rope_theta, neox=False)
+        # every projection of the model in one allocation, each layer's in
+        # the order Q, K, V, O, gate, up, down (views replace the model's
+        # weights): the Q/K/V and gate/up plans then load the activation and
+        # the weights from the launch's arguments (fabric.group_contiguous)
+        order = [(lay.W, nm) for lay in model.layers for nm in PROJ]
+        for (W, nm), w in zip(order, F.group_contiguous([W[nm] for W, nm in order])):
+            W[nm] = w
+        del order
         self.plans = []
         for lay in model.layers:
             W = lay.W
-            # Q/K/V and gate/up as one allocation each (views replace the
-            # model's weights): their plans then load the activation and the
-            # weights from the launch's arguments (fabric.group_contiguous)
-            W["Wq"], W["Wk"], W["Wv"] = F.group_contiguous([W["Wq"], W["Wk"], W["Wv"]])
-            W["Wgate"], W["Wup"] = F.group_contiguous([W["Wgate"], W["Wup"]])
             qkv = F.Plan([dict(w=W["Wq"], x=self.hidden, gamma=lay.attn_norm, eps=c.eps, y16=self.q),
                           dict(w=W["Wk"], x=self.hidden, gamma=lay.attn_norm, eps=c.eps, y16=self.k),
                           dict(w=W["Wv"], x=self.hidden, gamma=lay.attn_norm, eps=c.eps, y16=self.v)])
