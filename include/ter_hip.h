@@ -84,6 +84,14 @@ extern "C" {
  * TER_HIP_X_F16 and TER_HIP_X_SILU_MUL are single GEMVs and work lists
  * only; batched GEMMs refuse them (TER_HIP_ERR_PAYLOAD). */
 #define TER_HIP_X_SILU_MUL 7
+/* The second half of silu_mul_quant_k (cuda/ter_cuda_forward_packed.cu:325-343):
+ * `data` is fp32 silu(gate) [K], as the gate GEMV's `silu` output writes it
+ * (ter_hip_out_t), `up` the fp16 up projection [K]; v = data * float(up),
+ * then absmax -> int8.  With the gate GEMV's silu output this is
+ * TER_HIP_X_SILU_MUL bit for bit, with the exp computed once per element
+ * instead of in every workgroup of the down projection.  Single GEMVs and
+ * work lists only, like TER_HIP_X_SILU_MUL. */
+#define TER_HIP_X_SMUL 8
 
 /*
  * Packed ternary weight (replaces WPK, cuda/ter_cuda_forward_packed.cu:400).
@@ -144,13 +152,19 @@ typedef struct ter_hip_act {
  *         + float(half(y))), the projection followed by add_k into the Llama
  *         forward's fp16 residual stream (cuda/ter_cuda_forward_packed.cu:115-118,
  *         :538, :548); the same rule as resid.  GEMVs and GEMV work lists
- *         only: the batched GEMMs refuse it (TER_HIP_ERR_PAYLOAD). */
+ *         only: the batched GEMMs refuse it (TER_HIP_ERR_PAYLOAD).
+ *   silu  fp32 [N] = h / (1 + exp(-h)), h = float(half(y)): the gate
+ *         projection's fp16 output taken through the first half of
+ *         silu_mul_quant_k (cuda/ter_cuda_forward_packed.cu:322-324, this
+ *         build's exp), for the TER_HIP_X_SMUL activation of the down
+ *         projection.  GEMVs and GEMV work lists only, like resid16. */
 typedef struct ter_hip_out {
     float*    y;
     int32_t*  acc;
     uint16_t* y16;
     float*    resid;
     uint16_t* resid16;
+    float*    silu;
 } ter_hip_out_t;
 
 /* ---------------------------------------------------------------------- */
@@ -261,6 +275,7 @@ typedef struct ter_hip_gemv_item {
     uint16_t*            y16;  /* fp16 [N] or NULL (ter_hip_out_t)            */
     float*               resid;/* fp32 [N] residual, += half(y), or NULL      */
     uint16_t*            resid16; /* fp16 [N] residual, += half(y), or NULL   */
+    float*               silu; /* fp32 [N] silu(half(y)) or NULL (ter_hip_out_t) */
 } ter_hip_gemv_item_t;
 
 typedef struct ter_hip_plan ter_hip_plan_t;
@@ -341,6 +356,7 @@ typedef struct ter_hip_gemm_item {
     uint16_t*            y16;          /* fp16 [M][N] or NULL                */
     float*               resid;        /* fp32 [M][N] residual or NULL       */
     uint16_t*            resid16;      /* NULL: fp16 residuals are GEMV-only */
+    float*               silu;         /* NULL: the silu output is GEMV-only */
 } ter_hip_gemm_item_t;
 
 int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* items, int32_t n,

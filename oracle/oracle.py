@@ -74,6 +74,10 @@ def lib():
         L.orc_silu_mul.restype = C.c_float
         L.orc_silu_mul_quant.argtypes = [_P, _P, C.c_int, _P, _P, _P]
         L.orc_silu_mul_quant.restype = None
+        L.orc_silu_f16.argtypes = [_P, C.c_int, _P]
+        L.orc_silu_f16.restype = None
+        L.orc_smul_quant.argtypes = [_P, _P, C.c_int, _P, _P, _P]
+        L.orc_smul_quant.restype = None
         L.orc_rmsnorm_f16.argtypes = [_P, _P, C.c_int, C.c_float, _P, _P]
         L.orc_rmsnorm_f16.restype = None
         L.orc_lm_head_f16.argtypes = [_P, _P, C.c_int, C.c_int, _P, _P]
@@ -348,6 +352,28 @@ def silu_mul_quant(gate: np.ndarray, up: np.ndarray):
     v = np.empty(F, dtype=np.float32)
     lib().orc_silu_mul_quant(_ptr(g), _ptr(u), F, _ptr(q), _ptr(s), _ptr(v))
     return q, s[0], v
+
+
+def silu_f16(gate: np.ndarray) -> np.ndarray:
+    """The first step of silu_mul_quant_k (cuda/ter_cuda_forward_packed.cu:322-324)
+    alone: fp16 gate [F] -> fp32 g / (1 + expf(-g))."""
+    g = np.ascontiguousarray(gate, dtype=np.float16)
+    out = np.empty(g.size, dtype=np.float32)
+    lib().orc_silu_f16(_ptr(g), g.size, _ptr(out))
+    return out
+
+
+def smul_quant(s: np.ndarray, up: np.ndarray):
+    """The rest of silu_mul_quant_k (:325-343): fp32 silu(gate) [F] times fp16
+    up [F] -> (int8 [F], act_scale, fp32 products [F])."""
+    ss = np.ascontiguousarray(s, dtype=np.float32)
+    u = np.ascontiguousarray(up, dtype=np.float16)
+    F = ss.size
+    q = np.empty(F, dtype=np.int8)
+    sc = np.zeros(1, dtype=np.float32)
+    v = np.empty(F, dtype=np.float32)
+    lib().orc_smul_quant(_ptr(ss), _ptr(u), F, _ptr(q), _ptr(sc), _ptr(v))
+    return q, sc[0], v
 
 
 def rmsnorm_f16(x: np.ndarray, gamma: np.ndarray, eps: float = 1e-5):

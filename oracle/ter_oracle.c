@@ -42,6 +42,9 @@
  *   orc_residual_add_f16                 -- orc_float_to_half / orc_half_to_float.
  *   orc_residual_add_h16                 -- numpy's binary16 addition (one correctly
  *                                           rounded add) of hidden and half(y).
+ *   orc_silu_f16 / orc_smul_quant        -- equal to orc_silu_mul_quant taken in one
+ *                                           step (the split route), silu(g) equal to
+ *                                           orc_silu_mul(g, 1).
  *   orc_silu_mul / orc_silu_mul_quant    -- closed forms (g = 0 or u = 0 gives 0,
  *                                           large g gives g * u exactly, very
  *                                           negative g gives 0), float64
@@ -528,6 +531,28 @@ float orc_silu_mul(uint16_t g16, uint16_t u16) {
     const float d = 1.0f + orc_expf(-g);
     const float sg = g / d;
     return sg * u;
+}
+
+/* The same computation split in two, as the fabric's TER_HIP_X_SMUL route
+ * runs it: orc_silu_f16 is the first step alone, silu(g) = g / (1 + expf(-g))
+ * of each fp16 gate value; orc_smul_quant multiplies that fp32 value by the
+ * fp16 up value and quantizes.  smul_quant(silu(g), u) is silu_mul_quant(g, u)
+ * bit for bit (the same two rounded operations in the same order). */
+void orc_silu_f16(const uint16_t* gate, int n, float* out) {
+    for (int i = 0; i < n; ++i) {
+        const float g = orc_half_to_float(gate[i]);
+        const float d = 1.0f + orc_expf(-g);
+        out[i] = g / d;
+    }
+}
+
+void orc_smul_quant(const float* s, const uint16_t* up, int F, int8_t* q, float* act_scale, float* v_out) {
+    float* v = (float*)malloc(sizeof(float) * (size_t)(F > 0 ? F : 1));
+    if (!v) return;
+    for (int i = 0; i < F; ++i) v[i] = s[i] * orc_half_to_float(up[i]);
+    orc_quant_int8(v, F, q, act_scale);
+    if (v_out) memcpy(v_out, v, sizeof(float) * (size_t)F);
+    free(v);
 }
 
 void orc_silu_mul_quant(const uint16_t* gate, const uint16_t* up, int F, int8_t* q, float* act_scale, float* v_out) {

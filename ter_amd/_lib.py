@@ -40,6 +40,7 @@ X_RELU2_RMS = 4
 X_I16 = 5
 X_F16 = 6
 X_SILU_MUL = 7
+X_SMUL = 8
 PLAN_STRIPS, PLAN_STRIDED, PLAN_SHARED = 1, 2, 4  # ter_hip_plan_mode flags
 SLOT_MATMUL = b"tk_matmul_t16"
 LAYOUT_T16 = 16
@@ -89,6 +90,7 @@ class Out(C.Structure):
         ("y16", C.c_void_p),
         ("resid", C.c_void_p),
         ("resid16", C.c_void_p),
+        ("silu", C.c_void_p),
     ]
 
 
@@ -101,6 +103,7 @@ class GemvItem(C.Structure):
         ("y16", C.c_void_p),
         ("resid", C.c_void_p),
         ("resid16", C.c_void_p),
+        ("silu", C.c_void_p),
     ]
 
 
@@ -115,6 +118,7 @@ class GemmItem(C.Structure):
         ("y16", C.c_void_p),
         ("resid", C.c_void_p),
         ("resid16", C.c_void_p),
+        ("silu", C.c_void_p),
     ]
 
 

@@ -59,12 +59,19 @@ bool is_rms(int kind) {
 // Kinds whose GEMV descriptor stages fp32 activations in LDS where K allows:
 // the RMS kinds (their sum of squares reads them) and the fp16 absmax kinds
 // (the strided strip prologue quantizes from them).
-bool stages32(int kind) { return is_rms(kind) || kind == TER_HIP_X_F16 || kind == TER_HIP_X_SILU_MUL; }
+bool stages32(int kind) {
+    return is_rms(kind) || kind == TER_HIP_X_F16 || kind == TER_HIP_X_SILU_MUL || kind == TER_HIP_X_SMUL;
+}
+
+// The gated kinds: `up` multiplies the activation.
+bool gated(int kind) {
+    return kind == TER_HIP_X_RELU2_RMS || kind == TER_HIP_X_SILU_MUL || kind == TER_HIP_X_SMUL;
+}
 
 // Kinds whose prologue runs only inside the GEMV kernels (no batched row
 // quantizer): int16 rows, the fp16 absmax and the silu(gate) * up kinds.
 bool gemv_only_kind(int kind) {
-    return kind == TER_HIP_X_I16 || kind == TER_HIP_X_F16 || kind == TER_HIP_X_SILU_MUL;
+    return kind == TER_HIP_X_I16 || kind == TER_HIP_X_F16 || kind == TER_HIP_X_SILU_MUL || kind == TER_HIP_X_SMUL;
 }
 
 int check_act(const ter_hip_act_t* x, int M) {
@@ -75,13 +82,14 @@ int check_act(const ter_hip_act_t* x, int M) {
         return fail(TER_HIP_ERR_PAYLOAD, "activation kind %d runs as single GEMVs and GEMV work lists only (M=%d)",
                     x->kind, M);
     if (x->kind == TER_HIP_X_I16 && !aligned(x->data, 2)) return fail(TER_HIP_ERR_ALIGN, "int16 X misaligned");
-    if ((x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS) && !aligned(x->data, 4))
+    if ((x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS || x->kind == TER_HIP_X_SMUL) &&
+        !aligned(x->data, 4))
         return fail(TER_HIP_ERR_ALIGN, "fp32 X misaligned");
     if ((x->kind == TER_HIP_X_F16_RMS || x->kind == TER_HIP_X_RELU2_RMS || x->kind == TER_HIP_X_F16 ||
          x->kind == TER_HIP_X_SILU_MUL) &&
         !aligned(x->data, 2))
         return fail(TER_HIP_ERR_ALIGN, "fp16 X misaligned");
-    if (x->kind == TER_HIP_X_RELU2_RMS || x->kind == TER_HIP_X_SILU_MUL) {
+    if (gated(x->kind)) {
         if (!x->up) return fail(TER_HIP_ERR_NULL, "gated activation without up");
         if (!aligned(x->up, 2)) return fail(TER_HIP_ERR_ALIGN, "fp16 up misaligned");
     }
@@ -96,10 +104,10 @@ int check_act(const ter_hip_act_t* x, int M) {
 }
 
 int check_out(const ter_hip_out_t* o) {
-    if (!o || (!o->y && !o->acc && !o->y16 && !o->resid && !o->resid16))
+    if (!o || (!o->y && !o->acc && !o->y16 && !o->resid && !o->resid16 && !o->silu))
         return fail(TER_HIP_ERR_NULL, "no output buffer");
     if (!aligned(o->y, 4) || !aligned(o->acc, 4) || !aligned(o->y16, 2) || !aligned(o->resid, 4) ||
-        !aligned(o->resid16, 2))
+        !aligned(o->resid16, 2) || !aligned(o->silu, 4))
         return fail(TER_HIP_ERR_ALIGN, "output buffer misaligned");
     return TER_HIP_OK;
 }
@@ -115,11 +123,13 @@ unsigned act_bytes(int kind) {
         case TER_HIP_X_I16: return 2;
         case TER_HIP_X_F16: return 2;
         case TER_HIP_X_SILU_MUL: return 4;
+        case TER_HIP_X_SMUL: return 6;
         default: return 1;
     }
 }
 unsigned out_bytes(const ter_hip_out_t& o) {
-    return (o.y ? 4u : 0u) + (o.acc ? 4u : 0u) + (o.y16 ? 2u : 0u) + (o.resid ? 8u : 0u) + (o.resid16 ? 4u : 0u);
+    return (o.y ? 4u : 0u) + (o.acc ? 4u : 0u) + (o.y16 ? 2u : 0u) + (o.resid ? 8u : 0u) + (o.resid16 ? 4u : 0u) +
+           (o.silu ? 4u : 0u);
 }
 
 typedef std::vector<std::pair<uintptr_t, uintptr_t>> Ranges;
@@ -131,9 +141,13 @@ bool overlaps(const std::pair<uintptr_t, uintptr_t>& a, const std::pair<uintptr_
 // Device byte ranges an activation operand reads (M rows of K elements).
 void act_ranges(const ter_hip_act_t* x, int M, int K, Ranges* out) {
     const size_t n = (size_t)M * (size_t)K;
-    const size_t el = x->kind == TER_HIP_X_I8 ? 1 : (x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS ? 4 : 2);  // I16, fp16: 2
+    const size_t el = x->kind == TER_HIP_X_I8
+                          ? 1
+                          : (x->kind == TER_HIP_X_F32 || x->kind == TER_HIP_X_F32_RMS || x->kind == TER_HIP_X_SMUL
+                                 ? 4
+                                 : 2);  // I16, fp16: 2
     out->emplace_back((uintptr_t)x->data, (uintptr_t)x->data + n * el);
-    if ((x->kind == TER_HIP_X_RELU2_RMS || x->kind == TER_HIP_X_SILU_MUL) && x->up)
+    if (gated(x->kind) && x->up)
         out->emplace_back((uintptr_t)x->up, (uintptr_t)(x->up + n));
 }
 
@@ -166,11 +180,12 @@ GemvDesc make_desc(const ter_hip_wpk_t* w, const ter_hip_act_t* x, const ter_hip
     d.y16 = o.y16;
     d.resid = o.resid;
     d.resid16 = o.resid16;
+    d.silu = o.silu;
     const bool quantized = x->kind != TER_HIP_X_I8 && x->kind != TER_HIP_X_I16;
     d.xq_out = quantized ? x->q_out : nullptr;
     d.xs_out = quantized ? x->scale_out : nullptr;
     d.gamma = is_rms(x->kind) ? x->gamma : nullptr;
-    d.up = x->kind == TER_HIP_X_RELU2_RMS || x->kind == TER_HIP_X_SILU_MUL ? x->up : nullptr;
+    d.up = gated(x->kind) ? x->up : nullptr;
     d.eps = x->eps;
     d.fix = reinterpret_cast<unsigned long long*>(w->fix);
     d.tile0 = tile0;
@@ -221,7 +236,7 @@ int gemv_vec_kind(const ter_hip_gemv_item_t* items, int n) {
         if (x.kind != kind || items[i].w->K % 16 != 0 || !a16(x.data)) return -1;
         if (x.kind == TER_HIP_X_I16) return -1;  // the general prologue
         if (stages32(x.kind) && !gemv_stage32(items[i].w->K)) return -1;  // the vector prologues always stage
-        if ((x.kind == TER_HIP_X_RELU2_RMS || x.kind == TER_HIP_X_SILU_MUL) && !a16(x.up)) return -1;
+        if (gated(x.kind) && !a16(x.up)) return -1;
         if (is_rms(x.kind) && !a16(x.gamma)) return -1;
     }
     return kind;
@@ -312,7 +327,8 @@ bool ring_rows_ok(const int8_t* x, int K) { return aligned(x, 16) && K % 16 == 0
 ter_hip_out_t out_rows(const ter_hip_out_t& o, int r0, int N) {
     const size_t off = (size_t)r0 * (size_t)N;
     return ter_hip_out_t{o.y ? o.y + off : nullptr, o.acc ? o.acc + off : nullptr, o.y16 ? o.y16 + off : nullptr,
-                         o.resid ? o.resid + off : nullptr, o.resid16 ? o.resid16 + off : nullptr};
+                         o.resid ? o.resid + off : nullptr, o.resid16 ? o.resid16 + off : nullptr,
+                         o.silu ? o.silu + off : nullptr};
 }
 
 // GEMM workgroups: up to kGemmWgPerCu per CU (more weight bytes in flight
@@ -1047,7 +1063,7 @@ int ter_hip_plan_create(ter_hip_plan_t** plan, const ter_hip_gemv_item_t* items,
         if (rc) return rc;
         if (it.x.kind == TER_HIP_X_I16)
             return fail(TER_HIP_ERR_PAYLOAD, "item %d: int16 activations run as single GEMVs only", i);
-        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid, it.resid16};
+        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid, it.resid16, it.silu};
         rc = check_out(&o);
         if (rc) return rc;
         for (int k = 0; k < i; ++k)
@@ -1239,6 +1255,7 @@ static int gemm_out_ws(const ter_hip_wpk_t* w, const ter_hip_act_t* x, int32_t M
     rc = check_out(out);
     if (rc) return rc;
     if (out->resid16) return fail(TER_HIP_ERR_PAYLOAD, "fp16 residual outputs: GEMVs only");
+    if (out->silu) return fail(TER_HIP_ERR_PAYLOAD, "silu outputs: GEMVs only");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int8_t* xq = static_cast<const int8_t*>(x->data);
     const float* xs = x->scale_dev;
@@ -1348,10 +1365,11 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
         if (!it.x || !it.x_scale_dev) return fail(TER_HIP_ERR_NULL, "item %d: null X or X scales", i);
         if (it.M < 1 || it.M > TER_HIP_M_MAX)
             return fail(TER_HIP_ERR_SHAPE, "item %d: M=%d out of range [1,%d]", i, it.M, TER_HIP_M_MAX);
-        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid, nullptr};
+        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid, nullptr, nullptr};
         rc = check_out(&o);
         if (rc) return rc;
         if (it.resid16) return fail(TER_HIP_ERR_PAYLOAD, "item %d: fp16 residual outputs: GEMVs only", i);
+        if (it.silu) return fail(TER_HIP_ERR_PAYLOAD, "item %d: silu outputs: GEMVs only", i);
         if (it.resid) resid.emplace_back((uintptr_t)it.resid, (uintptr_t)(it.resid + (size_t)it.M * it.w->N));
         inputs.emplace_back((uintptr_t)it.x, (uintptr_t)(it.x + (size_t)it.M * it.w->K));
         if (it.M > max_m) max_m = it.M;
@@ -1370,7 +1388,7 @@ int ter_hip_gemm_plan_create(ter_hip_plan_t** plan, const ter_hip_gemm_item_t* i
     std::vector<int> piece0;  // first descriptor of each item (its pieces follow)
     for (int i = 0; i < n; ++i) {
         const ter_hip_gemm_item_t& it = items[i];
-        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid, nullptr};
+        const ter_hip_out_t o{it.y, it.acc, it.y16, it.resid, nullptr, nullptr};
         piece0.push_back((int)ds.size());
         for (int r0 = 0; r0 < it.M; r0 += rows) {
             const int m = std::min(rows, it.M - r0);

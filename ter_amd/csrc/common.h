@@ -55,6 +55,7 @@ struct alignas(16) GemvDesc {
     uint16_t* y16;               // fp16 [N] = half(y) or null
     float* resid;                // fp32 [N]: resid += float(half(y)), or null
     uint16_t* resid16;           // fp16 [N]: resid16 = half(float(resid16) + float(half(y))), or null
+    float* silu;                 // fp32 [N]: silu(float(half(y))) (the X_SMUL kind's input), or null
     unsigned long long* fix;     // N fix-up slots, zero at rest
     long long tile0;             // first tile of this GEMV in the launch's stream
     long long strip0;            // first strip of this GEMV in the launch's strip stream (strip mode)
@@ -288,15 +289,17 @@ __device__ __forceinline__ float acc_to_float(int val, int mag) {
 // add_k_f32 residual step into its fp32 stream) and, for GEMVs, resid16 =
 // half(float(resid16) + float(half(y))) (the Llama forward's add_k into its
 // fp16 stream, cuda/ter_cuda_forward_packed.cu:115-118).
+__device__ inline float silu_of(float g);
+
 template <class D>
 __device__ __forceinline__ void emit_out(const D& d, long long o, int val, float s) {
 #pragma clang fp contract(off)
     if (d.acc) gptr(d.acc)[o] = val;
     const float y = acc_to_float(val, d.w_mag) * s;
     if (d.y) gptr(d.y)[o] = y;
-    constexpr bool kR16 = std::is_same<D, GemvDesc>::value;
+    constexpr bool kR16 = std::is_same<D, GemvDesc>::value;  // the GEMV-only outputs
     bool half_out = d.y16 || d.resid;
-    if constexpr (kR16) half_out = half_out || d.resid16;
+    if constexpr (kR16) half_out = half_out || d.resid16 || d.silu;
     if (half_out) {
         const uint16_t h = float_to_half_bits(y);
         if (d.y16) gptr(d.y16)[o] = h;
@@ -305,6 +308,7 @@ __device__ __forceinline__ void emit_out(const D& d, long long o, int val, float
             if (d.resid16)
                 gptr(d.resid16)[o] =
                     float_to_half_bits(half_bits_to_float(gptr(d.resid16)[o]) + half_bits_to_float(h));
+            if (d.silu) gptr(d.silu)[o] = silu_of(half_bits_to_float(h));
         }
     }
 }
@@ -338,10 +342,17 @@ __device__ inline float ter_expf(float x) {
 
 // silu(gate) * up of silu_mul_quant_k (cuda/ter_cuda_forward_packed.cu:322-326):
 // g / (1 + exp(-g)) with this build's exp, then the product, each rounded
-// (the division correctly rounded, as nvcc's default division is).
+// (the division correctly rounded, as nvcc's default division is).  silu_of
+// is the first step alone (the gate GEMV's silu output; X_SMUL then forms
+// the product), so both routes round identically.
+__device__ inline float silu_of(float g) {
+#pragma clang fp contract(off)
+    return g / (1.0f + ter_expf(-g));
+}
+
 __device__ inline float silu_mul(float g, float u) {
 #pragma clang fp contract(off)
-    const float sg = g / (1.0f + ter_expf(-g));
+    const float sg = silu_of(g);
     return sg * u;
 }
 

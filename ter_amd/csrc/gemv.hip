@@ -237,9 +237,19 @@ __device__ __forceinline__ void load_silu16(const uint16_t* g, const uint16_t* u
 }
 
 // 16 activations of an fp32-family input (fp32, fp16 for X_F16 / X_F16_RMS,
-// relu^2(gate) * up for X_RELU2_RMS, silu(gate) * up for X_SILU_MUL) as fp32.
+// relu^2(gate) * up for X_RELU2_RMS, silu(gate) * up for X_SILU_MUL and
+// X_SMUL) as fp32.
 __device__ __forceinline__ void load_x16f(const GemvDesc& d, int k, float (&v)[16]) {
-    if (d.x_kind == TER_HIP_X_F16_RMS || d.x_kind == TER_HIP_X_F16) {
+    if (d.x_kind == TER_HIP_X_SMUL) {
+        // fp32 silu(gate) times fp16 up (zeros past K: 0 * 0)
+#pragma clang fp contract(off)
+        const float* xf = static_cast<const float*>(d.x);
+        float u[16];
+        load_f16(xf, k, d.K, (reinterpret_cast<uintptr_t>(xf) & 15u) == 0, v);
+        load_h16(d.up, k, d.K, u);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = v[i] * u[i];
+    } else if (d.x_kind == TER_HIP_X_F16_RMS || d.x_kind == TER_HIP_X_F16) {
         load_h16(static_cast<const uint16_t*>(d.x), k, d.K, v);
     } else if (d.x_kind == TER_HIP_X_RELU2_RMS) {
         load_relu2_16(static_cast<const uint16_t*>(d.x), d.up, k, d.K, v);
@@ -481,7 +491,8 @@ struct XRaw {
 constexpr bool kind_rms(int kind) { return kind != TER_HIP_X_F32 && kind != TER_HIP_X_I8; }
 // Bytes of one x element of a kind (gate's for X_RELU2_RMS).
 constexpr int kind_bytes(int kind) {
-    return kind == TER_HIP_X_I8 ? 1 : ((kind == TER_HIP_X_F32 || kind == TER_HIP_X_F32_RMS) ? 4 : 2);
+    return kind == TER_HIP_X_I8 ? 1
+                                : ((kind == TER_HIP_X_F32 || kind == TER_HIP_X_F32_RMS || kind == TER_HIP_X_SMUL) ? 4 : 2);
 }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t vec_rsrc(const void* p, int bytes) {
@@ -754,7 +765,7 @@ __device__ __forceinline__ float stage_x_vec(const GemvDesc& d, const XRaw& r, i
 // fp32 staging (stage32); gs16: fp16 gamma [Ku*256] in LDS.
 template <int kKind>
 constexpr int max_strided_ku() {
-    return kKind == TER_HIP_X_RELU2_RMS || kKind == TER_HIP_X_SILU_MUL ? 32 : 16;
+    return kKind == TER_HIP_X_RELU2_RMS || kKind == TER_HIP_X_SILU_MUL || kKind == TER_HIP_X_SMUL ? 32 : 16;
 }
 // Waves per workgroup of the strided strip kernel: 8 for the down
 // projections' kinds X_RELU2_RMS and X_SILU_MUL (their prologue over F values
@@ -766,25 +777,29 @@ constexpr int max_strided_ku() {
 #endif
 template <int kKind>
 constexpr int strided_waves() {
-    return kKind == TER_HIP_X_RELU2_RMS || kKind == TER_HIP_X_SILU_MUL ? TER_STRIDED_RELU2_WAVES : 4;
+    return kKind == TER_HIP_X_RELU2_RMS || kKind == TER_HIP_X_SILU_MUL || kKind == TER_HIP_X_SMUL
+               ? TER_STRIDED_RELU2_WAVES
+               : 4;
 }
 
 // Registers of the strided prologue.  The 256-thread kinds: x and gamma of
 // values t + T j.  X_RELU2_RMS: thread t owns the V = 1024 / T consecutive
 // virtual threads V t .. V t + V - 1 and reads their values V t + 1024 j as
 // one V-half vector each (gate, up and gamma: V = 4 a dwordx2, V = 2 a dword).
-// The absmax kinds X_F16 and X_SILU_MUL (no sum, so no order to keep): x (and
-// up) of values 8 t + 8 T j, 8 halves per dwordx4.
+// The absmax kinds X_F16, X_SILU_MUL and X_SMUL (no sum, so no order to
+// keep): x (and up) of values 8 t + 8 T j, 8 halves per dwordx4 (X_SMUL: 8
+// fp32 x values in two).
 template <int kKind, int kW>
 struct XStrided {
     static constexpr int T = 64 * kW;
     static constexpr bool R2 = kKind == TER_HIP_X_RELU2_RMS;
-    static constexpr bool ABS = kKind == TER_HIP_X_F16 || kKind == TER_HIP_X_SILU_MUL;
-    static constexpr bool UP = R2 || kKind == TER_HIP_X_SILU_MUL;
+    static constexpr bool ABS = kKind == TER_HIP_X_F16 || kKind == TER_HIP_X_SILU_MUL || kKind == TER_HIP_X_SMUL;
+    static constexpr bool UP = R2 || kKind == TER_HIP_X_SILU_MUL || kKind == TER_HIP_X_SMUL;
     static constexpr int V = R2 ? 1024 / T : (ABS ? 8 : 1);                                  // values per load
     static constexpr int J = max_strided_ku<kKind>() * kUnitK / (R2 ? 1024 : (ABS ? 8 * T : T));  // loads per operand
     static constexpr int DW = R2 ? (V + 1) / 2 : (ABS ? 4 : 1);                               // dwords per load
-    unsigned x[J][DW];  // fp32 bits (X_F32_RMS) or fp16 bits (X_F16_RMS, X_F16; the gate of X_RELU2_RMS / X_SILU_MUL)
+    static constexpr int DX = kKind == TER_HIP_X_SMUL ? 8 : DW;                              // dwords of x per load
+    unsigned x[J][DX];  // fp32 bits (X_F32_RMS, X_SMUL) or fp16 bits (X_F16_RMS, X_F16; the gate of X_RELU2_RMS / X_SILU_MUL)
     unsigned u[UP ? J : 1][DW];  // up (X_RELU2_RMS, X_SILU_MUL)
     unsigned g[ABS ? 1 : J][DW];  // gamma (fp16 bits; the RMS kinds)
 };
@@ -816,7 +831,16 @@ __device__ __forceinline__ void x_prefetch_strided(const GemvDesc& d, XStrided<k
     if constexpr (XS::ABS) {
         // (K is a multiple of 16: a vector is either inside K or reads as zeros)
 #pragma unroll
-        for (int j = 0; j < J; ++j) load_halves(rx, 2 * (8 * t + 8 * T * j), r.x[j]);
+        for (int j = 0; j < J; ++j) {
+            if constexpr (kKind == TER_HIP_X_SMUL) {
+                const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rx, 4 * (8 * t + 8 * T * j), 0, 0);
+                const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rx, 4 * (8 * t + 8 * T * j) + 16, 0, 0);
+                r.x[j][0] = a.x; r.x[j][1] = a.y; r.x[j][2] = a.z; r.x[j][3] = a.w;
+                r.x[j][4] = b.x; r.x[j][5] = b.y; r.x[j][6] = b.z; r.x[j][7] = b.w;
+            } else {
+                load_halves(rx, 2 * (8 * t + 8 * T * j), r.x[j]);
+            }
+        }
         if constexpr (XS::UP) {
             const __amdgpu_buffer_rsrc_t ru = vec_rsrc(d.up, d.K * 2);
 #pragma unroll
@@ -984,11 +1008,17 @@ __device__ __forceinline__ float stage_x_abs_strided(const GemvDesc& d, const XS
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float x = half_bits_to_float((uint16_t)(r.x[j][e >> 1] >> (16 * (e & 1))));
-            if constexpr (kKind == TER_HIP_X_SILU_MUL)
-                v[e] = silu_mul(x, half_bits_to_float((uint16_t)(r.u[j][e >> 1] >> (16 * (e & 1)))));
-            else
-                v[e] = x;  // past K: silu(0) * 0 = 0
+            if constexpr (kKind == TER_HIP_X_SMUL) {
+                // silu(gate) (fp32, from the gate GEMV) times up
+                v[e] = __builtin_bit_cast(float, r.x[j][e]) *
+                       half_bits_to_float((uint16_t)(r.u[j][e >> 1] >> (16 * (e & 1))));
+            } else {
+                const float x = half_bits_to_float((uint16_t)(r.x[j][e >> 1] >> (16 * (e & 1))));
+                if constexpr (kKind == TER_HIP_X_SILU_MUL)
+                    v[e] = silu_mul(x, half_bits_to_float((uint16_t)(r.u[j][e >> 1] >> (16 * (e & 1)))));
+                else
+                    v[e] = x;  // past K: silu(0) * 0 = 0
+            }
             mx = fmaxf(mx, fabsf(v[e]));
         }
         const int i = 8 * t + 8 * T * j;
@@ -1751,6 +1781,11 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_
                 grid, dim3(64 * strided_waves<TER_HIP_X_SILU_MUL>()), lds_bytes, st, *shared, list_dev, wg_desc_dev,
                 total_strips, n_wg, part_off);
             return hipGetLastError();
+        case TER_HIP_X_SMUL:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_SMUL, true, strided_waves<TER_HIP_X_SMUL>(), true>),
+                               grid, dim3(64 * strided_waves<TER_HIP_X_SMUL>()), lds_bytes, st, *shared, list_dev,
+                               wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
         default:
             return hipErrorInvalidValue;
         }
@@ -1779,6 +1814,11 @@ hipError_t launch_gemv_strips(const GemvDesc* list_dev, const GemvDesc* wg_desc_
         case TER_HIP_X_SILU_MUL:
             hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_SILU_MUL, true, strided_waves<TER_HIP_X_SILU_MUL>()>),
                                grid, dim3(64 * strided_waves<TER_HIP_X_SILU_MUL>()), lds_bytes, st, sh,
+                               list_dev, wg_desc_dev, total_strips, n_wg, part_off);
+            return hipGetLastError();
+        case TER_HIP_X_SMUL:
+            hipLaunchKernelGGL((gemv_strip_kernel<true, TER_HIP_X_SMUL, true, strided_waves<TER_HIP_X_SMUL>()>),
+                               grid, dim3(64 * strided_waves<TER_HIP_X_SMUL>()), lds_bytes, st, sh,
                                list_dev, wg_desc_dev, total_strips, n_wg, part_off);
             return hipGetLastError();
         default:
@@ -1817,6 +1857,7 @@ int gemv_strided_waves(int vec_kind) {
     switch (vec_kind) {
     case TER_HIP_X_RELU2_RMS: return strided_waves<TER_HIP_X_RELU2_RMS>();
     case TER_HIP_X_SILU_MUL: return strided_waves<TER_HIP_X_SILU_MUL>();
+    case TER_HIP_X_SMUL: return strided_waves<TER_HIP_X_SMUL>();
     case TER_HIP_X_F16: return strided_waves<TER_HIP_X_F16>();
     default: return kGemvWaves;
     }
@@ -1830,6 +1871,7 @@ bool gemv_strided_ok(int vec_kind, int32_t K, bool stage32) {
     case TER_HIP_X_RELU2_RMS: return stage32 && ku <= max_strided_ku<TER_HIP_X_RELU2_RMS>();
     case TER_HIP_X_F16: return stage32 && ku <= max_strided_ku<TER_HIP_X_F16>();
     case TER_HIP_X_SILU_MUL: return stage32 && ku <= max_strided_ku<TER_HIP_X_SILU_MUL>();
+    case TER_HIP_X_SMUL: return stage32 && ku <= max_strided_ku<TER_HIP_X_SMUL>();
     default: return false;
     }
 }

@@ -162,10 +162,12 @@ def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=No
     a = L.Act()
     a.data = x.data_ptr()
     if up is not None and gamma is None:
-        # silu(gate) * up, then absmax quantization (silu_mul_quant_k)
-        if x.dtype != torch.float16 or up.dtype != torch.float16 or not up.is_cuda or up.shape != x.shape:
-            raise TypeError("silu activations: gate and up must be CUDA float16 tensors of one shape")
-        a.kind = L.X_SILU_MUL
+        # silu(gate) * up, then absmax quantization (silu_mul_quant_k); with an
+        # fp32 x, x is silu(gate) already (a gate GEMV's silu output)
+        if x.dtype not in (torch.float16, torch.float32) or up.dtype != torch.float16 or not up.is_cuda \
+                or up.shape != x.shape:
+            raise TypeError("silu activations: gate (fp16) or silu(gate) (fp32) and fp16 up of one shape")
+        a.kind = L.X_SILU_MUL if x.dtype == torch.float16 else L.X_SMUL
         a.up = up.data_ptr()
         a.q_out = _ptr(q_out)
         a.scale_out = _ptr(scale_out)
@@ -202,33 +204,35 @@ def _act(x, x_scale=None, x_scale_dev=None, q_out=None, scale_out=None, gamma=No
     return a
 
 
-def _out(y, acc, y16, resid, resid16=None) -> L.Out:
+def _out(y, acc, y16, resid, resid16=None, silu=None) -> L.Out:
     o = L.Out()
     o.y, o.acc, o.y16, o.resid, o.resid16 = _ptr(y), _ptr(acc), _ptr(y16), _ptr(resid), _ptr(resid16)
+    o.silu = _ptr(silu)
     return o
 
 
 def gemv(W: PackedTrits, x, y=None, acc=None, x_scale: Optional[float] = None, x_scale_dev=None,
          q_out=None, scale_out=None, gamma=None, eps: float = 1e-5, up=None, y16=None, resid=None, resid16=None,
-         stream=None):
+         silu=None, stream=None):
     """M = 1 GEMV.  x: int8 or int16 [K] (with x_scale or x_scale_dev), or fp32 /
     fp16 [K] (absmax-quantized in the kernel prologue, quant_int8_k); with gamma
     (fp16 [K]), x fp32 or fp16 is RMS-normalized first (rmsnorm_quant_*_in_k
     steps), and with up as well, x is the fp16 gate and the prologue is
-    relu2_mul_rmsnorm_quant_k; with up but no gamma, silu_mul_quant_k.
-    Outputs: y fp32, acc int32, y16 fp16 = half(y), resid fp32 += half(y),
-    resid16 fp16 = half(resid16 + half(y)); y is allocated when none is given.
-    Returns (y, acc)."""
+    relu2_mul_rmsnorm_quant_k; with up but no gamma, silu_mul_quant_k (x the
+    fp16 gate), or its second half (x the fp32 silu(gate) a gate GEMV's silu
+    output wrote).  Outputs: y fp32, acc int32, y16 fp16 = half(y), resid fp32
+    += half(y), resid16 fp16 = half(resid16 + half(y)), silu fp32 =
+    silu(half(y)); y is allocated when none is given.  Returns (y, acc)."""
     torch = _torch()
     _require_cuda(x, "x", None, W.K)
-    if y is None and acc is None and y16 is None and resid is None and resid16 is None:
+    if y is None and acc is None and y16 is None and resid is None and resid16 is None and silu is None:
         y = torch.empty(W.N, dtype=torch.float32, device=x.device)
     a = _act(x, x_scale, x_scale_dev, q_out, scale_out, gamma, eps, up)
-    if y16 is None and resid is None and resid16 is None:
+    if y16 is None and resid is None and resid16 is None and silu is None:
         L.check(L.lib().ter_hip_gemv(C.byref(W.wpk), C.byref(a), _ptr(y), _ptr(acc), _stream(stream)),
                 "ter_hip_gemv")
     else:
-        o = _out(y, acc, y16, resid, resid16)
+        o = _out(y, acc, y16, resid, resid16, silu)
         L.check(L.lib().ter_hip_gemv_out(C.byref(W.wpk), C.byref(a), C.byref(o), _stream(stream)),
                 "ter_hip_gemv_out")
     return y, acc
@@ -550,7 +554,7 @@ def _held(it: dict) -> list:
 class Plan:
     """Many independent GEMVs in one launch (one work list).  `items` is a
     sequence of dicts: {w: PackedTrits, x: tensor, y?, acc?, y16?, resid?,
-    resid16?, x_scale?, x_scale_dev?, q_out?, scale_out?, gamma?, eps?, up?}."""
+    resid16?, silu?, x_scale?, x_scale_dev?, q_out?, scale_out?, gamma?, eps?, up?}."""
 
     def __init__(self, items: Sequence[dict], wg_per_cu: int = 0):
         n = len(items)
@@ -566,6 +570,7 @@ class Plan:
             arr[i].y16 = _ptr(it.get("y16"))
             arr[i].resid = _ptr(it.get("resid"))
             arr[i].resid16 = _ptr(it.get("resid16"))
+            arr[i].silu = _ptr(it.get("silu"))
             self._keep.extend(_held(it))
         h = C.c_void_p()
         L.check(L.lib().ter_hip_plan_create(C.byref(h), arr, n, int(wg_per_cu)), "ter_hip_plan_create")

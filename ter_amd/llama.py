@@ -10,7 +10,8 @@ down GEMV and add_k again.  Here a layer is five launches: the Q/K/V plan
 (fp16 RMSNorm prologue, fp16 outputs), the attention context (NORM RoPE,
 cache write, attention), the O projection (absmax prologue on the fp16
 attention output, fp16 residual epilogue), the gate/up plan and the down
-projection (silu(gate) * up prologue, fp16 residual epilogue).
+projection (silu(gate) * up prologue, fp16 residual epilogue; the SiLU of
+each gate value is computed once, by the gate GEMV's epilogue).
 
 The token tail has two forms, as in the reference (:541-557):
   * bench mode, a ternary lm_head [H][V] (alloc_model, :446-472): the fp16
@@ -138,7 +139,7 @@ class Decoder:
         self.k = torch.empty(hkv, dtype=f16, device=dev)
         self.v = torch.empty(hkv, dtype=f16, device=dev)
         self.attn_out = torch.empty(hq, dtype=f16, device=dev)
-        self.gate = torch.empty(c.F, dtype=f16, device=dev)
+        self.gate_silu = torch.empty(c.F, dtype=torch.float32, device=dev)
         self.up = torch.empty(c.F, dtype=f16, device=dev)
         self.K = torch.zeros((c.Nl, s_max, c.Nkv, c.Hd), dtype=f16, device=dev)
         self.V = torch.zeros((c.Nl, s_max, c.Nkv, c.Hd), dtype=f16, device=dev)
@@ -161,9 +162,13 @@ class Decoder:
                           dict(w=W["Wk"], x=self.hidden, gamma=lay.attn_norm, eps=c.eps, y16=self.k),
                           dict(w=W["Wv"], x=self.hidden, gamma=lay.attn_norm, eps=c.eps, y16=self.v)])
             o = F.Plan([dict(w=W["Wo"], x=self.attn_out, resid16=self.hidden)])
-            gu = F.Plan([dict(w=W["Wgate"], x=self.hidden, gamma=lay.ffn_norm, eps=c.eps, y16=self.gate),
+            # silu_mul_quant_k split in two: the gate GEMV's epilogue writes
+            # silu(half(gate)) once per element, the down projection's
+            # prologue multiplies by up and quantizes (bit for bit the fused
+            # form, without an exp per element in every down workgroup)
+            gu = F.Plan([dict(w=W["Wgate"], x=self.hidden, gamma=lay.ffn_norm, eps=c.eps, silu=self.gate_silu),
                          dict(w=W["Wup"], x=self.hidden, gamma=lay.ffn_norm, eps=c.eps, y16=self.up)])
-            dn = F.Plan([dict(w=W["Wdown"], x=self.gate, up=self.up, resid16=self.hidden)])
+            dn = F.Plan([dict(w=W["Wdown"], x=self.gate_silu, up=self.up, resid16=self.hidden)])
             self.plans.append((qkv, o, gu, dn))
         self.logits = None
         self.head = None

@@ -84,6 +84,14 @@ def test_gemv_validation_without_device():
     x.data = fake
     assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 4, fake, None, None) == L.ERR_PAYLOAD
     assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 1, fake, None, None) == L.ERR_PAYLOAD
+    # silu(gate) * up from an fp32 silu vector: up required, fp32 alignment, GEMV-only
+    x.kind, x.data, x.up = L.X_SMUL, fake, None
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_NULL
+    x.up, x.data = fake, fake + 2
+    assert lib.ter_hip_gemv(C.byref(w), C.byref(x), fake, None, None) == L.ERR_ALIGN
+    x.data = fake
+    assert lib.ter_hip_gemm(C.byref(w), C.byref(x), 4, fake, None, None) == L.ERR_PAYLOAD
+    x.kind, x.up = L.X_F16, None
     # fp16 residual outputs: 2-byte aligned, GEMVs only
     o = L.Out()
     o.resid16 = fake + 1
@@ -92,6 +100,12 @@ def test_gemv_validation_without_device():
     xi = L.Act()
     xi.data, xi.kind, xi.scale_dev = fake, L.X_I8, fake
     assert lib.ter_hip_gemm_out(C.byref(w), C.byref(xi), 4, C.byref(o), None) == L.ERR_PAYLOAD
+    # the silu output: 4-byte aligned, GEMVs only
+    o2 = L.Out()
+    o2.silu = fake + 2
+    assert lib.ter_hip_gemv_out(C.byref(w), C.byref(x), C.byref(o2), None) == L.ERR_ALIGN
+    o2.silu = fake
+    assert lib.ter_hip_gemm_out(C.byref(w), C.byref(xi), 4, C.byref(o2), None) == L.ERR_PAYLOAD
     x.kind = L.X_I8
     assert lib.ter_hip_gemv(C.byref(w), C.byref(x), None, None, None) == L.ERR_NULL  # no output
     x.kind = L.X_F32

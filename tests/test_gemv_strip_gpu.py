@@ -103,7 +103,7 @@ def test_decode_shaped_lists(cuda):
     run_list([(2560, 8448), (2560, 8448)], seed=16)
 
 
-@pytest.mark.parametrize("kind", ["f32-rms", "f16-rms", "relu2", "f16", "silu"])
+@pytest.mark.parametrize("kind", ["f32-rms", "f16-rms", "relu2", "f16", "silu", "smul"])
 @pytest.mark.parametrize("order", ["grouped", "reordered"])
 def test_shared_activation_plans(cuda, kind, order):
     """Strided strip-mode lists whose GEMVs read one activation vector: with
@@ -116,7 +116,7 @@ def test_shared_activation_plans(cuda, kind, order):
     import torch
     import ter_amd as T
     from ter_amd import _lib as L
-    K = {"f32-rms": 2560, "f16-rms": 2048, "relu2": 6912, "f16": 2048, "silu": 8192}[kind]
+    K = {"f32-rms": 2560, "f16-rms": 2048, "relu2": 6912, "f16": 2048, "silu": 8192, "smul": 8192}[kind]
     Ns = [4000, 48, 2000] if kind in ("f32-rms", "f16-rms") else [1024, 528]
     rng = np.random.default_rng(K + len(Ns))
     gm = rng.uniform(0.5, 1.5, K).astype(np.float16)
@@ -131,8 +131,11 @@ def test_shared_activation_plans(cuda, kind, order):
         rq, rs, _ = O.relu2_rmsnorm_quant(x, up, gm, 1e-5)
     elif kind == "f16":
         rq, rs = O.quant_int8(x.astype(np.float32))
-    else:
+    elif kind == "silu":
         rq, rs, _ = O.silu_mul_quant(x, up)
+    else:
+        x = O.silu_f16(x)
+        rq, rs, _ = O.smul_quant(x, up)
     v11s = [O.v11_pack(O.rand_trits(K * 3 + 7 * i, K, N, 0.4)) for i, N in enumerate(Ns)]
     Ws = [T.PackedTrits.from_v11(v, K, N, 0.01 * (i + 1)) for i, (v, N) in enumerate(zip(v11s, Ns))]
     Ws = T.group_contiguous(Ws)
@@ -145,7 +148,7 @@ def test_shared_activation_plans(cuda, kind, order):
                   y16=torch.empty(Ns[i], dtype=torch.float16, device="cuda"))
         if kind in ("f32-rms", "f16-rms", "relu2"):
             it.update(gamma=dg, eps=1e-5)
-        if kind in ("relu2", "silu"):
+        if kind in ("relu2", "silu", "smul"):
             it["up"] = du
         items.append(it)
     plan = T.Plan(items)

@@ -3,7 +3,9 @@
 
 * quant_int8_k on the fp16 attention output (:40-62) as the GEMV prologue
   TER_HIP_X_F16;
-* silu_mul_quant_k (:312-344) as the GEMV prologue TER_HIP_X_SILU_MUL;
+* silu_mul_quant_k (:312-344) as the GEMV prologue TER_HIP_X_SILU_MUL, and
+  split in two: the gate GEMV's silu output (silu of its fp16 value) and the
+  down projection's TER_HIP_X_SMUL prologue (times up, absmax);
 * add_k into the fp16 hidden stream (:113-116) as the GEMV's resid16
   epilogue;
 * one Llama layer's projection chain through work-list plans;
@@ -99,6 +101,53 @@ def test_gemv_silu_prologue(cuda, K, N, kind):
     assert_f16_equal(y16, ry)
 
 
+@pytest.mark.parametrize("K,N,ws", [(2048, 8192, 0.05), (777, 100, 0.3), (2048, 512, 3000.0)])
+def test_gemv_silu_output(cuda, K, N, ws):
+    """The gate projection's silu output: silu(float(half(y))) in fp32, beside
+    its fp16 output (ws = 3000: outputs past 65504, half(y) = inf, silu = inf
+    or -0)."""
+    import torch
+    import ter_amd as T
+    v11, W = weight(K * 13 + N, K, N, ws)
+    x8 = O.rand_int8(K + 3 * N, K)
+    _, ry = O.gemv_v11(x8, np.float32(0.04), v11, ws, K, N)
+    y16 = torch.empty(N, dtype=torch.float16, device="cuda")
+    sl = torch.empty(N, dtype=torch.float32, device="cuda")
+    T.gemv(W, dev(x8), x_scale=0.04, y16=y16, silu=sl)
+    assert_f16_equal(y16, ry)
+    want = O.silu_f16(half_of(ry))
+    got = host(sl)
+    assert (got.view(np.int32) == want.view(np.int32)).all(), np.flatnonzero(got.view(np.int32) != want.view(np.int32))[:8]
+    if ws > 1000:
+        assert np.isinf(half_of(ry).astype(np.float32)).any()
+    T.gemv(W, dev(x8), x_scale=0.04, silu=sl)  # the silu output alone
+    assert (host(sl).view(np.int32) == want.view(np.int32)).all()
+
+
+@pytest.mark.parametrize("K,N", [(8192, 2048), (769, 64), (9000, 300)])
+def test_gemv_smul_prologue(cuda, K, N):
+    """The down projection's input from the split route: fp32 silu(gate)
+    times fp16 up, then absmax -- the fused X_SILU_MUL prologue's int8
+    vector, scale and outputs, bit for bit."""
+    import torch
+    import ter_amd as T
+    g, u = gate_up(K * 3 + N, K)
+    s = O.silu_f16(g)
+    v11, W = weight(K * 7 + N, K, N, 0.019)
+    outs = []
+    for x in (dev(s), dev(g)):  # X_SMUL, then X_SILU_MUL
+        q = torch.empty(K, dtype=torch.int8, device="cuda")
+        sc = torch.empty(1, dtype=torch.float32, device="cuda")
+        acc = torch.empty(N, dtype=torch.int32, device="cuda")
+        T.gemv(W, x, acc=acc, q_out=q, scale_out=sc, up=dev(u))
+        outs.append((host(q), host(sc)[0], host(acc)))
+    rq, rs, _ = O.smul_quant(s, u)
+    ra, _ = O.gemv_v11(rq, rs, v11, 0.019, K, N)
+    for q, sc, acc in outs:
+        assert (q == rq).all() and sc.view(np.int32) == np.float32(rs).view(np.int32)
+        assert (acc == ra).all()
+
+
 @pytest.mark.parametrize("K,N,ws", [(2048, 2048, 0.02), (8192, 2048, 0.05), (300, 20, 2000.0)])
 def test_gemv_resid16_epilogue(cuda, K, N, ws):
     """hidden16 = half(float(hidden16) + float(half(y))), twice in a row
@@ -124,9 +173,10 @@ def test_gemv_resid16_epilogue(cuda, K, N, ws):
 
 @pytest.mark.parametrize("kind,K,N", [("f16", 2048, 2048), ("f16", 4112, 256), ("f16", 777, 64),
                                       ("silu", 8192, 2048), ("silu", 9000, 512), ("silu", 1000, 128),
-                                      ("silu", 512, 256)],
+                                      ("silu", 512, 256), ("smul", 8192, 2048), ("smul", 9000, 512),
+                                      ("smul", 1000, 128)],
                          ids=["f16-strided", "f16-beyond-strided", "f16-ragged", "silu-strided", "silu-beyond-strided",
-                              "silu-ragged", "silu-small"])
+                              "silu-ragged", "silu-small", "smul-strided", "smul-beyond-strided", "smul-ragged"])
 def test_plan_absmax_prologues(cuda, kind, K, N):
     """Work-list plans of the fp16 absmax kinds: the strided strip prologue
     (K a multiple of 16 within its unit limit), and the general one past the
@@ -144,6 +194,10 @@ def test_plan_absmax_prologues(cuda, kind, K, N):
     if kind == "silu":
         it["up"] = dev(u)
         rq, rs, _ = O.silu_mul_quant(x, u)
+    elif kind == "smul":
+        sl = O.silu_f16(x)
+        it.update(x=dev(sl), up=dev(u))
+        rq, rs, _ = O.smul_quant(sl, u)
     else:
         rq, rs = O.quant_int8(x.astype(np.float32))
     plan = T.Plan([it])
@@ -162,8 +216,9 @@ def test_plan_absmax_prologues(cuda, kind, K, N):
 def test_llama_layer_projection_chain(cuda):
     """hidden16 -> [fp16 RMSNorm prologue] Q, K, V ; synthetic fp16 attention
     output -> [absmax prologue] O, += hidden16 ; hidden16 -> [fp16 RMSNorm
-    prologue] gate, up -> [silu prologue] down, += hidden16.  Four plan
-    launches; every fp16 output and the final hidden16 bit-exact."""
+    prologue] gate (fp16 and silu outputs), up -> [silu(gate) * up prologue
+    from the gate's silu output] down, += hidden16.  Four plan launches;
+    every output and the final hidden16 bit-exact."""
     import torch
     import ter_amd as T
     H, F, KV = 2048, 8192, 512
@@ -190,9 +245,10 @@ def test_llama_layer_projection_chain(cuda):
                   dict(w=Wk, x=hid, gamma=d_na, eps=eps, y16=k16),
                   dict(w=Wv, x=hid, gamma=d_na, eps=eps, y16=v16)])
     oproj = T.Plan([dict(w=Wo, x=d_attn, resid16=hid)])
-    gu = T.Plan([dict(w=Wg, x=hid, gamma=d_nf, eps=eps, y16=g16),
+    sl = torch.empty(F, dtype=torch.float32, device="cuda")
+    gu = T.Plan([dict(w=Wg, x=hid, gamma=d_nf, eps=eps, y16=g16, silu=sl),
                  dict(w=Wu, x=hid, gamma=d_nf, eps=eps, y16=u16)])
-    down = T.Plan([dict(w=Wd, x=g16, up=u16, resid16=hid)])
+    down = T.Plan([dict(w=Wd, x=sl, up=u16, resid16=hid)])
     for p in (qkv, oproj, gu, down):
         p.launch()
 
@@ -213,6 +269,7 @@ def test_llama_layer_projection_chain(cuda):
     assert_f16_equal(v16, ref_v)
     assert_f16_equal(g16, ref_g)
     assert_f16_equal(u16, ref_u)
+    assert (host(sl).view(np.int32) == O.silu_f16(half_of(ref_g)).view(np.int32)).all()
     assert (host(hid).view(np.uint16) == h2.view(np.uint16)).all()
     for p in (qkv, oproj, gu, down):
         p.close()

@@ -596,6 +596,21 @@ def test_silu_mul_within_rounding_bound_and_odd_part():
     assert np.abs((vp.astype(np.float64) - vn) - gf).max() <= 1e-5 * np.abs(gf).max()
 
 
+def test_silu_split_route_equals_the_fused_one():
+    """silu_f16 then smul_quant (the gate GEMV's silu output, then the X_SMUL
+    prologue) against silu_mul_quant in one step: bit for bit."""
+    rng = np.random.default_rng(21)
+    g = np.concatenate([(rng.standard_normal(8192) * 4), rng.uniform(-120, 120, 1000),
+                        [0.0, -0.0, 60000.0, -60000.0]]).astype(np.float16)
+    u = rng.standard_normal(g.size).astype(np.float16)
+    s = O.silu_f16(g)
+    q1, s1, v1 = O.smul_quant(s, u)
+    q0, s0, v0 = O.silu_mul_quant(g, u)
+    assert (q1 == q0).all() and s1 == s0 and (v1.view(np.int32) == v0.view(np.int32)).all()
+    _, _, vs = O.silu_mul_quant(g, np.ones(g.size, np.float16))  # silu(g) * 1
+    assert (s.view(np.int32) == vs.view(np.int32)).all()
+
+
 def test_silu_mul_quant_is_quant_int8_of_silu():
     rng = np.random.default_rng(20)
     g = (rng.standard_normal(8192) * 3).astype(np.float16)
