@@ -18,7 +18,9 @@
 //     butterfly over the wave, o_c[d] = sum over the chunk's positions in
 //     order of e_s v_sd (fused multiply-adds);
 //   - the last workgroup of a head group to finish combines the chunks in
-//     order: w_c = exp(m_c - M), L = sum l_c w_c, O = sum o_c w_c, out = O/L.
+//     order: w_c = exp(m_c - M), L = sum l_c w_c, O = sum o_c w_c, out = O/L
+//     (while every position fits one chunk, that chunk's workgroup does it
+//     at once, with no partials published or counted).
 // The K and V rows of the chunk are staged in LDS with coalesced 16-byte
 // loads issued before anything else; the new position's key and value come
 // from the projection outputs (RoPE applied here), not from the cache, which
@@ -322,6 +324,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_decode_kernel(AttnArgs a_in
                 for (int j = 0; j < DPT; ++j) acc[j] = __builtin_fmaf(wv[i], half_bits_to_float(vv[i][j]), acc[j]);
         }
     }
+    // One chunk holds every position (seq <= kChunk): its workgroup combines
+    // that chunk itself, with the combine's own operations (w = exp(m - M)
+    // with M = m, so w = 1; L and O by the same fused multiply-adds), so the
+    // same bits; no workgroup publishes or counts, and the counter stays zero.
+    if (seq <= kChunk) {
+        if (chunk != 0 || !head_ok) return;
+        const float w = attn_expf(mc - mc);
+        const float L = __builtin_fmaf(lsum, w, 0.f);
+        uint16_t* oh = a.out + (long long)(h0 + wave) * HD + d0;
+#pragma unroll
+        for (int j = 0; j < DPT; ++j) gptr(oh)[j] = float_to_half_bits(__builtin_fmaf(acc[j], w, 0.f) / L);
+        return;
+    }
+
     // 6. publish the partials (written through), then count the arrival
     constexpr int kScope = kLocal ? __HIP_MEMORY_SCOPE_WORKGROUP : __HIP_MEMORY_SCOPE_AGENT;
     if (head_ok && n > 0) {
