@@ -91,7 +91,8 @@ struct LCfg {
     static constexpr int STB = XB + BS * kTileBytes;  // bytes per stage
     static constexpr int XSO = NST * STB;             // row-scale slots: NST x 1 KiB
     static constexpr int FLO = XSO + NST * 1024;      // stage counters: ready[NST], freed[NST]
-    static constexpr int LDS = FLO + 64;
+    static constexpr int RSO = FLO + 64;              // (PRS) row sums of X per block: NST slots x MB*16 ints
+    static constexpr int LDS = RSO + NST * MB * 16 * 4;
     static constexpr int XI = XB / 1024;              // 1 KiB load runs of X per stage
     static constexpr int NI = XI + BS;                // load runs per stage, run q issued by issuer q % IW
     static constexpr int NIW = NI / IW;               // runs of issuers >= NR ...
@@ -117,6 +118,13 @@ struct LCfg {
 #define TER_LDS_UC_MB 2
 #endif
     static constexpr bool UC = MBW <= TER_LDS_UC_MB;
+    // With producer waves, the producers form those row sums from the X rows
+    // they load (v_dot4 against ones, once per block) and hand them over in
+    // LDS; the compute waves then issue no row-sum MFMA (at 2 row blocks, 8
+    // of a wave's 40 MFMAs per stage).  Measured, alternating builds on one
+    // box: M = 32 119.7-121.1 -> 117.8-118.3 us, M = 16 95.8-96.2 -> 95.3-95.5
+    // us, provided only a block's last unit adds before its ready count.
+    static constexpr bool PRS = UC && PW > 0;
     static_assert(NST >= 2 && NST <= 8, "stage count");
     static_assert(S % 2 == 0, "the fp32 epilogue stores strips in pairs");
     static_assert(LDS <= kLdsMax, "LDS budget");
@@ -208,6 +216,55 @@ __device__ __forceinline__ void signal_one(unsigned char* lds_byte, int lane) {
     const unsigned a = lds_off(lds_byte);
     asm volatile("" ::: "memory");
     if (lane == 0) asm volatile("ds_add_u32 %0, %1" : : "v"(a), "v"(1u) : "memory");
+}
+
+// (PRS) A producer's LDS accesses for the row sums, inline for the same
+// reason as the counters: 16 bytes of a landed X run, and a row sum.
+__device__ __forceinline__ u32x4_t lds_read16(unsigned char* p) {
+    u32x4_t v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(lds_off(p)) : "memory");
+    return v;
+}
+
+__device__ __forceinline__ void lds_write4(unsigned char* p, int v) {
+    asm volatile("ds_write_b32 %0, %1" : : "v"(lds_off(p)), "v"(v) : "memory");
+}
+
+// Sum over each row of 16 lanes (every lane gets its row's total): xor 1 and
+// 2 within quads, then the half-row and row mirrors (DPP, no LDS).
+__device__ __forceinline__ int row_total16(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    v += __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    v += __builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+    v += __builtin_amdgcn_mov_dpp(v, 0x140, 0xF, 0xF, false);  // row_mirror
+    return v;
+}
+
+// (PRS) The producer's share of a unit's row sums: its X runs q = issuer +
+// IW r (rows 4 q .. 4 q + 3, lane l: row 4 q + l / 16, one 16-byte chunk) of
+// the landed stage, added into rsp[r]; at the block's last unit each row's
+// total goes to the block's slot (row 4 q + l / 16 by lane 16 (l / 16)).
+template <class C>
+__device__ __forceinline__ void producer_row_sums(unsigned char* stage, unsigned char* slot, int issuer, int lane,
+                                                  bool last, int (&rsp)[C::XI / C::IW + 1]) {
+#pragma unroll
+    for (int r = 0; r < C::XI / C::IW + 1; ++r) {
+        const int q = issuer + C::IW * r;  // wave-uniform
+        if (q < C::XI) {
+            const u32x4_t c = lds_read16(stage + q * 1024 + lane * 16);
+            int v = rsp[r];
+            v = __builtin_amdgcn_sdot4((int)c.x, 0x01010101, v, false);
+            v = __builtin_amdgcn_sdot4((int)c.y, 0x01010101, v, false);
+            v = __builtin_amdgcn_sdot4((int)c.z, 0x01010101, v, false);
+            v = __builtin_amdgcn_sdot4((int)c.w, 0x01010101, v, false);
+            rsp[r] = v;
+            if (last) {
+                const int t = row_total16(v);
+                if ((lane & 15) == 0) lds_write4(slot + (4 * q + (lane >> 4)) * 4, t);
+                rsp[r] = 0;
+            }
+        }
+    }
 }
 
 // Wait until this wave's loads of the unit `behind` stages older than the
@@ -362,7 +419,7 @@ __device__ __forceinline__ void compute_stage(const unsigned char* stage, int rg
 #pragma unroll
         for (int s = 0; s < C::S; ++s)
             acc[s][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, B[s], acc[s][mb], 0, 0, 0);
-        if constexpr (C::UC) {
+        if constexpr (C::UC && !C::PRS) {
             const i32x4 ones = {0x01010101, 0x01010101, 0x01010101, 0x01010101};
             rsum[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, ones, rsum[mb], 0, 0, 0);
         }
@@ -475,9 +532,20 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
         // flight) holds back no MFMA; the compute waves wait only when the
         // data is late.
         int cb = b_lo, cu = 0, j = 0, js = 0, cku = block_at<kList>(single, list, blocks, cb, C::BS).d.Ku;
+        int rsp[C::XI / C::IW + 1] = {};
         while (true) {
             wait_stage<C>(n_issued - j - 1, issuer);
+            // (the block's row sums written before its last unit's ready count,
+            // which the epilogue waits behind; the other units' added after
+            // their count, off the compute waves' path)
+            const bool last_u = cu + 1 == cku;
+            if constexpr (C::PRS)
+                if (last_u)
+                    producer_row_sums<C>(lds + js * C::STB, lds + C::RSO + (cb % C::NST) * C::MB * 64, issuer, lane,
+                                         true, rsp);
             signal_one(ready + 4 * js, lane);
+            if constexpr (C::PRS)
+                if (!last_u) producer_row_sums<C>(lds + js * C::STB, nullptr, issuer, lane, false, rsp);
             if (ib < b_hi) {
                 if (j >= 1) {
                     const int jp = j - 1, sp = js == 0 ? C::NST - 1 : js - 1;
@@ -501,8 +569,14 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
         // issue the unit that refills the stage the compute waves have just
         // left.  Same unit count and barrier count as the compute waves.
         int cb = b_lo, cu = 0, it = 0, cku = block_at<kList>(single, list, blocks, cb, C::BS).d.Ku;
+        int rsp[C::XI / C::IW + 1] = {};
         while (true) {
             wait_stage<C>(n_issued - it - 1, issuer);
+            if constexpr (C::PRS) {
+                producer_row_sums<C>(lds + (it % C::NST) * C::STB, lds + C::RSO + (cb % C::NST) * C::MB * 64, issuer,
+                                     lane, cu + 1 == cku, rsp);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the row sums written before the barrier
+            }
             lds_barrier();
             if (ib < b_hi) issue_next();
             ++it;
@@ -551,6 +625,14 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
             if constexpr (C::UC) {
                 // sum_k x u = sum_k x w + sum_k x (padding rows hold u = 1 and
                 // cancel too); the row sums are the same in every column
+                if constexpr (C::PRS) {
+                    // the producers' sums of this block (slot cb % NST): lane (j, g)
+                    // holds rows 4 g .. 4 g + 3 of each row block
+                    const int* rs = reinterpret_cast<const int*>(lds + C::RSO + (cb % C::NST) * C::MB * 64);
+#pragma unroll
+                    for (int mb = 0; mb < C::MBW; ++mb)
+                        rsum[mb] = *reinterpret_cast<const i32x4*>(rs + (rg * C::MBW + mb) * 16 + 4 * g);
+                }
 #pragma unroll
                 for (int s = 0; s < C::S; ++s)
 #pragma unroll
