@@ -75,17 +75,18 @@ __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirs
 
 constexpr int kLWaves = 8;
 
-// PW producer waves (0: the 8 compute waves issue the loads themselves).
-template <int MBW_, int S_, int RS_, int NST_, int PW_ = 0, int FS_ = 0>
+// PW producer waves (0: the compute waves issue the loads themselves), CW
+// compute waves.
+template <int MBW_, int S_, int RS_, int NST_, int PW_ = 0, int FS_ = 0, int CW_ = kLWaves>
 struct LCfg {
-    static constexpr int MBW = MBW_, S = S_, RS = RS_, NST = NST_, PW = PW_;
+    static constexpr int MBW = MBW_, S = S_, RS = RS_, NST = NST_, PW = PW_, CW = CW_;
     // FS: stage hand-over through LDS counters instead of a workgroup
     // barrier per unit (needs producer waves)
     static constexpr bool FS = FS_ != 0 && PW > 0;
-    static constexpr int THREADS = 64 * (kLWaves + PW);
-    static constexpr int IW = PW > 0 ? PW : kLWaves;  // waves that issue the loads
+    static constexpr int THREADS = 64 * (CW + PW);
+    static constexpr int IW = PW > 0 ? PW : CW;       // waves that issue the loads
     static constexpr int MB = RS * MBW;               // row blocks of 16
-    static constexpr int SG = kLWaves / RS;           // strip groups
+    static constexpr int SG = CW / RS;                // strip groups
     static constexpr int BS = SG * S;                 // strips per block
     static constexpr int XB = MB * 16 * kUnitK;       // X bytes per stage
     static constexpr int STB = XB + BS * kTileBytes;  // bytes per stage
@@ -180,7 +181,7 @@ __device__ __forceinline__ void lds_barrier() {
 // Stage hand-over without a workgroup barrier (PW > 0).  Two monotonic
 // counters per ring stage in LDS: ready[s] counts the producers' "my loads
 // of the unit in stage s have landed" signals (PW per use of the stage),
-// freed[s] the compute waves' "done reading stage s" signals (kLWaves per
+// freed[s] the compute waves' "done reading stage s" signals (C::CW per
 // use).  A compute wave waits for ready of its next unit only; a producer
 // waits for freed of the stage it is about to refill only.  So no wave
 // waits for the slowest of the others at every stage, and a stage is freed
@@ -467,8 +468,8 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
     if (b_lo >= b_hi) return;
     const int lane = threadIdx.x & 63;
     const int wave = uniform(threadIdx.x >> 6);
-    const bool producer = C::PW > 0 && wave >= kLWaves;  // wave-uniform
-    const int issuer = C::PW > 0 ? wave - kLWaves : wave;  // index among the issuing waves
+    const bool producer = C::PW > 0 && wave >= C::CW;  // wave-uniform
+    const int issuer = C::PW > 0 ? wave - C::CW : wave;  // index among the issuing waves
     const int rg = wave / C::SG, sg = wave % C::SG;
     const int j = lane & 15, g = lane >> 4;
 
@@ -549,7 +550,7 @@ __global__ __launch_bounds__(C::THREADS) void gemm_lds_kernel(GemmDesc single, c
             if (ib < b_hi) {
                 if (j >= 1) {
                     const int jp = j - 1, sp = js == 0 ? C::NST - 1 : js - 1;
-                    spin_ge(freed + 4 * sp, (unsigned)(kLWaves * (jp / C::NST + 1)));
+                    spin_ge(freed + 4 * sp, (unsigned)(C::CW * (jp / C::NST + 1)));
                 }
                 issue_next();
             }
