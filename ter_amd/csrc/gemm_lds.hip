@@ -37,7 +37,7 @@
 // Operands.  X rows sit in LDS as 256-byte rows whose 16-byte chunks are
 // XOR-swizzled by the row's low 4 bits (chunk c of row r at position
 // c ^ (r & 15)), so the 16 rows an MFMA A operand reads hit distinct banks.
-// The wave grid is RS row groups x (8 / RS) strip groups; a wave holds
+// The wave grid is RS row groups x (CW / RS) strip groups; a wave holds
 // MBW x S accumulators (MBW row blocks of 16 x S strips).  Per 64-row slab a
 // wave reads MBW A operands (ds_read_b128) and S weight dwords (ds_read_b32,
 // lane = column j + 16 * k-group g, one dword = 16 trits of column j) and
@@ -45,10 +45,11 @@
 // code u = w + 1 becomes the signed int8 w with one v_perm_b32 per 4 trits
 // (a byte table {-1, 0, +1, 0} indexed by u) and needs no correction.  Up to
 // 2 row blocks (C::UC) the MFMAs take the unsigned codes u themselves (7 bit
-// operations per 16 trits instead of 11), and one more MFMA per A operand
-// against all-ones sums the rows of X; the epilogue subtracts that row sum
-// (sum_k x u = sum_k x w + sum_k x, and the padding rows past K, which hold
-// u = 1, cancel the same way).  The A operands are read a few steps ahead of
+// operations per 16 trits instead of 11), and the epilogue subtracts the row
+// sums of X (sum_k x u = sum_k x w + sum_k x, and the padding rows past K,
+// which hold u = 1, cancel the same way): formed by the producer waves from
+// the X runs they load (C::PRS), or without producers by one more MFMA per A
+// operand against all-ones.  The A operands are read a few steps ahead of
 // their MFMAs.
 //
 // Epilogue.  The common output form (fp32 y only, payload magnitude 1, N a
@@ -112,17 +113,19 @@ struct LCfg {
     static constexpr bool TW = MBW >= TER_LDS_TW_MB;
     // Up to 2 row blocks the weights enter the MFMAs as their unsigned codes
     // u = w + 1 (7 bit operations per 16 trits instead of 11 for the signed
-    // table lookup) and one more MFMA per A operand sums the rows of X
-    // against all-ones, subtracted in the epilogue: there each weight dword
-    // feeds only MBW MFMAs, and its unpacking bounds the compute waves.
+    // table lookup) and the row sums of X are subtracted in the epilogue:
+    // there each weight dword feeds only MBW MFMAs, and its unpacking bounds
+    // the compute waves.  (At 4 and 8 row blocks, with the producers' row
+    // sums: M = 128 272-273 against 260-261 us, M = 256 515-520 against 491
+    // us; the producers' eight X runs per unit delay the barrier.)
 #ifndef TER_LDS_UC_MB
 #define TER_LDS_UC_MB 2
 #endif
     static constexpr bool UC = MBW <= TER_LDS_UC_MB;
     // With producer waves, the producers form those row sums from the X rows
-    // they load (v_dot4 against ones, once per block) and hand them over in
-    // LDS; the compute waves then issue no row-sum MFMA (at 2 row blocks, 8
-    // of a wave's 40 MFMAs per stage).  Measured, alternating builds on one
+    // they load (v_dot4 against ones) and hand them over in LDS once per
+    // block; the compute waves then issue no row-sum MFMA (at 2 row blocks, 8
+    // of a wave's 40 MFMAs per stage; without producers they do).  Measured, alternating builds on one
     // box: M = 32 119.7-121.1 -> 117.8-118.3 us, M = 16 95.8-96.2 -> 95.3-95.5
     // us, provided only a block's last unit adds before its ready count.
     static constexpr bool PRS = UC && PW > 0;
