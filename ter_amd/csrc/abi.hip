@@ -1542,7 +1542,9 @@ static int argmax_any(const uint16_t* logits, int32_t N, int32_t* out_idx, uint6
     if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
     const int cus = device_cu_count(dev);
     if (cus <= 0) return fail(TER_HIP_ERR_HIP, "cannot query CU count");
-    long long g = ((long long)N + 1023) / 1024;  // about 4 elements per thread
+    // one round per thread: 8 logits each (16-byte aligned logits), else 4
+    const long long per_wg = aligned(logits, 16) ? 8 * 256 : 1024;
+    long long g = ((long long)N + per_wg - 1) / per_wg;
     if (g > cus) g = cus;
     e = launch_argmax_f16(logits, N, out_idx, reinterpret_cast<unsigned long long*>(state), pos_advance, (int)g,
                           static_cast<hipStream_t>(stream));

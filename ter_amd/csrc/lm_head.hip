@@ -403,14 +403,35 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_generic_kernel(LmArgs a, i
 }
 
 // argmax of fp16 logits [N] (argmax_local_k + argmax_final_k semantics).
+// kVec (logits 16-byte aligned): each thread reads 8 consecutive logits with
+// one range-checked 16-byte load per round (past n: zeros, whose keys are not
+// taken), so a launch sized at one round waits for one load; otherwise one
+// logit per thread and round.  The maximum key does not depend on who
+// compares what, so both forms give the same index.
+template <bool kVec>
 __global__ __launch_bounds__(kLmThreads) void argmax_kernel(const uint16_t* __restrict__ logits, int n,
                                                             int32_t* token_out, unsigned long long* state,
                                                             int32_t* pos_advance) {
     __shared__ unsigned long long kred[kLmWaves];
     const int chunk = argmax_chunk(n);
     unsigned long long best = 0ull;
-    for (long long i = (long long)blockIdx.x * kLmThreads + threadIdx.x; i < n; i += (long long)gridDim.x * kLmThreads)
-        best = umax64(best, argmax_key(gptr(logits)[i], (int)i, chunk));
+    if constexpr (kVec) {
+        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)logits, 0, 2 * n, 0x00020000);
+        for (long long b = ((long long)blockIdx.x * kLmThreads + threadIdx.x) * 8; b < n;
+             b += (long long)gridDim.x * kLmThreads * 8) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(2 * b), 0, 0);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int i = (int)b + e;
+                const uint16_t h = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+                if (i < n) best = umax64(best, argmax_key(h, i, chunk));
+            }
+        }
+    } else {
+        for (long long i = (long long)blockIdx.x * kLmThreads + threadIdx.x; i < n;
+             i += (long long)gridDim.x * kLmThreads)
+            best = umax64(best, argmax_key(gptr(logits)[i], (int)i, chunk));
+    }
     argmax_finish(best, kred, state, token_out, chunk, pos_advance);
 }
 
@@ -539,7 +560,12 @@ hipError_t launch_lm_head(const float* hidden, const uint16_t* hidden16, const u
 
 hipError_t launch_argmax_f16(const uint16_t* logits, int n, int32_t* token_out, unsigned long long* state,
                              int32_t* pos_advance, int n_wg, hipStream_t st) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(n_wg), dim3(kLmThreads), 0, st, logits, n, token_out, state, pos_advance);
+    if ((reinterpret_cast<uintptr_t>(logits) & 15) == 0)
+        hipLaunchKernelGGL(argmax_kernel<true>, dim3(n_wg), dim3(kLmThreads), 0, st, logits, n, token_out, state,
+                           pos_advance);
+    else
+        hipLaunchKernelGGL(argmax_kernel<false>, dim3(n_wg), dim3(kLmThreads), 0, st, logits, n, token_out, state,
+                           pos_advance);
     return hipGetLastError();
 }
 

@@ -158,4 +158,8 @@ def test_argmax_f16_matches_reference_rule(cuda):
     for i, lg in enumerate(cases):
         got = int(host(T.argmax_f16(dev(lg), state=state))[0])
         assert got == O.argmax_f16(lg), (i, lg.size)
+        # logits 2 bytes past a 16-byte boundary: one logit per thread and round
+        off = dev(np.concatenate([np.zeros(1, np.float16), lg]))[1:]
+        got = int(host(T.argmax_f16(off, state=state))[0])
+        assert got == O.argmax_f16(lg), ("unaligned", i, lg.size)
     assert (host(state.t) == 0).all()
