@@ -404,10 +404,11 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_generic_kernel(LmArgs a, i
 
 // argmax of fp16 logits [N] (argmax_local_k + argmax_final_k semantics).
 // kVec (logits 16-byte aligned): each thread reads 8 consecutive logits with
-// one range-checked 16-byte load per round (past n: zeros, whose keys are not
-// taken), so a launch sized at one round waits for one load; otherwise one
-// logit per thread and round.  The maximum key does not depend on who
-// compares what, so both forms give the same index.
+// one 16-byte load per round, so a launch sized at one round waits for one
+// load; the one group that ends past n reads its logits one by one (no load
+// straddles the end).  Otherwise one logit per thread and round.  The
+// maximum key does not depend on who compares what, so both forms give the
+// same index.
 template <bool kVec>
 __global__ __launch_bounds__(kLmThreads) void argmax_kernel(const uint16_t* __restrict__ logits, int n,
                                                             int32_t* token_out, unsigned long long* state,
@@ -416,15 +417,15 @@ __global__ __launch_bounds__(kLmThreads) void argmax_kernel(const uint16_t* __re
     const int chunk = argmax_chunk(n);
     unsigned long long best = 0ull;
     if constexpr (kVec) {
-        const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)logits, 0, 2 * n, 0x00020000);
         for (long long b = ((long long)blockIdx.x * kLmThreads + threadIdx.x) * 8; b < n;
              b += (long long)gridDim.x * kLmThreads * 8) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)(2 * b), 0, 0);
+            if (b + 8 <= n) {
+                const u32x4 v = *reinterpret_cast<const TER_GLOBAL u32x4*>(gptr(logits) + b);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int i = (int)b + e;
-                const uint16_t h = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
-                if (i < n) best = umax64(best, argmax_key(h, i, chunk));
+                for (int e = 0; e < 8; ++e)
+                    best = umax64(best, argmax_key((uint16_t)(v[e >> 1] >> (16 * (e & 1))), (int)b + e, chunk));
+            } else {
+                for (int i = (int)b; i < n; ++i) best = umax64(best, argmax_key(gptr(logits)[i], i, chunk));
             }
         }
     } else {

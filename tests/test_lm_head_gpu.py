@@ -155,6 +155,16 @@ def test_argmax_f16_matches_reference_rule(cuda):
     z[[10, 300, 999]] = np.float16(0.0)
     z[300] = np.float16(-0.0)       # -0 ties with +0
     cases.append(z)
+    # a last group of 8 that ends past N (read one by one): the maximum in it,
+    # or values below every other (so a zero read there would win), or N = 1
+    t = rng.standard_normal(1003).astype(np.float16)
+    t[1001] = np.float16(8.5)
+    cases.append(t)
+    t = np.full(1003, -1.0, np.float16)
+    t[1000:] = np.float16(-2.0)
+    cases.append(t)
+    cases.append(np.full(1, -np.inf, np.float16))
+    cases.append(np.full(7, -3.0, np.float16))
     for i, lg in enumerate(cases):
         got = int(host(T.argmax_f16(dev(lg), state=state))[0])
         assert got == O.argmax_f16(lg), (i, lg.size)
