@@ -436,24 +436,54 @@ __global__ __launch_bounds__(kLmThreads) void argmax_kernel(const uint16_t* __re
     argmax_finish(best, kred, state, token_out, chunk, pos_advance);
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// The token through the scalar cache (invalidated at every launch; nothing
+// in the launch writes it): one scalar load, not a vector load per thread.
+__device__ __forceinline__ int token_of(const int32_t* token) {
+    return *(const __attribute__((address_space(4))) int32_t*)(size_t)token;
+}
+
 // token_embed_lookup_k: hidden[i] = float(token_embd[token][i]) (exact
-// widening); a token outside [0, V) writes nothing.
+// widening); a token outside [0, V) writes nothing.  Thread j copies
+// elements 8 j .. 8 j + 7 (one 16-byte load when H is a multiple of 8 and
+// the table and the output are 16-byte aligned, else one by one).
 __global__ void embed_kernel(const uint16_t* __restrict__ emb, int V, int H, const int32_t* __restrict__ token,
                              float* __restrict__ hidden) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    const int t = *gptr(token);
-    if (i >= H || t < 0 || t >= V) return;
-    gptr(hidden)[i] = half_bits_to_float(gptr(emb)[(long long)t * H + i]);
+    const int i0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    const int t = token_of(token);
+    if (i0 >= H || t < 0 || t >= V) return;
+    const uint16_t* row = emb + (long long)t * H;
+    if (i0 + 8 <= H && (H & 7) == 0 && ((reinterpret_cast<uintptr_t>(emb) | reinterpret_cast<uintptr_t>(hidden)) & 15) == 0) {
+        const u32x4 v = *reinterpret_cast<const TER_GLOBAL u32x4*>(gptr(row) + i0);
+        f32x4_t lo, hi;
+        for (int e = 0; e < 4; ++e) {
+            lo[e] = half_bits_to_float((uint16_t)(v[e >> 1] >> (16 * (e & 1))));
+            hi[e] = half_bits_to_float((uint16_t)(v[2 + (e >> 1)] >> (16 * (e & 1))));
+        }
+        *reinterpret_cast<TER_GLOBAL f32x4_t*>(gptr(hidden) + i0) = lo;
+        *reinterpret_cast<TER_GLOBAL f32x4_t*>(gptr(hidden) + i0 + 4) = hi;
+    } else {
+        for (int i = i0; i < H && i < i0 + 8; ++i) gptr(hidden)[i] = half_bits_to_float(gptr(row)[i]);
+    }
 }
 
 // token_embed_lookup_k (cuda/ter_cuda_forward_packed.cu:99-106): the token's
-// fp16 row into the fp16 hidden stream (a token outside [0, V) writes nothing).
+// fp16 row into the fp16 hidden stream (a token outside [0, V) writes
+// nothing); 8 elements per thread as above.
 __global__ void embed16_kernel(const uint16_t* __restrict__ emb, int V, int H, const int32_t* __restrict__ token,
                                uint16_t* __restrict__ hidden16) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    const int t = *gptr(token);
-    if (i >= H || t < 0 || t >= V) return;
-    gptr(hidden16)[i] = gptr(emb)[(long long)t * H + i];
+    const int i0 = (blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    const int t = token_of(token);
+    if (i0 >= H || t < 0 || t >= V) return;
+    const uint16_t* row = emb + (long long)t * H;
+    if (i0 + 8 <= H && (H & 7) == 0 &&
+        ((reinterpret_cast<uintptr_t>(emb) | reinterpret_cast<uintptr_t>(hidden16)) & 15) == 0) {
+        *reinterpret_cast<TER_GLOBAL u32x4*>(gptr(hidden16) + i0) =
+            *reinterpret_cast<const TER_GLOBAL u32x4*>(gptr(row) + i0);
+    } else {
+        for (int i = i0; i < H && i < i0 + 8; ++i) gptr(hidden16)[i] = gptr(row)[i];
+    }
 }
 
 // rmsnorm_f32_in_k per row (256 threads): y = half((x * rms_inv) * gamma).
@@ -571,13 +601,13 @@ hipError_t launch_argmax_f16(const uint16_t* logits, int n, int32_t* token_out, 
 }
 
 hipError_t launch_embed_f16(const uint16_t* emb, int V, int H, const int32_t* token, float* hidden, hipStream_t st) {
-    hipLaunchKernelGGL(embed_kernel, dim3((H + 255) / 256), dim3(256), 0, st, emb, V, H, token, hidden);
+    hipLaunchKernelGGL(embed_kernel, dim3((H + 2047) / 2048), dim3(256), 0, st, emb, V, H, token, hidden);
     return hipGetLastError();
 }
 
 hipError_t launch_embed_h16(const uint16_t* emb, int V, int H, const int32_t* token, uint16_t* hidden16,
                             hipStream_t st) {
-    hipLaunchKernelGGL(embed16_kernel, dim3((H + 255) / 256), dim3(256), 0, st, emb, V, H, token, hidden16);
+    hipLaunchKernelGGL(embed16_kernel, dim3((H + 2047) / 2048), dim3(256), 0, st, emb, V, H, token, hidden16);
     return hipGetLastError();
 }
 

@@ -173,3 +173,33 @@ def test_argmax_f16_matches_reference_rule(cuda):
         got = int(host(T.argmax_f16(off, state=state))[0])
         assert got == O.argmax_f16(lg), ("unaligned", i, lg.size)
     assert (host(state.t) == 0).all()
+
+
+@pytest.mark.parametrize("V,H", [(1000, 2560), (50, 77), (9, 8)])
+def test_embedding_rows(cuda, V, H):
+    """token_embed_lookup_k in both forms (fp32 hidden stream, fp16 hidden
+    stream): the token's row exactly, for the first and last tokens, into an
+    aligned and a misaligned output (one element past an aligned start); a
+    token outside [0, V) writes nothing."""
+    import torch
+    import ter_amd as T
+    rng = np.random.default_rng(V + H)
+    Eh = (rng.standard_normal((V, H)) * 0.1).astype(np.float16)
+    E = dev(Eh)
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for t in (0, V - 1, V // 2):
+        tok.fill_(t)
+        for off in (0, 1):
+            h32 = torch.full((H + off,), -7.0, dtype=torch.float32, device="cuda")
+            T.embed_f16(E, tok, h32[off:])
+            assert (host(h32[off:]) == Eh[t].astype(np.float32)).all(), (t, off)
+            h16 = torch.full((H + off,), -7.0, dtype=torch.float16, device="cuda")
+            T.embed_h16(E, tok, h16[off:])
+            assert (host(h16[off:]).view(np.uint16) == Eh[t].view(np.uint16)).all(), (t, off)
+    for t in (-1, V):
+        tok.fill_(t)
+        h32 = torch.full((H,), -7.0, dtype=torch.float32, device="cuda")
+        T.embed_f16(E, tok, h32)
+        h16 = torch.full((H,), -7.0, dtype=torch.float16, device="cuda")
+        T.embed_h16(E, tok, h16)
+        assert (host(h32) == -7.0).all() and (host(h16) == -7.0).all(), t
