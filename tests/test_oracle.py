@@ -218,6 +218,43 @@ def test_mm_row_blocked_vs_reference_build():
     assert (out.view(np.int32) == ref.view(np.int32)).all()
 
 
+@pytest.mark.skipif(not O.ref_available(), reason="reference build oracle/_ref absent")
+def test_mm_row_random_shapes_vs_reference_build():
+    """Generated cases against the reference build (src/tx/forward.cpp:299-352
+    and its per-block branch): K and N from 1 up, payload magnitudes 1, 3,
+    121 and 9841, int8 and 9-trit (|x| <= 9841) activations, zero rows and
+    columns, scales of either sign; every output bit for bit, both paths."""
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=60, deadline=None, derandomize=True)
+    @given(K=st.integers(1, 300), N=st.integers(1, 24), m=st.sampled_from([1, 3, 121, 9841]),
+           wide=st.booleans(), seed=st.integers(0, 2 ** 31 - 1),
+           xs=st.sampled_from([0.5, -0.25, 1.0 / 3.0, 7.0]), ws=st.sampled_from([0.25, -1.5, 2.0 ** -7]),
+           bs=st.integers(1, 64))
+    def check(K, N, m, wide, seed, xs, ws, bs):
+        rng = np.random.default_rng(seed)
+        W = (rng.integers(-1, 2, size=(K, N)) * m).astype(np.int32)
+        lim = 9841 if wide else 127
+        X = rng.integers(-lim, lim + 1, size=(2, K)).astype(np.int32)
+        X[1, : K // 2] = 0  # a half-zero row
+        if N > 1:
+            W[:, 0] = 0     # a zero column
+        r = O.RefMmRow(X, xs, W, ws)
+        for row in (0, 1):
+            ref = r.run(row).copy()
+            _, out = O.mm_row(X, row, xs, W, ws)
+            assert (out.view(np.int32) == ref.view(np.int32)).all(), (K, N, m, row)
+        if m * lim < (1 << 29):  # the per-block branch's exact-double range
+            nb = (K * N + bs - 1) // bs
+            bsc = (rng.standard_normal(nb) * 0.1).astype(np.float32)
+            rb = O.RefMmRow(X, xs, W, 1.0, bsc, bs)
+            ref = rb.run(0).copy()
+            out = O.mm_row_blocked(X, 0, xs, W, bsc, bs)
+            assert (out.view(np.int32) == ref.view(np.int32)).all(), (K, N, m, bs)
+
+    check()
+
+
 # ---------------------------------------------------------------- quantizers
 def test_quant_int8_half_way_ties():
     # amax = 127/64 (exact in fp32); + 1e-9f is below half an ulp, so
