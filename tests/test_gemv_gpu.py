@@ -64,6 +64,60 @@ def test_gemv_shapes(cuda, K, N):
     gemv_case(K, N, seed=K * 7 + N)
 
 
+def test_gemv_generated_shapes(cuda):
+    """Generated cases (hypothesis, derandomized): K from 1 to 5000 and N
+    from 1 to 700 (ragged units and strips, every launch form the size
+    picks; v11 weights where N is a multiple of 4, the TritTensor payload
+    otherwise), zero densities from none to all, single GEMVs and a
+    three-GEMV work list of unrelated shapes; int32 and fp32 outputs against
+    the oracle bit for bit."""
+    import torch
+    import ter_amd as T
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=40, deadline=None, derandomize=True)
+    @given(K=st.integers(1, 5000), N=st.integers(1, 700), p0=st.sampled_from([0.0, 0.4, 0.9, 1.0]),
+           seed=st.integers(0, 2 ** 20))
+    def single(K, N, p0, seed):
+        if N % 4 == 0:  # the v11 layout packs 4 columns per byte
+            gemv_case(K, N, seed=seed, p0=p0)
+            return
+        # any N: the TritTensor payload, against the restated mm_row
+        w = O.rand_trits(seed, K, N, p0).astype(np.int32)
+        x = O.rand_int8(seed + 1, K).astype(np.int32)
+        W = T.PackedTrits.from_payload(w, 0.05)
+        acc = torch.empty(N, dtype=torch.int32, device="cuda")
+        y = torch.empty(N, dtype=torch.float32, device="cuda")
+        T.gemv(W, dev(x.astype(np.int8)), y=y, acc=acc, x_scale=0.0312)
+        ra, ry = O.mm_row(x[None], 0, 0.0312, w, 0.05)
+        assert (host(acc).astype(np.int64) == ra).all(), (K, N)
+        assert_f32_equal(host(y), ry)
+
+    @settings(max_examples=12, deadline=None, derandomize=True)
+    @given(shapes=st.lists(st.tuples(st.integers(1, 3000), st.integers(1, 100).map(lambda v: 4 * v)), min_size=3,
+                           max_size=3),
+           seed=st.integers(0, 2 ** 20))
+    def plan(shapes, seed):
+        items, refs = [], []
+        for i, (K, N) in enumerate(shapes):
+            v11 = O.v11_pack(O.rand_trits(seed + i, K, N, 0.4))
+            x = O.rand_int8(seed + 10 + i, K)
+            W = T.PackedTrits.from_v11(v11, K, N, 0.05 + 0.01 * i)
+            acc = torch.empty(N, dtype=torch.int32, device="cuda")
+            y = torch.empty(N, dtype=torch.float32, device="cuda")
+            items.append(dict(w=W, x=dev(x), x_scale=0.03, y=y, acc=acc))
+            refs.append(O.gemv_v11(x, 0.03, v11, 0.05 + 0.01 * i, K, N))
+        P = T.Plan(items)
+        P.launch()
+        for it, (ra, ry) in zip(items, refs):
+            assert (host(it["acc"]) == ra).all(), shapes
+            assert_f32_equal(host(it["y"]), ry)
+        P.close()
+
+    single()
+    plan()
+
+
 def test_gemv_golden_reference_vectors(cuda, golden):
     """Vectors written by the reference mm_row itself (tests/golden)."""
     import torch
