@@ -77,6 +77,57 @@ def test_gemm_fp32_rows_quantized(cuda, M, K, N):
     assert_f32_equal(host(y), ry)
 
 
+def test_gemm_generated_shapes(cuda):
+    """Generated cases (hypothesis, derandomized): M from 2 to 256 (one to
+    two 128-row pieces, every row-block configuration), K from 1 to 3000
+    (16-byte aligned rows or not, so the LDS ring and the unaligned kernel
+    both run), N a multiple of 4 up to 600; single launches and a two-GEMM
+    plan; int32 and fp32 outputs against the oracle bit for bit."""
+    import torch
+    import ter_amd as T
+    from hypothesis import given, settings, strategies as st
+
+    def case(M, K, N, seed):
+        v11 = O.v11_pack(O.rand_trits(seed, K, N, 0.4))
+        X = O.rand_int8(seed + 1, M * K).reshape(M, K)
+        xs = (0.001 * (np.arange(M) + 1)).astype(np.float32)
+        return v11, X, xs, T.PackedTrits.from_v11(v11, K, N, 0.043)
+
+    @settings(max_examples=30, deadline=None, derandomize=True)
+    @given(M=st.integers(2, 256), K=st.integers(1, 3000), N=st.integers(1, 150).map(lambda v: 4 * v),
+           seed=st.integers(0, 2 ** 20))
+    def single(M, K, N, seed):
+        v11, X, xs, W = case(M, K, N, seed)
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+        T.mm_batched(W, dev(X), y=y, acc=acc, x_scale_dev=dev(xs))
+        ra, ry = O.gemm_v11(X, xs, v11, 0.043, K, N)
+        assert (host(acc) == ra).all(), (M, K, N)
+        assert_f32_equal(host(y), ry)
+
+    @settings(max_examples=10, deadline=None, derandomize=True)
+    @given(M=st.integers(2, 160), K1=st.integers(1, 100).map(lambda v: 16 * v),
+           K2=st.integers(1, 100).map(lambda v: 16 * v), N1=st.integers(1, 100).map(lambda v: 4 * v),
+           N2=st.integers(1, 100).map(lambda v: 4 * v), seed=st.integers(0, 2 ** 20))
+    def plan(M, K1, K2, N1, N2, seed):
+        items, refs = [], []
+        for i, (K, N) in enumerate(((K1, N1), (K2, N2))):
+            v11, X, xs, W = case(M, K, N, seed + 7 * i)
+            y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+            acc = torch.empty((M, N), dtype=torch.int32, device="cuda")
+            items.append(dict(w=W, x=dev(X), x_scale_dev=dev(xs), y=y, acc=acc))
+            refs.append(O.gemm_v11(X, xs, v11, 0.043, K, N))
+        P = T.GemmPlan(items)
+        P.launch()
+        for it, (ra, ry) in zip(items, refs):
+            assert (host(it["acc"]) == ra).all(), (M, K1, K2, N1, N2)
+            assert_f32_equal(host(it["y"]), ry)
+        P.close()
+
+    single()
+    plan()
+
+
 def test_gemm_m1_rows_match_gemv(cuda):
     """Each row of the batched product equals the M = 1 GEMV of that row."""
     import torch
