@@ -164,3 +164,66 @@ def test_shared_activation_plans(cuda, kind, order):
             assert (host(it["y"]).view(np.int32) == ry.view(np.int32)).all(), (rep, i)
             assert (host(it["y16"]).view(np.uint16) == O.float_to_half_bits(ry)).all(), (rep, i)
     plan.close()
+
+
+def test_prologue_plans_generated(cuda):
+    """Generated decode-step plans (hypothesis, derandomized): one of the six
+    prologue kinds, K a multiple of 16 up to the strided prologue's limit or
+    any K (the general prologue), one to four GEMVs of N a multiple of 4
+    reading one activation vector, weights grouped in one allocation or
+    not; whichever launch form the plan picks, every output, fp16 copy and
+    accumulator bit for bit against the oracle."""
+    import torch
+    import ter_amd as T
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=36, deadline=None, derandomize=True)
+    @given(kind=st.sampled_from(["f32-rms", "f16-rms", "relu2", "f16", "silu", "smul"]),
+           ku16=st.integers(1, 256), ragged=st.booleans(),
+           Ns=st.lists(st.integers(1, 600).map(lambda v: 4 * v), min_size=1, max_size=4),
+           grouped=st.booleans(), seed=st.integers(0, 2 ** 20))
+    def check(kind, ku16, ragged, Ns, grouped, seed):
+        limit = 8192 if kind in ("relu2", "silu", "smul") else 4096
+        K = min(16 * ku16, limit)
+        if ragged:
+            K = max(1, K - 5)
+        rng = np.random.default_rng(seed)
+        gm = rng.uniform(0.5, 1.5, K).astype(np.float16)
+        x = (rng.standard_normal(K) * 3).astype(np.float32 if kind == "f32-rms" else np.float16)
+        up = (rng.standard_normal(K) * 1.5).astype(np.float16)
+        if kind in ("f32-rms", "f16-rms"):
+            rq, rs, _ = O.rmsnorm_quant(x, gm, 1e-5)
+        elif kind == "relu2":
+            rq, rs, _ = O.relu2_rmsnorm_quant(x, up, gm, 1e-5)
+        elif kind == "f16":
+            rq, rs = O.quant_int8(x.astype(np.float32))
+        elif kind == "silu":
+            rq, rs, _ = O.silu_mul_quant(x, up)
+        else:
+            x = O.silu_f16(x)
+            rq, rs, _ = O.smul_quant(x, up)
+        v11s = [O.v11_pack(O.rand_trits(seed + 7 * i, K, N, 0.4)) for i, N in enumerate(Ns)]
+        Ws = [T.PackedTrits.from_v11(v, K, N, 0.01 * (i + 1)) for i, (v, N) in enumerate(zip(v11s, Ns))]
+        if grouped:
+            Ws = T.group_contiguous(Ws)
+        dx, dg, du = dev(x), dev(gm), dev(up)
+        items = []
+        for i, N in enumerate(Ns):
+            it = dict(w=Ws[i], x=dx, y=torch.empty(N, dtype=torch.float32, device="cuda"),
+                      acc=torch.empty(N, dtype=torch.int32, device="cuda"),
+                      y16=torch.empty(N, dtype=torch.float16, device="cuda"))
+            if kind in ("f32-rms", "f16-rms", "relu2"):
+                it.update(gamma=dg, eps=1e-5)
+            if kind in ("relu2", "silu", "smul"):
+                it["up"] = du
+            items.append(it)
+        plan = T.Plan(items)
+        plan.launch()
+        for i, it in enumerate(items):
+            ra, ry = O.gemv_v11(rq, rs, v11s[i], 0.01 * (i + 1), K, Ns[i])
+            assert (host(it["acc"]) == ra).all(), (kind, K, Ns, i)
+            assert (host(it["y"]).view(np.int32) == ry.view(np.int32)).all(), (kind, K, Ns, i)
+            assert (host(it["y16"]).view(np.uint16) == O.float_to_half_bits(ry)).all(), (kind, K, Ns, i)
+        plan.close()
+
+    check()
