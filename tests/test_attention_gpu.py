@@ -110,3 +110,22 @@ def test_rope_standalone(cuda):
     want = O.rope_f16(x, O.rope_table(500000.0, 128, 100)[77], True)
     assert (bits(host(t)) == bits(want)).all()
     A.close()
+
+
+def test_generated_attention_shapes(cuda):
+    """Generated contexts (hypothesis, derandomized): 1 to 16 KV heads with
+    1 to 12 query heads each, head_dim 64 or 128, either RoPE pairing,
+    s_max from 1 to 4096 (up to 64 chunks), three positions each (the first,
+    a random one and the last); outputs bit-exact against the chunked
+    oracle and within one fp16 ulp of the sequential order, the new cache
+    rows exact (run_decode's checks)."""
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=16, deadline=None, derandomize=True)
+    @given(nkv=st.integers(1, 16), g=st.integers(1, 12), hd=st.sampled_from([64, 128]), neox=st.booleans(),
+           smax=st.integers(1, 4096), frac=st.floats(0.0, 1.0), seed=st.integers(0, 2 ** 20))
+    def check(nkv, g, hd, neox, smax, frac, seed):
+        positions = sorted({0, int(frac * (smax - 1)), smax - 1})
+        run_decode(nkv * g, nkv, hd, smax, 10000.0, neox, positions, seed)
+
+    check()
