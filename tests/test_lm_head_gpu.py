@@ -87,6 +87,38 @@ def test_lm_head_logits(cuda, H, V):
     assert bad.size == 0, (bad[:8], got[bad[:4]], want[bad[:4]])
 
 
+def test_lm_head_generated_shapes(cuda):
+    """Generated tails (hypothesis, derandomized): H from 2 to 6000 (the
+    octet path where H is a multiple of 8 and fits it, the generic one
+    otherwise), V from 1 to 3000, fp32 or fp16 hidden stream; the fused
+    RMSNorm + lm_head + argmax against the oracle (normalized input, every
+    logit, the token), the argmax state left clean."""
+    import torch
+    import ter_amd as T
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=24, deadline=None, derandomize=True)
+    @given(H=st.integers(1, 3000).map(lambda v: 2 * v), V=st.integers(1, 3000), half=st.booleans(),
+           seed=st.integers(0, 2 ** 20))
+    def check(H, V, half, seed):
+        E, Eh = embedding(seed, V, H)
+        rng = np.random.default_rng(seed)
+        gamma = rng.uniform(0.5, 1.5, H).astype(np.float16)
+        hidden = (rng.standard_normal(H) * 3).astype(np.float16 if half else np.float32)
+        state = T.ArgmaxState()
+        x_out = torch.empty(H, dtype=torch.float16, device="cuda")
+        lg_out = torch.empty(V, dtype=torch.float16, device="cuda")
+        tok = T.lm_head_argmax(dev(hidden), dev(gamma), E, 1e-5, state=state, x_norm_out=x_out, logits_out=lg_out)
+        xn, _ = O.rmsnorm_f16(hidden, gamma, 1e-5)
+        assert (f16_bits(host(x_out)) == f16_bits(xn)).all(), (H, V, half)
+        want_lg, _ = O.lm_head_f16(xn, Eh)
+        assert (f16_bits(host(lg_out)) == f16_bits(want_lg)).all(), (H, V, half)
+        assert int(host(tok)[0]) == O.argmax_f16(want_lg), (H, V, half)
+        assert (host(state.t) == 0).all()
+
+    check()
+
+
 def test_lm_head_bitnet_full_size_and_fused_tail(cuda):
     """V = 128256, H = 2560 (BitNet-2B's tied lm_head): every logit, the
     normalized input and the token of the fused one-launch tail, over three
