@@ -335,6 +335,31 @@ def test_mm_row_host_contract(cuda):
     assert_f32_equal(out, ref)
 
 
+def test_mm_row_generated_host_calls(cuda):
+    """Generated host mm_row calls (hypothesis, derandomized): the host
+    forward's contract (int32 rows in host memory, a row index, outputs in
+    host memory) with K from 1 to 4000, N from 1 to 400, payload magnitudes
+    1, 3 and 9841, int8-range or 9-trit rows; every output bit for bit
+    against the restated mm_row."""
+    import ter_amd as T
+    from hypothesis import given, settings, strategies as st
+
+    @settings(max_examples=30, deadline=None, derandomize=True)
+    @given(K=st.integers(1, 4000), N=st.integers(1, 400), m=st.sampled_from([1, 3, 9841]), wide=st.booleans(),
+           row=st.integers(0, 2), seed=st.integers(0, 2 ** 20))
+    def check(K, N, m, wide, row, seed):
+        rng = np.random.default_rng(seed)
+        w = (rng.integers(-1, 2, size=(K, N)) * m).astype(np.int32)
+        lim = 9841 if wide else 127
+        X = rng.integers(-lim, lim + 1, size=(3, K)).astype(np.int32)
+        W = T.PackedTrits.from_payload(w, 0.02)
+        out = T.mm_row(X, row, 0.5, W, K, N)
+        _, ref = O.mm_row(X, row, 0.5, w, 0.02)
+        assert_f32_equal(out, ref)
+
+    check()
+
+
 def test_gemv_edge_values(cuda):
     import torch
     import ter_amd as T
